@@ -1,0 +1,228 @@
+"""Benchmark of the DiT joint-attention hot path on one MI355X (gfx950).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video] [--tile-config C]
+                    [--no-cpu-baseline]
+
+A step is one fused joint-attention call over one synthetic batch: keys RMSNorm + RoPE into the workspace
+(lr_joint_keys_prepare) followed by the attention kernel with the queries normalised and rotated in registers
+(lr_joint_attention_prepared) -- together exactly lr_joint_attention_fused. Inputs are resident in HBM before timing.
+The default workload is BASELINE's Qwen-Image-style step: B=1, 24 heads x 128, 512 text + 4096 image tokens (64x64
+grid, 2D RoPE on image tokens, text un-rotated), non-causal, QK-RMSNorm eps 1e-6 with weights 1.0, scale f32(1/sqrt(128)).
+
+Prints ONE JSON line on stdout (everything else goes to stderr). FLOPs per call = 4 * Sq * Sk * 128 * H (QK^T + PV;
+softmax, RMSNorm and RoPE not counted). `roofline` is the attention kernel alone, timed with HIP events on the stream
+it is launched on, against MI355X's published dense bf16 peak of 2.5 PFLOP/s. `cpu_baseline` times the CPU oracle's
+fp32 flash-style path (OpenMP) on a bounded sample of query rows of the same workload, as a reported baseline only.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0
+METRIC = "attention TFLOP/s + % bf16 MFMA peak; ms/call at 4096+512 tokens, 24x128"
+WORKLOADS = {
+    # name: (text tokens, grid description, heads)
+    "plumbing": dict(n_text=256, kind="grid2d", gh=32, gw=32, heads=24),
+    "qwen-step": dict(n_text=512, kind="grid2d", gh=64, gw=64, heads=24),
+    "edit": dict(n_text=512, kind="edit", frames=3, gh=64, gw=64, heads=24),
+    "video": dict(n_text=512, kind="video3d", t=49, gh=44, gw=80, heads=24),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def tables(w):
+    from localrouter_amd import rope
+    if w["kind"] == "grid2d":
+        return rope.grid2d_table(w["n_text"], w["gh"], w["gw"])
+    if w["kind"] == "edit":
+        return rope.edit_table(w["n_text"], w["frames"], w["gh"], w["gw"])
+    return rope.video3d_table(w["n_text"], w["t"], w["gh"], w["gw"])
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch of the attention kernel, from the committed rocprofv3 PMC summary (None if absent)."""
+    p = ROOT / "profiles" / f"attn_fwd_{name}_pmc.md"
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(q_bits, k_bits, v_bits, cos, sin, S, H, flops_per_row, budget_s=15.0):
+    """The oracle's fp32 flash-style path (norm + rope + attention) on a sample of query rows, timed on host cores."""
+    import numpy as np
+
+    import oracle
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(0)
+
+    def run(rows):
+        t0 = time.perf_counter()
+        qh = oracle.rms_rope(q_bits[rows], None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos[rows], tb=sin[rows])
+        kh = oracle.rms_rope(k_bits, None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos, tb=sin)
+        vf = oracle.bf16_to_f32(v_bits)
+        # all S keys for each sampled query row: the sampled rows are renumbered 0..n-1 (non-causal, so equivalent)
+        out = oracle.attention(qh, kh, vf, precise=False)
+        return time.perf_counter() - t0, out
+
+    probe = np.sort(rng.choice(S, size=64, replace=False))
+    dt, _ = run(probe)
+    rate = 64 * flops_per_row / dt
+    n = int(min(S, max(64, budget_s * rate / flops_per_row)) // 32 * 32)
+    rows = np.sort(rng.choice(S, size=n, replace=False))
+    dt, out = run(rows)
+    return dict(value=n * flops_per_row / dt / 1e12, threads=threads, rows=rows, out=out, seconds=dt)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS))
+    ap.add_argument("--tile-config", type=int, default=0, help="LR_ATTN_CFG_* (0 = library default)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=2)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); the "
+              "joint attention shards by heads with no exchange, so N GPUs would run this same kernel at H/N heads.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from localrouter_amd import _lib, ops
+
+    w = WORKLOADS[args.workload]
+    H = w["heads"]
+    cos_np, sin_np = tables(w)
+    S = cos_np.shape[0]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    L = _lib.load()
+    rc = L.lr_attn_init()
+    if rc != 0:
+        raise SystemExit(f"lr_attn_init: {rc} (not a gfx950?)")
+    props = torch.cuda.get_device_properties(dev)
+    log(f"[bench] device {props.name} {getattr(props, 'gcnArchName', '')} CUs {props.multi_processor_count}; "
+        f"workload {args.workload}: S={S} H={H}")
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    q = torch.randn((S, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    k = torch.randn((S, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    v = torch.randn((S, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    cos = torch.from_numpy(cos_np).to(dev)
+    sin = torch.from_numpy(sin_np).to(dev)
+    wq = torch.ones(128, dtype=torch.float32, device=dev)
+    wk = torch.ones(128, dtype=torch.float32, device=dev)
+    ws_bytes = ops.workspace_bytes(S, H)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    eps, scale, rs = 1e-6, ops.SCALE_128, H * 128
+
+    def keys():
+        _lib.call("lr_joint_keys_prepare", k.data_ptr(), rs, wk.data_ptr(), ops.TABLE_COSSIN_F32, cos.data_ptr(),
+                  sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, H, 0, ws.data_ptr(), ws_bytes, sh)
+
+    def attn():
+        _lib.call("lr_joint_attention_prepared", q.data_ptr(), ws.data_ptr(), ws_bytes, v.data_ptr(), out.data_ptr(),
+                  wq.data_ptr(), ops.TABLE_COSSIN_F32, cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128,
+                  eps, S, S, H, H, 0, 0, scale, rs, rs, rs, args.tile_config, sh)
+
+    for _ in range(args.warmup):
+        keys()
+        attn()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
+
+    K = args.steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    for i in range(K):
+        ev[2 * i].record(stream)
+        keys()
+        ev[2 * i + 1].record(stream)
+        attn()
+    ev[2 * K].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    t_keys = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(K)]
+    t_attn = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(K)]
+    total_ms = ev[0].elapsed_time(ev[2 * K])
+    ms_step = total_ms / K
+    flops = 4.0 * S * S * 128 * H
+    attn_ms = float(np.mean(t_attn))
+    keys_ms = float(np.mean(t_keys))
+    value = flops / (ms_step * 1e-3) / 1e12
+    achieved = flops / (attn_ms * 1e-3) / 1e12
+    log(f"[bench] step {ms_step:.4f} ms (keys {keys_ms:.4f} ms, attention {attn_ms:.4f} ms, median attention "
+        f"{float(np.median(t_attn)):.4f} ms); {value:.1f} TFLOP/s step, {achieved:.1f} TFLOP/s attention kernel "
+        f"({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); wall {wall:.3f} s")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}-joint-attention", "batch": 1, "tokens": S, "text_tokens": w["n_text"],
+                   "heads": H, "head_dim": 128, "causal": False, "qk_rmsnorm": True, "rope": w["kind"],
+                   "parallelism": "none (1 GPU)", "tile_config": args.tile_config},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic_from_profile(args.workload),
+                     "kernel": "attn_fwd_kernel", "kernel_ms": round(attn_ms, 5)},
+        "kernels_ms": {"keys_rms_rope": round(keys_ms, 5), "attention": round(attn_ms, 5)},
+        "flops_per_call": flops,
+    }
+
+    if not args.no_cpu_baseline:
+        fl_row = 4.0 * S * 128 * H
+        log("[bench] cpu baseline (oracle fp32 flash path, sampled query rows) ...")
+        qb = q.cpu().view(torch.int16).numpy().view(np.uint16)
+        kb = k.cpu().view(torch.int16).numpy().view(np.uint16)
+        vb = v.cpu().view(torch.int16).numpy().view(np.uint16)
+        cb = cpu_baseline(qb, kb, vb, cos_np, sin_np, S, H, fl_row)
+        got = out.cpu().view(torch.int16).numpy().view(np.uint16)[cb["rows"]]
+        gotf = (got.astype(np.uint32) << 16).view(np.float32)
+        d = np.abs(gotf.astype(np.float64) - cb["out"])
+        result["cpu_baseline"] = {"value": round(cb["value"], 4), "unit": "TFLOP/s", "cores": cb["threads"],
+                                  "kind": "port",
+                                  "sample": f"{len(cb['rows'])} of {S} query rows x {H} heads over all {S} keys "
+                                            f"(norm+rope+attention, fp32), {cb['seconds']:.1f} s"}
+        result["check"] = {"rows": int(len(cb["rows"])), "max_abs": float(d.max()), "mean_abs": float(d.mean()),
+                           "bar": {"max_abs": 2e-2, "mean_abs": 2e-3}}
+        log(f"[bench] cpu {cb['value']:.4f} TFLOP/s on {cb['threads']} threads; GPU vs CPU on sampled rows: "
+            f"max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

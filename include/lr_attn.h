@@ -1,0 +1,166 @@
+/*
+ * lr_attn.h -- the C ABI of the MI355X (gfx950) DiT joint-attention path.
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers, element strides and sizes, launches
+ * asynchronously on the caller's stream and returns an int that is a hipError_t:
+ *   0 (hipSuccess)             the work was launched;
+ *   1 (hipErrorInvalidValue)   an argument was rejected before anything was launched;
+ *   any other value            what the HIP runtime reported for the launch.
+ * No entry point synchronises, allocates, sets function attributes or keeps mutable global state, so every call
+ * may be captured into a HIP graph and may run concurrently on different streams. The caller owns every buffer.
+ *
+ * Tensors are bf16 "rows": token-major, heads contiguous, head h of token i at base + i*row_stride + h*128
+ * (strides in ELEMENTS). Head dim is 128. Base pointers and row strides must be 16-byte aligned
+ * (row strides multiples of 8 elements).
+ *
+ * The reference interfaces these replace (jayleaton/localrouter):
+ *   lr_attention_bf16        <- Ops.attention, src/engines/qwen_image/ops_launch.zig:163-172, which launches
+ *                               pattn2_kernel (kernels/cuda/qwen_image/attention.cu:253-444, :816-817)
+ *   lr_rms_rope_bf16         <- Triton.ropeRun, src/engines/qwen_image/triton_k.zig:44-53 (tfimage _rms_rope_kernel)
+ *   lr_rms_rope_qk_bf16      <- Kitchen.rmsRope, src/engines/minimax_h3/launch.zig:421-441, and
+ *                               kitchen_rms_rope_split_half_, kernels/cuda/minimax/kitchen_launch.cu:284-314
+ *   lr_joint_attention_fused <- the chain rope_q -> rope_k -> V copy -> attention of Dit.block,
+ *                               src/engines/qwen_image/dit.zig:252-293 (and minimax_h3/dit.zig:663-672), as one call
+ */
+#ifndef LR_ATTN_H
+#define LR_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers: an opaque pointer (NULL = the default stream). */
+typedef struct ihipStream_t* lr_stream_t;
+
+#define LR_ATTN_ABI_VERSION 1
+#define LR_HEAD_DIM 128
+
+/* RoPE table kinds: how rotation coefficients are stored per token row, per pair p < rot_dim/2. */
+#define LR_TABLE_NONE 0        /* RMSNorm only, no rotation */
+#define LR_TABLE_COSSIN_F32 1  /* table_a = cos fp32 [rows][row_stride], table_b = sin fp32, same shape (Qwen-Image) */
+#define LR_TABLE_MAT2_BF16 2   /* table_a = bf16 [rows][row_stride] holding [rot/2][2][2] {f00,f01,f10,f11} (H3) */
+#define LR_TABLE_MAT2_F32 3    /* as LR_TABLE_MAT2_BF16 in fp32 */
+/* A pair (a, b) becomes (f00*a + f01*b, f10*a + f11*b); for COSSIN that is (c*a - s*b, s*a + c*b). */
+
+/* Which dims form a rotated pair. */
+#define LR_PAIR_INTERLEAVED 0  /* (2p, 2p+1)        -- Qwen-Image / diffusers, Kandinsky-6 */
+#define LR_PAIR_SPLIT_HALF 1   /* (p, p + rot_dim/2) -- MiniMax H3 (comfy-kitchen) */
+
+/* Norm weight element types. */
+#define LR_WEIGHT_NONE 0       /* all ones */
+#define LR_WEIGHT_F32 1
+#define LR_WEIGHT_BF16 2
+
+/* Attention tile configurations for the _ex entry points (0 = the library's choice). */
+#define LR_ATTN_CFG_AUTO 0
+#define LR_ATTN_CFG_Q64_W4 1   /* 256 queries per workgroup, 4 waves x 64 queries */
+#define LR_ATTN_CFG_Q32_W8 2   /* 256 queries per workgroup, 8 waves x 32 queries */
+#define LR_ATTN_CFG_Q32_W4 3   /* 128 queries per workgroup, 4 waves x 32 queries */
+
+int lr_attn_abi_version(void);
+
+/* Checks that the current HIP device is a gfx950 (MI355X / MI350X). 0 on success, hipErrorInvalidDevice (101)
+ * otherwise. Optional: nothing else needs it, it sets no state. */
+int lr_attn_init(void);
+
+/*
+ * Attention over pre-normalised, pre-rotated q/k (drop-in for Ops.attention, ops_launch.zig:163-172).
+ *   q   [W][H][128]       row stride q_row_stride
+ *   k,v [nkeys][HK][128]  row stride kv_row_stride (both)
+ *   out [W][H][128]       row stride out_row_stride
+ * out_i = softmax_j(scale * <q_i, k_j>) v_j over j < nkeys, and j <= p0 + i when causal != 0; query head h reads
+ * kv head h / (H / HK). Requires W >= 1, nkeys >= 1, H % HK == 0, p0 >= 0, 0 < scale < inf.
+ * fp32 accumulation and softmax; P is rounded to bf16 for the PV product; out is rounded to bf16.
+ */
+int lr_attention_bf16(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK, int nkeys,
+                      int causal, float scale, int64_t q_row_stride, int64_t kv_row_stride, int64_t out_row_stride,
+                      lr_stream_t stream);
+
+/* lr_attention_bf16 with separate k/v row strides, kv-head strides (k/v head g at base + g*head_stride: 128 for rows,
+ * nkeys*128 for head-major [HK][nkeys][128]) and an explicit tile configuration (LR_ATTN_CFG_*). */
+int lr_attention_bf16_ex(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK,
+                         int nkeys, int causal, float scale, int64_t q_row_stride, int64_t k_row_stride,
+                         int64_t v_row_stride, int64_t out_row_stride, int64_t k_head_stride, int64_t v_head_stride,
+                         int config, lr_stream_t stream);
+
+/*
+ * Per-(token, head) RMSNorm + RoPE of one q/k part, out of place or in place (drop-in for Triton.ropeRun,
+ * triton_k.zig:44-53): for batch bi < b, token r < n, head h < heads:
+ *   x = src[bi*src_b_stride + r*src_row_stride + src_off + h*128 + d]
+ *   y = x / sqrt(mean(x^2) + eps) * w[d]       (fp32; rounded to bf16 here when round_norm != 0)
+ *   pairs rotated with table row r; dims >= rot_dim are norm-only
+ *   dst[bi*dst_b_stride + r*dst_row_stride + h*128 + d] = bf16(y)
+ * w: [128] of w_kind (LR_WEIGHT_*), NULL with LR_WEIGHT_NONE. table_kind LR_TABLE_*, table_row_stride in elements.
+ * rot_dim: even, <= 128 (0 = 128); LR_PAIR_SPLIT_HALF needs rot_dim % 16 == 0.
+ */
+int lr_rms_rope_bf16(const void* src, int64_t src_row_stride, int64_t src_off, void* dst, int64_t dst_row_stride,
+                     int64_t n, int b, int64_t src_b_stride, int64_t dst_b_stride, int heads, const void* w, int w_kind,
+                     int table_kind, const void* table_a, const void* table_b, int64_t table_row_stride, int rot_dim,
+                     int pairing, float eps, int round_norm, lr_stream_t stream);
+
+/*
+ * MiniMax H3's fused norm + rotation of q and k in place (drop-in for Kitchen.rmsRope, launch.zig:421-441):
+ * q, k [seq][heads][128] with row strides q_row_stride / k_row_stride (packed qkv: both 3*heads*128), bf16 norm
+ * weights [128], bf16 freqs [seq][freqs_row_stride] holding [rot_dim/2][2][2], split-half pairs, the normalised value
+ * rounded to bf16 before the rotation (rms_rope.cu:143-150). rot_dim 0 = 128.
+ */
+int lr_rms_rope_qk_bf16(void* q, void* k, int64_t seq, int heads, int64_t q_row_stride, int64_t k_row_stride,
+                        const void* q_norm, const void* k_norm, const void* freqs, int64_t freqs_row_stride,
+                        int rot_dim, float eps, lr_stream_t stream);
+
+/* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys, bf16 [HK][Sk][128]. */
+size_t lr_joint_attention_workspace_bytes(int Sk, int HK);
+
+/*
+ * The fused joint attention: QK-RMSNorm + RoPE + attention in two launches (keys normalised once into the workspace;
+ * queries normalised and rotated in registers inside the attention kernel).
+ *   q_raw [Sq][H][128], k_raw, v [Sk][HK][128], out [Sq][H][128] bf16 rows with the given row strides.
+ *   q_norm_w, k_norm_w: fp32 [128] or NULL (ones). eps >= 0.
+ *   Query i uses q-table row i; key j >= n_pre uses k-table row j - n_pre; keys j < n_pre are already normalised and
+ *   rotated (a cached text prefix) and are used as they are.
+ *   table_kind / pairing / rot_dim as in lr_rms_rope_bf16, except LR_PAIR_SPLIT_HALF needs rot_dim % 32 == 0.
+ *   Attention as lr_attention_bf16 with nkeys = Sk.
+ *   workspace: >= lr_joint_attention_workspace_bytes(Sk, HK) bytes, 256-byte aligned, owned by the caller; its
+ *   contents are scratch (clobbered by the call, not read before being written).
+ */
+int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,
+                             const float* k_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
+                             const void* k_table_a, const void* k_table_b, int64_t table_row_stride, int pairing,
+                             int rot_dim, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
+                             int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride, int64_t out_row_stride,
+                             int n_pre, void* workspace, size_t workspace_bytes, lr_stream_t stream);
+
+/*
+ * The two stages of lr_joint_attention_fused as separate calls (same kernels, same results):
+ *   lr_joint_keys_prepare      keys: RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre), rows j < n_pre
+ *                              copied, into workspace as bf16 [HK][Sk][128];
+ *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated in registers) over those keys and v.
+ * Useful when the keys are reused (a cached prefix) or to time the stages separately.
+ */
+int lr_joint_keys_prepare(const void* k_raw, int64_t k_row_stride, const float* k_norm_w, int table_kind,
+                          const void* k_table_a, const void* k_table_b, int64_t table_row_stride, int pairing,
+                          int rot_dim, float eps, int Sk, int HK, int n_pre, void* workspace, size_t workspace_bytes,
+                          lr_stream_t stream);
+int lr_joint_attention_prepared(const void* q_raw, const void* workspace, size_t workspace_bytes, const void* v,
+                                void* out, const float* q_norm_w, int table_kind, const void* q_table_a,
+                                const void* q_table_b, int64_t table_row_stride, int pairing, int rot_dim, float eps,
+                                int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_row_stride,
+                                int64_t v_row_stride, int64_t out_row_stride, int config, lr_stream_t stream);
+
+/* lr_joint_attention_fused with an explicit tile configuration (LR_ATTN_CFG_*). */
+int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,
+                                const float* k_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
+                                const void* k_table_a, const void* k_table_b, int64_t table_row_stride, int pairing,
+                                int rot_dim, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
+                                int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                                int64_t out_row_stride, int n_pre, void* workspace, size_t workspace_bytes, int config,
+                                lr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LR_ATTN_H */

@@ -1,0 +1,416 @@
+// Flash-style joint attention for gfx950 (CDNA4): bf16 in, fp32 MFMA accumulation and softmax, bf16 out.
+//
+// Semantics follow the reference's shipping kernel kernels/cuda/qwen_image/attention.cu:253-444 (pattn2_kernel) as
+// launched by src/engines/qwen_image/ops_launch.zig:163-172: O_i = softmax_j(scale * <q_i, k_j>) v_j over keys
+// j < nkeys (and j <= p0 + i when causal, attention.cu:304), query head h reading kv head h / (H / HK)
+// (attention.cu:264-266), keys past nkeys zero-filled and masked (attention.cu:275-276), P rounded to bf16 for the
+// PV product (attention.cu:418-424), output rounded to bf16 (attention.cu:432-443). The design is CDNA4's own:
+//
+//  * Scores are computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16_bf16 (M = 32 keys, N = 32 queries). In the
+//    32x32 accumulator layout lane l owns query column l % 32 and 16 key rows, so a row max is 15 in-register maxes
+//    plus one v_permlane32_swap with the partner lane l ^ 32; no LDS round trip, no 32-lane butterfly.
+//  * The K rows of each 32-key block are read in an order with bits 2 and 3 of the row index swapped. With that
+//    order, accumulator registers 0-7 / 8-15 of a score block are exactly the B operand (8 consecutive keys per lane
+//    half) of the next MFMA, O^T += V^T P^T: P never leaves registers.
+//  * V^T is staged into LDS by a 4x8 register transpose of coalesced 16-byte loads; both LDS tiles use XOR chunk
+//    swizzles chosen so that every ds_read_b128 (operand fetch) and ds_write (staging) touches each bank once.
+//  * Online softmax in the exp2 domain with scale*log2(e) folded into one FMA; the running max is only raised (and O
+//    rescaled) when a tile's max exceeds it by more than 2^8, so the 64-register O rescale is rare after the first
+//    tiles. Exact: every P and l use the same reference max, which cancels in O / l.
+//  * K/V tiles of 64 keys are double-buffered in LDS; the next tile's global loads are in flight during the current
+//    tile's MFMAs. Workgroups are remapped so that each XCD works on whole heads (its own L2 holds that head's K/V).
+//  * FUSEQ: the query block's per-head RMSNorm and RoPE are applied in registers before the first MFMA.
+#include "lr_common.h"
+#include "lr_kernels.h"
+
+namespace lr {
+
+namespace {
+
+constexpr int BN = 64;          // keys per tile
+constexpr float RESCALE_TAU = 8.0f;  // log2 headroom before the running max is raised
+
+__device__ __forceinline__ float wave_pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float wave_pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Row index (within a 32-key block) whose key the MFMA row m holds: bits 2 and 3 swapped.
+__device__ __forceinline__ int key_perm(int m) { return (m & 0x13) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
+// LDS element offsets (uint16 units). K tile: [64 keys][128 dims], 16-byte chunk c of row r stored at c ^ (r & 15).
+__device__ __forceinline__ int k_lds(int r, int c) { return r * D + 8 * (c ^ (r & 15)); }
+// V^T tile: [128 dims][64 keys], 16-byte chunk cc (8 keys) of row d stored at cc ^ (((d >> 1) ^ (d >> 4)) & 7).
+__device__ __forceinline__ int v_lds(int d, int cc) { return d * BN + 8 * (cc ^ (((d >> 1) ^ (d >> 4)) & 7)); }
+
+// Queries of one lane: B operand fragments for the 8 k-steps (dims 16*ks + 8*hf .. +8) of one 32-query block.
+__device__ __forceinline__ void load_q_plain(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
+    const bool valid = qrow < a.W;
+    const uint16_t* src = a.q + (int64_t)(valid ? qrow : a.W - 1) * a.q_rs + head * D + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        u32x4 w = *reinterpret_cast<const u32x4*>(src + 16 * ks);
+        if (!valid) w = u32x4{0, 0, 0, 0};
+        qf[ks] = __builtin_bit_cast(bf16x8, w);
+    }
+}
+
+// The same fragments with RMSNorm (fp32, eps, fp32 weight) and RoPE applied before a single bf16 rounding.
+// The lane and its partner (lane ^ 32) hold the two interleaved halves of the query's 128 dims.
+__device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
+    const bool valid = qrow < a.W;
+    const int row = valid ? qrow : a.W - 1;
+    const uint16_t* src = a.q + (int64_t)row * a.q_rs + head * D + 8 * hf;
+    float x[8][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        u32x4 w = *reinterpret_cast<const u32x4*>(src + 16 * ks);
+        if (!valid) w = u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[ks][2 * i] = lo_bf16(w[i]);
+            x[ks][2 * i + 1] = hi_bf16(w[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(x[ks][j], x[ks][j], ss);
+    }
+    ss = wave_pair_sum(ss);
+    const float rr = rsqrtf(ss * (1.0f / D) + a.eps);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float w = a.wq ? a.wq[16 * ks + 8 * hf + j] : 1.0f;
+            x[ks][j] = x[ks][j] * rr * w;
+        }
+    }
+    if (a.table_kind != TABLE_NONE) {
+        const int64_t toff = (int64_t)row * a.tab_stride;
+        if (a.pairing == PAIR_INTERLEAVED) {
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const int d = 16 * ks + 8 * hf + j;
+                    if (d < a.rot) {
+                        const Rot2 r = load_rot(a.table_kind, a.qta, a.qtb, toff, d >> 1);
+                        const float x0 = x[ks][j], x1 = x[ks][j + 1];
+                        x[ks][j] = fmaf(r.f00, x0, r.f01 * x1);
+                        x[ks][j + 1] = fmaf(r.f10, x0, r.f11 * x1);
+                    }
+                }
+            }
+        } else {
+            const int half_ks = a.rot >> 5;  // rot / 2 / 16 k-steps hold the first element of each pair
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                if (ks < half_ks) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int p = 16 * ks + 8 * hf + j;
+                        const Rot2 r = load_rot(a.table_kind, a.qta, a.qtb, toff, p);
+                        // the partner k-step ks + half_ks (< 8): select it without dynamic register indexing
+                        float x1 = 0.0f;
+#pragma unroll
+                        for (int k2 = 1; k2 < 8; ++k2)
+                            if (k2 == ks + half_ks) x1 = x[k2][j];
+                        const float x0 = x[ks][j];
+                        x[ks][j] = fmaf(r.f00, x0, r.f01 * x1);
+                        const float y1 = fmaf(r.f10, x0, r.f11 * x1);
+#pragma unroll
+                        for (int k2 = 1; k2 < 8; ++k2)
+                            if (k2 == ks + half_ks) x[k2][j] = y1;
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        bf16x8 f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = (bf16)x[ks][j];
+        qf[ks] = f;
+    }
+}
+
+template <int QW, int NW, bool FUSEQ>
+__global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnArgs a) {
+    constexpr int NQB = QW / 32;  // 32-query blocks per wave
+    constexpr int BM = QW * NW;   // queries per workgroup
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * D];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][D * BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 31, hf = lane >> 5;
+
+    // XCD-aware mapping: hardware workgroup b runs on XCD b % 8; give each XCD a contiguous range of logical ids
+    // (consecutive query blocks of the same head) so its L2 serves one head's K/V to all its CUs.
+    const int nwg = gridDim.x, b = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
+    const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int nqb = (a.W + BM - 1) / BM;
+    const int head = logical / nqb, qblk = logical - head * nqb;
+    const int hk = head / a.G;
+    const int row0 = qblk * BM, wrow0 = row0 + wave * QW;
+    const int last_row = min(row0 + BM, a.W) - 1;
+    int ntiles = (a.nkeys + BN - 1) / BN;
+    if (a.causal) ntiles = min(ntiles, (a.p0 + last_row) / BN + 1);
+    const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
+    const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs;
+
+    // ---- staging roles: with 4 waves every thread moves 4 K chunks and one V unit; with 8, waves 0-3 move K and
+    // waves 4-7 move V.
+    constexpr bool SPLIT = NW == 8;
+    const int st = SPLIT ? (tid & 255) : tid;           // staging thread index 0..255
+    const bool do_k = !SPLIT || wave < 4, do_v = !SPLIT || wave >= 4;
+    const int vc = st & 15, vkg = st >> 4;             // V unit: dims 8*vc..+8 of keys 4*vkg..+4
+    u32x4 kreg[4], vreg[4];
+
+    auto stage_load = [&](int t) {
+        const int key0 = t * BN;
+        if (do_k) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int u = st + 256 * i, r = u >> 4, c = u & 15;
+                const int key = key0 + r;
+                const uint16_t* p = kbase + (int64_t)min(key, a.nkeys - 1) * a.k_rs + 8 * c;
+                u32x4 w = *reinterpret_cast<const u32x4*>(p);
+                kreg[i] = key < a.nkeys ? w : u32x4{0, 0, 0, 0};
+            }
+        }
+        if (do_v) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = key0 + 4 * vkg + i;
+                const uint16_t* p = vbase + (int64_t)min(key, a.nkeys - 1) * a.v_rs + 8 * vc;
+                u32x4 w = *reinterpret_cast<const u32x4*>(p);
+                vreg[i] = key < a.nkeys ? w : u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    auto stage_store = [&](int buf) {
+        if (do_k) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int u = st + 256 * i, r = u >> 4, c = u & 15;
+                *reinterpret_cast<u32x4*>(&Ks[buf][k_lds(r, c)]) = kreg[i];
+            }
+        }
+        if (do_v) {
+            // 4 keys x 8 dims -> 8 rows of V^T (4 keys each). Lanes with odd vc write the rows in the order e ^ 1
+            // so that every store instruction spreads over both row parities (all 64 banks).
+            const bool odd = vc & 1;
+            const int cc = vkg >> 1, hh = vkg & 1;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                uint32_t lo[2], hi[2];
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const int ee = e ^ s, w = ee >> 1;
+                    if (ee & 1) {
+                        lo[s] = (vreg[0][w] >> 16) | (vreg[1][w] & 0xffff0000u);
+                        hi[s] = (vreg[2][w] >> 16) | (vreg[3][w] & 0xffff0000u);
+                    } else {
+                        lo[s] = (vreg[0][w] & 0xffffu) | (vreg[1][w] << 16);
+                        hi[s] = (vreg[2][w] & 0xffffu) | (vreg[3][w] << 16);
+                    }
+                }
+                const int ee = odd ? (e ^ 1) : e;
+                const int d = 8 * vc + ee;
+                const u32x2 val = odd ? u32x2{lo[1], hi[1]} : u32x2{lo[0], hi[0]};
+                *reinterpret_cast<u32x2*>(&Vs[buf][v_lds(d, cc) + 4 * hh]) = val;
+            }
+        }
+    };
+
+    // ---- queries
+    bf16x8 qf[NQB][8];
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+        if constexpr (FUSEQ)
+            load_q_fused(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
+        else
+            load_q_plain(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
+    }
+
+    stage_load(0);
+    stage_store(0);
+    __syncthreads();
+
+    f32x16 o[4][NQB];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb) o[db][nb] = f32x16{};
+    float m_used[NQB], l_sum[NQB];
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+        m_used[nb] = -INFINITY;
+        l_sum[nb] = 0.0f;
+    }
+
+    const int pr = key_perm(n);          // K row (within a 32-key block) this lane's A operand reads
+    const float c = a.c;
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        const bool more = t + 1 < ntiles;
+        if (more) stage_load(t + 1);
+
+        // ---- S^T = K Q^T for 64 keys x QW queries
+        f32x16 s[2][NQB];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < NQB; ++nb) s[mb][nb] = f32x16{};
+        const uint16_t* kt = Ks[buf];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+                const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kt + k_lds(32 * mb + pr, 2 * ks + hf));
+#pragma unroll
+                for (int nb = 0; nb < NQB; ++nb)
+                    s[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[nb][ks], s[mb][nb], 0, 0, 0);
+            }
+        }
+
+        // ---- mask (only tiles that reach past nkeys or, when causal, past some query's position)
+        const int key0 = t * BN;
+        const bool need_mask = key0 + BN > a.nkeys || (a.causal && key0 + BN - 1 > a.p0 + wrow0);
+        if (need_mask) {
+#pragma unroll
+            for (int nb = 0; nb < NQB; ++nb) {
+                const int pos = a.p0 + wrow0 + 32 * nb + n;
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = key0 + 32 * mb + 16 * (r >> 3) + 8 * hf + (r & 7);
+                        const bool vis = key < a.nkeys && (!a.causal || key <= pos);
+                        if (!vis) s[mb][nb][r] = -INFINITY;
+                    }
+            }
+        }
+
+        // ---- online softmax (exp2 domain), P -> bf16 B operands of the PV MFMAs
+        bf16x8 pf[NQB][4];
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb) {
+            float mx = s[0][nb][0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][nb][r]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[1][nb][r]);
+            mx = wave_pair_max(mx) * c;
+            const bool raise = mx > m_used[nb] + RESCALE_TAU;
+            if (__builtin_amdgcn_ballot_w64(raise)) {
+                const float mn = fmaxf(m_used[nb], mx);
+                // a row's first visible tile is tile 0 (key 0 is visible to every query), so m_used is finite after
+                // it; the guard keeps a (never expected) -inf - -inf from turning into NaN
+                const float alpha = m_used[nb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_used[nb] - mn);
+                l_sum[nb] *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) o[db][nb] *= alpha;
+                m_used[nb] = mn;
+            }
+            const float nm = -m_used[nb];
+            float ls = 0.0f;
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    bf16x8 f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float p = __builtin_amdgcn_exp2f(fmaf(s[mb][nb][8 * half + j], c, nm));
+                        ls += p;
+                        f[j] = (bf16)p;
+                    }
+                    pf[nb][2 * mb + half] = f;
+                }
+            }
+            l_sum[nb] += ls;
+        }
+
+        // ---- O^T += V^T P^T
+        const uint16_t* vt = Vs[buf];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vt + v_lds(32 * db + n, 2 * kk + hf));
+#pragma unroll
+                for (int nb = 0; nb < NQB; ++nb)
+                    o[db][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[nb][kk], o[db][nb], 0, 0, 0);
+            }
+        }
+
+        if (more) stage_store(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: O / l -> bf16 rows
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+        const int qrow = wrow0 + 32 * nb + n;
+        const float l = wave_pair_sum(l_sum[nb]);
+        const float inv = 1.0f / l;
+        if (qrow < a.W) {
+            uint16_t* dst = a.out + (int64_t)qrow * a.o_rs + head * D + 4 * hf;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& acc = o[db][nb];
+                    u32x2 w;
+                    w[0] = pack_bf16x2(acc[4 * g] * inv, acc[4 * g + 1] * inv);
+                    w[1] = pack_bf16x2(acc[4 * g + 2] * inv, acc[4 * g + 3] * inv);
+                    *reinterpret_cast<u32x2*>(dst + 32 * db + 8 * g) = w;
+                }
+        }
+    }
+}
+
+template <int QW, int NW, bool FUSEQ>
+hipError_t launch_cfg(const AttnArgs& a, hipStream_t stream) {
+    constexpr int BM = QW * NW;
+    const int64_t nqb = (a.W + BM - 1) / BM;
+    const int64_t blocks = nqb * a.H;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_fwd_kernel<QW, NW, FUSEQ>), dim3((unsigned)blocks), dim3(NW * 64), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int attention_block_rows(int config) {
+    switch (config) {
+        case ATTN_CFG_Q32_W4: return 128;
+        default: return 256;
+    }
+}
+
+hipError_t launch_attention(const AttnArgs& a, bool fuse_q, int config, hipStream_t stream) {
+    if (config == ATTN_CFG_AUTO) config = ATTN_CFG_Q32_W8;
+    switch (config) {
+        case ATTN_CFG_Q64_W4:
+            return fuse_q ? launch_cfg<64, 4, true>(a, stream) : launch_cfg<64, 4, false>(a, stream);
+        case ATTN_CFG_Q32_W8:
+            return fuse_q ? launch_cfg<32, 8, true>(a, stream) : launch_cfg<32, 8, false>(a, stream);
+        case ATTN_CFG_Q32_W4:
+            return fuse_q ? launch_cfg<32, 4, true>(a, stream) : launch_cfg<32, 4, false>(a, stream);
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace lr

@@ -1,0 +1,265 @@
+// The C ABI (include/lr_attn.h): argument validation, then launches on the caller's stream.
+// Like kernels/cuda/minimax/kitchen_launch.cu:193-316 every function checks its arguments before launching and
+// returns an int error code; nothing here synchronises, allocates or keeps state between calls.
+#include <limits.h>
+#include <math.h>
+#include <string.h>
+
+#include "../../include/lr_attn.h"
+#include "lr_common.h"
+#include "lr_kernels.h"
+
+namespace {
+
+constexpr int ERR_ARGS = (int)hipErrorInvalidValue;
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// A bf16 rows tensor: 16-byte aligned base, row stride a multiple of 8 elements and wide enough for its heads.
+inline bool rows_ok(const void* p, int64_t rs, int heads) {
+    return p && aligned(p, 16) && rs % 8 == 0 && rs >= (int64_t)heads * lr::D;
+}
+
+inline bool scale_ok(float s) { return s > 0.0f && isfinite(s); }
+
+int attention_impl(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK, int nkeys,
+                   int causal, float scale, int64_t q_rs, int64_t k_rs, int64_t v_rs, int64_t o_rs, int64_t k_hs,
+                   int64_t v_hs, int config, hipStream_t stream) {
+    if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || nkeys < 1 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
+    if (!scale_ok(scale) || config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_Q32_W4) return ERR_ARGS;
+    if ((int64_t)p0 + W > INT_MAX - 512 || nkeys > INT_MAX - 512 || W > INT_MAX - 512) return ERR_ARGS;
+    if (!rows_ok(q, q_rs, H) || !rows_ok(out, o_rs, H)) return ERR_ARGS;
+    if (!k || !v || !aligned(k, 16) || !aligned(v, 16) || k_rs % 8 || v_rs % 8 || k_hs % 8 || v_hs % 8) return ERR_ARGS;
+    if (k_rs < lr::D || v_rs < lr::D || k_hs < 0 || v_hs < 0) return ERR_ARGS;
+    lr::AttnArgs a{};
+    a.q = static_cast<const uint16_t*>(q);
+    a.k = static_cast<const uint16_t*>(k);
+    a.v = static_cast<const uint16_t*>(v);
+    a.out = static_cast<uint16_t*>(out);
+    a.q_rs = q_rs; a.k_rs = k_rs; a.v_rs = v_rs; a.o_rs = o_rs;
+    a.k_hs = k_hs; a.v_hs = v_hs;
+    a.W = W; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = nkeys; a.p0 = p0; a.causal = causal;
+    a.c = scale * 1.4426950408889634f;
+    a.table_kind = lr::TABLE_NONE;
+    return (int)lr::launch_attention(a, false, config, stream);
+}
+
+// Table checks shared by the rope entry points. rows_needed: table rows that will be read.
+bool table_ok(int kind, const void* ta, const void* tb, int64_t stride, int rot, int pairing, int split_mod) {
+    if (kind == LR_TABLE_NONE) return true;
+    if (kind < LR_TABLE_NONE || kind > LR_TABLE_MAT2_F32) return false;
+    if (rot <= 0 || rot > lr::D || rot % 2) return false;
+    if (pairing != LR_PAIR_INTERLEAVED && pairing != LR_PAIR_SPLIT_HALF) return false;
+    if (pairing == LR_PAIR_SPLIT_HALF && rot % split_mod) return false;
+    if (!ta || stride < 0) return false;
+    const int pairs = rot / 2;
+    if (kind == LR_TABLE_COSSIN_F32) return tb && aligned(ta, 4) && aligned(tb, 4) && stride >= pairs;
+    if (kind == LR_TABLE_MAT2_BF16) return aligned(ta, 8) && stride % 4 == 0 && stride >= 4 * pairs;
+    return aligned(ta, 16) && stride % 4 == 0 && stride >= 4 * pairs;  // LR_TABLE_MAT2_F32
+}
+
+// Shared checks of the fused op's two stages.
+int keys_impl(const void* k_raw, int64_t k_rs, const float* wk, int table_kind, const void* kta, const void* ktb,
+              int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK, int n_pre, void* ws,
+              size_t ws_bytes, hipStream_t stream) {
+    if (rot == 0) rot = lr::D;
+    if (Sk < 1 || HK < 1 || Sk > INT_MAX - 512 || n_pre < 0 || n_pre > Sk || !(eps >= 0.0f) || !isfinite(eps))
+        return ERR_ARGS;
+    if (!rows_ok(k_raw, k_rs, HK) || (wk && !aligned(wk, 4))) return ERR_ARGS;
+    if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
+    const size_t need = lr_joint_attention_workspace_bytes(Sk, HK);
+    if (!ws || !aligned(ws, 256) || ws_bytes < need) return ERR_ARGS;
+    lr::RopeArgs r{};
+    r.src = static_cast<const uint16_t*>(k_raw);
+    r.dst = static_cast<uint16_t*>(ws);
+    r.src_rs = k_rs; r.src_hs = lr::D;
+    r.dst_rs = lr::D; r.dst_hs = (int64_t)Sk * lr::D;
+    r.rows = Sk; r.heads = HK; r.n_copy = n_pre;
+    r.weight_kind = wk ? lr::W_F32 : lr::W_NONE; r.w = wk;
+    r.table_kind = Sk > n_pre ? table_kind : lr::TABLE_NONE; r.pairing = pairing; r.rot = rot;
+    r.ta = kta; r.tb = ktb; r.tab_stride = tab_stride;
+    r.eps = eps; r.round_norm = 0;
+    return (int)lr::launch_rms_rope(r, stream);
+}
+
+int prepared_impl(const void* q_raw, const void* ws, size_t ws_bytes, const void* v, void* out, const float* wq,
+                  int table_kind, const void* qta, const void* qtb, int64_t tab_stride, int pairing, int rot, float eps,
+                  int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_rs, int64_t v_rs,
+                  int64_t o_rs, int config, hipStream_t stream) {
+    if (rot == 0) rot = lr::D;
+    if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
+    if (!(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return ERR_ARGS;
+    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_Q32_W4) return ERR_ARGS;
+    if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return ERR_ARGS;
+    if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H) || !rows_ok(v, v_rs, HK)) return ERR_ARGS;
+    if (!table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) || (wq && !aligned(wq, 4))) return ERR_ARGS;
+    if (!ws || !aligned(ws, 256) || ws_bytes < lr_joint_attention_workspace_bytes(Sk, HK)) return ERR_ARGS;
+    lr::AttnArgs a{};
+    a.q = static_cast<const uint16_t*>(q_raw);
+    a.k = static_cast<const uint16_t*>(ws);
+    a.v = static_cast<const uint16_t*>(v);
+    a.out = static_cast<uint16_t*>(out);
+    a.q_rs = q_rs; a.k_rs = lr::D; a.v_rs = v_rs; a.o_rs = o_rs;
+    a.k_hs = (int64_t)Sk * lr::D; a.v_hs = lr::D;
+    a.W = Sq; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = Sk; a.p0 = p0; a.causal = causal;
+    a.c = scale * 1.4426950408889634f;
+    a.wq = wq;
+    a.table_kind = table_kind; a.pairing = pairing; a.rot = rot;
+    a.qta = qta; a.qtb = qtb; a.tab_stride = tab_stride; a.eps = eps;
+    return (int)lr::launch_attention(a, true, config, stream);
+}
+
+int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, const float* wq, const float* wk,
+               int table_kind, const void* qta, const void* qtb, const void* kta, const void* ktb, int64_t tab_stride,
+               int pairing, int rot, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
+               int64_t q_rs, int64_t k_rs, int64_t v_rs, int64_t o_rs, int n_pre, void* ws, size_t ws_bytes,
+               int config, hipStream_t stream) {
+    // validate both stages before launching either
+    if (rot == 0) rot = lr::D;
+    if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
+    if (n_pre < 0 || n_pre > Sk || !(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return ERR_ARGS;
+    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_Q32_W4) return ERR_ARGS;
+    if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return ERR_ARGS;
+    if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H) || !rows_ok(k_raw, k_rs, HK) || !rows_ok(v, v_rs, HK))
+        return ERR_ARGS;
+    if (!table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
+    if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
+    if ((wq && !aligned(wq, 4)) || (wk && !aligned(wk, 4))) return ERR_ARGS;
+    if (!ws || !aligned(ws, 256) || ws_bytes < lr_joint_attention_workspace_bytes(Sk, HK)) return ERR_ARGS;
+    const int e = keys_impl(k_raw, k_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws,
+                            ws_bytes, stream);
+    if (e != 0) return e;
+    return prepared_impl(q_raw, ws, ws_bytes, v, out, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, Sk,
+                         H, HK, p0, causal, scale, q_rs, v_rs, o_rs, config, stream);
+}
+
+int rope_impl(const void* src, int64_t src_rs, int64_t src_off, void* dst, int64_t dst_rs, int64_t n, int b,
+              int64_t src_bs, int64_t dst_bs, int heads, const void* w, int w_kind, int table_kind, const void* ta,
+              const void* tb, int64_t tab_stride, int rot, int pairing, float eps, int round_norm,
+              hipStream_t stream) {
+    if (rot == 0) rot = lr::D;
+    if (n < 1 || b < 1 || heads < 1 || !(eps >= 0.0f) || !isfinite(eps) || (round_norm != 0 && round_norm != 1))
+        return ERR_ARGS;
+    if (w_kind < LR_WEIGHT_NONE || w_kind > LR_WEIGHT_BF16 || (w_kind != LR_WEIGHT_NONE && !w)) return ERR_ARGS;
+    if (w && !aligned(w, w_kind == LR_WEIGHT_F32 ? 4 : 2)) return ERR_ARGS;
+    if (!table_ok(table_kind, ta, tb, tab_stride, rot, pairing, 16)) return ERR_ARGS;
+    if (!src || !dst || src_off < 0 || src_off % 8 || src_bs % 8 || dst_bs % 8) return ERR_ARGS;
+    const char* s0 = static_cast<const char*>(src) + src_off * 2;
+    if (!rows_ok(s0, src_rs, heads) || !rows_ok(dst, dst_rs, heads)) return ERR_ARGS;
+    if (n > ((int64_t)1 << 40) / heads) return ERR_ARGS;
+    for (int bi = 0; bi < b; ++bi) {
+        lr::RopeArgs r{};
+        r.src = reinterpret_cast<const uint16_t*>(s0) + (int64_t)bi * src_bs;
+        r.dst = static_cast<uint16_t*>(dst) + (int64_t)bi * dst_bs;
+        r.src_rs = src_rs; r.src_hs = lr::D; r.dst_rs = dst_rs; r.dst_hs = lr::D;
+        r.rows = n; r.heads = heads; r.n_copy = 0;
+        r.weight_kind = w_kind; r.w = w;
+        r.table_kind = table_kind; r.pairing = pairing; r.rot = rot;
+        r.ta = ta; r.tb = tb; r.tab_stride = tab_stride;
+        r.eps = eps; r.round_norm = round_norm;
+        const hipError_t e = lr::launch_rms_rope(r, stream);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lr_attn_abi_version(void) { return LR_ATTN_ABI_VERSION; }
+
+int lr_attn_init(void) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return (int)e;
+    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 0 : (int)hipErrorInvalidDevice;
+}
+
+int lr_attention_bf16(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK, int nkeys,
+                      int causal, float scale, int64_t q_row_stride, int64_t kv_row_stride, int64_t out_row_stride,
+                      lr_stream_t stream) {
+    if (kv_row_stride < (int64_t)HK * lr::D) return ERR_ARGS;
+    return attention_impl(q, k, v, out, p0, W, H, HK, nkeys, causal, scale, q_row_stride, kv_row_stride,
+                          kv_row_stride, out_row_stride, lr::D, lr::D, LR_ATTN_CFG_AUTO, stream);
+}
+
+int lr_attention_bf16_ex(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK,
+                         int nkeys, int causal, float scale, int64_t q_row_stride, int64_t k_row_stride,
+                         int64_t v_row_stride, int64_t out_row_stride, int64_t k_head_stride, int64_t v_head_stride,
+                         int config, lr_stream_t stream) {
+    return attention_impl(q, k, v, out, p0, W, H, HK, nkeys, causal, scale, q_row_stride, k_row_stride, v_row_stride,
+                          out_row_stride, k_head_stride, v_head_stride, config, stream);
+}
+
+int lr_rms_rope_bf16(const void* src, int64_t src_row_stride, int64_t src_off, void* dst, int64_t dst_row_stride,
+                     int64_t n, int b, int64_t src_b_stride, int64_t dst_b_stride, int heads, const void* w, int w_kind,
+                     int table_kind, const void* table_a, const void* table_b, int64_t table_row_stride, int rot_dim,
+                     int pairing, float eps, int round_norm, lr_stream_t stream) {
+    return rope_impl(src, src_row_stride, src_off, dst, dst_row_stride, n, b, src_b_stride, dst_b_stride, heads, w,
+                     w_kind, table_kind, table_a, table_b, table_row_stride, rot_dim, pairing, eps, round_norm, stream);
+}
+
+int lr_rms_rope_qk_bf16(void* q, void* k, int64_t seq, int heads, int64_t q_row_stride, int64_t k_row_stride,
+                        const void* q_norm, const void* k_norm, const void* freqs, int64_t freqs_row_stride,
+                        int rot_dim, float eps, lr_stream_t stream) {
+    if (!q_norm || !k_norm || !freqs) return ERR_ARGS;
+    int e = rope_impl(q, q_row_stride, 0, q, q_row_stride, seq, 1, 0, 0, heads, q_norm, LR_WEIGHT_BF16,
+                      LR_TABLE_MAT2_BF16, freqs, nullptr, freqs_row_stride, rot_dim, LR_PAIR_SPLIT_HALF, eps, 1, stream);
+    if (e != 0) return e;
+    return rope_impl(k, k_row_stride, 0, k, k_row_stride, seq, 1, 0, 0, heads, k_norm, LR_WEIGHT_BF16,
+                     LR_TABLE_MAT2_BF16, freqs, nullptr, freqs_row_stride, rot_dim, LR_PAIR_SPLIT_HALF, eps, 1, stream);
+}
+
+size_t lr_joint_attention_workspace_bytes(int Sk, int HK) {
+    if (Sk < 1 || HK < 1) return 0;
+    const size_t bytes = (size_t)Sk * (size_t)HK * lr::D * 2;
+    return (bytes + 255) & ~(size_t)255;
+}
+
+int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,
+                             const float* k_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
+                             const void* k_table_a, const void* k_table_b, int64_t table_row_stride, int pairing,
+                             int rot_dim, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
+                             int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride, int64_t out_row_stride,
+                             int n_pre, void* workspace, size_t workspace_bytes, lr_stream_t stream) {
+    return fused_impl(q_raw, k_raw, v, out, q_norm_w, k_norm_w, table_kind, q_table_a, q_table_b, k_table_a, k_table_b,
+                      table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale, q_row_stride,
+                      k_row_stride, v_row_stride, out_row_stride, n_pre, workspace, workspace_bytes, LR_ATTN_CFG_AUTO,
+                      stream);
+}
+
+int lr_joint_keys_prepare(const void* k_raw, int64_t k_row_stride, const float* k_norm_w, int table_kind,
+                          const void* k_table_a, const void* k_table_b, int64_t table_row_stride, int pairing,
+                          int rot_dim, float eps, int Sk, int HK, int n_pre, void* workspace, size_t workspace_bytes,
+                          lr_stream_t stream) {
+    return keys_impl(k_raw, k_row_stride, k_norm_w, table_kind, k_table_a, k_table_b, table_row_stride, pairing,
+                     rot_dim, eps, Sk, HK, n_pre, workspace, workspace_bytes, stream);
+}
+
+int lr_joint_attention_prepared(const void* q_raw, const void* workspace, size_t workspace_bytes, const void* v,
+                                void* out, const float* q_norm_w, int table_kind, const void* q_table_a,
+                                const void* q_table_b, int64_t table_row_stride, int pairing, int rot_dim, float eps,
+                                int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_row_stride,
+                                int64_t v_row_stride, int64_t out_row_stride, int config, lr_stream_t stream) {
+    return prepared_impl(q_raw, workspace, workspace_bytes, v, out, q_norm_w, table_kind, q_table_a, q_table_b,
+                         table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale, q_row_stride,
+                         v_row_stride, out_row_stride, config, stream);
+}
+
+int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,
+                                const float* k_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
+                                const void* k_table_a, const void* k_table_b, int64_t table_row_stride, int pairing,
+                                int rot_dim, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
+                                int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                                int64_t out_row_stride, int n_pre, void* workspace, size_t workspace_bytes, int config,
+                                lr_stream_t stream) {
+    return fused_impl(q_raw, k_raw, v, out, q_norm_w, k_norm_w, table_kind, q_table_a, q_table_b, k_table_a, k_table_b,
+                      table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale, q_row_stride,
+                      k_row_stride, v_row_stride, out_row_stride, n_pre, workspace, workspace_bytes, config, stream);
+}
+
+}  // extern "C"

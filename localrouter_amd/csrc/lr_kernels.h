@@ -1,0 +1,57 @@
+// Internal launch interface between the C ABI (lr_abi.hip) and the kernels (attn_fwd.hip, rms_rope.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lr {
+
+// Everything the attention kernel reads, by value (one kernel argument).
+struct AttnArgs {
+    const uint16_t* q;   // bf16 [W][...] rows, head h at h*128 (+ row stride q_rs)
+    const uint16_t* k;   // bf16 keys: key j of kv head g at k + g*k_hs + j*k_rs
+    const uint16_t* v;   // bf16 values, same addressing with v_hs / v_rs
+    uint16_t* out;       // bf16 [W][...] rows, head h at h*128 (+ row stride o_rs)
+    int64_t q_rs, k_rs, v_rs, o_rs;  // row strides (elements)
+    int64_t k_hs, v_hs;              // kv-head strides (elements)
+    int W, H, HK, G, nkeys, p0, causal;
+    float c;                          // scale * log2(e)
+    // Fused Q RMSNorm + RoPE (used by the FUSEQ kernels only)
+    const float* wq;                  // fp32 [128] norm weight, or null for ones
+    int table_kind, pairing, rot;
+    const void* qta;                  // table (see TableKind), query row i uses table row i
+    const void* qtb;
+    int64_t tab_stride;               // table row stride (elements)
+    float eps;
+};
+
+// The per-(row, head) RMSNorm + RoPE pass.
+struct RopeArgs {
+    const uint16_t* src;  // bf16, row r head h at src + r*src_rs + h*src_hs
+    uint16_t* dst;        // bf16, row r head h at dst + r*dst_rs + h*dst_hs (may equal src: in place)
+    int64_t src_rs, src_hs, dst_rs, dst_hs;
+    int64_t rows;
+    int heads;
+    int n_copy;           // leading rows copied unchanged (already normalised and rotated)
+    int weight_kind;      // WeightKind
+    const void* w;        // [128] fp32 or bf16
+    int table_kind, pairing, rot;
+    const void* ta;       // row r >= n_copy uses table row r - n_copy
+    const void* tb;
+    int64_t tab_stride;
+    float eps;
+    int round_norm;       // 1: round the normalised value to bf16 before the rotation
+};
+
+// Attention tile configurations (queries per wave x waves per workgroup).
+enum AttnConfig : int {
+    ATTN_CFG_AUTO = 0,
+    ATTN_CFG_Q64_W4 = 1,   // 64 queries/wave, 4 waves: 256-query blocks, one wave per SIMD
+    ATTN_CFG_Q32_W8 = 2,   // 32 queries/wave, 8 waves: 256-query blocks, two waves per SIMD
+    ATTN_CFG_Q32_W4 = 3,   // 32 queries/wave, 4 waves: 128-query blocks
+};
+
+hipError_t launch_attention(const AttnArgs& a, bool fuse_q, int config, hipStream_t stream);
+hipError_t launch_rms_rope(const RopeArgs& a, hipStream_t stream);
+int attention_block_rows(int config);
+
+}  // namespace lr

@@ -1,0 +1,151 @@
+"""torch-facing host interface, mirroring the reference engine's kernel bindings.
+
+  attention(...)        <- Ops.attention, src/engines/qwen_image/ops_launch.zig:163-172
+  rms_rope(...)         <- Triton.ropeRun + Rope, src/engines/qwen_image/triton_k.zig:44-53
+  rms_rope_qk(...)      <- Kitchen.rmsRope, src/engines/minimax_h3/launch.zig:421-441
+  joint_attention(...)  <- Dit.block's rope_q / rope_k / V copy / attention chain, src/engines/qwen_image/dit.zig:252-293
+
+Every call validates shapes on the host, then goes through the C ABI (liblr_attn.so) on torch's current HIP stream.
+torch supplies device memory and the stream handle only; all compute is the library's HIP kernels.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+D = 128
+TABLE_NONE, TABLE_COSSIN_F32, TABLE_MAT2_BF16, TABLE_MAT2_F32 = 0, 1, 2, 3
+PAIR_INTERLEAVED, PAIR_SPLIT_HALF = 0, 1
+WEIGHT_NONE, WEIGHT_F32, WEIGHT_BF16 = 0, 1, 2
+CFG_AUTO, CFG_Q64_W4, CFG_Q32_W8, CFG_Q32_W4 = 0, 1, 2, 3
+SCALE_128 = float(torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32))  # f32 1/sqrt(128) = 0x3DB504F3
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _rows(t: torch.Tensor, name: str, heads: int | None = None) -> int:
+    """A bf16 CUDA tensor viewed as rows [n, heads, 128] with unit stride inside a row; returns its row stride."""
+    if not t.is_cuda or t.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: expected a bf16 tensor on the GPU, got {t.dtype} on {t.device}")
+    if t.dim() == 3:
+        n, h, d = t.shape
+        if d != D or t.stride(2) != 1 or (h > 1 and t.stride(1) != D):
+            raise ValueError(f"{name}: expected [n, heads, 128] with contiguous heads, got {tuple(t.shape)} / {t.stride()}")
+        if heads is not None and h != heads:
+            raise ValueError(f"{name}: {h} heads, expected {heads}")
+        return t.stride(0)
+    if t.dim() == 2:
+        if t.stride(1) != 1:
+            raise ValueError(f"{name}: rows must be contiguous")
+        return t.stride(0)
+    raise ValueError(f"{name}: expected a 2-D or 3-D tensor")
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *, w: int | None = None,
+              heads: int | None = None, kv_heads: int | None = None, nkeys: int | None = None, causal: bool = False,
+              p0: int = 0, scale: float = SCALE_128, config: int = CFG_AUTO) -> torch.Tensor:
+    """q [w, heads, 128], k / v [>= nkeys, kv_heads, 128] -> out [w, heads, 128] (bf16 rows; query head h reads kv
+    head h / (heads / kv_heads)); causal: query i (position p0 + i) sees keys 0..p0 + i, else all nkeys keys."""
+    w = q.shape[0] if w is None else w
+    heads = q.shape[1] if heads is None else heads
+    kv_heads = k.shape[1] if kv_heads is None else kv_heads
+    nkeys = k.shape[0] if nkeys is None else nkeys
+    q_rs = _rows(q, "q", heads)
+    k_rs = _rows(k, "k", kv_heads)
+    v_rs = _rows(v, "v", kv_heads)
+    if out is None:
+        out = torch.empty((w, heads, D), dtype=torch.bfloat16, device=q.device)
+    o_rs = _rows(out, "out", heads)
+    if k.shape[0] < nkeys or v.shape[0] < nkeys or q.shape[0] < w or out.shape[0] < w:
+        raise ValueError("attention: tensors shorter than w / nkeys")
+    _lib.call("lr_attention_bf16_ex", _ptr(q), _ptr(k), _ptr(v), _ptr(out), p0, w, heads, kv_heads, nkeys,
+              int(causal), scale, q_rs, k_rs, v_rs, o_rs, D, D, config, _stream())
+    return out
+
+
+def rms_rope(src: torch.Tensor, dst: torch.Tensor, w: torch.Tensor | None, *, n: int, heads: int, b: int = 1,
+             src_row_stride: int, src_off: int = 0, dst_row_stride: int, src_b_stride: int = 0,
+             dst_b_stride: int = 0, table_kind: int = TABLE_COSSIN_F32, table_a: torch.Tensor | None = None,
+             table_b: torch.Tensor | None = None, table_row_stride: int | None = None, rot: int = 128,
+             pairing: int = PAIR_INTERLEAVED, eps: float = 1e-6, round_norm: bool = False) -> torch.Tensor:
+    """Triton.ropeRun's contract with element strides: dst[bi, r, h] = rope(rmsnorm(src[bi*sb + r*srs + off + h*128]))."""
+    for t, nm in ((src, "src"), (dst, "dst")):
+        if not t.is_cuda or t.dtype != torch.bfloat16:
+            raise ValueError(f"{nm}: expected bf16 on the GPU")
+    w_kind = WEIGHT_NONE if w is None else (WEIGHT_F32 if w.dtype == torch.float32 else WEIGHT_BF16)
+    if w is not None and (w.numel() < D or not w.is_contiguous()):
+        raise ValueError("w: expected a contiguous [128] tensor")
+    if table_row_stride is None:
+        table_row_stride = 0 if table_a is None else table_a.stride(0)
+    _lib.call("lr_rms_rope_bf16", _ptr(src), src_row_stride, src_off, _ptr(dst), dst_row_stride, n, b, src_b_stride,
+              dst_b_stride, heads, _ptr(w), w_kind, table_kind, _ptr(table_a), _ptr(table_b), table_row_stride, rot,
+              pairing, eps, int(round_norm), _stream())
+    return dst
+
+
+def rms_rope_qk(q: torch.Tensor, k: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor, freqs: torch.Tensor, *,
+                heads: int, seq: int, rot: int = 96, eps: float = 1e-5) -> None:
+    """Kitchen.rmsRope: q, k [seq, heads, 128] views (packed qkv allowed) normalised and rotated in place with bf16
+    weights and a bf16 [seq, rot/2, 2, 2] table (split-half pairs)."""
+    q_rs = _rows(q, "q", heads)
+    k_rs = _rows(k, "k", heads)
+    if freqs.dtype != torch.bfloat16 or q_norm.dtype != torch.bfloat16 or k_norm.dtype != torch.bfloat16:
+        raise ValueError("rms_rope_qk: bf16 weights and table expected")
+    f_rs = freqs.stride(0)
+    _lib.call("lr_rms_rope_qk_bf16", _ptr(q), _ptr(k), seq, heads, q_rs, k_rs, _ptr(q_norm), _ptr(k_norm),
+              _ptr(freqs), f_rs, rot, eps, _stream())
+
+
+def workspace_bytes(sk: int, kv_heads: int) -> int:
+    return int(_lib.load().lr_joint_attention_workspace_bytes(sk, kv_heads))
+
+
+def joint_attention(q_raw: torch.Tensor, k_raw: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *,
+                    q_norm: torch.Tensor | None = None, k_norm: torch.Tensor | None = None,
+                    table_kind: int = TABLE_COSSIN_F32, q_table: tuple | None = None, k_table: tuple | None = None,
+                    pairing: int = PAIR_INTERLEAVED, rot: int = 128, eps: float = 1e-6, causal: bool = False,
+                    p0: int = 0, scale: float = SCALE_128, n_pre: int = 0, workspace: torch.Tensor | None = None,
+                    config: int = CFG_AUTO) -> torch.Tensor:
+    """The fused op: per-head QK-RMSNorm + RoPE + attention. q_raw [Sq, H, 128], k_raw / v [Sk, HK, 128] bf16 rows;
+    q_table / k_table = (table_a, table_b) (table_b None for the 2x2 kinds; k_table defaults to q_table)."""
+    Sq, H = q_raw.shape[0], q_raw.shape[1]
+    Sk, HK = k_raw.shape[0], k_raw.shape[1]
+    q_rs, k_rs, v_rs = _rows(q_raw, "q_raw", H), _rows(k_raw, "k_raw", HK), _rows(v, "v", HK)
+    if v.shape[0] < Sk:
+        raise ValueError("v shorter than k")
+    if out is None:
+        out = torch.empty((Sq, H, D), dtype=torch.bfloat16, device=q_raw.device)
+    o_rs = _rows(out, "out", H)
+    for t, nm in ((q_norm, "q_norm"), (k_norm, "k_norm")):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != D):
+            raise ValueError(f"{nm}: expected fp32 [128]")
+    qa = qb = ka = kb = None
+    stride = 0
+    if table_kind != TABLE_NONE:
+        if q_table is None:
+            raise ValueError("joint_attention: q_table required")
+        k_table = q_table if k_table is None else k_table
+        qa, qb = q_table
+        ka, kb = k_table
+        stride = qa.stride(0)
+        if ka.stride(0) != stride:
+            raise ValueError("q and k tables must share a row stride")
+    need = workspace_bytes(Sk, HK)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q_raw.device)
+    if workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace: {need} bytes needed")
+    _lib.call("lr_joint_attention_fused_ex", _ptr(q_raw), _ptr(k_raw), _ptr(v), _ptr(out), _ptr(q_norm),
+              _ptr(k_norm), table_kind, _ptr(qa), _ptr(qb), _ptr(ka), _ptr(kb), stride, pairing, rot, eps, Sq, Sk, H,
+              HK, p0, int(causal), scale, q_rs, k_rs, v_rs, o_rs, n_pre, _ptr(workspace),
+              workspace.numel() * workspace.element_size(), config, _stream())
+    return out

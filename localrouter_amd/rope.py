@@ -1,0 +1,164 @@
+"""Host-side RoPE tables for the joint-attention path (numpy; built once per shape, then uploaded).
+
+Three families:
+
+* Qwen-Image (src/engines/qwen_image/rope.zig:7-45, tools/twin/stk_twin/dit.py:67-88): ids [N, 3] = (frame or
+  position, row, column); axes of 16 / 56 / 56 dims; omega_j = theta^(-2j/d_axis) per axis (the 64 values frozen in
+  kernels/qwen_image/rope_omega.json); angle = id * omega in f64, sin/cos in f64 rounded to f32; cos, sin [N, 64]
+  fp32, interleaved pairs (LR_TABLE_COSSIN_F32).
+* MiniMax H3 (src/engines/minimax_h3/layout.zig:60-134): positions (t, h, w) in f64 for the packed
+  [text | cond | audio | video] layout; angle = f32(pos) * inv_freq[j] (16 shared frequencies) in f32, sin/cos in f64
+  rounded to f32 then bf16; table [S, 48, 2, 2] = [c, -s, s, c] (LR_TABLE_MAT2_BF16), split-half pairs, rot 96.
+* The synthetic BASELINE shapes (the build's own definition, the reference has no such configs): 2D grid tables for
+  the 1024-token and 4096-token images, the three-frame edit layout, and the 3D video grid; text tokens un-rotated.
+
+The reference's portable sincos (src/engines/qwen_image/smath.zig:40-52) agrees with libm to 4e-15 (its own test,
+smath.zig:128-135); these builders use numpy's float64 sin/cos, which can differ from it in the last f64 bit only.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+QWEN_AXES = (16, 56, 56)
+QWEN_THETA = 10000.0
+H3_FRAME_PER_TOKEN = (1.0, 4.0, 4.0, 4.0, 4.0)   # layout.zig:12
+H3_FRAME_RESCALE = 5.0 / 3.0                      # layout.zig:13
+
+
+def axis_omegas(d: int, theta: float = QWEN_THETA) -> np.ndarray:
+    """omega_j = 1 / theta^(2j/d), j < d/2, in f64."""
+    j = np.arange(d // 2, dtype=np.float64)
+    return 1.0 / np.power(np.float64(theta), 2.0 * j / d)
+
+
+def qwen_omegas(axes=QWEN_AXES, theta: float = QWEN_THETA) -> np.ndarray:
+    """The 64 Qwen-Image frequencies, axis by axis (rope_omega.json's rule)."""
+    return np.concatenate([axis_omegas(d, theta) for d in axes])
+
+
+def qwen_text_ids(n: int, first: int = 0) -> np.ndarray:
+    """rope.zig:11-13: position p on all three axes."""
+    p = np.arange(first, first + n, dtype=np.float32)
+    return np.stack([p, p, p], axis=1)
+
+
+def qwen_image_ids(h: int, w: int, pos: int, target_h: int | None = None, target_w: int | None = None) -> np.ndarray:
+    """rope.zig:16-28: frame `pos`, centred rows and columns (half-pixel shifted for odd sides), f32 [h*w, 3]."""
+    target_h = h if target_h is None else target_h
+    target_w = w if target_w is None else target_w
+    fh, fw = np.float32(h), np.float32(w)
+    sh = -(fh - np.float32(h // 2)) + np.float32(0.5) * (np.float32(h % 2) - np.float32(target_h % 2))
+    sw = -(fw - np.float32(w // 2)) + np.float32(0.5) * (np.float32(w % 2) - np.float32(target_w % 2))
+    yy, xx = np.meshgrid(np.arange(h, dtype=np.float32), np.arange(w, dtype=np.float32), indexing="ij")
+    ids = np.empty((h * w, 3), dtype=np.float32)
+    ids[:, 0] = np.float32(pos)
+    ids[:, 1] = (yy + sh).reshape(-1)
+    ids[:, 2] = (xx + sw).reshape(-1)
+    return ids
+
+
+def qwen_table(ids: np.ndarray, om: np.ndarray | None = None, axes=QWEN_AXES):
+    """rope.zig:31-45: cos, sin [N, 64] f32 from ids [N, 3] (angle = f64(id) * omega in f64)."""
+    om = qwen_omegas(axes) if om is None else np.asarray(om, np.float64)
+    cols = np.concatenate([np.full(d // 2, ax) for ax, d in enumerate(axes)])
+    ang = ids.astype(np.float64)[:, cols] * om[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def identity_rows(n: int, pairs: int = 64):
+    """cos = 1, sin = 0 rows: tokens that are not rotated."""
+    return np.ones((n, pairs), np.float32), np.zeros((n, pairs), np.float32)
+
+
+def grid2d_table(n_text: int, gh: int, gw: int, theta: float = QWEN_THETA):
+    """BASELINE's "2D RoPE, split h/w halves": interleaved pairs; pairs 0-31 (dims 0-63) rotate by the grid row r,
+    pairs 32-63 (dims 64-127) by the column c, omega_j = theta^(-2j/64) for both; text rows first, un-rotated.
+    Returns cos, sin [n_text + gh*gw, 64] f32."""
+    om = axis_omegas(64, theta)                                   # 32 values
+    r, c = np.meshgrid(np.arange(gh, dtype=np.float64), np.arange(gw, dtype=np.float64), indexing="ij")
+    ang = np.concatenate([r.reshape(-1, 1) * om[None, :], c.reshape(-1, 1) * om[None, :]], axis=1)
+    tc, ts = identity_rows(n_text)
+    return (np.concatenate([tc, np.cos(ang).astype(np.float32)]),
+            np.concatenate([ts, np.sin(ang).astype(np.float32)]))
+
+
+def edit_table(n_text: int, frames: int, gh: int, gw: int):
+    """BASELINE's image-edit layout: text (un-rotated), then `frames` gh x gw latents, latent f on frame axis f, rows
+    and columns centred as rope.imageIds does; Qwen axes 16/56/56. cos, sin [n_text + frames*gh*gw, 64] f32."""
+    ids = np.concatenate([qwen_image_ids(gh, gw, f) for f in range(frames)])
+    c, s = qwen_table(ids)
+    tc, ts = identity_rows(n_text)
+    return np.concatenate([tc, c]), np.concatenate([ts, s])
+
+
+def video3d_table(n_text: int, t: int, gh: int, gw: int, dims=(32, 48, 48), theta: float = QWEN_THETA):
+    """BASELINE's video layout: text (un-rotated), then t x gh x gw tokens (frame-major); t/h/w take 32/48/48 dims
+    (16/24/24 interleaved pairs), omega_{a,j} = theta^(-2j/d_a), integer positions. cos, sin [n_text + t*gh*gw, 64]."""
+    om = np.concatenate([axis_omegas(d, theta) for d in dims])
+    cols = np.concatenate([np.full(d // 2, ax) for ax, d in enumerate(dims)])
+    tt, yy, xx = np.meshgrid(np.arange(t, dtype=np.float64), np.arange(gh, dtype=np.float64),
+                             np.arange(gw, dtype=np.float64), indexing="ij")
+    pos = np.stack([tt.reshape(-1), yy.reshape(-1), xx.reshape(-1)], axis=1)
+    n = pos.shape[0]
+    cos = np.empty((n_text + n, 64), np.float32)
+    sin = np.empty((n_text + n, 64), np.float32)
+    cos[:n_text], sin[:n_text] = identity_rows(n_text)
+    step = 1 << 16                                                # chunked: 172k x 64 angles at a time is fine,
+    for i in range(0, n, step):                                   # but keep the f64 temporaries small
+        ang = pos[i:i + step][:, cols] * om[None, :]
+        cos[n_text + i:n_text + i + step] = np.cos(ang)
+        sin[n_text + i:n_text + i + step] = np.sin(ang)
+    return cos, sin
+
+
+# ------------------------------------------------------------------------------------------------ MiniMax H3
+def _h3_axis(dim: int, area: float, i: np.ndarray) -> np.ndarray:
+    """layout.zig:78-82: (i * (ratio / n) + (1 - ratio) / 2) * 32, ratio = dim / area, n = dim / 2, in f64."""
+    ratio = np.float64(dim) / area
+    n = np.float64(dim // 2)
+    return (i.astype(np.float64) * (ratio / n) + (1.0 - ratio) / 2.0) * 32.0
+
+
+def h3_positions(l: int, t: int, h: int, w: int, a: int, first_frame: bool = False) -> np.ndarray:
+    """layout.zig:85-115: positions [S, 3] f64 (t, h, w) of the packed layout [text | cond | audio | video]."""
+    area = np.sqrt(np.float64(h * w))
+    hh, ww = np.meshgrid(np.arange(h // 2), np.arange(w // 2), indexing="ij")
+    ph, pw = _h3_axis(h, area, hh.reshape(-1)), _h3_axis(w, area, ww.reshape(-1))
+    w_lo = _h3_axis(w, area, np.array([0]))[0]
+    w_hi = _h3_axis(w, area, np.array([w // 2 - 1]))[0]
+    rows = []
+    i = np.arange(l, dtype=np.float64)
+    rows.append(np.stack([i, np.zeros(l), np.zeros(l)], axis=1))
+    cursor = np.float64(l)
+    if first_frame:
+        rows.append(np.stack([np.full(ph.shape, cursor), ph, pw], axis=1))
+    for ch in range(2):
+        ai = cursor + np.arange(a, dtype=np.float64)
+        rows.append(np.stack([ai, np.zeros(a), np.full(a, w_lo if ch == 0 else w_hi)], axis=1))
+    cum = 0.0
+    for k in range(t):
+        rows.append(np.stack([np.full(ph.shape, cursor + cum), ph, pw], axis=1))
+        cum += H3_FRAME_RESCALE * H3_FRAME_PER_TOKEN[k % 5]
+    return np.concatenate(rows).astype(np.float64)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round to nearest even, finite inputs (layout.zig:31-34)."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def h3_rope_table(pos: np.ndarray, inv_freq: np.ndarray) -> np.ndarray:
+    """layout.zig:117-134: bf16 bits [S, 48, 2, 2]: angle = f32(pos) * inv_freq (f32), cos/sin in f64 -> f32 -> bf16;
+    entry (r, ax*16 + j) = [c, -s, s, c]."""
+    inv = np.asarray(inv_freq, np.float32)
+    assert inv.shape == (16,)
+    ang = pos.astype(np.float32)[:, :, None] * inv[None, None, :]            # f32 product, [S, 3, 16]
+    c = np.cos(ang.astype(np.float64)).astype(np.float32).reshape(-1, 48)
+    s = np.sin(ang.astype(np.float64)).astype(np.float32).reshape(-1, 48)
+    out = np.empty((pos.shape[0], 48, 2, 2), np.uint16)
+    out[..., 0, 0] = f32_to_bf16_bits(c)
+    out[..., 0, 1] = f32_to_bf16_bits(-s)
+    out[..., 1, 0] = f32_to_bf16_bits(s)
+    out[..., 1, 1] = f32_to_bf16_bits(c)
+    return out

@@ -1,0 +1,258 @@
+"""CPU oracle for the DiT joint-attention path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only as the
+checker (or as the reported CPU baseline). The product (localrouter_amd) never imports it.
+
+Two layers:
+  * liblro.so (lro.c): the C restatement -- seeded bf16 inputs, RMSNorm + RoPE, fp64 brute-force attention (the pin),
+    fp32 flash-style attention (the CPU baseline), the fused op. Wrapped here with numpy arrays.
+  * brute_* below: an independent pure-numpy fp64 restatement for tiny shapes, used to cross-check liblro.so.
+
+Reference semantics (jayleaton/localrouter): kernels/cuda/qwen_image/attention.cu:253-444 (attention, mask, GQA),
+kernels/cuda/minimax/kitchen/rms_rope.cu:37-230 + rope_device.cuh:65-98 (RMSNorm + RoPE),
+src/engines/qwen_image/triton_k.zig:44-53 (Qwen's fp32 cos/sin form).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liblro.so"
+D = 128
+
+TABLE_NONE, TABLE_COSSIN_F32, TABLE_MAT2_BF16, TABLE_MAT2_F32 = 0, 1, 2, 3
+PAIR_INTERLEAVED, PAIR_SPLIT_HALF = 0, 1
+
+MUTANTS = {
+    "rope_sign": 1,
+    "no_eps": 2,
+    "pairing": 3,
+    "no_scale": 4,
+    "causal_off_by_one": 5,
+    "gqa_mod": 6,
+    "no_weight": 7,
+    "table_transposed": 8,
+}
+
+
+def build_oracle(force: bool = True) -> Path:
+    """Compile liblro.so with the committed Makefile (gcc, OpenMP)."""
+    cmd = ["make", "-C", str(HERE)] + (["-B"] if force else []) + ["liblro.so"]
+    subprocess.run(cmd, check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    return LIB_PATH
+
+
+_lib = None
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build_oracle()
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.lro_set_mutant.argtypes = [ctypes.c_int]
+        L.lro_num_threads.restype = ctypes.c_int
+        L.lro_set_threads.argtypes = [ctypes.c_int]
+        L.lro_synth_normal_bf16.argtypes = [ctypes.c_uint64, ctypes.c_uint64, _I64, _P]
+        L.lro_f32_to_bf16_array.argtypes = [_P, _P, _I64]
+        L.lro_bf16_to_f32_array.argtypes = [_P, _P, _I64]
+        L.lro_rms_rope.argtypes = [_P, _I64, ctypes.c_int, _I64, _P, _P, ctypes.c_int, _P, _P, _I64, ctypes.c_int,
+                                   ctypes.c_int, ctypes.c_float, _P]
+        L.lro_attention_f64.argtypes = [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        L.lro_attention_f32.argtypes = [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_float, _P, _I64]
+        L.lro_joint_attention.argtypes = [_P, _P, _P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _P, _P, _P, _I64,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                          ctypes.c_int, ctypes.c_int, _P]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class mutant:
+    """Context manager planting a mistake in the C oracle (tests of the pins only)."""
+
+    def __init__(self, name: str):
+        self.code = MUTANTS[name]
+
+    def __enter__(self):
+        lib().lro_set_mutant(self.code)
+        return self
+
+    def __exit__(self, *exc):
+        lib().lro_set_mutant(0)
+
+
+def set_threads(n: int) -> None:
+    lib().lro_set_threads(int(n))
+
+
+def num_threads() -> int:
+    return int(lib().lro_num_threads())
+
+
+# ------------------------------------------------------------------------------------------ bf16 helpers and inputs
+def synth_bf16(seed: int, stream: int, shape) -> np.ndarray:
+    """Seeded N(0,1) values rounded to bf16, as uint16 bits (splitmix64 counter -> Box-Muller; lro.c documents it)."""
+    n = int(np.prod(shape))
+    out = np.empty(n, dtype=np.uint16)
+    lib().lro_synth_normal_bf16(ctypes.c_uint64(seed), ctypes.c_uint64(stream), n, _ptr(out))
+    return out.reshape(shape)
+
+
+def bf16_to_f32(x: np.ndarray) -> np.ndarray:
+    return (x.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().lro_f32_to_bf16_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+# ------------------------------------------------------------------------------------------ liblro.so wrappers
+def rms_rope(x: np.ndarray, w=None, *, table_kind=TABLE_NONE, ta=None, tb=None, pairing=PAIR_INTERLEAVED,
+             rot=128, eps=1e-6, w_bf16=None) -> np.ndarray:
+    """x: uint16 (bf16 bits) [rows, heads, 128] -> fp32 [rows, heads, 128]. Row r uses table row r.
+    Tables: COSSIN: ta = cos, tb = sin fp32 [rows, >= rot/2]; MAT2_BF16: ta uint16 [rows, >= 2*rot];
+    MAT2_F32: ta fp32 [rows, >= 2*rot]."""
+    x = np.ascontiguousarray(x)
+    rows, heads, d = x.shape
+    assert d == D
+    y = np.empty((rows, heads, D), dtype=np.float32)
+    stride = 0
+    if table_kind != TABLE_NONE:
+        ta = np.ascontiguousarray(ta)
+        stride = ta.shape[1]
+        if tb is not None:
+            tb = np.ascontiguousarray(tb)
+            assert tb.shape == ta.shape
+    wp = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    wb = None if w_bf16 is None else np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    lib().lro_rms_rope(_ptr(x), rows, heads, heads * D, _ptr(wp), _ptr(wb), table_kind, _ptr(ta), _ptr(tb), stride,
+                       pairing, rot, ctypes.c_float(eps), _ptr(y))
+    return y
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, p0=0, nkeys=None, causal=False, scale=None,
+              precise=True, rows=None) -> np.ndarray:
+    """q fp32 [W, H, 128], k, v fp32 [nkeys, HK, 128] -> fp32 [W, H, 128] (or [len(rows), H, 128]).
+    precise: fp64 brute force; else the fp32 flash-style CPU path (the baseline), optionally on a subset of rows."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    W, H, _ = q.shape
+    nk, HK, _ = k.shape
+    nkeys = nk if nkeys is None else nkeys
+    scale = np.float32(1.0 / np.sqrt(np.float32(D))) if scale is None else np.float32(scale)
+    if precise:
+        assert rows is None
+        out = np.empty((W, H, D), dtype=np.float32)
+        lib().lro_attention_f64(_ptr(q), _ptr(k), _ptr(v), _ptr(out), p0, W, H, HK, nkeys, int(causal),
+                                ctypes.c_float(scale))
+        return out
+    if rows is not None:
+        rows = np.ascontiguousarray(rows, dtype=np.int64)
+        out = np.empty((len(rows), H, D), dtype=np.float32)
+        lib().lro_attention_f32(_ptr(q), _ptr(k), _ptr(v), _ptr(out), p0, W, H, HK, nkeys, int(causal),
+                                ctypes.c_float(scale), _ptr(rows), len(rows))
+        return out
+    out = np.empty((W, H, D), dtype=np.float32)
+    lib().lro_attention_f32(_ptr(q), _ptr(k), _ptr(v), _ptr(out), p0, W, H, HK, nkeys, int(causal),
+                            ctypes.c_float(scale), None, 0)
+    return out
+
+
+def joint_attention(q_raw, k_raw, v, *, wq=None, wk=None, table_kind=TABLE_NONE, qa=None, qb=None, ka=None,
+                    kb=None, pairing=PAIR_INTERLEAVED, rot=128, eps=1e-6, p0=0, causal=False, scale=None, n_pre=0,
+                    precise=True) -> np.ndarray:
+    """The fused op on bf16-bit inputs q_raw [Sq, H, 128], k_raw, v [Sk, HK, 128] -> fp32 [Sq, H, 128].
+    Query i uses q-table row i, key j >= n_pre uses k-table row j - n_pre, keys j < n_pre are used as given."""
+    q_raw, k_raw, v = (np.ascontiguousarray(a) for a in (q_raw, k_raw, v))
+    Sq, H, _ = q_raw.shape
+    Sk, HK, _ = k_raw.shape
+    scale = np.float32(1.0 / np.sqrt(np.float32(D))) if scale is None else np.float32(scale)
+    stride = 0
+    if table_kind != TABLE_NONE:
+        qa = np.ascontiguousarray(qa)
+        ka = qa if ka is None else np.ascontiguousarray(ka)
+        stride = qa.shape[1]
+        assert ka.shape[1] == stride
+        if table_kind == TABLE_COSSIN_F32:
+            qb = np.ascontiguousarray(qb)
+            kb = qb if kb is None else np.ascontiguousarray(kb)
+    wq = None if wq is None else np.ascontiguousarray(wq, dtype=np.float32)
+    wk = None if wk is None else np.ascontiguousarray(wk, dtype=np.float32)
+    out = np.empty((Sq, H, D), dtype=np.float32)
+    lib().lro_joint_attention(_ptr(q_raw), _ptr(k_raw), _ptr(v), H * D, HK * D, HK * D, _ptr(wq), _ptr(wk),
+                              table_kind, _ptr(qa), _ptr(qb), _ptr(ka), _ptr(kb), stride, pairing, rot,
+                              ctypes.c_float(eps), Sq, Sk, H, HK, p0, int(causal), ctypes.c_float(scale), n_pre,
+                              int(precise), _ptr(out))
+    return out
+
+
+# ------------------------------------------------------------------------------------------ pure numpy fp64 brute force
+def brute_rms_rope(x_f32: np.ndarray, w=None, *, cos=None, sin=None, mat=None, pairing=PAIR_INTERLEAVED, rot=128,
+                   eps=1e-6) -> np.ndarray:
+    """fp64 restatement on float inputs [rows, heads, 128]; cos/sin [rows, rot/2] or mat [rows, rot/2, 2, 2]."""
+    x = x_f32.astype(np.float64)
+    rr = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    y = x * rr * (1.0 if w is None else np.asarray(w, np.float64))
+    if cos is None and mat is None:
+        return y
+    P = rot // 2
+    if pairing == PAIR_INTERLEAVED:
+        a_idx, b_idx = np.arange(P) * 2, np.arange(P) * 2 + 1
+    else:
+        a_idx, b_idx = np.arange(P), np.arange(P) + P
+    if mat is None:
+        c = np.asarray(cos, np.float64)[:, None, :P]
+        s = np.asarray(sin, np.float64)[:, None, :P]
+        f00, f01, f10, f11 = c, -s, s, c
+    else:
+        m = np.asarray(mat, np.float64)[:, None, :P]
+        f00, f01, f10, f11 = m[..., 0, 0], m[..., 0, 1], m[..., 1, 0], m[..., 1, 1]
+    xa, xb = y[..., a_idx].copy(), y[..., b_idx].copy()
+    y[..., a_idx] = f00 * xa + f01 * xb
+    y[..., b_idx] = f10 * xa + f11 * xb
+    return y
+
+
+def brute_attention(q, k, v, *, p0=0, nkeys=None, causal=False, scale=None) -> np.ndarray:
+    """fp64 dense softmax attention: q [W, H, 128], k, v [nk, HK, 128]."""
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    W, H, _ = q.shape
+    nk, HK, _ = k.shape
+    nkeys = nk if nkeys is None else nkeys
+    scale = float(np.float32(1.0 / np.sqrt(np.float32(D)))) if scale is None else float(scale)
+    G = H // HK
+    out = np.zeros((W, H, D))
+    j = np.arange(nk)
+    for h in range(H):
+        s = q[:, h, :] @ k[:, h // G, :].T * scale
+        vis = (j[None, :] < nkeys)
+        if causal:
+            vis = vis & (j[None, :] <= p0 + np.arange(W)[:, None])
+        s = np.where(vis, s, -np.inf)
+        s = s - s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=1, keepdims=True)
+        out[:, h, :] = p @ v[:, h // G, :]
+    return out
