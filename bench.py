@@ -96,6 +96,9 @@ def main():
     ap.add_argument("--tile-config", type=int, default=0, help="LR_ATTN_CFG_* (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 256 MiB device-to-device copy after timing (the known-size kernel that scales "
+                         "rocprofv3's FETCH_SIZE / WRITE_SIZE into bytes)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -202,6 +205,13 @@ def main():
         "kernels_ms": {"keys_rms_rope": round(keys_ms, 5), "attention": round(attn_ms, 5)},
         "flops_per_call": flops,
     }
+
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     if not args.no_cpu_baseline:
         fl_row = 4.0 * S * 128 * H

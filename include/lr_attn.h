@@ -56,9 +56,10 @@ typedef struct ihipStream_t* lr_stream_t;
 
 /* Attention tile configurations for the _ex entry points (0 = the library's choice). */
 #define LR_ATTN_CFG_AUTO 0
-#define LR_ATTN_CFG_Q64_W4 1   /* 256 queries per workgroup, 4 waves x 64 queries */
-#define LR_ATTN_CFG_Q32_W8 2   /* 256 queries per workgroup, 8 waves x 32 queries */
-#define LR_ATTN_CFG_Q32_W4 3   /* 128 queries per workgroup, 4 waves x 32 queries */
+#define LR_ATTN_CFG_PIPE_W8 1      /* 256 queries per workgroup (8 waves x 32): direct-to-LDS K/V ring, next tile's
+                                      QK^T overlapped with the current tile's softmax */
+#define LR_ATTN_CFG_PIPE_W4 2      /* the same kernel with 128 queries per workgroup (4 waves x 32) */
+#define LR_ATTN_CFG_REGSTAGE_W8 3  /* 256 queries per workgroup, K/V staged through registers (2-stage ring) */
 
 int lr_attn_abi_version(void);
 

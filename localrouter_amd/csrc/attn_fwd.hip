@@ -140,8 +140,10 @@ __device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int he
     }
 }
 
+// The register-staged kernel: K/V tiles pass through VGPRs into a 2-stage LDS ring, V^T is formed by a register
+// transpose. Kept as the reference point for the pipelined kernel below.
 template <int QW, int NW, bool FUSEQ>
-__global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NW * 64, 1) void attn_fwd_regstage_kernel(AttnArgs a) {
     constexpr int NQB = QW / 32;  // 32-query blocks per wave
     constexpr int BM = QW * NW;   // queries per workgroup
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
@@ -173,30 +175,46 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnArgs a) {
     const bool do_k = !SPLIT || wave < 4, do_v = !SPLIT || wave >= 4;
     const int vc = st & 15, vkg = st >> 4;             // V unit: dims 8*vc..+8 of keys 4*vkg..+4
     u32x4 kreg[4], vreg[4];
+    uint32_t kvalid = 0, vvalid = 0;   // per-chunk "key < nkeys" bits of a partial tile, applied at store time
 
     auto stage_load = [&](int t) {
         const int key0 = t * BN;
+        const bool partial = key0 + BN > a.nkeys;
         if (do_k) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int u = st + 256 * i, r = u >> 4, c = u & 15;
-                const int key = key0 + r;
-                const uint16_t* p = kbase + (int64_t)min(key, a.nkeys - 1) * a.k_rs + 8 * c;
-                u32x4 w = *reinterpret_cast<const u32x4*>(p);
-                kreg[i] = key < a.nkeys ? w : u32x4{0, 0, 0, 0};
+                const int key = partial ? min(key0 + r, a.nkeys - 1) : key0 + r;
+                kreg[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)key * a.k_rs + 8 * c);
+            }
+            kvalid = 0;
+            if (partial) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) kvalid |= (key0 + ((st + 256 * i) >> 4) < a.nkeys) ? (1u << i) : 0u;
             }
         }
         if (do_v) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int key = key0 + 4 * vkg + i;
-                const uint16_t* p = vbase + (int64_t)min(key, a.nkeys - 1) * a.v_rs + 8 * vc;
-                u32x4 w = *reinterpret_cast<const u32x4*>(p);
-                vreg[i] = key < a.nkeys ? w : u32x4{0, 0, 0, 0};
+                const int key = partial ? min(key0 + 4 * vkg + i, a.nkeys - 1) : key0 + 4 * vkg + i;
+                vreg[i] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)key * a.v_rs + 8 * vc);
+            }
+            vvalid = 0;
+            if (partial) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) vvalid |= (key0 + 4 * vkg + i < a.nkeys) ? (1u << i) : 0u;
             }
         }
+        return partial;
     };
-    auto stage_store = [&](int buf) {
+    auto stage_store = [&](int buf, bool partial) {
+        if (partial) {   // zero the keys past nkeys (their rows were loaded clamped)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (do_k && !(kvalid >> i & 1)) kreg[i] = u32x4{0, 0, 0, 0};
+                if (do_v && !(vvalid >> i & 1)) vreg[i] = u32x4{0, 0, 0, 0};
+            }
+        }
         if (do_k) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -241,8 +259,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnArgs a) {
             load_q_plain(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
     }
 
-    stage_load(0);
-    stage_store(0);
+    stage_store(0, stage_load(0));
     __syncthreads();
 
     f32x16 o[4][NQB];
@@ -263,7 +280,8 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnArgs a) {
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
         const bool more = t + 1 < ntiles;
-        if (more) stage_load(t + 1);
+        bool next_partial = false;
+        if (more) next_partial = stage_load(t + 1);
 
         // ---- S^T = K Q^T for 64 keys x QW queries
         f32x16 s[2][NQB];
@@ -354,7 +372,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnArgs a) {
             }
         }
 
-        if (more) stage_store(buf ^ 1);
+        if (more) stage_store(buf ^ 1, next_partial);
         __syncthreads();
     }
 
@@ -380,13 +398,309 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------ pipelined kernel
+// K and V tiles both live row-major in LDS ([64 keys][128 dims], 16 KB each) in a 3-stage ring, filled by direct
+// global->LDS loads (global_load_lds_dwordx4: no VGPRs, no VALU). V is read transposed for the PV operand with
+// ds_read_b64_tr_b16. Per tile t a wave runs
+//   A: S(t+1) = K(t+1) Q^T on MFMA, interleaved with the softmax of S(t) on VALU (independent registers);
+//   B: O += V(t)^T P(t);
+//   the direct loads of K(t+3) and V(t+2), a wait for K(t+2) and V(t+1), one s_barrier.
+// so the QK^T MFMAs of the next tile hide the exp/max/sum work of the current one, and every load has two tiles of
+// compute to land.
+constexpr int NSTAGE = 3;
+
+// V tile: 16-byte chunk c of row r stored at c ^ ((r & 3) << 2). A transposed read instruction covers 8 rows x 4
+// chunks (rows 4 apart share r & 3 and differ in the XOR-ed bits), so it touches every bank exactly twice; whole-row
+// writes stay a permutation of the 16 chunks.
+__device__ __forceinline__ int vrow_swz(int r) { return (r & 3) << 2; }
+
+// Wait until at most n vector-memory operations of this wave are outstanding.
+#define LR_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+
+// One 16-byte-per-lane direct load, global -> LDS: lane l's 16 bytes land at LDS byte address lds + 16 * l. Written
+// as inline asm (M0 = destination) so that the compiler does not serialise LDS reads of other ring slots behind it;
+// completion is tracked by the explicit vmcnt waits above. Nothing else in these kernels uses M0.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// A workgroup barrier that neither waits for outstanding memory operations nor lets the compiler move memory
+// accesses across it (the waits that matter are issued explicitly).
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int NW, bool FUSEQ>
+__global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
+    constexpr int BM = 32 * NW;
+    constexpr int TILE = BN * D;       // elements per K or V tile
+    constexpr int LOADS = 16 / NW;     // direct loads (1 KB each) per wave per K or V tile
+    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+    __shared__ __attribute__((aligned(1024))) uint16_t Kr[NSTAGE * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vr[NSTAGE * TILE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 31, hf = lane >> 5;
+
+    const int nwg = gridDim.x, b = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
+    const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int nqb = (a.W + BM - 1) / BM;
+    const int head = logical / nqb, qblk = logical - head * nqb;
+    const int hk = head / a.G;
+    const int row0 = qblk * BM, wrow0 = row0 + wave * 32;
+    const int last_row = min(row0 + BM, a.W) - 1;
+    int ntiles = (a.nkeys + BN - 1) / BN;
+    if (a.causal) ntiles = min(ntiles, (a.p0 + last_row) / BN + 1);
+    const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
+    const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs;
+
+    // ---- direct loads: instruction i (0..15) of a tile fills rows 4i..4i+3; lane -> row 4i + (lane >> 4) and LDS
+    // chunk (lane & 15), which must hold logical chunk (lane & 15) ^ swizzle(row). Rows past nkeys read the last
+    // valid row instead (finite data; those keys are masked and their V rows meet P = 0).
+    const int lrow = lane >> 4, lchunk = lane & 15;
+    int krow[LOADS], kcol[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        krow[j] = 4 * (wave + NW * j) + lrow;
+        kcol[j] = 8 * (lchunk ^ (krow[j] & 15));
+    }
+    const int vcol = 8 * (lchunk ^ (lrow << 2));   // rows 4i + lrow: (r & 3) == lrow
+    const uint32_t kr_lds = lds_addr(Kr), vr_lds = lds_addr(Vr);
+    auto issue_k = [&](int t, int slot) {
+        const int key0 = t * BN;
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int key = min(key0 + krow[j], a.nkeys - 1);
+            dma16(kbase + (int64_t)key * a.k_rs + kcol[j], kr_lds + 2 * (slot * TILE + (wave + NW * j) * 512));
+        }
+    };
+    auto issue_v = [&](int t, int slot) {
+        const int key0 = t * BN;
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int key = min(key0 + krow[j], a.nkeys - 1);
+            dma16(vbase + (int64_t)key * a.v_rs + vcol, vr_lds + 2 * (slot * TILE + (wave + NW * j) * 512));
+        }
+    };
+
+    // ---- queries (B operands of S^T = K Q^T)
+    bf16x8 qf[8];
+    if constexpr (FUSEQ)
+        load_q_fused(a, wrow0 + n, head, hf, qf);
+    else
+        load_q_plain(a, wrow0 + n, head, hf, qf);
+
+    // ---- per-lane LDS offsets
+    const int pr = key_perm(n);
+    int kfrag[2];                        // K A-operand row offsets for the two 32-key blocks (chunk added per k-step)
+    kfrag[0] = pr * D;
+    kfrag[1] = (32 + pr) * D;
+    const int kswz = pr & 15;            // (32 + pr) & 15 == pr & 15
+    // V^T operand by transposed reads: lane (group g = lane >> 4, s = lane & 15) addresses row 16kk + 8h + 4part +
+    // (s >> 2), dims 32db + 16(g & 1) + 4(s & 3) .. +4, h = g >> 1.
+    const int g = lane >> 4, sl = lane & 15;
+    int vtr[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        const int chunk = 4 * (db ^ (sl >> 2)) + 2 * (g & 1) + ((sl & 3) >> 1);
+        vtr[db] = (8 * (g >> 1) + (sl >> 2)) * D + 8 * chunk + 4 * (sl & 1);
+    }
+
+    auto qk_block = [&](const uint16_t* kt, int ks, int mb, f32x16& acc) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kt + kfrag[mb] + 8 * ((2 * ks + hf) ^ kswz));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], acc, 0, 0, 0);
+    };
+
+    // ---- prologue: tiles 0 (K, V), 1 (K, V), 2 (K) in flight; S(0)
+    issue_k(0, 0);
+    issue_v(0, 0);
+    if (ntiles > 1) { issue_k(1, 1); issue_v(1, 1); }
+    if (ntiles > 2) issue_k(2, 2);
+    LR_WAIT_VMCNT(0);
+    block_barrier();
+    f32x16 sA[2], sB[2];
+    sA[0] = f32x16{};
+    sA[1] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) qk_block(Kr, ks, mb, sA[mb]);
+    block_barrier();   // every wave is done with K slot 0 before step 0 refills it
+
+    f32x16 o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+    // m_used starts at a finite -1e30 (not -inf): every alpha below is exp2 of a finite value or of -inf (= 0)
+    float m_used = -1e30f, l_sum = 0.0f;
+    const float c = a.c;
+    const int pos = a.p0 + wrow0 + n;
+
+    // keys past nkeys and (causal) past the query's position -> -inf; only tiles that reach either limit
+    auto needs_mask = [&](int t) {
+        const int key0 = t * BN;
+        return key0 + BN > a.nkeys || (a.causal && key0 + BN - 1 > a.p0 + wrow0);
+    };
+    auto mask_tile = [&](int t, f32x16 (&sc)[2]) {
+        const int key0 = t * BN;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = key0 + 32 * mb + 16 * (r >> 3) + 8 * hf + (r & 7);
+                if (!(key < a.nkeys && (!a.causal || key <= pos))) sc[mb][r] = -INFINITY;
+            }
+    };
+    // the query's max over a score tile, scaled into the exp2 domain (both lanes of the query agree)
+    auto tile_max = [&](const f32x16 (&sc)[2]) {
+        float mx = fmaxf(sc[0][0], sc[0][1]);
+#pragma unroll
+        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, sc[0][r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][r]);
+        return wave_pair_max(mx) * c;
+    };
+
+    float mx_cur = tile_max(sA);
+
+    // One tile t. On entry: sc = S(t) and mx = its unmasked max. Then
+    //   mask (only tiles at nkeys or the causal diagonal; branch): -inf the hidden keys, recompute mx;
+    //   rescale (rare, branch): raise the running max when the tile's exceeds it by more than 2^8;
+    //   A: S(t+1) on the MFMAs  ||  P(t) = exp2(S(t) c - m), its row sums and bf16 packing on the VALU;
+    //   B: O += V(t)^T P(t)     ||  the max of S(t+1) on the VALU;
+    //   refill the ring, wait for the next tiles, barrier.
+    // A and B form one basic block, so the scheduler can interleave across all of it.
+    auto step = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2], float& mx) {
+        if (needs_mask(t)) {
+            mask_tile(t, sc);
+            mx = tile_max(sc);
+        }
+        if (__builtin_amdgcn_ballot_w64(mx > m_used + RESCALE_TAU)) {
+            const float mn = fmaxf(m_used, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_used - mn);
+            m_used = mn;
+            l_sum *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+        }
+        const float nm = -m_used;
+        bf16x8 pf[4];
+        auto exps = [&]() {
+            float ls = l_sum;
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    bf16x8 f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) f[j] = (bf16)__builtin_amdgcn_exp2f(fmaf(sc[mb][8 * hh + j], c, nm));
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        bf16x2 pp = {f[j], f[j + 1]};
+                        ls = __builtin_amdgcn_fdot2_f32_bf16(pp, bf16x2{(bf16)1.0f, (bf16)1.0f}, ls, false);
+                    }
+                    pf[2 * mb + hh] = f;
+                }
+            }
+            l_sum = ls;
+        };
+        {
+            // the last tile computes a throw-away S from a stale slot rather than branching: A and B stay one block
+            const uint16_t* kt = Kr + ((t + 1) % NSTAGE) * TILE;
+            sn[0] = f32x16{};
+            sn[1] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) qk_block(kt, ks, mb, sn[mb]);
+            exps();
+            // interleave: two K reads ahead, then 16 x (1 MFMA, 6 VALU, 1 DS read)
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        }
+        // ---- B: O^T += V^T P^T, with the next tile's max on the VALU
+        const uint16_t* vt = Vr + (t % NSTAGE) * TILE;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const uint16_t* p0 = vt + vtr[db] + (16 * kk) * D;
+                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 4 * D));
+                const bf16x8 vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi),
+                                                          0, 1, 2, 3, 4, 5, 6, 7);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kk], o[db], 0, 0, 0);
+            }
+        }
+        mx = tile_max(sn);
+        // ---- refill: K(t+3) into the slot K(t) left, V(t+2) into the slot V(t-1) left; then K(t+2), V(t+1) landed
+        if (t + 3 < ntiles) {
+            issue_k(t + 3, t % NSTAGE);
+            issue_v(t + 2, (t + 2) % NSTAGE);
+            LR_WAIT_VMCNT(2 * LOADS);
+        } else if (t + 2 < ntiles) {
+            issue_v(t + 2, (t + 2) % NSTAGE);
+            LR_WAIT_VMCNT(LOADS);
+        } else {
+            LR_WAIT_VMCNT(0);
+        }
+        block_barrier();
+    };
+
+    int t = 0;
+    for (; t + 1 < ntiles; t += 2) {
+        step(t, sA, sB, mx_cur);
+        step(t + 1, sB, sA, mx_cur);
+    }
+    if (t < ntiles) step(t, sA, sB, mx_cur);
+
+    // ---- epilogue: O / l -> bf16 rows
+    const int qrow = wrow0 + n;
+    const float l = wave_pair_sum(l_sum);
+    const float inv = 1.0f / l;
+    if (qrow < a.W) {
+        uint16_t* dst = a.out + (int64_t)qrow * a.o_rs + head * D + 4 * hf;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                u32x2 w;
+                w[0] = pack_bf16x2(o[db][4 * gg] * inv, o[db][4 * gg + 1] * inv);
+                w[1] = pack_bf16x2(o[db][4 * gg + 2] * inv, o[db][4 * gg + 3] * inv);
+                *reinterpret_cast<u32x2*>(dst + 32 * db + 8 * gg) = w;
+            }
+    }
+}
+
 template <int QW, int NW, bool FUSEQ>
-hipError_t launch_cfg(const AttnArgs& a, hipStream_t stream) {
+hipError_t launch_regstage(const AttnArgs& a, hipStream_t stream) {
     constexpr int BM = QW * NW;
     const int64_t nqb = (a.W + BM - 1) / BM;
     const int64_t blocks = nqb * a.H;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_fwd_kernel<QW, NW, FUSEQ>), dim3((unsigned)blocks), dim3(NW * 64), 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_regstage_kernel<QW, NW, FUSEQ>), dim3((unsigned)blocks), dim3(NW * 64), 0, stream, a);
+    return hipGetLastError();
+}
+
+template <int NW, bool FUSEQ>
+hipError_t launch_pipe(const AttnArgs& a, hipStream_t stream) {
+    constexpr int BM = 32 * NW;
+    const int64_t nqb = (a.W + BM - 1) / BM;
+    const int64_t blocks = nqb * a.H;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, FUSEQ>), dim3((unsigned)blocks), dim3(NW * 64), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -394,20 +708,20 @@ hipError_t launch_cfg(const AttnArgs& a, hipStream_t stream) {
 
 int attention_block_rows(int config) {
     switch (config) {
-        case ATTN_CFG_Q32_W4: return 128;
+        case ATTN_CFG_PIPE_W4: return 128;
         default: return 256;
     }
 }
 
 hipError_t launch_attention(const AttnArgs& a, bool fuse_q, int config, hipStream_t stream) {
-    if (config == ATTN_CFG_AUTO) config = ATTN_CFG_Q32_W8;
+    if (config == ATTN_CFG_AUTO) config = ATTN_CFG_PIPE_W8;
     switch (config) {
-        case ATTN_CFG_Q64_W4:
-            return fuse_q ? launch_cfg<64, 4, true>(a, stream) : launch_cfg<64, 4, false>(a, stream);
-        case ATTN_CFG_Q32_W8:
-            return fuse_q ? launch_cfg<32, 8, true>(a, stream) : launch_cfg<32, 8, false>(a, stream);
-        case ATTN_CFG_Q32_W4:
-            return fuse_q ? launch_cfg<32, 4, true>(a, stream) : launch_cfg<32, 4, false>(a, stream);
+        case ATTN_CFG_PIPE_W8:
+            return fuse_q ? launch_pipe<8, true>(a, stream) : launch_pipe<8, false>(a, stream);
+        case ATTN_CFG_PIPE_W4:
+            return fuse_q ? launch_pipe<4, true>(a, stream) : launch_pipe<4, false>(a, stream);
+        case ATTN_CFG_REGSTAGE_W8:
+            return fuse_q ? launch_regstage<32, 8, true>(a, stream) : launch_regstage<32, 8, false>(a, stream);
         default:
             return hipErrorInvalidValue;
     }

@@ -45,9 +45,10 @@ struct RopeArgs {
 // Attention tile configurations (queries per wave x waves per workgroup).
 enum AttnConfig : int {
     ATTN_CFG_AUTO = 0,
-    ATTN_CFG_Q64_W4 = 1,   // 64 queries/wave, 4 waves: 256-query blocks, one wave per SIMD
-    ATTN_CFG_Q32_W8 = 2,   // 32 queries/wave, 8 waves: 256-query blocks, two waves per SIMD
-    ATTN_CFG_Q32_W4 = 3,   // 32 queries/wave, 4 waves: 128-query blocks
+    ATTN_CFG_PIPE_W8 = 1,      // pipelined kernel, 8 waves x 32 queries: 256-query blocks, two waves per SIMD
+    ATTN_CFG_PIPE_W4 = 2,      // pipelined kernel, 4 waves x 32 queries: 128-query blocks
+    ATTN_CFG_REGSTAGE_W8 = 3,  // register-staged kernel, 8 waves x 32 queries
+    ATTN_CFG_LAST = 3,
 };
 
 hipError_t launch_attention(const AttnArgs& a, bool fuse_q, int config, hipStream_t stream);

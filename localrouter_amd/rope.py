@@ -31,8 +31,29 @@ def axis_omegas(d: int, theta: float = QWEN_THETA) -> np.ndarray:
     return 1.0 / np.power(np.float64(theta), 2.0 * j / d)
 
 
+# The 64 Qwen-Image frequencies as the engine loads them (f64 bit patterns, big-endian hex; the values of
+# kernels/qwen_image/rope_omega.json, read by smath.omegas, smath.zig:112-126). They equal theta^(-2j/d) per axis to
+# within one f64 ulp (torch's float64 linspace/pow produced them); frozen so that tables match the engine's bits.
+QWEN_OMEGA_F64_HEX = (
+    "3ff0000000000000", "3fd43d136248490f", "3fb999999999999a", "3fa030dc4ea03a72", "3f847ae147ae147b", "3f69e7c6e43390b6",
+    "3f50624dd2f1a9fc", "3f34b96be9c2da2c", "3ff0000000000000", "3fe707aa3f9e1202", "3fe093069178d379", "3fd7db4a2009c6e3",
+    "3fd12b542ba56564", "3fc8b682a4336478", "3fc1c9194d504805", "3fb999999999999a", "3fb26c8832e4db35", "3faa84d74f27b8c3",
+    "3fa315d4e66e38b8", "3f9b7886ac3bd56d", "3f93c53550291d2d", "3f8c74f54880733d", "3f847ae147ae147b", "3f7d7a7384a15eb3",
+    "3f753712a5b96096", "3f6e8954a3e38dea", "3f65fa0556964454", "3f5fa1eee6a82eaa", "3f56c3f76d338f61", "3f50624dd2f1a9fc",
+    "3f47952936e77efc", "3f40f8dbb7c7807d", "3f386ddd4fe93e54", "3f3194d11211d043", "3f294e58b8868bbb", "3f22365f8a8fa5e7",
+    "3ff0000000000000", "3fe707aa3f9e1202", "3fe093069178d379", "3fd7db4a2009c6e3", "3fd12b542ba56564", "3fc8b682a4336478",
+    "3fc1c9194d504805", "3fb999999999999a", "3fb26c8832e4db35", "3faa84d74f27b8c3", "3fa315d4e66e38b8", "3f9b7886ac3bd56d",
+    "3f93c53550291d2d", "3f8c74f54880733d", "3f847ae147ae147b", "3f7d7a7384a15eb3", "3f753712a5b96096", "3f6e8954a3e38dea",
+    "3f65fa0556964454", "3f5fa1eee6a82eaa", "3f56c3f76d338f61", "3f50624dd2f1a9fc", "3f47952936e77efc", "3f40f8dbb7c7807d",
+    "3f386ddd4fe93e54", "3f3194d11211d043", "3f294e58b8868bbb", "3f22365f8a8fa5e7",
+)
+
+
 def qwen_omegas(axes=QWEN_AXES, theta: float = QWEN_THETA) -> np.ndarray:
-    """The 64 Qwen-Image frequencies, axis by axis (rope_omega.json's rule)."""
+    """The 64 Qwen-Image frequencies, axis by axis: the frozen engine values for the default axes and theta, else
+    the closed form theta^(-2j/d)."""
+    if tuple(axes) == QWEN_AXES and theta == QWEN_THETA:
+        return np.array([np.frombuffer(bytes.fromhex(h), dtype=">f8")[0] for h in QWEN_OMEGA_F64_HEX], np.float64)
     return np.concatenate([axis_omegas(d, theta) for d in axes])
 
 

@@ -1,0 +1,118 @@
+"""The C ABI library on the CPU: it loads, exports exactly what include/lr_attn.h declares, and rejects bad arguments
+with hipErrorInvalidValue before touching the GPU (no compute calls here)."""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from localrouter_amd import _lib
+
+HIP_ERROR_INVALID_VALUE = 1
+
+
+def _declared():
+    text = _lib.HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(?:int|size_t)\s+(lr_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    declared = _declared()
+    assert len(declared) >= 10
+    for name in declared:
+        assert hasattr(L, name), f"{name} declared in lr_attn.h but not exported"
+    assert sorted(_lib.SIGNATURES) == declared, "ctypes signatures out of sync with lr_attn.h"
+
+
+def test_abi_version():
+    assert _lib.load().lr_attn_abi_version() == 1
+
+
+def test_workspace_bytes():
+    L = _lib.load()
+    assert L.lr_joint_attention_workspace_bytes(4608, 24) == 4608 * 24 * 128 * 2
+    assert L.lr_joint_attention_workspace_bytes(3, 1) == 768
+    assert L.lr_joint_attention_workspace_bytes(0, 24) == 0
+
+
+# fake, well-aligned device addresses: validation must reject before any HIP call is made
+A = 0x10000
+
+
+@pytest.mark.parametrize("args,why", [
+    ((0, A, A, A, 0, 8, 2, 2, 8, 0, 0.088, 256, 256, 256, None), "null q"),
+    ((A, A, A, A, 0, 8, 2, 2, 0, 0, 0.088, 256, 256, 256, None), "nkeys 0"),
+    ((A, A, A, A, 0, 0, 2, 2, 8, 0, 0.088, 256, 256, 256, None), "W 0"),
+    ((A, A, A, A, 0, 8, 3, 2, 8, 0, 0.088, 384, 256, 384, None), "H % HK"),
+    ((A + 2, A, A, A, 0, 8, 2, 2, 8, 0, 0.088, 256, 256, 256, None), "misaligned q"),
+    ((A, A, A, A, 0, 8, 2, 2, 8, 0, 0.088, 260, 256, 256, None), "row stride not 16-byte"),
+    ((A, A, A, A, 0, 8, 2, 2, 8, 0, 0.088, 128, 256, 256, None), "row stride narrower than the heads"),
+    ((A, A, A, A, 0, 8, 2, 2, 8, 0, -1.0, 256, 256, 256, None), "negative scale"),
+    ((A, A, A, A, 0, 8, 2, 2, 8, 0, float("inf"), 256, 256, 256, None), "infinite scale"),
+    ((A, A, A, A, -1, 8, 2, 2, 8, 1, 0.088, 256, 256, 256, None), "negative p0"),
+    ((A, A, A, A, 0, 8, 2, 2, 8, 2, 0.088, 256, 256, 256, None), "causal not 0/1"),
+])
+def test_attention_rejects(args, why):
+    assert _lib.load().lr_attention_bf16(*args) == HIP_ERROR_INVALID_VALUE, why
+
+
+def test_attention_ex_rejects_bad_config():
+    L = _lib.load()
+    assert L.lr_attention_bf16_ex(A, A, A, A, 0, 8, 2, 2, 8, 0, 0.088, 256, 256, 256, 256, 128, 128, 99,
+                                  None) == HIP_ERROR_INVALID_VALUE
+
+
+def _fused(**kw):
+    a = dict(q=A, k=A, v=A, out=A, wq=None, wk=None, kind=1, qa=A, qb=A, ka=A, kb=A, ts=64, pairing=0, rot=128,
+             eps=1e-6, Sq=8, Sk=8, H=2, HK=2, p0=0, causal=0, scale=0.088, qrs=256, krs=256, vrs=256, ors=256, n_pre=0,
+             ws=A, wsb=8 * 2 * 256, stream=None)
+    a.update(kw)
+    return _lib.load().lr_joint_attention_fused(*a.values())
+
+
+@pytest.mark.parametrize("kw,why", [
+    (dict(ws=0), "no workspace"),
+    (dict(ws=A + 16), "workspace not 256-aligned"),
+    (dict(wsb=100), "workspace too small"),
+    (dict(kind=7), "table kind"),
+    (dict(pairing=1, rot=48), "split-half rot not a multiple of 32"),
+    (dict(rot=130), "rot > 128"),
+    (dict(rot=63), "odd rot"),
+    (dict(qb=0), "cos/sin table without sin"),
+    (dict(ts=10), "table stride below rot/2"),
+    (dict(n_pre=9), "n_pre > Sk"),
+    (dict(eps=-1.0), "negative eps"),
+    (dict(kind=2, ts=254), "bf16 2x2 table stride not a multiple of 4"),
+])
+def test_fused_rejects(kw, why):
+    assert _fused(**kw) == HIP_ERROR_INVALID_VALUE, why
+
+
+def test_rms_rope_rejects():
+    L = _lib.load()
+    ok = dict(src=A, srs=256, off=0, dst=A, drs=256, n=4, b=1, sbs=0, dbs=0, heads=2, w=None, wk=0, kind=1, ta=A,
+              tb=A, ts=64, rot=128, pairing=0, eps=1e-6, rn=0, stream=None)
+
+    def call(**kw):
+        a = dict(ok)
+        a.update(kw)
+        return L.lr_rms_rope_bf16(*a.values())
+
+    assert call(n=0) == HIP_ERROR_INVALID_VALUE
+    assert call(off=3) == HIP_ERROR_INVALID_VALUE
+    assert call(wk=1) == HIP_ERROR_INVALID_VALUE          # weight kind without a weight
+    assert call(pairing=1, rot=40) == HIP_ERROR_INVALID_VALUE
+    assert call(rn=2) == HIP_ERROR_INVALID_VALUE
+    assert L.lr_rms_rope_qk_bf16(A, A, 4, 2, 768, 768, None, A, A, 192, 96, 1e-5, None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_ops_has_no_cpu_path():
+    """The torch-facing layer refuses CPU tensors instead of computing anything itself."""
+    torch = pytest.importorskip("torch")
+    from localrouter_amd import ops
+    q = torch.zeros((4, 1, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        ops.attention(q, q, q)

@@ -18,7 +18,7 @@ torch = pytest.importorskip("torch")
 
 from localrouter_amd import ops  # noqa: E402
 
-CONFIGS = [ops.CFG_Q32_W8, ops.CFG_Q32_W4, ops.CFG_Q64_W4]
+CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8]
 
 
 def _qkv(seed, W, nk, H, HK):
@@ -156,11 +156,11 @@ def test_rms_rope_qk_h3_in_place():
     """Kitchen.rmsRope semantics: q and k of a packed qkv, in place, bf16 weights, bf16 [S,48,2,2] table, rot 96."""
     print("\n[rms_rope_qk] H3 packed in place", flush=True)
     from localrouter_amd import rope
-    S, H = 120, 4
+    pos = rope.h3_positions(10, 2, 8, 10, 15)
+    S, H = pos.shape[0], 4
     qkv = oracle.synth_bf16(22, 1, (S, 3, H, 128))
     qn = oracle.f32_to_bf16(1.0 + 0.1 * oracle.bf16_to_f32(oracle.synth_bf16(22, 2, (128,))))
     kn = oracle.f32_to_bf16(1.0 + 0.1 * oracle.bf16_to_f32(oracle.synth_bf16(22, 3, (128,))))
-    pos = rope.h3_positions(10, 2, 8, 10, 15)[:S]
     inv = (1.0 / np.power(10000.0, np.arange(16) / 16.0)).astype(np.float32)
     tab = rope.h3_rope_table(pos, inv).reshape(S, 192)
     d = to_dev(qkv)

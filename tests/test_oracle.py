@@ -1,0 +1,297 @@
+"""Pins of the CPU oracle (oracle/lro.c), on the CPU only.
+
+Each oracle function is checked against something it does not share code with:
+  * attention: torch-CPU scaled_dot_product_attention in fp32 (the library routine the reference's own harness calls
+    "exact", tools/twin/stk_twin/attnbench.py:134), an independent numpy fp64 brute force, and closed forms /
+    invariants (constant V, one key, zero query, softmax-ratio law, key permutation, score shift, convexity, GQA
+    equivalence, causal == non-causal when p0 covers every key);
+  * RMSNorm: its closed form with and without eps, the unit-RMS property, scale invariance;
+  * RoPE: torch's complex multiplication (the diffusers / Qwen-Image convention for interleaved pairs), the
+    rotate-half formula (split-half pairs), identity at position 0, norm preservation per pair, the
+    relative-position law <R(p+c)q, R(p'+c)k> = <R(p)q, R(p')k>, and the 2x2 tables equal to the cos/sin ones;
+  * the fused op: its composition from the pinned parts.
+Planted mistakes (oracle.mutant) must each make at least one pin fail.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import PAIR_INTERLEAVED, PAIR_SPLIT_HALF, TABLE_COSSIN_F32, TABLE_MAT2_BF16, TABLE_MAT2_F32
+
+SCALE = float(np.float32(1.0 / np.sqrt(np.float32(128.0))))
+
+
+def _inputs(seed, W, nk, H, HK):
+    q = oracle.bf16_to_f32(oracle.synth_bf16(seed, 1, (W, H, 128)))
+    k = oracle.bf16_to_f32(oracle.synth_bf16(seed, 2, (nk, HK, 128)))
+    v = oracle.bf16_to_f32(oracle.synth_bf16(seed, 3, (nk, HK, 128)))
+    return q, k, v
+
+
+def _sdpa(q, k, v, *, p0=0, causal=False, nkeys=None, scale=SCALE):
+    """torch fp32 SDPA with an explicit boolean mask and kv heads repeated for GQA."""
+    W, H, _ = q.shape
+    nk, HK, _ = k.shape
+    nkeys = nk if nkeys is None else nkeys
+    qt = torch.from_numpy(q).permute(1, 0, 2)
+    kt = torch.from_numpy(k[:nkeys]).permute(1, 0, 2).repeat_interleave(H // HK, 0)
+    vt = torch.from_numpy(v[:nkeys]).permute(1, 0, 2).repeat_interleave(H // HK, 0)
+    mask = None
+    if causal:
+        mask = torch.arange(nkeys)[None, :] <= (p0 + torch.arange(W))[:, None]
+    o = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask, scale=scale)
+    return o.permute(1, 0, 2).numpy()
+
+
+# ------------------------------------------------------------------------------------------ attention pins
+CASES = [
+    dict(W=33, nk=70, H=2, HK=2),
+    dict(W=64, nk=64, H=4, HK=1),
+    dict(W=50, nk=91, H=4, HK=2, causal=True, p0=41),
+    dict(W=40, nk=40, H=2, HK=2, causal=True, p0=0),
+    dict(W=17, nk=100, H=2, HK=2, nkeys=61),
+]
+
+
+def _attn_pins(case) -> dict:
+    """Every attention pin on one case -> {name: passed}."""
+    c = dict(case)
+    W, nk, H, HK = c.pop("W"), c.pop("nk"), c.pop("H"), c.pop("HK")
+    q, k, v = _inputs(3, W, nk, H, HK)
+    res = {}
+    got = oracle.attention(q, k, v, precise=True, **c)
+    res["sdpa"] = np.abs(got - _sdpa(q, k, v, **c)).max() < 2e-5
+    res["brute"] = np.abs(got - oracle.brute_attention(q, k, v, **c)).max() < 2e-6
+    fast = oracle.attention(q, k, v, precise=False, **c)
+    res["flash_f32"] = np.abs(fast - got).max() < 2e-5
+    return res
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_attention_matches_sdpa_and_brute_force(case):
+    res = _attn_pins(case)
+    assert all(res.values()), res
+
+
+def test_attention_closed_forms():
+    q, k, v = _inputs(4, 20, 50, 2, 2)
+    # V == c  =>  O == c
+    vc = np.full_like(v, 0.375)
+    assert np.allclose(oracle.attention(q, k, vc), 0.375, atol=1e-6)
+    # one key  =>  O = v0
+    o = oracle.attention(q, k[:1], v[:1])
+    assert np.allclose(o, np.broadcast_to(v[0][None], o.shape), atol=1e-6)
+    # q == 0  =>  O = mean of the visible V rows (causal: rows 0..p0+i)
+    z = np.zeros_like(q)
+    assert np.allclose(oracle.attention(z, k, v), v.mean(axis=0)[None], atol=1e-6)
+    oc = oracle.attention(z, k, v, causal=True, p0=5)
+    for i in (0, 7, 19):
+        assert np.allclose(oc[i], v[: 5 + i + 1].mean(axis=0), atol=1e-6)
+
+
+def test_attention_softmax_ratio_law():
+    """One-hot V columns give the softmax weights: O[i, j] / O[i, j'] = exp(scale * (<q_i,k_j> - <q_i,k_j'>))."""
+    q, k, _ = _inputs(5, 6, 40, 1, 1)
+    v = np.zeros((40, 1, 128), np.float32)
+    v[np.arange(40), 0, np.arange(40)] = 1.0
+    o = oracle.attention(q, k, v).astype(np.float64)[:, 0, :40]
+    assert np.allclose(o.sum(axis=1), 1.0, atol=1e-6)
+    s = (q[:, 0].astype(np.float64) @ k[:, 0].astype(np.float64).T) * SCALE
+    lr = np.log(o[:, 1:]) - np.log(o[:, :1])
+    assert np.allclose(lr, s[:, 1:] - s[:, :1], atol=1e-4)
+
+
+def test_attention_invariants():
+    q, k, v = _inputs(6, 30, 64, 2, 2)
+    base = oracle.attention(q, k, v)
+    perm = np.random.default_rng(0).permutation(64)
+    assert np.allclose(oracle.attention(q, k[perm], v[perm]), base, atol=1e-6)
+    # shift every score of a row by the same amount: k[:, :, 127] = 1 for all keys, vary q[:, :, 127]
+    k2 = k.copy()
+    k2[:, :, 127] = 1.0
+    q2 = q.copy()
+    q2[:, :, 127] = 0.0
+    a = oracle.attention(q2, k2, v)
+    q2[:, :, 127] = 3.0
+    assert np.allclose(oracle.attention(q2, k2, v), a, atol=1e-5)
+    # convex combination of V rows
+    assert (base >= v.min(axis=0)[None] - 1e-6).all() and (base <= v.max(axis=0)[None] + 1e-6).all()
+    # GQA: H=4 over HK=2 equals HK=4 with kv heads [0, 0, 1, 1]
+    q4, _, _ = _inputs(6, 30, 64, 4, 2)
+    g = oracle.attention(q4, k, v)
+    kd, vd = np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1)
+    assert np.allclose(g, oracle.attention(q4, kd, vd), atol=1e-6)
+    # causal with p0 >= nkeys - 1 == non-causal
+    assert np.allclose(oracle.attention(q, k, v, causal=True, p0=63), base, atol=1e-6)
+
+
+# ------------------------------------------------------------------------------------------ RMSNorm + RoPE pins
+def _angles(S, P, seed=0):
+    return np.random.default_rng(seed).uniform(-4, 4, size=(S, P))
+
+
+def _rope_torch_complex(x, ang):
+    """Interleaved pairs as complex numbers times e^{i angle} (the diffusers / Qwen-Image apply_rotary_emb form)."""
+    xt = torch.from_numpy(x.astype(np.float64)).reshape(*x.shape[:-1], -1, 2)
+    xc = torch.view_as_complex(xt)
+    P = ang.shape[1]
+    rot = torch.polar(torch.ones(ang.shape, dtype=torch.float64), torch.from_numpy(ang))[:, None, :]
+    out = xc.clone()
+    out[..., :P] = xc[..., :P] * rot
+    return torch.view_as_real(out).reshape(x.shape).numpy()
+
+
+def _rope_rotate_half(x, ang, rot):
+    """Split-half pairs: x * cos + rotate_half(x) * sin over the first rot dims (the GPT-NeoX / H3 form)."""
+    P = rot // 2
+    c = np.cos(ang)[:, None, :]
+    s = np.sin(ang)[:, None, :]
+    y = x.astype(np.float64).copy()
+    x1, x2 = y[..., :P].copy(), y[..., P:rot].copy()
+    y[..., :P] = x1 * c - x2 * s
+    y[..., P:rot] = x2 * c + x1 * s
+    return y
+
+
+def _rope_pins() -> dict:
+    res = {}
+    S, H = 12, 3
+    x = oracle.synth_bf16(8, 1, (S, H, 128))
+    xf = oracle.bf16_to_f32(x).astype(np.float64)
+    w = (1.0 + 0.3 * np.sin(np.arange(128))).astype(np.float32)
+    eps = 0.5  # large, so a dropped eps is visible
+    # RMSNorm closed form
+    ref = xf / np.sqrt((xf ** 2).mean(-1, keepdims=True) + eps) * w
+    res["rms_closed_form"] = np.abs(oracle.rms_rope(x, w, eps=eps) - ref).max() < 1e-5
+    # unit RMS with w = 1, eps -> 0; scale invariance (x2 is exact in bf16)
+    y1 = oracle.rms_rope(x, None, eps=1e-12)
+    res["rms_unit"] = np.abs(np.sqrt((y1.astype(np.float64) ** 2).mean(-1)) - 1).max() < 1e-5
+    x2 = oracle.f32_to_bf16(oracle.bf16_to_f32(x) * 2)
+    res["rms_scale_inv"] = np.abs(oracle.rms_rope(x2, w, eps=1e-12) - oracle.rms_rope(x, w, eps=1e-12)).max() < 1e-5
+    n = oracle.rms_rope(x, w, eps=eps).astype(np.float64)
+    # RoPE, interleaved, full and partial rotation, against torch complex multiplication
+    for rot in (128, 64):
+        ang = _angles(S, rot // 2)
+        c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+        got = oracle.rms_rope(x, w, table_kind=TABLE_COSSIN_F32, ta=c, tb=s, pairing=PAIR_INTERLEAVED, rot=rot,
+                              eps=eps)
+        ref = _rope_torch_complex(n, np.arctan2(s.astype(np.float64), c.astype(np.float64)))
+        res[f"complex_interleaved_{rot}"] = np.abs(got - ref).max() < 1e-5
+    # split-half against rotate_half
+    for rot in (128, 96):
+        ang = _angles(S, rot // 2, 1)
+        c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+        got = oracle.rms_rope(x, w, table_kind=TABLE_COSSIN_F32, ta=c, tb=s, pairing=PAIR_SPLIT_HALF, rot=rot, eps=eps)
+        ref = _rope_rotate_half(n, np.arctan2(s.astype(np.float64), c.astype(np.float64)), rot)
+        res[f"rotate_half_{rot}"] = np.abs(got - ref).max() < 1e-5
+    # 2x2 tables [c, -s, s, c] == cos/sin tables (fp32 exactly, bf16 within bf16 rounding of the table)
+    ang = _angles(S, 48, 2)
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    m = np.stack([c, -s, s, c], axis=-1).reshape(S, 192)
+    a = oracle.rms_rope(x, w, table_kind=TABLE_COSSIN_F32, ta=c, tb=s, pairing=PAIR_SPLIT_HALF, rot=96, eps=eps)
+    b = oracle.rms_rope(x, w, table_kind=TABLE_MAT2_F32, ta=m, pairing=PAIR_SPLIT_HALF, rot=96, eps=eps)
+    res["mat2_f32_equals_cossin"] = np.abs(a - b).max() < 1e-6
+    mb = oracle.f32_to_bf16(m)
+    b2 = oracle.rms_rope(x, w, table_kind=TABLE_MAT2_BF16, ta=mb, pairing=PAIR_SPLIT_HALF, rot=96, eps=eps)
+    res["mat2_bf16_close"] = np.abs(a - b2).max() < 0.05
+    # identity at angle 0, and norm preservation per pair
+    z = np.zeros((S, 64))
+    got = oracle.rms_rope(x, w, table_kind=TABLE_COSSIN_F32, ta=np.cos(z).astype(np.float32),
+                          tb=np.sin(z).astype(np.float32), eps=eps)
+    res["identity_at_zero"] = np.abs(got - n).max() < 1e-6
+    ang = _angles(S, 64, 3)
+    got = oracle.rms_rope(x, w, table_kind=TABLE_COSSIN_F32, ta=np.cos(ang).astype(np.float32),
+                          tb=np.sin(ang).astype(np.float32), eps=eps).astype(np.float64)
+    pn = lambda y: (y.reshape(S, H, 64, 2) ** 2).sum(-1)  # noqa: E731
+    res["pair_norms"] = np.abs(pn(got) - pn(n)).max() < 1e-5
+    return res
+
+
+def test_rms_rope_pins():
+    res = _rope_pins()
+    assert all(res.values()), res
+
+
+def test_rope_relative_position_law():
+    """Scores after RoPE depend only on position differences: shift every position of a Qwen-style 3-axis id table
+    by the same amount and the q.k products stay the same."""
+    from localrouter_amd import rope
+    S = 10
+    x = oracle.synth_bf16(9, 1, (S, 1, 128))
+    y = oracle.synth_bf16(9, 2, (S, 1, 128))
+    ids = rope.qwen_image_ids(2, 5, 0)
+    shifted = ids + np.array([3, -7, 11], np.float32)
+
+    def dots(ids_):
+        c, s = rope.qwen_table(ids_)
+        qa = oracle.rms_rope(x, None, table_kind=TABLE_COSSIN_F32, ta=c, tb=s).astype(np.float64)[:, 0]
+        ka = oracle.rms_rope(y, None, table_kind=TABLE_COSSIN_F32, ta=c, tb=s).astype(np.float64)[:, 0]
+        return qa @ ka.T
+
+    assert np.abs(dots(ids) - dots(shifted)).max() < 2e-4
+
+
+def test_fused_is_the_composition():
+    """lro_joint_attention == rms_rope(q), rms_rope(k) (k-table rows offset by n_pre, prefix rows as given), then
+    attention -- checked through torch SDPA so it does not lean on lro_attention_f64."""
+    Sq, Sk, H, HK, n_pre = 40, 55, 2, 1, 9
+    q = oracle.synth_bf16(10, 1, (Sq, H, 128))
+    k = oracle.synth_bf16(10, 2, (Sk, HK, 128))
+    v = oracle.synth_bf16(10, 3, (Sk, HK, 128))
+    angq, angk = _angles(Sq, 64, 4), _angles(Sk, 64, 5)
+    qc, qs = np.cos(angq).astype(np.float32), np.sin(angq).astype(np.float32)
+    kc, ks = np.cos(angk).astype(np.float32), np.sin(angk).astype(np.float32)
+    wq = np.linspace(0.5, 1.5, 128).astype(np.float32)
+    got = oracle.joint_attention(q, k, v, wq=wq, table_kind=TABLE_COSSIN_F32, qa=qc, qb=qs, ka=kc, kb=ks,
+                                 causal=True, p0=20, n_pre=n_pre)
+    qh = oracle.rms_rope(q, wq, table_kind=TABLE_COSSIN_F32, ta=qc, tb=qs)
+    kh = np.concatenate([oracle.bf16_to_f32(k[:n_pre]),
+                         oracle.rms_rope(k[n_pre:], None, table_kind=TABLE_COSSIN_F32, ta=kc[: Sk - n_pre],
+                                         tb=ks[: Sk - n_pre])])
+    ref = _sdpa(qh, kh, oracle.bf16_to_f32(v), causal=True, p0=20)
+    assert np.abs(got - ref).max() < 2e-5
+    fast = oracle.joint_attention(q, k, v, wq=wq, table_kind=TABLE_COSSIN_F32, qa=qc, qb=qs, ka=kc, kb=ks,
+                                  causal=True, p0=20, n_pre=n_pre, precise=False)
+    assert np.abs(fast - got).max() < 2e-5
+
+
+# ------------------------------------------------------------------------------------------ planted mistakes
+def _all_pins() -> dict:
+    res = {}
+    for i, c in enumerate(CASES):
+        for kk, vv in _attn_pins(c).items():
+            if kk != "flash_f32" and kk != "brute":   # the brute force is numpy's: it does not see the mutant
+                res[f"attn{i}_{kk}"] = vv
+    res.update(_rope_pins())
+    return res
+
+
+@pytest.mark.parametrize("name", sorted(oracle.MUTANTS))
+def test_planted_mistake_is_caught(name):
+    assert all(_all_pins().values()), "pins must pass on the clean oracle"
+    with oracle.mutant(name):
+        res = _all_pins()
+    failed = [k for k, ok in res.items() if not ok]
+    assert failed, f"mutant {name} passed every pin"
+
+
+# ------------------------------------------------------------------------------------------ inputs
+def test_synth_inputs_seeded_and_normal():
+    a = oracle.synth_bf16(1, 1, (1000, 128))
+    b = oracle.synth_bf16(1, 1, (1000, 128))
+    c = oracle.synth_bf16(1, 2, (1000, 128))
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    x = oracle.bf16_to_f32(a).astype(np.float64)
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 1) < 0.01
+    # first values are a committed regression vector (lro.c documents the generator)
+    assert a.reshape(-1)[:4].tolist() == [49054, 48277, 15911, 49086]
+
+
+def test_bf16_rounding_is_rne():
+    vals = np.array([1.0, 1.00390625, 1.005859375, 1.0078125, -2.5, 3.0e38, 1e-40], np.float32)
+    got = oracle.f32_to_bf16(vals)
+    ref = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
