@@ -94,7 +94,7 @@ int lr_attention_bf16_ex(const void* q, const void* k, const void* v, void* out,
  *   y = x / sqrt(mean(x^2) + eps) * w[d]       (fp32; rounded to bf16 here when round_norm != 0)
  *   pairs rotated with table row r; dims >= rot_dim are norm-only
  *   dst[bi*dst_b_stride + r*dst_row_stride + h*128 + d] = bf16(y)
- * w: [128] of w_kind (LR_WEIGHT_*), NULL with LR_WEIGHT_NONE. table_kind LR_TABLE_*, table_row_stride in elements.
+ * w: [128] of w_kind (LR_WEIGHT_*), 16-byte aligned, NULL with LR_WEIGHT_NONE. table_kind LR_TABLE_*, table_row_stride in elements.
  * rot_dim: even, <= 128 (0 = 128); LR_PAIR_SPLIT_HALF needs rot_dim % 16 == 0.
  */
 int lr_rms_rope_bf16(const void* src, int64_t src_row_stride, int64_t src_off, void* dst, int64_t dst_row_stride,
@@ -119,7 +119,7 @@ size_t lr_joint_attention_workspace_bytes(int Sk, int HK);
  * The fused joint attention: QK-RMSNorm + RoPE + attention in two launches (keys normalised once into the workspace;
  * queries normalised and rotated in registers inside the attention kernel).
  *   q_raw [Sq][H][128], k_raw, v [Sk][HK][128], out [Sq][H][128] bf16 rows with the given row strides.
- *   q_norm_w, k_norm_w: fp32 [128] or NULL (ones). eps >= 0.
+ *   q_norm_w, k_norm_w: fp32 [128], 16-byte aligned, or NULL (ones). eps >= 0.
  *   Query i uses q-table row i; key j >= n_pre uses k-table row j - n_pre; keys j < n_pre are already normalised and
  *   rotated (a cached text prefix) and are used as they are.
  *   table_kind / pairing / rot_dim as in lr_rms_rope_bf16, except LR_PAIR_SPLIT_HALF needs rot_dim % 32 == 0.

@@ -474,21 +474,47 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
     }
     const int vcol = 8 * (lchunk ^ (lrow << 2));   // rows 4i + lrow: (r & 3) == lrow
     const uint32_t kr_lds = lds_addr(Kr), vr_lds = lds_addr(Vr);
+    // Source pointers of the next K and V tiles to load, advanced one tile per issue; a tile reaching past nkeys
+    // takes the clamped path instead.
+    const int64_t kstep = (int64_t)BN * a.k_rs, vstep = (int64_t)BN * a.v_rs;
+    const uint16_t* kp[LOADS];
+    const uint16_t* vp[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        kp[j] = kbase + (int64_t)krow[j] * a.k_rs + kcol[j];
+        vp[j] = vbase + (int64_t)krow[j] * a.v_rs + vcol;
+    }
     auto issue_k = [&](int t, int slot) {
         const int key0 = t * BN;
+        const uint32_t dst = kr_lds + 2 * (slot * TILE + wave * 512);
+        if (key0 + BN <= a.nkeys) {
 #pragma unroll
-        for (int j = 0; j < LOADS; ++j) {
-            const int key = min(key0 + krow[j], a.nkeys - 1);
-            dma16(kbase + (int64_t)key * a.k_rs + kcol[j], kr_lds + 2 * (slot * TILE + (wave + NW * j) * 512));
+            for (int j = 0; j < LOADS; ++j) dma16(kp[j], dst + 2 * NW * 512 * j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < LOADS; ++j) {
+                const int key = min(key0 + krow[j], a.nkeys - 1);
+                dma16(kbase + (int64_t)key * a.k_rs + kcol[j], dst + 2 * NW * 512 * j);
+            }
         }
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) kp[j] += kstep;
     };
     auto issue_v = [&](int t, int slot) {
         const int key0 = t * BN;
+        const uint32_t dst = vr_lds + 2 * (slot * TILE + wave * 512);
+        if (key0 + BN <= a.nkeys) {
 #pragma unroll
-        for (int j = 0; j < LOADS; ++j) {
-            const int key = min(key0 + krow[j], a.nkeys - 1);
-            dma16(vbase + (int64_t)key * a.v_rs + vcol, vr_lds + 2 * (slot * TILE + (wave + NW * j) * 512));
+            for (int j = 0; j < LOADS; ++j) dma16(vp[j], dst + 2 * NW * 512 * j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < LOADS; ++j) {
+                const int key = min(key0 + krow[j], a.nkeys - 1);
+                dma16(vbase + (int64_t)key * a.v_rs + vcol, dst + 2 * NW * 512 * j);
+            }
         }
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) vp[j] += vstep;
     };
 
     // ---- queries (B operands of S^T = K Q^T)
@@ -542,6 +568,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
     float m_used = -1e30f, l_sum = 0.0f;
     const float c = a.c;
     const int pos = a.p0 + wrow0 + n;
+    const bf16x2 ones2 = {(bf16)1.0f, (bf16)1.0f};
 
     // keys past nkeys and (causal) past the query's position -> -inf; only tiles that reach either limit
     auto needs_mask = [&](int t) {
@@ -598,15 +625,18 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
             for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
-                    bf16x8 f;
+                    // scalars, not a u32x4 indexed in a loop: hipcc 7.2 folds __builtin_bit_cast(bf16x2, w[j])
+                    // of a vector element to w[0] for every j
+                    uint32_t w[4];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) f[j] = (bf16)__builtin_amdgcn_exp2f(fmaf(sc[mb][8 * hh + j], c, nm));
+                    for (int j = 0; j < 4; ++j)
+                        w[j] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sc[mb][8 * hh + 2 * j], c, nm)),
+                                           __builtin_amdgcn_exp2f(fmaf(sc[mb][8 * hh + 2 * j + 1], c, nm)));
+                    // the row sum of the bf16 P exactly as the PV MFMA consumes it
 #pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        bf16x2 pp = {f[j], f[j + 1]};
-                        ls = __builtin_amdgcn_fdot2_f32_bf16(pp, bf16x2{(bf16)1.0f, (bf16)1.0f}, ls, false);
-                    }
-                    pf[2 * mb + hh] = f;
+                    for (int j = 0; j < 4; ++j)
+                        ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]), ones2, ls, false);
+                    pf[2 * mb + hh] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
                 }
             }
             l_sum = ls;

@@ -65,7 +65,7 @@ int keys_impl(const void* k_raw, int64_t k_rs, const float* wk, int table_kind, 
     if (rot == 0) rot = lr::D;
     if (Sk < 1 || HK < 1 || Sk > INT_MAX - 512 || n_pre < 0 || n_pre > Sk || !(eps >= 0.0f) || !isfinite(eps))
         return ERR_ARGS;
-    if (!rows_ok(k_raw, k_rs, HK) || (wk && !aligned(wk, 4))) return ERR_ARGS;
+    if (!rows_ok(k_raw, k_rs, HK) || (wk && !aligned(wk, 16))) return ERR_ARGS;
     if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
     const size_t need = lr_joint_attention_workspace_bytes(Sk, HK);
     if (!ws || !aligned(ws, 256) || ws_bytes < need) return ERR_ARGS;
@@ -92,7 +92,7 @@ int prepared_impl(const void* q_raw, const void* ws, size_t ws_bytes, const void
     if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_REGSTAGE_W8) return ERR_ARGS;
     if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return ERR_ARGS;
     if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H) || !rows_ok(v, v_rs, HK)) return ERR_ARGS;
-    if (!table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) || (wq && !aligned(wq, 4))) return ERR_ARGS;
+    if (!table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) || (wq && !aligned(wq, 16))) return ERR_ARGS;
     if (!ws || !aligned(ws, 256) || ws_bytes < lr_joint_attention_workspace_bytes(Sk, HK)) return ERR_ARGS;
     lr::AttnArgs a{};
     a.q = static_cast<const uint16_t*>(q_raw);
@@ -124,7 +124,7 @@ int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, c
         return ERR_ARGS;
     if (!table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
     if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
-    if ((wq && !aligned(wq, 4)) || (wk && !aligned(wk, 4))) return ERR_ARGS;
+    if ((wq && !aligned(wq, 16)) || (wk && !aligned(wk, 16))) return ERR_ARGS;
     if (!ws || !aligned(ws, 256) || ws_bytes < lr_joint_attention_workspace_bytes(Sk, HK)) return ERR_ARGS;
     const int e = keys_impl(k_raw, k_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws,
                             ws_bytes, stream);
@@ -141,7 +141,7 @@ int rope_impl(const void* src, int64_t src_rs, int64_t src_off, void* dst, int64
     if (n < 1 || b < 1 || heads < 1 || !(eps >= 0.0f) || !isfinite(eps) || (round_norm != 0 && round_norm != 1))
         return ERR_ARGS;
     if (w_kind < LR_WEIGHT_NONE || w_kind > LR_WEIGHT_BF16 || (w_kind != LR_WEIGHT_NONE && !w)) return ERR_ARGS;
-    if (w && !aligned(w, w_kind == LR_WEIGHT_F32 ? 4 : 2)) return ERR_ARGS;
+    if (w && !aligned(w, 16)) return ERR_ARGS;
     if (!table_ok(table_kind, ta, tb, tab_stride, rot, pairing, 16)) return ERR_ARGS;
     if (!src || !dst || src_off < 0 || src_off % 8 || src_bs % 8 || dst_bs % 8) return ERR_ARGS;
     const char* s0 = static_cast<const char*>(src) + src_off * 2;
