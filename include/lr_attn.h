@@ -60,6 +60,10 @@ typedef struct ihipStream_t* lr_stream_t;
                                       QK^T overlapped with the current tile's softmax */
 #define LR_ATTN_CFG_PIPE_W4 2      /* the same kernel with 128 queries per workgroup (4 waves x 32) */
 #define LR_ATTN_CFG_REGSTAGE_W8 3  /* 256 queries per workgroup, K/V staged through registers (2-stage ring) */
+#define LR_ATTN_CFG_PINGPONG_W8 4  /* 256 queries per workgroup, two groups of 4 waves alternating an MFMA cluster and
+                                      a softmax cluster, 4-stage direct-to-LDS K/V ring */
+#define LR_ATTN_CFG_WIDE_W4 5      /* 256 queries per workgroup (4 waves x 64): every K/V operand fragment feeds two
+                                      MFMAs, one wave per SIMD */
 
 int lr_attn_abi_version(void);
 

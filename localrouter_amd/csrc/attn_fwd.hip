@@ -437,17 +437,364 @@ __device__ __forceinline__ void block_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int NW, bool FUSEQ>
-__global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
-    constexpr int BM = 32 * NW;
-    constexpr int TILE = BN * D;       // elements per K or V tile
-    constexpr int LOADS = 16 / NW;     // direct loads (1 KB each) per wave per K or V tile
+// NW waves of NQB x 32 queries each; tiles of BT keys in an NS-stage K/V ring. NQB = 2 reads every K and V operand
+// fragment from LDS once for two 32-query MFMAs, halving LDS traffic per MFMA, at one wave per SIMD (its registers
+// need it); BT = 32 then keeps the two score buffers at 32 registers each.
+template <int NW, int NQB, int BT, int NS, bool FUSEQ>
+__global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1) void attn_fwd_pipe_kernel(AttnArgs a) {
+    static_assert(NS >= 2 && NS <= 4, "2- to 4-stage ring");
+    static_assert(NQB == 1 || NQB == 2, "one or two 32-query blocks per wave");
+    static_assert(BT == 32 || BT == 64, "32- or 64-key tiles");
+    constexpr int BM = 32 * NQB * NW;
+    constexpr int MB = BT / 32;        // 32-key score blocks per tile
+    constexpr int KK = BT / 16;        // 16-key PV steps per tile
+    constexpr int TILE = BT * D;       // elements per K or V tile
+    constexpr int LOADS = BT / 4 / NW; // direct loads (1 KB = 4 rows each) per wave per K or V tile
+    static_assert(LOADS >= 1, "every wave loads");
     typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
-    __shared__ __attribute__((aligned(1024))) uint16_t Kr[NSTAGE * TILE];
-    __shared__ __attribute__((aligned(1024))) uint16_t Vr[NSTAGE * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t Kr[NS * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vr[NS * TILE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, hf = lane >> 5;
+
+    const int nwg = gridDim.x, b = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
+    const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int nqb = (a.W + BM - 1) / BM;
+    const int head = logical / nqb, qblk = logical - head * nqb;
+    const int hk = head / a.G;
+    const int row0 = qblk * BM, wrow0 = row0 + wave * 32 * NQB;
+    const int last_row = min(row0 + BM, a.W) - 1;
+    int ntiles = (a.nkeys + BT - 1) / BT;
+    if (a.causal) ntiles = min(ntiles, (a.p0 + last_row) / BT + 1);
+    const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
+    const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs;
+
+    // ---- direct loads: instruction i (0 .. BT/4 - 1) of a tile fills rows 4i..4i+3; lane -> row 4i + (lane >> 4) and LDS
+    // chunk (lane & 15), which must hold logical chunk (lane & 15) ^ swizzle(row). Rows past nkeys read the last
+    // valid row instead (finite data; those keys are masked and their V rows meet P = 0).
+    const int lrow = lane >> 4, lchunk = lane & 15;
+    int krow[LOADS], kcol[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        krow[j] = 4 * (wave + NW * j) + lrow;
+        kcol[j] = 8 * (lchunk ^ (krow[j] & 15));
+    }
+    const int vcol = 8 * (lchunk ^ (lrow << 2));   // rows 4i + lrow: (r & 3) == lrow
+    const uint32_t kr_lds = lds_addr(Kr), vr_lds = lds_addr(Vr);
+    // Source pointers of the next K and V tiles to load, advanced one tile per issue; a tile reaching past nkeys
+    // takes the clamped path instead.
+    const int64_t kstep = (int64_t)BT * a.k_rs, vstep = (int64_t)BT * a.v_rs;
+    const uint16_t* kp[LOADS];
+    const uint16_t* vp[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        kp[j] = kbase + (int64_t)krow[j] * a.k_rs + kcol[j];
+        vp[j] = vbase + (int64_t)krow[j] * a.v_rs + vcol;
+    }
+    auto issue_k = [&](int t, int slot) {
+        const int key0 = t * BT;
+        const uint32_t dst = kr_lds + 2 * (slot * TILE + wave * 512);
+        if (key0 + BT <= a.nkeys) {
+#pragma unroll
+            for (int j = 0; j < LOADS; ++j) dma16(kp[j], dst + 2 * NW * 512 * j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < LOADS; ++j) {
+                const int key = min(key0 + krow[j], a.nkeys - 1);
+                dma16(kbase + (int64_t)key * a.k_rs + kcol[j], dst + 2 * NW * 512 * j);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) kp[j] += kstep;
+    };
+    auto issue_v = [&](int t, int slot) {
+        const int key0 = t * BT;
+        const uint32_t dst = vr_lds + 2 * (slot * TILE + wave * 512);
+        if (key0 + BT <= a.nkeys) {
+#pragma unroll
+            for (int j = 0; j < LOADS; ++j) dma16(vp[j], dst + 2 * NW * 512 * j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < LOADS; ++j) {
+                const int key = min(key0 + krow[j], a.nkeys - 1);
+                dma16(vbase + (int64_t)key * a.v_rs + vcol, dst + 2 * NW * 512 * j);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) vp[j] += vstep;
+    };
+
+    // ---- queries (B operands of S^T = K Q^T), one set per 32-query block
+    bf16x8 qf[NQB][8];
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+        if constexpr (FUSEQ)
+            load_q_fused(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
+        else
+            load_q_plain(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
+    }
+
+    // ---- per-lane LDS offsets
+    const int pr = key_perm(n);
+    int kfrag[MB];                       // K A-operand row offsets of the 32-key blocks (chunk added per k-step)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) kfrag[mb] = (32 * mb + pr) * D;
+    const int kswz = pr & 15;            // (32 + pr) & 15 == pr & 15
+    // V^T operand by transposed reads: lane (group g = lane >> 4, s = lane & 15) addresses row 16kk + 8h + 4part +
+    // (s >> 2), dims 32db + 16(g & 1) + 4(s & 3) .. +4, h = g >> 1.
+    const int g = lane >> 4, sl = lane & 15;
+    int vtr[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        const int chunk = 4 * (db ^ (sl >> 2)) + 2 * (g & 1) + ((sl & 3) >> 1);
+        vtr[db] = (8 * (g >> 1) + (sl >> 2)) * D + 8 * chunk + 4 * (sl & 1);
+    }
+
+    // one K operand fragment, used by every query block
+    auto qk_block = [&](const uint16_t* kt, int ks, int mb, f32x16 (&acc)[NQB][MB]) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kt + kfrag[mb] + 8 * ((2 * ks + hf) ^ kswz));
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb)
+            acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[nb][ks], acc[nb][mb], 0, 0, 0);
+    };
+
+    // ---- prologue: K(0 .. NS-1) and V(0 .. NS-2) resident; S(0)
+    for (int i = 0; i < NS && i < ntiles; ++i) issue_k(i, i);
+    for (int i = 0; i < NS - 1 && i < ntiles; ++i) issue_v(i, i);
+    LR_WAIT_VMCNT(0);
+    block_barrier();
+    f32x16 sA[NQB][MB], sB[NQB][MB];
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) sA[nb][mb] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) qk_block(Kr, ks, mb, sA);
+    block_barrier();   // every wave is done with K slot 0 before step 0 refills it
+
+    f32x16 o[NQB][4];
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[nb][db] = f32x16{};
+    // m_used starts at a finite -1e30 (not -inf): every alpha below is exp2 of a finite value or of -inf (= 0)
+    float m_used[NQB], l_sum[NQB];
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+        m_used[nb] = -1e30f;
+        l_sum[nb] = 0.0f;
+    }
+    const float c = a.c;
+    const bf16x2 ones2 = {(bf16)1.0f, (bf16)1.0f};
+
+    // keys past nkeys and (causal) past the query's position -> -inf; only tiles that reach either limit
+    auto needs_mask = [&](int t) {
+        const int key0 = t * BT;
+        return key0 + BT > a.nkeys || (a.causal && key0 + BT - 1 > a.p0 + wrow0);
+    };
+    auto mask_tile = [&](int t, f32x16 (&sc)[NQB][MB]) {
+        const int key0 = t * BT;
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb) {
+            const int pos = a.p0 + wrow0 + 32 * nb + n;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = key0 + 32 * mb + 16 * (r >> 3) + 8 * hf + (r & 7);
+                    if (!(key < a.nkeys && (!a.causal || key <= pos))) sc[nb][mb][r] = -INFINITY;
+                }
+        }
+    };
+    // a query's max over a score tile, scaled into the exp2 domain (both lanes of the query agree)
+    auto tile_max = [&](const f32x16 (&sc)[NQB][MB], float (&mx)[NQB]) {
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb) {
+            float m = fmaxf(sc[nb][0][0], sc[nb][0][1]);
+#pragma unroll
+            for (int r = 2; r < 16; ++r) m = fmaxf(m, sc[nb][0][r]);
+#pragma unroll
+            for (int mb = 1; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) m = fmaxf(m, sc[nb][mb][r]);
+            mx[nb] = wave_pair_max(m) * c;
+        }
+    };
+    // raise the running max (and rescale O, l) when a tile's max exceeds it by more than 2^8
+    auto rescale_for = [&](const float (&mx)[NQB]) {
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb) {
+            if (__builtin_amdgcn_ballot_w64(mx[nb] > m_used[nb] + RESCALE_TAU)) {
+                const float mn = fmaxf(m_used[nb], mx[nb]);
+                const float alpha = __builtin_amdgcn_exp2f(m_used[nb] - mn);
+                m_used[nb] = mn;
+                l_sum[nb] *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) o[nb][db] *= alpha;
+            }
+        }
+    };
+    float mx_cur[NQB];
+    tile_max(sA, mx_cur);
+    if (!needs_mask(0)) rescale_for(mx_cur);
+
+    // One tile t. On entry: sc = S(t), its max mx, and -- unless tile t needs masking -- the running max already
+    // raised for it. Then
+    //   mask (only tiles at nkeys or the causal diagonal; branch): -inf the hidden keys, recompute mx, raise;
+    //   refill the ring for later tiles;
+    //   A: S(t+1) on the MFMAs  ||  P(t) = exp2(S(t) c - m), its row sums and bf16 packing on the VALU;
+    //   B: O += V(t)^T P(t)     ||  the max of S(t+1) on the VALU;
+    //   raise the running max for tile t+1 (rare, branch), wait for the next tiles, barrier.
+    // A and B form one basic block, so the scheduler can interleave across all of it.
+    auto step = [&](int t, f32x16 (&sc)[NQB][MB], f32x16 (&sn)[NQB][MB], float (&mx)[NQB]) {
+        if (needs_mask(t)) {
+            mask_tile(t, sc);
+            tile_max(sc, mx);
+            rescale_for(mx);
+        }
+        // ---- refill: K(t+NS) into the slot K(t) left, V(t+NS-1) into the slot V(t-1) left (both read last step)
+        const bool refilled = t + NS < ntiles;
+        if (refilled) {
+            issue_k(t + NS, t % NS);
+            issue_v(t + NS - 1, (t + NS - 1) % NS);
+        } else if (t + NS - 1 < ntiles) {
+            issue_v(t + NS - 1, (t + NS - 1) % NS);
+        }
+        bf16x8 pf[NQB][KK];
+        auto exps = [&]() {
+#pragma unroll
+            for (int nb = 0; nb < NQB; ++nb) {
+                const float nm = -m_used[nb];
+                float ls = l_sum[nb];
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        // scalars, not a u32x4 indexed in a loop: hipcc 7.2 folds __builtin_bit_cast(bf16x2, w[j])
+                        // of a vector element to w[0] for every j
+                        uint32_t w[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            w[j] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sc[nb][mb][8 * hh + 2 * j], c, nm)),
+                                               __builtin_amdgcn_exp2f(fmaf(sc[nb][mb][8 * hh + 2 * j + 1], c, nm)));
+                        // the row sum of the bf16 P exactly as the PV MFMA consumes it
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]), ones2, ls, false);
+                        pf[nb][2 * mb + hh] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
+                    }
+                }
+                l_sum[nb] = ls;
+            }
+        };
+        {
+            // the last tile computes a throw-away S from a stale slot rather than branching: A and B stay one block
+            const uint16_t* kt = Kr + ((t + 1) % NS) * TILE;
+#pragma unroll
+            for (int nb = 0; nb < NQB; ++nb)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) sn[nb][mb] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) qk_block(kt, ks, mb, sn);
+            exps();
+            // interleave: two K reads ahead, then 8 MB x (NQB x (1 MFMA, 6 VALU), 1 DS read)
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < 8 * MB; ++i) {
+#pragma unroll
+                for (int nb = 0; nb < NQB; ++nb) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        }
+        // ---- B: O^T += V^T P^T, with the next tile's max on the VALU
+        const uint16_t* vt = Vr + (t % NS) * TILE;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const uint16_t* p0 = vt + vtr[db] + (16 * kk) * D;
+                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 4 * D));
+                const bf16x8 vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi),
+                                                          0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int nb = 0; nb < NQB; ++nb)
+                    o[nb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[nb][kk], o[nb][db], 0, 0, 0);
+            }
+        }
+        tile_max(sn, mx);
+        if (t + 1 < ntiles && !needs_mask(t + 1)) rescale_for(mx);
+        // ---- K(t+2) and V(t+1) (issued a step ago with 3 stages, at this step's start with 2) must have landed
+        if (NS == 2 || !refilled) LR_WAIT_VMCNT(0);
+        else LR_WAIT_VMCNT(2 * LOADS);
+        block_barrier();
+    };
+
+    int t = 0;
+    for (; t + 1 < ntiles; t += 2) {
+        step(t, sA, sB, mx_cur);
+        step(t + 1, sB, sA, mx_cur);
+    }
+    if (t < ntiles) step(t, sA, sB, mx_cur);
+
+    // ---- epilogue: O / l -> bf16 rows
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+        const int qrow = wrow0 + 32 * nb + n;
+        const float l = wave_pair_sum(l_sum[nb]);
+        const float inv = 1.0f / l;
+        if (qrow < a.W) {
+            uint16_t* dst = a.out + (int64_t)qrow * a.o_rs + head * D + 4 * hf;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) {
+                    u32x2 w;
+                    w[0] = pack_bf16x2(o[nb][db][4 * gg] * inv, o[nb][db][4 * gg + 1] * inv);
+                    w[1] = pack_bf16x2(o[nb][db][4 * gg + 2] * inv, o[nb][db][4 * gg + 3] * inv);
+                    *reinterpret_cast<u32x2*>(dst + 32 * db + 8 * gg) = w;
+                }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ ping-pong kernel
+// Eight waves in two groups of four (waves w and w + 4 share a SIMD). Each wave alternates two clusters per tile t:
+//   M(t): S(t+1) = K(t+1) Q^T and O += V(t)^T P(t) -- MFMAs and their LDS operand reads only;
+//   V(t): mask / max / rescale / exp2 / bf16 packing / row sums of S(t+1) -> P(t+1), and the direct loads of
+//         K(t+4) and V(t+3) -- VALU and VMEM only.
+// Group 1 trails group 0 by one cluster, and every cluster ends at a workgroup barrier, so while one wave of a SIMD
+// issues back-to-back MFMAs the other runs its softmax on the VALU. K and V tiles sit in a 4-stage ring (128 KB):
+// a slot is refilled two clusters after its last reader and read at least four clusters after the refill is issued.
+constexpr int PP_STAGES = 4;
+
+__device__ __forceinline__ void wait_vm_le(int n) {
+    // s_waitcnt takes an immediate: the counts that occur here are 0, 2, 4, 6, 8
+    if (n >= 8) LR_WAIT_VMCNT(8);
+    else if (n >= 6) LR_WAIT_VMCNT(6);
+    else if (n >= 4) LR_WAIT_VMCNT(4);
+    else if (n >= 2) LR_WAIT_VMCNT(2);
+    else LR_WAIT_VMCNT(0);
+}
+
+template <bool FUSEQ>
+__global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(AttnArgs a) {
+    constexpr int NW = 8, BM = 32 * NW, TILE = BN * D, LOADS = 16 / NW;
+    __shared__ __attribute__((aligned(1024))) uint16_t Kr[PP_STAGES * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vr[PP_STAGES * TILE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 31, hf = lane >> 5;
+    const int grp = wave >> 2;
 
     const int nwg = gridDim.x, b = blockIdx.x;
     const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
@@ -462,9 +809,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
     const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
     const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs;
 
-    // ---- direct loads: instruction i (0..15) of a tile fills rows 4i..4i+3; lane -> row 4i + (lane >> 4) and LDS
-    // chunk (lane & 15), which must hold logical chunk (lane & 15) ^ swizzle(row). Rows past nkeys read the last
-    // valid row instead (finite data; those keys are masked and their V rows meet P = 0).
+    // ---- direct loads (as in the pipelined kernel)
     const int lrow = lane >> 4, lchunk = lane & 15;
     int krow[LOADS], kcol[LOADS];
 #pragma unroll
@@ -472,10 +817,8 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
         krow[j] = 4 * (wave + NW * j) + lrow;
         kcol[j] = 8 * (lchunk ^ (krow[j] & 15));
     }
-    const int vcol = 8 * (lchunk ^ (lrow << 2));   // rows 4i + lrow: (r & 3) == lrow
+    const int vcol = 8 * (lchunk ^ (lrow << 2));
     const uint32_t kr_lds = lds_addr(Kr), vr_lds = lds_addr(Vr);
-    // Source pointers of the next K and V tiles to load, advanced one tile per issue; a tile reaching past nkeys
-    // takes the clamped path instead.
     const int64_t kstep = (int64_t)BN * a.k_rs, vstep = (int64_t)BN * a.v_rs;
     const uint16_t* kp[LOADS];
     const uint16_t* vp[LOADS];
@@ -484,9 +827,9 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
         kp[j] = kbase + (int64_t)krow[j] * a.k_rs + kcol[j];
         vp[j] = vbase + (int64_t)krow[j] * a.v_rs + vcol;
     }
-    auto issue_k = [&](int t, int slot) {
+    auto issue_k = [&](int t) {
         const int key0 = t * BN;
-        const uint32_t dst = kr_lds + 2 * (slot * TILE + wave * 512);
+        const uint32_t dst = kr_lds + 2 * ((t % PP_STAGES) * TILE + wave * 512);
         if (key0 + BN <= a.nkeys) {
 #pragma unroll
             for (int j = 0; j < LOADS; ++j) dma16(kp[j], dst + 2 * NW * 512 * j);
@@ -500,9 +843,9 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < LOADS; ++j) kp[j] += kstep;
     };
-    auto issue_v = [&](int t, int slot) {
+    auto issue_v = [&](int t) {
         const int key0 = t * BN;
-        const uint32_t dst = vr_lds + 2 * (slot * TILE + wave * 512);
+        const uint32_t dst = vr_lds + 2 * ((t % PP_STAGES) * TILE + wave * 512);
         if (key0 + BN <= a.nkeys) {
 #pragma unroll
             for (int j = 0; j < LOADS; ++j) dma16(vp[j], dst + 2 * NW * 512 * j);
@@ -516,22 +859,21 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < LOADS; ++j) vp[j] += vstep;
     };
+    // loads issued by V(x): K(x+4) and V(x+3) while those tiles exist
+    auto loads_in = [&](int x) { return (x + 4 < ntiles ? LOADS : 0) + (x + 3 < ntiles ? LOADS : 0); };
 
-    // ---- queries (B operands of S^T = K Q^T)
+    // ---- queries
     bf16x8 qf[8];
     if constexpr (FUSEQ)
         load_q_fused(a, wrow0 + n, head, hf, qf);
     else
         load_q_plain(a, wrow0 + n, head, hf, qf);
 
-    // ---- per-lane LDS offsets
     const int pr = key_perm(n);
-    int kfrag[2];                        // K A-operand row offsets for the two 32-key blocks (chunk added per k-step)
+    int kfrag[2];
     kfrag[0] = pr * D;
     kfrag[1] = (32 + pr) * D;
-    const int kswz = pr & 15;            // (32 + pr) & 15 == pr & 15
-    // V^T operand by transposed reads: lane (group g = lane >> 4, s = lane & 15) addresses row 16kk + 8h + 4part +
-    // (s >> 2), dims 32db + 16(g & 1) + 4(s & 3) .. +4, h = g >> 1.
+    const int kswz = pr & 15;
     const int g = lane >> 4, sl = lane & 15;
     int vtr[4];
 #pragma unroll
@@ -539,76 +881,65 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
         const int chunk = 4 * (db ^ (sl >> 2)) + 2 * (g & 1) + ((sl & 3) >> 1);
         vtr[db] = (8 * (g >> 1) + (sl >> 2)) * D + 8 * chunk + 4 * (sl & 1);
     }
+    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
 
     auto qk_block = [&](const uint16_t* kt, int ks, int mb, f32x16& acc) {
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kt + kfrag[mb] + 8 * ((2 * ks + hf) ^ kswz));
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], acc, 0, 0, 0);
     };
+    auto pv_block = [&](const uint16_t* vt, int kk, int db, const bf16x8& p, f32x16& acc) {
+        const uint16_t* p0 = vt + vtr[db] + (16 * kk) * D;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 4 * D));
+        const bf16x8 vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi), 0, 1,
+                                                  2, 3, 4, 5, 6, 7);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, p, acc, 0, 0, 0);
+    };
 
-    // ---- prologue: tiles 0 (K, V), 1 (K, V), 2 (K) in flight; S(0)
-    issue_k(0, 0);
-    issue_v(0, 0);
-    if (ntiles > 1) { issue_k(1, 1); issue_v(1, 1); }
-    if (ntiles > 2) issue_k(2, 2);
+    // ---- prologue: K(0..3), V(0..2) resident; S(0) and P(0)
+    issue_k(0);
+    issue_v(0);
+    if (ntiles > 1) { issue_k(1); issue_v(1); }
+    if (ntiles > 2) { issue_k(2); issue_v(2); }
+    if (ntiles > 3) issue_k(3);
     LR_WAIT_VMCNT(0);
     block_barrier();
-    f32x16 sA[2], sB[2];
-    sA[0] = f32x16{};
-    sA[1] = f32x16{};
+
+    f32x16 s[2];
+    s[0] = f32x16{};
+    s[1] = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) qk_block(Kr, ks, mb, sA[mb]);
-    block_barrier();   // every wave is done with K slot 0 before step 0 refills it
+        for (int mb = 0; mb < 2; ++mb) qk_block(Kr, ks, mb, s[mb]);
 
     f32x16 o[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] = f32x16{};
-    // m_used starts at a finite -1e30 (not -inf): every alpha below is exp2 of a finite value or of -inf (= 0)
-    float m_used = -1e30f, l_sum = 0.0f;
+    float m_used = -1e30f, l_sum = 0.0f;   // finite start: every alpha is exp2 of a finite value or of -inf
     const float c = a.c;
     const int pos = a.p0 + wrow0 + n;
     const bf16x2 ones2 = {(bf16)1.0f, (bf16)1.0f};
+    bf16x8 pf[4];
 
-    // keys past nkeys and (causal) past the query's position -> -inf; only tiles that reach either limit
-    auto needs_mask = [&](int t) {
+    // softmax of the score tile t held in s -> pf (P(t)), with the running max and row sum
+    auto softmax_tile = [&](int t) {
         const int key0 = t * BN;
-        return key0 + BN > a.nkeys || (a.causal && key0 + BN - 1 > a.p0 + wrow0);
-    };
-    auto mask_tile = [&](int t, f32x16 (&sc)[2]) {
-        const int key0 = t * BN;
+        if (key0 + BN > a.nkeys || (a.causal && key0 + BN - 1 > a.p0 + wrow0)) {
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+            for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = key0 + 32 * mb + 16 * (r >> 3) + 8 * hf + (r & 7);
-                if (!(key < a.nkeys && (!a.causal || key <= pos))) sc[mb][r] = -INFINITY;
-            }
-    };
-    // the query's max over a score tile, scaled into the exp2 domain (both lanes of the query agree)
-    auto tile_max = [&](const f32x16 (&sc)[2]) {
-        float mx = fmaxf(sc[0][0], sc[0][1]);
-#pragma unroll
-        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, sc[0][r]);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][r]);
-        return wave_pair_max(mx) * c;
-    };
-
-    float mx_cur = tile_max(sA);
-
-    // One tile t. On entry: sc = S(t) and mx = its unmasked max. Then
-    //   mask (only tiles at nkeys or the causal diagonal; branch): -inf the hidden keys, recompute mx;
-    //   rescale (rare, branch): raise the running max when the tile's exceeds it by more than 2^8;
-    //   A: S(t+1) on the MFMAs  ||  P(t) = exp2(S(t) c - m), its row sums and bf16 packing on the VALU;
-    //   B: O += V(t)^T P(t)     ||  the max of S(t+1) on the VALU;
-    //   refill the ring, wait for the next tiles, barrier.
-    // A and B form one basic block, so the scheduler can interleave across all of it.
-    auto step = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2], float& mx) {
-        if (needs_mask(t)) {
-            mask_tile(t, sc);
-            mx = tile_max(sc);
+                for (int r = 0; r < 16; ++r) {
+                    const int key = key0 + 32 * mb + 16 * (r >> 3) + 8 * hf + (r & 7);
+                    if (!(key < a.nkeys && (!a.causal || key <= pos))) s[mb][r] = -INFINITY;
+                }
         }
+        float mx = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[1][r]);
+        mx = wave_pair_max(mx) * c;
         if (__builtin_amdgcn_ballot_w64(mx > m_used + RESCALE_TAU)) {
             const float mn = fmaxf(m_used, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_used - mn);
@@ -618,83 +949,71 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
             for (int db = 0; db < 4; ++db) o[db] *= alpha;
         }
         const float nm = -m_used;
-        bf16x8 pf[4];
-        auto exps = [&]() {
-            float ls = l_sum;
+        float ls = l_sum;
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    // scalars, not a u32x4 indexed in a loop: hipcc 7.2 folds __builtin_bit_cast(bf16x2, w[j])
-                    // of a vector element to w[0] for every j
-                    uint32_t w[4];
+            for (int hh = 0; hh < 2; ++hh) {
+                // scalars, not a u32x4 indexed in a loop: hipcc 7.2 folds __builtin_bit_cast(bf16x2, w[j]) of a
+                // vector element to w[0] for every j
+                uint32_t w[4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        w[j] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sc[mb][8 * hh + 2 * j], c, nm)),
-                                           __builtin_amdgcn_exp2f(fmaf(sc[mb][8 * hh + 2 * j + 1], c, nm)));
-                    // the row sum of the bf16 P exactly as the PV MFMA consumes it
+                for (int j = 0; j < 4; ++j)
+                    w[j] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[mb][8 * hh + 2 * j], c, nm)),
+                                       __builtin_amdgcn_exp2f(fmaf(s[mb][8 * hh + 2 * j + 1], c, nm)));
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]), ones2, ls, false);
-                    pf[2 * mb + hh] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
-                }
-            }
-            l_sum = ls;
-        };
-        {
-            // the last tile computes a throw-away S from a stale slot rather than branching: A and B stay one block
-            const uint16_t* kt = Kr + ((t + 1) % NSTAGE) * TILE;
-            sn[0] = f32x16{};
-            sn[1] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb) qk_block(kt, ks, mb, sn[mb]);
-            exps();
-            // interleave: two K reads ahead, then 16 x (1 MFMA, 6 VALU, 1 DS read)
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int j = 0; j < 4; ++j)
+                    ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]), ones2, ls, false);
+                pf[2 * mb + hh] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
             }
         }
-        // ---- B: O^T += V^T P^T, with the next tile's max on the VALU
-        const uint16_t* vt = Vr + (t % NSTAGE) * TILE;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const uint16_t* p0 = vt + vtr[db] + (16 * kk) * D;
-                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
-                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 4 * D));
-                const bf16x8 vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi),
-                                                          0, 1, 2, 3, 4, 5, 6, 7);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kk], o[db], 0, 0, 0);
-            }
-        }
-        mx = tile_max(sn);
-        // ---- refill: K(t+3) into the slot K(t) left, V(t+2) into the slot V(t-1) left; then K(t+2), V(t+1) landed
-        if (t + 3 < ntiles) {
-            issue_k(t + 3, t % NSTAGE);
-            issue_v(t + 2, (t + 2) % NSTAGE);
-            LR_WAIT_VMCNT(2 * LOADS);
-        } else if (t + 2 < ntiles) {
-            issue_v(t + 2, (t + 2) % NSTAGE);
-            LR_WAIT_VMCNT(LOADS);
-        } else {
-            LR_WAIT_VMCNT(0);
-        }
-        block_barrier();
+        l_sum = ls;
     };
 
-    int t = 0;
-    for (; t + 1 < ntiles; t += 2) {
-        step(t, sA, sB, mx_cur);
-        step(t + 1, sB, sA, mx_cur);
+    softmax_tile(0);
+    block_barrier();                 // K slot 0 is free for K(4) once every wave has its S(0)
+    if (grp == 1) block_barrier();   // group 1 trails by one cluster
+
+    for (int t = 0; t < ntiles; ++t) {
+        const bool has_next = t + 1 < ntiles;
+        // ---- M(t)
+        __builtin_amdgcn_s_setprio(1);
+        {
+            const uint16_t* vt = Vr + (t % PP_STAGES) * TILE;
+            if (has_next) {
+                const uint16_t* kt = Kr + ((t + 1) % PP_STAGES) * TILE;
+                s[0] = f32x16{};
+                s[1] = f32x16{};
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    qk_block(kt, i >> 1, i & 1, s[i & 1]);
+                    pv_block(vt, i >> 2, i & 3, pf[i >> 2], o[i & 3]);
+                }
+                // operands: six reads ahead, then two MFMAs per three reads
+                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) pv_block(vt, i >> 2, i & 3, pf[i >> 2], o[i & 3]);
+            }
+        }
+        __builtin_amdgcn_s_setprio(0);
+        wait_vm_le(t >= 1 ? loads_in(t - 1) : 0);
+        block_barrier();
+        // ---- V(t)
+        if (has_next) softmax_tile(t + 1);
+        if (t + 4 < ntiles) issue_k(t + 4);
+        if (t + 3 < ntiles) issue_v(t + 3);
+        wait_vm_le((t >= 1 ? loads_in(t - 1) : 0) + loads_in(t));
+        block_barrier();
     }
-    if (t < ntiles) step(t, sA, sB, mx_cur);
+    if (grp == 0) block_barrier();   // group 0 leads by one cluster
 
     // ---- epilogue: O / l -> bf16 rows
     const int qrow = wrow0 + n;
@@ -714,6 +1033,15 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_pipe_kernel(AttnArgs a) {
     }
 }
 
+template <bool FUSEQ>
+hipError_t launch_pp(const AttnArgs& a, hipStream_t stream) {
+    const int64_t nqb = (a.W + 255) / 256;
+    const int64_t blocks = nqb * a.H;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_fwd_pp_kernel<FUSEQ>), dim3((unsigned)blocks), dim3(512), 0, stream, a);
+    return hipGetLastError();
+}
+
 template <int QW, int NW, bool FUSEQ>
 hipError_t launch_regstage(const AttnArgs& a, hipStream_t stream) {
     constexpr int BM = QW * NW;
@@ -724,13 +1052,14 @@ hipError_t launch_regstage(const AttnArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int NW, bool FUSEQ>
+template <int NW, int NQB, int BT, int NS, bool FUSEQ>
 hipError_t launch_pipe(const AttnArgs& a, hipStream_t stream) {
-    constexpr int BM = 32 * NW;
+    constexpr int BM = 32 * NQB * NW;
     const int64_t nqb = (a.W + BM - 1) / BM;
     const int64_t blocks = nqb * a.H;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, FUSEQ>), dim3((unsigned)blocks), dim3(NW * 64), 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, NQB, BT, NS, FUSEQ>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+                       stream, a);
     return hipGetLastError();
 }
 
@@ -747,11 +1076,15 @@ hipError_t launch_attention(const AttnArgs& a, bool fuse_q, int config, hipStrea
     if (config == ATTN_CFG_AUTO) config = ATTN_CFG_PIPE_W8;
     switch (config) {
         case ATTN_CFG_PIPE_W8:
-            return fuse_q ? launch_pipe<8, true>(a, stream) : launch_pipe<8, false>(a, stream);
-        case ATTN_CFG_PIPE_W4:
-            return fuse_q ? launch_pipe<4, true>(a, stream) : launch_pipe<4, false>(a, stream);
+            return fuse_q ? launch_pipe<8, 1, 64, 3, true>(a, stream) : launch_pipe<8, 1, 64, 3, false>(a, stream);
+        case ATTN_CFG_PIPE_W4:   // 64 KB of LDS so that two 4-wave blocks share a CU
+            return fuse_q ? launch_pipe<4, 1, 64, 2, true>(a, stream) : launch_pipe<4, 1, 64, 2, false>(a, stream);
+        case ATTN_CFG_WIDE_W4:
+            return fuse_q ? launch_pipe<4, 2, 32, 4, true>(a, stream) : launch_pipe<4, 2, 32, 4, false>(a, stream);
         case ATTN_CFG_REGSTAGE_W8:
             return fuse_q ? launch_regstage<32, 8, true>(a, stream) : launch_regstage<32, 8, false>(a, stream);
+        case ATTN_CFG_PINGPONG_W8:
+            return fuse_q ? launch_pp<true>(a, stream) : launch_pp<false>(a, stream);
         default:
             return hipErrorInvalidValue;
     }

@@ -26,7 +26,7 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
                    int causal, float scale, int64_t q_rs, int64_t k_rs, int64_t v_rs, int64_t o_rs, int64_t k_hs,
                    int64_t v_hs, int config, hipStream_t stream) {
     if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || nkeys < 1 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
-    if (!scale_ok(scale) || config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_REGSTAGE_W8) return ERR_ARGS;
+    if (!scale_ok(scale) || config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WIDE_W4) return ERR_ARGS;
     if ((int64_t)p0 + W > INT_MAX - 512 || nkeys > INT_MAX - 512 || W > INT_MAX - 512) return ERR_ARGS;
     if (!rows_ok(q, q_rs, H) || !rows_ok(out, o_rs, H)) return ERR_ARGS;
     if (!k || !v || !aligned(k, 16) || !aligned(v, 16) || k_rs % 8 || v_rs % 8 || k_hs % 8 || v_hs % 8) return ERR_ARGS;
@@ -89,7 +89,7 @@ int prepared_impl(const void* q_raw, const void* ws, size_t ws_bytes, const void
     if (rot == 0) rot = lr::D;
     if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
     if (!(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return ERR_ARGS;
-    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_REGSTAGE_W8) return ERR_ARGS;
+    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WIDE_W4) return ERR_ARGS;
     if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return ERR_ARGS;
     if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H) || !rows_ok(v, v_rs, HK)) return ERR_ARGS;
     if (!table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) || (wq && !aligned(wq, 16))) return ERR_ARGS;
@@ -118,7 +118,7 @@ int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, c
     if (rot == 0) rot = lr::D;
     if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
     if (n_pre < 0 || n_pre > Sk || !(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return ERR_ARGS;
-    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_REGSTAGE_W8) return ERR_ARGS;
+    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WIDE_W4) return ERR_ARGS;
     if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return ERR_ARGS;
     if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H) || !rows_ok(k_raw, k_rs, HK) || !rows_ok(v, v_rs, HK))
         return ERR_ARGS;

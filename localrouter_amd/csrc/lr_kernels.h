@@ -48,7 +48,9 @@ enum AttnConfig : int {
     ATTN_CFG_PIPE_W8 = 1,      // pipelined kernel, 8 waves x 32 queries: 256-query blocks, two waves per SIMD
     ATTN_CFG_PIPE_W4 = 2,      // pipelined kernel, 4 waves x 32 queries: 128-query blocks
     ATTN_CFG_REGSTAGE_W8 = 3,  // register-staged kernel, 8 waves x 32 queries
-    ATTN_CFG_LAST = 3,
+    ATTN_CFG_PINGPONG_W8 = 4,  // ping-pong kernel: two wave groups alternating MFMA and VALU clusters
+    ATTN_CFG_WIDE_W4 = 5,      // pipelined kernel, 4 waves x 64 queries: 256-query blocks, one wave per SIMD
+    ATTN_CFG_LAST = 5,
 };
 
 hipError_t launch_attention(const AttnArgs& a, bool fuse_q, int config, hipStream_t stream);

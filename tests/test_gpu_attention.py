@@ -18,7 +18,7 @@ torch = pytest.importorskip("torch")
 
 from localrouter_amd import ops  # noqa: E402
 
-CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8]
+CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4]
 
 
 def _qkv(seed, W, nk, H, HK):
