@@ -12,13 +12,14 @@
 //  * The K rows of each 32-key block are read in an order with bits 2 and 3 of the row index swapped. With that
 //    order, accumulator registers 0-7 / 8-15 of a score block are exactly the B operand (8 consecutive keys per lane
 //    half) of the next MFMA, O^T += V^T P^T: P never leaves registers.
-//  * V^T is staged into LDS by a 4x8 register transpose of coalesced 16-byte loads; both LDS tiles use XOR chunk
-//    swizzles chosen so that every ds_read_b128 (operand fetch) and ds_write (staging) touches each bank once.
 //  * Online softmax in the exp2 domain with scale*log2(e) folded into one FMA; the running max is only raised (and O
 //    rescaled) when a tile's max exceeds it by more than 2^8, so the 64-register O rescale is rare after the first
 //    tiles. Exact: every P and l use the same reference max, which cancels in O / l.
-//  * K/V tiles of 64 keys are double-buffered in LDS; the next tile's global loads are in flight during the current
-//    tile's MFMAs. Workgroups are remapped so that each XCD works on whole heads (its own L2 holds that head's K/V).
+//  * The default kernel (attn_fwd_pipe_kernel) keeps K and V tiles row-major in an LDS ring filled by direct
+//    global->LDS loads and reads V transposed (ds_read_b64_tr_b16); the QK^T MFMAs of the next tile run interleaved
+//    with the softmax VALU work of the current one. Variants: 4-wave blocks (two per CU), 64 queries per wave, a
+//    ping-pong pair of wave groups, and the first register-staged kernel (V^T formed by a register transpose).
+//  * Workgroups are remapped so that each XCD works on whole heads (its own L2 holds that head's K/V).
 //  * FUSEQ: the query block's per-head RMSNorm and RoPE are applied in registers before the first MFMA.
 #include "lr_common.h"
 #include "lr_kernels.h"

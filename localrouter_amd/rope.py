@@ -32,8 +32,9 @@ def axis_omegas(d: int, theta: float = QWEN_THETA) -> np.ndarray:
 
 
 # The 64 Qwen-Image frequencies as the engine loads them (f64 bit patterns, big-endian hex; the values of
-# kernels/qwen_image/rope_omega.json, read by smath.omegas, smath.zig:112-126). They equal theta^(-2j/d) per axis to
-# within one f64 ulp (torch's float64 linspace/pow produced them); frozen so that tables match the engine's bits.
+# kernels/qwen_image/rope_omega.json, read by smath.omegas, smath.zig:112-126). They are torch's float64
+# 1 / 10000 ** linspace(0, (d - 2) / d, d / 2) per axis, within 9 f64 ulp of theta^(-2j/d); frozen so that tables
+# match the engine's bits.
 QWEN_OMEGA_F64_HEX = (
     "3ff0000000000000", "3fd43d136248490f", "3fb999999999999a", "3fa030dc4ea03a72", "3f847ae147ae147b", "3f69e7c6e43390b6",
     "3f50624dd2f1a9fc", "3f34b96be9c2da2c", "3ff0000000000000", "3fe707aa3f9e1202", "3fe093069178d379", "3fd7db4a2009c6e3",

@@ -8,6 +8,7 @@ import struct
 from pathlib import Path
 
 import numpy as np
+import pytest
 
 from localrouter_amd import rope
 
@@ -24,11 +25,17 @@ def test_qwen_omegas_are_the_engine_bits():
     assert np.array_equal(rope.qwen_omegas(), _frozen_omegas())
 
 
-def test_qwen_omegas_closed_form():
-    """theta^(-2j/d) per axis, to within a few f64 ulp of the frozen values (torch's linspace/pow rounded them)."""
-    closed = np.concatenate([rope.axis_omegas(d) for d in (16, 56, 56)])
+def test_qwen_omegas_recipe_and_closed_form():
+    """The fixture's stated recipe (torch float64 1 / 10000 ** linspace(0, (d - 2) / d, d / 2) per axis, as tfimage
+    computes it) reproduces every frozen bit; the closed form theta^(-2j/d) agrees to a few f64 ulp (linspace's
+    two-sided stepping rounds differently from 2j/d)."""
+    torch = pytest.importorskip("torch")
     frozen = _frozen_omegas()
-    assert np.all(np.abs(closed - frozen) <= 4 * np.spacing(frozen))
+    recipe = np.concatenate([(1.0 / 10000.0 ** torch.linspace(0, (d - 2) / d, d // 2, dtype=torch.float64)).numpy()
+                             for d in (16, 56, 56)])
+    assert np.array_equal(recipe.view(np.uint64), frozen.view(np.uint64))
+    closed = np.concatenate([rope.axis_omegas(d) for d in (16, 56, 56)])
+    assert np.all(np.abs(closed - frozen) <= 16 * np.spacing(frozen))
     # a plausible mistake (2j/(d-2) instead of 2j/d, or theta 1e5) is far outside that
     wrong = np.concatenate([1.0 / 10000.0 ** (2 * np.arange(d // 2) / (d - 2)) for d in (16, 56, 56)])
     assert np.abs(wrong - frozen).max() > 1e-3
