@@ -4,8 +4,8 @@
                     [--no-cpu-baseline]
 
 A step is one fused joint-attention call over one synthetic batch: keys RMSNorm + RoPE into the workspace
-(lr_joint_keys_prepare) followed by the attention kernel with the queries normalised and rotated in registers
-(lr_joint_attention_prepared) -- together exactly lr_joint_attention_fused. Inputs are resident in HBM before timing.
+and V packed into transposed 64-key tiles (lr_joint_kv_prepare), followed by the attention kernel with the queries
+normalised and rotated in registers (lr_joint_attention_prepared) -- together exactly lr_joint_attention_fused. Inputs are resident in HBM before timing.
 The default workload is BASELINE's Qwen-Image-style step: B=1, 24 heads x 128, 512 text + 4096 image tokens (64x64
 grid, 2D RoPE on image tokens, text un-rotated), non-causal, QK-RMSNorm eps 1e-6 with weights 1.0, scale f32(1/sqrt(128)).
 
@@ -29,14 +29,12 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "attention TFLOP/s + % bf16 MFMA peak; ms/call at 4096+512 tokens, 24x128"
-# attention kernel each tile configuration launches (queries normalised and rotated in registers: FUSEQ = true)
+# attention kernel each tile configuration launches (FUSEQ: queries normalised and rotated in registers; VT: values
+# read as packed V^T tiles) -- the configurations lr_joint_attention_prepared accepts
 KERNELS = {
-    0: "attn_fwd_pipe_kernel<8, 1, 64, 3, true>",
-    1: "attn_fwd_pipe_kernel<8, 1, 64, 3, true>",
-    2: "attn_fwd_pipe_kernel<4, 1, 64, 2, true>",
-    3: "attn_fwd_regstage_kernel<32, 8, true>",
-    4: "attn_fwd_pp_kernel<true>",
-    5: "attn_fwd_pipe_kernel<4, 2, 32, 4, true>",
+    0: "attn_fwd_pipe_kernel<8, 1, 64, 3, true, true>",
+    1: "attn_fwd_pipe_kernel<8, 1, 64, 3, true, true>",
+    2: "attn_fwd_pipe_kernel<4, 1, 64, 2, true, true>",
 }
 WORKLOADS = {
     # name: (text tokens, grid description, heads)
@@ -109,7 +107,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS))
-    ap.add_argument("--tile-config", type=int, default=0, help="LR_ATTN_CFG_* (0 = library default)")
+    ap.add_argument("--tile-config", type=int, default=0, choices=sorted(KERNELS),
+                    help="LR_ATTN_CFG_* (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -160,13 +159,14 @@ def main():
     eps, scale, rs = 1e-6, ops.SCALE_128, H * 128
 
     def keys():
-        _lib.call("lr_joint_keys_prepare", k.data_ptr(), rs, wk.data_ptr(), ops.TABLE_COSSIN_F32, cos.data_ptr(),
-                  sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, H, 0, ws.data_ptr(), ws_bytes, sh)
+        _lib.call("lr_joint_kv_prepare", k.data_ptr(), rs, v.data_ptr(), rs, wk.data_ptr(), ops.TABLE_COSSIN_F32,
+                  cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, H, 0, ws.data_ptr(), ws_bytes,
+                  sh)
 
     def attn():
-        _lib.call("lr_joint_attention_prepared", q.data_ptr(), ws.data_ptr(), ws_bytes, v.data_ptr(), out.data_ptr(),
-                  wq.data_ptr(), ops.TABLE_COSSIN_F32, cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128,
-                  eps, S, S, H, H, 0, 0, scale, rs, rs, rs, args.tile_config, sh)
+        _lib.call("lr_joint_attention_prepared", q.data_ptr(), ws.data_ptr(), ws_bytes, out.data_ptr(), wq.data_ptr(),
+                  ops.TABLE_COSSIN_F32, cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, S, H, H,
+                  0, 0, scale, rs, rs, args.tile_config, sh)
 
     for _ in range(args.warmup):
         keys()
@@ -195,7 +195,7 @@ def main():
     keys_ms = float(np.mean(t_keys))
     value = flops / (ms_step * 1e-3) / 1e12
     achieved = flops / (attn_ms * 1e-3) / 1e12
-    log(f"[bench] step {ms_step:.4f} ms (keys {keys_ms:.4f} ms, attention {attn_ms:.4f} ms, median attention "
+    log(f"[bench] step {ms_step:.4f} ms (kv prepare {keys_ms:.4f} ms, attention {attn_ms:.4f} ms, median attention "
         f"{float(np.median(t_attn)):.4f} ms); {value:.1f} TFLOP/s step, {achieved:.1f} TFLOP/s attention kernel "
         f"({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); wall {wall:.3f} s")
 
@@ -218,7 +218,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic_from_profile(args.workload),
                      "kernel": KERNELS[args.tile_config], "kernel_ms": round(attn_ms, 5)},
-        "kernels_ms": {"keys_rms_rope": round(keys_ms, 5), "attention": round(attn_ms, 5)},
+        "kernels_ms": {"kv_prepare": round(keys_ms, 5), "attention": round(attn_ms, 5)},
         "flops_per_call": flops,
     }
 

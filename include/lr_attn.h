@@ -35,7 +35,7 @@ extern "C" {
 /* hipStream_t without pulling in the HIP headers: an opaque pointer (NULL = the default stream). */
 typedef struct ihipStream_t* lr_stream_t;
 
-#define LR_ATTN_ABI_VERSION 1
+#define LR_ATTN_ABI_VERSION 2
 #define LR_HEAD_DIM 128
 
 /* RoPE table kinds: how rotation coefficients are stored per token row, per pair p < rot_dim/2. */
@@ -116,12 +116,13 @@ int lr_rms_rope_qk_bf16(void* q, void* k, int64_t seq, int heads, int64_t q_row_
                         const void* q_norm, const void* k_norm, const void* freqs, int64_t freqs_row_stride,
                         int rot_dim, float eps, lr_stream_t stream);
 
-/* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys, bf16 [HK][Sk][128]. */
+/* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys, bf16 [HK][Sk][128], then (at a
+ * 256-byte boundary) V packed as transposed 64-key tiles, bf16 [HK][ceil(Sk/64)][128][64]. */
 size_t lr_joint_attention_workspace_bytes(int Sk, int HK);
 
 /*
- * The fused joint attention: QK-RMSNorm + RoPE + attention in two launches (keys normalised once into the workspace;
- * queries normalised and rotated in registers inside the attention kernel).
+ * The fused joint attention: QK-RMSNorm + RoPE + attention (keys normalised once and values packed into the
+ * workspace; queries normalised and rotated in registers inside the attention kernel).
  *   q_raw [Sq][H][128], k_raw, v [Sk][HK][128], out [Sq][H][128] bf16 rows with the given row strides.
  *   q_norm_w, k_norm_w: fp32 [128], 16-byte aligned, or NULL (ones). eps >= 0.
  *   Query i uses q-table row i; key j >= n_pre uses k-table row j - n_pre; keys j < n_pre are already normalised and
@@ -139,21 +140,24 @@ int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v
                              int n_pre, void* workspace, size_t workspace_bytes, lr_stream_t stream);
 
 /*
- * The two stages of lr_joint_attention_fused as separate calls (same kernels, same results):
- *   lr_joint_keys_prepare      keys: RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre), rows j < n_pre
- *                              copied, into workspace as bf16 [HK][Sk][128];
- *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated in registers) over those keys and v.
- * Useful when the keys are reused (a cached prefix) or to time the stages separately.
+ * The two stages of lr_joint_attention_fused as separate calls (same kernels, same results as the default
+ * configuration):
+ *   lr_joint_kv_prepare         RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre), rows j < n_pre
+ *                               copied, into the workspace's keys; v [Sk][HK][128] packed into its V^T tiles;
+ *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated in registers) over that workspace.
+ *                               config: LR_ATTN_CFG_AUTO, _PIPE_W8 or _PIPE_W4 (the configurations that read V^T
+ *                               tiles; the others are reached through lr_joint_attention_fused_ex).
+ * Useful when keys and values are reused (a cached prefix) or to time the stages separately.
  */
-int lr_joint_keys_prepare(const void* k_raw, int64_t k_row_stride, const float* k_norm_w, int table_kind,
-                          const void* k_table_a, const void* k_table_b, int64_t table_row_stride, int pairing,
-                          int rot_dim, float eps, int Sk, int HK, int n_pre, void* workspace, size_t workspace_bytes,
-                          lr_stream_t stream);
-int lr_joint_attention_prepared(const void* q_raw, const void* workspace, size_t workspace_bytes, const void* v,
-                                void* out, const float* q_norm_w, int table_kind, const void* q_table_a,
-                                const void* q_table_b, int64_t table_row_stride, int pairing, int rot_dim, float eps,
-                                int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_row_stride,
-                                int64_t v_row_stride, int64_t out_row_stride, int config, lr_stream_t stream);
+int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                        const float* k_norm_w, int table_kind, const void* k_table_a, const void* k_table_b,
+                        int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sk, int HK, int n_pre,
+                        void* workspace, size_t workspace_bytes, lr_stream_t stream);
+int lr_joint_attention_prepared(const void* q_raw, const void* workspace, size_t workspace_bytes, void* out,
+                                const float* q_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
+                                int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sq, int Sk, int H,
+                                int HK, int p0, int causal, float scale, int64_t q_row_stride, int64_t out_row_stride,
+                                int config, lr_stream_t stream);
 
 /* lr_joint_attention_fused with an explicit tile configuration (LR_ATTN_CFG_*). */
 int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,

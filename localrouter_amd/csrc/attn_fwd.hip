@@ -441,9 +441,13 @@ __device__ __forceinline__ void block_barrier() {
 // NW waves of NQB x 32 queries each; tiles of BT keys in an NS-stage K/V ring. NQB = 2 reads every K and V operand
 // fragment from LDS once for two 32-query MFMAs, halving LDS traffic per MFMA, at one wave per SIMD (its registers
 // need it); BT = 32 then keeps the two score buffers at 32 registers each.
-template <int NW, int NQB, int BT, int NS, bool FUSEQ>
-__global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1) void attn_fwd_pipe_kernel(AttnArgs a) {
+// VT: values arrive packed as V^T tiles ([128 dims][64 keys], 16 KB contiguous per tile, zero past nkeys), stored in
+// LDS with 16-byte chunk c of dim row d at c ^ ((d >> 1) & 7), and the PV A operand is one ds_read_b128 per MFMA.
+template <int NW, int NQB, int BT, int NS, bool FUSEQ, bool VT>
+__global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1)
+__attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void attn_fwd_pipe_kernel(AttnArgs a) {
     static_assert(NS >= 2 && NS <= 4, "2- to 4-stage ring");
+    static_assert(!VT || (BT == 64 && NQB == 1), "packed V^T tiles are 64 keys wide");
     static_assert(NQB == 1 || NQB == 2, "one or two 32-query blocks per wave");
     static_assert(BT == 32 || BT == 64, "32- or 64-key tiles");
     constexpr int BM = 32 * NQB * NW;
@@ -486,13 +490,20 @@ __global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1) void attn_fwd_pipe_
     const uint32_t kr_lds = lds_addr(Kr), vr_lds = lds_addr(Vr);
     // Source pointers of the next K and V tiles to load, advanced one tile per issue; a tile reaching past nkeys
     // takes the clamped path instead.
-    const int64_t kstep = (int64_t)BT * a.k_rs, vstep = (int64_t)BT * a.v_rs;
+    const int64_t kstep = (int64_t)BT * a.k_rs, vstep = VT ? (int64_t)TILE : (int64_t)BT * a.v_rs;
     const uint16_t* kp[LOADS];
     const uint16_t* vp[LOADS];
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
         kp[j] = kbase + (int64_t)krow[j] * a.k_rs + kcol[j];
-        vp[j] = vbase + (int64_t)krow[j] * a.v_rs + vcol;
+        if constexpr (VT) {
+            // instruction j fills V^T dim rows 8i .. 8i+7 (i = wave + NW j): lane -> row 8i + (lane >> 3), LDS chunk
+            // lane & 7, which holds logical chunk (lane & 7) ^ ((row >> 1) & 7)
+            const int d = 8 * (wave + NW * j) + (lane >> 3);
+            vp[j] = vbase + d * BT + 8 * ((lane & 7) ^ ((d >> 1) & 7));
+        } else {
+            vp[j] = vbase + (int64_t)krow[j] * a.v_rs + vcol;
+        }
     }
     auto issue_k = [&](int t, int slot) {
         const int key0 = t * BT;
@@ -513,7 +524,7 @@ __global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1) void attn_fwd_pipe_
     auto issue_v = [&](int t, int slot) {
         const int key0 = t * BT;
         const uint32_t dst = vr_lds + 2 * (slot * TILE + wave * 512);
-        if (key0 + BT <= a.nkeys) {
+        if (VT || key0 + BT <= a.nkeys) {   // packed V^T tiles are whole (zero past nkeys)
 #pragma unroll
             for (int j = 0; j < LOADS; ++j) dma16(vp[j], dst + 2 * NW * 512 * j);
         } else {
@@ -552,6 +563,10 @@ __global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1) void attn_fwd_pipe_
         const int chunk = 4 * (db ^ (sl >> 2)) + 2 * (g & 1) + ((sl & 3) >> 1);
         vtr[db] = (8 * (g >> 1) + (sl >> 2)) * D + 8 * chunk + 4 * (sl & 1);
     }
+    // packed V^T operand: lane reads dim row 32db + n, keys 16kk + 8hf .. +8 (logical chunk 2kk + hf)
+    int vto[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) vto[kk] = n * BT + 8 * ((2 * kk + hf) ^ ((n >> 1) & 7));
 
     // one K operand fragment, used by every query block
     auto qk_block = [&](const uint16_t* kt, int ks, int mb, f32x16 (&acc)[NQB][MB]) {
@@ -665,6 +680,80 @@ __global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1) void attn_fwd_pipe_
         } else if (t + NS - 1 < ntiles) {
             issue_v(t + NS - 1, (t + NS - 1) % NS);
         }
+        if constexpr (NQB == 1 && BT == 64) {
+            // Explicit schedule of the tile's 32 MFMA slots (one wave's instruction stream; a sched_barrier closes
+            // every slot, so the compiler keeps each slot's work in it):
+            //   slots 0-15   S(t+1) = K(t+1) Q^T, the two 32-key accumulator chains alternating;
+            //   slots 16-31  O += V(t)^T P(t), 16-key step kk = (s - 16) / 4, the four 32-dim chains alternating;
+            //   LDS operand fragments read 3 slots ahead into a 4-entry ring (K fragments, then V fragments);
+            //   exp2 pair k of P(t) (k = 4 kk + j) in slot floor(3k / 2): VALU work spread over slots 0-22, and P
+            //   for step kk complete before its first PV slot;
+            //   the max of S(t+1) in slots 24-31, long after its MFMAs retired.
+            const uint16_t* kt = Kr + ((t + 1) % NS) * TILE;
+            const uint16_t* vt = Vr + (t % NS) * TILE;
+            auto frag = [&](int f) -> bf16x8 {
+                if (f < 16) {
+                    const int ks = f >> 1, mb = f & 1;
+                    return *reinterpret_cast<const bf16x8*>(kt + kfrag[mb] + 8 * ((2 * ks + hf) ^ kswz));
+                }
+                const int i = f - 16, kk = i >> 2, db = i & 3;
+                if constexpr (VT) {
+                    return *reinterpret_cast<const bf16x8*>(vt + vto[kk] + 32 * BT * db);
+                } else {
+                    const uint16_t* p0 = vt + vtr[db] + (16 * kk) * D;
+                    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+                    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 4 * D));
+                    return __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi), 0,
+                                                   1, 2, 3, 4, 5, 6, 7);
+                }
+            };
+            bf16x8 fr[4];
+            fr[0] = frag(0);
+            fr[1] = frag(1);
+            fr[2] = frag(2);
+            const float nm = -m_used[0];
+            float ls = l_sum[0];
+            float mloc = -INFINITY;
+            // packed bf16 pairs of P(t), scalars (hipcc 7.2 folds __builtin_bit_cast(bf16x2, w[j]) of a vector
+            // element to w[0] for every j)
+            uint32_t pw[16];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 32; ++s) {
+                if (s + 3 < 32) fr[(s + 3) & 3] = frag(s + 3);
+                if (s < 16) {
+                    sn[0][s & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[s & 3], qf[0][s >> 1],
+                                                                          s < 2 ? f32x16{} : sn[0][s & 1], 0, 0, 0);
+                } else {
+                    const int kk = (s - 16) >> 2, db = (s - 16) & 3;
+                    const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pw[4 * kk], pw[4 * kk + 1], pw[4 * kk + 2],
+                                                                       pw[4 * kk + 3]});
+                    o[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[s & 3], pb, o[0][db], 0, 0, 0);
+                }
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    if ((3 * k) / 2 != s) continue;
+                    const int kk = k >> 2, j = k & 3, r = 8 * (kk & 1) + 2 * j;
+                    pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sc[0][kk >> 1][r], c, nm)),
+                                        __builtin_amdgcn_exp2f(fmaf(sc[0][kk >> 1][r + 1], c, nm)));
+                    // the row sum of the bf16 P exactly as the PV MFMA consumes it
+                    ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[k]), ones2, ls, false);
+                }
+                if (s >= 24) {
+                    const int g = 4 * (s - 24);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) mloc = fmaxf(mloc, sn[0][(g + u) >> 4][(g + u) & 15]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            l_sum[0] = ls;
+            mx[0] = wave_pair_max(mloc) * c;
+            if (t + 1 < ntiles && !needs_mask(t + 1)) rescale_for(mx);
+            if (NS == 2 || !refilled) LR_WAIT_VMCNT(0);
+            else LR_WAIT_VMCNT(2 * LOADS);
+            block_barrier();
+            return;
+        }
         bf16x8 pf[NQB][KK];
         auto exps = [&]() {
 #pragma unroll
@@ -722,11 +811,16 @@ __global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1) void attn_fwd_pipe_
         for (int kk = 0; kk < KK; ++kk) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const uint16_t* p0 = vt + vtr[db] + (16 * kk) * D;
-                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
-                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 4 * D));
-                const bf16x8 vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi),
-                                                          0, 1, 2, 3, 4, 5, 6, 7);
+                bf16x8 vf;
+                if constexpr (VT) {
+                    vf = *reinterpret_cast<const bf16x8*>(vt + vto[kk] + 32 * BT * db);
+                } else {
+                    const uint16_t* p0 = vt + vtr[db] + (16 * kk) * D;
+                    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+                    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 4 * D));
+                    vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi), 0, 1,
+                                                 2, 3, 4, 5, 6, 7);
+                }
 #pragma unroll
                 for (int nb = 0; nb < NQB; ++nb)
                     o[nb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[nb][kk], o[nb][db], 0, 0, 0);
@@ -1053,13 +1147,13 @@ hipError_t launch_regstage(const AttnArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int NW, int NQB, int BT, int NS, bool FUSEQ>
+template <int NW, int NQB, int BT, int NS, bool FUSEQ, bool VT = false>
 hipError_t launch_pipe(const AttnArgs& a, hipStream_t stream) {
     constexpr int BM = 32 * NQB * NW;
     const int64_t nqb = (a.W + BM - 1) / BM;
     const int64_t blocks = nqb * a.H;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, NQB, BT, NS, FUSEQ>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, NQB, BT, NS, FUSEQ, VT>), dim3((unsigned)blocks), dim3(NW * 64), 0,
                        stream, a);
     return hipGetLastError();
 }
@@ -1073,8 +1167,20 @@ int attention_block_rows(int config) {
     }
 }
 
-hipError_t launch_attention(const AttnArgs& a, bool fuse_q, int config, hipStream_t stream) {
+bool attention_config_reads_vt(int config) {
+    return config == ATTN_CFG_AUTO || config == ATTN_CFG_PIPE_W8 || config == ATTN_CFG_PIPE_W4;
+}
+
+hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config, hipStream_t stream) {
     if (config == ATTN_CFG_AUTO) config = ATTN_CFG_PIPE_W8;
+    if (v_t) {
+        if (!fuse_q) return hipErrorInvalidValue;
+        switch (config) {
+            case ATTN_CFG_PIPE_W8: return launch_pipe<8, 1, 64, 3, true, true>(a, stream);
+            case ATTN_CFG_PIPE_W4: return launch_pipe<4, 1, 64, 2, true, true>(a, stream);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (config) {
         case ATTN_CFG_PIPE_W8:
             return fuse_q ? launch_pipe<8, 1, 64, 3, true>(a, stream) : launch_pipe<8, 1, 64, 3, false>(a, stream);

@@ -41,7 +41,7 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
     a.W = W; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = nkeys; a.p0 = p0; a.causal = causal;
     a.c = scale * 1.4426950408889634f;
     a.table_kind = lr::TABLE_NONE;
-    return (int)lr::launch_attention(a, false, config, stream);
+    return (int)lr::launch_attention(a, false, false, config, stream);
 }
 
 // Table checks shared by the rope entry points. rows_needed: table rows that will be read.
@@ -58,17 +58,25 @@ bool table_ok(int kind, const void* ta, const void* tb, int64_t stride, int rot,
     return aligned(ta, 16) && stride % 4 == 0 && stride >= 4 * pairs;  // LR_TABLE_MAT2_F32
 }
 
-// Shared checks of the fused op's two stages.
-int keys_impl(const void* k_raw, int64_t k_rs, const float* wk, int table_kind, const void* kta, const void* ktb,
-              int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK, int n_pre, void* ws,
-              size_t ws_bytes, hipStream_t stream) {
+// Workspace of the fused op: the prepared keys bf16 [HK][Sk][128], then (256-byte aligned) the packed V^T tiles
+// bf16 [HK][ceil(Sk/64)][128][64].
+size_t ws_keys_bytes(int Sk, int HK) { return ((size_t)Sk * (size_t)HK * lr::D * 2 + 255) & ~(size_t)255; }
+int vt_tiles(int Sk) { return (Sk + lr::VT_TILE_KEYS - 1) / lr::VT_TILE_KEYS; }
+size_t ws_bytes_needed(int Sk, int HK) {
+    return ws_keys_bytes(Sk, HK) + (size_t)HK * (size_t)vt_tiles(Sk) * lr::D * lr::VT_TILE_KEYS * 2;
+}
+
+// The keys stage: RMSNorm + RoPE of k_raw rows j >= n_pre (rows j < n_pre copied) into the workspace's keys, and,
+// when v is given, V packed into the workspace's V^T tiles.
+int kv_impl(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
+            const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK,
+            int n_pre, void* ws, size_t ws_bytes, hipStream_t stream) {
     if (rot == 0) rot = lr::D;
     if (Sk < 1 || HK < 1 || Sk > INT_MAX - 512 || n_pre < 0 || n_pre > Sk || !(eps >= 0.0f) || !isfinite(eps))
         return ERR_ARGS;
-    if (!rows_ok(k_raw, k_rs, HK) || (wk && !aligned(wk, 16))) return ERR_ARGS;
+    if (!rows_ok(k_raw, k_rs, HK) || (v && !rows_ok(v, v_rs, HK)) || (wk && !aligned(wk, 16))) return ERR_ARGS;
     if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
-    const size_t need = lr_joint_attention_workspace_bytes(Sk, HK);
-    if (!ws || !aligned(ws, 256) || ws_bytes < need) return ERR_ARGS;
+    if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return ERR_ARGS;
     lr::RopeArgs r{};
     r.src = static_cast<const uint16_t*>(k_raw);
     r.dst = static_cast<uint16_t*>(ws);
@@ -79,34 +87,56 @@ int keys_impl(const void* k_raw, int64_t k_rs, const float* wk, int table_kind, 
     r.table_kind = Sk > n_pre ? table_kind : lr::TABLE_NONE; r.pairing = pairing; r.rot = rot;
     r.ta = kta; r.tb = ktb; r.tab_stride = tab_stride;
     r.eps = eps; r.round_norm = 0;
+    if (v) {   // packed by extra blocks of the same launch
+        r.vp.v = static_cast<const uint16_t*>(v);
+        r.vp.vt = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + ws_keys_bytes(Sk, HK));
+        r.vp.v_rs = v_rs; r.vp.Sk = Sk; r.vp.HK = HK; r.vp.ntiles = vt_tiles(Sk);
+    }
     return (int)lr::launch_rms_rope(r, stream);
 }
 
-int prepared_impl(const void* q_raw, const void* ws, size_t ws_bytes, const void* v, void* out, const float* wq,
-                  int table_kind, const void* qta, const void* qtb, int64_t tab_stride, int pairing, int rot, float eps,
-                  int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_rs, int64_t v_rs,
+// Checks shared by the attention stage's entry points.
+bool attn_stage_ok(const void* q_raw, const void* out, const float* wq, int table_kind, const void* qta,
+                   const void* qtb, int64_t tab_stride, int pairing, int rot, float eps, int Sq, int Sk, int H, int HK,
+                   int p0, int causal, float scale, int64_t q_rs, int64_t o_rs, int config) {
+    if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return false;
+    if (!(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return false;
+    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WIDE_W4) return false;
+    if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return false;
+    if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H)) return false;
+    return table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) && (!wq || aligned(wq, 16));
+}
+
+// The attention stage over prepared keys: values from the workspace's V^T tiles when v is null, else from v rows.
+int prepared_impl(const void* q_raw, const void* ws, size_t ws_bytes, const void* v, int64_t v_rs, void* out,
+                  const float* wq, int table_kind, const void* qta, const void* qtb, int64_t tab_stride, int pairing,
+                  int rot, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_rs,
                   int64_t o_rs, int config, hipStream_t stream) {
     if (rot == 0) rot = lr::D;
-    if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
-    if (!(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return ERR_ARGS;
-    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WIDE_W4) return ERR_ARGS;
-    if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return ERR_ARGS;
-    if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H) || !rows_ok(v, v_rs, HK)) return ERR_ARGS;
-    if (!table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) || (wq && !aligned(wq, 16))) return ERR_ARGS;
-    if (!ws || !aligned(ws, 256) || ws_bytes < lr_joint_attention_workspace_bytes(Sk, HK)) return ERR_ARGS;
+    if (!attn_stage_ok(q_raw, out, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, Sk, H, HK, p0, causal,
+                       scale, q_rs, o_rs, config))
+        return ERR_ARGS;
+    if (v ? !rows_ok(v, v_rs, HK) : !lr::attention_config_reads_vt(config)) return ERR_ARGS;
+    if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return ERR_ARGS;
     lr::AttnArgs a{};
     a.q = static_cast<const uint16_t*>(q_raw);
     a.k = static_cast<const uint16_t*>(ws);
-    a.v = static_cast<const uint16_t*>(v);
     a.out = static_cast<uint16_t*>(out);
-    a.q_rs = q_rs; a.k_rs = lr::D; a.v_rs = v_rs; a.o_rs = o_rs;
-    a.k_hs = (int64_t)Sk * lr::D; a.v_hs = lr::D;
+    a.q_rs = q_rs; a.k_rs = lr::D; a.o_rs = o_rs;
+    a.k_hs = (int64_t)Sk * lr::D;
+    if (v) {
+        a.v = static_cast<const uint16_t*>(v);
+        a.v_rs = v_rs; a.v_hs = lr::D;
+    } else {
+        a.v = reinterpret_cast<const uint16_t*>(static_cast<const char*>(ws) + ws_keys_bytes(Sk, HK));
+        a.v_rs = 0; a.v_hs = (int64_t)vt_tiles(Sk) * lr::D * lr::VT_TILE_KEYS;
+    }
     a.W = Sq; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = Sk; a.p0 = p0; a.causal = causal;
     a.c = scale * 1.4426950408889634f;
     a.wq = wq;
     a.table_kind = table_kind; a.pairing = pairing; a.rot = rot;
     a.qta = qta; a.qtb = qtb; a.tab_stride = tab_stride; a.eps = eps;
-    return (int)lr::launch_attention(a, true, config, stream);
+    return (int)lr::launch_attention(a, true, v == nullptr, config, stream);
 }
 
 int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, const float* wq, const float* wk,
@@ -116,21 +146,20 @@ int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, c
                int config, hipStream_t stream) {
     // validate both stages before launching either
     if (rot == 0) rot = lr::D;
-    if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
-    if (n_pre < 0 || n_pre > Sk || !(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return ERR_ARGS;
-    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WIDE_W4) return ERR_ARGS;
-    if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return ERR_ARGS;
-    if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H) || !rows_ok(k_raw, k_rs, HK) || !rows_ok(v, v_rs, HK))
+    if (!attn_stage_ok(q_raw, out, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, Sk, H, HK, p0, causal,
+                       scale, q_rs, o_rs, config))
         return ERR_ARGS;
-    if (!table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
+    if (n_pre < 0 || n_pre > Sk || !rows_ok(k_raw, k_rs, HK) || !rows_ok(v, v_rs, HK)) return ERR_ARGS;
     if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
-    if ((wq && !aligned(wq, 16)) || (wk && !aligned(wk, 16))) return ERR_ARGS;
-    if (!ws || !aligned(ws, 256) || ws_bytes < lr_joint_attention_workspace_bytes(Sk, HK)) return ERR_ARGS;
-    const int e = keys_impl(k_raw, k_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws,
-                            ws_bytes, stream);
+    if (wk && !aligned(wk, 16)) return ERR_ARGS;
+    if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return ERR_ARGS;
+    // the 64-key pipelined configurations read packed V^T tiles; the others read the v rows directly
+    const bool vt = lr::attention_config_reads_vt(config);
+    const int e = kv_impl(k_raw, k_rs, vt ? v : nullptr, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps,
+                          Sk, HK, n_pre, ws, ws_bytes, stream);
     if (e != 0) return e;
-    return prepared_impl(q_raw, ws, ws_bytes, v, out, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, Sk,
-                         H, HK, p0, causal, scale, q_rs, v_rs, o_rs, config, stream);
+    return prepared_impl(q_raw, ws, ws_bytes, vt ? nullptr : v, v_rs, out, wq, table_kind, qta, qtb, tab_stride,
+                         pairing, rot, eps, Sq, Sk, H, HK, p0, causal, scale, q_rs, o_rs, config, stream);
 }
 
 int rope_impl(const void* src, int64_t src_rs, int64_t src_off, void* dst, int64_t dst_rs, int64_t n, int b,
@@ -216,8 +245,7 @@ int lr_rms_rope_qk_bf16(void* q, void* k, int64_t seq, int heads, int64_t q_row_
 
 size_t lr_joint_attention_workspace_bytes(int Sk, int HK) {
     if (Sk < 1 || HK < 1) return 0;
-    const size_t bytes = (size_t)Sk * (size_t)HK * lr::D * 2;
-    return (bytes + 255) & ~(size_t)255;
+    return ws_bytes_needed(Sk, HK);
 }
 
 int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,
@@ -232,22 +260,23 @@ int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v
                       stream);
 }
 
-int lr_joint_keys_prepare(const void* k_raw, int64_t k_row_stride, const float* k_norm_w, int table_kind,
-                          const void* k_table_a, const void* k_table_b, int64_t table_row_stride, int pairing,
-                          int rot_dim, float eps, int Sk, int HK, int n_pre, void* workspace, size_t workspace_bytes,
-                          lr_stream_t stream) {
-    return keys_impl(k_raw, k_row_stride, k_norm_w, table_kind, k_table_a, k_table_b, table_row_stride, pairing,
-                     rot_dim, eps, Sk, HK, n_pre, workspace, workspace_bytes, stream);
+int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                        const float* k_norm_w, int table_kind, const void* k_table_a, const void* k_table_b,
+                        int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sk, int HK, int n_pre,
+                        void* workspace, size_t workspace_bytes, lr_stream_t stream) {
+    if (!v) return ERR_ARGS;
+    return kv_impl(k_raw, k_row_stride, v, v_row_stride, k_norm_w, table_kind, k_table_a, k_table_b, table_row_stride,
+                   pairing, rot_dim, eps, Sk, HK, n_pre, workspace, workspace_bytes, stream);
 }
 
-int lr_joint_attention_prepared(const void* q_raw, const void* workspace, size_t workspace_bytes, const void* v,
-                                void* out, const float* q_norm_w, int table_kind, const void* q_table_a,
-                                const void* q_table_b, int64_t table_row_stride, int pairing, int rot_dim, float eps,
-                                int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_row_stride,
-                                int64_t v_row_stride, int64_t out_row_stride, int config, lr_stream_t stream) {
-    return prepared_impl(q_raw, workspace, workspace_bytes, v, out, q_norm_w, table_kind, q_table_a, q_table_b,
-                         table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale, q_row_stride,
-                         v_row_stride, out_row_stride, config, stream);
+int lr_joint_attention_prepared(const void* q_raw, const void* workspace, size_t workspace_bytes, void* out,
+                                const float* q_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
+                                int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sq, int Sk, int H,
+                                int HK, int p0, int causal, float scale, int64_t q_row_stride, int64_t out_row_stride,
+                                int config, lr_stream_t stream) {
+    return prepared_impl(q_raw, workspace, workspace_bytes, nullptr, 0, out, q_norm_w, table_kind, q_table_a,
+                         q_table_b, table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale,
+                         q_row_stride, out_row_stride, config, stream);
 }
 
 int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,

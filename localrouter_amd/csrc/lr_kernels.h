@@ -24,7 +24,17 @@ struct AttnArgs {
     float eps;
 };
 
-// The per-(row, head) RMSNorm + RoPE pass.
+// V^T packing of the prepared-keys path: bf16 V rows (key j of kv head g at v + j*v_rs + g*128) into
+// [HK][ntiles][128][64], one contiguous 16 KB block of 128 dim rows x 64 keys per 64-key tile, keys past Sk zero.
+struct VPackArgs {
+    const uint16_t* v;   // null: nothing to pack
+    uint16_t* vt;
+    int64_t v_rs;
+    int Sk, HK, ntiles;
+};
+constexpr int VT_TILE_KEYS = 64;
+
+// The per-(row, head) RMSNorm + RoPE pass; the same launch also packs vp when vp.v is set (extra blocks).
 struct RopeArgs {
     const uint16_t* src;  // bf16, row r head h at src + r*src_rs + h*src_hs
     uint16_t* dst;        // bf16, row r head h at dst + r*dst_rs + h*dst_hs (may equal src: in place)
@@ -40,6 +50,7 @@ struct RopeArgs {
     int64_t tab_stride;
     float eps;
     int round_norm;       // 1: round the normalised value to bf16 before the rotation
+    VPackArgs vp;
 };
 
 // Attention tile configurations (queries per wave x waves per workgroup).
@@ -53,7 +64,10 @@ enum AttnConfig : int {
     ATTN_CFG_LAST = 5,
 };
 
-hipError_t launch_attention(const AttnArgs& a, bool fuse_q, int config, hipStream_t stream);
+// v_t: values come as packed V^T tiles (VPackArgs layout; a.v = the [HK][ntiles] tile array, a.v_hs = ntiles*8192)
+// instead of rows; only the pipelined 64-key-tile configurations (AUTO, PIPE_W8, PIPE_W4) read that layout.
+hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config, hipStream_t stream);
+bool attention_config_reads_vt(int config);
 hipError_t launch_rms_rope(const RopeArgs& a, hipStream_t stream);
 int attention_block_rows(int config);
 

@@ -4,6 +4,7 @@
   rms_rope(...)         <- Triton.ropeRun + Rope, src/engines/qwen_image/triton_k.zig:44-53
   rms_rope_qk(...)      <- Kitchen.rmsRope, src/engines/minimax_h3/launch.zig:421-441
   joint_attention(...)  <- Dit.block's rope_q / rope_k / V copy / attention chain, src/engines/qwen_image/dit.zig:252-293
+  joint_kv_prepare(...), joint_attention_prepared(...)  <- its two stages (keys / values reused across calls)
 
 Every call validates shapes on the host, then goes through the C ABI (liblr_attn.so) on torch's current HIP stream.
 torch supplies device memory and the stream handle only; all compute is the library's HIP kernels.
@@ -148,4 +149,58 @@ def joint_attention(q_raw: torch.Tensor, k_raw: torch.Tensor, v: torch.Tensor, o
               _ptr(k_norm), table_kind, _ptr(qa), _ptr(qb), _ptr(ka), _ptr(kb), stride, pairing, rot, eps, Sq, Sk, H,
               HK, p0, int(causal), scale, q_rs, k_rs, v_rs, o_rs, n_pre, _ptr(workspace),
               workspace.numel() * workspace.element_size(), config, _stream())
+    return out
+
+
+def joint_kv_prepare(k_raw: torch.Tensor, v: torch.Tensor, workspace: torch.Tensor, *,
+                     k_norm: torch.Tensor | None = None, table_kind: int = TABLE_COSSIN_F32,
+                     k_table: tuple | None = None, pairing: int = PAIR_INTERLEAVED, rot: int = 128, eps: float = 1e-6,
+                     n_pre: int = 0) -> torch.Tensor:
+    """First stage of joint_attention: k_raw [Sk, HK, 128] normalised and rotated (rows < n_pre copied) and v packed
+    into the workspace (lr_joint_kv_prepare). Returns the workspace."""
+    Sk, HK = k_raw.shape[0], k_raw.shape[1]
+    k_rs, v_rs = _rows(k_raw, "k_raw", HK), _rows(v, "v", HK)
+    if v.shape[0] < Sk:
+        raise ValueError("v shorter than k")
+    if k_norm is not None and (k_norm.dtype != torch.float32 or not k_norm.is_contiguous() or k_norm.numel() != D):
+        raise ValueError("k_norm: expected fp32 [128]")
+    ka = kb = None
+    stride = 0
+    if table_kind != TABLE_NONE:
+        if k_table is None:
+            raise ValueError("joint_kv_prepare: k_table required")
+        ka, kb = k_table
+        stride = ka.stride(0)
+    nbytes = workspace.numel() * workspace.element_size()
+    if nbytes < workspace_bytes(Sk, HK):
+        raise ValueError(f"workspace: {workspace_bytes(Sk, HK)} bytes needed")
+    _lib.call("lr_joint_kv_prepare", _ptr(k_raw), k_rs, _ptr(v), v_rs, _ptr(k_norm), table_kind, _ptr(ka), _ptr(kb),
+              stride, pairing, rot, eps, Sk, HK, n_pre, _ptr(workspace), nbytes, _stream())
+    return workspace
+
+
+def joint_attention_prepared(q_raw: torch.Tensor, workspace: torch.Tensor, sk: int, kv_heads: int,
+                             out: torch.Tensor | None = None, *, q_norm: torch.Tensor | None = None,
+                             table_kind: int = TABLE_COSSIN_F32, q_table: tuple | None = None,
+                             pairing: int = PAIR_INTERLEAVED, rot: int = 128, eps: float = 1e-6, causal: bool = False,
+                             p0: int = 0, scale: float = SCALE_128, config: int = CFG_AUTO) -> torch.Tensor:
+    """Second stage of joint_attention: q_raw [Sq, H, 128] over a workspace filled by joint_kv_prepare
+    (lr_joint_attention_prepared)."""
+    Sq, H = q_raw.shape[0], q_raw.shape[1]
+    q_rs = _rows(q_raw, "q_raw", H)
+    if out is None:
+        out = torch.empty((Sq, H, D), dtype=torch.bfloat16, device=q_raw.device)
+    o_rs = _rows(out, "out", H)
+    if q_norm is not None and (q_norm.dtype != torch.float32 or not q_norm.is_contiguous() or q_norm.numel() != D):
+        raise ValueError("q_norm: expected fp32 [128]")
+    qa = qb = None
+    stride = 0
+    if table_kind != TABLE_NONE:
+        if q_table is None:
+            raise ValueError("joint_attention_prepared: q_table required")
+        qa, qb = q_table
+        stride = qa.stride(0)
+    _lib.call("lr_joint_attention_prepared", _ptr(q_raw), _ptr(workspace), workspace.numel() * workspace.element_size(),
+              _ptr(out), _ptr(q_norm), table_kind, _ptr(qa), _ptr(qb), stride, pairing, rot, eps, Sq, sk, H, kv_heads,
+              p0, int(causal), scale, q_rs, o_rs, config, _stream())
     return out

@@ -28,13 +28,17 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().lr_attn_abi_version() == 1
+    header = _lib.HEADER.read_text()
+    declared = int(re.search(r"#define LR_ATTN_ABI_VERSION (\d+)", header).group(1))
+    assert _lib.load().lr_attn_abi_version() == declared == 2
 
 
 def test_workspace_bytes():
     L = _lib.load()
-    assert L.lr_joint_attention_workspace_bytes(4608, 24) == 4608 * 24 * 128 * 2
-    assert L.lr_joint_attention_workspace_bytes(3, 1) == 768
+    # prepared keys [HK][Sk][128] rounded up to 256 bytes, then V^T tiles [HK][ceil(Sk/64)][128][64], all bf16
+    assert L.lr_joint_attention_workspace_bytes(4608, 24) == 4608 * 24 * 128 * 2 + 24 * 72 * 128 * 64 * 2
+    assert L.lr_joint_attention_workspace_bytes(3, 1) == 768 + 128 * 64 * 2
+    assert L.lr_joint_attention_workspace_bytes(65, 2) == 65 * 2 * 256 + 2 * 2 * 128 * 64 * 2
     assert L.lr_joint_attention_workspace_bytes(0, 24) == 0
 
 
@@ -68,7 +72,7 @@ def test_attention_ex_rejects_bad_config():
 def _fused(**kw):
     a = dict(q=A, k=A, v=A, out=A, wq=None, wk=None, kind=1, qa=A, qb=A, ka=A, kb=A, ts=64, pairing=0, rot=128,
              eps=1e-6, Sq=8, Sk=8, H=2, HK=2, p0=0, causal=0, scale=0.088, qrs=256, krs=256, vrs=256, ors=256, n_pre=0,
-             ws=A, wsb=8 * 2 * 256, stream=None)
+             ws=A, wsb=8 * 2 * 256 + 2 * 128 * 64 * 2, stream=None)
     a.update(kw)
     return _lib.load().lr_joint_attention_fused(*a.values())
 
@@ -77,6 +81,7 @@ def _fused(**kw):
     (dict(ws=0), "no workspace"),
     (dict(ws=A + 16), "workspace not 256-aligned"),
     (dict(wsb=100), "workspace too small"),
+    (dict(wsb=8 * 2 * 256), "workspace holds the keys but not the V^T tiles"),
     (dict(kind=7), "table kind"),
     (dict(pairing=1, rot=48), "split-half rot not a multiple of 32"),
     (dict(rot=130), "rot > 128"),
@@ -89,6 +94,33 @@ def _fused(**kw):
 ])
 def test_fused_rejects(kw, why):
     assert _fused(**kw) == HIP_ERROR_INVALID_VALUE, why
+
+
+def test_stage_entry_points_reject():
+    L = _lib.load()
+    wsb = L.lr_joint_attention_workspace_bytes(8, 2)
+    kv = dict(k=A, krs=256, v=A, vrs=256, wk=None, kind=1, ka=A, kb=A, ts=64, pairing=0, rot=128, eps=1e-6, Sk=8, HK=2,
+              n_pre=0, ws=A, wsb=wsb, stream=None)
+
+    def kv_call(**kw):
+        a = dict(kv)
+        a.update(kw)
+        return L.lr_joint_kv_prepare(*a.values())
+
+    assert kv_call(v=0) == HIP_ERROR_INVALID_VALUE              # the values are part of the prepared workspace
+    assert kv_call(wsb=wsb - 2) == HIP_ERROR_INVALID_VALUE
+    assert kv_call(vrs=200) == HIP_ERROR_INVALID_VALUE
+    pr = dict(q=A, ws=A, wsb=wsb, out=A, wq=None, kind=1, qa=A, qb=A, ts=64, pairing=0, rot=128, eps=1e-6, Sq=8, Sk=8,
+              H=2, HK=2, p0=0, causal=0, scale=0.088, qrs=256, ors=256, config=0, stream=None)
+
+    def pr_call(**kw):
+        a = dict(pr)
+        a.update(kw)
+        return L.lr_joint_attention_prepared(*a.values())
+
+    for cfg in (3, 4, 5, 99):                                   # configurations that read V rows, or none at all
+        assert pr_call(config=cfg) == HIP_ERROR_INVALID_VALUE, cfg
+    assert pr_call(wsb=wsb - 256) == HIP_ERROR_INVALID_VALUE
 
 
 def test_rms_rope_rejects():

@@ -205,3 +205,58 @@ def test_fused_small(cfg, kind, pairing, rot, causal, p0, n_pre, HK):
                               causal=bool(causal), p0=p0, n_pre=n_pre, config=cfg)
     torch.cuda.synchronize()
     assert_close(from_dev(out), ref, what="fused")
+
+
+# ------------------------------------------------------------------------------------------ the two stages
+@pytest.mark.parametrize("Sk,HK,n_pre", [(190, 2, 0), (64, 1, 0), (1, 1, 0), (200, 3, 50)])
+def test_kv_prepare_layout_and_prepared_equals_fused(Sk, HK, n_pre):
+    """lr_joint_kv_prepare writes the normalised keys [HK][Sk][128] and V^T tiles [HK][ceil(Sk/64)][128][64] (zero past
+    Sk, exact copies of V otherwise); lr_joint_attention_prepared over that workspace equals the fused call bit for bit."""
+    print(f"\n[kv-prepare] Sk={Sk} HK={HK} n_pre={n_pre}", flush=True)
+    Sq, H = 130, 2 * HK
+    q = oracle.synth_bf16(41, 1, (Sq, H, 128))
+    k = oracle.synth_bf16(41, 2, (Sk, HK, 128))
+    v = oracle.synth_bf16(41, 3, (Sk, HK, 128))
+    qa, qb = _tables(1, Sq, 128, seed=8)
+    ka, kb = _tables(1, Sk, 128, seed=9)
+    need = ops.workspace_bytes(Sk, HK)
+    ws = torch.full((need,), 0xAB, dtype=torch.uint8, device="cuda")   # stale bytes: all must be overwritten
+    ops.joint_kv_prepare(to_dev(k), to_dev(v), ws, k_table=(_dev_table(ka), _dev_table(kb)), n_pre=n_pre)
+    torch.cuda.synchronize()
+    raw = ws.cpu().numpy()
+    kbytes = (Sk * HK * 256 + 255) // 256 * 256
+    nt = (Sk + 63) // 64
+    keys = raw[:Sk * HK * 256].view(np.uint16).reshape(HK, Sk, 128)
+    vt = raw[kbytes:kbytes + HK * nt * 128 * 64 * 2].view(np.uint16).reshape(HK, nt, 128, 64)
+    vpad = np.zeros((nt * 64, HK, 128), np.uint16)
+    vpad[:Sk] = v
+    expect_vt = vpad.reshape(nt, 64, HK, 128).transpose(2, 0, 3, 1)
+    assert np.array_equal(vt, expect_vt), "V^T tiles"
+    kref = oracle.rms_rope(k[n_pre:], None, table_kind=oracle.TABLE_COSSIN_F32, ta=ka[:Sk - n_pre], tb=kb[:Sk - n_pre],
+                           eps=1e-6) if Sk > n_pre else np.zeros((0, HK, 128), np.float32)
+    assert np.array_equal(keys[:, :n_pre].transpose(1, 0, 2), k[:n_pre]), "prefix keys copied"
+    if Sk > n_pre:
+        assert np.allclose(bf16_f32(keys[:, n_pre:].transpose(1, 0, 2)), kref, rtol=1e-2, atol=1e-2)
+    tq = (_dev_table(qa), _dev_table(qb))
+    outs = []
+    for cfg in (ops.CFG_AUTO, ops.CFG_PIPE_W4):
+        o = ops.joint_attention_prepared(to_dev(q), ws, Sk, HK, q_table=tq, config=cfg)
+        f = ops.joint_attention(to_dev(q), to_dev(k), to_dev(v), q_table=tq, k_table=(_dev_table(ka), _dev_table(kb)),
+                                n_pre=n_pre, config=cfg)
+        torch.cuda.synchronize()
+        assert np.array_equal(from_dev(o), from_dev(f)), f"prepared != fused (config {cfg})"
+        outs.append(from_dev(o))
+    ref = oracle.joint_attention(q, k, v, table_kind=1, qa=qa, qb=qb, ka=ka, kb=kb, eps=1e-6, n_pre=n_pre,
+                                 precise=True)
+    for o in outs:
+        assert_close(o, ref, what="prepared")
+
+
+def test_prepared_rejects_row_v_configs():
+    """Configurations that read V rows cannot run on a prepared workspace (it holds V^T tiles only)."""
+    Sk, HK = 64, 1
+    ws = torch.zeros(ops.workspace_bytes(Sk, HK), dtype=torch.uint8, device="cuda")
+    q = to_dev(oracle.synth_bf16(42, 1, (32, 1, 128)))
+    for cfg in (ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4):
+        with pytest.raises(Exception):
+            ops.joint_attention_prepared(q, ws, Sk, HK, table_kind=ops.TABLE_NONE, config=cfg)
