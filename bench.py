@@ -29,12 +29,13 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "attention TFLOP/s + % bf16 MFMA peak; ms/call at 4096+512 tokens, 24x128"
-# attention kernel each tile configuration launches (FUSEQ: queries normalised and rotated in registers; VT: values
-# read as packed V^T tiles) -- the configurations lr_joint_attention_prepared accepts
+# attention kernel each tile configuration launches for the benchmark's cos/sin table (QK = 1: queries normalised and
+# rotated in registers with that table kind; VT: values read as packed V^T tiles) -- the configurations
+# lr_joint_attention_prepared accepts
 KERNELS = {
-    0: "attn_fwd_pipe_kernel<8, 1, 64, 3, true, true>",
-    1: "attn_fwd_pipe_kernel<8, 1, 64, 3, true, true>",
-    2: "attn_fwd_pipe_kernel<4, 1, 64, 2, true, true>",
+    0: "attn_fwd_pipe_kernel<8, 1, 64, 3, 1, true>",
+    1: "attn_fwd_pipe_kernel<8, 1, 64, 3, 1, true>",
+    2: "attn_fwd_pipe_kernel<4, 1, 64, 2, 1, true>",
 }
 WORKLOADS = {
     # name: (text tokens, grid description, heads)

@@ -61,18 +61,121 @@ __device__ __forceinline__ void load_q_plain(const AttnArgs& a, int qrow, int he
     }
 }
 
+// Buffer resource over exactly the bytes the call's W query-table rows hold (row r at r * tab_stride elements, P =
+// rot/2 pairs of PAIR elements of ESZ bytes in the last row): the table loads below use 32-bit offsets into it and
+// never address anything outside the table.
+template <int KIND>
+struct QTable {
+    static constexpr int ESZ = KIND == TABLE_MAT2_BF16 ? 2 : 4;    // bytes per table element
+    static constexpr int PAIR = KIND == TABLE_COSSIN_F32 ? 1 : 4;  // elements per pair (per table for cos/sin)
+    static constexpr int PB = PAIR * ESZ;                          // bytes per pair
+    __amdgpu_buffer_rsrc_t ra, rb;
+    int rowb, P;
+    __device__ __forceinline__ QTable(const AttnArgs& a, int row) {
+        P = a.rot >> 1;
+        const uint32_t bytes = (uint32_t)(((int64_t)(a.W - 1) * a.tab_stride + (int64_t)PAIR * P) * ESZ);
+        ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.qta), 0, bytes, 0x00020000);
+        rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(KIND == TABLE_COSSIN_F32 ? a.qtb : a.qta), 0, bytes,
+                                              0x00020000);
+        rowb = (int)((int64_t)row * a.tab_stride * ESZ);
+    }
+    // pairs p0 .. p0+3 (p0 % 4 == 0) in one go; a chunk past the rotated width reads the row's first chunk instead
+    __device__ __forceinline__ void chunk(int p0, Rot2 (&r)[4]) const {
+        const int off = rowb + (p0 + 3 < P ? p0 : 0) * PB;
+        if constexpr (KIND == TABLE_COSSIN_F32) {
+            const auto c = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+            const auto sn = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                r[i].f00 = __uint_as_float(c[i]); r[i].f01 = -__uint_as_float(sn[i]);
+                r[i].f10 = __uint_as_float(sn[i]); r[i].f11 = __uint_as_float(c[i]);
+            }
+        } else if constexpr (KIND == TABLE_MAT2_BF16) {
+            const auto m0 = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+            const auto m1 = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w0 = i < 2 ? m0[2 * i] : m1[2 * i - 4], w1 = i < 2 ? m0[2 * i + 1] : m1[2 * i - 3];
+                r[i].f00 = lo_bf16(w0); r[i].f01 = hi_bf16(w0); r[i].f10 = lo_bf16(w1); r[i].f11 = hi_bf16(w1);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const auto m = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16 * i, 0, 0);
+                r[i].f00 = __uint_as_float(m[0]); r[i].f01 = __uint_as_float(m[1]);
+                r[i].f10 = __uint_as_float(m[2]); r[i].f11 = __uint_as_float(m[3]);
+            }
+        }
+    }
+    // one pair (any p); past the rotated width it reads pair 0 instead
+    __device__ __forceinline__ Rot2 pair(int p) const {
+        const int off = rowb + (p < P ? p : 0) * PB;
+        Rot2 r;
+        if constexpr (KIND == TABLE_COSSIN_F32) {
+            const float c = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, off, 0, 0));
+            const float sn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0));
+            r.f00 = c; r.f01 = -sn; r.f10 = sn; r.f11 = c;
+        } else if constexpr (KIND == TABLE_MAT2_BF16) {
+            const auto m = __builtin_amdgcn_raw_buffer_load_b64(ra, off, 0, 0);
+            r.f00 = lo_bf16(m[0]); r.f01 = hi_bf16(m[0]); r.f10 = lo_bf16(m[1]); r.f11 = hi_bf16(m[1]);
+        } else {
+            const auto m = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+            r.f00 = __uint_as_float(m[0]); r.f01 = __uint_as_float(m[1]);
+            r.f10 = __uint_as_float(m[2]); r.f11 = __uint_as_float(m[3]);
+        }
+        return r;
+    }
+};
+
 // The same fragments with RMSNorm (fp32, eps, fp32 weight) and RoPE applied before a single bf16 rounding.
-// The lane and its partner (lane ^ 32) hold the two interleaved halves of the query's 128 dims.
-__device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
+// The lane and its partner (lane ^ 32) hold the two interleaved halves of the query's 128 dims: this lane has dims
+// 16 ks + 8 hf + j. Its 32 rotation pairs form 8 chunks of 4 consecutive pairs: interleaved pairs, chunk c = pairs
+// 8c + 4hf .. +3 (k-step c); split-half pairs (p, p + rot/2), chunk c = pairs 16(c/2) + 8hf + 4(c%2) .. +3 (k-step
+// c/2, partner k-step c/2 + rot/32). Loads are batched so that few memory latencies are exposed: the query chunks, the
+// weight and the first 4 table chunks together, then the other 4 chunks. CHUNKED: 16-byte table loads (needs rot/2 a
+// multiple of 4); otherwise one load per pair.
+template <int KIND, bool CHUNKED>
+__device__ __forceinline__ void load_q_fused_t(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
     const bool valid = qrow < a.W;
     const int row = valid ? qrow : a.W - 1;
     const uint16_t* src = a.q + (int64_t)row * a.q_rs + head * D + 8 * hf;
+    const bool inter = a.pairing == PAIR_INTERLEAVED;
+    const int half_ks = a.rot >> 5;   // split-half: k-steps holding the first element of each pair
+    QTable<KIND> tab(a, row);
+    auto chunk_p0 = [&](int c) { return inter ? 8 * c + 4 * hf : 16 * (c >> 1) + 8 * hf + 4 * (c & 1); };
+    auto load_batch = [&](int b, Rot2 (&rt)[4][4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = 4 * b + i;
+            if constexpr (CHUNKED) {
+                tab.chunk(chunk_p0(c), rt[i]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rt[i][e] = tab.pair(chunk_p0(c) + e);
+            }
+        }
+    };
+    // ---- loads: query, weight, table chunks 0-3
+    u32x4 raw[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(src + 16 * ks);
+    f32x4 wv[16];
+    if (a.wq) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) wv[i] = *reinterpret_cast<const f32x4*>(a.wq + 16 * (i >> 1) + 8 * hf + 4 * (i & 1));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) wv[i] = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+    }
+    Rot2 rt[4][4];
+    if constexpr (KIND != TABLE_NONE) load_batch(0, rt);
+
+    // ---- RMSNorm
     float x[8][8];
     float ss = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-        u32x4 w = *reinterpret_cast<const u32x4*>(src + 16 * ks);
-        if (!valid) w = u32x4{0, 0, 0, 0};
+        const u32x4 w = valid ? raw[ks] : u32x4{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             x[ks][2 * i] = lo_bf16(w[i]);
@@ -84,38 +187,30 @@ __device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int he
     ss = wave_pair_sum(ss);
     const float rr = rsqrtf(ss * (1.0f / D) + a.eps);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float w = a.wq ? a.wq[16 * ks + 8 * hf + j] : 1.0f;
-            x[ks][j] = x[ks][j] * rr * w;
-        }
-    }
-    if (a.table_kind != TABLE_NONE) {
-        const int64_t toff = (int64_t)row * a.tab_stride;
-        if (a.pairing == PAIR_INTERLEAVED) {
+        for (int j = 0; j < 8; ++j) x[ks][j] = x[ks][j] * rr * wv[2 * ks + (j >> 2)][j & 3];
+
+    // ---- RoPE, chunk by chunk
+    if constexpr (KIND != TABLE_NONE) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
+        for (int b = 0; b < 2; ++b) {
+            if (b == 1) load_batch(1, rt);
 #pragma unroll
-                for (int j = 0; j < 8; j += 2) {
-                    const int d = 16 * ks + 8 * hf + j;
-                    if (d < a.rot) {
-                        const Rot2 r = load_rot(a.table_kind, a.qta, a.qtb, toff, d >> 1);
+            for (int i = 0; i < 4; ++i) {
+                const int c = 4 * b + i;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const Rot2 r = rt[i][e];
+                    if (inter) {
+                        const int ks = c, j = 2 * e;
+                        const bool on = 16 * ks + 8 * hf + j < a.rot;
                         const float x0 = x[ks][j], x1 = x[ks][j + 1];
-                        x[ks][j] = fmaf(r.f00, x0, r.f01 * x1);
-                        x[ks][j + 1] = fmaf(r.f10, x0, r.f11 * x1);
-                    }
-                }
-            }
-        } else {
-            const int half_ks = a.rot >> 5;  // rot / 2 / 16 k-steps hold the first element of each pair
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                if (ks < half_ks) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int p = 16 * ks + 8 * hf + j;
-                        const Rot2 r = load_rot(a.table_kind, a.qta, a.qtb, toff, p);
+                        x[ks][j] = on ? fmaf(r.f00, x0, r.f01 * x1) : x0;
+                        x[ks][j + 1] = on ? fmaf(r.f10, x0, r.f11 * x1) : x1;
+                    } else {
+                        const int ks = c >> 1, j = 4 * (c & 1) + e;
+                        if (ks >= half_ks) continue;
                         // the partner k-step ks + half_ks (< 8): select it without dynamic register indexing
                         float x1 = 0.0f;
 #pragma unroll
@@ -138,6 +233,28 @@ __device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int he
 #pragma unroll
         for (int j = 0; j < 8; ++j) f[j] = (bf16)x[ks][j];
         qf[ks] = f;
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
+    if (KIND == TABLE_NONE || ((a.rot >> 1) & 3) == 0)
+        load_q_fused_t<KIND, true>(a, qrow, head, hf, qf);
+    else
+        load_q_fused_t<KIND, false>(a, qrow, head, hf, qf);
+}
+
+// Query modes of the pipelined kernel besides a TableKind (0-3): plain queries, or the table kind read at run time.
+constexpr int QK_PLAIN = -1;
+constexpr int QK_ANY = 4;
+
+// load_q_fused for the table kind of the call (a uniform branch; each kind's loads batch on their own).
+__device__ __forceinline__ void load_q_fused_any(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
+    switch (a.table_kind) {
+        case TABLE_COSSIN_F32: load_q_fused<TABLE_COSSIN_F32>(a, qrow, head, hf, qf); break;
+        case TABLE_MAT2_BF16: load_q_fused<TABLE_MAT2_BF16>(a, qrow, head, hf, qf); break;
+        case TABLE_MAT2_F32: load_q_fused<TABLE_MAT2_F32>(a, qrow, head, hf, qf); break;
+        default: load_q_fused<TABLE_NONE>(a, qrow, head, hf, qf); break;
     }
 }
 
@@ -255,7 +372,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_regstage_kernel(AttnArgs 
 #pragma unroll
     for (int nb = 0; nb < NQB; ++nb) {
         if constexpr (FUSEQ)
-            load_q_fused(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
+            load_q_fused_any(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
         else
             load_q_plain(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
     }
@@ -441,9 +558,11 @@ __device__ __forceinline__ void block_barrier() {
 // NW waves of NQB x 32 queries each; tiles of BT keys in an NS-stage K/V ring. NQB = 2 reads every K and V operand
 // fragment from LDS once for two 32-query MFMAs, halving LDS traffic per MFMA, at one wave per SIMD (its registers
 // need it); BT = 32 then keeps the two score buffers at 32 registers each.
+// QK: how queries arrive -- QK_PLAIN (already normalised and rotated), a TableKind (RMSNorm + RoPE in registers
+// with that table kind, its loads specialised), or QK_ANY (the table kind read at run time).
 // VT: values arrive packed as V^T tiles ([128 dims][64 keys], 16 KB contiguous per tile, zero past nkeys), stored in
 // LDS with 16-byte chunk c of dim row d at c ^ ((d >> 1) & 7), and the PV A operand is one ds_read_b128 per MFMA.
-template <int NW, int NQB, int BT, int NS, bool FUSEQ, bool VT>
+template <int NW, int NQB, int BT, int NS, int QK, bool VT>
 __global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1)
 __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void attn_fwd_pipe_kernel(AttnArgs a) {
     static_assert(NS >= 2 && NS <= 4, "2- to 4-stage ring");
@@ -539,13 +658,19 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
     };
 
     // ---- queries (B operands of S^T = K Q^T), one set per 32-query block
+    // ---- prologue loads: K(0 .. NS-1) and V(0 .. NS-2) into the ring first, so that their latency overlaps the
+    // query loads (the query's own waits, issued after, are conservative for the ring loads: older loads finish first)
+    for (int i = 0; i < NS && i < ntiles; ++i) issue_k(i, i);
+    for (int i = 0; i < NS - 1 && i < ntiles; ++i) issue_v(i, i);
     bf16x8 qf[NQB][8];
 #pragma unroll
     for (int nb = 0; nb < NQB; ++nb) {
-        if constexpr (FUSEQ)
-            load_q_fused(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
-        else
+        if constexpr (QK == QK_PLAIN)
             load_q_plain(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
+        else if constexpr (QK == QK_ANY)
+            load_q_fused_any(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
+        else
+            load_q_fused<QK>(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
     }
 
     // ---- per-lane LDS offsets
@@ -576,9 +701,7 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
             acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[nb][ks], acc[nb][mb], 0, 0, 0);
     };
 
-    // ---- prologue: K(0 .. NS-1) and V(0 .. NS-2) resident; S(0)
-    for (int i = 0; i < NS && i < ntiles; ++i) issue_k(i, i);
-    for (int i = 0; i < NS - 1 && i < ntiles; ++i) issue_v(i, i);
+    // ---- K(0 .. NS-1) and V(0 .. NS-2) resident; S(0)
     LR_WAIT_VMCNT(0);
     block_barrier();
     f32x16 sA[NQB][MB], sB[NQB][MB];
@@ -749,8 +872,10 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
             l_sum[0] = ls;
             mx[0] = wave_pair_max(mloc) * c;
             if (t + 1 < ntiles && !needs_mask(t + 1)) rescale_for(mx);
+            // K(t+2) and V(t+1) must have landed; the loads of the last NS-2 steps (all refills while this step
+            // refilled) may stay in flight
             if (NS == 2 || !refilled) LR_WAIT_VMCNT(0);
-            else LR_WAIT_VMCNT(2 * LOADS);
+            else LR_WAIT_VMCNT((NS - 2) * 2 * LOADS);
             block_barrier();
             return;
         }
@@ -830,7 +955,7 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
         if (t + 1 < ntiles && !needs_mask(t + 1)) rescale_for(mx);
         // ---- K(t+2) and V(t+1) (issued a step ago with 3 stages, at this step's start with 2) must have landed
         if (NS == 2 || !refilled) LR_WAIT_VMCNT(0);
-        else LR_WAIT_VMCNT(2 * LOADS);
+        else LR_WAIT_VMCNT((NS - 2) * 2 * LOADS);
         block_barrier();
     };
 
@@ -960,7 +1085,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(AttnArgs a) {
     // ---- queries
     bf16x8 qf[8];
     if constexpr (FUSEQ)
-        load_q_fused(a, wrow0 + n, head, hf, qf);
+        load_q_fused_any(a, wrow0 + n, head, hf, qf);
     else
         load_q_plain(a, wrow0 + n, head, hf, qf);
 
@@ -1147,13 +1272,13 @@ hipError_t launch_regstage(const AttnArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int NW, int NQB, int BT, int NS, bool FUSEQ, bool VT = false>
+template <int NW, int NQB, int BT, int NS, int QK, bool VT = false>
 hipError_t launch_pipe(const AttnArgs& a, hipStream_t stream) {
     constexpr int BM = 32 * NQB * NW;
     const int64_t nqb = (a.W + BM - 1) / BM;
     const int64_t blocks = nqb * a.H;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, NQB, BT, NS, FUSEQ, VT>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, NQB, BT, NS, QK, VT>), dim3((unsigned)blocks), dim3(NW * 64), 0,
                        stream, a);
     return hipGetLastError();
 }
@@ -1171,23 +1296,38 @@ bool attention_config_reads_vt(int config) {
     return config == ATTN_CFG_AUTO || config == ATTN_CFG_PIPE_W8 || config == ATTN_CFG_PIPE_W4;
 }
 
+// The prepared-keys path over packed V^T tiles, queries fused with table kind K (the 64-key pipelined shapes).
+template <int K>
+hipError_t launch_vt(const AttnArgs& a, int config, hipStream_t stream) {
+    switch (config) {
+        case ATTN_CFG_PIPE_W8: return launch_pipe<8, 1, 64, 3, K, true>(a, stream);
+        case ATTN_CFG_PIPE_W4: return launch_pipe<4, 1, 64, 2, K, true>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config, hipStream_t stream) {
     if (config == ATTN_CFG_AUTO) config = ATTN_CFG_PIPE_W8;
     if (v_t) {
         if (!fuse_q) return hipErrorInvalidValue;
-        switch (config) {
-            case ATTN_CFG_PIPE_W8: return launch_pipe<8, 1, 64, 3, true, true>(a, stream);
-            case ATTN_CFG_PIPE_W4: return launch_pipe<4, 1, 64, 2, true, true>(a, stream);
+        switch (a.table_kind) {
+            case TABLE_NONE: return launch_vt<TABLE_NONE>(a, config, stream);
+            case TABLE_COSSIN_F32: return launch_vt<TABLE_COSSIN_F32>(a, config, stream);
+            case TABLE_MAT2_BF16: return launch_vt<TABLE_MAT2_BF16>(a, config, stream);
+            case TABLE_MAT2_F32: return launch_vt<TABLE_MAT2_F32>(a, config, stream);
             default: return hipErrorInvalidValue;
         }
     }
+    // values as rows: the plain attention entry points, and the fused call's row-reading configurations
     switch (config) {
         case ATTN_CFG_PIPE_W8:
-            return fuse_q ? launch_pipe<8, 1, 64, 3, true>(a, stream) : launch_pipe<8, 1, 64, 3, false>(a, stream);
+            if (fuse_q) return hipErrorInvalidValue;   // the fused call reaches this shape through packed V^T
+            return launch_pipe<8, 1, 64, 3, QK_PLAIN>(a, stream);
         case ATTN_CFG_PIPE_W4:   // 64 KB of LDS so that two 4-wave blocks share a CU
-            return fuse_q ? launch_pipe<4, 1, 64, 2, true>(a, stream) : launch_pipe<4, 1, 64, 2, false>(a, stream);
+            if (fuse_q) return hipErrorInvalidValue;
+            return launch_pipe<4, 1, 64, 2, QK_PLAIN>(a, stream);
         case ATTN_CFG_WIDE_W4:
-            return fuse_q ? launch_pipe<4, 2, 32, 4, true>(a, stream) : launch_pipe<4, 2, 32, 4, false>(a, stream);
+            return fuse_q ? launch_pipe<4, 2, 32, 4, QK_ANY>(a, stream) : launch_pipe<4, 2, 32, 4, QK_PLAIN>(a, stream);
         case ATTN_CFG_REGSTAGE_W8:
             return fuse_q ? launch_regstage<32, 8, true>(a, stream) : launch_regstage<32, 8, false>(a, stream);
         case ATTN_CFG_PINGPONG_W8:
