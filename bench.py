@@ -33,8 +33,8 @@ METRIC = "attention TFLOP/s + % bf16 MFMA peak; ms/call at 4096+512 tokens, 24x1
 # rotated in registers with that table kind; VT: values read as packed V^T tiles) -- the configurations
 # lr_joint_attention_prepared accepts
 KERNELS = {
-    0: "attn_fwd_pipe_kernel<8, 1, 64, 3, 1, true>",
-    1: "attn_fwd_pipe_kernel<8, 1, 64, 3, 1, true>",
+    0: "attn_fwd_pipe_kernel<8, 1, 64, 4, 1, true>",
+    1: "attn_fwd_pipe_kernel<8, 1, 64, 4, 1, true>",
     2: "attn_fwd_pipe_kernel<4, 1, 64, 2, 1, true>",
 }
 WORKLOADS = {

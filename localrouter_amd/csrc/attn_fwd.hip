@@ -797,12 +797,8 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
         }
         // ---- refill: K(t+NS) into the slot K(t) left, V(t+NS-1) into the slot V(t-1) left (both read last step)
         const bool refilled = t + NS < ntiles;
-        if (refilled) {
-            issue_k(t + NS, t % NS);
-            issue_v(t + NS - 1, (t + NS - 1) % NS);
-        } else if (t + NS - 1 < ntiles) {
-            issue_v(t + NS - 1, (t + NS - 1) % NS);
-        }
+        if (refilled) issue_k(t + NS, t % NS);
+        if (t + NS - 1 < ntiles) issue_v(t + NS - 1, (t + NS - 1) % NS);
         if constexpr (NQB == 1 && BT == 64) {
             // Explicit schedule of the tile's 32 MFMA slots (one wave's instruction stream; a sched_barrier closes
             // every slot, so the compiler keeps each slot's work in it):
@@ -1300,7 +1296,7 @@ bool attention_config_reads_vt(int config) {
 template <int K>
 hipError_t launch_vt(const AttnArgs& a, int config, hipStream_t stream) {
     switch (config) {
-        case ATTN_CFG_PIPE_W8: return launch_pipe<8, 1, 64, 3, K, true>(a, stream);
+        case ATTN_CFG_PIPE_W8: return launch_pipe<8, 1, 64, 4, K, true>(a, stream);
         case ATTN_CFG_PIPE_W4: return launch_pipe<4, 1, 64, 2, K, true>(a, stream);
         default: return hipErrorInvalidValue;
     }
