@@ -133,9 +133,10 @@ struct QTable {
 // 8c + 4hf .. +3 (k-step c); split-half pairs (p, p + rot/2), chunk c = pairs 16(c/2) + 8hf + 4(c%2) .. +3 (k-step
 // c/2, partner k-step c/2 + rot/32). Loads are batched so that few memory latencies are exposed: the query chunks, the
 // weight and the first 4 table chunks together, then the other 4 chunks. CHUNKED: 16-byte table loads (needs rot/2 a
-// multiple of 4); otherwise one load per pair.
+// multiple of 4); otherwise one load per pair. qscale multiplies the normalised query before its single rounding.
 template <int KIND, bool CHUNKED>
-__device__ __forceinline__ void load_q_fused_t(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
+__device__ __forceinline__ void load_q_fused_t(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8],
+                                               float qscale) {
     const bool valid = qrow < a.W;
     const int row = valid ? qrow : a.W - 1;
     const uint16_t* src = a.q + (int64_t)row * a.q_rs + head * D + 8 * hf;
@@ -185,7 +186,7 @@ __device__ __forceinline__ void load_q_fused_t(const AttnArgs& a, int qrow, int 
         for (int j = 0; j < 8; ++j) ss = fmaf(x[ks][j], x[ks][j], ss);
     }
     ss = wave_pair_sum(ss);
-    const float rr = rsqrtf(ss * (1.0f / D) + a.eps);
+    const float rr = rsqrtf(ss * (1.0f / D) + a.eps) * qscale;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
@@ -237,11 +238,12 @@ __device__ __forceinline__ void load_q_fused_t(const AttnArgs& a, int qrow, int 
 }
 
 template <int KIND>
-__device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
+__device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8],
+                                             float qscale = 1.0f) {
     if (KIND == TABLE_NONE || ((a.rot >> 1) & 3) == 0)
-        load_q_fused_t<KIND, true>(a, qrow, head, hf, qf);
+        load_q_fused_t<KIND, true>(a, qrow, head, hf, qf, qscale);
     else
-        load_q_fused_t<KIND, false>(a, qrow, head, hf, qf);
+        load_q_fused_t<KIND, false>(a, qrow, head, hf, qf, qscale);
 }
 
 // Query modes of the pipelined kernel besides a TableKind (0-3): plain queries, or the table kind read at run time.
@@ -567,6 +569,10 @@ __global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1)
 __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void attn_fwd_pipe_kernel(AttnArgs a) {
     static_assert(NS >= 2 && NS <= 4, "2- to 4-stage ring");
     static_assert(!VT || (BT == 64 && NQB == 1), "packed V^T tiles are 64 keys wide");
+    // FOLD (fused queries on the scheduled 64-key shape): queries arrive multiplied by scale * log2(e), and the running
+    // max m is subtracted by the score MFMAs themselves (their accumulator starts at -m instead of 0), so a score
+    // register already holds s * scale * log2(e) - m and P = exp2(score) needs no per-score FMA.
+    constexpr bool FOLD = QK != QK_PLAIN && NQB == 1 && BT == 64;
     static_assert(NQB == 1 || NQB == 2, "one or two 32-query blocks per wave");
     static_assert(BT == 32 || BT == 64, "32- or 64-key tiles");
     constexpr int BM = 32 * NQB * NW;
@@ -670,7 +676,7 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
         else if constexpr (QK == QK_ANY)
             load_q_fused_any(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
         else
-            load_q_fused<QK>(a, wrow0 + 32 * nb + n, head, hf, qf[nb]);
+            load_q_fused<QK>(a, wrow0 + 32 * nb + n, head, hf, qf[nb], FOLD ? a.c : 1.0f);
     }
 
     // ---- per-lane LDS offsets
@@ -720,13 +726,18 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
     for (int nb = 0; nb < NQB; ++nb)
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[nb][db] = f32x16{};
-    // m_used starts at a finite -1e30 (not -inf): every alpha below is exp2 of a finite value or of -inf (= 0)
+    // m_used starts at a finite -1e30 (not -inf): every alpha below is exp2 of a finite value or of -inf (= 0).
+    // FOLD: m_used is also the offset the score MFMAs subtract; it starts at 0 (S(0) above was computed that way) and
+    // `m_set` marks lanes whose reference has been taken from a finite tile max.
     float m_used[NQB], l_sum[NQB];
+    bool m_set[NQB];
 #pragma unroll
     for (int nb = 0; nb < NQB; ++nb) {
-        m_used[nb] = -1e30f;
+        m_used[nb] = FOLD ? 0.0f : -1e30f;
         l_sum[nb] = 0.0f;
+        m_set[nb] = false;
     }
+    f32x16 negm = f32x16{};   // FOLD: -m_used in every accumulator slot (the score MFMAs' initial accumulator)
     const float c = a.c;
     const bf16x2 ones2 = {(bf16)1.0f, (bf16)1.0f};
 
@@ -760,14 +771,29 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
             for (int mb = 1; mb < MB; ++mb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) m = fmaxf(m, sc[nb][mb][r]);
-            mx[nb] = wave_pair_max(m) * c;
+            mx[nb] = FOLD ? wave_pair_max(m) : wave_pair_max(m) * c;
         }
     };
-    // raise the running max (and rescale O, l) when a tile's max exceeds it by more than 2^8
-    auto rescale_for = [&](const float (&mx)[NQB]) {
+    // raise the running max (and rescale O, l) when a tile's max exceeds it by more than 2^8. FOLD: mx is relative to
+    // the current offset, and the tile's scores sc (computed with the old offset) are shifted with it.
+    auto rescale_for = [&](const float (&mx)[NQB], f32x16 (&sc)[NQB][MB]) {
 #pragma unroll
         for (int nb = 0; nb < NQB; ++nb) {
-            if (__builtin_amdgcn_ballot_w64(mx[nb] > m_used[nb] + RESCALE_TAU)) {
+            if constexpr (FOLD) {
+                const bool want = (!m_set[nb] && mx[nb] > -INFINITY) || mx[nb] > RESCALE_TAU;
+                if (__builtin_amdgcn_ballot_w64(want)) {
+                    const float d = want ? mx[nb] : 0.0f;
+                    const float alpha = m_set[nb] ? __builtin_amdgcn_exp2f(-d) : 1.0f;   // O, l are still 0 if unset
+                    m_used[nb] += d;
+                    m_set[nb] = m_set[nb] || want;
+                    l_sum[nb] *= alpha;
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) o[nb][db] *= alpha;
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) sc[nb][mb] -= d;
+                    negm = f32x16{} - m_used[nb];
+                }
+            } else if (__builtin_amdgcn_ballot_w64(mx[nb] > m_used[nb] + RESCALE_TAU)) {
                 const float mn = fmaxf(m_used[nb], mx[nb]);
                 const float alpha = __builtin_amdgcn_exp2f(m_used[nb] - mn);
                 m_used[nb] = mn;
@@ -779,7 +805,7 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
     };
     float mx_cur[NQB];
     tile_max(sA, mx_cur);
-    if (!needs_mask(0)) rescale_for(mx_cur);
+    if (!needs_mask(0)) rescale_for(mx_cur, sA);
 
     // One tile t. On entry: sc = S(t), its max mx, and -- unless tile t needs masking -- the running max already
     // raised for it. Then
@@ -793,7 +819,7 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
         if (needs_mask(t)) {
             mask_tile(t, sc);
             tile_max(sc, mx);
-            rescale_for(mx);
+            rescale_for(mx, sc);
         }
         // ---- refill: K(t+NS) into the slot K(t) left, V(t+NS-1) into the slot V(t-1) left (both read last step)
         const bool refilled = t + NS < ntiles;
@@ -841,8 +867,8 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
             for (int s = 0; s < 32; ++s) {
                 if (s + 3 < 32) fr[(s + 3) & 3] = frag(s + 3);
                 if (s < 16) {
-                    sn[0][s & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[s & 3], qf[0][s >> 1],
-                                                                          s < 2 ? f32x16{} : sn[0][s & 1], 0, 0, 0);
+                    sn[0][s & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        fr[s & 3], qf[0][s >> 1], s < 2 ? (FOLD ? negm : f32x16{}) : sn[0][s & 1], 0, 0, 0);
                 } else {
                     const int kk = (s - 16) >> 2, db = (s - 16) & 3;
                     const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pw[4 * kk], pw[4 * kk + 1], pw[4 * kk + 2],
@@ -853,8 +879,9 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
                 for (int k = 0; k < 16; ++k) {
                     if ((3 * k) / 2 != s) continue;
                     const int kk = k >> 2, j = k & 3, r = 8 * (kk & 1) + 2 * j;
-                    pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sc[0][kk >> 1][r], c, nm)),
-                                        __builtin_amdgcn_exp2f(fmaf(sc[0][kk >> 1][r + 1], c, nm)));
+                    const float e0 = FOLD ? sc[0][kk >> 1][r] : fmaf(sc[0][kk >> 1][r], c, nm);
+                    const float e1 = FOLD ? sc[0][kk >> 1][r + 1] : fmaf(sc[0][kk >> 1][r + 1], c, nm);
+                    pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(e0), __builtin_amdgcn_exp2f(e1));
                     // the row sum of the bf16 P exactly as the PV MFMA consumes it
                     ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[k]), ones2, ls, false);
                 }
@@ -866,8 +893,8 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
                 __builtin_amdgcn_sched_barrier(0);
             }
             l_sum[0] = ls;
-            mx[0] = wave_pair_max(mloc) * c;
-            if (t + 1 < ntiles && !needs_mask(t + 1)) rescale_for(mx);
+            mx[0] = FOLD ? wave_pair_max(mloc) : wave_pair_max(mloc) * c;
+            if (t + 1 < ntiles && !needs_mask(t + 1)) rescale_for(mx, sn);
             // K(t+2) and V(t+1) must have landed; the loads of the last NS-2 steps (all refills while this step
             // refilled) may stay in flight
             if (NS == 2 || !refilled) LR_WAIT_VMCNT(0);
@@ -948,7 +975,7 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
             }
         }
         tile_max(sn, mx);
-        if (t + 1 < ntiles && !needs_mask(t + 1)) rescale_for(mx);
+        if (t + 1 < ntiles && !needs_mask(t + 1)) rescale_for(mx, sn);
         // ---- K(t+2) and V(t+1) (issued a step ago with 3 stages, at this step's start with 2) must have landed
         if (NS == 2 || !refilled) LR_WAIT_VMCNT(0);
         else LR_WAIT_VMCNT((NS - 2) * 2 * LOADS);
