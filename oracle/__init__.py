@@ -8,6 +8,9 @@ Two layers:
     fp32 flash-style attention (the CPU baseline), the fused op. Wrapped here with numpy arrays.
   * brute_* below: an independent pure-numpy fp64 restatement for tiny shapes, used to cross-check liblro.so.
 
+  * lro_int8.c: MiniMax H3's INT8 attention chain (K anchor, Hadamard rotation, int8 quantisers, attention over the
+    quantised operands); wrapped by the i8_* functions and int8_attention below.
+
 Reference semantics (jayleaton/localrouter): kernels/cuda/qwen_image/attention.cu:253-444 (attention, mask, GQA),
 kernels/cuda/minimax/kitchen/rms_rope.cu:37-230 + rope_device.cuh:65-98 (RMSNorm + RoPE),
 src/engines/qwen_image/triton_k.zig:44-53 (Qwen's fp32 cos/sin form).
@@ -74,6 +77,12 @@ def lib() -> ctypes.CDLL:
                                           ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                           ctypes.c_int, ctypes.c_int, _P]
+        L.lro_i8_rotate.argtypes = [_P, ctypes.c_int]
+        L.lro_i8_anchor.argtypes = [_P, _I64, ctypes.c_int]
+        L.lro_i8_anchor.restype = ctypes.c_int
+        L.lro_i8_quant_rows.argtypes = [_P, _I64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P]
+        L.lro_i8_quant_v.argtypes = [_P, _I64, ctypes.c_int, _P, _P]
+        L.lro_i8_attention.argtypes = [_P, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, _P]
         _lib = L
     return _lib
 
@@ -256,3 +265,74 @@ def brute_attention(q, k, v, *, p0=0, nkeys=None, causal=False, scale=None) -> n
         p /= p.sum(axis=1, keepdims=True)
         out[:, h, :] = p @ v[:, h // G, :]
     return out
+
+
+# ------------------------------------------------------------------------------------------ INT8 chain (lro_int8.c)
+I8_KGROUP = 16   # keys per K scale
+
+
+def i8_rotation_for(seq: int) -> int:
+    """H4 for sequences up to 256 tokens, the signed H128 above (src/engines/minimax_h3/launch.zig:387-391)."""
+    return 4 if seq <= 256 else 128
+
+
+def i8_rotate(x: np.ndarray, kind: int) -> np.ndarray:
+    """Rotate every 128-channel row of x (fp32) in place order of the reference's convrot helpers; returns a copy."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    for row in y.reshape(-1, D):
+        lib().lro_i8_rotate(_ptr(row), kind)
+    return y
+
+
+def i8_anchor(k_head_bits: np.ndarray) -> int:
+    """Anchor row of one kv head's keys (uint16 bf16 bits [Lk, 128] or a strided [Lk, ..., 128] view's head slice)."""
+    k = np.ascontiguousarray(k_head_bits, dtype=np.uint16)
+    return int(lib().lro_i8_anchor(_ptr(k), D, k.shape[0]))
+
+
+def i8_quant_rows(x_bits: np.ndarray, rot: int, anchor: int = -1, group: int = 1):
+    """int8 [rows, 128] and the per-group scales of one head's rows (bf16 bits [rows, 128])."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows = x.shape[0]
+    out = np.zeros((rows, D), np.int8)
+    sc = np.zeros(((rows + group - 1) // group,), np.float32)
+    lib().lro_i8_quant_rows(_ptr(x), D, rows, rot, anchor, group, _ptr(out), _ptr(sc))
+    return out, sc
+
+
+def i8_quant_v(v_bits: np.ndarray):
+    v = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    out = np.zeros((v.shape[0], D), np.int8)
+    sc = np.zeros((D,), np.float32)
+    lib().lro_i8_quant_v(_ptr(v), D, v.shape[0], _ptr(out), _ptr(sc))
+    return out, sc
+
+
+def i8_attention(q8, qs, k8, ks, v8, vs, kgroup: int = I8_KGROUP) -> np.ndarray:
+    q8, k8, v8 = (np.ascontiguousarray(a, dtype=np.int8) for a in (q8, k8, v8))
+    qs, ks, vs = (np.ascontiguousarray(a, dtype=np.float32) for a in (qs, ks, vs))
+    out = np.zeros((q8.shape[0], D), np.float32)
+    lib().lro_i8_attention(_ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), kgroup, _ptr(v8), _ptr(vs), q8.shape[0],
+                           k8.shape[0], _ptr(out))
+    return out
+
+
+def int8_attention(qkv_bits: np.ndarray, heads: int, rows=None) -> tuple[np.ndarray, dict]:
+    """The whole chain for packed qkv (bf16 bits [S, 3, heads, 128]): per head the K anchor, Q (one scale per row) and
+    K (one scale per 16 keys, anchor subtracted) rotated and quantised, V quantised per channel, then attention of the
+    selected query rows (all by default). Returns fp32 [heads, len(rows), 128] and the quantised operands."""
+    S = qkv_bits.shape[0]
+    rot = i8_rotation_for(S)
+    rows = np.arange(S) if rows is None else np.asarray(rows)
+    out = np.zeros((heads, len(rows), D), np.float32)
+    parts = {"q8": [], "qs": [], "k8": [], "ks": [], "v8": [], "vs": [], "anchor": []}
+    for h in range(heads):
+        q, k, v = (np.ascontiguousarray(qkv_bits[:, i, h]) for i in range(3))
+        a = i8_anchor(k)
+        q8, qs = i8_quant_rows(q, rot)
+        k8, ks = i8_quant_rows(k, rot, a, I8_KGROUP)
+        v8, vs = i8_quant_v(v)
+        out[h] = i8_attention(q8[rows], qs[rows], k8, ks, v8, vs)
+        for name, val in zip(parts, (q8, qs, k8, ks, v8, vs, a)):
+            parts[name].append(val)
+    return out, parts

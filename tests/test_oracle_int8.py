@@ -1,0 +1,141 @@
+"""Pins of the INT8-chain oracle (oracle/lro_int8.c), on the CPU only.
+
+Each part is checked against something it does not share code with:
+  * the rotations: the signed H128 equals the closed form (-1)^popcount(i & j) / sqrt(128) times the reference's sign
+    vector (the constants of kernels/cuda/minimax/kitchen/quant_qk_int8.cu:93-97), H4 is block-diagonal with the
+    4-point Sylvester Hadamard, both are orthogonal and leave dot products of rotated pairs unchanged;
+  * the K anchor: an independent numpy restatement of the criterion of quant_qk_int8.cu:461-596, on data where the
+    centring helps (it must pick an anchor) and where it does not (it must decline);
+  * the quantisers: scale = absmax / 127 + 1e-7 (Q, K) and absmax / 127 per channel (V), the largest magnitude maps to
+    +-127, every element within half a step, ties to even;
+  * the attention over quantised operands: an independent numpy fp64 softmax over the dequantised operands, and the
+    whole chain against exact attention of the unquantised inputs within the quantisation error.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+
+SCALE = float(np.frombuffer(np.uint32(0x3DB504F3).tobytes(), np.float32)[0])
+SIGNS = [0x1035997B, 0x8087F5EE, 0xEE2E4E1A, 0x71132418]
+
+
+def _sign_vector():
+    out = np.ones(128)
+    for j in range(128):
+        lane, c = j // 4, j % 4
+        flip = ((SIGNS[lane >> 3] >> ((lane & 7) * 4 + c)) & 1) ^ 1
+        out[j] = -1.0 if flip else 1.0
+    return out
+
+
+def _rotation_matrix(kind):
+    # row i of the result is the rotation of basis vector e_i, so its transpose maps inputs to outputs
+    return oracle.i8_rotate(np.eye(128, dtype=np.float32), kind).T.astype(np.float64)
+
+
+def test_signed_h128_closed_form():
+    M = _rotation_matrix(128)
+    pc = np.array([[bin(i & j).count("1") & 1 for j in range(128)] for i in range(128)])
+    closed = np.where(pc == 1, -1.0, 1.0) / np.sqrt(128.0) * _sign_vector()[None, :]
+    assert np.abs(M - closed).max() < 1e-7
+    assert np.abs(M @ M.T - np.eye(128)).max() < 1e-6
+    # a wrong sign word would be caught: the sign vector has both signs in every word's lanes
+    assert (_sign_vector() < 0).sum() not in (0, 128)
+
+
+def test_h4_blocks():
+    M = _rotation_matrix(4)
+    h4 = 0.5 * np.array([[1, 1, 1, 1], [1, -1, 1, -1], [1, 1, -1, -1], [1, -1, -1, 1]], np.float64)
+    assert np.array_equal(M, np.kron(np.eye(32), h4))
+
+
+def test_rotation_keeps_dot_products():
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((5, 128)).astype(np.float32)
+    k = rng.standard_normal((7, 128)).astype(np.float32)
+    for kind in (4, 128):
+        qr, kr = oracle.i8_rotate(q, kind), oracle.i8_rotate(k, kind)
+        assert np.allclose(qr @ kr.T, q @ k.T, atol=1e-4)
+
+
+def _anchor_numpy(k):
+    """Independent restatement: 9 samples at i (L-1)/8, argmin of ||9 s_j - sum s||^2, accepted when the residual
+    energy drops and the residual abs-max grows by at most 12.5 %."""
+    L = k.shape[0]
+    idx = [i * (L - 1) // 8 for i in range(9)]
+    s = k[idx].astype(np.float64)
+    dist = ((9 * s - s.sum(0)[None]) ** 2).sum(1)
+    best = int(np.argmin(dist))
+    r = s - s[best][None]
+    ok = (r ** 2).sum() < (s ** 2).sum() and np.abs(r).max() <= np.abs(s).max() * 1.125
+    return idx[best] if ok else -1
+
+
+def test_anchor_against_numpy():
+    rng = np.random.default_rng(1)
+    seen = set()
+    for trial in range(40):
+        L = int(rng.integers(9, 400))
+        base = rng.standard_normal(128) * (4.0 if trial % 2 else 0.0)
+        k = base[None] + rng.standard_normal((L, 128)) * (0.3 if trial % 2 else 1.0)
+        bits = oracle.f32_to_bf16(k.astype(np.float32))
+        got = oracle.i8_anchor(bits)
+        assert got == _anchor_numpy(oracle.bf16_to_f32(bits)), trial
+        seen.add(got >= 0)
+    assert seen == {True, False}, "both outcomes must occur"
+
+
+def test_quantisers():
+    rng = np.random.default_rng(2)
+    x = oracle.f32_to_bf16((rng.standard_normal((70, 128)) * 3).astype(np.float32))
+    xf = oracle.bf16_to_f32(x)
+    for rot, group in ((128, 1), (4, 16), (0, 16)):
+        q8, sc = oracle.i8_quant_rows(x, rot, -1, group)
+        xr = oracle.i8_rotate(xf, rot) if rot else xf
+        for g in range(len(sc)):
+            blk = xr[g * group:(g + 1) * group]
+            assert sc[g] == np.float32(np.float32(np.abs(blk).max()) / np.float32(127.0) + np.float32(1e-7))
+            qb = q8[g * group:(g + 1) * group].astype(np.float64)
+            assert np.abs(qb * sc[g] - blk).max() <= 0.5 * sc[g] * (1 + 1e-5)
+            assert np.abs(qb).max() == 127
+    v8, vs = oracle.i8_quant_v(x)
+    assert np.allclose(vs, np.abs(xf).max(0) / 127.0, rtol=1e-6)
+    assert np.all(np.abs(v8.astype(np.float64) * vs[None] - xf) <= 0.5 * vs[None] * (1 + 1e-5))
+
+
+def test_attention_over_quantised_operands():
+    rng = np.random.default_rng(3)
+    W, nk = 20, 77
+    q8 = rng.integers(-127, 128, (W, 128)).astype(np.int8)
+    k8 = rng.integers(-127, 128, (nk, 128)).astype(np.int8)
+    v8 = rng.integers(-127, 128, (nk, 128)).astype(np.int8)
+    qs = rng.uniform(0.005, 0.02, W).astype(np.float32)
+    ks = rng.uniform(0.005, 0.02, (nk + 15) // 16).astype(np.float32)
+    vs = rng.uniform(0.005, 0.02, 128).astype(np.float32)
+    got = oracle.i8_attention(q8, qs, k8, ks, v8, vs)
+    kd = k8.astype(np.float64) * np.repeat(ks.astype(np.float64), 16)[:nk, None]
+    s = (q8.astype(np.float64) * qs[:, None]) @ kd.T * SCALE
+    p = np.exp(s - s.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    ref = p @ (v8.astype(np.float64) * vs[None])
+    assert np.abs(got - ref).max() < 1e-6
+
+
+def test_chain_close_to_exact_attention():
+    """Quantisation error only: the chain against fp64 attention of the bf16 inputs, both with the anchor and without
+    (an anchor shifts every score of a query equally, which softmax ignores)."""
+    S, H = 300, 2
+    qkv = oracle.synth_bf16(7, 1, (S, 3, H, 128))
+    # give head 1 a large common key offset so that its anchor is used
+    f = oracle.bf16_to_f32(qkv)
+    f[:, 1, 1] += 3.0 * oracle.bf16_to_f32(oracle.synth_bf16(7, 2, (1, 128)))
+    qkv = oracle.f32_to_bf16(f)
+    out, parts = oracle.int8_attention(qkv, H)
+    assert parts["anchor"][1] >= 0
+    qf = oracle.bf16_to_f32(qkv)
+    for h in range(H):
+        exact = oracle.brute_attention(qf[:, 0, h][:, None], qf[:, 1, h][:, None], qf[:, 2, h][:, None])[:, 0]
+        d = np.abs(out[h] - exact)
+        assert d.max() < 2e-2 and d.mean() < 2e-3, (h, d.max(), d.mean())
