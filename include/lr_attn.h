@@ -21,6 +21,9 @@
  *                               kitchen_rms_rope_split_half_, kernels/cuda/minimax/kitchen_launch.cu:284-314
  *   lr_joint_attention_fused <- the chain rope_q -> rope_k -> V copy -> attention of Dit.block,
  *                               src/engines/qwen_image/dit.zig:252-293 (and minimax_h3/dit.zig:663-672), as one call
+ *   lr_int8_attention*       <- MiniMax H3's INT8 attention: Kitchen.Plan / attentionPrep / attentionKernel /
+ *                               attention, src/engines/minimax_h3/launch.zig:317-419, and kitchen_int8_attention
+ *                               {,_rows,_workspace_bytes}, kernels/cuda/minimax/kitchen_launch.cu:193-280
  */
 #ifndef LR_ATTN_H
 #define LR_ATTN_H
@@ -35,7 +38,7 @@ extern "C" {
 /* hipStream_t without pulling in the HIP headers: an opaque pointer (NULL = the default stream). */
 typedef struct ihipStream_t* lr_stream_t;
 
-#define LR_ATTN_ABI_VERSION 2
+#define LR_ATTN_ABI_VERSION 3
 #define LR_HEAD_DIM 128
 
 /* RoPE table kinds: how rotation coefficients are stored per token row, per pair p < rot_dim/2. */
@@ -167,6 +170,37 @@ int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void
                                 int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
                                 int64_t out_row_stride, int n_pre, void* workspace, size_t workspace_bytes, int config,
                                 lr_stream_t stream);
+
+/*
+ * MiniMax H3's INT8 attention (the reference's comfy-kitchen SageAttention chain): per kv head a K anchor, Q and K
+ * rotated (H4 blocks when Sk <= 256, else the signed H128) and quantised to int8, V quantised per channel, then
+ * out = softmax(scale * Q K^T) V with int8 Q K^T and u8 P x s8 V products (P rounded per key tile of 64 keys, 128 past
+ * Sk = 1024). Arguments as kitchen_int8_attention (kitchen_launch.cu:193-270):
+ *   q [B][H][Sq][D], k and v [B][HK][Sk][D] bf16 with element strides (sb, sh, sn) per tensor, last stride 1; each
+ *   stride a multiple of 8 elements and each base 16-byte aligned (views into one packed qkv buffer qualify);
+ *   D must be 128; H a multiple of HK; scale > 0 (the reference passes 128^-0.5 rounded to fp32, 0x3db504f3);
+ *   workspace: lr_int8_attention_workspace_bytes(B, H, HK, Sq, Sk, D) bytes, 256-byte aligned, no initial contents.
+ * lr_int8_attention writes out bf16 [B][H][Sq][D] contiguous; lr_int8_attention_rows writes rows [Sq][H * D]
+ * (B must be 1), the same values. The workspace layout is this library's own (quantised operands, scales, per-tile
+ * column sums): it is written by the prep and read by the kernel, nothing else.
+ *   lr_int8_attention_workspace_bytes  <- Kitchen.Plan.of / kitchen_int8_attention_workspace_bytes (0: unsupported)
+ *   lr_int8_attention_prep             <- Kitchen.attentionPrep (launch.zig:360-397): anchor, Q/K and V to int8
+ *   lr_int8_attention_kernel           <- Kitchen.attentionKernel (launch.zig:399-419); o_rows 0: out [B][H][Sq][D],
+ *                                         1: rows [Sq][H * D] (B 1)
+ */
+size_t lr_int8_attention_workspace_bytes(int B, int H, int HK, int Sq, int Sk, int D);
+int lr_int8_attention(const void* q, const void* k, const void* v, void* out, void* workspace, int B, int H, int HK,
+                      int Sq, int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
+                      int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, float scale, lr_stream_t stream);
+int lr_int8_attention_rows(const void* q, const void* k, const void* v, void* out, void* workspace, int B, int H,
+                           int HK, int Sq, int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb,
+                           int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, float scale,
+                           lr_stream_t stream);
+int lr_int8_attention_prep(const void* q, const void* k, const void* v, void* workspace, int B, int H, int HK, int Sq,
+                           int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
+                           int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, lr_stream_t stream);
+int lr_int8_attention_kernel(void* out, const void* workspace, int B, int H, int HK, int Sq, int Sk, int D,
+                             float scale, int o_rows, lr_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "liblr_attn.so"
-SOURCES = ["attn_fwd.hip", "rms_rope.hip", "lr_abi.hip"]
+SOURCES = ["attn_fwd.hip", "rms_rope.hip", "int8_attn.hip", "lr_abi.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -527,7 +527,6 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_regstage_kernel(AttnArgs 
 //   the direct loads of K(t+3) and V(t+2), a wait for K(t+2) and V(t+1), one s_barrier.
 // so the QK^T MFMAs of the next tile hide the exp/max/sum work of the current one, and every load has two tiles of
 // compute to land.
-constexpr int NSTAGE = 3;
 
 // V tile: 16-byte chunk c of row r stored at c ^ ((r & 3) << 2). A transposed read instruction covers 8 rows x 4
 // chunks (rows 4 apart share r & 3 and differ in the XOR-ed bits), so it touches every bank exactly twice; whole-row

@@ -1,0 +1,656 @@
+// The INT8 attention chain for gfx950: the prep (K anchor, V channel abs-max, Q/K rotation + quantisation, V
+// quantisation into transposed tiles) and the attention kernel (int8 MFMA for Q K^T and P V).
+//
+// Reference semantics (jayleaton/localrouter, comfy-kitchen 0.2.35 vendored at kernels/cuda/minimax/kitchen/):
+//   detect_k_anchor        quant_qk_int8.cu:461-596
+//   Hadamard rotations     quant_qk_int8.cu:75-155 (convrot4, the sign words, five xor butterflies, 1/sqrt(128))
+//   Q/K quantisation       quant_qk_int8.cu:245-247 (scale = absmax / 127 + 1e-7), float_utils.cuh:40-51 (rn, sat)
+//   V quantisation         quant_v_int8.cu:64-140 (per channel, max(absmax / 127, 1e-12))
+//   attention              qk_int_sv_i8_cuda.cuh:56-770 with attn_utils.cuh:610-695 (update_mdo_i32_u8): per key
+//                          tile the row max m_t of the scores, P = exp2(s - m_t + 7.9943534) rounded to u8 (so the
+//                          tile's largest P is 255), the row sum taken over the rounded P, O accumulated in fp32 with
+//                          the tile's scale exp2(m_t - m_running)
+//
+// gfx950 mapping of the attention kernel (one workgroup = 512 threads = 8 waves x 32 queries, two waves per SIMD):
+//   S^T = K Q^T with v_mfma_i32_32x32x32_i8: the A operand is 32 key rows read from LDS in the order key_perm, which
+//   makes the 16 scores a lane holds per 32-key block the 16 consecutive keys 16*(lane/32) .. + 15 -- exactly the
+//   B operand layout of the P V product, so P goes from registers into the next MFMA with no shuffle.
+//   The MFMA is signed x signed, the reference's P is unsigned: P is stored as P ^ 0x80 (= P - 128) and the missing
+//   128 * sum_j v_j is added back per tile by one v_mfma_f32_32x32x2_f32 per 32-dim block whose A operand is the
+//   tile's precomputed int16 column sums and B operand 128 * tile_scale, accumulating straight into O.
+//   K, V^T and the per-tile aux block stream through a 3-stage LDS ring with direct global->LDS loads.
+#include <limits.h>
+#include <math.h>
+
+#include "lr_common.h"
+#include "lr_int8.h"
+
+namespace lr {
+namespace i8 {
+
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+constexpr float S_U8_OFFSET = 7.9943534f;  // log2(255): the tile's largest P becomes 255 (attn_utils.cuh:41)
+
+// ------------------------------------------------------------------------------------------------ prep helpers
+// Exchange with lane ^ M inside each 32-lane half (ds_swizzle, bit-mask mode: and 0x1f, xor M).
+template <int M>
+__device__ __forceinline__ float xor32(float x) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (M << 10)));
+}
+
+__device__ __forceinline__ float max32(float x) {
+    x = fmaxf(x, xor32<1>(x));
+    x = fmaxf(x, xor32<2>(x));
+    x = fmaxf(x, xor32<4>(x));
+    x = fmaxf(x, xor32<8>(x));
+    return fmaxf(x, xor32<16>(x));
+}
+
+// Round to nearest even, saturate to [-128, 127]; NaN -> 0 (float_utils.cuh:40-51).
+__device__ __forceinline__ int rn_sat(float x) {
+    if (x != x) return 0;
+    const float r = fminf(fmaxf(rintf(x), -128.0f), 127.0f);
+    return (int)r;
+}
+
+template <int M>
+__device__ __forceinline__ void butterfly(float (&x)[4], int j) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float o = xor32<M>(x[c]);
+        x[c] = (j & M) ? o - x[c] : x[c] + o;
+    }
+}
+
+// The rotation of one 128-channel row held as 4 channels (4j .. 4j+3) per lane j of a 32-lane half, in the
+// reference's operation order: [sign flip], H4 on the lane's 4 channels, [five butterflies over the lane index,
+// then * 1/sqrt(128)].
+template <int ROT>
+__device__ __forceinline__ void rotate(float (&x)[4], int j) {
+#pragma clang fp contract(off)
+    if (ROT == 128) {
+        const uint32_t w = j < 8 ? 0x1035997bu : j < 16 ? 0x8087f5eeu : j < 24 ? 0xee2e4e1au : 0x71132418u;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t flip = ((w >> ((j & 7) * 4 + c)) & 1u) ^ 1u;
+            x[c] = __uint_as_float(__float_as_uint(x[c]) ^ (flip << 31));
+        }
+    }
+    const float a0 = x[0] + x[1], a1 = x[0] - x[1], a2 = x[2] + x[3], a3 = x[2] - x[3];
+    x[0] = (a0 + a2) * 0.5f;
+    x[1] = (a1 + a3) * 0.5f;
+    x[2] = (a0 - a2) * 0.5f;
+    x[3] = (a1 - a3) * 0.5f;
+    if (ROT == 128) {
+        butterfly<1>(x, j);
+        butterfly<2>(x, j);
+        butterfly<4>(x, j);
+        butterfly<8>(x, j);
+        butterfly<16>(x, j);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) x[c] *= 0.1767766952966369f;
+    }
+}
+
+__device__ __forceinline__ void load4(const uint16_t* p, float (&x)[4]) {
+    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+    x[0] = lo_bf16(w[0]);
+    x[1] = hi_bf16(w[0]);
+    x[2] = lo_bf16(w[1]);
+    x[3] = hi_bf16(w[1]);
+}
+
+__device__ __forceinline__ uint32_t pack_s8(const float (&x)[4], float inv) {
+#pragma clang fp contract(off)
+    uint32_t w = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w |= (uint32_t)(rn_sat(x[c] * inv) & 0xff) << (8 * c);
+    return w;
+}
+
+// ------------------------------------------------------------------------------------------------ prep launch 1
+// Blocks x < nvchunk: channel abs-max of V over keys [x * 256, x * 256 + 256) of kv head y -> vpart.
+// Block x == nvchunk: the anchor of kv head y (nine sample keys at i * (Sk - 1) / 8; the sample with the least
+// squared distance to the others is subtracted from every key when that lowers the samples' energy and raises their
+// abs-max by at most 12.5 %), in fp64 like the checker.
+__global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
+#pragma clang fp contract(off)
+    const Plan& p = a.p;
+    const int b = blockIdx.z, hk = blockIdx.y, t = threadIdx.x;
+    if ((int)blockIdx.x < p.nvchunk) {
+        __shared__ float red[16][128];
+        const int cg = t & 15, r0 = t >> 4;
+        float m[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m[j] = 0.0f;
+        const int base = blockIdx.x * VCHUNK;
+        const uint16_t* vb = a.v + b * a.v_sb + hk * a.v_sh + 8 * cg;
+        for (int i = 0; i < VCHUNK / 16; ++i) {
+            const int row = base + r0 + 16 * i;
+            if (row < a.Sk) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(vb + (int64_t)row * a.v_sn);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    m[2 * j] = fmaxf(m[2 * j], fabsf(lo_bf16(w[j])));
+                    m[2 * j + 1] = fmaxf(m[2 * j + 1], fabsf(hi_bf16(w[j])));
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[r0][8 * cg + j] = m[j];
+        __syncthreads();
+        if (t < 128) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, red[r][t]);
+            float* vpart = reinterpret_cast<float*>(a.ws + p.vpart);
+            vpart[((size_t)(b * a.HK + hk) * p.nvchunk + blockIdx.x) * 128 + t] = mx;
+        }
+        return;
+    }
+    // the anchor
+    constexpr int NSAMP = 9;
+    __shared__ double sd[NSAMP + 2][128];
+    double s[NSAMP];
+    const uint16_t* kb = a.k + b * a.k_sb + hk * a.k_sh;
+    if (t < 128) {
+        double e = 0.0, mx = 0.0, sum = 0.0;
+#pragma unroll
+        for (int i = 0; i < NSAMP; ++i) {
+            const int row = (int)((int64_t)i * (a.Sk - 1) / (NSAMP - 1));
+            s[i] = (double)bf16_bits_to_f32(kb[(int64_t)row * a.k_sn + t]);
+            e += s[i] * s[i];
+            mx = fmax(mx, fabs(s[i]));
+            sum += s[i];
+        }
+        sd[0][t] = e;
+        sd[1][t] = mx;
+#pragma unroll
+        for (int j = 0; j < NSAMP; ++j) {
+            const double d = NSAMP * s[j] - sum;
+            sd[2 + j][t] = d * d;
+        }
+    }
+    __syncthreads();
+    for (int st = 64; st > 0; st >>= 1) {
+        if (t < st) {
+            sd[1][t] = fmax(sd[1][t], sd[1][t + st]);
+            sd[0][t] += sd[0][t + st];
+#pragma unroll
+            for (int j = 0; j < NSAMP; ++j) sd[2 + j][t] += sd[2 + j][t + st];
+        }
+        __syncthreads();
+    }
+    const double orig_e = sd[0][0], orig_m = sd[1][0];
+    int best = 0;
+    for (int j = 1; j < NSAMP; ++j)
+        if (sd[2 + j][0] < sd[2 + best][0]) best = j;
+    __syncthreads();
+    if (t < 128) {
+        double be = 0.0, bm = 0.0;
+#pragma unroll
+        for (int i = 0; i < NSAMP; ++i) {
+            const double r = s[i] - s[best];
+            be += r * r;
+            bm = fmax(bm, fabs(r));
+        }
+        sd[0][t] = be;
+        sd[1][t] = bm;
+    }
+    __syncthreads();
+    for (int st = 64; st > 0; st >>= 1) {
+        if (t < st) {
+            sd[0][t] += sd[0][t + st];
+            sd[1][t] = fmax(sd[1][t], sd[1][t + st]);
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        const bool improves = sd[0][0] < orig_e && sd[1][0] <= orig_m * 1.125;
+        reinterpret_cast<int*>(a.ws + p.anchor)[b * a.HK + hk] =
+            improves ? (int)((int64_t)best * (a.Sk - 1) / (NSAMP - 1)) : -1;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ prep launch 2
+// Q: 16 rows of head h per block; each 32-lane half holds one row (4 channels per lane), one scale per row.
+template <int ROT>
+__device__ void quant_q(const PrepArgs& a, int b, int h, int qb) {
+#pragma clang fp contract(off)
+    const Plan& p = a.p;
+    const int t = threadIdx.x, slot = t >> 5, j = t & 31;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int row = qb * 16 + slot + 8 * i;
+        const bool ok = row < a.Sq;
+        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (ok) load4(a.q + b * a.q_sb + h * a.q_sh + (int64_t)row * a.q_sn + 4 * j, x);
+        rotate<ROT>(x, j);
+        const float mx = max32(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
+        const float sc = mx / 127.0f + 1e-7f;
+        const float inv = 1.0f / sc;
+        if (ok) {
+            const size_t r = (size_t)(b * a.H + h) * a.Sq + row;
+            *reinterpret_cast<uint32_t*>(a.ws + p.q8 + r * 128 + 4 * j) = pack_s8(x, inv);
+            if (j == 0) reinterpret_cast<float*>(a.ws + p.qs)[r] = sc;
+        }
+    }
+}
+
+// K: 32 key rows (two scale groups of 16) of kv head hk per block, the anchor row subtracted before the rotation.
+template <int ROT>
+__device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
+#pragma clang fp contract(off)
+    __shared__ float red[2][8];
+    const Plan& p = a.p;
+    const int t = threadIdx.x, slot = t >> 5, j = t & 31;
+    const int anc = reinterpret_cast<const int*>(a.ws + p.anchor)[b * a.HK + hk];
+    const uint16_t* kbase = a.k + b * a.k_sb + hk * a.k_sh + 4 * j;
+    float av[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (anc >= 0) load4(kbase + (int64_t)anc * a.k_sn, av);
+    float x[4][4], m[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = kb * 32 + slot + 8 * i;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (row < a.Sk) {
+            load4(kbase + (int64_t)row * a.k_sn, v);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = v[c] - av[c];
+        }
+        rotate<ROT>(v, j);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) x[i][c] = v[c];
+        m[i] = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    }
+    const float g0 = max32(fmaxf(m[0], m[1])), g1 = max32(fmaxf(m[2], m[3]));
+    if (j == 0) {
+        red[0][slot] = g0;
+        red[1][slot] = g1;
+    }
+    __syncthreads();
+    float mx[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        mx[0] = fmaxf(mx[0], red[0][s]);
+        mx[1] = fmaxf(mx[1], red[1][s]);
+    }
+    float sc[2], inv[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        sc[g] = mx[g] / 127.0f + 1e-7f;
+        inv[g] = 1.0f / sc[g];
+    }
+    uint8_t* k8 = a.ws + p.k8 + (size_t)(b * a.HK + hk) * p.skp * 128;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = kb * 32 + slot + 8 * i;  // rows past Sk are written as zeros
+        *reinterpret_cast<uint32_t*>(k8 + (size_t)row * 128 + 16 * ((j >> 2) ^ k_swz(row & 31)) + 4 * (j & 3)) =
+            pack_s8(x[i], inv[i >> 1]);
+    }
+    if (t == 0 || t == 32) {
+        const int g = t >> 5, grp = kb * 2 + g;  // keys 16 grp .. + 15
+        const int tile = grp * KGROUP / p.cta, local = grp * KGROUP - tile * p.cta;
+        const int blk = local >> 5, half = (local >> 4) & 1;
+        float* ks = reinterpret_cast<float*>(a.ws + p.aux + ((size_t)(b * a.HK + hk) * p.ntiles + tile) * AUX_BYTES +
+                                             AUX_KS_OFF);
+        ks[half * (p.cta / 32) + blk] = grp * KGROUP < a.Sk ? sc[g] : 1.0f;
+    }
+}
+
+// V: one tile of cta keys of kv head hk per block: per-channel scales from the abs-max partials, int8, transposed into
+// [128 dims][cta keys], column sums per half tile into the aux block, then stored swizzled.
+__device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
+#pragma clang fp contract(off)
+    __shared__ float inv_s[128];
+    __shared__ __attribute__((aligned(16))) uint8_t vts[128 * 128];
+    const Plan& p = a.p;
+    const int cta = p.cta, t = threadIdx.x;
+    const size_t bhk = (size_t)b * a.HK + hk;
+    if (t < 128) {
+        const float* vpart = reinterpret_cast<const float*>(a.ws + p.vpart) + bhk * p.nvchunk * 128;
+        float mx = 0.0f;
+        for (int c = 0; c < p.nvchunk; ++c) mx = fmaxf(mx, vpart[c * 128 + t]);
+        const float sc = fmaxf(mx * (1.0f / 127.0f), 1e-12f);
+        inv_s[t] = 1.0f / sc;
+        if (tile == 0) reinterpret_cast<float*>(a.ws + p.vs)[bhk * 128 + t] = sc;
+    }
+    __syncthreads();
+    const int cq = t & 31, k0 = t >> 5;
+    float inv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) inv[c] = inv_s[4 * cq + c];
+    const uint16_t* vb = a.v + b * a.v_sb + hk * a.v_sh + 4 * cq;
+    for (int i = 0; i < cta / 32; ++i) {
+        const int kq = k0 + 8 * i;  // keys 4 kq .. 4 kq + 3 of the tile
+        uint32_t col[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = tile * cta + 4 * kq + r;
+            if (key < a.Sk) {
+                float x[4];
+                load4(vb + (int64_t)key * a.v_sn, x);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) col[c] |= (uint32_t)(rn_sat(x[c] * inv[c]) & 0xff) << (8 * r);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) *reinterpret_cast<uint32_t*>(vts + (4 * cq + c) * cta + 4 * kq) = col[c];
+    }
+    __syncthreads();
+    uint8_t* aux = a.ws + p.aux + (bhk * p.ntiles + tile) * AUX_BYTES;
+    {
+        const int d = t & 127, half = t >> 7;
+        int s = 0;
+        for (int w = 0; w < cta / 8; ++w)
+            s = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(vts + d * cta + half * (cta / 2) + 4 * w),
+                                       0x01010101, s, false);
+        reinterpret_cast<int16_t*>(aux)[(half * 32 + (d & 31)) * 4 + (d >> 5)] = (int16_t)s;
+    }
+    uint8_t* vt = a.ws + p.vt + (bhk * p.ntiles + tile) * (size_t)(128 * cta);
+    const int cpr = cta / 16;  // chunks per dim row
+    for (int idx = t; idx < 128 * cpr; idx += 256) {
+        const int d = idx / cpr, c = idx - d * cpr;
+        *reinterpret_cast<u32x4*>(vt + d * cta + 16 * (c ^ v_swz(d, cta))) =
+            *reinterpret_cast<const u32x4*>(vts + d * cta + 16 * c);
+    }
+}
+
+// grid (ceil(Sq/16) + skp/32 + ntiles, max(H, HK), B): Q blocks, then K blocks, then V tiles.
+template <int ROT>
+__global__ __launch_bounds__(256) void i8_quant_kernel(PrepArgs a) {
+    const int b = blockIdx.z, y = blockIdx.y;
+    const int nqb = (a.Sq + 15) / 16, nkb = a.p.skp / 32;
+    int x = blockIdx.x;
+    if (x < nqb) {
+        if (y < a.H) quant_q<ROT>(a, b, y, x);
+        return;
+    }
+    x -= nqb;
+    if (x < nkb) {
+        if (y < a.HK) quant_k<ROT>(a, b, y, x);
+        return;
+    }
+    x -= nkb;
+    if (y < a.HK) quant_v(a, b, y, x);
+}
+
+// ------------------------------------------------------------------------------------------------ attention
+#define LR_I8_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+
+// One 16-byte-per-lane direct load, global -> LDS: lane l's 16 bytes land at LDS byte address lds + 16 * l.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Key (within a 32-key block) held by MFMA row m: bits (b4 b3 b2 b1 b0) -> (b2 b4 b3 b1 b0), so that score register
+// r of lane half h is key 16 h + r.
+__device__ __forceinline__ int key_perm(int m) {
+    return (m & 3) | (((m >> 3) & 1) << 2) | (((m >> 4) & 1) << 3) | (((m >> 2) & 1) << 4);
+}
+
+template <typename T>
+__device__ __forceinline__ T lds_load(const uint8_t* p) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) T*>(
+        (__attribute__((address_space(3))) const uint8_t*)p);
+}
+
+// Wait until the loads of every tile up to `upto` have landed, given that the loads of tiles up to `issued` are in
+// flight; each tile is LPT loads of this wave (compile-time counts for s_waitcnt).
+template <int NS, int LPT>
+__device__ __forceinline__ void wait_tiles(int ahead) {
+    static_assert(NS >= 2 && NS <= 4, "2- to 4-stage ring");
+    if (NS >= 4 && ahead >= 2) {
+        LR_I8_WAIT_VMCNT((NS >= 4 ? 2 : 0) * LPT);
+    } else if (NS >= 3 && ahead >= 1) {
+        LR_I8_WAIT_VMCNT((NS >= 3 ? 1 : 0) * LPT);
+    } else {
+        LR_I8_WAIT_VMCNT(0);
+    }
+}
+
+template <int CTA, int NS>
+__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void i8_attn_kernel(AttnArgs a) {
+    constexpr int NB = CTA / 32;                   // 32-key blocks per tile
+    constexpr int TB = CTA * 128;                  // bytes of a K (or V^T) tile
+    constexpr int STAGE = 2 * TB + AUX_BYTES;
+    constexpr int NW = 8;                          // waves per workgroup, 32 queries each
+    constexpr int KVL = TB / 1024 / NW;            // 1 KB direct loads per wave per K (or V^T) tile
+    static_assert(KVL >= 1, "every wave loads");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
+
+    const Plan& p = a.p;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 31, hf = lane >> 5;
+
+    // XCD-aware order: consecutive logical blocks (same head) land on the same XCD and share its L2
+    const int nwg = gridDim.x, bx = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = bx & 7, idx = bx >> 3;
+    const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int nqb = (a.Sq + 255) / 256;
+    const int qblk = logical % nqb, bh = logical / nqb;
+    const int head = bh % a.H, b = bh / a.H;
+    const int hk = head / a.G;
+    const size_t bhk = (size_t)b * a.HK + hk;
+
+    const uint8_t* k8 = a.ws + p.k8 + bhk * p.skp * 128;
+    const uint8_t* vt = a.ws + p.vt + bhk * p.skp * 128;
+    const uint8_t* aux = a.ws + p.aux + bhk * p.ntiles * AUX_BYTES;
+    const int ntiles = p.ntiles;
+
+    // queries: B operand fragments (dims 32 s + 16 hf .. + 15) and the row scale
+    const int q = qblk * 256 + wave * 32 + n;
+    const bool qok = q < a.Sq;
+    const size_t qr = (size_t)(b * a.H + head) * a.Sq + (qok ? q : a.Sq - 1);
+    i32x4 Qf[4];
+    {
+        const uint8_t* src = a.ws + p.q8 + qr * 128 + 16 * hf;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) Qf[s] = qok ? *reinterpret_cast<const i32x4*>(src + 32 * s) : i32x4{0, 0, 0, 0};
+    }
+    const float cq = (qok ? reinterpret_cast<const float*>(a.ws + p.qs)[qr] : 1.0f) * a.c;
+
+    auto issue = [&](int t) {
+        uint8_t* st = ring + (t % NS) * STAGE;
+#pragma unroll
+        for (int i = 0; i < KVL; ++i) {
+            const int blk = wave * KVL + i;
+            dma16(k8 + (size_t)t * TB + blk * 1024 + lane * 16, lds_addr(st + blk * 1024));
+            dma16(vt + (size_t)t * TB + blk * 1024 + lane * 16, lds_addr(st + TB + blk * 1024));
+        }
+        if (wave == 0) dma16(aux + (size_t)t * AUX_BYTES + lane * 16, lds_addr(st + 2 * TB));
+    };
+
+    f32x16 O[4];
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) O[bb][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t)
+        if (t < ntiles) issue(t);
+    LR_I8_WAIT_VMCNT(0);
+    block_barrier();
+
+    const int tail = a.Sk - (ntiles - 1) * CTA;  // valid keys of the last tile
+    for (int t = 0; t < ntiles; ++t) {
+        if (t + NS - 1 < ntiles) issue(t + NS - 1);
+        const uint8_t* st = ring + (t % NS) * STAGE;
+
+        // S^T = K Q^T, 32 keys per block
+        i32x16 S[NB];
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            const int row = 32 * kb + key_perm(n);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) S[kb][r] = 0;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const i32x4 A = lds_load<i32x4>(st + row * 128 + 16 * ((2 * s + hf) ^ k_swz(row & 31)));
+                S[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Qf[s], S[kb], 0, 0, 0);
+            }
+        }
+        const i16x4 cs = lds_load<i16x4>(st + 2 * TB + 8 * lane);
+        float cc[NB];
+        {
+            const uint8_t* ksp = st + 2 * TB + AUX_KS_OFF + 4 * NB * hf;
+#pragma unroll
+            for (int kb = 0; kb < NB; ++kb) cc[kb] = cq * lds_load<float>(ksp + 4 * kb);
+        }
+        const bool last = t == ntiles - 1 && tail < CTA;
+        if (last) {
+#pragma unroll
+            for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (32 * kb + 16 * hf + r >= tail) S[kb][r] = INT_MIN;
+        }
+
+        // tile max (log2 domain, minus log2(255)), running max, the two scales
+        float tmx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            int mi = S[kb][0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mi = max(mi, S[kb][r]);
+            tmx = fmaxf(tmx, (float)mi * cc[kb]);
+        }
+        tmx = pair_max(tmx) - S_U8_OFFSET;
+        const float m_new = fmaxf(m_run, tmx);
+        const float os = __builtin_amdgcn_exp2f(m_run - m_new);
+        const float ts = __builtin_amdgcn_exp2f(tmx - m_new);
+        m_run = m_new;
+
+        // P = exp2(s c - tmx) as u8, its row sum, then P - 128 as the signed B operand
+        uint32_t P[NB][4];
+        uint32_t rs = 0;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = __builtin_amdgcn_exp2f(fmaf((float)S[kb][4 * qd + i], cc[kb], -tmx));
+                    w = __builtin_amdgcn_cvt_pk_u8_f32(e, i, w);
+                }
+                if (last) {
+                    uint32_t keep = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (32 * kb + 16 * hf + 4 * qd + i < tail) keep |= 0xffu << (8 * i);
+                    w &= keep;
+                }
+                rs = __builtin_amdgcn_udot4(w, 0x01010101u, rs, false);
+                P[kb][qd] = w ^ 0x80808080u;
+            }
+        l_run = l_run * os + ts * (float)rs;
+        if (__builtin_amdgcn_ballot_w64(os != 1.0f) != 0) {
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) O[bb][r] *= os;
+        }
+
+        // O^T += V^T P^T (int32 per tile), scaled into fp32, plus the column-sum correction
+        const float w128 = 128.0f * ts;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            const int d = 32 * bb + n;
+            i32x16 acc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] = 0;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const i32x4 A = lds_load<i32x4>(st + TB + d * CTA + 16 * ((2 * j + hf) ^ v_swz(d, CTA)));
+                const i32x4 B = {(int)P[j][0], (int)P[j][1], (int)P[j][2], (int)P[j][3]};
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) O[bb][r] = fmaf((float)acc[r], ts, O[bb][r]);
+            O[bb] = __builtin_amdgcn_mfma_f32_32x32x2f32((float)cs[bb], w128, O[bb], 0, 0, 0);
+        }
+
+        if (t + 1 < ntiles) {
+            const int ahead = min(ntiles - 1, t + NS - 1) - (t + 1);  // tiles in flight beyond t + 1
+            if (wave == 0)
+                wait_tiles<NS, 2 * KVL + 1>(ahead);
+            else
+                wait_tiles<NS, 2 * KVL>(ahead);
+        }
+        block_barrier();
+    }
+
+    if (!qok) return;
+    const float inv = 1.0f / pair_sum(l_run);
+    const float* vs = reinterpret_cast<const float*>(a.ws + p.vs) + bhk * 128;
+    uint16_t* orow = a.out + b * a.o_sb + head * a.o_sh + (int64_t)q * a.o_sn;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 32 * bb + 8 * g + 4 * hf;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(vs + d0);
+            u32x2 w;
+            w[0] = pack_bf16x2(O[bb][4 * g] * inv * v[0], O[bb][4 * g + 1] * inv * v[1]);
+            w[1] = pack_bf16x2(O[bb][4 * g + 2] * inv * v[2], O[bb][4 * g + 3] * inv * v[3]);
+            *reinterpret_cast<u32x2*>(orow + d0) = w;
+        }
+}
+
+}  // namespace
+
+hipError_t launch_prep(const PrepArgs& a, hipStream_t stream) {
+    const Plan& p = a.p;
+    hipLaunchKernelGGL(i8_stats_kernel, dim3(p.nvchunk + 1, a.HK, a.B), dim3(256), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 grid((a.Sq + 15) / 16 + p.skp / 32 + p.ntiles, a.H > a.HK ? a.H : a.HK, a.B);
+    if (p.rot == 4)
+        hipLaunchKernelGGL(i8_quant_kernel<4>, grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(i8_quant_kernel<128>, grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
+    const int nqb = (a.Sq + 255) / 256;
+    const dim3 grid((unsigned)((int64_t)nqb * a.H * a.B));
+    if (a.p.cta == 128)
+        hipLaunchKernelGGL((i8_attn_kernel<128, 3>), grid, dim3(512), 0, stream, a);
+    else
+        hipLaunchKernelGGL((i8_attn_kernel<64, 3>), grid, dim3(512), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace i8
+}  // namespace lr

@@ -7,6 +7,7 @@
 
 #include "../../include/lr_attn.h"
 #include "lr_common.h"
+#include "lr_int8.h"
 #include "lr_kernels.h"
 
 namespace {
@@ -192,6 +193,69 @@ int rope_impl(const void* src, int64_t src_rs, int64_t src_off, void* dst, int64
     return 0;
 }
 
+// ------------------------------------------------------------------------------------------------ INT8 chain
+// The checks of kitchen_int8_attention_impl (kernels/cuda/minimax/kitchen_launch.cu:199-214): sizes, head dim,
+// H % HK, 16-byte aligned bases and strides (a stride whose extent is 1 is never used), a 256-byte aligned workspace.
+bool i8_sizes_ok(int B, int H, int HK, int Sq, int Sk, int D) {
+    if (B < 1 || H < 1 || HK < 1 || Sq < 1 || Sk < 1 || D != lr::D || H % HK != 0) return false;
+    if (B > 65535 || H > 65535 || Sq > INT_MAX - 512 || Sk > INT_MAX - 512) return false;
+    return (int64_t)((Sq + 255) / 256) * H * B <= INT_MAX;
+}
+
+bool i8_tensor_ok(const void* p, int64_t sb, int64_t sh, int64_t sn, int nb, int nh, int nn) {
+    auto ok = [](int64_t s, int extent) { return extent < 2 || (s >= 0 && s % 8 == 0); };
+    return p && aligned(p, 16) && ok(sb, nb) && ok(sh, nh) && ok(sn, nn);
+}
+
+int i8_prep_impl(const void* q, const void* k, const void* v, void* ws, int B, int H, int HK, int Sq, int Sk, int D,
+                 int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn, int64_t v_sb,
+                 int64_t v_sh, int64_t v_sn, hipStream_t stream) {
+    if (!i8_sizes_ok(B, H, HK, Sq, Sk, D) || !ws || !aligned(ws, 256)) return ERR_ARGS;
+    if (!i8_tensor_ok(q, q_sb, q_sh, q_sn, B, H, Sq) || !i8_tensor_ok(k, k_sb, k_sh, k_sn, B, HK, Sk) ||
+        !i8_tensor_ok(v, v_sb, v_sh, v_sn, B, HK, Sk))
+        return ERR_ARGS;
+    lr::i8::PrepArgs a{};
+    a.q = static_cast<const uint16_t*>(q);
+    a.k = static_cast<const uint16_t*>(k);
+    a.v = static_cast<const uint16_t*>(v);
+    a.q_sb = q_sb; a.q_sh = q_sh; a.q_sn = q_sn;
+    a.k_sb = k_sb; a.k_sh = k_sh; a.k_sn = k_sn;
+    a.v_sb = v_sb; a.v_sh = v_sh; a.v_sn = v_sn;
+    a.B = B; a.H = H; a.HK = HK; a.Sq = Sq; a.Sk = Sk;
+    a.ws = static_cast<uint8_t*>(ws);
+    a.p = lr::i8::plan_of(B, H, HK, Sq, Sk);
+    return (int)lr::i8::launch_prep(a, stream);
+}
+
+int i8_kernel_impl(void* out, const void* ws, int B, int H, int HK, int Sq, int Sk, int D, float scale, int o_rows,
+                   hipStream_t stream) {
+    if (!i8_sizes_ok(B, H, HK, Sq, Sk, D) || !ws || !aligned(ws, 256) || !out || !aligned(out, 16)) return ERR_ARGS;
+    if (!scale_ok(scale) || (o_rows != 0 && o_rows != 1) || (o_rows && B != 1)) return ERR_ARGS;
+    lr::i8::AttnArgs a{};
+    a.ws = static_cast<const uint8_t*>(ws);
+    a.out = static_cast<uint16_t*>(out);
+    a.o_sb = (int64_t)H * Sq * lr::D;
+    a.o_sh = o_rows ? lr::D : (int64_t)Sq * lr::D;
+    a.o_sn = o_rows ? (int64_t)H * lr::D : lr::D;
+    a.B = B; a.H = H; a.HK = HK; a.G = H / HK; a.Sq = Sq; a.Sk = Sk;
+    a.c = scale * 1.4426950408889634f;
+    a.p = lr::i8::plan_of(B, H, HK, Sq, Sk);
+    return (int)lr::i8::launch_attention(a, stream);
+}
+
+int i8_attention_impl(const void* q, const void* k, const void* v, void* out, void* ws, int B, int H, int HK, int Sq,
+                      int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
+                      int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, float scale, int o_rows,
+                      hipStream_t stream) {
+    // every argument is checked before the first launch
+    if (!i8_sizes_ok(B, H, HK, Sq, Sk, D) || !out || !aligned(out, 16) || !scale_ok(scale) || (o_rows && B != 1))
+        return ERR_ARGS;
+    const int e = i8_prep_impl(q, k, v, ws, B, H, HK, Sq, Sk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn,
+                               stream);
+    if (e != 0) return e;
+    return i8_kernel_impl(out, ws, B, H, HK, Sq, Sk, D, scale, o_rows, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -289,6 +353,38 @@ int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void
     return fused_impl(q_raw, k_raw, v, out, q_norm_w, k_norm_w, table_kind, q_table_a, q_table_b, k_table_a, k_table_b,
                       table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale, q_row_stride,
                       k_row_stride, v_row_stride, out_row_stride, n_pre, workspace, workspace_bytes, config, stream);
+}
+
+size_t lr_int8_attention_workspace_bytes(int B, int H, int HK, int Sq, int Sk, int D) {
+    if (!i8_sizes_ok(B, H, HK, Sq, Sk, D)) return 0;
+    return lr::i8::plan_of(B, H, HK, Sq, Sk).total;
+}
+
+int lr_int8_attention(const void* q, const void* k, const void* v, void* out, void* workspace, int B, int H, int HK,
+                      int Sq, int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
+                      int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, float scale, lr_stream_t stream) {
+    return i8_attention_impl(q, k, v, out, workspace, B, H, HK, Sq, Sk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb,
+                             v_sh, v_sn, scale, 0, stream);
+}
+
+int lr_int8_attention_rows(const void* q, const void* k, const void* v, void* out, void* workspace, int B, int H,
+                           int HK, int Sq, int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb,
+                           int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, float scale,
+                           lr_stream_t stream) {
+    return i8_attention_impl(q, k, v, out, workspace, B, H, HK, Sq, Sk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb,
+                             v_sh, v_sn, scale, 1, stream);
+}
+
+int lr_int8_attention_prep(const void* q, const void* k, const void* v, void* workspace, int B, int H, int HK, int Sq,
+                           int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
+                           int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, lr_stream_t stream) {
+    return i8_prep_impl(q, k, v, workspace, B, H, HK, Sq, Sk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn,
+                        stream);
+}
+
+int lr_int8_attention_kernel(void* out, const void* workspace, int B, int H, int HK, int Sq, int Sk, int D,
+                             float scale, int o_rows, lr_stream_t stream) {
+    return i8_kernel_impl(out, workspace, B, H, HK, Sq, Sk, D, scale, o_rows, stream);
 }
 
 }  // extern "C"

@@ -83,6 +83,8 @@ def lib() -> ctypes.CDLL:
         L.lro_i8_quant_rows.argtypes = [_P, _I64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P]
         L.lro_i8_quant_v.argtypes = [_P, _I64, ctypes.c_int, _P, _P]
         L.lro_i8_attention.argtypes = [_P, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, _P]
+        L.lro_i8_attention_p8.argtypes = [_P, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, _P]
         _lib = L
     return _lib
 
@@ -315,6 +317,21 @@ def i8_attention(q8, qs, k8, ks, v8, vs, kgroup: int = I8_KGROUP) -> np.ndarray:
     lib().lro_i8_attention(_ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), kgroup, _ptr(v8), _ptr(vs), q8.shape[0],
                            k8.shape[0], _ptr(out))
     return out
+
+
+def i8_attention_p8(q8, qs, k8, ks, v8, vs, cta: int, kgroup: int = I8_KGROUP) -> np.ndarray:
+    """i8_attention with P rounded to u8 against each cta-key tile's row max, as the reference's kernel rounds it."""
+    q8, k8, v8 = (np.ascontiguousarray(a, dtype=np.int8) for a in (q8, k8, v8))
+    qs, ks, vs = (np.ascontiguousarray(a, dtype=np.float32) for a in (qs, ks, vs))
+    out = np.zeros((q8.shape[0], D), np.float32)
+    lib().lro_i8_attention_p8(_ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), kgroup, _ptr(v8), _ptr(vs), q8.shape[0],
+                              k8.shape[0], cta, _ptr(out))
+    return out
+
+
+def i8_cta_for(sk: int) -> int:
+    """Key tile of the P rounding: 128 keys past 1024 keys, else 64 (src/engines/minimax_h3/launch.zig:333)."""
+    return 128 if sk > 1024 else 64
 
 
 def int8_attention(qkv_bits: np.ndarray, heads: int, rows=None) -> tuple[np.ndarray, dict]:

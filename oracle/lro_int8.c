@@ -178,3 +178,45 @@ void lro_i8_attention(const int8_t* q8, const float* qs, const int8_t* k8, const
         for (int c = 0; c < D; ++c) out[(int64_t)i * D + c] = (float)(o[c] / l * vs[c]);
     }
 }
+
+/* The same attention with P rounded the way the reference's kernel rounds it (attn_utils.cuh:610-695): per key tile of
+ * `cta` keys (tiles start at multiples of cta) and per query row, m_t = max_j x_j - 7.9943534 with x_j = s_j * log2(e);
+ * P_j = round(exp2(x_j - m_t)) in [0, 255]; the row sum is taken over the rounded P; tile t enters O and the row sum
+ * with weight exp2(m_t - M), M = max_t m_t. fp64 otherwise. */
+void lro_i8_attention_p8(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, int kgroup,
+                         const int8_t* v8, const float* vs, int W, int nk, int cta, float* out) {
+    union { uint32_t u; float f; } sm;
+    sm.u = 0x3db504f3u;
+    const double log2e = 1.4426950408889634, offset = (double)7.9943534f;
+    const int ntiles = (nk + cta - 1) / cta;
+    double* x = (double*)__builtin_alloca(sizeof(double) * (size_t)nk);
+    double* mt = (double*)__builtin_alloca(sizeof(double) * (size_t)ntiles);
+    for (int i = 0; i < W; ++i) {
+        for (int j = 0; j < nk; ++j) {
+            int64_t dot = 0;
+            for (int c = 0; c < D; ++c) dot += (int64_t)q8[(int64_t)i * D + c] * k8[(int64_t)j * D + c];
+            x[j] = (double)dot * qs[i] * ks[j / kgroup] * (double)sm.f * log2e;
+        }
+        double M = -INFINITY;
+        for (int t = 0; t < ntiles; ++t) {
+            double m = -INFINITY;
+            for (int j = t * cta; j < nk && j < (t + 1) * cta; ++j) m = x[j] > m ? x[j] : m;
+            mt[t] = m - offset;
+            if (mt[t] > M) M = mt[t];
+        }
+        double l = 0.0, o[D] = {0};
+        for (int t = 0; t < ntiles; ++t) {
+            const double w = exp2(mt[t] - M);
+            double lt = 0.0, ot[D] = {0};
+            for (int j = t * cta; j < nk && j < (t + 1) * cta; ++j) {
+                double p = rint(exp2(x[j] - mt[t]));
+                p = p < 0.0 ? 0.0 : p > 255.0 ? 255.0 : p;
+                lt += p;
+                for (int c = 0; c < D; ++c) ot[c] += p * v8[(int64_t)j * D + c];
+            }
+            l += w * lt;
+            for (int c = 0; c < D; ++c) o[c] += w * ot[c];
+        }
+        for (int c = 0; c < D; ++c) out[(int64_t)i * D + c] = (float)(o[c] / l * vs[c]);
+    }
+}

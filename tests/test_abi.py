@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version():
     header = _lib.HEADER.read_text()
     declared = int(re.search(r"#define LR_ATTN_ABI_VERSION (\d+)", header).group(1))
-    assert _lib.load().lr_attn_abi_version() == declared == 2
+    assert _lib.load().lr_attn_abi_version() == declared == 3
 
 
 def test_workspace_bytes():
@@ -139,6 +139,47 @@ def test_rms_rope_rejects():
     assert call(pairing=1, rot=40) == HIP_ERROR_INVALID_VALUE
     assert call(rn=2) == HIP_ERROR_INVALID_VALUE
     assert L.lr_rms_rope_qk_bf16(A, A, 4, 2, 768, 768, None, A, A, 192, 96, 1e-5, None) == HIP_ERROR_INVALID_VALUE
+
+
+def _i8_plan(B, H, HK, Sq, Sk):
+    """The INT8 workspace layout, restated: parts in order, each starting on a 256-byte boundary."""
+    cta = 128 if Sk > 1024 else 64
+    nt = -(-Sk // cta)
+    skp, nvc = nt * cta, -(-Sk // 256)
+    parts = [B * H * Sq * 128, B * HK * skp * 128, B * HK * skp * 128, B * HK * nt * 1024, B * H * Sq * 4,
+             B * HK * 128 * 4, B * HK * nvc * 128 * 4, B * HK * 4]
+    return sum(-(-p // 256) * 256 for p in parts)
+
+
+def test_int8_workspace_bytes():
+    L = _lib.load()
+    for args in ((1, 56, 56, 5967, 5967), (1, 2, 2, 80, 80), (2, 4, 2, 300, 1100), (1, 3, 1, 1, 1), (1, 2, 2, 1024, 1024),
+                 (1, 2, 2, 1025, 1025)):
+        assert L.lr_int8_attention_workspace_bytes(*args, 128) == _i8_plan(*args), args
+    assert L.lr_int8_attention_workspace_bytes(1, 2, 2, 8, 8, 64) == 0       # head dim 64 is not built
+    assert L.lr_int8_attention_workspace_bytes(1, 3, 2, 8, 8, 128) == 0      # H % HK
+    assert L.lr_int8_attention_workspace_bytes(0, 2, 2, 8, 8, 128) == 0
+
+
+def test_int8_rejects():
+    L = _lib.load()
+    ok = dict(q=A, k=A, v=A, o=A, ws=0x100000, B=1, H=2, HK=2, Sq=8, Sk=8, D=128, q_sb=0, q_sh=768, q_sn=768 * 2,
+              k_sb=0, k_sh=768, k_sn=768 * 2, v_sb=0, v_sh=768, v_sn=768 * 2, scale=0.088, stream=None)
+
+    def call(fn="lr_int8_attention", **kw):
+        a = dict(ok)
+        a.update(kw)
+        return getattr(L, fn)(*a.values())
+
+    for kw, why in ((dict(D=64), "head dim"), (dict(H=3), "H % HK"), (dict(q=A + 8), "misaligned q"),
+                    (dict(k_sn=100), "stride not a multiple of 8"), (dict(ws=A + 16), "workspace alignment"),
+                    (dict(ws=0), "no workspace"), (dict(scale=0.0), "scale"), (dict(Sk=0), "empty"),
+                    (dict(o=A + 2), "misaligned out")):
+        assert call(**kw) == HIP_ERROR_INVALID_VALUE, why
+    assert call("lr_int8_attention_rows", B=2, q_sb=8 * 768) == HIP_ERROR_INVALID_VALUE  # rows: B 1 only
+    assert L.lr_int8_attention_kernel(A, 0x100000, 1, 2, 2, 8, 8, 128, 0.088, 2, None) == HIP_ERROR_INVALID_VALUE
+    assert L.lr_int8_attention_prep(A, A, A, A + 64, 1, 2, 2, 8, 8, 128, 0, 768, 1536, 0, 768, 1536, 0, 768, 1536,
+                                    None) == HIP_ERROR_INVALID_VALUE
 
 
 def test_ops_has_no_cpu_path():

@@ -1,0 +1,230 @@
+"""GPU parity of the INT8 attention chain (MiniMax H3's quantised attention) against the CPU oracle (oracle/lro_int8.c),
+through the C ABI.
+
+  * the prep is bit-exact: anchor row, int8 Q / K / V, every scale, the per-tile column sums;
+  * the attention is checked three ways: against the oracle's emulation of the reference's u8 P rounding (tight: the
+    only differences are fp32 vs fp64 exponent arithmetic and the bf16 output rounding), against fp64 attention over
+    the same quantised operands, and against exact attention of the bf16 inputs at the BASELINE bar (2e-2 / 2e-3);
+  * the rows output equals the [H, S, D] output transposed, bit for bit; the one-call entry point equals prep + kernel.
+Cases follow the reference's own gate (tools/twin/stk_twin/h3/test_kitchen.py:22-100): packed qkv views, S on both
+sides of the H4 / H128 switch (256) and of the 64 / 128 key tile switch (1024), a biased K that makes the anchor fire,
+GQA and batches, and H3's shape (5,967 tokens x 56 heads).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import MAX_ABS, MEAN_ABS, bf16_f32, from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from localrouter_amd import ops  # noqa: E402
+
+
+# ------------------------------------------------------------------------------------------ workspace layout, restated
+def _k_swz(r):
+    return ((r >> 2) & 4) | ((((r >> 2) ^ r) & 1) << 1) | ((r >> 1) & 1)
+
+
+def _v_swz(d, cta):
+    return (((d >> 1) & 7) ^ ((d & 1) << 2)) if cta == 128 else (((d >> 1) ^ (d >> 3)) & 3)
+
+
+def _decode(ws: np.ndarray, B, H, HK, Sq, Sk) -> dict:
+    cta = oracle.i8_cta_for(Sk)
+    nt = -(-Sk // cta)
+    skp, nvc = nt * cta, -(-Sk // 256)
+    sizes = [B * H * Sq * 128, B * HK * skp * 128, B * HK * skp * 128, B * HK * nt * 1024, B * H * Sq * 4,
+             B * HK * 128 * 4, B * HK * nvc * 128 * 4, B * HK * 4]
+    off, at = [], 0
+    for s in sizes:
+        off.append(at)
+        at += -(-s // 256) * 256
+    part = lambda i: ws[off[i]:off[i] + sizes[i]]  # noqa: E731
+    r = np.arange(skp)
+    kst = part(1).view(np.int8).reshape(B, HK, skp, 8, 16)
+    kidx = np.arange(8)[None, :] ^ np.array([_k_swz(x & 31) for x in r])[:, None]
+    k8 = np.take_along_axis(kst, kidx[None, None, :, :, None], axis=3).reshape(B, HK, skp, 128)
+    cpr = cta // 16
+    vst = part(2).view(np.int8).reshape(B, HK, nt, 128, cpr, 16)
+    vidx = np.arange(cpr)[None, :] ^ np.array([_v_swz(d, cta) for d in range(128)])[:, None]
+    vt = np.take_along_axis(vst, vidx[None, None, None, :, :, None], axis=4).reshape(B, HK, nt, 128, cta)
+    v8 = vt.transpose(0, 1, 2, 4, 3).reshape(B, HK, skp, 128)
+    aux = part(3).reshape(B, HK, nt, 1024)
+    cs = aux[..., :512].copy().view(np.int16).reshape(B, HK, nt, 2, 32, 4)
+    cs = cs.transpose(0, 1, 2, 3, 5, 4).reshape(B, HK, nt, 2, 128)          # [half][dim]
+    nb = cta // 32
+    ks = aux[..., 512:512 + 8 * nb].copy().view(np.float32).reshape(B, HK, nt, 2, nb)
+    ks = ks.transpose(0, 1, 2, 4, 3).reshape(B, HK, nt * 2 * nb)              # group order 2 kb + half per tile
+    return dict(cta=cta, skp=skp, q8=part(0).view(np.int8).reshape(B, H, Sq, 128),
+                qs=part(4).view(np.float32).reshape(B, H, Sq), k8=k8, ks=ks, v8=v8, cs=cs,
+                vs=part(5).view(np.float32).reshape(B, HK, 128), anchor=part(7).view(np.int32).reshape(B, HK))
+
+
+# ------------------------------------------------------------------------------------------ inputs and the oracle
+def _qkv(seed, S, H, bias_heads=()):
+    """Packed qkv bits [S, 3, H, 128] ~ N(0, 1); heads in bias_heads get a large common key offset (anchor fires)."""
+    qkv = oracle.synth_bf16(seed, 1, (S, 3, H, 128))
+    if bias_heads:
+        f = bf16_f32(qkv)
+        off = 3.0 * bf16_f32(oracle.synth_bf16(seed, 2, (1, 128)))
+        for h in bias_heads:
+            f[:, 1, h] += off[0]
+        qkv = oracle.f32_to_bf16(f)
+    return qkv
+
+
+def _oracle_head(q, k, v, Sk):
+    """The oracle's quantised operands of one (query head, kv head) pair: bf16 bits [Sq,128], [Sk,128], [Sk,128]."""
+    rot = oracle.i8_rotation_for(Sk)
+    a = oracle.i8_anchor(k)
+    q8, qs = oracle.i8_quant_rows(q, rot)
+    k8, ks = oracle.i8_quant_rows(k, rot, a, oracle.I8_KGROUP)
+    v8, vs = oracle.i8_quant_v(v)
+    return dict(anchor=a, q8=q8, qs=qs, k8=k8, ks=ks, v8=v8, vs=vs)
+
+
+def _check_parts(dec, ref, b, h, hk, Sk, what):
+    cta = dec["cta"]
+    assert dec["anchor"][b, hk] == ref["anchor"], f"{what}: anchor"
+    assert np.array_equal(dec["q8"][b, h], ref["q8"]), f"{what}: q8"
+    assert np.array_equal(dec["qs"][b, h].view(np.uint32), ref["qs"].view(np.uint32)), f"{what}: q scales"
+    assert np.array_equal(dec["k8"][b, hk, :Sk], ref["k8"]), f"{what}: k8"
+    assert not dec["k8"][b, hk, Sk:].any(), f"{what}: k8 padding"
+    ng = len(ref["ks"])
+    assert np.array_equal(dec["ks"][b, hk, :ng].view(np.uint32), ref["ks"].view(np.uint32)), f"{what}: k scales"
+    assert np.array_equal(dec["v8"][b, hk, :Sk], ref["v8"]), f"{what}: v8"
+    assert not dec["v8"][b, hk, Sk:].any(), f"{what}: v8 padding"
+    assert np.array_equal(dec["vs"][b, hk].view(np.uint32), ref["vs"].view(np.uint32)), f"{what}: v scales"
+    v8p = np.zeros((dec["skp"], 128), np.int64)
+    v8p[:Sk] = ref["v8"]
+    halves = v8p.reshape(-1, 2, cta // 2, 128).sum(2)
+    assert np.array_equal(dec["cs"][b, hk].astype(np.int64), halves), f"{what}: column sums"
+
+
+def _check_out(got_bits, ref, rows, what):
+    """got: bf16 [Sq_sel, 128] of one head; ref: the oracle's quantised operands of that head."""
+    got = bf16_f32(got_bits).astype(np.float64)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite"
+    args = (ref["q8"][rows], ref["qs"][rows], ref["k8"], ref["ks"], ref["v8"], ref["vs"])
+    emu = oracle.i8_attention_p8(*args, oracle.i8_cta_for(len(ref["k8"]))).astype(np.float64)
+    # the emulation differs only by fp32 exponent arithmetic (a u8 step flips now and then: <= 2 * max|v| / rowsum)
+    # and the bf16 output rounding (<= 2^-9 relative)
+    d = np.abs(got - emu)
+    bound = 2.0 ** -8 * np.abs(emu) + 2e-3
+    assert np.all(d <= bound), f"{what}: vs u8-P emulation max {d.max():.3e} at {np.unravel_index(d.argmax(), d.shape)}"
+    # bf16 rounding alone is <= 2^-9 |x| per element, so its mean is <= 2^-9 mean|x|; flips add little on average
+    assert d.mean() <= 2.0 ** -9 * np.abs(emu).mean() + 5e-5, f"{what}: vs u8-P emulation mean {d.mean():.3e}"
+    exact_q = oracle.i8_attention(*args).astype(np.float64)
+    d2 = np.abs(got - exact_q)
+    assert d2.max() <= MAX_ABS and d2.mean() <= MEAN_ABS, f"{what}: vs fp64 quantised {d2.max():.3e} {d2.mean():.3e}"
+    return d.max(), d.mean(), d2.max(), d2.mean()
+
+
+CASES = [(80, 2, ()), (256, 2, (1,)), (300, 2, (0,)), (1024, 2, ()), (1100, 3, (2,)), (777, 1, (0,))]
+
+
+@pytest.mark.parametrize("S,H,bias", CASES)
+def test_int8_packed_qkv(S, H, bias):
+    """Kitchen.attention on a packed qkv buffer: prep bit-exact, attention within the bars, rows == transpose."""
+    print(f"\n[int8 qkv] S={S} H={H} bias={bias}", flush=True)
+    qkv = _qkv(21, S, H, bias)
+    dq = to_dev(qkv.reshape(S, 3 * H * 128))
+    ws = ops.kitchen_attention_prep(dq, None, H)
+    out = ops.kitchen_attention_kernel(torch.empty((H, S, 128), dtype=torch.bfloat16, device="cuda"), ws, H, S, False)
+    rows = ops.kitchen_attention_kernel(torch.empty((S, H * 128), dtype=torch.bfloat16, device="cuda"), ws, H, S, True)
+    one = ops.kitchen_attention(dq, H)
+    torch.cuda.synchronize()
+    dec = _decode(ws.cpu().numpy(), 1, H, H, S, S)
+    got, got_rows, got_one = from_dev(out), from_dev(rows), from_dev(one)
+    assert np.array_equal(got_rows.reshape(S, H, 128).transpose(1, 0, 2), got), "rows != [H, S, D] transposed"
+    assert np.array_equal(got_one, got), "one call != prep + kernel"
+    qf = bf16_f32(qkv)
+    for h in range(H):
+        ref = _oracle_head(*(np.ascontiguousarray(qkv[:, i, h]) for i in range(3)), S)
+        if h in bias:
+            assert ref["anchor"] >= 0, "the biased head must use its anchor"
+        _check_parts(dec, ref, 0, h, h, S, f"S={S} h={h}")
+        stats = _check_out(got[h], ref, np.arange(S), f"S={S} h={h}")
+        exact = oracle.brute_attention(qf[:, 0, h][:, None], qf[:, 1, h][:, None], qf[:, 2, h][:, None])[:, 0]
+        d = np.abs(bf16_f32(got[h]).astype(np.float64) - exact)
+        print(f"  h={h} anchor={ref['anchor']} emu {stats[0]:.2e}/{stats[1]:.2e} fp64q {stats[2]:.2e}/{stats[3]:.2e} "
+              f"exact {d.max():.2e}/{d.mean():.2e}", flush=True)
+        assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS, f"S={S} h={h}: vs exact {d.max():.3e} {d.mean():.3e}"
+
+
+@pytest.mark.parametrize("B,H,HK,Sq,Sk", [(2, 4, 2, 200, 333), (1, 3, 1, 513, 1500), (2, 2, 2, 1, 70)])
+def test_int8_gqa_batch_cross(B, H, HK, Sq, Sk):
+    """Separate q [B,H,Sq,D] and k, v [B,HK,Sk,D] tensors: GQA (query head h reads kv head h // (H / HK)), batches,
+    Sq != Sk, a single query."""
+    print(f"\n[int8 gqa] B={B} H={H} HK={HK} Sq={Sq} Sk={Sk}", flush=True)
+    q = oracle.synth_bf16(22, 1, (B, H, Sq, 128))
+    k = oracle.synth_bf16(22, 2, (B, HK, Sk, 128))
+    v = oracle.synth_bf16(22, 3, (B, HK, Sk, 128))
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    ws = ops.int8_attention_prep(dq, dk, dv)
+    out = ops.int8_attention_kernel(ws, torch.empty((B, H, Sq, 128), dtype=torch.bfloat16, device="cuda"), batch=B,
+                                    heads=H, kv_heads=HK, sq=Sq, sk=Sk)
+    torch.cuda.synchronize()
+    dec = _decode(ws.cpu().numpy(), B, H, HK, Sq, Sk)
+    got = from_dev(out)
+    G = H // HK
+    for b in range(B):
+        for h in range(H):
+            hk = h // G
+            ref = _oracle_head(q[b, h], k[b, hk], v[b, hk], Sk)
+            _check_parts(dec, ref, b, h, hk, Sk, f"b={b} h={h}")
+            _check_out(got[b, h], ref, np.arange(Sq), f"b={b} h={h}")
+
+
+def test_int8_degenerate_inputs():
+    """Zero query rows (uniform attention), identical keys (the anchor removes everything: all scores 0), constant V
+    channels, on a tail tile: the masked keys past Sk must not enter the row sums."""
+    S, H = 333, 2
+    print(f"\n[int8 degenerate] S={S}", flush=True)
+    qkv = bf16_f32(_qkv(23, S, H))
+    qkv[::7, 0, 0] = 0.0                       # zero query rows
+    qkv[:, 1, 1] = qkv[0, 1, 1][None]          # one key repeated
+    qkv[:, 2, 0, :4] = 1.5                     # constant value channels
+    qkv = oracle.f32_to_bf16(qkv)
+    dq = to_dev(qkv.reshape(S, 3 * H * 128))
+    out = ops.kitchen_attention(dq, H)
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    qf = bf16_f32(qkv)
+    for h in range(H):
+        ref = _oracle_head(*(np.ascontiguousarray(qkv[:, i, h]) for i in range(3)), S)
+        _check_out(got[h], ref, np.arange(S), f"h={h}")
+        exact = oracle.brute_attention(qf[:, 0, h][:, None], qf[:, 1, h][:, None], qf[:, 2, h][:, None])[:, 0]
+        d = np.abs(bf16_f32(got[h]).astype(np.float64) - exact)
+        assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS, f"h={h}: vs exact {d.max():.3e} {d.mean():.3e}"
+    # uniform attention of a zero query row over a repeated-key head: the mean of V exactly as the oracle has it
+    assert np.all(np.isfinite(bf16_f32(got)))
+
+
+def test_int8_h3_shape():
+    """H3's attention: 5,967 tokens x 56 heads from one packed qkv buffer, the [H, S, D] and rows outputs. The oracle
+    checks two heads (every prep part, 96 query rows each, first, last and a spread between)."""
+    S, H = 5967, 56
+    print(f"\n[int8 h3] S={S} H={H}", flush=True)
+    qkv = _qkv(24, S, H, bias_heads=(55,))
+    dq = to_dev(qkv.reshape(S, 3 * H * 128))
+    ws = torch.empty(ops.int8_workspace_bytes(H, S), dtype=torch.uint8, device="cuda")
+    out = ops.kitchen_attention(dq, H, workspace=ws)
+    rows = ops.kitchen_attention(dq, H, workspace=ws, rows=True)
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    assert np.array_equal(from_dev(rows).reshape(S, H, 128).transpose(1, 0, 2), got)
+    dec = _decode(ws.cpu().numpy(), 1, H, H, S, S)
+    sel = np.unique(np.concatenate([np.arange(32), np.linspace(32, S - 33, 32).astype(int), np.arange(S - 32, S)]))
+    for h in (0, 55):
+        ref = _oracle_head(*(np.ascontiguousarray(qkv[:, i, h]) for i in range(3)), S)
+        if h == 55:
+            assert ref["anchor"] >= 0
+        _check_parts(dec, ref, 0, h, h, S, f"h={h}")
+        stats = _check_out(got[h][sel], ref, sel, f"h={h}")
+        print(f"  h={h} emu {stats[0]:.2e}/{stats[1]:.2e} fp64q {stats[2]:.2e}/{stats[3]:.2e}", flush=True)

@@ -139,3 +139,43 @@ def test_chain_close_to_exact_attention():
         exact = oracle.brute_attention(qf[:, 0, h][:, None], qf[:, 1, h][:, None], qf[:, 2, h][:, None])[:, 0]
         d = np.abs(out[h] - exact)
         assert d.max() < 2e-2 and d.mean() < 2e-3, (h, d.max(), d.mean())
+
+
+def _p8_numpy(q8, qs, k8, ks, v8, vs, cta):
+    """Independent restatement of the u8 P rounding: per row and per cta-key tile, P = round(255 * exp(s - max_tile s))
+    (the kernel's exp2(x - max + 7.9943534) with the offset's fp32 value), the row sum over the rounded P, tiles
+    combined with weights exp(max_tile - max_row)."""
+    nk = k8.shape[0]
+    kd = k8.astype(np.float64) * np.repeat(ks.astype(np.float64), 16)[:nk, None]
+    x = (q8.astype(np.float64) * qs[:, None]) @ kd.T * SCALE * np.log2(np.e)
+    off = float(np.float32(7.9943534))
+    num = np.zeros((q8.shape[0], 128))
+    den = np.zeros((q8.shape[0], 1))
+    tiles = [(t, min(t + cta, nk)) for t in range(0, nk, cta)]
+    mt = np.stack([x[:, a:b].max(1) - off for a, b in tiles], 1)
+    M = mt.max(1, keepdims=True)
+    for i, (a, b) in enumerate(tiles):
+        p = np.clip(np.rint(np.exp2(x[:, a:b] - mt[:, i:i + 1])), 0, 255)
+        w = np.exp2(mt[:, i:i + 1] - M)
+        num += w * (p @ v8[a:b].astype(np.float64))
+        den += w * p.sum(1, keepdims=True)
+    return num / den * vs[None].astype(np.float64)
+
+
+def test_p8_rounding_against_numpy():
+    rng = np.random.default_rng(4)
+    for W, nk, cta in ((7, 200, 64), (5, 300, 128), (3, 64, 64), (4, 65, 64)):
+        q8 = rng.integers(-127, 128, (W, 128)).astype(np.int8)
+        k8 = rng.integers(-127, 128, (nk, 128)).astype(np.int8)
+        v8 = rng.integers(-127, 128, (nk, 128)).astype(np.int8)
+        qs = rng.uniform(0.01, 0.05, W).astype(np.float32)
+        ks = rng.uniform(0.01, 0.05, (nk + 15) // 16).astype(np.float32)
+        vs = rng.uniform(0.005, 0.02, 128).astype(np.float32)
+        got = oracle.i8_attention_p8(q8, qs, k8, ks, v8, vs, cta)
+        ref = _p8_numpy(q8, qs, k8, ks, v8, vs, cta)
+        assert np.abs(got - ref).max() < 1e-6, (W, nk, cta)
+        # the rounding is a perturbation of the exact softmax: within a few u8 steps of it, not equal to it
+        exact = oracle.i8_attention(q8, qs, k8, ks, v8, vs)
+        d = np.abs(got - exact)
+        assert 0 < d.max() < 4 * 127 * vs.max() / 255, (W, nk, cta, d.max())
+    assert oracle.i8_cta_for(1024) == 64 and oracle.i8_cta_for(1025) == 128
