@@ -1,7 +1,7 @@
 """Benchmark of the DiT joint-attention hot path on one MI355X (gfx950).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video] [--tile-config C]
-                    [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video|h3-int8]
+                    [--tile-config C] [--no-cpu-baseline]
 
 A step is one fused joint-attention call over one synthetic batch: keys RMSNorm + RoPE into the workspace
 and V packed into transposed 64-key tiles (lr_joint_kv_prepare), followed by the attention kernel with the queries
@@ -13,6 +13,12 @@ Prints ONE JSON line on stdout (everything else goes to stderr). FLOPs per call 
 softmax, RMSNorm and RoPE not counted). `roofline` is the attention kernel alone, timed with HIP events on the stream
 it is launched on, against MI355X's published dense bf16 peak of 2.5 PFLOP/s. `cpu_baseline` times the CPU oracle's
 fp32 flash-style path (OpenMP) on a bounded sample of query rows of the same workload, as a reported baseline only.
+
+--workload h3-int8 measures MiniMax H3's INT8 attention instead (5,967 tokens x 56 heads, the reference's headline
+shape for it): a step is Kitchen.attention on one packed qkv buffer, i.e. the prep (anchor, rotation, int8 Q / K / V,
+lr_int8_attention_prep) then the attention kernel (lr_int8_attention_kernel, rows output). Ops per call = 4 * S^2 *
+128 * H; `roofline` is the attention kernel against MI355X's dense int8 peak of 5.0 POP/s; `cpu_baseline` is the
+CPU oracle of the same chain (prep + fp64 attention over the quantised operands) on a sample of heads and rows.
 """
 from __future__ import annotations
 
@@ -28,6 +34,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_INT8_TOPS = 5000.0
 METRIC = "attention TFLOP/s + % bf16 MFMA peak; ms/call at 4096+512 tokens, 24x128"
 # attention kernel each tile configuration launches for the benchmark's cos/sin table (QK = 1: queries normalised and
 # rotated in registers with that table kind; VT: values read as packed V^T tiles) -- the configurations
@@ -59,9 +66,9 @@ def tables(w):
     return rope.video3d_table(w["n_text"], w["t"], w["gh"], w["gw"])
 
 
-def traffic_from_profile(name: str):
+def traffic_from_profile(name: str, kernel: str = "attn_fwd"):
     """HBM bytes per launch of the attention kernel, from the committed rocprofv3 PMC summary (None if absent)."""
-    p = ROOT / "profiles" / f"attn_fwd_{name}_pmc.md"
+    p = ROOT / "profiles" / f"{kernel}_{name}_pmc.md"
     if not p.exists():
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
@@ -107,7 +114,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS) + ["h3-int8"])
     ap.add_argument("--tile-config", type=int, default=0, choices=sorted(KERNELS),
                     help="LR_ATTN_CFG_* (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -123,6 +130,9 @@ def main():
               "joint attention shards by heads with no exchange, so N GPUs would run this same kernel at H/N heads.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "h3-int8":
+        return bench_int8(args)
 
     import numpy as np
     import torch
@@ -248,6 +258,152 @@ def main():
         result["check"] = {"rows": int(len(cb["rows"])), "max_abs": float(d.max()), "mean_abs": float(d.mean()),
                            "bar": {"max_abs": 2e-2, "mean_abs": 2e-3}}
         log(f"[bench] cpu {cb['value']:.4f} TFLOP/s on {cb['threads']} threads; GPU vs CPU on sampled rows: "
+            f"max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_int8(qkv_bits, S, H, budget_s=10.0):
+    """The oracle's INT8 chain (anchor, rotation, quantisers, fp64 attention over the quantised operands) for a sample
+    of heads and query rows, timed on host cores. Returns ops/s over the sampled rows and the outputs."""
+    import numpy as np
+
+    import oracle
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(0)
+    heads = [0, H // 2, H - 1]
+
+    def run(rows):
+        t0 = time.perf_counter()
+        outs = {}
+        for h in heads:
+            q, k, v = (np.ascontiguousarray(qkv_bits[:, i, h]) for i in range(3))
+            rot = oracle.i8_rotation_for(S)
+            a = oracle.i8_anchor(k)
+            q8, qs = oracle.i8_quant_rows(q[rows], rot)
+            k8, ks = oracle.i8_quant_rows(k, rot, a, oracle.I8_KGROUP)
+            v8, vs = oracle.i8_quant_v(v)
+            outs[h] = oracle.i8_attention(q8, qs, k8, ks, v8, vs)
+        return time.perf_counter() - t0, outs
+
+    ops_row = 4.0 * S * 128 * len(heads)
+    probe = np.sort(rng.choice(S, size=64, replace=False))
+    dt, _ = run(probe)
+    n = int(min(S, max(64, budget_s / 3 * (64 * ops_row / dt) / ops_row)) // 32 * 32)
+    rows = np.sort(rng.choice(S, size=n, replace=False))
+    times, outs, spent = [], None, 0.0
+    while spent < budget_s or len(times) < 3:
+        dt, outs = run(rows)
+        times.append(dt)
+        spent += dt
+    dt = float(np.median(times))
+    return dict(value=n * ops_row / dt / 1e12, threads=threads, rows=rows, heads=heads, outs=outs, seconds=dt,
+                runs=len(times))
+
+
+def bench_int8(args):
+    import numpy as np
+    import torch
+
+    from localrouter_amd import _lib, ops
+
+    S, H = 5967, 56
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    L = _lib.load()
+    rc = L.lr_attn_init()
+    if rc != 0:
+        raise SystemExit(f"lr_attn_init: {rc} (not a gfx950?)")
+    log(f"[bench] workload h3-int8: S={S} H={H}, packed qkv [S, 3*H*128]")
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    qkv = torch.randn((S, 3 * H * 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    out = torch.empty((S, H * 128), dtype=torch.bfloat16, device=dev)
+    ws_bytes = ops.int8_workspace_bytes(H, S)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    row = 3 * H * 128
+    q_ptr, k_ptr, v_ptr = (qkv.data_ptr() + i * H * 128 * 2 for i in range(3))
+    strides = (S * row, 128, row)
+
+    def prep():
+        _lib.call("lr_int8_attention_prep", q_ptr, k_ptr, v_ptr, ws.data_ptr(), 1, H, H, S, S, 128, *strides, *strides,
+                  *strides, sh)
+
+    def attn():
+        _lib.call("lr_int8_attention_kernel", out.data_ptr(), ws.data_ptr(), 1, H, H, S, S, 128, ops.SCALE_128, 1, sh)
+
+    for _ in range(args.warmup):
+        prep()
+        attn()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
+    K = args.steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    for i in range(K):
+        ev[2 * i].record(stream)
+        prep()
+        ev[2 * i + 1].record(stream)
+        attn()
+    ev[2 * K].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    t_prep = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(K)]
+    t_attn = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(K)]
+    ms_step = ev[0].elapsed_time(ev[2 * K]) / K
+    ops_call = 4.0 * S * S * 128 * H
+    attn_ms, prep_ms = float(np.mean(t_attn)), float(np.mean(t_prep))
+    value = ops_call / (ms_step * 1e-3) / 1e12
+    achieved = ops_call / (attn_ms * 1e-3) / 1e12
+    log(f"[bench] step {ms_step:.4f} ms (prep {prep_ms:.4f} ms, attention {attn_ms:.4f} ms, median "
+        f"{float(np.median(t_attn)):.4f} ms); {value:.1f} TOP/s step, {achieved:.1f} TOP/s attention kernel "
+        f"({100 * achieved / PEAK_INT8_TOPS:.1f}% of int8 peak); wall {wall:.3f} s")
+    result = {
+        "metric": "int8 attention TOP/s + % int8 MFMA peak; ms/call at 5967 tokens, 56x128 (MiniMax H3)",
+        "value": round(value, 2),
+        "unit": "TOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "h3-int8-attention", "batch": 1, "tokens": S, "heads": H, "head_dim": 128,
+                   "causal": False, "input": "packed qkv [S, 3*H*128] bf16 ~ N(0,1)", "output": "rows [S, H*128]",
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profile("h3-int8", "i8_attn"),
+                     "kernel": "i8_attn_kernel<128, 3>", "kernel_ms": round(attn_ms, 5)},
+        "kernels_ms": {"prep": round(prep_ms, 5), "attention": round(attn_ms, 5)},
+        "ops_per_call": ops_call,
+    }
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline (oracle INT8 chain, sampled heads and query rows) ...")
+        qb = qkv.cpu().view(torch.int16).numpy().view(np.uint16).reshape(S, 3, H, 128)
+        cb = cpu_baseline_int8(qb, S, H)
+        got = out.cpu().view(torch.int16).numpy().view(np.uint16).reshape(S, H, 128)
+        d = np.concatenate([np.abs(((got[cb["rows"], h].astype(np.uint32) << 16).view(np.float32)).astype(np.float64)
+                                   - cb["outs"][h]).ravel() for h in cb["heads"]])
+        result["cpu_baseline"] = {"value": round(cb["value"], 4), "unit": "TOP/s", "cores": cb["threads"],
+                                  "kind": "port",
+                                  "sample": f"{len(cb['rows'])} of {S} query rows x heads {cb['heads']} over all {S} "
+                                            f"keys (anchor + quantisers + fp64 attention): median of {cb['runs']} runs, "
+                                            f"{cb['seconds']:.2f} s each"}
+        result["check"] = {"rows": int(len(cb["rows"])), "heads": cb["heads"], "max_abs": float(d.max()),
+                           "mean_abs": float(d.mean()), "bar": {"max_abs": 2e-2, "mean_abs": 2e-3}}
+        log(f"[bench] cpu {cb['value']:.4f} TOP/s on {cb['threads']} threads; GPU vs CPU on sampled rows: "
             f"max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
     print(json.dumps(result), flush=True)
 

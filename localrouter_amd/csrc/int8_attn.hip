@@ -22,6 +22,8 @@
 #include <limits.h>
 #include <math.h>
 
+#include <type_traits>
+
 #include "lr_common.h"
 #include "lr_int8.h"
 
@@ -254,16 +256,20 @@ __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
     const uint16_t* kbase = a.k + b * a.k_sb + hk * a.k_sh + 4 * j;
     float av[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (anc >= 0) load4(kbase + (int64_t)anc * a.k_sn, av);
+    // Rows past Sk (the last tile's padding) repeat real keys: those of the last key's scale group gL, key Sk - 1
+    // standing in past its end. A padded row of group gL then equals key Sk - 1 and leaves the group's scale as it
+    // is; a wholly padded group is a copy of group gL, scale included. Their scores equal real scores, so they never
+    // raise a row max; the attention zeroes their P.
+    const int last = a.Sk - 1, gl = last / KGROUP;
     float x[4][4], m[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = kb * 32 + slot + 8 * i;
-        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (row < a.Sk) {
-            load4(kbase + (int64_t)row * a.k_sn, v);
+        const int src = row <= last ? row : min(gl * KGROUP + (row & (KGROUP - 1)), last);
+        float v[4];
+        load4(kbase + (int64_t)src * a.k_sn, v);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = v[c] - av[c];
-        }
+        for (int c = 0; c < 4; ++c) v[c] = v[c] - av[c];
         rotate<ROT>(v, j);
 #pragma unroll
         for (int c = 0; c < 4; ++c) x[i][c] = v[c];
@@ -290,7 +296,7 @@ __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
     uint8_t* k8 = a.ws + p.k8 + (size_t)(b * a.HK + hk) * p.skp * 128;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int row = kb * 32 + slot + 8 * i;  // rows past Sk are written as zeros
+        const int row = kb * 32 + slot + 8 * i;
         *reinterpret_cast<uint32_t*>(k8 + (size_t)row * 128 + 16 * ((j >> 2) ^ k_swz(row & 31)) + 4 * (j & 3)) =
             pack_s8(x[i], inv[i >> 1]);
     }
@@ -300,7 +306,7 @@ __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
         const int blk = local >> 5, half = (local >> 4) & 1;
         float* ks = reinterpret_cast<float*>(a.ws + p.aux + ((size_t)(b * a.HK + hk) * p.ntiles + tile) * AUX_BYTES +
                                              AUX_KS_OFF);
-        ks[half * (p.cta / 32) + blk] = grp * KGROUP < a.Sk ? sc[g] : 1.0f;
+        ks[half * (p.cta / 32) + blk] = sc[g];
     }
 }
 
@@ -422,20 +428,21 @@ __device__ __forceinline__ T lds_load(const uint8_t* p) {
         (__attribute__((address_space(3))) const uint8_t*)p);
 }
 
-// Wait until the loads of every tile up to `upto` have landed, given that the loads of tiles up to `issued` are in
-// flight; each tile is LPT loads of this wave (compile-time counts for s_waitcnt).
-template <int NS, int LPT>
-__device__ __forceinline__ void wait_tiles(int ahead) {
-    static_assert(NS >= 2 && NS <= 4, "2- to 4-stage ring");
-    if (NS >= 4 && ahead >= 2) {
-        LR_I8_WAIT_VMCNT((NS >= 4 ? 2 : 0) * LPT);
-    } else if (NS >= 3 && ahead >= 1) {
-        LR_I8_WAIT_VMCNT((NS >= 3 ? 1 : 0) * LPT);
-    } else {
-        LR_I8_WAIT_VMCNT(0);
-    }
-}
+// Accumulators start at this bias instead of 0: an int32 accumulator a with |a - MAGIC| < 2^22 read as an fp32 is
+// exactly 12582912 + (a - MAGIC), so no int -> float conversion is needed; the bias is taken out by the same FMA
+// (scores) or by the column-sum MFMA (P V).
+constexpr int MAGIC = 0x4B400000;
+constexpr float MAGF = 12582912.0f;
 
+// One workgroup: 8 waves x 32 queries. Per key tile t a wave runs two phases, each an explicit slot schedule (one
+// MFMA per slot; a sched_barrier closes every slot, so its VALU work stays with it):
+//   A: S(t+1) = K(t+1) Q^T (int8 MFMA, two 32-key accumulator chains alternating), and in the same slots P(t) from
+//      S(t): x = s * c - m_t (one FMA on the biased score), P = exp2(x) to u8, its row sum (udot4), P ^ 0x80;
+//   B: O^T += V(t)^T P(t) (int8 MFMA, one 32-dim block after the other, two accumulators alternating), and in the
+//      same slots the fp32 update of the previous block, O += ts * acc, and the row max of S(t+1);
+//   operand fragments are read from LDS two slots ahead;
+//   then the column-sum correction (one f32 MFMA per 32-dim block) and tile t+1's constants (max, scales).
+// K, V^T and the aux block of tile t+3 are loaded into a 4-stage LDS ring while tiles t and t+1 are read.
 template <int CTA, int NS>
 __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void i8_attn_kernel(AttnArgs a) {
     constexpr int NB = CTA / 32;                   // 32-key blocks per tile
@@ -443,7 +450,9 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     constexpr int STAGE = 2 * TB + AUX_BYTES;
     constexpr int NW = 8;                          // waves per workgroup, 32 queries each
     constexpr int KVL = TB / 1024 / NW;            // 1 KB direct loads per wave per K (or V^T) tile
-    static_assert(KVL >= 1, "every wave loads");
+    constexpr int QS = 4 * NB;                     // score MFMAs per tile (NB blocks x 4 dim steps)
+    constexpr int PS = 4 * NB;                     // P V MFMAs per tile (4 dim blocks x NB key steps)
+    static_assert(KVL >= 1 && NS == 4, "every wave loads; K(t+2) gets two tiles to land");
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
 
     const Plan& p = a.p;
@@ -464,6 +473,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const uint8_t* vt = a.ws + p.vt + bhk * p.skp * 128;
     const uint8_t* aux = a.ws + p.aux + bhk * p.ntiles * AUX_BYTES;
     const int ntiles = p.ntiles;
+    const int tail = a.Sk - (ntiles - 1) * CTA;  // valid keys of the last tile
 
     // queries: B operand fragments (dims 32 s + 16 hf .. + 15) and the row scale
     const int q = qblk * 256 + wave * 32 + n;
@@ -477,6 +487,18 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     }
     const float cq = (qok ? reinterpret_cast<const float*>(a.ws + p.qs)[qr] : 1.0f) * a.c;
 
+    // per-lane LDS offsets of the operand fragments
+    const int kp = key_perm(n), kx = k_swz(kp), vx = v_swz(n, CTA);
+    auto kfrag = [&](const uint8_t* st, int f) -> i32x4 {  // score MFMA f of a tile: block, dim step
+        const int kb = NB == 4 ? 2 * (f >> 3) + (f & 1) : (f & 1);
+        const int ks = NB == 4 ? (f >> 1) & 3 : f >> 1;
+        return lds_load<i32x4>(st + (32 * kb + kp) * 128 + 16 * ((2 * ks + hf) ^ kx));
+    };
+    auto vfrag = [&](const uint8_t* st, int f) -> i32x4 {  // P V MFMA f of a tile: dim block f / NB, key step f % NB
+        const int bb = f / NB, j = f % NB;
+        return lds_load<i32x4>(st + TB + (32 * bb + n) * CTA + 16 * ((2 * j + hf) ^ vx));
+    };
+
     auto issue = [&](int t) {
         uint8_t* st = ring + (t % NS) * STAGE;
 #pragma unroll
@@ -487,83 +509,123 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
         if (wave == 0) dma16(aux + (size_t)t * AUX_BYTES + lane * 16, lds_addr(st + 2 * TB));
     };
+    // wait until tile `need` has landed, given that tiles up to `issued` were issued
+    auto wait_for = [&](int need, int issued) {
+        const bool one = issued > need;  // at most one later tile (NS = 4: issued <= need + 1)
+        if (wave == 0) {
+            if (one) LR_I8_WAIT_VMCNT(2 * KVL + 1);
+            else LR_I8_WAIT_VMCNT(0);
+        } else {
+            if (one) LR_I8_WAIT_VMCNT(2 * KVL);
+            else LR_I8_WAIT_VMCNT(0);
+        }
+    };
 
+    i32x16 magic;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) magic[r] = MAGIC;
     f32x16 O[4];
 #pragma unroll
     for (int bb = 0; bb < 4; ++bb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) O[bb][r] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f, ts = 0.0f;
+    float cc[NB], nbias[NB];
 
-#pragma unroll
-    for (int t = 0; t < NS - 1; ++t)
-        if (t < ntiles) issue(t);
-    LR_I8_WAIT_VMCNT(0);
-    block_barrier();
-
-    const int tail = a.Sk - (ntiles - 1) * CTA;  // valid keys of the last tile
-    for (int t = 0; t < ntiles; ++t) {
-        if (t + NS - 1 < ntiles) issue(t + NS - 1);
-        const uint8_t* st = ring + (t % NS) * STAGE;
-
-        // S^T = K Q^T, 32 keys per block
-        i32x16 S[NB];
-#pragma unroll
-        for (int kb = 0; kb < NB; ++kb) {
-            const int row = 32 * kb + key_perm(n);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) S[kb][r] = 0;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const i32x4 A = lds_load<i32x4>(st + row * 128 + 16 * ((2 * s + hf) ^ k_swz(row & 31)));
-                S[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Qf[s], S[kb], 0, 0, 0);
-            }
-        }
-        const i16x4 cs = lds_load<i16x4>(st + 2 * TB + 8 * lane);
-        float cc[NB];
-        {
-            const uint8_t* ksp = st + 2 * TB + AUX_KS_OFF + 4 * NB * hf;
-#pragma unroll
-            for (int kb = 0; kb < NB; ++kb) cc[kb] = cq * lds_load<float>(ksp + 4 * kb);
-        }
-        const bool last = t == ntiles - 1 && tail < CTA;
-        if (last) {
-#pragma unroll
-            for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (32 * kb + 16 * hf + r >= tail) S[kb][r] = INT_MIN;
-        }
-
-        // tile max (log2 domain, minus log2(255)), running max, the two scales
+    // tile constants from the biased int row maxima mi of a tile's scores (K scales from its aux block):
+    // c = q_scale * k_scale * scale * log2(e) per 16-key group, m_t = tile max - log2(255), the running max and the
+    // two scales, then the per-block FMA bias -(12582912 c + m_t) that takes out the accumulator bias too.
+    auto constants = [&](const int (&mi)[NB], const uint8_t* st) {
+        const uint8_t* ksp = st + 2 * TB + AUX_KS_OFF + 4 * NB * hf;
         float tmx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < NB; ++kb) {
-            int mi = S[kb][0];
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mi = max(mi, S[kb][r]);
-            tmx = fmaxf(tmx, (float)mi * cc[kb]);
+            cc[kb] = cq * lds_load<float>(ksp + 4 * kb);
+            tmx = fmaxf(tmx, (__int_as_float(mi[kb]) - MAGF) * cc[kb]);
         }
         tmx = pair_max(tmx) - S_U8_OFFSET;
         const float m_new = fmaxf(m_run, tmx);
         const float os = __builtin_amdgcn_exp2f(m_run - m_new);
-        const float ts = __builtin_amdgcn_exp2f(tmx - m_new);
+        ts = __builtin_amdgcn_exp2f(tmx - m_new);
         m_run = m_new;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) nbias[kb] = -fmaf(MAGF, cc[kb], tmx);
+        if (__builtin_amdgcn_ballot_w64(os != 1.0f) != 0) {
+            l_run *= os;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) O[bb][r] *= os;
+        }
+    };
+    auto rowmax = [&](const i32x16 (&S)[NB], int (&mi)[NB]) {
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            mi[kb] = S[kb][0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mi[kb] = max(mi[kb], S[kb][r]);
+        }
+    };
 
-        // P = exp2(s c - tmx) as u8, its row sum, then P - 128 as the signed B operand
+    // prologue: tiles 0 .. NS-2 in flight, S(0) and its constants
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t)
+        if (t < ntiles) issue(t);
+    wait_for(1, min(NS - 2, ntiles - 1));
+    block_barrier();
+    i32x16 S[NB];
+    {
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) S[kb] = magic;
+#pragma unroll
+        for (int f = 0; f < QS; ++f) {
+            const int kb = NB == 4 ? 2 * (f >> 3) + (f & 1) : (f & 1);
+            const int ks = NB == 4 ? (f >> 1) & 3 : f >> 1;
+            S[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kfrag(ring, f), Qf[ks], S[kb], 0, 0, 0);
+        }
+        int mi[NB];
+        rowmax(S, mi);
+        constants(mi, ring);
+    }
+
+    // One key tile. NEXT: S(t+1) is computed in phase A (every tile but the last); LAST: tile t is the last one (P
+    // of keys past Sk zeroed when it is partial). A partial last tile needs no mask for its row max: the prep fills
+    // its key rows past Sk with duplicates of real keys (same int8 row, same scale), which never exceed the max.
+    auto step = [&](int t, auto next_c, auto last_c) {
+        constexpr bool NEXT = decltype(next_c)::value;
+        constexpr bool LAST = decltype(last_c)::value;
+        if (t + NS - 1 < ntiles) issue(t + NS - 1);
+        const uint8_t* stK = ring + ((t + 1) % NS) * STAGE;
+        const uint8_t* stV = ring + (t % NS) * STAGE;
+        const bool mask_p = LAST && tail < CTA;
+
+        // ---- phase A: S(t+1) on MFMA, P(t) on VALU
+        i32x16 Sn[NB];
         uint32_t P[NB][4];
         uint32_t rs = 0;
+        i32x4 fr[3];
+        if (NEXT) {
+            fr[0] = kfrag(stK, 0);
+            fr[1] = kfrag(stK, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
+        for (int s = 0; s < QS; ++s) {
+            if (NEXT) {
+                if (s + 2 < QS) fr[(s + 2) % 3] = kfrag(stK, s + 2);
+                const int kb = NB == 4 ? 2 * (s >> 3) + (s & 1) : (s & 1);
+                const int ks = NB == 4 ? (s >> 1) & 3 : s >> 1;
+                Sn[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[s % 3], Qf[ks], ks == 0 ? magic : Sn[kb], 0, 0, 0);
+            }
+            {
+                const int kb = s >> 2, qd = s & 3;  // P dword s: block kb, keys 16 hf + 4 qd .. + 3
                 uint32_t w = 0;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float e = __builtin_amdgcn_exp2f(fmaf((float)S[kb][4 * qd + i], cc[kb], -tmx));
+                    const float e = __builtin_amdgcn_exp2f(fmaf(__int_as_float(S[kb][4 * qd + i]), cc[kb], nbias[kb]));
                     w = __builtin_amdgcn_cvt_pk_u8_f32(e, i, w);
                 }
-                if (last) {
+                if (mask_p) {
                     uint32_t keep = 0;
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
@@ -573,42 +635,64 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 rs = __builtin_amdgcn_udot4(w, 0x01010101u, rs, false);
                 P[kb][qd] = w ^ 0x80808080u;
             }
-        l_run = l_run * os + ts * (float)rs;
-        if (__builtin_amdgcn_ballot_w64(os != 1.0f) != 0) {
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        l_run = fmaf(ts, (float)rs, l_run);
+
+        // ---- phase B: O^T += V(t)^T P(t) on MFMA; the previous block's fp32 update and the max of S(t+1) on VALU
+        int mi[NB];
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) mi[kb] = MAGIC - (1 << 22);
+        i32x16 acc[2];
+        fr[0] = vfrag(stV, 0);
+        fr[1] = vfrag(stV, 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < PS; ++s) {
+            if (s + 2 < PS) fr[(s + 2) % 3] = vfrag(stV, s + 2);
+            const int bb = s / NB, j = s % NB;
+            const i32x4 B = {(int)P[j][0], (int)P[j][1], (int)P[j][2], (int)P[j][3]};
+            acc[bb & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[s % 3], B, j == 0 ? magic : acc[bb & 1], 0, 0, 0);
+            if (NEXT) {  // max of S(t+1): 4 registers per slot
+#pragma unroll
+                for (int u = 0; u < 4 * NB * 16 / PS / 4; ++u) {
+                    const int g = (4 * NB * 16 / PS) * s + 4 * u;  // flat register index kb * 16 + r
+                    const int kb = g >> 4, r = g & 15;
+                    mi[kb] = max(max(mi[kb], Sn[kb][r]), max(max(Sn[kb][r + 1], Sn[kb][r + 2]), Sn[kb][r + 3]));
+                }
+            }
+            if (bb >= 1) {  // fp32 update of block bb - 1, spread over block bb's slots
+                const int pb = bb - 1;
+#pragma unroll
+                for (int u = 0; u < 16 / NB; ++u) {
+                    const int r = j * (16 / NB) + u;
+                    O[pb][r] = fmaf(__int_as_float(acc[pb & 1][r]), ts, O[pb][r]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) O[3][r] = fmaf(__int_as_float(acc[1][r]), ts, O[3][r]);
+        {
+            // + 128 * ts * (column sums of V(t)) - 12582912 * ts (the P V accumulator bias), per 32-dim block
+            const i16x4 cs = lds_load<i16x4>(stV + 2 * TB + 8 * lane);
+            const float w128 = 128.0f * ts;
 #pragma unroll
             for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) O[bb][r] *= os;
+                O[bb] = __builtin_amdgcn_mfma_f32_32x32x2f32((float)cs[bb] - 49152.0f, w128, O[bb], 0, 0, 0);
         }
-
-        // O^T += V^T P^T (int32 per tile), scaled into fp32, plus the column-sum correction
-        const float w128 = 128.0f * ts;
+        if (NEXT) {
+            constants(mi, stK);
 #pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
-            const int d = 32 * bb + n;
-            i32x16 acc;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] = 0;
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const i32x4 A = lds_load<i32x4>(st + TB + d * CTA + 16 * ((2 * j + hf) ^ v_swz(d, CTA)));
-                const i32x4 B = {(int)P[j][0], (int)P[j][1], (int)P[j][2], (int)P[j][3]};
-                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, acc, 0, 0, 0);
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) O[bb][r] = fmaf((float)acc[r], ts, O[bb][r]);
-            O[bb] = __builtin_amdgcn_mfma_f32_32x32x2f32((float)cs[bb], w128, O[bb], 0, 0, 0);
+            for (int kb = 0; kb < NB; ++kb) S[kb] = Sn[kb];
+            if (t + 2 < ntiles) wait_for(t + 2, min(ntiles - 1, t + NS - 1));
+            else LR_I8_WAIT_VMCNT(0);
+            block_barrier();
         }
-
-        if (t + 1 < ntiles) {
-            const int ahead = min(ntiles - 1, t + NS - 1) - (t + 1);  // tiles in flight beyond t + 1
-            if (wave == 0)
-                wait_tiles<NS, 2 * KVL + 1>(ahead);
-            else
-                wait_tiles<NS, 2 * KVL>(ahead);
-        }
-        block_barrier();
-    }
+    };
+    int t = 0;
+    for (; t < ntiles - 1; ++t) step(t, std::true_type{}, std::false_type{});
+    step(t, std::false_type{}, std::true_type{});  // the last tile; every load has landed (the wait before the previous barrier)
 
     if (!qok) return;
     const float inv = 1.0f / pair_sum(l_run);
@@ -646,9 +730,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
     const int nqb = (a.Sq + 255) / 256;
     const dim3 grid((unsigned)((int64_t)nqb * a.H * a.B));
     if (a.p.cta == 128)
-        hipLaunchKernelGGL((i8_attn_kernel<128, 3>), grid, dim3(512), 0, stream, a);
+        hipLaunchKernelGGL((i8_attn_kernel<128, 4>), grid, dim3(512), 0, stream, a);
     else
-        hipLaunchKernelGGL((i8_attn_kernel<64, 3>), grid, dim3(512), 0, stream, a);
+        hipLaunchKernelGGL((i8_attn_kernel<64, 4>), grid, dim3(512), 0, stream, a);
     return hipGetLastError();
 }
 

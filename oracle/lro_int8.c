@@ -24,6 +24,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define D 128
@@ -160,7 +161,10 @@ void lro_i8_attention(const int8_t* q8, const float* qs, const int8_t* k8, const
                       const int8_t* v8, const float* vs, int W, int nk, float* out) {
     union { uint32_t u; float f; } sm;
     sm.u = 0x3db504f3u;   /* f32(1/sqrt(128)) */
-    double* s = (double*)__builtin_alloca(sizeof(double) * (size_t)nk);
+#pragma omp parallel
+    {
+    double* s = (double*)malloc(sizeof(double) * (size_t)nk);
+#pragma omp for schedule(dynamic, 4)
     for (int i = 0; i < W; ++i) {
         double m = -INFINITY;
         for (int j = 0; j < nk; ++j) {
@@ -177,6 +181,8 @@ void lro_i8_attention(const int8_t* q8, const float* qs, const int8_t* k8, const
         }
         for (int c = 0; c < D; ++c) out[(int64_t)i * D + c] = (float)(o[c] / l * vs[c]);
     }
+    free(s);
+    }
 }
 
 /* The same attention with P rounded the way the reference's kernel rounds it (attn_utils.cuh:610-695): per key tile of
@@ -189,8 +195,11 @@ void lro_i8_attention_p8(const int8_t* q8, const float* qs, const int8_t* k8, co
     sm.u = 0x3db504f3u;
     const double log2e = 1.4426950408889634, offset = (double)7.9943534f;
     const int ntiles = (nk + cta - 1) / cta;
-    double* x = (double*)__builtin_alloca(sizeof(double) * (size_t)nk);
-    double* mt = (double*)__builtin_alloca(sizeof(double) * (size_t)ntiles);
+#pragma omp parallel
+    {
+    double* x = (double*)malloc(sizeof(double) * (size_t)nk);
+    double* mt = (double*)malloc(sizeof(double) * (size_t)ntiles);
+#pragma omp for schedule(dynamic, 4)
     for (int i = 0; i < W; ++i) {
         for (int j = 0; j < nk; ++j) {
             int64_t dot = 0;
@@ -218,5 +227,8 @@ void lro_i8_attention_p8(const int8_t* q8, const float* qs, const int8_t* k8, co
             for (int c = 0; c < D; ++c) o[c] += w * ot[c];
         }
         for (int c = 0; c < D; ++c) out[(int64_t)i * D + c] = (float)(o[c] / l * vs[c]);
+    }
+    free(x);
+    free(mt);
     }
 }

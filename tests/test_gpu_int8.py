@@ -94,9 +94,14 @@ def _check_parts(dec, ref, b, h, hk, Sk, what):
     assert np.array_equal(dec["q8"][b, h], ref["q8"]), f"{what}: q8"
     assert np.array_equal(dec["qs"][b, h].view(np.uint32), ref["qs"].view(np.uint32)), f"{what}: q scales"
     assert np.array_equal(dec["k8"][b, hk, :Sk], ref["k8"]), f"{what}: k8"
-    assert not dec["k8"][b, hk, Sk:].any(), f"{what}: k8 padding"
+    # padding rows repeat real keys: row r > Sk - 1 holds key min(16 gL + r % 16, Sk - 1), gL = (Sk - 1) // 16, so
+    # that its score equals a real score; groups past gL carry gL's scale
+    last, gl = Sk - 1, (Sk - 1) // 16
+    src = [min(gl * 16 + r % 16, last) for r in range(Sk, dec["skp"])]
+    assert np.array_equal(dec["k8"][b, hk, Sk:], ref["k8"][src]), f"{what}: k8 padding"
     ng = len(ref["ks"])
     assert np.array_equal(dec["ks"][b, hk, :ng].view(np.uint32), ref["ks"].view(np.uint32)), f"{what}: k scales"
+    assert np.all(dec["ks"][b, hk, ng:] == ref["ks"][gl]), f"{what}: padded k scales"
     assert np.array_equal(dec["v8"][b, hk, :Sk], ref["v8"]), f"{what}: v8"
     assert not dec["v8"][b, hk, Sk:].any(), f"{what}: v8 padding"
     assert np.array_equal(dec["vs"][b, hk].view(np.uint32), ref["vs"].view(np.uint32)), f"{what}: v scales"
