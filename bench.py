@@ -379,7 +379,7 @@ def bench_int8(args):
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profile("h3-int8", "i8_attn"),
-                     "kernel": "i8_attn_kernel<128, 3>", "kernel_ms": round(attn_ms, 5)},
+                     "kernel": "i8_attn_kernel<128, 4>", "kernel_ms": round(attn_ms, 5)},
         "kernels_ms": {"prep": round(prep_ms, 5), "attention": round(attn_ms, 5)},
         "ops_per_call": ops_call,
     }

@@ -202,6 +202,7 @@ int lr_int8_attention_prep(const void* q, const void* k, const void* v, void* wo
 int lr_int8_attention_kernel(void* out, const void* workspace, int B, int H, int HK, int Sq, int Sk, int D,
                              float scale, int o_rows, lr_stream_t stream);
 
+
 #ifdef __cplusplus
 }
 #endif

@@ -390,9 +390,16 @@ __global__ __launch_bounds__(256) void i8_quant_kernel(PrepArgs a) {
 // ------------------------------------------------------------------------------------------------ attention
 #define LR_I8_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
 
-// One 16-byte-per-lane direct load, global -> LDS: lane l's 16 bytes land at LDS byte address lds + 16 * l.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
+// One 16-byte-per-lane direct load, global -> LDS: lane l reads 16 bytes at base + voff and they land at LDS byte
+// address lds + 16 * l. base and lds are wave-uniform (SGPRs); only the 32-bit offset is per lane.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+    // readfirstlane returns a signed int: widen through uint32_t, or the low half would be sign-extended into the
+    // high half of the address
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
                  : "memory");
 }
 
@@ -400,10 +407,14 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 
+// A workgroup barrier that neither waits for outstanding memory operations nor lets the compiler move any
+// instruction across it (the waits that matter are issued explicitly; the clusters on either side stay apart).
 __device__ __forceinline__ void block_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 __device__ __forceinline__ float pair_max(float x) {
@@ -420,6 +431,20 @@ __device__ __forceinline__ float pair_sum(float x) {
 // r of lane half h is key 16 h + r.
 __device__ __forceinline__ int key_perm(int m) {
     return (m & 3) | (((m >> 3) & 1) << 2) | (((m >> 4) & 1) << 3) | (((m >> 2) & 1) << 4);
+}
+
+// a ^ b on the VALU, opaque to the optimiser: keeps per-fragment LDS addresses from being precomputed and held in
+// registers across the loop (they are one XOR away from a per-stage base). b is wave-uniform.
+__device__ __forceinline__ uint32_t xor_opaque(uint32_t a, uint32_t b) {
+    if (b == 0) return a;
+    uint32_t r;
+    asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "s"(b), "v"(a));
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T lds_at(uint32_t addr) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) T*>((uintptr_t)addr);
 }
 
 template <typename T>
@@ -487,16 +512,19 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     }
     const float cq = (qok ? reinterpret_cast<const float*>(a.ws + p.qs)[qr] : 1.0f) * a.c;
 
-    // per-lane LDS offsets of the operand fragments
+    // Fragment addresses: chunk (2 s + hf) ^ x of a row is chunk hf ^ x with bits 5-6 of the byte address flipped by
+    // 32 s (every other address term has those bits clear), so each fragment is one XOR from a per-stage base.
     const int kp = key_perm(n), kx = k_swz(kp), vx = v_swz(n, CTA);
-    auto kfrag = [&](const uint8_t* st, int f) -> i32x4 {  // score MFMA f of a tile: block, dim step
+    const uint32_t k_lane = (uint32_t)(kp * 128 + 16 * (hf ^ kx));
+    const uint32_t v_lane = (uint32_t)(TB + n * CTA + 16 * (hf ^ vx));
+    auto kfrag = [&](const uint8_t* st, int f) -> i32x4 {  // score MFMA f of a tile: block kb, dim step ks
         const int kb = NB == 4 ? 2 * (f >> 3) + (f & 1) : (f & 1);
         const int ks = NB == 4 ? (f >> 1) & 3 : f >> 1;
-        return lds_load<i32x4>(st + (32 * kb + kp) * 128 + 16 * ((2 * ks + hf) ^ kx));
+        return lds_at<i32x4>(xor_opaque(lds_addr(st) + k_lane, 32 * ks) + 4096 * kb);
     };
-    auto vfrag = [&](const uint8_t* st, int f) -> i32x4 {  // P V MFMA f of a tile: dim block f / NB, key step f % NB
+    auto vfrag = [&](const uint8_t* st, int f) -> i32x4 {  // P V MFMA f: dim block f / NB, key step f % NB
         const int bb = f / NB, j = f % NB;
-        return lds_load<i32x4>(st + TB + (32 * bb + n) * CTA + 16 * ((2 * j + hf) ^ vx));
+        return lds_at<i32x4>(xor_opaque(lds_addr(st) + v_lane, 32 * j) + 32 * CTA * bb);
     };
 
     auto issue = [&](int t) {
@@ -504,10 +532,10 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
         for (int i = 0; i < KVL; ++i) {
             const int blk = wave * KVL + i;
-            dma16(k8 + (size_t)t * TB + blk * 1024 + lane * 16, lds_addr(st + blk * 1024));
-            dma16(vt + (size_t)t * TB + blk * 1024 + lane * 16, lds_addr(st + TB + blk * 1024));
+            dma16(k8 + (size_t)t * TB + blk * 1024, lane * 16, lds_addr(st + blk * 1024));
+            dma16(vt + (size_t)t * TB + blk * 1024, lane * 16, lds_addr(st + TB + blk * 1024));
         }
-        if (wave == 0) dma16(aux + (size_t)t * AUX_BYTES + lane * 16, lds_addr(st + 2 * TB));
+        if (wave == 0) dma16(aux + (size_t)t * AUX_BYTES, lane * 16, lds_addr(st + 2 * TB));
     };
     // wait until tile `need` has landed, given that tiles up to `issued` were issued
     auto wait_for = [&](int need, int issued) {

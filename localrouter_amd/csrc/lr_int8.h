@@ -7,7 +7,8 @@
 // u8 P x s8 V products. The workspace layout is this library's own, laid out for the gfx950 kernels:
 //   q8     int8 [B][H][Sq][128]                     rotated queries, plain rows
 //   k8     int8 [B][HK][skp][128]                   rotated keys minus the anchor; 16-byte chunk c of key row r stored at
-//                                                   c ^ k_swz(r), rows past Sk zero (skp = ntiles * cta)
+//                                                   c ^ k_swz(r); rows past Sk (skp = ntiles * cta) repeat real keys
+//                                                   (see quant_k), so that their scores never raise a row max
 //   vt     int8 [B][HK][ntiles][128][cta]           V^T tiles; chunk c of dim row d at c ^ v_swz(d), keys past Sk zero
 //   aux    [B][HK][ntiles] blocks of 1 KB           per tile: int16 column sums of vt over each half tile, laid out
 //                                                   [half][lane 0..31][dim block 0..3] (dim = 32 * block + lane), then
