@@ -43,6 +43,7 @@ KERNELS = {
     0: "attn_fwd_pipe_kernel<8, 1, 64, 4, 1, true>",
     1: "attn_fwd_pipe_kernel<8, 1, 64, 4, 1, true>",
     2: "attn_fwd_pipe_kernel<4, 1, 64, 2, 1, true>",
+    6: "attn_pair_kernel<1, true>",
 }
 WORKLOADS = {
     # name: (text tokens, grid description, heads)

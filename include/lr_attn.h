@@ -65,8 +65,11 @@ typedef struct ihipStream_t* lr_stream_t;
 #define LR_ATTN_CFG_REGSTAGE_W8 3  /* 256 queries per workgroup, K/V staged through registers (2-stage ring) */
 #define LR_ATTN_CFG_PINGPONG_W8 4  /* 256 queries per workgroup, two groups of 4 waves alternating an MFMA cluster and
                                       a softmax cluster, 4-stage direct-to-LDS K/V ring */
-#define LR_ATTN_CFG_WIDE_W4 5      /* 256 queries per workgroup (4 waves x 64): every K/V operand fragment feeds two
-                                      MFMAs, one wave per SIMD */
+#define LR_ATTN_CFG_WIDE_W4 5      /* 256 queries per workgroup (4 waves x 64), 32-key tiles: every K/V operand
+                                      fragment feeds two MFMAs, one wave per SIMD */
+#define LR_ATTN_CFG_PAIR_W4 6      /* 256 queries per workgroup (4 waves x 64), 64-key tiles in a 4-stage direct-to-LDS
+                                      ring, explicit MFMA schedule: every K/V^T operand fragment feeds two MFMAs,
+                                      one wave per SIMD */
 
 int lr_attn_abi_version(void);
 

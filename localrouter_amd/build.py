@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "liblr_attn.so"
-SOURCES = ["attn_fwd.hip", "rms_rope.hip", "int8_attn.hip", "lr_abi.hip"]
+SOURCES = ["attn_fwd.hip", "attn_pair.hip", "rms_rope.hip", "int8_attn.hip", "lr_abi.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -30,6 +30,11 @@ HIPCC_FLAGS = [
     # packed fp32 (v_pk_*_f32) selection off for all device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+
+
+# per-source extra flags: the 64-query-per-wave kernel's fully unrolled 64-slot schedule is larger than clang's
+# default limit for `#pragma unroll`, and a partly unrolled schedule would index its register arrays at run time
+EXTRA_FLAGS = {"attn_pair.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]}
 
 
 def hipcc() -> str:
@@ -56,7 +61,7 @@ def build(verbose: bool = False) -> Path:
     objs = []
     for src in SOURCES:
         obj = objdir / (Path(src).stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), file=sys.stderr)
         _run(cmd)

@@ -28,237 +28,7 @@ namespace lr {
 
 namespace {
 
-constexpr int BN = 64;          // keys per tile
-constexpr float RESCALE_TAU = 8.0f;  // log2 headroom before the running max is raised
-
-__device__ __forceinline__ float wave_pair_max(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-__device__ __forceinline__ float wave_pair_sum(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Row index (within a 32-key block) whose key the MFMA row m holds: bits 2 and 3 swapped.
-__device__ __forceinline__ int key_perm(int m) { return (m & 0x13) | ((m & 4) << 1) | ((m & 8) >> 1); }
-
-// LDS element offsets (uint16 units). K tile: [64 keys][128 dims], 16-byte chunk c of row r stored at c ^ (r & 15).
-__device__ __forceinline__ int k_lds(int r, int c) { return r * D + 8 * (c ^ (r & 15)); }
-// V^T tile: [128 dims][64 keys], 16-byte chunk cc (8 keys) of row d stored at cc ^ (((d >> 1) ^ (d >> 4)) & 7).
-__device__ __forceinline__ int v_lds(int d, int cc) { return d * BN + 8 * (cc ^ (((d >> 1) ^ (d >> 4)) & 7)); }
-
-// Queries of one lane: B operand fragments for the 8 k-steps (dims 16*ks + 8*hf .. +8) of one 32-query block.
-__device__ __forceinline__ void load_q_plain(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
-    const bool valid = qrow < a.W;
-    const uint16_t* src = a.q + (int64_t)(valid ? qrow : a.W - 1) * a.q_rs + head * D + 8 * hf;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-        u32x4 w = *reinterpret_cast<const u32x4*>(src + 16 * ks);
-        if (!valid) w = u32x4{0, 0, 0, 0};
-        qf[ks] = __builtin_bit_cast(bf16x8, w);
-    }
-}
-
-// Buffer resource over exactly the bytes the call's W query-table rows hold (row r at r * tab_stride elements, P =
-// rot/2 pairs of PAIR elements of ESZ bytes in the last row): the table loads below use 32-bit offsets into it and
-// never address anything outside the table.
-template <int KIND>
-struct QTable {
-    static constexpr int ESZ = KIND == TABLE_MAT2_BF16 ? 2 : 4;    // bytes per table element
-    static constexpr int PAIR = KIND == TABLE_COSSIN_F32 ? 1 : 4;  // elements per pair (per table for cos/sin)
-    static constexpr int PB = PAIR * ESZ;                          // bytes per pair
-    __amdgpu_buffer_rsrc_t ra, rb;
-    int rowb, P;
-    __device__ __forceinline__ QTable(const AttnArgs& a, int row) {
-        P = a.rot >> 1;
-        const uint32_t bytes = (uint32_t)(((int64_t)(a.W - 1) * a.tab_stride + (int64_t)PAIR * P) * ESZ);
-        ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.qta), 0, bytes, 0x00020000);
-        rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(KIND == TABLE_COSSIN_F32 ? a.qtb : a.qta), 0, bytes,
-                                              0x00020000);
-        rowb = (int)((int64_t)row * a.tab_stride * ESZ);
-    }
-    // pairs p0 .. p0+3 (p0 % 4 == 0) in one go; a chunk past the rotated width reads the row's first chunk instead
-    __device__ __forceinline__ void chunk(int p0, Rot2 (&r)[4]) const {
-        const int off = rowb + (p0 + 3 < P ? p0 : 0) * PB;
-        if constexpr (KIND == TABLE_COSSIN_F32) {
-            const auto c = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
-            const auto sn = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                r[i].f00 = __uint_as_float(c[i]); r[i].f01 = -__uint_as_float(sn[i]);
-                r[i].f10 = __uint_as_float(sn[i]); r[i].f11 = __uint_as_float(c[i]);
-            }
-        } else if constexpr (KIND == TABLE_MAT2_BF16) {
-            const auto m0 = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
-            const auto m1 = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t w0 = i < 2 ? m0[2 * i] : m1[2 * i - 4], w1 = i < 2 ? m0[2 * i + 1] : m1[2 * i - 3];
-                r[i].f00 = lo_bf16(w0); r[i].f01 = hi_bf16(w0); r[i].f10 = lo_bf16(w1); r[i].f11 = hi_bf16(w1);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const auto m = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16 * i, 0, 0);
-                r[i].f00 = __uint_as_float(m[0]); r[i].f01 = __uint_as_float(m[1]);
-                r[i].f10 = __uint_as_float(m[2]); r[i].f11 = __uint_as_float(m[3]);
-            }
-        }
-    }
-    // one pair (any p); past the rotated width it reads pair 0 instead
-    __device__ __forceinline__ Rot2 pair(int p) const {
-        const int off = rowb + (p < P ? p : 0) * PB;
-        Rot2 r;
-        if constexpr (KIND == TABLE_COSSIN_F32) {
-            const float c = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, off, 0, 0));
-            const float sn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0));
-            r.f00 = c; r.f01 = -sn; r.f10 = sn; r.f11 = c;
-        } else if constexpr (KIND == TABLE_MAT2_BF16) {
-            const auto m = __builtin_amdgcn_raw_buffer_load_b64(ra, off, 0, 0);
-            r.f00 = lo_bf16(m[0]); r.f01 = hi_bf16(m[0]); r.f10 = lo_bf16(m[1]); r.f11 = hi_bf16(m[1]);
-        } else {
-            const auto m = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
-            r.f00 = __uint_as_float(m[0]); r.f01 = __uint_as_float(m[1]);
-            r.f10 = __uint_as_float(m[2]); r.f11 = __uint_as_float(m[3]);
-        }
-        return r;
-    }
-};
-
-// The same fragments with RMSNorm (fp32, eps, fp32 weight) and RoPE applied before a single bf16 rounding.
-// The lane and its partner (lane ^ 32) hold the two interleaved halves of the query's 128 dims: this lane has dims
-// 16 ks + 8 hf + j. Its 32 rotation pairs form 8 chunks of 4 consecutive pairs: interleaved pairs, chunk c = pairs
-// 8c + 4hf .. +3 (k-step c); split-half pairs (p, p + rot/2), chunk c = pairs 16(c/2) + 8hf + 4(c%2) .. +3 (k-step
-// c/2, partner k-step c/2 + rot/32). Loads are batched so that few memory latencies are exposed: the query chunks, the
-// weight and the first 4 table chunks together, then the other 4 chunks. CHUNKED: 16-byte table loads (needs rot/2 a
-// multiple of 4); otherwise one load per pair. qscale multiplies the normalised query before its single rounding.
-template <int KIND, bool CHUNKED>
-__device__ __forceinline__ void load_q_fused_t(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8],
-                                               float qscale) {
-    const bool valid = qrow < a.W;
-    const int row = valid ? qrow : a.W - 1;
-    const uint16_t* src = a.q + (int64_t)row * a.q_rs + head * D + 8 * hf;
-    const bool inter = a.pairing == PAIR_INTERLEAVED;
-    const int half_ks = a.rot >> 5;   // split-half: k-steps holding the first element of each pair
-    QTable<KIND> tab(a, row);
-    auto chunk_p0 = [&](int c) { return inter ? 8 * c + 4 * hf : 16 * (c >> 1) + 8 * hf + 4 * (c & 1); };
-    auto load_batch = [&](int b, Rot2 (&rt)[4][4]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = 4 * b + i;
-            if constexpr (CHUNKED) {
-                tab.chunk(chunk_p0(c), rt[i]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) rt[i][e] = tab.pair(chunk_p0(c) + e);
-            }
-        }
-    };
-    // ---- loads: query, weight, table chunks 0-3
-    u32x4 raw[8];
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(src + 16 * ks);
-    f32x4 wv[16];
-    if (a.wq) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) wv[i] = *reinterpret_cast<const f32x4*>(a.wq + 16 * (i >> 1) + 8 * hf + 4 * (i & 1));
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) wv[i] = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
-    }
-    Rot2 rt[4][4];
-    if constexpr (KIND != TABLE_NONE) load_batch(0, rt);
-
-    // ---- RMSNorm
-    float x[8][8];
-    float ss = 0.0f;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-        const u32x4 w = valid ? raw[ks] : u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[ks][2 * i] = lo_bf16(w[i]);
-            x[ks][2 * i + 1] = hi_bf16(w[i]);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss = fmaf(x[ks][j], x[ks][j], ss);
-    }
-    ss = wave_pair_sum(ss);
-    const float rr = rsqrtf(ss * (1.0f / D) + a.eps) * qscale;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[ks][j] = x[ks][j] * rr * wv[2 * ks + (j >> 2)][j & 3];
-
-    // ---- RoPE, chunk by chunk
-    if constexpr (KIND != TABLE_NONE) {
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            if (b == 1) load_batch(1, rt);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int c = 4 * b + i;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const Rot2 r = rt[i][e];
-                    if (inter) {
-                        const int ks = c, j = 2 * e;
-                        const bool on = 16 * ks + 8 * hf + j < a.rot;
-                        const float x0 = x[ks][j], x1 = x[ks][j + 1];
-                        x[ks][j] = on ? fmaf(r.f00, x0, r.f01 * x1) : x0;
-                        x[ks][j + 1] = on ? fmaf(r.f10, x0, r.f11 * x1) : x1;
-                    } else {
-                        const int ks = c >> 1, j = 4 * (c & 1) + e;
-                        if (ks >= half_ks) continue;
-                        // the partner k-step ks + half_ks (< 8): select it without dynamic register indexing
-                        float x1 = 0.0f;
-#pragma unroll
-                        for (int k2 = 1; k2 < 8; ++k2)
-                            if (k2 == ks + half_ks) x1 = x[k2][j];
-                        const float x0 = x[ks][j];
-                        x[ks][j] = fmaf(r.f00, x0, r.f01 * x1);
-                        const float y1 = fmaf(r.f10, x0, r.f11 * x1);
-#pragma unroll
-                        for (int k2 = 1; k2 < 8; ++k2)
-                            if (k2 == ks + half_ks) x[k2][j] = y1;
-                    }
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-        bf16x8 f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = (bf16)x[ks][j];
-        qf[ks] = f;
-    }
-}
-
-template <int KIND>
-__device__ __forceinline__ void load_q_fused(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8],
-                                             float qscale = 1.0f) {
-    if (KIND == TABLE_NONE || ((a.rot >> 1) & 3) == 0)
-        load_q_fused_t<KIND, true>(a, qrow, head, hf, qf, qscale);
-    else
-        load_q_fused_t<KIND, false>(a, qrow, head, hf, qf, qscale);
-}
-
-// Query modes of the pipelined kernel besides a TableKind (0-3): plain queries, or the table kind read at run time.
-constexpr int QK_PLAIN = -1;
-constexpr int QK_ANY = 4;
-
-// load_q_fused for the table kind of the call (a uniform branch; each kind's loads batch on their own).
-__device__ __forceinline__ void load_q_fused_any(const AttnArgs& a, int qrow, int head, int hf, bf16x8 (&qf)[8]) {
-    switch (a.table_kind) {
-        case TABLE_COSSIN_F32: load_q_fused<TABLE_COSSIN_F32>(a, qrow, head, hf, qf); break;
-        case TABLE_MAT2_BF16: load_q_fused<TABLE_MAT2_BF16>(a, qrow, head, hf, qf); break;
-        case TABLE_MAT2_F32: load_q_fused<TABLE_MAT2_F32>(a, qrow, head, hf, qf); break;
-        default: load_q_fused<TABLE_NONE>(a, qrow, head, hf, qf); break;
-    }
-}
+#include "attn_common.inc"
 
 // The register-staged kernel: K/V tiles pass through VGPRs into a 2-stage LDS ring, V^T is formed by a register
 // transpose. Kept as the reference point for the pipelined kernel below.
@@ -528,34 +298,6 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_regstage_kernel(AttnArgs 
 // so the QK^T MFMAs of the next tile hide the exp/max/sum work of the current one, and every load has two tiles of
 // compute to land.
 
-// V tile: 16-byte chunk c of row r stored at c ^ ((r & 3) << 2). A transposed read instruction covers 8 rows x 4
-// chunks (rows 4 apart share r & 3 and differ in the XOR-ed bits), so it touches every bank exactly twice; whole-row
-// writes stay a permutation of the 16 chunks.
-__device__ __forceinline__ int vrow_swz(int r) { return (r & 3) << 2; }
-
-// Wait until at most n vector-memory operations of this wave are outstanding.
-#define LR_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
-
-// One 16-byte-per-lane direct load, global -> LDS: lane l's 16 bytes land at LDS byte address lds + 16 * l. Written
-// as inline asm (M0 = destination) so that the compiler does not serialise LDS reads of other ring slots behind it;
-// completion is tracked by the explicit vmcnt waits above. Nothing else in these kernels uses M0.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
-// A workgroup barrier that neither waits for outstanding memory operations nor lets the compiler move memory
-// accesses across it (the waits that matter are issued explicitly).
-__device__ __forceinline__ void block_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 // NW waves of NQB x 32 queries each; tiles of BT keys in an NS-stage K/V ring. NQB = 2 reads every K and V operand
 // fragment from LDS once for two 32-query MFMAs, halving LDS traffic per MFMA, at one wave per SIMD (its registers
 // need it); BT = 32 then keeps the two score buffers at 32 registers each.
@@ -563,7 +305,10 @@ __device__ __forceinline__ void block_barrier() {
 // with that table kind, its loads specialised), or QK_ANY (the table kind read at run time).
 // VT: values arrive packed as V^T tiles ([128 dims][64 keys], 16 KB contiguous per tile, zero past nkeys), stored in
 // LDS with 16-byte chunk c of dim row d at c ^ ((d >> 1) & 7), and the PV A operand is one ds_read_b128 per MFMA.
-template <int NW, int NQB, int BT, int NS, int QK, bool VT>
+// REDO: the second launch after the 64-query-per-wave kernel (attn_pair.hip), same 256-query blocks: a workgroup
+// recomputes its block only if that kernel marked one of the block's 64-row quarters (a NaN in its first row: some
+// P overflowed its fixed reference), and exits otherwise.
+template <int NW, int NQB, int BT, int NS, int QK, bool VT, bool REDO = false>
 __global__ __launch_bounds__(NW * 64, NQB == 1 ? 8 / NW : 1)
 __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void attn_fwd_pipe_kernel(AttnArgs a) {
     static_assert(NS >= 2 && NS <= 4, "2- to 4-stage ring");
@@ -595,6 +340,16 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
     const int hk = head / a.G;
     const int row0 = qblk * BM, wrow0 = row0 + wave * 32 * NQB;
     const int last_row = min(row0 + BM, a.W) - 1;
+    if constexpr (REDO) {
+        static_assert(BM == 256, "the marked blocks are 256 queries");
+        bool marked = false;
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            const int r = row0 + 64 * qq;
+            if (r < a.W) marked = marked || (a.out[(int64_t)r * a.o_rs + head * D] & 0x7fffu) > 0x7f80u;
+        }
+        if (!marked) return;   // uniform over the workgroup: every thread read the same four values
+    }
     int ntiles = (a.nkeys + BT - 1) / BT;
     if (a.causal) ntiles = min(ntiles, (a.p0 + last_row) / BT + 1);
     const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
@@ -1294,15 +1049,23 @@ hipError_t launch_regstage(const AttnArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int NW, int NQB, int BT, int NS, int QK, bool VT = false>
+template <int NW, int NQB, int BT, int NS, int QK, bool VT = false, bool REDO = false>
 hipError_t launch_pipe(const AttnArgs& a, hipStream_t stream) {
     constexpr int BM = 32 * NQB * NW;
     const int64_t nqb = (a.W + BM - 1) / BM;
     const int64_t blocks = nqb * a.H;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, NQB, BT, NS, QK, VT>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+    hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, NQB, BT, NS, QK, VT, REDO>), dim3((unsigned)blocks), dim3(NW * 64), 0,
                        stream, a);
     return hipGetLastError();
+}
+
+// The 64-query-per-wave kernel, then the running-max kernel on the blocks it marked.
+template <int QK, bool VT>
+hipError_t launch_pair_checked(const AttnArgs& a, hipStream_t stream) {
+    const hipError_t e = launch_pair(a, QK, VT, stream);
+    if (e != hipSuccess) return e;
+    return launch_pipe<8, 1, 64, VT ? 4 : 3, QK, VT, true>(a, stream);
 }
 
 }  // namespace
@@ -1315,7 +1078,8 @@ int attention_block_rows(int config) {
 }
 
 bool attention_config_reads_vt(int config) {
-    return config == ATTN_CFG_AUTO || config == ATTN_CFG_PIPE_W8 || config == ATTN_CFG_PIPE_W4;
+    return config == ATTN_CFG_AUTO || config == ATTN_CFG_PIPE_W8 || config == ATTN_CFG_PIPE_W4 ||
+           config == ATTN_CFG_PAIR_W4;
 }
 
 // The prepared-keys path over packed V^T tiles, queries fused with table kind K (the 64-key pipelined shapes).
@@ -1324,6 +1088,7 @@ hipError_t launch_vt(const AttnArgs& a, int config, hipStream_t stream) {
     switch (config) {
         case ATTN_CFG_PIPE_W8: return launch_pipe<8, 1, 64, 4, K, true>(a, stream);
         case ATTN_CFG_PIPE_W4: return launch_pipe<4, 1, 64, 2, K, true>(a, stream);
+        case ATTN_CFG_PAIR_W4: return launch_pair_checked<K, true>(a, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1348,6 +1113,9 @@ hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config
         case ATTN_CFG_PIPE_W4:   // 64 KB of LDS so that two 4-wave blocks share a CU
             if (fuse_q) return hipErrorInvalidValue;
             return launch_pipe<4, 1, 64, 2, QK_PLAIN>(a, stream);
+        case ATTN_CFG_PAIR_W4:
+            if (fuse_q) return hipErrorInvalidValue;
+            return launch_pair_checked<QK_PLAIN, false>(a, stream);
         case ATTN_CFG_WIDE_W4:
             return fuse_q ? launch_pipe<4, 2, 32, 4, QK_ANY>(a, stream) : launch_pipe<4, 2, 32, 4, QK_PLAIN>(a, stream);
         case ATTN_CFG_REGSTAGE_W8:

@@ -1,0 +1,506 @@
+// Flash-style joint attention for gfx950 with 64 queries per wave ("pair" kernel): bf16 in, fp32 MFMA accumulation
+// and softmax, bf16 out. Same semantics as the pipelined kernel in attn_fwd.hip, which follow the reference's
+// kernels/cuda/qwen_image/attention.cu:253-444 (pattn2_kernel) as launched by
+// src/engines/qwen_image/ops_launch.zig:163-172: O_i = softmax_j(scale <q_i, k_j>) v_j over keys j < nkeys (and
+// j <= p0 + i when causal, attention.cu:304), query head h reading kv head h / (H / HK) (attention.cu:264-266), P
+// rounded to bf16 for the PV product (attention.cu:418-424), output rounded to bf16 (attention.cu:432-443).
+//
+// Why 64 queries per wave. Every 32x32x16 MFMA takes one 1 KB operand fragment (a K or V^T slice) from LDS. On
+// gfx950 one ds_read_b128 per MFMA holds the matrix pipe at about two thirds of its rate (LDS bandwidth), one per two
+// MFMAs does not. A wave that owns two 32-query blocks feeds each fragment to two MFMAs. Its state does not fit the
+// 256 VGPRs of two waves per SIMD, so the kernel runs one wave per SIMD (4 waves, 256 queries per workgroup) and
+// places it explicitly: O (128) and Q (64) in AGPRs, which MFMAs read and write directly; scores, P and the fragment
+// ring in VGPRs. The MFMAs are inline asm so that the compiler cannot move accumulators between the two files; the
+// compiler does not see them as MFMAs, so every VALU read of an MFMA result below is either many MFMA slots after
+// that MFMA or behind a fence_* (wait states that the registers they protect depend on).
+//
+// Per 64-key tile t a wave runs one step of 64 MFMA slots (one wave instruction stream, a sched_barrier per slot):
+//   slots  0-3    O += V(t-1)^T P(t-1), fragments V0-V1   | VALU: max of S(t) key block 1, then the (rare) rescale
+//   slots  4-23   O += V(t-1)^T P(t-1), fragments V2-V11  | VALU: P(t) of key block 0 (exp2, bf16 pack, row sums)
+//   slots 24-39   S(t+1) key block 0 = K(t+1) Q^T         | VALU: P(t) of key block 1
+//   slots 40-47   O += V(t-1)^T P(t-1), fragments V12-V15 |
+//   slots 48-63   S(t+1) key block 1                      | VALU: max of S(t+1) key block 0
+// Scores are single-buffered: a key block's exps finish before the MFMAs that overwrite it start. P is double-buffered
+// (P(t) is written while P(t-1) is consumed). K and V^T tiles stream through a 4-stage LDS ring by direct
+// global->LDS loads; the first three fragments of the next step are read before the step-closing barrier.
+//
+// Softmax reference. The running reference m of each query is an integer (ceil of a tile max, in the exp2 domain)
+// and only rises when a tile's max exceeds it by more than 2^8. A rise by d multiplies O, the row sum and the pending
+// P(t-1) by 2^-d, which is exact for the bf16 P (an exponent change), so every P and l of a row keep sharing one
+// reference that cancels in O / l.
+#include "lr_common.h"
+#include "lr_kernels.h"
+
+namespace lr {
+
+namespace {
+
+#include "attn_common.inc"
+
+// One 16-byte-per-lane ring load, buffer -> LDS: lane l reads 16 bytes at descriptor base + voff (zeros past the
+// descriptor's record count) and they land at LDS byte address lds + 16 l. The descriptor and lds are wave-uniform.
+__device__ __forceinline__ void dma16_buf(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+
+// S = K Q^T (accumulator starts at 0, or at c); S += K Q^T, as inline asm: scores in VGPRs (the VALU reads them), Q in
+// AGPRs.
+__device__ __forceinline__ void mfma_qk0(f32x16& d, const bf16x8& k, const bf16x8& q) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(k), "a"(q));
+}
+__device__ __forceinline__ void mfma_qk_c(f32x16& d, const bf16x8& k, const bf16x8& q, const f32x16& c) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "a"(q), "v"(c));
+}
+__device__ __forceinline__ void mfma_qk(f32x16& d, const bf16x8& k, const bf16x8& q) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "a"(q));
+}
+// O += V^T P through the builtin: the compiler knows this one is an MFMA, so any copy it makes of O (which lives in
+// AGPRs, the accumulator form it selects for a one-wave-per-SIMD kernel) gets the hazard waits it needs.
+__device__ __forceinline__ void mfma_pv(f32x16& o, const bf16x8& v, const bf16x8& p) {
+    o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, p, o, 0, 0, 0);
+}
+// Hazard fences: 48 wait states, more than any MFMA -> VALU or VALU -> MFMA dependency needs on gfx950. Each takes the
+// registers it protects as in/out operands, so that no access to them can be scheduled across it.
+#define LR_NOP48 "s_nop 15\n\ts_nop 15\n\ts_nop 15"
+__device__ __forceinline__ void fence_o(f32x16 (&o)[2][4]) {
+    asm volatile(LR_NOP48 : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[0][2]), "+a"(o[0][3]), "+a"(o[1][0]), "+a"(o[1][1]),
+                 "+a"(o[1][2]), "+a"(o[1][3]));
+}
+__device__ __forceinline__ void fence_s(f32x16 (&s)[2][2]) {
+    asm volatile(LR_NOP48 : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1]));
+}
+__device__ __forceinline__ void fence_negm(f32x16 (&m)[2]) { asm volatile(LR_NOP48 : "+v"(m[0]), "+v"(m[1])); }
+__device__ __forceinline__ void fence_q(bf16x8 (&q)[8]) {
+    asm volatile(LR_NOP48 : "+a"(q[0]), "+a"(q[1]), "+a"(q[2]), "+a"(q[3]), "+a"(q[4]), "+a"(q[5]), "+a"(q[6]),
+                 "+a"(q[7]));
+}
+
+constexpr int PW = 4;                 // waves per workgroup
+constexpr int PBM = 64 * PW;          // queries per workgroup
+constexpr int PNS = 4;                // ring stages
+constexpr int PTILE = BN * D;         // elements per K or V^T tile
+constexpr int PLOADS = BN / 4 / PW;   // 1 KB direct loads per wave per tile
+
+template <int QK, bool VT>
+__global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_pair_kernel(AttnArgs a) {
+    // FOLD: fused queries arrive multiplied by scale * log2(e), so a score is already in the exp2 domain, and the
+    // reference m is subtracted by the score MFMAs themselves (their accumulator starts at -m): P = exp2(S) with no
+    // per-score VALU op. Plain queries keep exact raw scores: P = exp2(S * c - m).
+    constexpr bool FOLD = QK != QK_PLAIN;
+    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+    __shared__ __attribute__((aligned(1024))) uint16_t Kr[PNS * PTILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vr[PNS * PTILE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: LDS destinations stay in SGPRs
+    const int n = lane & 31, hf = lane >> 5;
+
+    // XCD-aware mapping: hardware workgroup b runs on XCD b % 8; each XCD gets a contiguous range of logical ids
+    const int nwg = gridDim.x, b = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
+    const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int nqb = (a.W + PBM - 1) / PBM;
+    const int head = logical / nqb, qblk = logical - head * nqb;
+    const int hk = head / a.G;
+    const int row0 = qblk * PBM, wrow0 = row0 + wave * 64;
+    const int last_row = min(row0 + PBM, a.W) - 1;
+    int ntiles = (a.nkeys + BN - 1) / BN;
+    if (a.causal) ntiles = min(ntiles, (a.p0 + last_row) / BN + 1);
+    const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
+    const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs;
+
+    // ---- ring loads: load j of a tile fills rows 4i..4i+3 (K, V rows) or dim rows 8i..8i+7 (V^T), i = wave + PW j, by
+    // buffer_load_dwordx4 ... lds from a per-tile descriptor (SGPRs) and a constant per-lane byte offset. The
+    // descriptor's record count ends at the last valid key row, so rows past nkeys read as zeros (masked keys; their V
+    // rows meet P = 0). A load for a tile past the last one reads nothing (record count 0) into a dummy LDS area, so
+    // every step issues the same loads and waits the same counts.
+    __shared__ __attribute__((aligned(1024))) uint16_t Dummy[PTILE];
+    const int lrow = lane >> 4, lchunk = lane & 15;
+    uint32_t koff[PLOADS], voff[PLOADS];
+#pragma unroll
+    for (int j = 0; j < PLOADS; ++j) {
+        const int r = 4 * (wave + PW * j) + lrow;
+        koff[j] = 2u * (uint32_t)(r * a.k_rs + 8 * (lchunk ^ (r & 15)));
+        if constexpr (VT) {
+            const int d = 8 * (wave + PW * j) + (lane >> 3);
+            voff[j] = 2u * (uint32_t)(d * BN + 8 * ((lane & 7) ^ ((d >> 1) & 7)));
+        } else {
+            voff[j] = 2u * (uint32_t)(r * a.v_rs + 8 * (lchunk ^ (lrow << 2)));
+        }
+    }
+    const uint32_t kr_lds = lds_addr(Kr), vr_lds = lds_addr(Vr), dummy_lds = lds_addr(Dummy);
+    // descriptor of rows key0.. of a [rows][row_elems] bf16 array at base (row stride rs elements); nothing past nkeys
+    auto rows_rsrc = [&](const uint16_t* base, int64_t rs, int t) __attribute__((always_inline)) {
+        const int key0 = t * BN;
+        const uint64_t addr = (uint64_t)(uintptr_t)(base + (int64_t)key0 * rs);
+        const int64_t valid = t < ntiles ? (int64_t)(a.nkeys - 1 - key0) * rs * 2 + 2 * D : 0;
+        return u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xffffu,
+                     (uint32_t)(valid < 0xffffffffLL ? valid : 0xffffffffLL), 0x00020000u};
+    };
+    // this wave's LDS base for tile t of a ring (load j adds j * 4 KB); past the last tile, the dummy area
+    auto lds_dst = [&](uint32_t ring, int t) __attribute__((always_inline)) {
+        return (t < ntiles ? ring + (uint32_t)(2 * (t % PNS) * PTILE) : dummy_lds) + (uint32_t)(2 * wave * 512);
+    };
+    auto k_rsrc = [&](int t) __attribute__((always_inline)) { return rows_rsrc(kbase, a.k_rs, t); };
+    auto v_rsrc = [&](int t) __attribute__((always_inline)) {
+        if constexpr (VT) {   // packed V^T tiles are whole (zero past nkeys)
+            const uint64_t addr = (uint64_t)(uintptr_t)(vbase + (int64_t)t * PTILE);
+            return u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xffffu, t < ntiles ? 2u * PTILE : 0u, 0x00020000u};
+        } else {
+            return rows_rsrc(vbase, a.v_rs, t);
+        }
+    };
+    // load j of K / V tile t, from its descriptor and LDS base
+    auto dma_k = [&](const u32x4& rs, uint32_t dst, int j) __attribute__((always_inline)) {
+        dma16_buf(rs, koff[j], dst + (uint32_t)(2 * PW * 512 * j));
+    };
+    auto dma_v = [&](const u32x4& rs, uint32_t dst, int j) __attribute__((always_inline)) {
+        dma16_buf(rs, voff[j], dst + (uint32_t)(2 * PW * 512 * j));
+    };
+
+    // ---- prologue loads: K(0..3), V(0..1), then the queries (their latency overlaps the ring's)
+#pragma unroll
+    for (int i = 0; i < PNS; ++i) {
+        const u32x4 rs = k_rsrc(i);
+        const uint32_t dst = lds_dst(kr_lds, i);
+#pragma unroll
+        for (int j = 0; j < PLOADS; ++j) dma_k(rs, dst, j);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const u32x4 rs = v_rsrc(i);
+        const uint32_t dst = lds_dst(vr_lds, i);
+#pragma unroll
+        for (int j = 0; j < PLOADS; ++j) dma_v(rs, dst, j);
+    }
+    bf16x8 qa[2][8];   // AGPR-resident B operands of S^T = K Q^T
+    {
+        bf16x8 qv[8];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int qrow = wrow0 + 32 * nb + n;
+            if constexpr (QK == QK_PLAIN)
+                load_q_plain(a, qrow, head, hf, qv);
+            else
+                load_q_fused<QK>(a, qrow, head, hf, qv, a.c);
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) asm volatile("; q -> agpr" : "=a"(qa[nb][ks]) : "0"(qv[ks]));
+            fence_q(qa[nb]);   // the AGPR writes above land before the first MFMA reads them
+        }
+    }
+
+    // ---- per-lane LDS byte offsets. K fragment (k-step ks, 32-key block mb) of a tile: row 32 mb + key_perm(n),
+    // chunk (2 ks + hf) ^ (row & 15); with the row a multiple of 256 bytes that is lane_k ^ (32 ks) + 8192 mb.
+    // Packed V^T fragment (16-key step kk, 32-dim block db): dim row 32 db + n, chunk (2 kk + hf) ^ ((n >> 1) & 7),
+    // i.e. lane_v ^ (32 kk) + 4096 db.
+    const int pr = key_perm(n);
+    const uint32_t lane_k = (uint32_t)(pr * 256 + 16 * (hf ^ (pr & 15)));
+    const uint32_t lane_v = (uint32_t)(n * 128 + 16 * (hf ^ ((n >> 1) & 7)));
+    const int g = lane >> 4, sl = lane & 15;
+    int vtr[4];   // V rows read transposed (plain path)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        const int chunk = 4 * (db ^ (sl >> 2)) + 2 * (g & 1) + ((sl & 3) >> 1);
+        vtr[db] = (8 * (g >> 1) + (sl >> 2)) * D + 8 * chunk + 4 * (sl & 1);
+    }
+    typedef __attribute__((address_space(3))) const bf16x8 lds_bf16x8;
+    // kslot / vslot: LDS byte address of the tile's ring slot
+    auto kfrag = [&](uint32_t kslot, int mb, int ks) __attribute__((always_inline)) -> bf16x8 {
+        return *(lds_bf16x8*)(uintptr_t)(kslot + (lane_k ^ (uint32_t)(32 * ks)) + 8192 * mb);
+    };
+    auto vfrag = [&](uint32_t vslot, int i) __attribute__((always_inline)) -> bf16x8 {   // i = 4 kk + db
+        const int kk = i >> 2, db = i & 3;
+        if constexpr (VT) {
+            return *(lds_bf16x8*)(uintptr_t)(vslot + (lane_v ^ (uint32_t)(32 * kk)) + 4096 * db);
+        } else {
+            const uint32_t p0 = vslot + 2 * (vtr[db] + (16 * kk) * D);
+            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)p0);
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)(p0 + 8 * D));
+            return __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi), 0, 1, 2, 3,
+                                           4, 5, 6, 7);
+        }
+    };
+    auto kslot_of = [&](int t) __attribute__((always_inline)) { return kr_lds + (uint32_t)((t % PNS) * PTILE * 2); };
+    auto vslot_of = [&](int t) __attribute__((always_inline)) { return vr_lds + (uint32_t)((t % PNS) * PTILE * 2); };
+
+    LR_WAIT_VMCNT(0);
+    block_barrier();
+
+    // ---- S(0) = K(0) Q^T
+    f32x16 s[2][2];   // [query block][32-key block]
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const bf16x8 kf = kfrag(kslot_of(0), mb, ks);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                if (ks == 0) mfma_qk0(s[nb][mb], kf, qa[nb][0]);
+                else mfma_qk(s[nb][mb], kf, qa[nb][ks]);
+            }
+        }
+
+    const float c = a.c;
+    auto needs_mask = [&](int t) __attribute__((always_inline)) {
+        const int key0 = t * BN;
+        return key0 + BN > a.nkeys || (a.causal && key0 + BN - 1 > a.p0 + wrow0);
+    };
+    auto mask_tile = [&](int t) __attribute__((always_inline)) {
+        const int key0 = t * BN;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int pos = a.p0 + wrow0 + 32 * nb + n;
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = key0 + 32 * mb + 16 * (r >> 3) + 8 * hf + (r & 7);
+                    if (!(key < a.nkeys && (!a.causal || key <= pos))) s[nb][mb][r] = -INFINITY;
+                }
+        }
+    };
+    auto block_max = [&](int nb, int mb) __attribute__((always_inline)) {
+        float m = fmaxf(s[nb][mb][0], s[nb][mb][1]);
+#pragma unroll
+        for (int r = 2; r < 16; ++r) m = fmaxf(m, s[nb][mb][r]);
+        return m;
+    };
+
+    // ---- the reference: ceil of tile 0's exact max (the exp2 domain), fixed for the whole call. Later tiles' P are
+    // exp2(s - m) with no running max: exact as long as they stay finite, which the epilogue verifies
+    fence_s(s);
+    if (needs_mask(0)) mask_tile(0);
+    float m_used[2], ls[2] = {0.0f, 0.0f};
+    f32x16 negm[2];   // FOLD: -m in every slot, the initial accumulator of the score MFMAs
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        float mx = wave_pair_max(fmaxf(block_max(nb, 0), block_max(nb, 1)));
+        if constexpr (!FOLD) mx *= c;
+        m_used[nb] = mx > -INFINITY ? ceilf(mx) : 0.0f;
+        negm[nb] = f32x16{} - m_used[nb];
+        if constexpr (FOLD) {
+            s[nb][0] -= m_used[nb];
+            s[nb][1] -= m_used[nb];
+        }
+    }
+    fence_negm(negm);
+    f32x16 o[2][4];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[nb][db] = f32x16{};
+    block_barrier();   // every wave is done with K slot 0 before step 0 refills it
+
+    const bf16x2 ones2 = {(bf16)1.0f, (bf16)1.0f};
+    u32x4 pA[2][4], pB[2][4];   // P double buffer: packed bf16 pairs, [query block][16-key step kk][j]
+
+    // P word (nb, kk, j) of S(t): keys 16 kk + 8 hf + 2 j, +1 of the 64-key tile
+    auto exp_word = [&](u32x4 (&p)[2][4], int nb, int kk, int j) __attribute__((always_inline)) {
+        const int mb = kk >> 1, r = 8 * (kk & 1) + 2 * j;
+        const float x0 = s[nb][mb][r], x1 = s[nb][mb][r + 1];
+        const float e0 = FOLD ? x0 : fmaf(x0, c, -m_used[nb]);
+        const float e1 = FOLD ? x1 : fmaf(x1, c, -m_used[nb]);
+        uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(e0), __builtin_amdgcn_exp2f(e1));
+        asm volatile("" : "+v"(w));   // computed in this slot: not sunk to its use in the next step
+        p[nb][kk][j] = w;
+        // the row sum of the bf16 P exactly as the PV MFMA consumes it
+        ls[nb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones2, ls[nb], false);
+    };
+    // word w (0..15) of key block mb: (nb, kk, j) = (w / 8, 2 mb + (w / 4) % 2, w % 4)
+    auto exp_block_word = [&](u32x4 (&p)[2][4], int mb, int w) __attribute__((always_inline)) {
+        exp_word(p, w >> 3, 2 * mb + ((w >> 2) & 1), w & 3);
+    };
+    auto pv_operand = [&](const u32x4 (&p)[2][4], int nb, int kk) __attribute__((always_inline)) {
+        return __builtin_bit_cast(bf16x8, p[nb][kk]);
+    };
+    // QK MFMA k-step ks of score tile (nb, mb) of the next tile
+    auto qk = [&](int nb, int mb, int ks, const bf16x8& kf) __attribute__((always_inline)) {
+        if (ks == 0) {
+            if constexpr (FOLD) mfma_qk_c(s[nb][mb], kf, qa[nb][0], negm[nb]);
+            else mfma_qk0(s[nb][mb], kf, qa[nb][0]);
+        } else {
+            mfma_qk(s[nb][mb], kf, qa[nb][ks]);
+        }
+    };
+
+    bf16x8 fr[4];   // fragment ring, read 3 fragments ahead
+    // fragment f of a step: V0-V11, K(block 0, ks 0-7), V12-V15, K(block 1, ks 0-7); the first step has no V
+    auto frag_of = [&](bool first, uint32_t kt, uint32_t vt, int f) __attribute__((always_inline)) -> bf16x8 {
+        if (first) return kfrag(kt, f >> 3, f & 7);
+        if (f < 12) return vfrag(vt, f);
+        if (f < 20) return kfrag(kt, 0, f - 12);
+        if (f < 24) return vfrag(vt, f - 8);
+        return kfrag(kt, 1, f - 24);
+    };
+    // the first three fragments of step 0 (K(1)); later steps read theirs before the previous step's barrier
+    fr[0] = frag_of(true, kslot_of(1), 0, 0);
+    fr[1] = frag_of(true, kslot_of(1), 0, 1);
+    fr[2] = frag_of(true, kslot_of(1), 0, 2);
+
+    // the ring refill of step t, one load per slot 1, 5, ..., 29: V(t+2) loads 0-3, then K(t+4) loads 0-3
+    struct Refill {
+        u32x4 krs, vrs;
+        uint32_t kdst, vdst;
+    };
+    auto refill_of = [&](int t) __attribute__((always_inline)) {
+        return Refill{k_rsrc(t + PNS), v_rsrc(t + 2), lds_dst(kr_lds, t + PNS), lds_dst(vr_lds, t + 2)};
+    };
+    auto refill_slot = [&](const Refill& rf, int sl2) __attribute__((always_inline)) {
+        if ((sl2 & 3) != 1 || sl2 >= 32) return;
+        const int j = sl2 >> 2;
+        if (j < 4) dma_v(rf.vrs, rf.vdst, j);
+        else dma_k(rf.krs, rf.kdst, j - 4);
+    };
+    // end of step t: wait for this wave's loads of earlier steps, read the next step's first fragments (V(t), resident
+    // since the previous barrier), barrier
+    auto close_step = [&](int t) __attribute__((always_inline)) {
+        LR_WAIT_VMCNT(2 * PLOADS);
+        const uint32_t vt = vslot_of(t);
+        fr[0] = vfrag(vt, 0);
+        fr[1] = vfrag(vt, 1);
+        fr[2] = vfrag(vt, 2);
+        block_barrier();
+    };
+
+    // ---- step 0: P(0), S(1); no PV yet
+    {
+        const uint32_t kt = kslot_of(1);
+        const Refill rf = refill_of(0);
+        // P(0) of key block 0 before its scores are overwritten
+#pragma unroll
+        for (int w = 0; w < 16; ++w) exp_block_word(pA, 0, w);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int sl2 = 0; sl2 < 32; ++sl2) {
+            const int f = sl2 >> 1, nb = sl2 & 1, mb = f >> 3, ks = f & 7;
+            if (nb == 0 && f + 3 < 16) fr[(f + 3) & 3] = frag_of(true, kt, 0, f + 3);
+            qk(nb, mb, ks, fr[f & 3]);
+            if (sl2 < 16) exp_block_word(pA, 1, sl2);   // P(0) of key block 1 while key block 0 is recomputed
+            refill_slot(rf, sl2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        close_step(0);
+    }
+
+    // ---- step t >= 1: PV(t-1), P(t), S(t+1), one uninterrupted run of 64 slots:
+    //   slots  0-23  PV fragments V0-V11        | P(t) key block 0 (word w in slot floor(3 w / 2))
+    //   slots 24-39  S(t+1) key block 0          | P(t) key block 1 (word w in slot 24 + floor(3 w / 2))
+    //   slots 40-47  PV fragments V12-V15        |
+    //   slots 48-63  S(t+1) key block 1
+    //   ring loads in slots 1, 5, ..., 29
+    auto step = [&](int t, u32x4 (&pc)[2][4], u32x4 (&pp)[2][4]) __attribute__((always_inline)) {
+        if (needs_mask(t)) {
+            fence_s(s);
+            mask_tile(t);
+        }
+        const uint32_t kt = kslot_of(t + 1);
+        const uint32_t vt = vslot_of(t - 1);
+        const Refill rf = refill_of(t);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int sl2 = 0; sl2 < 64; ++sl2) {
+            const int f = sl2 >> 1, nb = sl2 & 1;
+            if (nb == 0 && f + 3 < 32) fr[(f + 3) & 3] = frag_of(false, kt, vt, f + 3);
+            if (f < 12 || (f >= 20 && f < 24)) {
+                const int i = f < 12 ? f : f - 8;   // V fragment 4 kk + db
+                mfma_pv(o[nb][i & 3], fr[f & 3], pv_operand(pp, nb, i >> 2));
+            } else {
+                const int mb = f < 20 ? 0 : 1, ks = f < 20 ? f - 12 : f - 24;
+                qk(nb, mb, ks, fr[f & 3]);
+            }
+            if (sl2 < 24) {
+                const int w = (2 * sl2 + 2) / 3;
+                if (w < 16 && (3 * w) / 2 == sl2) exp_block_word(pc, 0, w);
+            } else if (sl2 < 48) {
+                const int w = (2 * (sl2 - 24) + 2) / 3;
+                if (w < 16 && 24 + (3 * w) / 2 == sl2) exp_block_word(pc, 1, w);
+            }
+            refill_slot(rf, sl2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        close_step(t);
+    };
+
+    int t = 1;
+    for (; t + 1 < ntiles; t += 2) {
+        step(t, pB, pA);
+        step(t + 1, pA, pB);
+    }
+    if (t < ntiles) step(t, pB, pA);
+
+    // ---- PV of the last tile (its first three fragments are in the ring)
+    auto last_pv = [&](const u32x4 (&p)[2][4]) __attribute__((always_inline)) {
+        const uint32_t vt = vslot_of(ntiles - 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int sl2 = 0; sl2 < 32; ++sl2) {
+            const int f = sl2 >> 1, nb = sl2 & 1;
+            if (nb == 0 && f + 3 < 16) fr[(f + 3) & 3] = vfrag(vt, f + 3);
+            mfma_pv(o[nb][f & 3], fr[f & 3], pv_operand(p, nb, f >> 2));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if ((ntiles - 1) & 1) last_pv(pB);
+    else last_pv(pA);
+    LR_WAIT_VMCNT(0);   // the last steps' loads (into the dummy area) have landed before the workgroup ends
+    fence_o(o);
+
+    // ---- epilogue: O / l -> bf16 rows. A row whose P overflowed the fixed reference (l or O not finite) marks its
+    // wave's first row with a NaN; the second launch recomputes such blocks with a running max.
+    bool overflow = false;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int qrow = wrow0 + 32 * nb + n;
+        const float l = wave_pair_sum(ls[nb]);
+        const float inv = 1.0f / l;
+        bool bad = !__builtin_isfinite(l);
+        if (qrow < a.W) {
+            uint16_t* dst = a.out + (int64_t)qrow * a.o_rs + head * D + 4 * hf;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) {
+                    const float y0 = o[nb][db][4 * gg] * inv, y1 = o[nb][db][4 * gg + 1] * inv;
+                    const float y2 = o[nb][db][4 * gg + 2] * inv, y3 = o[nb][db][4 * gg + 3] * inv;
+                    bad = bad || !__builtin_isfinite(y0) || !__builtin_isfinite(y1) || !__builtin_isfinite(y2) ||
+                          !__builtin_isfinite(y3);
+                    u32x2 w;
+                    w[0] = pack_bf16x2(y0, y1);
+                    w[1] = pack_bf16x2(y2, y3);
+                    *reinterpret_cast<u32x2*>(dst + 32 * db + 8 * gg) = w;
+                }
+        }
+        overflow = overflow || bad;
+    }
+    if (__builtin_amdgcn_ballot_w64(overflow) && lane == 0 && wrow0 < a.W)
+        a.out[(int64_t)wrow0 * a.o_rs + head * D] = 0x7fc0;   // bf16 quiet NaN
+}
+
+template <int QK, bool VT>
+hipError_t launch_pair_t(const AttnArgs& a, hipStream_t stream) {
+    const int64_t nqb = (a.W + PBM - 1) / PBM;
+    const int64_t blocks = nqb * a.H;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_pair_kernel<QK, VT>), dim3((unsigned)blocks), dim3(PW * 64), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_pair(const AttnArgs& a, int qk, bool v_t, hipStream_t stream) {
+    if (v_t) {
+        switch (qk) {
+            case TABLE_NONE: return launch_pair_t<TABLE_NONE, true>(a, stream);
+            case TABLE_COSSIN_F32: return launch_pair_t<TABLE_COSSIN_F32, true>(a, stream);
+            case TABLE_MAT2_BF16: return launch_pair_t<TABLE_MAT2_BF16, true>(a, stream);
+            case TABLE_MAT2_F32: return launch_pair_t<TABLE_MAT2_F32, true>(a, stream);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    if (qk == QK_PLAIN) return launch_pair_t<QK_PLAIN, false>(a, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace lr

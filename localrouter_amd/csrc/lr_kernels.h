@@ -60,13 +60,17 @@ enum AttnConfig : int {
     ATTN_CFG_PIPE_W4 = 2,      // pipelined kernel, 4 waves x 32 queries: 128-query blocks
     ATTN_CFG_REGSTAGE_W8 = 3,  // register-staged kernel, 8 waves x 32 queries
     ATTN_CFG_PINGPONG_W8 = 4,  // ping-pong kernel: two wave groups alternating MFMA and VALU clusters
-    ATTN_CFG_WIDE_W4 = 5,      // pipelined kernel, 4 waves x 64 queries: 256-query blocks, one wave per SIMD
-    ATTN_CFG_LAST = 5,
+    ATTN_CFG_WIDE_W4 = 5,      // pipelined kernel, 4 waves x 64 queries, 32-key tiles: 256-query blocks, one wave per SIMD
+    ATTN_CFG_PAIR_W4 = 6,      // pipelined kernel, 4 waves x 64 queries, 64-key tiles, scheduled: 256-query blocks
+    ATTN_CFG_LAST = 6,
 };
 
 // v_t: values come as packed V^T tiles (VPackArgs layout; a.v = the [HK][ntiles] tile array, a.v_hs = ntiles*8192)
 // instead of rows; only the pipelined 64-key-tile configurations (AUTO, PIPE_W8, PIPE_W4) read that layout.
 hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config, hipStream_t stream);
+// The 64-queries-per-wave kernel (attn_pair.hip): qk = a TableKind (queries normalised and rotated in registers, values
+// as packed V^T tiles when v_t) or -1 (plain queries, values as rows).
+hipError_t launch_pair(const AttnArgs& a, int qk, bool v_t, hipStream_t stream);
 bool attention_config_reads_vt(int config);
 hipError_t launch_rms_rope(const RopeArgs& a, hipStream_t stream);
 int attention_block_rows(int config);

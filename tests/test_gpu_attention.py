@@ -18,7 +18,7 @@ torch = pytest.importorskip("torch")
 
 from localrouter_amd import ops  # noqa: E402
 
-CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4]
+CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4, ops.CFG_PAIR_W4]
 
 
 def _qkv(seed, W, nk, H, HK):
@@ -51,6 +51,39 @@ def test_attention_causal(cfg, W, nk, p0):
     out = ops.attention(to_dev(q), to_dev(k), to_dev(v), causal=True, p0=p0, config=cfg)
     torch.cuda.synchronize()
     assert_close(from_dev(out), _ref(q, k, v, causal=True, p0=p0), what=f"cfg{cfg}")
+
+
+@pytest.mark.parametrize("cfg", CONFIGS)
+def test_attention_rising_scores(cfg):
+    """Scores that rise along the keys by ~65 in the exp2 domain force the running reference up many times (the lazy
+    rescale by more than 2^8); queries with the opposite sign keep their maximum in the first tile."""
+    print(f"\n[attention rising] cfg={cfg}", flush=True)
+    W, nk, H = 96, 300, 2
+    sign = np.where(np.arange(W) % 3 == 0, -1.0, 1.0).astype(np.float32)
+    q = oracle.f32_to_bf16(np.broadcast_to((2.0 * sign)[:, None, None], (W, H, 128)).copy())
+    kk = oracle.f32_to_bf16(np.broadcast_to((2.0 * np.arange(nk) / nk)[:, None, None].astype(np.float32),
+                                            (nk, H, 128)).copy())
+    v = oracle.synth_bf16(14, 3, (nk, H, 128))
+    out = ops.attention(to_dev(q), to_dev(kk), to_dev(v), config=cfg)
+    torch.cuda.synchronize()
+    assert_close(from_dev(out), _ref(q, kk, v), what=f"cfg{cfg}")
+
+
+@pytest.mark.parametrize("cfg", CONFIGS)
+def test_attention_overflowing_scores(cfg):
+    """Scores that rise along the keys by ~260 in the exp2 domain: exp2 relative to the first tile's maximum overflows
+    fp32, so a kernel must raise its reference (running max) or recompute the block (the 64-query-per-wave kernel's
+    second launch)."""
+    print(f"\n[attention overflow] cfg={cfg}", flush=True)
+    W, nk, H = 300, 300, 2
+    sign = np.where(np.arange(W) % 4 == 0, -1.0, 1.0).astype(np.float32)
+    q = oracle.f32_to_bf16(np.broadcast_to((4.0 * sign)[:, None, None], (W, H, 128)).copy())
+    kk = oracle.f32_to_bf16(np.broadcast_to((4.0 * np.arange(nk) / nk)[:, None, None].astype(np.float32),
+                                            (nk, H, 128)).copy())
+    v = oracle.synth_bf16(15, 3, (nk, H, 128))
+    out = ops.attention(to_dev(q), to_dev(kk), to_dev(v), config=cfg)
+    torch.cuda.synchronize()
+    assert_close(from_dev(out), _ref(q, kk, v), what=f"cfg{cfg}")
 
 
 def test_attention_keys_past_nkeys_ignored():
@@ -207,6 +240,32 @@ def test_fused_small(cfg, kind, pairing, rot, causal, p0, n_pre, HK):
     assert_close(from_dev(out), ref, what="fused")
 
 
+def test_fused_overflowing_scores():
+    """Large norm weights (5.0) make the normalised scores span about +-400 in the exp2 domain. Keys turn from opposing
+    u to agreeing with it along the sequence; query rows 0-63, 128-191, ... point along u (relative to the first tile's
+    maximum their later P overflow fp32), the others along -u (their maximum is in the first tile). The 64-query-per-
+    wave kernel must give the running-max kernel's result on both kinds of rows (both see the same bf16-rounded
+    normalised operands; at these score magnitudes the oracle's unrounded operands differ by more than the bar)."""
+    print("\n[fused overflow]", flush=True)
+    Sq, Sk, H = 260, 330, 2
+    u = np.zeros(128, np.float32); u[::2] = 1.0
+    w_ = np.zeros(128, np.float32); w_[1::2] = 1.0
+    sgn = np.where((np.arange(Sq) // 64) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    q = oracle.f32_to_bf16(np.broadcast_to((sgn[:, None] * u[None, :])[:, None, :], (Sq, H, 128)).copy())
+    a_ = (2.0 * np.arange(Sk) / Sk - 1.0).astype(np.float32)
+    kf = a_[:, None] * u[None, :] + 0.1 * w_[None, :]
+    k = oracle.f32_to_bf16(np.broadcast_to(kf[:, None, :], (Sk, H, 128)).copy())
+    v = oracle.synth_bf16(32, 3, (Sk, H, 128))
+    wq = torch.full((128,), 5.0, dtype=torch.float32, device="cuda")
+    wk = torch.full((128,), 5.0, dtype=torch.float32, device="cuda")
+    outs = []
+    for cfg in (ops.CFG_AUTO, ops.CFG_PAIR_W4):
+        o = ops.joint_attention(to_dev(q), to_dev(k), to_dev(v), q_norm=wq, k_norm=wk, table_kind=0, config=cfg)
+        torch.cuda.synchronize()
+        outs.append(from_dev(o))
+    assert_close(outs[1], bf16_f32(outs[0]), what="fused overflow: pair vs running max")
+
+
 # ------------------------------------------------------------------------------------------ the two stages
 @pytest.mark.parametrize("Sk,HK,n_pre", [(190, 2, 0), (64, 1, 0), (1, 1, 0), (200, 3, 50)])
 def test_kv_prepare_layout_and_prepared_equals_fused(Sk, HK, n_pre):
@@ -239,7 +298,7 @@ def test_kv_prepare_layout_and_prepared_equals_fused(Sk, HK, n_pre):
         assert np.allclose(bf16_f32(keys[:, n_pre:].transpose(1, 0, 2)), kref, rtol=1e-2, atol=1e-2)
     tq = (_dev_table(qa), _dev_table(qb))
     outs = []
-    for cfg in (ops.CFG_AUTO, ops.CFG_PIPE_W4):
+    for cfg in (ops.CFG_AUTO, ops.CFG_PIPE_W4, ops.CFG_PAIR_W4):
         o = ops.joint_attention_prepared(to_dev(q), ws, Sk, HK, q_table=tq, config=cfg)
         f = ops.joint_attention(to_dev(q), to_dev(k), to_dev(v), q_table=tq, k_table=(_dev_table(ka), _dev_table(kb)),
                                 n_pre=n_pre, config=cfg)

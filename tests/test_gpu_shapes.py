@@ -42,15 +42,16 @@ def _oracle_rows(qb, kb, vb, cos, sin, rows):
     return oracle.attention(qh, kh, oracle.bf16_to_f32(vb), precise=False)
 
 
+@pytest.mark.parametrize("cfg", [ops.CFG_AUTO, ops.CFG_PAIR_W4])
 @pytest.mark.parametrize("name,n_text,grid", [("cfg1", 256, (32, 32)), ("cfg2", 512, (64, 64))])
-def test_baseline_image_shapes_all_rows(name, n_text, grid):
+def test_baseline_image_shapes_all_rows(name, n_text, grid, cfg):
     cos, sin = rope.grid2d_table(n_text, *grid)
     S = cos.shape[0]
-    print(f"\n[{name}] S={S} H={H}", flush=True)
+    print(f"\n[{name}] S={S} H={H} config={cfg}", flush=True)
     qb = oracle.synth_bf16(100, 1, (S, H, 128))
     kb = oracle.synth_bf16(100, 2, (S, H, 128))
     vb = oracle.synth_bf16(100, 3, (S, H, 128))
-    out = from_dev(_run_fused(to_dev(qb), to_dev(kb), to_dev(vb), cos, sin))
+    out = from_dev(_run_fused(to_dev(qb), to_dev(kb), to_dev(vb), cos, sin, config=cfg))
     ref = _oracle_rows(qb, kb, vb, cos, sin, np.arange(S))
     mx, mn = assert_close(out, ref, what=name)
     print(f"[{name}] max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
@@ -121,7 +122,8 @@ def test_default_config_matches_every_config_bitwise_class():
     kb = oracle.synth_bf16(106, 2, (S, 4, 128))
     vb = oracle.synth_bf16(106, 3, (S, 4, 128))
     outs = []
-    for cfg in (ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4):
+    for cfg in (ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4,
+                ops.CFG_PAIR_W4):
         tc, ts = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
         o = ops.joint_attention(to_dev(qb), to_dev(kb), to_dev(vb), table_kind=ops.TABLE_COSSIN_F32,
                                 q_table=(tc, ts), config=cfg)
