@@ -57,7 +57,8 @@ typedef struct ihipStream_t* lr_stream_t;
 #define LR_WEIGHT_F32 1
 #define LR_WEIGHT_BF16 2
 
-/* Attention tile configurations for the _ex entry points (0 = the library's choice). */
+/* Attention tile configurations for the _ex entry points (0 = the library's choice: LR_ATTN_CFG_PAIR_W4 for the fused
+ * and prepared calls, LR_ATTN_CFG_PIPE_W8 for attention over value rows). */
 #define LR_ATTN_CFG_AUTO 0
 #define LR_ATTN_CFG_PIPE_W8 1      /* 256 queries per workgroup (8 waves x 32): direct-to-LDS K/V ring, next tile's
                                       QK^T overlapped with the current tile's softmax */
@@ -69,7 +70,9 @@ typedef struct ihipStream_t* lr_stream_t;
                                       fragment feeds two MFMAs, one wave per SIMD */
 #define LR_ATTN_CFG_PAIR_W4 6      /* 256 queries per workgroup (4 waves x 64), 64-key tiles in a 4-stage direct-to-LDS
                                       ring, explicit MFMA schedule: every K/V^T operand fragment feeds two MFMAs,
-                                      one wave per SIMD */
+                                      one wave per SIMD; softmax against a fixed reference (the first key tile's
+                                      maximum), blocks whose sums overflowed it recomputed by a second launch of the
+                                      PIPE_W8 kernel */
 
 int lr_attn_abi_version(void);
 
@@ -151,8 +154,8 @@ int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v
  *   lr_joint_kv_prepare         RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre), rows j < n_pre
  *                               copied, into the workspace's keys; v [Sk][HK][128] packed into its V^T tiles;
  *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated in registers) over that workspace.
- *                               config: LR_ATTN_CFG_AUTO, _PIPE_W8 or _PIPE_W4 (the configurations that read V^T
- *                               tiles; the others are reached through lr_joint_attention_fused_ex).
+ *                               config: LR_ATTN_CFG_AUTO, _PIPE_W8, _PIPE_W4 or _PAIR_W4 (the configurations that
+ *                               read V^T tiles; the others are reached through lr_joint_attention_fused_ex).
  * Useful when keys and values are reused (a cached prefix) or to time the stages separately.
  */
 int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,

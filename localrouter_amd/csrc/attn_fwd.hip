@@ -1094,7 +1094,10 @@ hipError_t launch_vt(const AttnArgs& a, int config, hipStream_t stream) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config, hipStream_t stream) {
-    if (config == ATTN_CFG_AUTO) config = ATTN_CFG_PIPE_W8;
+    // the library's choice: the 64-query-per-wave kernel where queries are fused and values are packed V^T tiles (the
+    // joint-attention path; measured at least as fast at every BASELINE shape), the 32-query-per-wave pipelined kernel
+    // for plain attention over value rows
+    if (config == ATTN_CFG_AUTO) config = v_t ? ATTN_CFG_PAIR_W4 : ATTN_CFG_PIPE_W8;
     if (v_t) {
         if (!fuse_q) return hipErrorInvalidValue;
         switch (a.table_kind) {

@@ -24,10 +24,13 @@
 // (P(t) is written while P(t-1) is consumed). K and V^T tiles stream through a 4-stage LDS ring by direct
 // global->LDS loads; the first three fragments of the next step are read before the step-closing barrier.
 //
-// Softmax reference. The running reference m of each query is an integer (ceil of a tile max, in the exp2 domain)
-// and only rises when a tile's max exceeds it by more than 2^8. A rise by d multiplies O, the row sum and the pending
-// P(t-1) by 2^-d, which is exact for the bf16 P (an exponent change), so every P and l of a row keep sharing one
-// reference that cancels in O / l.
+// Softmax reference. Each query's reference m is the ceil of its exact maximum over the first key tile (exp2 domain)
+// and stays fixed: P = exp2(s - m), folded into the score MFMAs (their accumulator starts at -m), with no running max,
+// no rescaling and no per-score VALU op. Softmax is shift-invariant, so this is exact as long as every P, the row sums
+// and O stay finite; P can exceed 1 by up to 2^127 before that fails, i.e. only when a later key scores ~128 (exp2
+// domain) above the first tile's maximum. The epilogue checks l and O of every row; a wave with a row that is not
+// finite marks its first row with a NaN, and a second launch (the running-max kernel of attn_fwd.hip, over the same
+// 256-query blocks) recomputes exactly the marked blocks.
 #include "lr_common.h"
 #include "lr_kernels.h"
 
@@ -160,20 +163,14 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         dma16_buf(rs, voff[j], dst + (uint32_t)(2 * PW * 512 * j));
     };
 
-    // ---- prologue loads: K(0..3), V(0..1), then the queries (their latency overlaps the ring's)
-#pragma unroll
-    for (int i = 0; i < PNS; ++i) {
-        const u32x4 rs = k_rsrc(i);
-        const uint32_t dst = lds_dst(kr_lds, i);
+    // ---- prologue loads: K(0), then the queries, then the rest of the ring (K(1..3), V(0..1)). The queries' loads
+    // are waited for with vmcnt counts that also cover every earlier load: only K(0), which S(0) needs next, is
+    // issued before them; the rest of the ring lands while S(0) and the first P are computed.
+    {
+        const u32x4 rs = k_rsrc(0);
+        const uint32_t dst = lds_dst(kr_lds, 0);
 #pragma unroll
         for (int j = 0; j < PLOADS; ++j) dma_k(rs, dst, j);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const u32x4 rs = v_rsrc(i);
-        const uint32_t dst = lds_dst(vr_lds, i);
-#pragma unroll
-        for (int j = 0; j < PLOADS; ++j) dma_v(rs, dst, j);
     }
     bf16x8 qa[2][8];   // AGPR-resident B operands of S^T = K Q^T
     {
@@ -189,6 +186,20 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
             for (int ks = 0; ks < 8; ++ks) asm volatile("; q -> agpr" : "=a"(qa[nb][ks]) : "0"(qv[ks]));
             fence_q(qa[nb]);   // the AGPR writes above land before the first MFMA reads them
         }
+    }
+#pragma unroll
+    for (int i = 1; i < PNS; ++i) {
+        const u32x4 rs = k_rsrc(i);
+        const uint32_t dst = lds_dst(kr_lds, i);
+#pragma unroll
+        for (int j = 0; j < PLOADS; ++j) dma_k(rs, dst, j);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const u32x4 rs = v_rsrc(i);
+        const uint32_t dst = lds_dst(vr_lds, i);
+#pragma unroll
+        for (int j = 0; j < PLOADS; ++j) dma_v(rs, dst, j);
     }
 
     // ---- per-lane LDS byte offsets. K fragment (k-step ks, 32-key block mb) of a tile: row 32 mb + key_perm(n),
@@ -225,7 +236,7 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     auto kslot_of = [&](int t) __attribute__((always_inline)) { return kr_lds + (uint32_t)((t % PNS) * PTILE * 2); };
     auto vslot_of = [&](int t) __attribute__((always_inline)) { return vr_lds + (uint32_t)((t % PNS) * PTILE * 2); };
 
-    LR_WAIT_VMCNT(0);
+    LR_WAIT_VMCNT(5 * PLOADS);   // K(0) has landed; K(1..3), V(0..1) may still be in flight
     block_barrier();
 
     // ---- S(0) = K(0) Q^T
@@ -291,7 +302,8 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[nb][db] = f32x16{};
-    block_barrier();   // every wave is done with K slot 0 before step 0 refills it
+    LR_WAIT_VMCNT(4 * PLOADS);   // K(1) has landed (step 0 reads it from its first slot)
+    block_barrier();             // ... in every wave; and every wave is done with K slot 0 before step 0 refills it
 
     const bf16x2 ones2 = {(bf16)1.0f, (bf16)1.0f};
     u32x4 pA[2][4], pB[2][4];   // P double buffer: packed bf16 pairs, [query block][16-key step kk][j]
