@@ -80,6 +80,11 @@ __device__ __forceinline__ void fence_q(bf16x8 (&q)[8]) {
                  "+a"(q[7]));
 }
 
+template <bool B>
+struct BoolTag {
+    static constexpr bool value = B;
+};
+
 constexpr int PW = 4;                 // waves per workgroup
 constexpr int PBM = 64 * PW;          // queries per workgroup
 constexpr int PNS = 4;                // ring stages
@@ -134,27 +139,34 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         }
     }
     const uint32_t kr_lds = lds_addr(Kr), vr_lds = lds_addr(Vr), dummy_lds = lds_addr(Dummy);
-    // descriptor of rows key0.. of a [rows][row_elems] bf16 array at base (row stride rs elements); nothing past nkeys
-    auto rows_rsrc = [&](const uint16_t* base, int64_t rs, int t) __attribute__((always_inline)) {
-        const int key0 = t * BN;
-        const uint64_t addr = (uint64_t)(uintptr_t)(base + (int64_t)key0 * rs);
-        const int64_t valid = t < ntiles ? (int64_t)(a.nkeys - 1 - key0) * rs * 2 + 2 * D : 0;
-        return u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xffffu,
-                     (uint32_t)(valid < 0xffffffffLL ? valid : 0xffffffffLL), 0x00020000u};
+    // Descriptors of tile t of a [rows][row_elems] bf16 array (row stride rs elements). The tiles are loaded in order,
+    // so the base address advances by one tile per call. The record count (bytes from the base) is unlimited for a
+    // whole tile, ends at the last valid key row for the last tile, and is 0 past it.
+    struct TileStream {
+        uint64_t addr, step;
+        uint32_t last_rec;
     };
+    auto rows_stream = [&](const uint16_t* base, int64_t rs) __attribute__((always_inline)) {
+        const int64_t last = (int64_t)(a.nkeys - 1 - (ntiles - 1) * BN) * rs * 2 + 2 * D;
+        return TileStream{(uint64_t)(uintptr_t)base, (uint64_t)(BN * rs * 2),
+                          (uint32_t)(last < 0xffffffffLL ? last : 0xffffffffLL)};
+    };
+    auto next_rsrc = [&](TileStream& ts, int t) __attribute__((always_inline)) {
+        const uint64_t addr = ts.addr;
+        ts.addr += ts.step;
+        const uint32_t rec = t < ntiles - 1 ? 0xffffffffu : t == ntiles - 1 ? ts.last_rec : 0u;
+        return u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xffffu, rec, 0x00020000u};
+    };
+    TileStream kst = rows_stream(kbase, a.k_rs);
+    // packed V^T tiles are whole (zero past nkeys)
+    TileStream vst = VT ? TileStream{(uint64_t)(uintptr_t)vbase, 2u * PTILE, 2u * PTILE} : rows_stream(vbase, a.v_rs);
     // this wave's LDS base for tile t of a ring (load j adds j * 4 KB); past the last tile, the dummy area
+    const uint32_t wave_lds = (uint32_t)(2 * wave * 512);
     auto lds_dst = [&](uint32_t ring, int t) __attribute__((always_inline)) {
-        return (t < ntiles ? ring + (uint32_t)(2 * (t % PNS) * PTILE) : dummy_lds) + (uint32_t)(2 * wave * 512);
+        return (t < ntiles ? ring + (uint32_t)(2 * (t % PNS) * PTILE) : dummy_lds) + wave_lds;
     };
-    auto k_rsrc = [&](int t) __attribute__((always_inline)) { return rows_rsrc(kbase, a.k_rs, t); };
-    auto v_rsrc = [&](int t) __attribute__((always_inline)) {
-        if constexpr (VT) {   // packed V^T tiles are whole (zero past nkeys)
-            const uint64_t addr = (uint64_t)(uintptr_t)(vbase + (int64_t)t * PTILE);
-            return u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xffffu, t < ntiles ? 2u * PTILE : 0u, 0x00020000u};
-        } else {
-            return rows_rsrc(vbase, a.v_rs, t);
-        }
-    };
+    auto k_rsrc = [&](int t) __attribute__((always_inline)) { return next_rsrc(kst, t); };
+    auto v_rsrc = [&](int t) __attribute__((always_inline)) { return next_rsrc(vst, t); };
     // load j of K / V tile t, from its descriptor and LDS base
     auto dma_k = [&](const u32x4& rs, uint32_t dst, int j) __attribute__((always_inline)) {
         dma16_buf(rs, koff[j], dst + (uint32_t)(2 * PW * 512 * j));
@@ -163,9 +175,9 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         dma16_buf(rs, voff[j], dst + (uint32_t)(2 * PW * 512 * j));
     };
 
-    // ---- prologue loads: K(0), then the queries, then the rest of the ring (K(1..3), V(0..1)). The queries' loads
-    // are waited for with vmcnt counts that also cover every earlier load: only K(0), which S(0) needs next, is
-    // issued before them; the rest of the ring lands while S(0) and the first P are computed.
+    // ---- prologue loads: K(0), then the queries, then the rest of the ring (K(1), V(0), V(1), K(2), K(3)). The
+    // queries' loads are waited for with vmcnt counts that also cover every earlier load: only K(0), which S(0) needs
+    // next, is issued before them; the rest of the ring lands while S(0) and the first P are computed.
     {
         const u32x4 rs = k_rsrc(0);
         const uint32_t dst = lds_dst(kr_lds, 0);
@@ -187,19 +199,18 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
             fence_q(qa[nb]);   // the AGPR writes above land before the first MFMA reads them
         }
     }
+    // K(1), V(0), V(1), K(2), K(3): the step-closing waits count on V(1) being older than K(3)
 #pragma unroll
-    for (int i = 1; i < PNS; ++i) {
-        const u32x4 rs = k_rsrc(i);
-        const uint32_t dst = lds_dst(kr_lds, i);
+    for (int i = 0; i < 5; ++i) {
+        const bool is_v = i == 1 || i == 2;
+        const int tt = i == 0 ? 1 : i - 1;
+        const u32x4 rs = is_v ? v_rsrc(tt) : k_rsrc(tt);
+        const uint32_t dst = lds_dst(is_v ? vr_lds : kr_lds, tt);
 #pragma unroll
-        for (int j = 0; j < PLOADS; ++j) dma_k(rs, dst, j);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const u32x4 rs = v_rsrc(i);
-        const uint32_t dst = lds_dst(vr_lds, i);
-#pragma unroll
-        for (int j = 0; j < PLOADS; ++j) dma_v(rs, dst, j);
+        for (int j = 0; j < PLOADS; ++j) {
+            if (is_v) dma_v(rs, dst, j);
+            else dma_k(rs, dst, j);
+        }
     }
 
     // ---- per-lane LDS byte offsets. K fragment (k-step ks, 32-key block mb) of a tile: row 32 mb + key_perm(n),
@@ -236,7 +247,7 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     auto kslot_of = [&](int t) __attribute__((always_inline)) { return kr_lds + (uint32_t)((t % PNS) * PTILE * 2); };
     auto vslot_of = [&](int t) __attribute__((always_inline)) { return vr_lds + (uint32_t)((t % PNS) * PTILE * 2); };
 
-    LR_WAIT_VMCNT(5 * PLOADS);   // K(0) has landed; K(1..3), V(0..1) may still be in flight
+    LR_WAIT_VMCNT(5 * PLOADS);   // K(0) and the queries have landed; K(1..3), V(0..1) may still be in flight
     block_barrier();
 
     // ---- S(0) = K(0) Q^T
@@ -254,22 +265,21 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         }
 
     const float c = a.c;
-    auto needs_mask = [&](int t) __attribute__((always_inline)) {
-        const int key0 = t * BN;
-        return key0 + BN > a.nkeys || (a.causal && key0 + BN - 1 > a.p0 + wrow0);
-    };
-    auto mask_tile = [&](int t) __attribute__((always_inline)) {
-        const int key0 = t * BN;
+    // the tiles from t_mask on have keys past nkeys or, causal, past some query of this wave
+    int t_mask = a.nkeys / BN;
+    if (a.causal) t_mask = min(t_mask, (a.p0 + wrow0 - (BN - 1)) >= 0 ? (a.p0 + wrow0 - (BN - 1)) / BN + 1 : 0);
+    auto needs_mask = [&](int t) __attribute__((always_inline)) { return t >= t_mask; };
+    // Register r of score tile (nb, mb) holds key t BN + 32 mb + 8 hf + c(r), c(r) = 16 (r >> 3) + (r & 7), of query
+    // row wrow0 + 32 nb + n. It is valid iff c(r) < lim: the compile-time c(r) against one lane value per tile.
+    auto mask_block = [&](int t, int mb) __attribute__((always_inline)) {
+        const int key0 = t * BN + 32 * mb + 8 * hf;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int pos = a.p0 + wrow0 + 32 * nb + n;
+            int lim = a.nkeys - key0;
+            if (a.causal) lim = min(lim, a.p0 + wrow0 + 32 * nb + n - key0 + 1);
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = key0 + 32 * mb + 16 * (r >> 3) + 8 * hf + (r & 7);
-                    if (!(key < a.nkeys && (!a.causal || key <= pos))) s[nb][mb][r] = -INFINITY;
-                }
+            for (int r = 0; r < 16; ++r)
+                if (!(16 * (r >> 3) + (r & 7) < lim)) s[nb][mb][r] = -INFINITY;
         }
     };
     auto block_max = [&](int nb, int mb) __attribute__((always_inline)) {
@@ -282,7 +292,10 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     // ---- the reference: ceil of tile 0's exact max (the exp2 domain), fixed for the whole call. Later tiles' P are
     // exp2(s - m) with no running max: exact as long as they stay finite, which the epilogue verifies
     fence_s(s);
-    if (needs_mask(0)) mask_tile(0);
+    if (needs_mask(0)) {
+        mask_block(0, 0);
+        mask_block(0, 1);
+    }
     float m_used[2], ls[2] = {0.0f, 0.0f};
     f32x16 negm[2];   // FOLD: -m in every slot, the initial accumulator of the score MFMAs
 #pragma unroll
@@ -305,24 +318,31 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     LR_WAIT_VMCNT(4 * PLOADS);   // K(1) has landed (step 0 reads it from its first slot)
     block_barrier();             // ... in every wave; and every wave is done with K slot 0 before step 0 refills it
 
-    const bf16x2 ones2 = {(bf16)1.0f, (bf16)1.0f};
     u32x4 pA[2][4], pB[2][4];   // P double buffer: packed bf16 pairs, [query block][16-key step kk][j]
 
-    // P word (nb, kk, j) of S(t): keys 16 kk + 8 hf + 2 j, +1 of the 64-key tile
-    auto exp_word = [&](u32x4 (&p)[2][4], int nb, int kk, int j) __attribute__((always_inline)) {
-        const int mb = kk >> 1, r = 8 * (kk & 1) + 2 * j;
+    // P word w (0..15) of key block mb: (nb, kk, j) = (w / 8, 2 mb + (w / 4) % 2, w % 4), keys 16 kk + 8 hf + 2 j, +1
+    // of the tile, from score registers r, r + 1 of tile (nb, mb), r = 8 ((w / 4) % 2) + 2 j. A word takes three
+    // stages in consecutive slots, so that no instruction waits on the one before it: E (two exp2), C (bf16 pack into
+    // the P buffer, and the pair's fp32 sum), D (the pair sum into the row sum). The row sum is over the fp32 P, as
+    // the reference's (attention.cu:403-407); the PV product takes P rounded to bf16 (attention.cu:418-424).
+    float e0, e1, es;
+    auto stage_e = [&](int mb, int w) __attribute__((always_inline)) {
+        const int nb = w >> 3, r = 8 * ((w >> 2) & 1) + 2 * (w & 3);
         const float x0 = s[nb][mb][r], x1 = s[nb][mb][r + 1];
-        const float e0 = FOLD ? x0 : fmaf(x0, c, -m_used[nb]);
-        const float e1 = FOLD ? x1 : fmaf(x1, c, -m_used[nb]);
-        uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(e0), __builtin_amdgcn_exp2f(e1));
-        asm volatile("" : "+v"(w));   // computed in this slot: not sunk to its use in the next step
-        p[nb][kk][j] = w;
-        // the row sum of the bf16 P exactly as the PV MFMA consumes it
-        ls[nb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones2, ls[nb], false);
+        e0 = __builtin_amdgcn_exp2f(FOLD ? x0 : fmaf(x0, c, -m_used[nb]));
+        e1 = __builtin_amdgcn_exp2f(FOLD ? x1 : fmaf(x1, c, -m_used[nb]));
+        asm volatile("" ::"v"(e0), "v"(e1));   // computed in this slot, not sunk towards their use
     };
-    // word w (0..15) of key block mb: (nb, kk, j) = (w / 8, 2 mb + (w / 4) % 2, w % 4)
-    auto exp_block_word = [&](u32x4 (&p)[2][4], int mb, int w) __attribute__((always_inline)) {
-        exp_word(p, w >> 3, 2 * mb + ((w >> 2) & 1), w & 3);
+    auto stage_c = [&](u32x4 (&p)[2][4], int mb, int w) __attribute__((always_inline)) {
+        const uint32_t x = pack_bf16x2(e0, e1);
+        es = e0 + e1;
+        asm volatile("" ::"v"(x), "v"(es));
+        p[w >> 3][2 * mb + ((w >> 2) & 1)][w & 3] = x;
+    };
+    auto stage_d = [&](int w) __attribute__((always_inline)) {
+        const int nb = w >> 3;
+        ls[nb] += es;
+        asm volatile("" ::"v"(ls[nb]));
     };
     auto pv_operand = [&](const u32x4 (&p)[2][4], int nb, int kk) __attribute__((always_inline)) {
         return __builtin_bit_cast(bf16x8, p[nb][kk]);
@@ -337,19 +357,23 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         }
     };
 
+    // P(0) of key block 0, words 0-10 (the steps carry the rest)
+#pragma unroll
+    for (int w = 0; w < 11; ++w) {
+        stage_e(0, w);
+        stage_c(pA, 0, w);
+        stage_d(w);
+    }
+
     bf16x8 fr[4];   // fragment ring, read 3 fragments ahead
-    // fragment f of a step: V0-V11, K(block 0, ks 0-7), V12-V15, K(block 1, ks 0-7); the first step has no V
-    auto frag_of = [&](bool first, uint32_t kt, uint32_t vt, int f) __attribute__((always_inline)) -> bf16x8 {
-        if (first) return kfrag(kt, f >> 3, f & 7);
+    // fragment f of a step: V0-V11, K(block 0, ks 0-7), V12-V15, K(block 1, ks 0-7)
+    auto frag_is_v = [](int f) { return f < 12 || (f >= 20 && f < 24); };
+    auto frag_of = [&](uint32_t kt, uint32_t vt, int f) __attribute__((always_inline)) -> bf16x8 {
         if (f < 12) return vfrag(vt, f);
         if (f < 20) return kfrag(kt, 0, f - 12);
         if (f < 24) return vfrag(vt, f - 8);
         return kfrag(kt, 1, f - 24);
     };
-    // the first three fragments of step 0 (K(1)); later steps read theirs before the previous step's barrier
-    fr[0] = frag_of(true, kslot_of(1), 0, 0);
-    fr[1] = frag_of(true, kslot_of(1), 0, 1);
-    fr[2] = frag_of(true, kslot_of(1), 0, 2);
 
     // the ring refill of step t, one load per slot 1, 5, ..., 29: V(t+2) loads 0-3, then K(t+4) loads 0-3
     struct Refill {
@@ -365,10 +389,11 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         if (j < 4) dma_v(rf.vrs, rf.vdst, j);
         else dma_k(rf.krs, rf.kdst, j - 4);
     };
-    // end of step t: wait for this wave's loads of earlier steps, read the next step's first fragments (V(t), resident
-    // since the previous barrier), barrier
+    // end of step t: wait for this wave's loads up to V(t+1) (issued in step t-1; only K(t+3) and this step's loads may
+    // stay in flight), read the next step's first fragments (V(t), resident in every wave since the previous barrier),
+    // barrier. Step t+1 reads K(t+2) and V(t), both issued in step t-2, so the K loads get two steps to land.
     auto close_step = [&](int t) __attribute__((always_inline)) {
-        LR_WAIT_VMCNT(2 * PLOADS);
+        LR_WAIT_VMCNT(3 * PLOADS);
         const uint32_t vt = vslot_of(t);
         fr[0] = vfrag(vt, 0);
         fr[1] = vfrag(vt, 1);
@@ -376,36 +401,19 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         block_barrier();
     };
 
-    // ---- step 0: P(0), S(1); no PV yet
-    {
-        const uint32_t kt = kslot_of(1);
-        const Refill rf = refill_of(0);
-        // P(0) of key block 0 before its scores are overwritten
-#pragma unroll
-        for (int w = 0; w < 16; ++w) exp_block_word(pA, 0, w);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int sl2 = 0; sl2 < 32; ++sl2) {
-            const int f = sl2 >> 1, nb = sl2 & 1, mb = f >> 3, ks = f & 7;
-            if (nb == 0 && f + 3 < 16) fr[(f + 3) & 3] = frag_of(true, kt, 0, f + 3);
-            qk(nb, mb, ks, fr[f & 3]);
-            if (sl2 < 16) exp_block_word(pA, 1, sl2);   // P(0) of key block 1 while key block 0 is recomputed
-            refill_slot(rf, sl2);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        close_step(0);
-    }
-
-    // ---- step t >= 1: PV(t-1), P(t), S(t+1), one uninterrupted run of 64 slots:
-    //   slots  0-23  PV fragments V0-V11        | P(t) key block 0 (word w in slot floor(3 w / 2))
-    //   slots 24-39  S(t+1) key block 0          | P(t) key block 1 (word w in slot 24 + floor(3 w / 2))
-    //   slots 40-47  PV fragments V12-V15        |
-    //   slots 48-63  S(t+1) key block 1
-    //   ring loads in slots 1, 5, ..., 29
-    auto step = [&](int t, u32x4 (&pc)[2][4], u32x4 (&pp)[2][4]) __attribute__((always_inline)) {
-        if (needs_mask(t)) {
+    // ---- step t: PV(t-1) (none in the first step), the rest of P(t), S(t+1), and P(t+1) of key block 0 as soon as
+    // its scores are out of the MFMA pipe. One uninterrupted run of 64 slots:
+    //   slots  0-23  PV fragments V0-V11   | P(t) key block 0, words 11-15 (E in slots 0, 2, ..., 8)
+    //   slots 24-39  S(t+1) key block 0    | P(t) key block 1, words 0-15 (E in slots 10, 12, ..., 40)
+    //   slots 40-47  PV fragments V12-V15  | (slot 41) mask S(t+1) key block 0 if the tile needs it
+    //   slots 48-63  S(t+1) key block 1    | P(t+1) key block 0, words 0-10 (E in slots 42, 44, ..., 62)
+    // A word's C and D stages follow its E one and two slots later; word 10 of P(t+1)'s D runs in slot 0 of step t+1.
+    // Ring loads in slots 1, 5, ..., 29. For the last tile, S(t+1) is past every key, so P(t+1) is masked to zeros.
+    auto step = [&](int t, u32x4 (&pc)[2][4], u32x4 (&pn)[2][4], auto first_tag) __attribute__((always_inline)) {
+        constexpr bool FIRST = decltype(first_tag)::value;
+        if (!FIRST && needs_mask(t)) {   // key block 0 of S(t) was masked in the previous step
             fence_s(s);
-            mask_tile(t);
+            mask_block(t, 1);
         }
         const uint32_t kt = kslot_of(t + 1);
         const uint32_t vt = vslot_of(t - 1);
@@ -414,20 +422,33 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
 #pragma unroll
         for (int sl2 = 0; sl2 < 64; ++sl2) {
             const int f = sl2 >> 1, nb = sl2 & 1;
-            if (nb == 0 && f + 3 < 32) fr[(f + 3) & 3] = frag_of(false, kt, vt, f + 3);
-            if (f < 12 || (f >= 20 && f < 24)) {
-                const int i = f < 12 ? f : f - 8;   // V fragment 4 kk + db
-                mfma_pv(o[nb][i & 3], fr[f & 3], pv_operand(pp, nb, i >> 2));
+            if (nb == 0 && f + 3 < 32 && !(FIRST && frag_is_v(f + 3))) fr[(f + 3) & 3] = frag_of(kt, vt, f + 3);
+            if (frag_is_v(f)) {
+                if constexpr (!FIRST) {
+                    const int i = f < 12 ? f : f - 8;   // V fragment 4 kk + db
+                    mfma_pv(o[nb][i & 3], fr[f & 3], pv_operand(pn, nb, i >> 2));
+                }
             } else {
                 const int mb = f < 20 ? 0 : 1, ks = f < 20 ? f - 12 : f - 24;
                 qk(nb, mb, ks, fr[f & 3]);
             }
-            if (sl2 < 24) {
-                const int w = (2 * sl2 + 2) / 3;
-                if (w < 16 && (3 * w) / 2 == sl2) exp_block_word(pc, 0, w);
-            } else if (sl2 < 48) {
-                const int w = (2 * (sl2 - 24) + 2) / 3;
-                if (w < 16 && 24 + (3 * w) / 2 == sl2) exp_block_word(pc, 1, w);
+            // the word whose stage X runs in this slot had its E stage in slot sl2 - X
+            auto word_at = [&](int e_slot, auto&& fn) __attribute__((always_inline)) {
+                if (e_slot < 0 || (e_slot & 1)) return;
+                if (e_slot <= 8) fn(pc, 0, 11 + e_slot / 2);
+                else if (e_slot <= 40) fn(pc, 1, (e_slot - 10) / 2);
+                else fn(pn, 0, (e_slot - 42) / 2);
+            };
+            if (!FIRST && sl2 == 0) stage_d(10);   // D of the last word the previous step started
+            word_at(sl2 - 2, [&](const u32x4 (&)[2][4], int, int w) __attribute__((always_inline)) { stage_d(w); });
+            word_at(sl2 - 1, [&](u32x4 (&p)[2][4], int mb, int w) __attribute__((always_inline)) { stage_c(p, mb, w); });
+            word_at(sl2, [&](u32x4 (&)[2][4], int mb, int w) __attribute__((always_inline)) { stage_e(mb, w); });
+            if (sl2 == 41) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (needs_mask(t + 1)) {
+                    fence_s(s);
+                    mask_block(t + 1, 0);
+                }
             }
             refill_slot(rf, sl2);
             __builtin_amdgcn_sched_barrier(0);
@@ -435,12 +456,13 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         close_step(t);
     };
 
+    step(0, pA, pB, BoolTag<true>{});
     int t = 1;
     for (; t + 1 < ntiles; t += 2) {
-        step(t, pB, pA);
-        step(t + 1, pA, pB);
+        step(t, pB, pA, BoolTag<false>{});
+        step(t + 1, pA, pB, BoolTag<false>{});
     }
-    if (t < ntiles) step(t, pB, pA);
+    if (t < ntiles) step(t, pB, pA, BoolTag<false>{});
 
     // ---- PV of the last tile (its first three fragments are in the ring)
     auto last_pv = [&](const u32x4 (&p)[2][4]) __attribute__((always_inline)) {
