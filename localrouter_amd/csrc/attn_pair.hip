@@ -15,11 +15,12 @@
 // that MFMA or behind a fence_* (wait states that the registers they protect depend on).
 //
 // Per 64-key tile t a wave runs one step of 64 MFMA slots (one wave instruction stream, a sched_barrier per slot):
-//   slots  0-3    O += V(t-1)^T P(t-1), fragments V0-V1   | VALU: max of S(t) key block 1, then the (rare) rescale
-//   slots  4-23   O += V(t-1)^T P(t-1), fragments V2-V11  | VALU: P(t) of key block 0 (exp2, bf16 pack, row sums)
-//   slots 24-39   S(t+1) key block 0 = K(t+1) Q^T         | VALU: P(t) of key block 1
-//   slots 40-47   O += V(t-1)^T P(t-1), fragments V12-V15 |
-//   slots 48-63   S(t+1) key block 1                      | VALU: max of S(t+1) key block 0
+//   slots  0-23   O += V(t-1)^T P(t-1), fragments V0-V11   | VALU: P(t) of key block 0, words 11-15
+//   slots 24-39   S(t+1) key block 0 = K(t+1) Q^T           | VALU: P(t) of key block 1, words 0-15
+//   slots 40-47   O += V(t-1)^T P(t-1), fragments V12-V15   | VALU: P(t+1) of key block 0 from slot 42 on
+//   slots 48-63   S(t+1) key block 1                        | VALU: P(t+1) of key block 0, words 0-10
+// One P word (two keys of one query) every two slots, in three stages one slot apart (exp2; bf16 pack and pair sum;
+// row sum), so that no VALU instruction waits on the one before it and the MFMA issue never waits on the VALU.
 // Scores are single-buffered: a key block's exps finish before the MFMAs that overwrite it start. P is double-buffered
 // (P(t) is written while P(t-1) is consumed). K and V^T tiles stream through a 4-stage LDS ring by direct
 // global->LDS loads; the first three fragments of the next step are read before the step-closing barrier.
@@ -375,16 +376,21 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         return kfrag(kt, 1, f - 24);
     };
 
-    // the ring refill of step t, one load per slot 1, 5, ..., 29: V(t+2) loads 0-3, then K(t+4) loads 0-3
+    // the ring refill of step t, one load per slot 3, 7, ..., 31: V(t+2) loads 0-3, then K(t+4) loads 0-3. Their
+    // descriptors are formed in slots 0 and 2, under the MFMAs, rather than before the step's first MFMA.
     struct Refill {
         u32x4 krs, vrs;
         uint32_t kdst, vdst;
     };
-    auto refill_of = [&](int t) __attribute__((always_inline)) {
-        return Refill{k_rsrc(t + PNS), v_rsrc(t + 2), lds_dst(kr_lds, t + PNS), lds_dst(vr_lds, t + 2)};
-    };
-    auto refill_slot = [&](const Refill& rf, int sl2) __attribute__((always_inline)) {
-        if ((sl2 & 3) != 1 || sl2 >= 32) return;
+    auto refill_slot = [&](Refill& rf, int t, int sl2) __attribute__((always_inline)) {
+        if (sl2 == 0) {
+            rf.vrs = v_rsrc(t + 2);
+            rf.vdst = lds_dst(vr_lds, t + 2);
+        } else if (sl2 == 2) {
+            rf.krs = k_rsrc(t + PNS);
+            rf.kdst = lds_dst(kr_lds, t + PNS);
+        }
+        if ((sl2 & 3) != 3 || sl2 >= 32) return;
         const int j = sl2 >> 2;
         if (j < 4) dma_v(rf.vrs, rf.vdst, j);
         else dma_k(rf.krs, rf.kdst, j - 4);
@@ -408,7 +414,7 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     //   slots 40-47  PV fragments V12-V15  | (slot 41) mask S(t+1) key block 0 if the tile needs it
     //   slots 48-63  S(t+1) key block 1    | P(t+1) key block 0, words 0-10 (E in slots 42, 44, ..., 62)
     // A word's C and D stages follow its E one and two slots later; word 10 of P(t+1)'s D runs in slot 0 of step t+1.
-    // Ring loads in slots 1, 5, ..., 29. For the last tile, S(t+1) is past every key, so P(t+1) is masked to zeros.
+    // Ring loads in slots 3, 7, ..., 31. For the last tile, S(t+1) is past every key, so P(t+1) is masked to zeros.
     auto step = [&](int t, u32x4 (&pc)[2][4], u32x4 (&pn)[2][4], auto first_tag) __attribute__((always_inline)) {
         constexpr bool FIRST = decltype(first_tag)::value;
         if (!FIRST && needs_mask(t)) {   // key block 0 of S(t) was masked in the previous step
@@ -417,7 +423,7 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         }
         const uint32_t kt = kslot_of(t + 1);
         const uint32_t vt = vslot_of(t - 1);
-        const Refill rf = refill_of(t);
+        Refill rf;
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int sl2 = 0; sl2 < 64; ++sl2) {
@@ -450,7 +456,7 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
                     mask_block(t + 1, 0);
                 }
             }
-            refill_slot(rf, sl2);
+            refill_slot(rf, t, sl2);
             __builtin_amdgcn_sched_barrier(0);
         }
         close_step(t);
