@@ -61,7 +61,8 @@ def log(*a):
 
 
 def tables(w):
-    from localrouter_amd import rope
+    """The workload's cos/sin tables, from the library's host RoPE builders (bit-equal to localrouter_amd.rope)."""
+    from localrouter_amd import rope_host as rope
     if w["kind"] == "grid2d":
         return rope.grid2d_table(w["n_text"], w["gh"], w["gw"])
     if w["kind"] == "edit":

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "liblr_attn.so"
-SOURCES = ["attn_fwd.hip", "attn_pair.hip", "rms_rope.hip", "int8_attn.hip", "lr_abi.hip"]
+SOURCES = ["attn_fwd.hip", "attn_pair.hip", "rms_rope.hip", "int8_attn.hip", "lr_abi.hip", "rope_host.cpp"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -35,6 +35,10 @@ HIPCC_FLAGS = [
 # per-source extra flags: the 64-query-per-wave kernel's fully unrolled 64-slot schedule is larger than clang's
 # default limit for `#pragma unroll`, and a partly unrolled schedule would index its register arrays at run time
 EXTRA_FLAGS = {"attn_pair.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]}
+
+# host-only C++ (the RoPE table builders of include/lr_rope.h): the system compiler, no contraction of f64 products
+# and sums into FMAs, so that tables are the same bits as the numpy builders
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-ffp-contract=off"]
 
 
 def hipcc() -> str:
@@ -61,7 +65,10 @@ def build(verbose: bool = False) -> Path:
     objs = []
     for src in SOURCES:
         obj = objdir / (Path(src).stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
+        if src.endswith(".cpp"):
+            cmd = [shutil.which("g++") or "g++", *CXX_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        else:
+            cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), file=sys.stderr)
         _run(cmd)
