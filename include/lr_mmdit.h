@@ -1,0 +1,74 @@
+/* The MMDiT double-stream block forward around the joint attention: plain C ABI, gfx950.
+ *
+ * The reference has no double-stream block (its Qwen engine is the single-stream Qwen 2.1, src/engines/qwen_image/
+ * dit.zig:242-308). This block is this library's own definition, in the standard MMDiT form, with the reference's
+ * elementwise arithmetic where it has one: the 256-d time sinusoid of kernels/cuda/qwen_image/ops.cu:84-99, the
+ * GELU-tanh of ops.cu:48-57 and the gated residual x = fma(a, g, x) of ops.cu:25-31.
+ *
+ *   emb  = sinusoid(t)                                   [256]   (t in [0, 1], scaled by 1000 as the reference)
+ *   temb = silu(emb W_t1^T) W_t2^T                       [D]
+ *   mod_s = silu(temb) W_mod_s^T = shift1 | scale1 | gate1 | shift2 | scale2 | gate2, per stream s in {txt, img}
+ *   per stream:  h = LayerNorm(x_s) (1 + scale1) + shift1;   qkv_s = h W_qkv_s^T                  [rows_s, 3D]
+ *   joint:       rows = txt rows then img rows; per-head QK-RMSNorm (weights q_norm, k_norm) and RoPE (cos/sin
+ *                [S, 64] f32, interleaved pairs) fused into the attention: lr_joint_attention_fused_ex
+ *   per stream:  x_s += gate1 * (attn_s W_out_s^T)
+ *                h = LayerNorm(x_s) (1 + scale2) + shift2;  x_s += gate2 * (gelu_tanh(h W_up_s^T) W_down_s^T)
+ *
+ * Weights are bf16 row-major [out, in] (torch nn.Linear layout), no biases; LayerNorm without affine, eps 1e-6;
+ * activations bf16 between the steps (fp32 inside each kernel and GEMM). The GEMMs are hipBLASLt's (bf16 in and out,
+ * fp32 compute); everything else is this library's HIP kernels.
+ *
+ * Return values follow lr_attn.h: 0 launched, 1 (hipErrorInvalidValue) an argument rejected before any launch, other
+ * hipError_t / hipblasStatus_t failures as returned (a hipBLASLt status is reported as 1000 + the status).
+ */
+#ifndef LR_MMDIT_H
+#define LR_MMDIT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "lr_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One stream's weights (device pointers, bf16 [out, in] row-major). */
+typedef struct lr_mmdit_stream_weights {
+    const void* mod;      /* [6 D, D]  adaLN modulation */
+    const void* qkv;      /* [3 D, D]  q | k | v, heads of 128 in each */
+    const void* out;      /* [D, D]    attention output projection */
+    const void* mlp_up;   /* [F, D] */
+    const void* mlp_down; /* [D, F] */
+} lr_mmdit_stream_weights;
+
+typedef struct lr_mmdit_weights {
+    const void* t1;       /* [D, 256]  time embedding, first linear */
+    const void* t2;       /* [D, D]    time embedding, second linear */
+    const float* q_norm;  /* [128] f32 per-head RMSNorm weights of q (both streams) */
+    const float* k_norm;  /* [128] f32, of k */
+    lr_mmdit_stream_weights txt, img;
+} lr_mmdit_weights;
+
+/* A context: the hipBLASLt handle and the GEMM plans of the shapes seen so far (host memory only). *ctx is set on
+ * success. Call on the device the blocks will run on. */
+int lr_mmdit_create(void** ctx);
+int lr_mmdit_destroy(void* ctx);
+
+/* Device scratch one block call needs, bytes (256-aligned); 0 for an unsupported shape (D not a multiple of 128,
+ * F not a multiple of 8, sizes <= 0). */
+size_t lr_mmdit_workspace_bytes(int n_txt, int n_img, int hidden, int mlp);
+
+/* One block forward, in place on txt [n_txt, D] and img [n_img, D] bf16 (contiguous rows). t: device pointer to one
+ * f32 timestep. cos, sin: device [n_txt + n_img, 64] f32 (text rows first). The first call for a new shape builds
+ * its GEMM plans (hipBLASLt heuristics, host memory); later calls of that shape launch only. Not reentrant per
+ * context: concurrent calls need a context each. */
+int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* img, int n_txt, int n_img, int hidden,
+                        int mlp, const float* t, const float* cos, const float* sin, void* workspace,
+                        size_t workspace_bytes, lr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LR_MMDIT_H */

@@ -17,7 +17,9 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "liblr_attn.so"
-SOURCES = ["attn_fwd.hip", "attn_pair.hip", "rms_rope.hip", "int8_attn.hip", "lr_abi.hip", "rope_host.cpp"]
+SOURCES = ["attn_fwd.hip", "attn_pair.hip", "rms_rope.hip", "int8_attn.hip", "lr_abi.hip", "mmdit.hip", "rope_host.cpp"]
+# libraries the shared object links: hipBLASLt for the MMDiT block's projections and MLP
+LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -74,7 +76,7 @@ def build(verbose: bool = False) -> Path:
         _run(cmd)
         objs.append(str(obj))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, *LIBS, "-o", str(tmp)])
     os.replace(tmp, LIB)
     return LIB
 

@@ -1,0 +1,388 @@
+// The MMDiT double-stream block forward (include/lr_mmdit.h): hipBLASLt GEMMs for the projections and the MLP, the
+// joint attention of this library (norm + RoPE fused), and HBM-bound HIP kernels for the rest: the time sinusoid,
+// SiLU, LayerNorm + adaLN modulation, GELU-tanh and the gated residual. Every kernel reads and writes bf16 rows with
+// 16-byte accesses and computes in fp32.
+//
+// The reference has no double-stream block; its elementwise arithmetic is followed where it has one: the time
+// sinusoid (kernels/cuda/qwen_image/ops.cu:84-99), GELU-tanh in torch's operation order (ops.cu:48-57), the gated
+// residual x = fma(a, g, x) (ops.cu:25-31) and SiLU x / (1 + exp(-x)) (ops.cu:34-39).
+#include <hipblaslt/hipblaslt.h>
+
+#include <cmath>
+#include <map>
+#include <tuple>
+
+#include "../../include/lr_mmdit.h"
+#include "lr_common.h"
+
+namespace lr {
+namespace {
+
+constexpr int EW_THREADS = 256;
+constexpr size_t GEMM_WS = 64u << 20;   // hipBLASLt workspace inside the block's scratch
+constexpr float LN_EPS = 1e-6f;
+
+__device__ __forceinline__ float bf(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t tobf(float f) { return __builtin_bit_cast(uint16_t, (bf16)f); }
+
+// emb[256] from t (ops.cu:84-99): t scaled by 1000 and rounded to bf16, divided by 1000 (reciprocal multiply) and
+// rounded again, times 1000; freq_i = exp(-ln(10000) i / 128); cos for j < 128, sin for j >= 128.
+__global__ void time_sinusoid_kernel(const float* t, uint16_t* emb) {
+    const int j = threadIdx.x, i = j & 127;
+    float tr = bf(tobf(t[0] * 1000.0f));
+    tr = bf(tobf(tr * (1.0f / 1000.0f)));
+    tr = tr * 1000.0f;
+    const float c = -9.210340371976184f;   // -ln(10000)
+    const float freq = expf((c * (float)i) * (1.0f / 128.0f));
+    const float arg = tr * freq;
+    emb[j] = tobf(j < 128 ? cosf(arg) : sinf(arg));
+}
+
+// y = x / (1 + exp(-x)), n elements (small vectors)
+__global__ void silu_kernel(const uint16_t* x, uint16_t* y, int n) {
+    const int i = blockIdx.x * EW_THREADS + threadIdx.x;
+    if (i >= n) return;
+    const float v = bf(x[i]);
+    y[i] = tobf(v / (1.0f + expf(-v)));
+}
+
+struct Chunk8 {
+    float v[8];
+};
+__device__ __forceinline__ Chunk8 load8(const uint16_t* p) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+    Chunk8 c;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        c.v[2 * k] = lo_bf16(w[k]);
+        c.v[2 * k + 1] = hi_bf16(w[k]);
+    }
+    return c;
+}
+__device__ __forceinline__ void store8(uint16_t* p, const Chunk8& c) {
+    u32x4 w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = pack_bf16x2(c.v[2 * k], c.v[2 * k + 1]);
+    *reinterpret_cast<u32x4*>(p) = w;
+}
+
+// Row sums over a workgroup of LN_THREADS: wave butterflies, then the waves' partials through LDS.
+constexpr int LN_THREADS = 256;
+constexpr int LN_MAX_CHUNKS = 4;   // D <= 8 * LN_THREADS * LN_MAX_CHUNKS = 8192
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();   // red is reused by consecutive sums
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < LN_THREADS / 64; ++w) s += red[w];
+    return s;
+}
+
+// out row r (txt rows 0..n_txt-1, then img rows) = LayerNorm(x_r) * (1 + scale) + shift with the row's stream's
+// modulation chunk (shift = mod[which * 3 D .. + D), scale = the next D), two-pass mean and variance in fp32.
+__global__ __launch_bounds__(LN_THREADS) void ln_modulate_kernel(const uint16_t* txt, const uint16_t* img, int n_txt,
+                                                                 int D, const uint16_t* mod_txt,
+                                                                 const uint16_t* mod_img, int which, uint16_t* out) {
+    __shared__ float red[LN_THREADS / 64];
+    const int r = blockIdx.x;
+    const bool is_txt = r < n_txt;
+    const uint16_t* x = is_txt ? txt + (int64_t)r * D : img + (int64_t)(r - n_txt) * D;
+    const uint16_t* mod = (is_txt ? mod_txt : mod_img) + (int64_t)which * 3 * D;
+    const int chunks = D / 8;
+    Chunk8 c[LN_MAX_CHUNKS];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < LN_MAX_CHUNKS; ++k) {
+        const int ch = threadIdx.x + k * LN_THREADS;
+        if (ch < chunks) {
+            c[k] = load8(x + 8 * ch);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += c[k].v[e];
+        }
+    }
+    const float mean = block_sum(s, red) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int k = 0; k < LN_MAX_CHUNKS; ++k) {
+        const int ch = threadIdx.x + k * LN_THREADS;
+        if (ch < chunks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = c[k].v[e] - mean;
+                q += d * d;
+            }
+        }
+    }
+    const float rstd = rsqrtf(block_sum(q, red) / (float)D + LN_EPS);
+    uint16_t* y = out + (int64_t)r * D;
+#pragma unroll
+    for (int k = 0; k < LN_MAX_CHUNKS; ++k) {
+        const int ch = threadIdx.x + k * LN_THREADS;
+        if (ch < chunks) {
+            const Chunk8 sh = load8(mod + 8 * ch), sc = load8(mod + D + 8 * ch);
+            Chunk8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o.v[e] = (c[k].v[e] - mean) * rstd * (1.0f + sc.v[e]) + sh.v[e];
+            store8(y + 8 * ch, o);
+        }
+    }
+}
+
+// x = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in place, torch's order (ops.cu:48-57); n8 chunks of 8.
+__global__ void gelu_tanh_kernel(uint16_t* x, int64_t n8) {
+    const int64_t i = (int64_t)blockIdx.x * EW_THREADS + threadIdx.x;
+    if (i >= n8) return;
+    const float kBeta = (float)(1.4142135623730951 * 1.1283791670955126 * 0.5);
+    const float kKappa = 0.044715f;
+    Chunk8 c = load8(x + 8 * i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float v = c.v[e];
+        const float cube = v * v * v;
+        const float inner = kBeta * fmaf(kKappa, cube, v);
+        c.v[e] = (0.5f * v) * (1.0f + tanhf(inner));
+    }
+    store8(x + 8 * i, c);
+}
+
+// x_r += g * a_r (fma(a, g, x), ops.cu:25-31) for the joint rows, g the row's stream's gate chunk
+// (mod[which * 3 D + 2 D .. + D)); one 8-element chunk per thread.
+__global__ void gated_residual_kernel(uint16_t* txt, uint16_t* img, int n_txt, int n_rows, int D, const uint16_t* a,
+                                      const uint16_t* mod_txt, const uint16_t* mod_img, int which) {
+    const int chunks = D / 8;
+    const int64_t i = (int64_t)blockIdx.x * EW_THREADS + threadIdx.x;
+    if (i >= (int64_t)n_rows * chunks) return;
+    const int r = (int)(i / chunks), ch = (int)(i - (int64_t)r * chunks);
+    const bool is_txt = r < n_txt;
+    uint16_t* x = is_txt ? txt + (int64_t)r * D : img + (int64_t)(r - n_txt) * D;
+    const uint16_t* g = (is_txt ? mod_txt : mod_img) + (int64_t)which * 3 * D + 2 * D;
+    Chunk8 xv = load8(x + 8 * ch);
+    const Chunk8 av = load8(a + (int64_t)r * D + 8 * ch), gv = load8(g + 8 * ch);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xv.v[e] = fmaf(av.v[e], gv.v[e], xv.v[e]);
+    store8(x + 8 * ch, xv);
+}
+
+// ---- hipBLASLt GEMMs: row-major Y[M, N] (row stride ldy) = X[M, K] (row stride ldx) W[N, K]^T, bf16 in and out,
+// fp32 compute. Column-major, that is C (N x M, ldc = ldy) = op(A) op(B) with A = W viewed K x N (lda = K,
+// transposed) and B = X viewed K x M (ldb = ldx).
+struct GemmPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    size_t ws = 0;
+};
+using GemmKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>;   // M, N, K, ldx, ldy
+
+struct Ctx {
+    hipblasLtHandle_t lt = nullptr;
+    std::map<GemmKey, GemmPlan> plans;
+};
+
+int blas_err(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS ? 0 : 1000 + (int)s; }
+
+int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, GemmPlan** out) {
+    const GemmKey key{M, N, K, ldx, ldy};
+    auto it = c.plans.find(key);
+    if (it != c.plans.end()) {
+        *out = &it->second;
+        return 0;
+    }
+    GemmPlan p;
+    int rc;
+    if ((rc = blas_err(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)))) return rc;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K)))) return rc;
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, ldx)))) return rc;
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, ldy)))) return rc;
+    hipblasLtMatmulPreference_t pref;
+    if ((rc = blas_err(hipblasLtMatmulPreferenceCreate(&pref)))) return rc;
+    const uint64_t ws = GEMM_WS;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof ws);
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int found = 0;
+    rc = blas_err(hipblasLtMatmulAlgoGetHeuristic(c.lt, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &found));
+    hipblasLtMatmulPreferenceDestroy(pref);
+    if (rc) return rc;
+    if (found < 1) return 1000 + (int)HIPBLAS_STATUS_NOT_SUPPORTED;
+    p.algo = res[0].algo;
+    p.ws = res[0].workspaceSize;
+    auto ins = c.plans.emplace(key, p);
+    *out = &ins.first->second;
+    return 0;
+}
+
+int gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+         void* ws, hipStream_t s) {
+    GemmPlan* p;
+    int rc = plan_gemm(c, M, N, K, ldx, ldy, &p);
+    if (rc) return rc;
+    const float alpha = 1.0f, beta = 0.0f;
+    return blas_err(hipblasLtMatmul(c.lt, p->desc, &alpha, W, p->la, X, p->lb, &beta, Y, p->lc, Y, p->lc, &p->algo, ws,
+                                    p->ws, s));
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// scratch layout of one block call
+struct Scratch {
+    size_t emb, h1, temb, ts, mod_txt, mod_img, hn, qkv, attn, big, gws, attn_ws, total;
+};
+Scratch layout(int64_t n_txt, int64_t n_img, int64_t D, int64_t F) {
+    const int64_t S = n_txt + n_img;
+    Scratch s;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o += align256(bytes);
+        return at;
+    };
+    s.emb = take(256 * 2);
+    s.h1 = take(D * 2);
+    s.temb = take(D * 2);
+    s.ts = take(D * 2);
+    s.mod_txt = take(6 * D * 2);
+    s.mod_img = take(6 * D * 2);
+    s.hn = take(S * D * 2);          // LayerNorm + modulation, then the out projection, then the MLP output
+    s.qkv = take(S * 3 * D * 2);
+    s.attn = take(S * D * 2);        // attention output
+    s.big = take(S * F * 2);         // MLP hidden
+    s.gws = take(GEMM_WS);
+    s.attn_ws = take(lr_joint_attention_workspace_bytes((int)S, (int)(D / 128)));
+    s.total = o;
+    return s;
+}
+
+}  // namespace
+}  // namespace lr
+
+using namespace lr;
+
+extern "C" {
+
+int lr_mmdit_create(void** ctx) {
+    if (!ctx) return hipErrorInvalidValue;
+    Ctx* c = new Ctx;
+    const int rc = blas_err(hipblasLtCreate(&c->lt));
+    if (rc) {
+        delete c;
+        return rc;
+    }
+    *ctx = c;
+    return 0;
+}
+
+int lr_mmdit_destroy(void* ctx) {
+    if (!ctx) return hipErrorInvalidValue;
+    Ctx* c = static_cast<Ctx*>(ctx);
+    for (auto& kv : c->plans) {
+        hipblasLtMatrixLayoutDestroy(kv.second.la);
+        hipblasLtMatrixLayoutDestroy(kv.second.lb);
+        hipblasLtMatrixLayoutDestroy(kv.second.lc);
+        hipblasLtMatmulDescDestroy(kv.second.desc);
+    }
+    const int rc = blas_err(hipblasLtDestroy(c->lt));
+    delete c;
+    return rc;
+}
+
+size_t lr_mmdit_workspace_bytes(int n_txt, int n_img, int hidden, int mlp) {
+    if (n_txt < 0 || n_img < 0 || n_txt + n_img <= 0 || hidden <= 0 || hidden % 128 || mlp <= 0 || mlp % 8 ||
+        hidden > 8 * LN_THREADS * LN_MAX_CHUNKS)
+        return 0;
+    return layout(n_txt, n_img, hidden, mlp).total;
+}
+
+int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* img, int n_txt, int n_img, int hidden,
+                        int mlp, const float* t, const float* cos, const float* sin, void* workspace,
+                        size_t workspace_bytes, lr_stream_t stream) {
+    const size_t need = lr_mmdit_workspace_bytes(n_txt, n_img, hidden, mlp);
+    if (!ctx || !w || !t || !cos || !sin || !workspace || need == 0 || workspace_bytes < need) return hipErrorInvalidValue;
+    if ((n_txt > 0 && !txt) || (n_img > 0 && !img)) return hipErrorInvalidValue;
+    const void* ptrs[] = {w->t1, w->t2, w->q_norm, w->k_norm, w->txt.mod, w->txt.qkv, w->txt.out, w->txt.mlp_up,
+                          w->txt.mlp_down, w->img.mod, w->img.qkv, w->img.out, w->img.mlp_up, w->img.mlp_down};
+    for (const void* p : ptrs)
+        if (!p) return hipErrorInvalidValue;
+    if ((((uintptr_t)txt | (uintptr_t)img | (uintptr_t)workspace) & 15) != 0) return hipErrorInvalidValue;
+
+    Ctx& c = *static_cast<Ctx*>(ctx);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t D = hidden, F = mlp, S = (int64_t)n_txt + n_img, H = D / 128;
+    const Scratch L = layout(n_txt, n_img, D, F);
+    char* ws = static_cast<char*>(workspace);
+    auto at = [&](size_t off) { return reinterpret_cast<uint16_t*>(ws + off); };
+    uint16_t *emb = at(L.emb), *h1 = at(L.h1), *temb = at(L.temb), *ts = at(L.ts);
+    uint16_t *mod_txt = at(L.mod_txt), *mod_img = at(L.mod_img), *hn = at(L.hn), *qkv = at(L.qkv);
+    uint16_t *attn = at(L.attn), *big = at(L.big);
+    void* gws = ws + L.gws;
+    uint16_t* xt = static_cast<uint16_t*>(txt);
+    uint16_t* xi = static_cast<uint16_t*>(img);
+    int rc;
+#define LR_TRY(expr)                     \
+    do {                                 \
+        if ((rc = (expr)) != 0) return rc; \
+    } while (0)
+#define LR_LAUNCHED() LR_TRY((int)hipGetLastError())
+
+    // time embedding and modulation (vectors: one row)
+    hipLaunchKernelGGL(time_sinusoid_kernel, dim3(1), dim3(256), 0, s, t, emb);
+    LR_LAUNCHED();
+    LR_TRY(gemm(c, emb, 256, w->t1, h1, D, 1, D, 256, gws, s));
+    hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((D + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s, h1, h1,
+                       (int)D);
+    LR_LAUNCHED();
+    LR_TRY(gemm(c, h1, D, w->t2, temb, D, 1, D, D, gws, s));
+    hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((D + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s, temb,
+                       ts, (int)D);
+    LR_LAUNCHED();
+    LR_TRY(gemm(c, ts, D, w->txt.mod, mod_txt, 6 * D, 1, 6 * D, D, gws, s));
+    LR_TRY(gemm(c, ts, D, w->img.mod, mod_img, 6 * D, 1, 6 * D, D, gws, s));
+
+    // attention half: LN + modulation (both streams, one launch), QKV per stream into the joint rows
+    hipLaunchKernelGGL(ln_modulate_kernel, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D, mod_txt,
+                       mod_img, 0, hn);
+    LR_LAUNCHED();
+    if (n_txt > 0) LR_TRY(gemm(c, hn, D, w->txt.qkv, qkv, 3 * D, n_txt, 3 * D, D, gws, s));
+    if (n_img > 0) LR_TRY(gemm(c, hn + (int64_t)n_txt * D, D, w->img.qkv, qkv + (int64_t)n_txt * 3 * D, 3 * D, n_img,
+                               3 * D, D, gws, s));
+    LR_TRY(lr_joint_attention_fused(qkv, qkv + D, qkv + 2 * D, attn, w->q_norm, w->k_norm, LR_TABLE_COSSIN_F32, cos, sin,
+                                    cos, sin, 64, LR_PAIR_INTERLEAVED, 128, 1e-6f, (int)S, (int)S, (int)H, (int)H, 0, 0,
+                                    1.0f / sqrtf(128.0f), 3 * D, 3 * D, 3 * D, D, 0, ws + L.attn_ws,
+                                    lr_joint_attention_workspace_bytes((int)S, (int)H), stream));
+    if (n_txt > 0) LR_TRY(gemm(c, attn, D, w->txt.out, hn, D, n_txt, D, D, gws, s));
+    if (n_img > 0)
+        LR_TRY(gemm(c, attn + (int64_t)n_txt * D, D, w->img.out, hn + (int64_t)n_txt * D, D, n_img, D, D, gws, s));
+    const unsigned res_blocks = (unsigned)((S * (D / 8) + EW_THREADS - 1) / EW_THREADS);
+    hipLaunchKernelGGL(gated_residual_kernel, dim3(res_blocks), dim3(EW_THREADS), 0, s, xt, xi, n_txt, (int)S, (int)D,
+                       hn, mod_txt, mod_img, 0);
+    LR_LAUNCHED();
+
+    // MLP half
+    hipLaunchKernelGGL(ln_modulate_kernel, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D, mod_txt,
+                       mod_img, 1, hn);
+    LR_LAUNCHED();
+    if (n_txt > 0) LR_TRY(gemm(c, hn, D, w->txt.mlp_up, big, F, n_txt, F, D, gws, s));
+    if (n_img > 0)
+        LR_TRY(gemm(c, hn + (int64_t)n_txt * D, D, w->img.mlp_up, big + (int64_t)n_txt * F, F, n_img, F, D, gws, s));
+    const int64_t n8 = S * F / 8;
+    hipLaunchKernelGGL(gelu_tanh_kernel, dim3((unsigned)((n8 + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s,
+                       big, n8);
+    LR_LAUNCHED();
+    if (n_txt > 0) LR_TRY(gemm(c, big, F, w->txt.mlp_down, attn, D, n_txt, D, F, gws, s));
+    if (n_img > 0)
+        LR_TRY(gemm(c, big + (int64_t)n_txt * F, F, w->img.mlp_down, attn + (int64_t)n_txt * D, D, n_img, D, F, gws, s));
+    hipLaunchKernelGGL(gated_residual_kernel, dim3(res_blocks), dim3(EW_THREADS), 0, s, xt, xi, n_txt, (int)S, (int)D,
+                       attn, mod_txt, mod_img, 1);
+    LR_LAUNCHED();
+#undef LR_LAUNCHED
+#undef LR_TRY
+    return 0;
+}
+
+}  // extern "C"

@@ -189,3 +189,23 @@ def test_ops_has_no_cpu_path():
     q = torch.zeros((4, 1, 128), dtype=torch.bfloat16)
     with pytest.raises(ValueError):
         ops.attention(q, q, q)
+
+
+def test_mmdit_abi_on_cpu():
+    """include/lr_mmdit.h: exports, workspace sizes and argument rejection (no GPU call is reached)."""
+    import ctypes
+
+    from localrouter_amd import mmdit
+    text = re.sub(r"/\*.*?\*/", "", mmdit.HEADER.read_text(), flags=re.S)
+    declared = sorted(set(re.findall(r"\b(?:int|size_t)\s+(lr_mmdit_\w+)\s*\(", text)))
+    assert sorted(mmdit.SIGNATURES) == declared
+    L = mmdit.lib()
+    assert mmdit.workspace_bytes(512, 4096, 3072, 12288) > 4608 * 12288 * 2
+    assert mmdit.workspace_bytes(512, 4096, 3000, 12288) == 0        # hidden not a multiple of 128
+    assert mmdit.workspace_bytes(0, 0, 3072, 12288) == 0
+    assert mmdit.workspace_bytes(1, 1, 3072, 12) == 0                 # mlp not a multiple of 8
+    w = mmdit.Weights()
+    assert L.lr_mmdit_block_bf16(None, ctypes.byref(w), None, None, 1, 1, 256, 512, None, None, None, None, 0,
+                                 None) == HIP_ERROR_INVALID_VALUE
+    assert L.lr_mmdit_create(None) == HIP_ERROR_INVALID_VALUE
+    assert L.lr_mmdit_destroy(None) == HIP_ERROR_INVALID_VALUE

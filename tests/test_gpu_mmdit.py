@@ -1,0 +1,108 @@
+"""The MMDiT block forward (include/lr_mmdit.h) on the GPU against its fp32 oracle (oracle/mmdit.py).
+
+Bar: the outputs (bf16 residual streams, values of order 1) within max-abs 6.25e-2 and mean-abs 2e-3 of the oracle,
+which rounds at the same points; and the block's update (output - input) within 3 % relative L2 of the oracle's,
+which a wrong gate, modulation chunk or branch would miss by far. The composition has no reference block to be
+pinned to (parity unpinned beyond the oracle's own checks in tests/test_oracle_mmdit.py)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import oracle  # noqa: E402
+from oracle import mmdit as om  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def _rope(n_txt, gh, gw):
+    from localrouter_amd import rope_host
+    return rope_host.grid2d_table(n_txt, gh, gw)
+
+
+def _to_np_bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _run(n_txt, gh, gw, D, F, std, seed=0, zero_mod=False, tval=0.5):
+    from localrouter_amd import mmdit
+    dev = torch.device("cuda", 0)
+    n_img = gh * gw
+    print(f"mmdit block: n_txt {n_txt} n_img {n_img} D {D} F {F} std {std} zero_mod {zero_mod}", flush=True)
+    w = mmdit.make_weights(D, F, dev, seed=seed, std=std, zero_mod=zero_mod)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1)
+    txt = torch.randn((n_txt, D), generator=g, device=dev).to(torch.bfloat16)
+    img = torch.randn((n_img, D), generator=g, device=dev).to(torch.bfloat16)
+    cos_np, sin_np = _rope(n_txt, gh, gw)
+    cos, sin = torch.from_numpy(cos_np).to(dev), torch.from_numpy(sin_np).to(dev)
+    t = torch.tensor([tval], dtype=torch.float32, device=dev)
+    txt0, img0 = _to_np_bits(txt), _to_np_bits(img)
+    blk = mmdit.MMDiTBlock(w)
+    blk(txt, img, t, cos, sin)
+    torch.cuda.synchronize()
+    got_t, got_i = oracle.bf16_to_f32(_to_np_bits(txt)), oracle.bf16_to_f32(_to_np_bits(img))
+    wn = {k: (_to_np_bits(v) if v.dtype == torch.bfloat16 else v.cpu().numpy()) for k, v in w.items()}
+    blk.close()
+    return (txt0, img0), (got_t, got_i), wn, cos_np, sin_np, tval
+
+
+def _check(case):
+    (txt0, img0), (got_t, got_i), wn, cos_np, sin_np, tval = case
+    ref_t, ref_i = om.mmdit_block(txt0, img0, wn, tval, cos_np, sin_np)
+    got = np.concatenate([got_t, got_i])
+    ref = np.concatenate([ref_t, ref_i])
+    x0 = oracle.bf16_to_f32(np.concatenate([txt0, img0]))
+    err = np.abs(got - ref)
+    rel = np.linalg.norm((got - x0) - (ref - x0)) / max(np.linalg.norm(ref - x0), 1e-30)
+    print(f"  max-abs {err.max():.3e} mean-abs {err.mean():.3e} update rel-L2 {rel:.3e} "
+          f"|update| mean {np.abs(ref - x0).mean():.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err.max() <= 6.25e-2 and err.mean() <= 2e-3
+    assert rel <= 0.03
+
+
+def test_block_small():
+    _check(_run(16, 6, 8, 256, 512, 0.05))
+
+
+def test_block_image_only_and_odd_rows():
+    _check(_run(0, 5, 9, 384, 1024, 0.05, seed=3, tval=0.81))
+
+
+def test_block_adaln_zero_is_identity():
+    """Zero modulation weights: every gate is 0, both streams come back bit for bit."""
+    (txt0, img0), (got_t, got_i), *_ = _run(24, 4, 10, 256, 768, 0.05, seed=5, zero_mod=True)
+    assert np.array_equal(got_t, oracle.bf16_to_f32(txt0)) and np.array_equal(got_i, oracle.bf16_to_f32(img0))
+
+
+def test_block_cfg3_full_shape():
+    """512 text + 4096 image tokens (64 x 64 grid), hidden 3072, 24 heads, MLP 12288, weights
+    N(0, 0.02), activations N(0, 1)."""
+    _check(_run(512, 64, 64, 3072, 12288, 0.02, seed=7))
+
+
+def test_block_repeated_calls_reuse_plans():
+    """A second call of the same shape on the same context gives the same bits as the first on fresh inputs."""
+    from localrouter_amd import mmdit
+    dev = torch.device("cuda", 0)
+    D, F, n_txt, gh, gw = 256, 512, 8, 4, 4
+    w = mmdit.make_weights(D, F, dev, seed=9, std=0.05)
+    blk = mmdit.MMDiTBlock(w)
+    cos_np, sin_np = _rope(n_txt, gh, gw)
+    cos, sin = torch.from_numpy(cos_np).to(dev), torch.from_numpy(sin_np).to(dev)
+    t = torch.tensor([0.3], dtype=torch.float32, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(10)
+    txt = torch.randn((n_txt, D), generator=g, device=dev).to(torch.bfloat16)
+    img = torch.randn((gh * gw, D), generator=g, device=dev).to(torch.bfloat16)
+    outs = []
+    for _ in range(2):
+        a, b = txt.clone(), img.clone()
+        blk(a, b, t, cos, sin)
+        outs.append((a, b))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    blk.close()
