@@ -1,6 +1,6 @@
 """Benchmark of the DiT joint-attention hot path on one MI355X (gfx950).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video|h3-int8]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video|h3-int8|mmdit]
                     [--tile-config C] [--no-cpu-baseline]
 
 A step is one fused joint-attention call over one synthetic batch: keys RMSNorm + RoPE into the workspace
@@ -21,6 +21,13 @@ shape for it): a step is Kitchen.attention on one packed qkv buffer, i.e. the pr
 lr_int8_attention_prep) then the attention kernel (lr_int8_attention_kernel, rows output). Ops per call = 4 * S^2 *
 128 * H; `roofline` is the attention kernel against MI355X's dense int8 peak of 5.0 POP/s; `cpu_baseline` is the
 CPU oracle of the same chain (prep + fp64 attention over the quantised operands) on a sample of heads and rows.
+
+--workload mmdit measures BASELINE configs[2], the MMDiT double-stream block forward at the same shape (512 text +
+4096 image tokens, hidden 3072, 24 heads, GELU-tanh MLP 12288, adaLN-zero modulation from the 256-d time sinusoid,
+weights N(0, 0.02), activations N(0, 1)): a step is one lr_mmdit_block_bf16 call (in place on the two streams).
+FLOPs per block = the GEMMs + the joint attention (elementwise work not counted). `roofline` is the block's largest
+GEMM (the image stream's MLP up-projection, 4096 x 12288 x 3072) timed alone through lr_mmdit_linear_bf16;
+`cpu_baseline` is the numpy fp32 oracle of the whole block (multithreaded BLAS) on the same inputs.
 """
 from __future__ import annotations
 
@@ -122,7 +129,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS) + ["h3-int8"])
+    ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS) + ["h3-int8", "mmdit"])
     ap.add_argument("--tile-config", type=int, default=0, choices=sorted(KERNELS),
                     help="LR_ATTN_CFG_* (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -141,6 +148,8 @@ def main():
 
     if args.workload == "h3-int8":
         return bench_int8(args)
+    if args.workload == "mmdit":
+        return bench_mmdit(args)
 
     import numpy as np
     import torch
@@ -414,6 +423,116 @@ def bench_int8(args):
                            "mean_abs": float(d.mean()), "bar": {"max_abs": 2e-2, "mean_abs": 2e-3}}
         log(f"[bench] cpu {cb['value']:.4f} TOP/s on {cb['threads']} threads; GPU vs CPU on sampled rows: "
             f"max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+    print(json.dumps(result), flush=True)
+
+
+def bench_mmdit(args):
+    import numpy as np
+    import torch
+
+    from localrouter_amd import _lib, mmdit, rope_host
+    from oracle import mmdit as om
+
+    n_txt, gh, gw, D, F = 512, 64, 64, 3072, 12288
+    n_img = gh * gw
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    rc = _lib.load().lr_attn_init()
+    if rc != 0:
+        raise SystemExit(f"lr_attn_init: {rc} (not a gfx950?)")
+    log(f"[bench] workload mmdit: {n_txt} text + {n_img} image tokens, hidden {D}, MLP {F}")
+    w = mmdit.make_weights(D, F, dev, seed=args.seed, std=0.02)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 1)
+    txt0 = torch.randn((n_txt, D), generator=g, device=dev).to(torch.bfloat16)
+    img0 = torch.randn((n_img, D), generator=g, device=dev).to(torch.bfloat16)
+    c_np, s_np = rope_host.grid2d_table(n_txt, gh, gw)
+    cos, sin = torch.from_numpy(c_np).to(dev), torch.from_numpy(s_np).to(dev)
+    t = torch.tensor([0.5], dtype=torch.float32, device=dev)
+    blk = mmdit.MMDiTBlock(w)
+    blk.workspace(n_txt, n_img)
+    blk.tune(n_txt, n_img)          # the fastest hipBLASLt candidate per GEMM shape (before anything is timed)
+    stream = torch.cuda.current_stream()
+    # one checked call on fresh copies (kept for the CPU comparison), then the timed calls in place
+    txt_c, img_c = txt0.clone(), img0.clone()
+    blk(txt_c, img_c, t, cos, sin)
+    txt, img = txt0.clone(), img0.clone()
+    for _ in range(args.warmup):
+        blk(txt, img, t, cos, sin)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done; timing {args.steps} blocks")
+    K = args.steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    e0.record(stream)
+    for _ in range(K):
+        blk(txt, img, t, cos, sin)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms_step = e0.elapsed_time(e1) / K
+    flops = om.block_flops(n_txt, n_img, D, F)
+    value = flops / (ms_step * 1e-3) / 1e12
+    # the dominant kernel alone: the image stream's MLP up-projection GEMM
+    x = torch.randn((n_img, D), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty((n_img, F), dtype=torch.bfloat16, device=dev)
+    for _ in range(5):
+        blk.linear(x, w["img.mlp_up"], y)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    for _ in range(20):
+        blk.linear(x, w["img.mlp_up"], y)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    gemm_ms = ev[0].elapsed_time(ev[1]) / 20
+    gemm_flops = 2.0 * n_img * F * D
+    achieved = gemm_flops / (gemm_ms * 1e-3) / 1e12
+    log(f"[bench] block {ms_step:.4f} ms = {value:.1f} TFLOP/s; MLP-up GEMM alone {gemm_ms:.4f} ms = "
+        f"{achieved:.1f} TFLOP/s ({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); wall {wall:.3f} s")
+    result = {
+        "metric": "MMDiT block TFLOP/s; ms/block at 4096+512 tokens, hidden 3072, 24x128, MLP 12288",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "mmdit-double-stream-block", "batch": 1, "text_tokens": n_txt, "image_tokens": n_img,
+                   "hidden": D, "heads": D // 128, "mlp": F, "weights": "N(0, 0.02) bf16", "activations": "N(0, 1)",
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "hipBLASLt GEMM 4096 x 12288 x 3072 (image MLP up-projection)",
+                     "kernel_ms": round(gemm_ms, 5)},
+        "flops_per_block": flops,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline (numpy fp32 oracle of the whole block) ...")
+        bits = lambda a: a.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)  # noqa: E731
+        wn = {k: (bits(v) if v.dtype == torch.bfloat16 else v.cpu().numpy()) for k, v in w.items()}
+        tb, ib = bits(txt0), bits(img0)
+        t0 = time.perf_counter()
+        ref_t, ref_i = om.mmdit_block(tb, ib, wn, 0.5, c_np, s_np)
+        cpu_s = time.perf_counter() - t0
+        got = np.concatenate([bits(txt_c), bits(img_c)])
+        got = (got.astype(np.uint32) << 16).view(np.float32)
+        d = np.abs(got - np.concatenate([ref_t, ref_i]))
+        result["cpu_baseline"] = {"value": round(flops / cpu_s / 1e12, 4), "unit": "TFLOP/s",
+                                  "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+                                  "kind": "port", "sample": f"one whole block (all {n_txt + n_img} rows, numpy fp32 "
+                                                            f"BLAS GEMMs + the oracle's fp32 attention): {cpu_s:.2f} s"}
+        result["check"] = {"rows": n_txt + n_img, "max_abs": float(d.max()), "mean_abs": float(d.mean()),
+                           "bar": {"max_abs": 6.25e-2, "mean_abs": 2e-3}}
+        log(f"[bench] cpu {flops / cpu_s / 1e12:.4f} TFLOP/s ({cpu_s:.2f} s); GPU vs oracle max-abs {d.max():.3e} "
+            f"mean-abs {d.mean():.3e}")
+    blk.close()
     print(json.dumps(result), flush=True)
 
 

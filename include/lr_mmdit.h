@@ -59,6 +59,21 @@ int lr_mmdit_destroy(void* ctx);
  * F not a multiple of 8, sizes <= 0). */
 size_t lr_mmdit_workspace_bytes(int n_txt, int n_img, int hidden, int mlp);
 
+/* Optional: time up to `candidates` (<= 16) hipBLASLt heuristic candidates of each of the block's row GEMMs for
+ * this shape on the workspace's buffers and keep the fastest. Synchronises the stream and creates events; call it
+ * once per shape before timing or capturing blocks (the block call itself plans with the first heuristic result). */
+int lr_mmdit_tune(void* ctx, const lr_mmdit_weights* w, int n_txt, int n_img, int hidden, int mlp, int candidates,
+                  void* workspace, size_t workspace_bytes, lr_stream_t stream);
+
+/* Device scratch of one lr_mmdit_linear_bf16 call, bytes (a block's workspace is larger and also qualifies). */
+#define LR_MMDIT_GEMM_WORKSPACE (64u << 20)
+
+/* One linear as the block runs it: y[M, N] (row stride ldy) = x[M, K] (row stride ldx) w[N, K]^T, bf16 in and out,
+ * fp32 compute (hipBLASLt), workspace >= LR_MMDIT_GEMM_WORKSPACE bytes. The engines' dense
+ * (src/engines/qwen_image/dit.zig:185) on this path; also what bench.py times alone. */
+int lr_mmdit_linear_bf16(void* ctx, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int M, int N,
+                         int K, void* workspace, size_t workspace_bytes, lr_stream_t stream);
+
 /* One block forward, in place on txt [n_txt, D] and img [n_img, D] bf16 (contiguous rows). t: device pointer to one
  * f32 timestep. cos, sin: device [n_txt + n_img, 64] f32 (text rows first). The first call for a new shape builds
  * its GEMM plans (hipBLASLt heuristics, host memory); later calls of that shape launch only. Not reentrant per

@@ -19,7 +19,7 @@ namespace lr {
 namespace {
 
 constexpr int EW_THREADS = 256;
-constexpr size_t GEMM_WS = 64u << 20;   // hipBLASLt workspace inside the block's scratch
+constexpr size_t GEMM_WS = LR_MMDIT_GEMM_WORKSPACE;   // hipBLASLt workspace, at the start of the block's scratch
 constexpr float LN_EPS = 1e-6f;
 
 __device__ __forceinline__ float bf(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
@@ -167,6 +167,25 @@ __global__ void gated_residual_kernel(uint16_t* txt, uint16_t* img, int n_txt, i
     store8(x + 8 * ch, xv);
 }
 
+// y[n] = sum_k x[k] w[n, k] for one input row (the time and modulation vectors): HBM-bound on w, one wave per
+// output, 16-byte loads along the weight row, a butterfly sum. K a multiple of 8.
+constexpr int GEMV_WAVES = 4;
+__global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(const uint16_t* x, const uint16_t* w, uint16_t* y, int N,
+                                                               int K) {
+    const int n = blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (n >= N) return;
+    const uint16_t* row = w + (int64_t)n * K;
+    float acc = 0.0f;
+    for (int c = lane; c < K / 8; c += 64) {
+        const Chunk8 a = load8(row + 8 * c), b = load8(x + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf(a.v[e], b.v[e], acc);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) y[n] = tobf(acc);
+}
+
 // ---- hipBLASLt GEMMs: row-major Y[M, N] (row stride ldy) = X[M, K] (row stride ldx) W[N, K]^T, bf16 in and out,
 // fp32 compute. Column-major, that is C (N x M, ldc = ldy) = op(A) op(B) with A = W viewed K x N (lda = K,
 // transposed) and B = X viewed K x M (ldb = ldx).
@@ -218,8 +237,63 @@ int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
     return 0;
 }
 
+// Time up to `cands` heuristic candidates of one GEMM on the given buffers and keep the fastest as its plan
+// (replacing a heuristic-first plan). Synchronises on its own events.
+int tune_gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, int64_t M, int64_t N,
+              int64_t K, void* ws, hipStream_t s, int cands) {
+    GemmPlan* p;
+    int rc = plan_gemm(c, M, N, K, ldx, ldy, &p);
+    if (rc) return rc;
+    hipblasLtMatmulPreference_t pref;
+    if ((rc = blas_err(hipblasLtMatmulPreferenceCreate(&pref)))) return rc;
+    const uint64_t wsb = GEMM_WS;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof wsb);
+    hipblasLtMatmulHeuristicResult_t res[16];
+    int found = 0;
+    cands = cands > 16 ? 16 : cands;
+    rc = blas_err(hipblasLtMatmulAlgoGetHeuristic(c.lt, p->desc, p->la, p->lb, p->lc, p->lc, pref, cands, res, &found));
+    hipblasLtMatmulPreferenceDestroy(pref);
+    if (rc) return rc;
+    hipEvent_t e0, e1;
+    if ((rc = (int)hipEventCreate(&e0))) return rc;
+    if ((rc = (int)hipEventCreate(&e1))) {
+        (void)hipEventDestroy(e0);
+        return rc;
+    }
+    const float alpha = 1.0f, beta = 0.0f;
+    float best = 1e30f;
+    for (int i = 0; i < found && rc == 0; ++i) {
+        if (res[i].workspaceSize > GEMM_WS) continue;
+        auto run = [&]() {
+            return hipblasLtMatmul(c.lt, p->desc, &alpha, W, p->la, X, p->lb, &beta, Y, p->lc, Y, p->lc, &res[i].algo,
+                                   ws, res[i].workspaceSize, s);
+        };
+        if (run() != HIPBLAS_STATUS_SUCCESS) continue;   // a candidate that does not run is skipped
+        (void)hipEventRecord(e0, s);
+        for (int r = 0; r < 5; ++r) run();
+        (void)hipEventRecord(e1, s);
+        if ((rc = (int)hipEventSynchronize(e1))) break;
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        if (ms < best) {
+            best = ms;
+            p->algo = res[i].algo;
+            p->ws = res[i].workspaceSize;
+        }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
+}
+
 int gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
          void* ws, hipStream_t s) {
+    if (M == 1 && K % 8 == 0 && ((uintptr_t)X & 15) == 0 && ((uintptr_t)W & 15) == 0) {   // a vector: HBM-bound
+        hipLaunchKernelGGL(gemv_kernel, dim3((unsigned)((N + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), 0,
+                           s, static_cast<const uint16_t*>(X), static_cast<const uint16_t*>(W),
+                           static_cast<uint16_t*>(Y), (int)N, (int)K);
+        return (int)hipGetLastError();
+    }
     GemmPlan* p;
     int rc = plan_gemm(c, M, N, K, ldx, ldy, &p);
     if (rc) return rc;
@@ -243,6 +317,7 @@ Scratch layout(int64_t n_txt, int64_t n_img, int64_t D, int64_t F) {
         o += align256(bytes);
         return at;
     };
+    s.gws = take(GEMM_WS);
     s.emb = take(256 * 2);
     s.h1 = take(D * 2);
     s.temb = take(D * 2);
@@ -253,7 +328,6 @@ Scratch layout(int64_t n_txt, int64_t n_img, int64_t D, int64_t F) {
     s.qkv = take(S * 3 * D * 2);
     s.attn = take(S * D * 2);        // attention output
     s.big = take(S * F * 2);         // MLP hidden
-    s.gws = take(GEMM_WS);
     s.attn_ws = take(lr_joint_attention_workspace_bytes((int)S, (int)(D / 128)));
     s.total = o;
     return s;
@@ -271,7 +345,7 @@ int lr_mmdit_create(void** ctx) {
     Ctx* c = new Ctx;
     const int rc = blas_err(hipblasLtCreate(&c->lt));
     if (rc) {
-        delete c;
+        lr_mmdit_destroy(c);
         return rc;
     }
     *ctx = c;
@@ -287,7 +361,7 @@ int lr_mmdit_destroy(void* ctx) {
         hipblasLtMatrixLayoutDestroy(kv.second.lc);
         hipblasLtMatmulDescDestroy(kv.second.desc);
     }
-    const int rc = blas_err(hipblasLtDestroy(c->lt));
+    const int rc = c->lt ? blas_err(hipblasLtDestroy(c->lt)) : 0;
     delete c;
     return rc;
 }
@@ -297,6 +371,44 @@ size_t lr_mmdit_workspace_bytes(int n_txt, int n_img, int hidden, int mlp) {
         hidden > 8 * LN_THREADS * LN_MAX_CHUNKS)
         return 0;
     return layout(n_txt, n_img, hidden, mlp).total;
+}
+
+int lr_mmdit_tune(void* ctx, const lr_mmdit_weights* w, int n_txt, int n_img, int hidden, int mlp, int candidates,
+                  void* workspace, size_t workspace_bytes, lr_stream_t stream) {
+    const size_t need = lr_mmdit_workspace_bytes(n_txt, n_img, hidden, mlp);
+    if (!ctx || !w || !workspace || need == 0 || workspace_bytes < need || candidates < 1) return hipErrorInvalidValue;
+    if (!w->txt.qkv || !w->txt.out || !w->txt.mlp_up || !w->txt.mlp_down || !w->img.qkv || !w->img.out ||
+        !w->img.mlp_up || !w->img.mlp_down)
+        return hipErrorInvalidValue;
+    Ctx& c = *static_cast<Ctx*>(ctx);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t D = hidden, F = mlp;
+    const Scratch L = layout(n_txt, n_img, D, F);
+    char* ws = static_cast<char*>(workspace);
+    auto at = [&](size_t off) { return reinterpret_cast<uint16_t*>(ws + off); };
+    uint16_t *hn = at(L.hn), *qkv = at(L.qkv), *attn = at(L.attn), *big = at(L.big);
+    void* gws = ws + L.gws;
+    // the block's GEMMs of rows > 1, on its own scratch buffers (contents irrelevant for timing)
+    const lr_mmdit_stream_weights* sw[2] = {&w->txt, &w->img};
+    const int64_t rows[2] = {n_txt, n_img}, row0[2] = {0, n_txt};
+    int rc = 0;
+    for (int k = 0; k < 2 && rc == 0; ++k) {
+        const int64_t M = rows[k], r0 = row0[k];
+        if (M <= 1) continue;
+        if (!rc) rc = tune_gemm(c, hn + r0 * D, D, sw[k]->qkv, qkv + r0 * 3 * D, 3 * D, M, 3 * D, D, gws, s, candidates);
+        if (!rc) rc = tune_gemm(c, attn + r0 * D, D, sw[k]->out, hn + r0 * D, D, M, D, D, gws, s, candidates);
+        if (!rc) rc = tune_gemm(c, hn + r0 * D, D, sw[k]->mlp_up, big + r0 * F, F, M, F, D, gws, s, candidates);
+        if (!rc) rc = tune_gemm(c, big + r0 * F, F, sw[k]->mlp_down, attn + r0 * D, D, M, D, F, gws, s, candidates);
+    }
+    return rc;
+}
+
+int lr_mmdit_linear_bf16(void* ctx, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int M, int N,
+                         int K, void* workspace, size_t workspace_bytes, lr_stream_t stream) {
+    if (!ctx || !x || !w || !y || !workspace || workspace_bytes < GEMM_WS || M <= 0 || N <= 0 || K <= 0 || ldx < K ||
+        ldy < N)
+        return hipErrorInvalidValue;
+    return gemm(*static_cast<Ctx*>(ctx), x, ldx, w, y, ldy, M, N, K, workspace, reinterpret_cast<hipStream_t>(stream));
 }
 
 int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* img, int n_txt, int n_img, int hidden,
@@ -329,6 +441,15 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
         if ((rc = (expr)) != 0) return rc; \
     } while (0)
 #define LR_LAUNCHED() LR_TRY((int)hipGetLastError())
+    // one GEMM per stream of rows, each with its own weights (the text rows first in every joint buffer). Running
+    // the text rows' GEMMs on a second stream beside the image rows' was measured slower (1.50 vs 1.34 ms a block).
+    auto pair_gemm = [&](const uint16_t* xt_, const uint16_t* xi_, int64_t ldx, const void* wt, const void* wi,
+                         uint16_t* yt, uint16_t* yi, int64_t ldy, int64_t N, int64_t K) -> int {
+        int r = 0;
+        if (n_txt > 0) r = gemm(c, xt_, ldx, wt, yt, ldy, n_txt, N, K, gws, s);
+        if (!r && n_img > 0) r = gemm(c, xi_, ldx, wi, yi, ldy, n_img, N, K, gws, s);
+        return r;
+    };
 
     // time embedding and modulation (vectors: one row)
     hipLaunchKernelGGL(time_sinusoid_kernel, dim3(1), dim3(256), 0, s, t, emb);
@@ -348,16 +469,13 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     hipLaunchKernelGGL(ln_modulate_kernel, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D, mod_txt,
                        mod_img, 0, hn);
     LR_LAUNCHED();
-    if (n_txt > 0) LR_TRY(gemm(c, hn, D, w->txt.qkv, qkv, 3 * D, n_txt, 3 * D, D, gws, s));
-    if (n_img > 0) LR_TRY(gemm(c, hn + (int64_t)n_txt * D, D, w->img.qkv, qkv + (int64_t)n_txt * 3 * D, 3 * D, n_img,
-                               3 * D, D, gws, s));
+    const int64_t tD = (int64_t)n_txt * D, tF = (int64_t)n_txt * F;
+    LR_TRY(pair_gemm(hn, hn + tD, D, w->txt.qkv, w->img.qkv, qkv, qkv + 3 * tD, 3 * D, 3 * D, D));
     LR_TRY(lr_joint_attention_fused(qkv, qkv + D, qkv + 2 * D, attn, w->q_norm, w->k_norm, LR_TABLE_COSSIN_F32, cos, sin,
                                     cos, sin, 64, LR_PAIR_INTERLEAVED, 128, 1e-6f, (int)S, (int)S, (int)H, (int)H, 0, 0,
                                     1.0f / sqrtf(128.0f), 3 * D, 3 * D, 3 * D, D, 0, ws + L.attn_ws,
                                     lr_joint_attention_workspace_bytes((int)S, (int)H), stream));
-    if (n_txt > 0) LR_TRY(gemm(c, attn, D, w->txt.out, hn, D, n_txt, D, D, gws, s));
-    if (n_img > 0)
-        LR_TRY(gemm(c, attn + (int64_t)n_txt * D, D, w->img.out, hn + (int64_t)n_txt * D, D, n_img, D, D, gws, s));
+    LR_TRY(pair_gemm(attn, attn + tD, D, w->txt.out, w->img.out, hn, hn + tD, D, D, D));
     const unsigned res_blocks = (unsigned)((S * (D / 8) + EW_THREADS - 1) / EW_THREADS);
     hipLaunchKernelGGL(gated_residual_kernel, dim3(res_blocks), dim3(EW_THREADS), 0, s, xt, xi, n_txt, (int)S, (int)D,
                        hn, mod_txt, mod_img, 0);
@@ -367,16 +485,12 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     hipLaunchKernelGGL(ln_modulate_kernel, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D, mod_txt,
                        mod_img, 1, hn);
     LR_LAUNCHED();
-    if (n_txt > 0) LR_TRY(gemm(c, hn, D, w->txt.mlp_up, big, F, n_txt, F, D, gws, s));
-    if (n_img > 0)
-        LR_TRY(gemm(c, hn + (int64_t)n_txt * D, D, w->img.mlp_up, big + (int64_t)n_txt * F, F, n_img, F, D, gws, s));
+    LR_TRY(pair_gemm(hn, hn + tD, D, w->txt.mlp_up, w->img.mlp_up, big, big + tF, F, F, D));
     const int64_t n8 = S * F / 8;
     hipLaunchKernelGGL(gelu_tanh_kernel, dim3((unsigned)((n8 + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s,
                        big, n8);
     LR_LAUNCHED();
-    if (n_txt > 0) LR_TRY(gemm(c, big, F, w->txt.mlp_down, attn, D, n_txt, D, F, gws, s));
-    if (n_img > 0)
-        LR_TRY(gemm(c, big + (int64_t)n_txt * F, F, w->img.mlp_down, attn + (int64_t)n_txt * D, D, n_img, D, F, gws, s));
+    LR_TRY(pair_gemm(big, big + tF, F, w->txt.mlp_down, w->img.mlp_down, attn, attn + tD, D, D, F));
     hipLaunchKernelGGL(gated_residual_kernel, dim3(res_blocks), dim3(EW_THREADS), 0, s, xt, xi, n_txt, (int)S, (int)D,
                        attn, mod_txt, mod_img, 1);
     LR_LAUNCHED();

@@ -30,6 +30,8 @@ SIGNATURES = {
     "lr_mmdit_create": (_I, [ctypes.POINTER(_P)]),
     "lr_mmdit_destroy": (_I, [_P]),
     "lr_mmdit_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "lr_mmdit_tune": (_I, [_P, ctypes.POINTER(Weights), _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "lr_mmdit_linear_bf16": (_I, [_P, _P, ctypes.c_int64, _P, _P, ctypes.c_int64, _I, _I, _I, _P, _SZ, _P]),
     "lr_mmdit_block_bf16": (_I, [_P, ctypes.POINTER(Weights), _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P]),
 }
 
@@ -114,6 +116,29 @@ class MMDiTBlock:
         if self._ws is None or self._ws.numel() < nb:
             self._ws = torch.empty(nb, dtype=torch.uint8, device=self.w["t1"].device)
         return self._ws
+
+    def tune(self, n_txt: int, n_img: int, candidates: int = 16, stream=None):
+        """Pick the fastest of the hipBLASLt candidates for this shape's GEMMs (synchronises)."""
+        import torch
+        ws = self.workspace(n_txt, n_img)
+        s = torch.cuda.current_stream().cuda_stream if stream is None else stream
+        rc = lib().lr_mmdit_tune(self.ctx, ctypes.byref(self.cw), n_txt, n_img, self.hidden, self.mlp, candidates,
+                                 ws.data_ptr(), ws.numel(), s)
+        if rc != 0:
+            raise _lib.LrError("lr_mmdit_tune", rc)
+
+    def linear(self, x, w, y, stream=None):
+        """y = x w^T through the block's GEMM path (x [M, K], w [N, K], y [M, N] bf16 CUDA tensors, rows may be
+        strided). Uses this block's workspace (allocate it with workspace() first)."""
+        import torch
+        assert self._ws is not None
+        M, K = x.shape
+        N = w.shape[0]
+        s = torch.cuda.current_stream().cuda_stream if stream is None else stream
+        rc = lib().lr_mmdit_linear_bf16(self.ctx, x.data_ptr(), x.stride(0), w.data_ptr(), y.data_ptr(), y.stride(0),
+                                        M, N, K, self._ws.data_ptr(), self._ws.numel(), s)
+        if rc != 0:
+            raise _lib.LrError("lr_mmdit_linear_bf16", rc)
 
     def __call__(self, txt, img, t, cos, sin, stream=None):
         import torch

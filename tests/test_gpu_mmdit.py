@@ -26,7 +26,7 @@ def _to_np_bits(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def _run(n_txt, gh, gw, D, F, std, seed=0, zero_mod=False, tval=0.5):
+def _run(n_txt, gh, gw, D, F, std, seed=0, zero_mod=False, tval=0.5, tune=False):
     from localrouter_amd import mmdit
     dev = torch.device("cuda", 0)
     n_img = gh * gw
@@ -41,6 +41,8 @@ def _run(n_txt, gh, gw, D, F, std, seed=0, zero_mod=False, tval=0.5):
     t = torch.tensor([tval], dtype=torch.float32, device=dev)
     txt0, img0 = _to_np_bits(txt), _to_np_bits(img)
     blk = mmdit.MMDiTBlock(w)
+    if tune:
+        blk.tune(n_txt, n_img, candidates=8)
     blk(txt, img, t, cos, sin)
     torch.cuda.synchronize()
     got_t, got_i = oracle.bf16_to_f32(_to_np_bits(txt)), oracle.bf16_to_f32(_to_np_bits(img))
@@ -80,8 +82,12 @@ def test_block_adaln_zero_is_identity():
 
 def test_block_cfg3_full_shape():
     """512 text + 4096 image tokens (64 x 64 grid), hidden 3072, 24 heads, MLP 12288, weights
-    N(0, 0.02), activations N(0, 1)."""
-    _check(_run(512, 64, 64, 3072, 12288, 0.02, seed=7))
+    N(0, 0.02), activations N(0, 1); GEMM candidates tuned first, as bench.py runs it."""
+    _check(_run(512, 64, 64, 3072, 12288, 0.02, seed=7, tune=True))
+
+
+def test_block_tuned_small():
+    _check(_run(40, 8, 12, 512, 1536, 0.05, seed=11, tune=True))
 
 
 def test_block_repeated_calls_reuse_plans():
