@@ -38,7 +38,7 @@ extern "C" {
 /* hipStream_t without pulling in the HIP headers: an opaque pointer (NULL = the default stream). */
 typedef struct ihipStream_t* lr_stream_t;
 
-#define LR_ATTN_ABI_VERSION 3
+#define LR_ATTN_ABI_VERSION 4
 #define LR_HEAD_DIM 128
 
 /* RoPE table kinds: how rotation coefficients are stored per token row, per pair p < rot_dim/2. */
@@ -99,6 +99,20 @@ int lr_attention_bf16_ex(const void* q, const void* k, const void* v, void* out,
                          int nkeys, int causal, float scale, int64_t q_row_stride, int64_t k_row_stride,
                          int64_t v_row_stride, int64_t out_row_stride, int64_t k_head_stride, int64_t v_head_stride,
                          int config, lr_stream_t stream);
+
+/*
+ * Attention under a key-padding mask: keys j with kmask[j] == 0 are left out (torch's bool key-padding mask, SDPA's
+ * additive 0 / -inf), the drop-in for Kandinsky-6's attention.Call with mask = .keys
+ * (src/engines/kandinsky6/dit/attention.zig:21-27, dispatched by launch.zig:239-255). Non-causal; q, out rows
+ * [W][H*128], k, v rows [nkeys][HK*128] (kv_row_stride for both). kmask: device u8 [nkeys]; n_valid: the number of
+ * nonzero bytes, known on the host as the engine's `valid` (1 <= n_valid <= nkeys). The kept keys and value rows are
+ * gathered into the workspace, then attended as lr_attention_bf16 does. kmask = NULL: no mask (n_valid = nkeys, no
+ * workspace needed).
+ */
+size_t lr_attention_kmask_workspace_bytes(int n_valid, int HK);
+int lr_attention_kmask_bf16(const void* q, const void* k, const void* v, void* out, const void* kmask, int n_valid,
+                            int W, int H, int HK, int nkeys, float scale, int64_t q_row_stride, int64_t kv_row_stride,
+                            int64_t out_row_stride, void* workspace, size_t workspace_bytes, lr_stream_t stream);
 
 /*
  * Per-(token, head) RMSNorm + RoPE of one q/k part, out of place or in place (drop-in for Triton.ropeRun,

@@ -17,7 +17,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "liblr_attn.so"
-SOURCES = ["attn_fwd.hip", "attn_pair.hip", "rms_rope.hip", "int8_attn.hip", "lr_abi.hip", "mmdit.hip", "rope_host.cpp"]
+SOURCES = ["attn_fwd.hip", "attn_pair.hip", "rms_rope.hip", "int8_attn.hip", "keys.hip", "lr_abi.hip", "mmdit.hip",
+           "rope_host.cpp"]
 # libraries the shared object links: hipBLASLt for the MMDiT block's projections and MLP
 LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
 ARCH = "gfx950"

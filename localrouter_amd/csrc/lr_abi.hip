@@ -280,6 +280,42 @@ int lr_attention_bf16(const void* q, const void* k, const void* v, void* out, in
                           kv_row_stride, out_row_stride, lr::D, lr::D, LR_ATTN_CFG_AUTO, stream);
 }
 
+size_t lr_attention_kmask_workspace_bytes(int n_valid, int HK) {
+    if (n_valid < 1 || HK < 1) return 0;
+    const size_t idx = ((size_t)n_valid * 4 + 255) & ~(size_t)255;
+    const size_t rows = (((size_t)n_valid * HK * lr::D * 2) + 255) & ~(size_t)255;
+    return idx + 2 * rows;
+}
+
+int lr_attention_kmask_bf16(const void* q, const void* k, const void* v, void* out, const void* kmask, int n_valid,
+                            int W, int H, int HK, int nkeys, float scale, int64_t q_row_stride, int64_t kv_row_stride,
+                            int64_t out_row_stride, void* workspace, size_t workspace_bytes, lr_stream_t stream) {
+    if (!kmask)
+        return lr_attention_bf16(q, k, v, out, 0, W, H, HK, nkeys, 0, scale, q_row_stride, kv_row_stride,
+                                 out_row_stride, stream);
+    const size_t need = lr_attention_kmask_workspace_bytes(n_valid, HK);
+    if (n_valid < 1 || n_valid > nkeys || need == 0 || !workspace || workspace_bytes < need ||
+        !aligned(workspace, 256))
+        return ERR_ARGS;
+    if (kv_row_stride < (int64_t)HK * lr::D || kv_row_stride % 8 || !k || !v || !aligned(k, 16) || !aligned(v, 16))
+        return ERR_ARGS;
+    // the attention's own checks first, against the compacted keys, so that nothing is launched on a bad call
+    if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || !scale_ok(scale) || !rows_ok(q, q_row_stride, H) ||
+        !rows_ok(out, out_row_stride, H))
+        return ERR_ARGS;
+    char* ws = static_cast<char*>(workspace);
+    const size_t idx_bytes = ((size_t)n_valid * 4 + 255) & ~(size_t)255;
+    const size_t rows = (((size_t)n_valid * HK * lr::D * 2) + 255) & ~(size_t)255;
+    void* kc = ws + idx_bytes;
+    void* vc = ws + idx_bytes + rows;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const hipError_t e = lr::launch_compact_keys(k, v, kv_row_stride, static_cast<const uint8_t*>(kmask), nkeys,
+                                                 n_valid, HK, ws, kc, vc, s);
+    if (e != hipSuccess) return (int)e;
+    return lr_attention_bf16(q, kc, vc, out, 0, W, H, HK, n_valid, 0, scale, q_row_stride, (int64_t)HK * lr::D,
+                             out_row_stride, stream);
+}
+
 int lr_attention_bf16_ex(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK,
                          int nkeys, int causal, float scale, int64_t q_row_stride, int64_t k_row_stride,
                          int64_t v_row_stride, int64_t out_row_stride, int64_t k_head_stride, int64_t v_head_stride,

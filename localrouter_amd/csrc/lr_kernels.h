@@ -70,6 +70,10 @@ enum AttnConfig : int {
 hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config, hipStream_t stream);
 // The 64-queries-per-wave kernel (attn_pair.hip): qk = a TableKind (queries normalised and rotated in registers, values
 // as packed V^T tiles when v_t) or -1 (plain queries, values as rows).
+// keys.hip: gather the kept keys (kmask[j] != 0, in order) and their value rows into kc / vc [n_valid][HK * 128];
+// idx: n_valid ints of scratch
+hipError_t launch_compact_keys(const void* k, const void* v, int64_t kv_rs, const uint8_t* kmask, int nkeys,
+                               int n_valid, int HK, void* idx, void* kc, void* vc, hipStream_t stream);
 hipError_t launch_pair(const AttnArgs& a, int qk, bool v_t, hipStream_t stream);
 bool attention_config_reads_vt(int config);
 hipError_t launch_rms_rope(const RopeArgs& a, hipStream_t stream);

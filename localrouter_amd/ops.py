@@ -78,6 +78,39 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tens
     return out
 
 
+def attention_kmask(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kmask: torch.Tensor | None,
+                    out: torch.Tensor | None = None, *, n_valid: int | None = None, scale: float = SCALE_128,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Kandinsky-6's attention with a key-padding mask: q [w, heads, 128], k / v [nkeys, kv_heads, 128] (the same row
+    stride), kmask u8 [nkeys] on the GPU (nonzero = keep) or None; n_valid = the number of kept keys (computed here,
+    with a device sync, when not given; the engine knows it on the host)."""
+    w, heads = q.shape[0], q.shape[1]
+    nkeys, kv_heads = k.shape[0], k.shape[1]
+    q_rs = _rows(q, "q", heads)
+    k_rs = _rows(k, "k", kv_heads)
+    if _rows(v, "v", kv_heads) != k_rs:
+        raise ValueError("attention_kmask: k and v need the same row stride")
+    if out is None:
+        out = torch.empty((w, heads, D), dtype=torch.bfloat16, device=q.device)
+    o_rs = _rows(out, "out", heads)
+    ws_ptr, ws_bytes = None, 0
+    if kmask is not None:
+        if kmask.dtype != torch.uint8 or not kmask.is_cuda or kmask.numel() < nkeys:
+            raise ValueError("kmask: expected u8 [nkeys] on the GPU")
+        if n_valid is None:
+            n_valid = int((kmask[:nkeys] != 0).sum().item())
+        ws_bytes = int(_lib.load().lr_attention_kmask_workspace_bytes(n_valid, kv_heads))
+        if workspace is None:
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        ws_ptr = _ptr(workspace)
+        ws_bytes = workspace.numel()
+    else:
+        n_valid = nkeys
+    _lib.call("lr_attention_kmask_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(kmask), n_valid, w, heads,
+              kv_heads, nkeys, scale, q_rs, k_rs, o_rs, ws_ptr, ws_bytes, _stream())
+    return out
+
+
 def rms_rope(src: torch.Tensor, dst: torch.Tensor, w: torch.Tensor | None, *, n: int, heads: int, b: int = 1,
              src_row_stride: int, src_off: int = 0, dst_row_stride: int, src_b_stride: int = 0,
              dst_b_stride: int = 0, table_kind: int = TABLE_COSSIN_F32, table_a: torch.Tensor | None = None,

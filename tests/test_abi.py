@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version():
     header = _lib.HEADER.read_text()
     declared = int(re.search(r"#define LR_ATTN_ABI_VERSION (\d+)", header).group(1))
-    assert _lib.load().lr_attn_abi_version() == declared == 3
+    assert _lib.load().lr_attn_abi_version() == declared == 4
 
 
 def test_workspace_bytes():
@@ -209,3 +209,24 @@ def test_mmdit_abi_on_cpu():
                                  None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_mmdit_create(None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_mmdit_destroy(None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_kmask_attention_rejects():
+    L = _lib.load()
+    assert L.lr_attention_kmask_workspace_bytes(0, 32) == 0
+    assert L.lr_attention_kmask_workspace_bytes(218, 32) >= 2 * 218 * 32 * 128 * 2 + 218 * 4
+    fake = 1 << 20   # never dereferenced: every call below is rejected before any launch
+    ws = L.lr_attention_kmask_workspace_bytes(10, 2)
+    args = dict(q=fake, k=fake, v=fake, out=fake, kmask=fake, n_valid=10, W=4, H=2, HK=2, nkeys=20, scale=0.088,
+                q_rs=256, kv_rs=256, out_rs=256, ws=fake, ws_bytes=ws, stream=None)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return L.lr_attention_kmask_bf16(*a.values())
+    assert call(n_valid=0) == HIP_ERROR_INVALID_VALUE
+    assert call(n_valid=21) == HIP_ERROR_INVALID_VALUE         # more kept keys than keys
+    assert call(ws_bytes=ws - 1) == HIP_ERROR_INVALID_VALUE
+    assert call(ws=None) == HIP_ERROR_INVALID_VALUE
+    assert call(kv_rs=255) == HIP_ERROR_INVALID_VALUE
+    assert call(H=3) == HIP_ERROR_INVALID_VALUE                 # H % HK
+    assert call(scale=0.0) == HIP_ERROR_INVALID_VALUE
