@@ -73,6 +73,10 @@ typedef struct ihipStream_t* lr_stream_t;
                                       one wave per SIMD; softmax against a fixed reference (the first key tile's
                                       maximum), blocks whose sums overflowed it recomputed by a second launch of the
                                       PIPE_W8 kernel */
+#define LR_ATTN_CFG_WS_W8 7        /* 256 queries per workgroup, 8 waves in 4 pairs per SIMD: one wave of a pair
+                                      computes scores and softmax, the other the PV products, P handed over in LDS;
+                                      fused / prepared calls, non-causal (causal calls run PAIR_W4); same fixed
+                                      reference and second launch as PAIR_W4 */
 
 int lr_attn_abi_version(void);
 

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "liblr_attn.so"
-SOURCES = ["attn_fwd.hip", "attn_pair.hip", "rms_rope.hip", "int8_attn.hip", "keys.hip", "lr_abi.hip", "mmdit.hip",
+SOURCES = ["attn_fwd.hip", "attn_pair.hip", "attn_ws.hip", "rms_rope.hip", "int8_attn.hip", "keys.hip", "lr_abi.hip", "mmdit.hip",
            "rope_host.cpp"]
 # libraries the shared object links: hipBLASLt for the MMDiT block's projections and MLP
 LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
@@ -37,7 +37,8 @@ HIPCC_FLAGS = [
 
 # per-source extra flags: the 64-query-per-wave kernel's fully unrolled 64-slot schedule is larger than clang's
 # default limit for `#pragma unroll`, and a partly unrolled schedule would index its register arrays at run time
-EXTRA_FLAGS = {"attn_pair.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]}
+EXTRA_FLAGS = {"attn_pair.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"],
+               "attn_ws.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]}
 
 # host-only C++ (the RoPE table builders of include/lr_rope.h): the system compiler, no contraction of f64 products
 # and sums into FMAs, so that tables are the same bits as the numpy builders

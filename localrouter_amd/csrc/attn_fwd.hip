@@ -1068,6 +1068,15 @@ hipError_t launch_pair_checked(const AttnArgs& a, hipStream_t stream) {
     return launch_pipe<8, 1, 64, VT ? 4 : 3, QK, VT, true>(a, stream);
 }
 
+// The warp-specialised kernel, then the running-max kernel on the blocks it marked (the same 256-query blocks).
+template <int QK>
+hipError_t launch_ws_checked(const AttnArgs& a, hipStream_t stream) {
+    if (a.causal) return launch_pair_checked<QK, true>(a, stream);   // the warp-specialised kernel is non-causal
+    const hipError_t e = launch_ws(a, QK, stream);
+    if (e != hipSuccess) return e;
+    return launch_pipe<8, 1, 64, 4, QK, true, true>(a, stream);
+}
+
 }  // namespace
 
 int attention_block_rows(int config) {
@@ -1079,7 +1088,7 @@ int attention_block_rows(int config) {
 
 bool attention_config_reads_vt(int config) {
     return config == ATTN_CFG_AUTO || config == ATTN_CFG_PIPE_W8 || config == ATTN_CFG_PIPE_W4 ||
-           config == ATTN_CFG_PAIR_W4;
+           config == ATTN_CFG_PAIR_W4 || config == ATTN_CFG_WS_W8;
 }
 
 // The prepared-keys path over packed V^T tiles, queries fused with table kind K (the 64-key pipelined shapes).
@@ -1089,6 +1098,7 @@ hipError_t launch_vt(const AttnArgs& a, int config, hipStream_t stream) {
         case ATTN_CFG_PIPE_W8: return launch_pipe<8, 1, 64, 4, K, true>(a, stream);
         case ATTN_CFG_PIPE_W4: return launch_pipe<4, 1, 64, 2, K, true>(a, stream);
         case ATTN_CFG_PAIR_W4: return launch_pair_checked<K, true>(a, stream);
+        case ATTN_CFG_WS_W8: return launch_ws_checked<K>(a, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -27,7 +27,7 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
                    int causal, float scale, int64_t q_rs, int64_t k_rs, int64_t v_rs, int64_t o_rs, int64_t k_hs,
                    int64_t v_hs, int config, hipStream_t stream) {
     if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || nkeys < 1 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
-    if (!scale_ok(scale) || config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_PAIR_W4) return ERR_ARGS;
+    if (!scale_ok(scale) || config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WS_W8) return ERR_ARGS;
     if ((int64_t)p0 + W > INT_MAX - 512 || nkeys > INT_MAX - 512 || W > INT_MAX - 512) return ERR_ARGS;
     if (!rows_ok(q, q_rs, H) || !rows_ok(out, o_rs, H)) return ERR_ARGS;
     if (!k || !v || !aligned(k, 16) || !aligned(v, 16) || k_rs % 8 || v_rs % 8 || k_hs % 8 || v_hs % 8) return ERR_ARGS;
@@ -102,7 +102,7 @@ bool attn_stage_ok(const void* q_raw, const void* out, const float* wq, int tabl
                    int p0, int causal, float scale, int64_t q_rs, int64_t o_rs, int config) {
     if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return false;
     if (!(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return false;
-    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_PAIR_W4) return false;
+    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WS_W8) return false;
     if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return false;
     if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H)) return false;
     return table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) && (!wq || aligned(wq, 16));

@@ -62,7 +62,8 @@ enum AttnConfig : int {
     ATTN_CFG_PINGPONG_W8 = 4,  // ping-pong kernel: two wave groups alternating MFMA and VALU clusters
     ATTN_CFG_WIDE_W4 = 5,      // pipelined kernel, 4 waves x 64 queries, 32-key tiles: 256-query blocks, one wave per SIMD
     ATTN_CFG_PAIR_W4 = 6,      // pipelined kernel, 4 waves x 64 queries, 64-key tiles, scheduled: 256-query blocks
-    ATTN_CFG_LAST = 6,
+    ATTN_CFG_WS_W8 = 7,        // warp-specialised kernel: 4 pairs of waves (scores + softmax | PV), 256-query blocks
+    ATTN_CFG_LAST = 7,
 };
 
 // v_t: values come as packed V^T tiles (VPackArgs layout; a.v = the [HK][ntiles] tile array, a.v_hs = ntiles*8192)
@@ -75,6 +76,8 @@ hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config
 hipError_t launch_compact_keys(const void* k, const void* v, int64_t kv_rs, const uint8_t* kmask, int nkeys,
                                int n_valid, int HK, void* idx, void* kc, void* vc, hipStream_t stream);
 hipError_t launch_pair(const AttnArgs& a, int qk, bool v_t, hipStream_t stream);
+// The warp-specialised kernel (attn_ws.hip): queries fused with table kind qk, values as packed V^T tiles, non-causal.
+hipError_t launch_ws(const AttnArgs& a, int qk, hipStream_t stream);
 bool attention_config_reads_vt(int config);
 hipError_t launch_rms_rope(const RopeArgs& a, hipStream_t stream);
 int attention_block_rows(int config);

@@ -27,6 +27,7 @@ TABLE_NONE, TABLE_COSSIN_F32, TABLE_MAT2_BF16, TABLE_MAT2_F32 = 0, 1, 2, 3
 PAIR_INTERLEAVED, PAIR_SPLIT_HALF = 0, 1
 WEIGHT_NONE, WEIGHT_F32, WEIGHT_BF16 = 0, 1, 2
 CFG_AUTO, CFG_PIPE_W8, CFG_PIPE_W4, CFG_REGSTAGE_W8, CFG_PINGPONG_W8, CFG_WIDE_W4, CFG_PAIR_W4 = 0, 1, 2, 3, 4, 5, 6
+CFG_WS_W8 = 7
 SCALE_128 = float(torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32))  # f32 1/sqrt(128) = 0x3DB504F3
 
 

@@ -19,6 +19,8 @@ torch = pytest.importorskip("torch")
 from localrouter_amd import ops  # noqa: E402
 
 CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4, ops.CFG_PAIR_W4]
+# the fused / prepared calls also run the warp-specialised kernel (it reads packed V^T tiles only)
+FUSED_CONFIGS = CONFIGS + [ops.CFG_WS_W8]
 
 
 def _qkv(seed, W, nk, H, HK):
@@ -208,7 +210,7 @@ def test_rms_rope_qk_h3_in_place():
 
 
 # ------------------------------------------------------------------------------------------ the fused op
-@pytest.mark.parametrize("cfg", CONFIGS)
+@pytest.mark.parametrize("cfg", FUSED_CONFIGS)
 @pytest.mark.parametrize("kind,pairing,rot,causal,p0,n_pre,HK", [
     (1, 0, 128, 0, 0, 0, 2),
     (1, 1, 128, 0, 0, 0, 2),
@@ -259,11 +261,12 @@ def test_fused_overflowing_scores():
     wq = torch.full((128,), 5.0, dtype=torch.float32, device="cuda")
     wk = torch.full((128,), 5.0, dtype=torch.float32, device="cuda")
     outs = []
-    for cfg in (ops.CFG_PIPE_W8, ops.CFG_PAIR_W4):
+    for cfg in (ops.CFG_PIPE_W8, ops.CFG_PAIR_W4, ops.CFG_WS_W8):
         o = ops.joint_attention(to_dev(q), to_dev(k), to_dev(v), q_norm=wq, k_norm=wk, table_kind=0, config=cfg)
         torch.cuda.synchronize()
         outs.append(from_dev(o))
     assert_close(outs[1], bf16_f32(outs[0]), what="fused overflow: pair vs running max")
+    assert_close(outs[2], bf16_f32(outs[0]), what="fused overflow: warp-specialised vs running max")
 
 
 # ------------------------------------------------------------------------------------------ the two stages
@@ -298,7 +301,7 @@ def test_kv_prepare_layout_and_prepared_equals_fused(Sk, HK, n_pre):
         assert np.allclose(bf16_f32(keys[:, n_pre:].transpose(1, 0, 2)), kref, rtol=1e-2, atol=1e-2)
     tq = (_dev_table(qa), _dev_table(qb))
     outs = []
-    for cfg in (ops.CFG_AUTO, ops.CFG_PIPE_W4, ops.CFG_PAIR_W4):
+    for cfg in (ops.CFG_AUTO, ops.CFG_PIPE_W4, ops.CFG_PAIR_W4, ops.CFG_WS_W8):
         o = ops.joint_attention_prepared(to_dev(q), ws, Sk, HK, q_table=tq, config=cfg)
         f = ops.joint_attention(to_dev(q), to_dev(k), to_dev(v), q_table=tq, k_table=(_dev_table(ka), _dev_table(kb)),
                                 n_pre=n_pre, config=cfg)

@@ -42,7 +42,7 @@ def _oracle_rows(qb, kb, vb, cos, sin, rows):
     return oracle.attention(qh, kh, oracle.bf16_to_f32(vb), precise=False)
 
 
-@pytest.mark.parametrize("cfg", [ops.CFG_AUTO, ops.CFG_PAIR_W4])
+@pytest.mark.parametrize("cfg", [ops.CFG_AUTO, ops.CFG_PAIR_W4, ops.CFG_WS_W8])
 @pytest.mark.parametrize("name,n_text,grid", [("cfg1", 256, (32, 32)), ("cfg2", 512, (64, 64))])
 def test_baseline_image_shapes_all_rows(name, n_text, grid, cfg):
     cos, sin = rope.grid2d_table(n_text, *grid)
@@ -123,7 +123,7 @@ def test_default_config_matches_every_config_bitwise_class():
     vb = oracle.synth_bf16(106, 3, (S, 4, 128))
     outs = []
     for cfg in (ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4,
-                ops.CFG_PAIR_W4):
+                ops.CFG_PAIR_W4, ops.CFG_WS_W8):
         tc, ts = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
         o = ops.joint_attention(to_dev(qb), to_dev(kb), to_dev(vb), table_kind=ops.TABLE_COSSIN_F32,
                                 q_table=(tc, ts), config=cfg)
