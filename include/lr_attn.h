@@ -105,6 +105,17 @@ int lr_attention_bf16_ex(const void* q, const void* k, const void* v, void* out,
                          int config, lr_stream_t stream);
 
 /*
+ * lr_attention_bf16 with device scratch: a call with few query blocks (fewer than 128 blocks of 256 queries x heads,
+ * non-causal, e.g. 218 queries over 50,220 keys) is split over the keys into ranges that fill the GPU, each range's
+ * partial result written to the workspace, then merged (flash-decoding). lr_attention_ws_bytes is the workspace the
+ * call needs (0: it will not split; workspace may then be NULL). Results equal lr_attention_bf16's to fp32 rounding.
+ */
+size_t lr_attention_ws_bytes(int W, int H, int nkeys, int causal);
+int lr_attention_bf16_ws(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK,
+                         int nkeys, int causal, float scale, int64_t q_row_stride, int64_t kv_row_stride,
+                         int64_t out_row_stride, void* workspace, size_t workspace_bytes, lr_stream_t stream);
+
+/*
  * Attention under a key-padding mask: keys j with kmask[j] == 0 are left out (torch's bool key-padding mask, SDPA's
  * additive 0 / -inf), the drop-in for Kandinsky-6's attention.Call with mask = .keys
  * (src/engines/kandinsky6/dit/attention.zig:21-27, dispatched by launch.zig:239-255). Non-causal; q, out rows

@@ -336,7 +336,19 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
     const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
     const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
     const int nqb = (a.W + BM - 1) / BM;
-    const int head = logical / nqb, qblk = logical - head * nqb;
+    // key split: workgroup (query block, split) takes key tiles [split * per_split, ...) as if they were all the keys
+    const int nsplit = REDO ? 1 : (a.nsplit > 1 ? a.nsplit : 1);
+    const int split = logical % nsplit, lq = logical / nsplit;
+    const int head = lq / nqb, qblk = lq - head * nqb;
+    if (nsplit > 1) {
+        const int all_tiles = (a.nkeys + BT - 1) / BT;
+        const int per_split = (all_tiles + nsplit - 1) / nsplit;
+        const int key0 = split * per_split * BT;
+        const int64_t t0 = (int64_t)split * per_split;
+        a.k += t0 * BT * a.k_rs;
+        a.v += VT ? t0 * TILE : t0 * BT * a.v_rs;
+        a.nkeys = max(0, min(a.nkeys - key0, per_split * BT));
+    }
     const int hk = head / a.G;
     const int row0 = qblk * BM, wrow0 = row0 + wave * 32 * NQB;
     const int last_row = min(row0 + BM, a.W) - 1;
@@ -743,7 +755,31 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
     }
     if (t < ntiles) step(t, sA, sB, mx_cur);
 
-    // ---- epilogue: O / l -> bf16 rows
+    // ---- epilogue: O / l -> bf16 rows (or, with a key split, this range's partial result)
+    if (nsplit > 1) {
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb) {
+            const int qrow = wrow0 + 32 * nb + n;
+            const float l = wave_pair_sum(l_sum[nb]);
+            if (qrow < a.W) {
+                const int64_t slot = ((int64_t)head * a.W + qrow) * nsplit + split;
+                float* po = a.part_o + slot * D + 4 * hf;
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int gg = 0; gg < 4; ++gg)
+                        *reinterpret_cast<f32x4*>(po + 32 * db + 8 * gg) =
+                            f32x4{o[nb][db][4 * gg], o[nb][db][4 * gg + 1], o[nb][db][4 * gg + 2],
+                                  o[nb][db][4 * gg + 3]};
+                if (hf == 0) {
+                    // an empty key range (l = 0) contributes nothing whatever its reference
+                    a.part_ml[2 * slot] = l > 0.0f ? m_used[nb] : -INFINITY;
+                    a.part_ml[2 * slot + 1] = l;
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int nb = 0; nb < NQB; ++nb) {
         const int qrow = wrow0 + 32 * nb + n;
@@ -762,6 +798,30 @@ __attribute__((amdgpu_waves_per_eu(NQB == 1 ? 2 : 1, NQB == 1 ? 2 : 1))) void at
                 }
         }
     }
+}
+
+// One wave per (head, query row): O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s, two dims a lane.
+__global__ void attn_split_combine_kernel(AttnArgs a) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= (int64_t)a.H * a.W) return;
+    const int head = (int)(r / a.W), qrow = (int)(r - (int64_t)head * a.W);
+    const int ns = a.nsplit;
+    const float* ml = a.part_ml + r * ns * 2;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, ml[2 * s]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int s = 0; s < ns; ++s) {
+        const float m = ml[2 * s];
+        if (m == -INFINITY) continue;
+        const float w = __builtin_amdgcn_exp2f(m - M);
+        L = fmaf(w, ml[2 * s + 1], L);
+        const float* po = a.part_o + (r * ns + s) * D + 2 * lane;
+        o0 = fmaf(w, po[0], o0);
+        o1 = fmaf(w, po[1], o1);
+    }
+    const float inv = 1.0f / L;
+    *reinterpret_cast<uint32_t*>(a.out + (int64_t)qrow * a.o_rs + head * D + 2 * lane) = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
 // ------------------------------------------------------------------------------------------------ ping-pong kernel
@@ -1053,7 +1113,7 @@ template <int NW, int NQB, int BT, int NS, int QK, bool VT = false, bool REDO = 
 hipError_t launch_pipe(const AttnArgs& a, hipStream_t stream) {
     constexpr int BM = 32 * NQB * NW;
     const int64_t nqb = (a.W + BM - 1) / BM;
-    const int64_t blocks = nqb * a.H;
+    const int64_t blocks = nqb * a.H * (!REDO && a.nsplit > 1 ? a.nsplit : 1);
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL((attn_fwd_pipe_kernel<NW, NQB, BT, NS, QK, VT, REDO>), dim3((unsigned)blocks), dim3(NW * 64), 0,
                        stream, a);
@@ -1078,6 +1138,12 @@ hipError_t launch_ws_checked(const AttnArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+hipError_t launch_split_combine(const AttnArgs& a, hipStream_t stream) {
+    const int64_t rows = (int64_t)a.H * a.W;
+    hipLaunchKernelGGL(attn_split_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
 
 int attention_block_rows(int config) {
     switch (config) {

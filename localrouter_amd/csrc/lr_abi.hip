@@ -23,9 +23,28 @@ inline bool rows_ok(const void* p, int64_t rs, int heads) {
 
 inline bool scale_ok(float s) { return s > 0.0f && isfinite(s); }
 
+// Key-split count for plain attention over value rows (the pipelined kernel, 256-query blocks): a launch with fewer
+// than 128 query blocks is split over the keys into enough ranges of at least 4 key tiles to give ~256 workgroups,
+// then merged by a combine pass. 1 = no split (causal calls are never split).
+int split_count(int W, int H, int nkeys, int causal) {
+    if (causal || W < 1 || H < 1 || nkeys < 1) return 1;
+    const int64_t blocks = (int64_t)((W + 255) / 256) * H;
+    const int tiles = (nkeys + 63) / 64;
+    if (blocks >= 128 || tiles < 8) return 1;
+    int ns = (int)std::min<int64_t>((256 + blocks - 1) / blocks, tiles / 4);
+    ns = std::max(1, std::min(ns, 64));
+    const int per = (tiles + ns - 1) / ns;
+    return (tiles + per - 1) / per;   // no empty range
+}
+size_t split_bytes(int W, int H, int ns) {
+    if (ns <= 1) return 0;
+    const size_t rows = (size_t)H * W * ns;
+    return ((rows * lr::D * 4 + 255) & ~(size_t)255) + ((rows * 8 + 255) & ~(size_t)255);
+}
+
 int attention_impl(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK, int nkeys,
                    int causal, float scale, int64_t q_rs, int64_t k_rs, int64_t v_rs, int64_t o_rs, int64_t k_hs,
-                   int64_t v_hs, int config, hipStream_t stream) {
+                   int64_t v_hs, int config, hipStream_t stream, void* workspace = nullptr, size_t ws_bytes = 0) {
     if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || nkeys < 1 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
     if (!scale_ok(scale) || config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WS_W8) return ERR_ARGS;
     if ((int64_t)p0 + W > INT_MAX - 512 || nkeys > INT_MAX - 512 || W > INT_MAX - 512) return ERR_ARGS;
@@ -42,6 +61,18 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
     a.W = W; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = nkeys; a.p0 = p0; a.causal = causal;
     a.c = scale * 1.4426950408889634f;
     a.table_kind = lr::TABLE_NONE;
+    const int ns = split_count(W, H, nkeys, causal);
+    const bool split = workspace && ns > 1 && (config == LR_ATTN_CFG_AUTO || config == LR_ATTN_CFG_PIPE_W8) &&
+                       k_hs == lr::D && v_hs == lr::D && ws_bytes >= split_bytes(W, H, ns) && aligned(workspace, 256);
+    if (split) {
+        a.nsplit = ns;
+        a.part_o = static_cast<float*>(workspace);
+        a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                             (((size_t)H * W * ns * lr::D * 4 + 255) & ~(size_t)255));
+        const hipError_t e = lr::launch_attention(a, false, false, LR_ATTN_CFG_PIPE_W8, stream);
+        if (e != hipSuccess) return (int)e;
+        return (int)lr::launch_split_combine(a, stream);
+    }
     return (int)lr::launch_attention(a, false, false, config, stream);
 }
 
@@ -278,6 +309,22 @@ int lr_attention_bf16(const void* q, const void* k, const void* v, void* out, in
     if (kv_row_stride < (int64_t)HK * lr::D) return ERR_ARGS;
     return attention_impl(q, k, v, out, p0, W, H, HK, nkeys, causal, scale, q_row_stride, kv_row_stride,
                           kv_row_stride, out_row_stride, lr::D, lr::D, LR_ATTN_CFG_AUTO, stream);
+}
+
+size_t lr_attention_ws_bytes(int W, int H, int nkeys, int causal) {
+    return split_bytes(W, H, split_count(W, H, nkeys, causal));
+}
+
+int lr_attention_bf16_ws(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK,
+                         int nkeys, int causal, float scale, int64_t q_row_stride, int64_t kv_row_stride,
+                         int64_t out_row_stride, void* workspace, size_t workspace_bytes, lr_stream_t stream) {
+    if (kv_row_stride < (int64_t)HK * lr::D) return ERR_ARGS;
+    if (workspace_bytes < lr_attention_ws_bytes(W, H, nkeys, causal) || (workspace && !aligned(workspace, 256)))
+        return ERR_ARGS;
+    if (workspace_bytes > 0 && !workspace) return ERR_ARGS;
+    return attention_impl(q, k, v, out, p0, W, H, HK, nkeys, causal, scale, q_row_stride, kv_row_stride,
+                          kv_row_stride, out_row_stride, lr::D, lr::D, LR_ATTN_CFG_AUTO,
+                          reinterpret_cast<hipStream_t>(stream), workspace, workspace_bytes);
 }
 
 size_t lr_attention_kmask_workspace_bytes(int n_valid, int HK) {

@@ -22,6 +22,12 @@ struct AttnArgs {
     const void* qtb;
     int64_t tab_stride;               // table row stride (elements)
     float eps;
+    // Split over the keys (plain pipelined kernel, non-causal): nsplit > 1 runs every query block as nsplit workgroups
+    // over consecutive key-tile ranges, each writing its unnormalised O (fp32 [H][W][nsplit][128]) and its reference
+    // and row sum (fp32 [H][W][nsplit][2], exp2 domain) instead of out; attn_split_combine merges them.
+    int nsplit;
+    float* part_o;
+    float* part_ml;
 };
 
 // V^T packing of the prepared-keys path: bf16 V rows (key j of kv head g at v + j*v_rs + g*128) into
@@ -76,6 +82,8 @@ hipError_t launch_attention(const AttnArgs& a, bool fuse_q, bool v_t, int config
 hipError_t launch_compact_keys(const void* k, const void* v, int64_t kv_rs, const uint8_t* kmask, int nkeys,
                                int n_valid, int HK, void* idx, void* kc, void* vc, hipStream_t stream);
 hipError_t launch_pair(const AttnArgs& a, int qk, bool v_t, hipStream_t stream);
+// Merge the key-split partials of a launch with a.nsplit > 1 into out (bf16 rows).
+hipError_t launch_split_combine(const AttnArgs& a, hipStream_t stream);
 // The warp-specialised kernel (attn_ws.hip): queries fused with table kind qk, values as packed V^T tiles, non-causal.
 hipError_t launch_ws(const AttnArgs& a, int qk, hipStream_t stream);
 bool attention_config_reads_vt(int config);

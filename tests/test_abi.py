@@ -230,3 +230,17 @@ def test_kmask_attention_rejects():
     assert call(kv_rs=255) == HIP_ERROR_INVALID_VALUE
     assert call(H=3) == HIP_ERROR_INVALID_VALUE                 # H % HK
     assert call(scale=0.0) == HIP_ERROR_INVALID_VALUE
+
+
+def test_split_workspace_sizes_and_rejects():
+    L = _lib.load()
+    assert L.lr_attention_ws_bytes(50220, 32, 50220, 0) == 0          # plenty of query blocks: no split
+    assert L.lr_attention_ws_bytes(218, 16, 50220, 1) == 0            # causal: never split
+    nb = L.lr_attention_ws_bytes(218, 16, 50220, 0)                   # K6 audio-from-video: split
+    assert nb >= 218 * 16 * 2 * 130 * 4
+    assert L.lr_attention_ws_bytes(218, 16, 300, 0) == 0              # too few key tiles to split
+    fake = 1 << 20
+    args = [fake, fake, fake, fake, 0, 218, 16, 16, 50220, 0, 0.088, 2048, 2048, 2048]
+    assert L.lr_attention_bf16_ws(*args, fake, nb - 1, None) == HIP_ERROR_INVALID_VALUE   # workspace too small
+    assert L.lr_attention_bf16_ws(*args, None, nb, None) == HIP_ERROR_INVALID_VALUE       # size without a pointer
+    assert L.lr_attention_bf16_ws(*args, fake + 16, nb, None) == HIP_ERROR_INVALID_VALUE  # not 256-aligned

@@ -101,3 +101,26 @@ def test_kmask_fewer_kept_than_declared_is_memory_safe():
     out = ops.attention_kmask(q, k, v, m, n_valid=12, scale=SCALE, workspace=ws)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
+
+
+@pytest.mark.parametrize("W,S,H,HK", [(218, 50220, 16, 16), (100, 4000, 4, 2), (256, 1000, 3, 3), (37, 517, 8, 1)])
+def test_key_split_attention(W, S, H, HK):
+    """lr_attention_bf16_ws splits few-query calls over the keys; the merged result meets the same bar as the unsplit
+    call (sampled rows at the K6 shape, every row otherwise)."""
+    from localrouter_amd import _lib, ops
+    dev = torch.device("cuda", 0)
+    nb = int(_lib.load().lr_attention_ws_bytes(W, H, S, 0))
+    print(f"key split: W {W} nkeys {S} heads {H}/{HK} workspace {nb}", flush=True)
+    assert nb > 0
+    g = torch.Generator(device=dev)
+    g.manual_seed(W + S)
+    q, k, v = _rand((W, H, 128), g, dev), _rand((S, HK, 128), g, dev), _rand((S, HK, 128), g, dev)
+    out = ops.attention_ws(q, k, v, scale=SCALE)
+    plain = ops.attention(q, k, v, scale=SCALE)
+    torch.cuda.synchronize()
+    rows = np.arange(W)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), scale=SCALE, precise=False, rows=rows)
+    err = np.abs(_f32(out) - ref)
+    dp = np.abs(_f32(out) - _f32(plain))
+    print(f"  max-abs {err.max():.3e} mean-abs {err.mean():.3e}; vs unsplit max {dp.max():.3e}", flush=True)
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3
