@@ -38,7 +38,7 @@ extern "C" {
 /* hipStream_t without pulling in the HIP headers: an opaque pointer (NULL = the default stream). */
 typedef struct ihipStream_t* lr_stream_t;
 
-#define LR_ATTN_ABI_VERSION 4
+#define LR_ATTN_ABI_VERSION 5
 #define LR_HEAD_DIM 128
 
 /* RoPE table kinds: how rotation coefficients are stored per token row, per pair p < rot_dim/2. */
@@ -77,6 +77,14 @@ typedef struct ihipStream_t* lr_stream_t;
                                       computes scores and softmax, the other the PV products, P handed over in LDS;
                                       fused / prepared calls, non-causal (causal calls run PAIR_W4); same fixed
                                       reference and second launch as PAIR_W4 */
+#define LR_ATTN_CFG_PAIR_SK_W4 8   /* PAIR_W4 under a stream-K schedule (fused / prepared calls): one workgroup per CU
+                                      over the blocks' key tiles laid end to end, a block cut between two workgroups
+                                      merged from two partials by a second kernel. Runs when the call is non-causal,
+                                      has at least as many 256-query blocks as CUs and whole blocks would leave more
+                                      than 3% of the last round idle (else as PAIR_W4). Needs LR_ATTN_SK_AREA_BYTES
+                                      more workspace. Measured slower than PAIR_W4 at the BASELINE shapes (the
+                                      workgroups of a head no longer stream the same K/V tiles together). */
+#define LR_ATTN_SK_AREA_BYTES ((size_t)2 * 256 * 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64) * 4)
 
 int lr_attn_abi_version(void);
 
@@ -155,7 +163,8 @@ int lr_rms_rope_qk_bf16(void* q, void* k, int64_t seq, int heads, int64_t q_row_
                         int rot_dim, float eps, lr_stream_t stream);
 
 /* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys, bf16 [HK][Sk][128], then (at a
- * 256-byte boundary) V packed as transposed 64-key tiles, bf16 [HK][ceil(Sk/64)][128][64]. */
+ * 256-byte boundary) V packed as transposed 64-key tiles, bf16 [HK][ceil(Sk/64)][128][64]. LR_ATTN_CFG_PAIR_SK_W4
+ * needs LR_ATTN_SK_AREA_BYTES more, right after them (the stream-K partials). */
 size_t lr_joint_attention_workspace_bytes(int Sk, int HK);
 
 /*
@@ -185,13 +194,15 @@ int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v
  *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated in registers) over that workspace.
  *                               config: LR_ATTN_CFG_AUTO, _PIPE_W8, _PIPE_W4 or _PAIR_W4 (the configurations that
  *                               read V^T tiles; the others are reached through lr_joint_attention_fused_ex).
- * Useful when keys and values are reused (a cached prefix) or to time the stages separately.
+ * Useful when keys and values are reused (a cached prefix) or to time the stages separately. The attention call
+ * reads the keys and V^T tiles and uses the stream-K area (when present) as scratch, so calls sharing one workspace
+ * run one at a time (one stream).
  */
 int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,
                         const float* k_norm_w, int table_kind, const void* k_table_a, const void* k_table_b,
                         int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sk, int HK, int n_pre,
                         void* workspace, size_t workspace_bytes, lr_stream_t stream);
-int lr_joint_attention_prepared(const void* q_raw, const void* workspace, size_t workspace_bytes, void* out,
+int lr_joint_attention_prepared(const void* q_raw, void* workspace, size_t workspace_bytes, void* out,
                                 const float* q_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
                                 int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sq, int Sk, int H,
                                 int HK, int p0, int causal, float scale, int64_t q_row_stride, int64_t out_row_stride,

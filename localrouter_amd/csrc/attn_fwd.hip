@@ -1154,7 +1154,7 @@ int attention_block_rows(int config) {
 
 bool attention_config_reads_vt(int config) {
     return config == ATTN_CFG_AUTO || config == ATTN_CFG_PIPE_W8 || config == ATTN_CFG_PIPE_W4 ||
-           config == ATTN_CFG_PAIR_W4 || config == ATTN_CFG_WS_W8;
+           config == ATTN_CFG_PAIR_W4 || config == ATTN_CFG_WS_W8 || config == ATTN_CFG_PAIR_SK_W4;
 }
 
 // The prepared-keys path over packed V^T tiles, queries fused with table kind K (the 64-key pipelined shapes).
@@ -1163,7 +1163,8 @@ hipError_t launch_vt(const AttnArgs& a, int config, hipStream_t stream) {
     switch (config) {
         case ATTN_CFG_PIPE_W8: return launch_pipe<8, 1, 64, 4, K, true>(a, stream);
         case ATTN_CFG_PIPE_W4: return launch_pipe<4, 1, 64, 2, K, true>(a, stream);
-        case ATTN_CFG_PAIR_W4: return launch_pair_checked<K, true>(a, stream);
+        case ATTN_CFG_PAIR_W4:
+        case ATTN_CFG_PAIR_SK_W4: return launch_pair_checked<K, true>(a, stream);   // stream-K when a.sk_part is set
         case ATTN_CFG_WS_W8: return launch_ws_checked<K>(a, stream);
         default: return hipErrorInvalidValue;
     }

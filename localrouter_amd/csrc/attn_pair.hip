@@ -32,6 +32,15 @@
 // domain) above the first tile's maximum. The epilogue checks l and O of every row; a wave with a row that is not
 // finite marks its first row with a NaN, and a second launch (the running-max kernel of attn_fwd.hip, over the same
 // 256-query blocks) recomputes exactly the marked blocks.
+//
+// Stream-K (SK). 256-query blocks over a whole number of CUs leave the last round of workgroups part-empty (432 blocks
+// on 256 CUs: 1.69 rounds of work in 2 rounds of time). The SK launch runs one workgroup per CU over the blocks' key
+// tiles laid end to end (block-major) and gives workgroup c the tiles [c T / n, (c + 1) T / n). With at least as many
+// blocks as workgroups a range holds the tail of one block, whole blocks, then the head of another, so a block is cut
+// at most once, at the start c T / n of some range c. Both parts of a cut block store their unnormalised O, reference
+// and per-lane row sums (the head part to slot 2c, the tail part to slot 2c + 1 of the partials area) and write no
+// output; no workgroup waits for another. A second kernel (attn_sk_combine_kernel) merges each cut block's two parts,
+// O = O1 2^(m1 - m) + O2 2^(m2 - m), l likewise, m = max, and writes its rows, marking overflow as the epilogue does.
 #include "lr_common.h"
 #include "lr_kernels.h"
 
@@ -92,8 +101,24 @@ constexpr int PNS = 4;                // ring stages
 constexpr int PTILE = BN * D;         // elements per K or V^T tile
 constexpr int PLOADS = BN / 4 / PW;   // 1 KB direct loads per wave per tile
 
-template <int QK, bool VT>
-__global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_pair_kernel(AttnArgs a) {
+// stream-K partials: per slot and wave, O as [2 nb][4 db][4 gg][64 lanes] float4, then m and the per-lane row sums as
+// [2 nb][2][64 lanes]
+constexpr int SK_WAVE_FLOATS = 2 * 4 * 16 * 64 + 2 * 2 * 64;
+constexpr int SK_ML = 2 * 4 * 16 * 64;   // offset of m, l in a wave's partial
+static_assert(PW * SK_WAVE_FLOATS == SK_SLOT_FLOATS, "partial slot size");
+
+// Cut point of stream-K range c (block, first tile of the tail part); tile 0 when the range starts at a block boundary
+struct SkCut {
+    int blk, t;
+};
+__device__ __forceinline__ SkCut sk_cut(int c, int nblk, int blk_tiles, int nwg) {
+    const int64_t pos = (int64_t)c * ((int64_t)nblk * blk_tiles) / nwg;
+    const int blk = (int)(pos / blk_tiles);
+    return SkCut{blk, (int)(pos - (int64_t)blk * blk_tiles)};
+}
+
+template <int QK, bool VT, bool SK>
+__global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_pair_kernel(AttnArgs a0) {
     // FOLD: fused queries arrive multiplied by scale * log2(e), so a score is already in the exp2 domain, and the
     // reference m is subtracted by the score MFMAs themselves (their accumulator starts at -m): P = exp2(S) with no
     // per-score VALU op. Plain queries keep exact raw scores: P = exp2(S * c - m).
@@ -110,15 +135,35 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     const int nwg = gridDim.x, b = blockIdx.x;
     const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
     const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
-    const int nqb = (a.W + PBM - 1) / PBM;
-    const int head = logical / nqb, qblk = logical - head * nqb;
+    const int nqb = (a0.W + PBM - 1) / PBM;
+    // SK: this workgroup's range of block-major key tiles; otherwise one whole block
+    const int blk_tiles = (a0.nkeys + BN - 1) / BN;
+    int64_t seg_pos = 0, seg_end = 1;
+    if constexpr (SK) {
+        const int64_t total = (int64_t)nqb * a0.H * blk_tiles;
+        seg_pos = (int64_t)logical * total / nwg;
+        seg_end = (int64_t)(logical + 1) * total / nwg;
+    }
+    const AttnArgs& a = a0;
+    for (bool first_seg = true; seg_pos < seg_end; first_seg = false) {
+    int blk = logical, t0 = 0, t1 = blk_tiles;
+    if constexpr (SK) {
+        blk = (int)(seg_pos / blk_tiles);
+        t0 = (int)(seg_pos - (int64_t)blk * blk_tiles);
+        t1 = (int)min((int64_t)blk_tiles, seg_end - (int64_t)blk * blk_tiles);
+        if (!first_seg) block_barrier();   // every wave is done with the previous segment's LDS
+    }
+    seg_pos = SK ? (int64_t)blk * blk_tiles + t1 : seg_end;
+    // the segment's key tiles [t0, t1) as if they were all the keys (non-causal when t0 > 0)
+    const int nk = SK ? min(a.nkeys - t0 * BN, (t1 - t0) * BN) : a.nkeys;
+    const int head = blk / nqb, qblk = blk - head * nqb;
     const int hk = head / a.G;
     const int row0 = qblk * PBM, wrow0 = row0 + wave * 64;
     const int last_row = min(row0 + PBM, a.W) - 1;
-    int ntiles = (a.nkeys + BN - 1) / BN;
+    int ntiles = (nk + BN - 1) / BN;
     if (a.causal) ntiles = min(ntiles, (a.p0 + last_row) / BN + 1);
-    const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
-    const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs;
+    const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs + (int64_t)t0 * BN * a.k_rs;
+    const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs + (int64_t)t0 * PTILE;
 
     // ---- ring loads: load j of a tile fills rows 4i..4i+3 (K, V rows) or dim rows 8i..8i+7 (V^T), i = wave + PW j, by
     // buffer_load_dwordx4 ... lds from a per-tile descriptor (SGPRs) and a constant per-lane byte offset. The
@@ -148,7 +193,7 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         uint32_t last_rec;
     };
     auto rows_stream = [&](const uint16_t* base, int64_t rs) __attribute__((always_inline)) {
-        const int64_t last = (int64_t)(a.nkeys - 1 - (ntiles - 1) * BN) * rs * 2 + 2 * D;
+        const int64_t last = (int64_t)(nk - 1 - (ntiles - 1) * BN) * rs * 2 + 2 * D;
         return TileStream{(uint64_t)(uintptr_t)base, (uint64_t)(BN * rs * 2),
                           (uint32_t)(last < 0xffffffffLL ? last : 0xffffffffLL)};
     };
@@ -267,7 +312,7 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
 
     const float c = a.c;
     // the tiles from t_mask on have keys past nkeys or, causal, past some query of this wave
-    int t_mask = a.nkeys / BN;
+    int t_mask = nk / BN;
     if (a.causal) t_mask = min(t_mask, (a.p0 + wrow0 - (BN - 1)) >= 0 ? (a.p0 + wrow0 - (BN - 1)) / BN + 1 : 0);
     auto needs_mask = [&](int t) __attribute__((always_inline)) { return t >= t_mask; };
     // Register r of score tile (nb, mb) holds key t BN + 32 mb + 8 hf + c(r), c(r) = 16 (r >> 3) + (r & 7), of query
@@ -276,7 +321,7 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
         const int key0 = t * BN + 32 * mb + 8 * hf;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            int lim = a.nkeys - key0;
+            int lim = nk - key0;
             if (a.causal) lim = min(lim, a.p0 + wrow0 + 32 * nb + n - key0 + 1);
 #pragma unroll
             for (int r = 0; r < 16; ++r)
@@ -487,8 +532,29 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     LR_WAIT_VMCNT(0);   // the last steps' loads (into the dummy area) have landed before the workgroup ends
     fence_o(o);
 
-    // ---- epilogue: O / l -> bf16 rows. A row whose P overflowed the fixed reference (l or O not finite) marks its
-    // wave's first row with a NaN; the second launch recomputes such blocks with a running max.
+    if constexpr (SK) {
+        if (t0 > 0 || t1 < blk_tiles) {   // a part of a cut block: store the partial, go on with the next segment
+            const int slot = t0 > 0 ? 2 * logical + 1 : 2 * (logical + 1);
+            float* part = a.sk_part + (size_t)slot * (PW * SK_WAVE_FLOATS) + wave * SK_WAVE_FLOATS;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int gg = 0; gg < 4; ++gg) {
+                        const float4 v = {o[nb][db][4 * gg], o[nb][db][4 * gg + 1], o[nb][db][4 * gg + 2],
+                                          o[nb][db][4 * gg + 3]};
+                        *reinterpret_cast<float4*>(part + 4 * (((nb * 4 + db) * 4 + gg) * 64 + lane)) = v;
+                    }
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                part[SK_ML + (2 * nb) * 64 + lane] = m_used[nb];
+                part[SK_ML + (2 * nb + 1) * 64 + lane] = ls[nb];
+            }
+            continue;
+        }
+    }
+
     bool overflow = false;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
@@ -516,6 +582,69 @@ __global__ __launch_bounds__(PW * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1
     }
     if (__builtin_amdgcn_ballot_w64(overflow) && lane == 0 && wrow0 < a.W)
         a.out[(int64_t)wrow0 * a.o_rs + head * D] = 0x7fc0;   // bf16 quiet NaN
+    }   // segments
+}
+
+// Merge the two parts of the block cut at the start of stream-K range c = blockIdx.x + 1 (none when that range starts at a
+// block boundary) and write its rows: one wave per 64-query quarter, each lane the (row, dims) set its wave's lane held
+// in the attention kernel.
+__global__ __launch_bounds__(PW * 64) void attn_sk_combine_kernel(AttnArgs a, int blk_tiles) {
+    const int c = blockIdx.x + 1, nwg = gridDim.x + 1;
+    const int nqb = (a.W + PBM - 1) / PBM;
+    const SkCut cut = sk_cut(c, nqb * a.H, blk_tiles, nwg);
+    if (cut.t == 0) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, hf = lane >> 5;
+    const int head = cut.blk / nqb, qblk = cut.blk - head * nqb;
+    const int wrow0 = qblk * PBM + wave * 64;
+    const float* ph = a.sk_part + (size_t)(2 * c) * (PW * SK_WAVE_FLOATS) + wave * SK_WAVE_FLOATS;
+    const float* pt = ph + PW * SK_WAVE_FLOATS;
+    bool overflow = false;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const float mh = ph[SK_ML + (2 * nb) * 64 + lane], lh = ph[SK_ML + (2 * nb + 1) * 64 + lane];
+        const float mt = pt[SK_ML + (2 * nb) * 64 + lane], lt = pt[SK_ML + (2 * nb + 1) * 64 + lane];
+        const float mn = fmaxf(mh, mt);
+        const float sh = __builtin_amdgcn_exp2f(mh - mn), st = __builtin_amdgcn_exp2f(mt - mn);
+        const float l = wave_pair_sum(lh * sh + lt * st);
+        const float inv = 1.0f / l;
+        bool bad = !__builtin_isfinite(l);
+        const int qrow = wrow0 + 32 * nb + n;
+        uint16_t* dst = a.out + (int64_t)qrow * a.o_rs + head * D + 4 * hf;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                const int i = 4 * (((nb * 4 + db) * 4 + gg) * 64 + lane);
+                const float4 x = *reinterpret_cast<const float4*>(ph + i);
+                const float4 y = *reinterpret_cast<const float4*>(pt + i);
+                const float y0 = (x.x * sh + y.x * st) * inv, y1 = (x.y * sh + y.y * st) * inv;
+                const float y2 = (x.z * sh + y.z * st) * inv, y3 = (x.w * sh + y.w * st) * inv;
+                bad = bad || !__builtin_isfinite(y0) || !__builtin_isfinite(y1) || !__builtin_isfinite(y2) ||
+                      !__builtin_isfinite(y3);
+                if (qrow < a.W) {
+                    u32x2 w;
+                    w[0] = pack_bf16x2(y0, y1);
+                    w[1] = pack_bf16x2(y2, y3);
+                    *reinterpret_cast<u32x2*>(dst + 32 * db + 8 * gg) = w;
+                }
+            }
+        overflow = overflow || (bad && qrow < a.W);
+    }
+    if (__builtin_amdgcn_ballot_w64(overflow) && lane == 0 && wrow0 < a.W)
+        a.out[(int64_t)wrow0 * a.o_rs + head * D] = 0x7fc0;   // marked for the running-max launch
+}
+
+// CUs of the current device (cached per device), capped at SK_MAX_WG
+int sk_workgroups() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) return 0;
+        cus[dev] = min(n, SK_MAX_WG);
+    }
+    return cus[dev];
 }
 
 template <int QK, bool VT>
@@ -523,7 +652,23 @@ hipError_t launch_pair_t(const AttnArgs& a, hipStream_t stream) {
     const int64_t nqb = (a.W + PBM - 1) / PBM;
     const int64_t blocks = nqb * a.H;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_pair_kernel<QK, VT>), dim3((unsigned)blocks), dim3(PW * 64), 0, stream, a);
+    if constexpr (VT) {
+        // stream-K where whole blocks would leave more than 3% of the last round idle, given the partials area and at
+        // least one block per workgroup
+        const int nwg = a.sk_part && !a.causal ? sk_workgroups() : 0;
+        if (nwg > 1 && blocks >= nwg) {
+            const int64_t rounds = (blocks + nwg - 1) / nwg;
+            if (blocks * 100 < rounds * nwg * 97) {
+                hipLaunchKernelGGL((attn_pair_kernel<QK, VT, true>), dim3((unsigned)nwg), dim3(PW * 64), 0, stream, a);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                hipLaunchKernelGGL(attn_sk_combine_kernel, dim3((unsigned)(nwg - 1)), dim3(PW * 64), 0, stream, a,
+                                   (int)((a.nkeys + BN - 1) / BN));
+                return hipGetLastError();
+            }
+        }
+    }
+    hipLaunchKernelGGL((attn_pair_kernel<QK, VT, false>), dim3((unsigned)blocks), dim3(PW * 64), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -10,6 +10,8 @@
 #include "lr_int8.h"
 #include "lr_kernels.h"
 
+static_assert(LR_ATTN_SK_AREA_BYTES == lr::SK_AREA_BYTES, "stream-K area size");
+
 namespace {
 
 constexpr int ERR_ARGS = (int)hipErrorInvalidValue;
@@ -133,14 +135,14 @@ bool attn_stage_ok(const void* q_raw, const void* out, const float* wq, int tabl
                    int p0, int causal, float scale, int64_t q_rs, int64_t o_rs, int config) {
     if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return false;
     if (!(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return false;
-    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WS_W8) return false;
+    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_PAIR_SK_W4) return false;
     if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return false;
     if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H)) return false;
     return table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) && (!wq || aligned(wq, 16));
 }
 
 // The attention stage over prepared keys: values from the workspace's V^T tiles when v is null, else from v rows.
-int prepared_impl(const void* q_raw, const void* ws, size_t ws_bytes, const void* v, int64_t v_rs, void* out,
+int prepared_impl(const void* q_raw, void* ws, size_t ws_bytes, const void* v, int64_t v_rs, void* out,
                   const float* wq, int table_kind, const void* qta, const void* qtb, int64_t tab_stride, int pairing,
                   int rot, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_rs,
                   int64_t o_rs, int config, hipStream_t stream) {
@@ -168,6 +170,10 @@ int prepared_impl(const void* q_raw, const void* ws, size_t ws_bytes, const void
     a.wq = wq;
     a.table_kind = table_kind; a.pairing = pairing; a.rot = rot;
     a.qta = qta; a.qtb = qtb; a.tab_stride = tab_stride; a.eps = eps;
+    if (config == LR_ATTN_CFG_PAIR_SK_W4) {   // the stream-K partials follow the V^T tiles
+        if (v || ws_bytes < ws_bytes_needed(Sk, HK) + lr::SK_AREA_BYTES) return ERR_ARGS;
+        a.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_bytes_needed(Sk, HK));
+    }
     return (int)lr::launch_attention(a, true, v == nullptr, config, stream);
 }
 
@@ -416,7 +422,7 @@ int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, 
                    pairing, rot_dim, eps, Sk, HK, n_pre, workspace, workspace_bytes, stream);
 }
 
-int lr_joint_attention_prepared(const void* q_raw, const void* workspace, size_t workspace_bytes, void* out,
+int lr_joint_attention_prepared(const void* q_raw, void* workspace, size_t workspace_bytes, void* out,
                                 const float* q_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
                                 int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sq, int Sk, int H,
                                 int HK, int p0, int causal, float scale, int64_t q_row_stride, int64_t out_row_stride,

@@ -28,7 +28,14 @@ struct AttnArgs {
     int nsplit;
     float* part_o;
     float* part_ml;
+    // Stream-K launch of the 64-query-per-wave kernel over packed V^T (used when set): 2 SK_MAX_WG slots of
+    // SK_SLOT_FLOATS floats, the two parts of each cut block
+    float* sk_part;
 };
+
+constexpr int SK_MAX_WG = 256;                                   // stream-K workgroups at most (one per CU)
+constexpr int SK_SLOT_FLOATS = 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64);   // one part: 4 waves of O, m, l
+constexpr size_t SK_AREA_BYTES = (size_t)2 * SK_MAX_WG * SK_SLOT_FLOATS * 4;
 
 // V^T packing of the prepared-keys path: bf16 V rows (key j of kv head g at v + j*v_rs + g*128) into
 // [HK][ntiles][128][64], one contiguous 16 KB block of 128 dim rows x 64 keys per 64-key tile, keys past Sk zero.
@@ -69,7 +76,8 @@ enum AttnConfig : int {
     ATTN_CFG_WIDE_W4 = 5,      // pipelined kernel, 4 waves x 64 queries, 32-key tiles: 256-query blocks, one wave per SIMD
     ATTN_CFG_PAIR_W4 = 6,      // pipelined kernel, 4 waves x 64 queries, 64-key tiles, scheduled: 256-query blocks
     ATTN_CFG_WS_W8 = 7,        // warp-specialised kernel: 4 pairs of waves (scores + softmax | PV), 256-query blocks
-    ATTN_CFG_LAST = 7,
+    ATTN_CFG_PAIR_SK_W4 = 8,   // PAIR_W4 under the stream-K schedule (AttnArgs::sk_part set)
+    ATTN_CFG_LAST = 8,
 };
 
 // v_t: values come as packed V^T tiles (VPackArgs layout; a.v = the [HK][ntiles] tile array, a.v_hs = ntiles*8192)

@@ -28,6 +28,7 @@ PAIR_INTERLEAVED, PAIR_SPLIT_HALF = 0, 1
 WEIGHT_NONE, WEIGHT_F32, WEIGHT_BF16 = 0, 1, 2
 CFG_AUTO, CFG_PIPE_W8, CFG_PIPE_W4, CFG_REGSTAGE_W8, CFG_PINGPONG_W8, CFG_WIDE_W4, CFG_PAIR_W4 = 0, 1, 2, 3, 4, 5, 6
 CFG_WS_W8 = 7
+CFG_PAIR_SK_W4 = 8
 SCALE_128 = float(torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32))  # f32 1/sqrt(128) = 0x3DB504F3
 
 
@@ -167,8 +168,15 @@ def rms_rope_qk(q: torch.Tensor, k: torch.Tensor, q_norm: torch.Tensor, k_norm: 
               _ptr(freqs), f_rs, rot, eps, _stream())
 
 
-def workspace_bytes(sk: int, kv_heads: int) -> int:
-    return int(_lib.load().lr_joint_attention_workspace_bytes(sk, kv_heads))
+# the stream-K area at the end of a joint-attention workspace: 512 partial slots of 4 waves x
+# (O [2][4][4][64] float4 + m, l [2][2][64]) fp32
+SK_AREA_BYTES = 2 * 256 * 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64) * 4
+
+
+def workspace_bytes(sk: int, kv_heads: int, stream_k: bool = False) -> int:
+    """lr_joint_attention_workspace_bytes; stream_k=True: plus the stream-K area CFG_PAIR_SK_W4 needs."""
+    n = int(_lib.load().lr_joint_attention_workspace_bytes(sk, kv_heads))
+    return n + SK_AREA_BYTES if stream_k and n else n
 
 
 def joint_attention(q_raw: torch.Tensor, k_raw: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *,
@@ -201,7 +209,7 @@ def joint_attention(q_raw: torch.Tensor, k_raw: torch.Tensor, v: torch.Tensor, o
         stride = qa.stride(0)
         if ka.stride(0) != stride:
             raise ValueError("q and k tables must share a row stride")
-    need = workspace_bytes(Sk, HK)
+    need = workspace_bytes(Sk, HK, stream_k=config == CFG_PAIR_SK_W4)
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q_raw.device)
     if workspace.numel() * workspace.element_size() < need:

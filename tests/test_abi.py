@@ -7,7 +7,7 @@ import re
 
 import pytest
 
-from localrouter_amd import _lib
+from localrouter_amd import _lib, ops
 
 HIP_ERROR_INVALID_VALUE = 1
 
@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version():
     header = _lib.HEADER.read_text()
     declared = int(re.search(r"#define LR_ATTN_ABI_VERSION (\d+)", header).group(1))
-    assert _lib.load().lr_attn_abi_version() == declared == 4
+    assert _lib.load().lr_attn_abi_version() == declared == 5
 
 
 def test_workspace_bytes():
@@ -39,6 +39,11 @@ def test_workspace_bytes():
     assert L.lr_joint_attention_workspace_bytes(4608, 24) == 4608 * 24 * 128 * 2 + 24 * 72 * 128 * 64 * 2
     assert L.lr_joint_attention_workspace_bytes(3, 1) == 768 + 128 * 64 * 2
     assert L.lr_joint_attention_workspace_bytes(65, 2) == 65 * 2 * 256 + 2 * 2 * 128 * 64 * 2
+    # LR_ATTN_CFG_PAIR_SK_W4: 512 stream-K partial slots of 4 waves x (O [2][4][4][64] float4 + m, l [2][2][64])
+    header = _lib.HEADER.read_text()
+    assert "#define LR_ATTN_SK_AREA_BYTES ((size_t)2 * 256 * 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64) * 4)" in header
+    assert ops.SK_AREA_BYTES == 2 * 256 * 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64) * 4
+    assert ops.workspace_bytes(65, 2, stream_k=True) == 65 * 2 * 256 + 2 * 2 * 128 * 64 * 2 + ops.SK_AREA_BYTES
     assert L.lr_joint_attention_workspace_bytes(0, 24) == 0
 
 
@@ -121,6 +126,7 @@ def test_stage_entry_points_reject():
     for cfg in (3, 4, 5, 99):                                   # configurations that read V rows, or none at all
         assert pr_call(config=cfg) == HIP_ERROR_INVALID_VALUE, cfg
     assert pr_call(wsb=wsb - 256) == HIP_ERROR_INVALID_VALUE
+    assert pr_call(config=8) == HIP_ERROR_INVALID_VALUE         # stream-K without its partials area
 
 
 def test_rms_rope_rejects():

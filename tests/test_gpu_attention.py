@@ -19,8 +19,8 @@ torch = pytest.importorskip("torch")
 from localrouter_amd import ops  # noqa: E402
 
 CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4, ops.CFG_PAIR_W4]
-# the fused / prepared calls also run the warp-specialised kernel (it reads packed V^T tiles only)
-FUSED_CONFIGS = CONFIGS + [ops.CFG_WS_W8]
+# the fused / prepared calls also run the warp-specialised kernel and the stream-K configuration (packed V^T only)
+FUSED_CONFIGS = CONFIGS + [ops.CFG_WS_W8, ops.CFG_PAIR_SK_W4]
 
 
 def _qkv(seed, W, nk, H, HK):
