@@ -1,0 +1,40 @@
+"""The capture reader of the replay gate (CPU): records, notes, refs and the comparison it reports."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from localrouter_amd import replay
+from tests import capture_util
+
+
+def test_read_ops_and_refs(tmp_path):
+    q = np.arange(3 * 2 * 128, dtype=np.uint16).reshape(1, 3, 2, 128)
+    w = np.linspace(-1, 1, 128, dtype=np.float32)
+    capture_util.write(tmp_path, [
+        {"note": "sigmas", "values": [1.0, 0.5]},
+        {"name": "blk0.attn", "kind": "attention", "attrs": {"impl": "stk", "causal": False}, "ins": {"q": q, "k": q,
+         "v": q}, "outs": {"y": q.reshape(1, 3, 256)}},
+        {"name": "blk0.norm", "kind": "rms_norm_f32", "ins": {"w": w}, "outs": {"y": w}},
+    ])
+    ops = replay.read_ops(tmp_path)
+    assert [o.kind for o in ops] == ["attention", "rms_norm_f32"] and [o.i for o in ops] == [1, 2]
+    assert np.array_equal(replay.load_ref(tmp_path, ops[0].ins["q"]), q)
+    assert replay.load_ref(tmp_path, ops[0].outs["y"]).shape == (1, 3, 256)
+    assert np.array_equal(replay.load_ref(tmp_path, ops[1].ins["w"]), w)
+    bad = dict(ops[0].ins["q"], shape=[1, 3, 2, 129])
+    with pytest.raises(ValueError):
+        replay.load_ref(tmp_path, bad)
+    with pytest.raises(ValueError):
+        replay.load_ref(tmp_path, dict(ops[0].ins["q"], dtype="complex64"))
+
+
+def test_compare_reports_equal_within_and_differ():
+    a = np.array([0x3F80, 0x4000, 0xBF80] * 4, dtype=np.uint16)      # 1, 2, -1, ...
+    assert replay.compare(a, a)[:2] == (True, True)
+    b = a.copy(); b[0] = 0x3F81                                       # 1 + 2^-7
+    eq, ok, mx, _ = replay.compare(b, a)
+    assert not eq and ok and abs(mx - 2 ** -7) < 1e-9                 # mean-abs 2^-7 / 12 is within the bar too
+    c = a.copy(); c[1] = 0x4040                                       # 3 instead of 2
+    assert replay.compare(c, a)[:2] == (False, False)
+    assert replay.compare(a[:2], a)[:2] == (False, False)
