@@ -10,7 +10,9 @@ from its captured inputs ("alone" mode), and compares with the captured outputs 
 mean-abs 2e-3 on bf16 outputs) -- other kernels than the twin's cannot be expected to round identically -- and also
 reports how many outputs are byte-equal. Replayed kinds (tools/twin/stk_twin/dit.py:225-282):
   attention  q [B, N, H, D], k / v [B, S, HK, D] -> y [B, N, H * D]; attrs causal, and p0 / nkeys for a segment;
-             scale 1 / sqrt(D). A masked SDPA record (attrs "masked" true) is skipped.
+             scale 1 / sqrt(D). A masked SDPA record (attrs "masked", input "mask" boolean or additive, broadcast
+             over [B, *, N, S]) is replayed when the mask is a key-padding mask (every query row the same: through
+             lr_attention_kmask_bf16) or exactly causal; other masks are skipped.
   rms_rope   qkv [B, N, 3, H, D], w [D], cos / sin [N, D / 2] f32, attrs part (0 q, 1 k) and eps -> y [B, N, H, D]:
              per-head RMSNorm then interleaved-pair rotation (the Qwen engine's _rms_rope_kernel).
 Every other kind is counted as skipped.
@@ -109,8 +111,6 @@ def replay_op(root: str | Path, op: Op):
         return (t.view(torch.bfloat16) if a.dtype == np.uint16 else t).cuda()
 
     if op.kind == "attention":
-        if _bool(op.attrs.get("masked", False)) or "mask" in op.ins:
-            return None
         q, k, v = dev("q"), dev("k"), dev("v")
         B, N, H, D = q.shape
         S, HK = k.shape[1], k.shape[2]
@@ -119,10 +119,34 @@ def replay_op(root: str | Path, op: Op):
         causal = _bool(op.attrs.get("causal", False))
         p0 = int(op.attrs.get("p0", 0))
         nkeys = int(op.attrs.get("nkeys", S))
+        keep = None
+        if "mask" in op.ins:
+            m = load_ref(root, op.ins["mask"])
+            m = m if m.dtype == np.bool_ else (m.astype(np.float32) == 0.0)   # additive: 0 keeps, -inf drops
+            try:
+                m = np.broadcast_to(m, (B, 1, N, S)) if m.ndim <= 4 else None
+            except ValueError:
+                return None
+            if m is None or (m != m[:, :1]).any():          # per head masks: not replayed
+                return None
+            m = m[:, 0]
+            if (m == m[:, :1, :]).all():                    # key padding
+                keep = m[:, 0, :]
+            elif N == S and (m == np.tril(np.ones((N, S), bool))[None]).all():
+                causal = True
+            else:
+                return None
+        elif _bool(op.attrs.get("masked", False)):
+            return None
         ys = []
         for b in range(B):
-            ys.append(ops.attention(q[b], k[b], v[b], nkeys=nkeys, causal=causal, p0=p0, heads=H, kv_heads=HK,
-                                    scale=1.0 / math.sqrt(D)))
+            if keep is not None:
+                km = torch.from_numpy(keep[b].astype(np.uint8)).cuda()
+                ys.append(ops.attention_kmask(q[b], k[b], v[b], km, n_valid=int(keep[b].sum()),
+                                              scale=1.0 / math.sqrt(D)))
+            else:
+                ys.append(ops.attention(q[b], k[b], v[b], nkeys=nkeys, causal=causal, p0=p0, heads=H, kv_heads=HK,
+                                        scale=1.0 / math.sqrt(D)))
         torch.cuda.synchronize()
         return torch.stack(ys).reshape(B, N, H * D).view(torch.int16).cpu().numpy().view(np.uint16)
     if op.kind == "rms_rope":

@@ -1,6 +1,7 @@
 """The replay gate on the GPU: a capture in the reference's recorder format (tools/twin/stk_twin/rec.py:1-9) with an
-unmasked attention, a causal segment (p0, nkeys) with GQA, a q-part rms_rope and a skipped kind, expected outputs
-from the CPU oracle; every replayed op must pass the bar, and a perturbed expected output must be reported."""
+unmasked attention, a causal segment (p0, nkeys) with GQA, a q-part rms_rope, SDPA records with a key-padding mask, a
+causal mask and an unsupported (diagonal) mask, and a skipped kind; expected outputs from the CPU oracle. Every
+replayed op must pass the bar, and a perturbed expected output must be reported."""
 from __future__ import annotations
 
 import numpy as np
@@ -31,6 +32,13 @@ def _capture(root, perturb=False):
     cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
     y2 = oracle.rms_rope(np.ascontiguousarray(qkv[0, :, 0]), w, table_kind=oracle.TABLE_COSSIN_F32, ta=cos, tb=sin,
                          pairing=oracle.PAIR_INTERLEAVED, rot=128, eps=1e-6)
+    keep = np.random.default_rng(62).random(150) < 0.7                 # key padding: 30 % of the keys dropped
+    kept = np.nonzero(keep)[0]
+    yk = oracle.f32_to_bf16(oracle.attention(bf16_f32(q[0]), bf16_f32(k[0][kept]), bf16_f32(v[0][kept]), scale=s))
+    yk = yk.reshape(1, 100, 512)
+    kq = oracle.synth_bf16(61, 6, (1, 150, 4, 128))
+    yc = oracle.f32_to_bf16(oracle.attention(bf16_f32(kq[0]), bf16_f32(k[0]), bf16_f32(v[0]), causal=True, scale=s))
+    yc = yc.reshape(1, 150, 512)
     b0 = oracle.f32_to_bf16(y0).reshape(1, 100, 512)
     if perturb:
         b0 = oracle.f32_to_bf16(bf16_f32(b0) + 0.25)
@@ -43,6 +51,12 @@ def _capture(root, perturb=False):
         {"name": "blk0.q_rope", "kind": "rms_rope", "attrs": {"part": 0, "eps": 1e-6},
          "ins": {"qkv": qkv, "w": w, "cos": cos, "sin": sin}, "outs": {"y": oracle.f32_to_bf16(y2)[None]}},
         {"name": "blk0.mlp", "kind": "swiglu", "ins": {"gu": qkv.reshape(40, -1)}, "outs": {"y": qkv.reshape(40, -1)}},
+        {"name": "te.attn", "kind": "attention", "attrs": {"impl": "sdpa", "masked": True},
+         "ins": {"q": q, "k": k, "v": v, "mask": keep[None, None, None, :]}, "outs": {"y": yk}},
+        {"name": "te.attn_causal", "kind": "attention", "attrs": {"impl": "sdpa", "masked": True},
+         "ins": {"q": kq, "k": k, "v": v, "mask": np.tril(np.ones((150, 150), bool))[None, None]}, "outs": {"y": yc}},
+        {"name": "te.attn_diag", "kind": "attention", "attrs": {"impl": "sdpa", "masked": True},
+         "ins": {"q": kq, "k": k, "v": v, "mask": np.eye(150, dtype=bool)[None, None]}, "outs": {"y": yc}},
     ])
 
 
@@ -50,7 +64,8 @@ def test_replay_capture(tmp_path):
     print("\n[replay] synthetic capture", flush=True)
     _capture(tmp_path)
     st = replay.replay(tmp_path)
-    assert (st.differ, st.skipped) == (0, 1) and st.equal + st.within == 3, st.notes
+    # replayed: two attentions, the rms_rope, the key-padding and the causal SDPA masks; skipped: swiglu, the diagonal
+    assert (st.differ, st.skipped) == (0, 2) and st.equal + st.within == 5, st.notes
 
 
 def test_replay_reports_a_difference(tmp_path):
