@@ -6,7 +6,8 @@ The capture format is the reference's (tools/twin/stk_twin/rec.py:1-9): a direct
   blobs/<sha> raw contiguous tensor bytes; a ref is {sha, dtype, shape} (rec.py:22-28)
 The reference's gate (src/engines/qwen_image/replay.zig:1-3) replays every op of a capture through the Zig forward
 and compares outputs byte for byte with its own CUDA kernels. This gate replays the ops on this library's path, each
-from its captured inputs ("alone" mode), and compares with the captured outputs to the attention bar (max-abs 2e-2,
+from its captured inputs ("alone" mode) or, with --chained, from the outputs of the ops replayed before it whose
+recorded outputs it consumed (matched by blob hash), and compares with the captured outputs to the attention bar (max-abs 2e-2,
 mean-abs 2e-3 on bf16 outputs) -- other kernels than the twin's cannot be expected to round identically -- and also
 reports how many outputs are byte-equal. Replayed kinds (tools/twin/stk_twin/dit.py:225-282):
   attention  q [B, N, H, D], k / v [B, S, HK, D] -> y [B, N, H * D]; attrs causal, and p0 / nkeys for a segment;
@@ -17,7 +18,7 @@ reports how many outputs are byte-equal. Replayed kinds (tools/twin/stk_twin/dit
              per-head RMSNorm then interleaved-pair rotation (the Qwen engine's _rms_rope_kernel).
 Every other kind is counted as skipped.
 
-    python -m localrouter_amd.replay CAPTURE_DIR [--limit N]
+    python -m localrouter_amd.replay CAPTURE_DIR [--limit N] [--chained]
 """
 from __future__ import annotations
 
@@ -99,14 +100,18 @@ def compare(got_bits: np.ndarray, want_bits: np.ndarray) -> tuple[bool, bool, fl
     return bool(np.array_equal(got_bits, want_bits)), mx <= BAR_MAX_ABS and mean <= BAR_MEAN_ABS, mx, mean
 
 
-def replay_op(root: str | Path, op: Op):
-    """Run one op through the library from its captured inputs; returns the output bits, or None if not replayed."""
+def replay_op(root: str | Path, op: Op, produced: dict | None = None):
+    """Run one op through the library from its captured inputs; returns the output bits, or None if not replayed.
+    produced: sha -> array; an input whose recorded blob is the recorded output of an op replayed earlier is taken
+    from that op's replayed output instead (chained mode)."""
     import torch
 
     from . import ops
 
     def dev(name):
-        a = load_ref(root, op.ins[name])
+        ref = op.ins[name]
+        a = produced[ref["sha"]] if produced and ref["sha"] in produced else load_ref(root, ref)
+        a = a.reshape(tuple(ref["shape"]))
         t = torch.from_numpy(np.array(a))   # a writable copy of the read-only blob view
         return (t.view(torch.bfloat16) if a.dtype == np.uint16 else t).cuda()
 
@@ -170,14 +175,19 @@ def replay_op(root: str | Path, op: Op):
     return None
 
 
-def replay(root: str | Path, limit: int | None = None, log=print) -> Stats:
+def replay(root: str | Path, limit: int | None = None, log=print, chained: bool = False) -> Stats:
+    """Alone: every op from its captured inputs. Chained: inputs that are outputs of ops replayed earlier come from
+    those replayed outputs, so differences accumulate along the chain as they would in an engine."""
     st = Stats()
+    produced = {} if chained else None
     for op in read_ops(root)[:limit]:
-        got = replay_op(root, op)
+        got = replay_op(root, op, produced)
         if got is None:
             st.skipped += 1
             continue
         want = load_ref(root, op.outs["y"])
+        if chained:
+            produced[op.outs["y"]["sha"]] = got
         eq, ok, mx, mean = compare(got, want.reshape(got.shape) if want.size == got.size else want)
         if eq:
             st.equal += 1
@@ -196,8 +206,9 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("capture")
     ap.add_argument("--limit", type=int, default=None)
+    ap.add_argument("--chained", action="store_true", help="inputs from earlier replayed outputs")
     a = ap.parse_args(argv)
-    st = replay(a.capture, a.limit)
+    st = replay(a.capture, a.limit, chained=a.chained)
     print(f"equal {st.equal}, within bar {st.within}, differ {st.differ}, skipped {st.skipped}")
     return 1 if st.differ else 0
 

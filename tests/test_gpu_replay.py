@@ -73,3 +73,28 @@ def test_replay_reports_a_difference(tmp_path):
     _capture(tmp_path, perturb=True)
     st = replay.replay(tmp_path)
     assert st.differ == 1 and "DIFFERS" in st.notes[0], st.notes
+
+
+def test_replay_chained(tmp_path):
+    """An rms_rope whose recorded output is the q of the next attention (the same blob): chained, the attention reads
+    the replayed rms_rope output; both stay within the bar."""
+    print("\n[replay] chained", flush=True)
+    qkv = oracle.synth_bf16(63, 1, (1, 120, 3, 2, 128))
+    w = np.ones(128, np.float32)
+    ang = np.random.default_rng(63).uniform(-3, 3, (120, 64))
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    qn = oracle.f32_to_bf16(oracle.rms_rope(np.ascontiguousarray(qkv[0, :, 0]), w, table_kind=oracle.TABLE_COSSIN_F32,
+                                            ta=cos, tb=sin, rot=128, eps=1e-6))
+    k = oracle.synth_bf16(63, 2, (1, 120, 2, 128))
+    v = oracle.synth_bf16(63, 3, (1, 120, 2, 128))
+    y = oracle.attention(bf16_f32(qn), bf16_f32(k[0]), bf16_f32(v[0]), scale=1.0 / np.sqrt(128.0))
+    capture_util.write(tmp_path, [
+        {"name": "q_rope", "kind": "rms_rope", "attrs": {"part": 0, "eps": 1e-6},
+         "ins": {"qkv": qkv, "w": w, "cos": cos, "sin": sin}, "outs": {"y": qn[None]}},
+        {"name": "attn", "kind": "attention", "attrs": {"impl": "stk", "causal": False},
+         "ins": {"q": qn[None], "k": k, "v": v}, "outs": {"y": oracle.f32_to_bf16(y).reshape(1, 120, 256)}},
+    ])
+    for chained in (False, True):
+        st = replay.replay(tmp_path, chained=chained)
+        assert st.differ == 0 and st.equal + st.within == 2, (chained, st.notes)
+
