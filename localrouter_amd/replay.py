@@ -100,6 +100,24 @@ def compare(got_bits: np.ndarray, want_bits: np.ndarray) -> tuple[bool, bool, fl
     return bool(np.array_equal(got_bits, want_bits)), mx <= BAR_MAX_ABS and mean <= BAR_MEAN_ABS, mx, mean
 
 
+def classify_mask(m: np.ndarray, B: int, N: int, S: int):
+    """An SDPA mask (boolean, True keeps; or additive, 0 keeps) broadcast over [B, 1, N, S]: ("keys", keep [B, S])
+    when every query row of a batch is the same (key padding), ("causal", None) when it is exactly lower-triangular
+    over N == S, else (None, None) (per-head or other masks)."""
+    m = m if m.dtype == np.bool_ else (m.astype(np.float32) == 0.0)
+    if m.ndim > 4:
+        return None, None
+    try:
+        m = np.broadcast_to(m, (B, 1, N, S))[:, 0]
+    except ValueError:
+        return None, None
+    if (m == m[:, :1, :]).all():
+        return "keys", np.ascontiguousarray(m[:, 0, :])
+    if N == S and (m == np.tril(np.ones((N, S), bool))[None]).all():
+        return "causal", None
+    return None, None
+
+
 def replay_op(root: str | Path, op: Op, produced: dict | None = None):
     """Run one op through the library from its captured inputs; returns the output bits, or None if not replayed.
     produced: sha -> array; an input whose recorded blob is the recorded output of an op replayed earlier is taken
@@ -126,21 +144,10 @@ def replay_op(root: str | Path, op: Op, produced: dict | None = None):
         nkeys = int(op.attrs.get("nkeys", S))
         keep = None
         if "mask" in op.ins:
-            m = load_ref(root, op.ins["mask"])
-            m = m if m.dtype == np.bool_ else (m.astype(np.float32) == 0.0)   # additive: 0 keeps, -inf drops
-            try:
-                m = np.broadcast_to(m, (B, 1, N, S)) if m.ndim <= 4 else None
-            except ValueError:
+            how, keep = classify_mask(load_ref(root, op.ins["mask"]), B, N, S)
+            if how is None:
                 return None
-            if m is None or (m != m[:, :1]).any():          # per head masks: not replayed
-                return None
-            m = m[:, 0]
-            if (m == m[:, :1, :]).all():                    # key padding
-                keep = m[:, 0, :]
-            elif N == S and (m == np.tril(np.ones((N, S), bool))[None]).all():
-                causal = True
-            else:
-                return None
+            causal = causal or how == "causal"
         elif _bool(op.attrs.get("masked", False)):
             return None
         ys = []

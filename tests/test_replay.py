@@ -38,3 +38,16 @@ def test_compare_reports_equal_within_and_differ():
     c = a.copy(); c[1] = 0x4040                                       # 3 instead of 2
     assert replay.compare(c, a)[:2] == (False, False)
     assert replay.compare(a[:2], a)[:2] == (False, False)
+
+
+def test_classify_mask():
+    keep = np.array([True, False, True, True])
+    how, k = replay.classify_mask(keep[None, None, None, :], 1, 3, 4)
+    assert how == "keys" and np.array_equal(k, keep[None])
+    add = np.where(keep, 0.0, -np.inf).astype(np.float32)[None, None, None, :]      # additive form
+    assert replay.classify_mask(add, 2, 3, 4)[0] == "keys"
+    assert replay.classify_mask(np.tril(np.ones((4, 4), bool))[None, None], 1, 4, 4)[0] == "causal"
+    assert replay.classify_mask(np.eye(4, dtype=bool)[None, None], 1, 4, 4)[0] is None
+    per_head = np.ones((1, 2, 3, 4), bool); per_head[0, 1, :, 0] = False           # heads differ
+    assert replay.classify_mask(per_head, 1, 3, 4)[0] is None
+
