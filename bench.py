@@ -1,20 +1,22 @@
 """Benchmark of the DiT joint-attention hot path on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video|h3-int8|mmdit]
-                    [--tile-config C] [--no-cpu-baseline]
+                    [--no-cpu-baseline]
 
-A step is one fused joint-attention call over one synthetic batch: keys RMSNorm + RoPE into the workspace
-and V packed into transposed 64-key tiles (lr_joint_kv_prepare), followed by the attention kernel with the queries
-normalised and rotated in registers (lr_joint_attention_prepared) -- together exactly lr_joint_attention_fused. Inputs are resident in HBM before timing.
+A step is one fused joint-attention call over one synthetic batch, made as the fused call's own three launches so that
+each is timed: keys RMSNorm + RoPE and values into the workspace's tile images (lr_joint_kv_prepare), queries
+RMSNorm + RoPE into the output rows (lr_joint_q_prepare), then the persistent streaming attention kernel over
+them (lr_joint_attention_images) -- together exactly what lr_joint_attention_fused launches. Inputs are resident in
+HBM before timing.
 The default workload is BASELINE's Qwen-Image-style step: B=1, 24 heads x 128, 512 text + 4096 image tokens (64x64
 grid, 2D RoPE on image tokens, text un-rotated), non-causal, QK-RMSNorm eps 1e-6 with weights 1.0, scale f32(1/sqrt(128)).
 
 Prints ONE JSON line on stdout (everything else goes to stderr). FLOPs per call = 4 * Sq * Sk * 128 * H (QK^T + PV;
-softmax, RMSNorm and RoPE not counted). `roofline` is the attention stage alone, timed with HIP events on the stream
-it is launched on, against MI355X's published dense bf16 peak of 2.5 PFLOP/s. For the default tile configuration that
-stage is the 64-query-per-wave kernel plus its check-only second launch (~4 us: it recomputes the blocks whose
-softmax overflowed the fixed reference, and exits at once otherwise), so `achieved` slightly understates the kernel. `cpu_baseline` times the CPU oracle's
-fp32 flash-style path (OpenMP) on a bounded sample of query rows of the same workload, as a reported baseline only.
+softmax, RMSNorm and RoPE not counted). `roofline` is the attention kernel (attn_stream_kernel) alone, timed with HIP
+events on the stream it is launched on, against MI355X's published dense bf16 peak of 2.5 PFLOP/s; its `traffic` and
+the shader clock come from the committed rocprofv3 PMC summary of the same command (profiles/). `cpu_baseline` times
+the CPU oracle's fp32 flash-style path (OpenMP, every core the process may use) on a bounded sample of query rows of
+the same workload, as a reported baseline only.
 
 --workload h3-int8 measures MiniMax H3's INT8 attention instead (5,967 tokens x 56 heads, the reference's headline
 shape for it): a step is Kitchen.attention on one packed qkv buffer, i.e. the prep (anchor, rotation, int8 Q / K / V,
@@ -45,15 +47,8 @@ sys.path.insert(0, str(ROOT))
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_INT8_TOPS = 5000.0
 METRIC = "attention TFLOP/s + % bf16 MFMA peak; ms/call at 4096+512 tokens, 24x128"
-# attention kernel each tile configuration launches for the benchmark's cos/sin table (QK = 1: queries normalised and
-# rotated in registers with that table kind; VT: values read as packed V^T tiles) -- the configurations
-# lr_joint_attention_prepared accepts
-KERNELS = {
-    0: "attn_pair_kernel<1, true>",
-    1: "attn_fwd_pipe_kernel<8, 1, 64, 4, 1, true>",
-    2: "attn_fwd_pipe_kernel<4, 1, 64, 2, 1, true>",
-    6: "attn_pair_kernel<1, true>",
-}
+# the attention kernel of the fused call, as rocprofv3 names it
+KERNEL = "attn_stream_kernel"
 WORKLOADS = {
     # name: (text tokens, grid description, heads)
     "plumbing": dict(n_text=256, kind="grid2d", gh=32, gw=32, heads=24),
@@ -77,17 +72,37 @@ def tables(w):
     return rope.video3d_table(w["n_text"], w["t"], w["gh"], w["gw"])
 
 
-# the source file (and profile name prefix) of each tile configuration's attention kernel
-KERNEL_FILES = {0: "attn_pair", 1: "attn_fwd", 2: "attn_fwd", 6: "attn_pair"}
-
-
-def traffic_from_profile(name: str, kernel: str = "attn_fwd"):
-    """HBM bytes per launch of the attention kernel, from the committed rocprofv3 PMC summary (None if absent)."""
+def from_profile(name: str, kernel: str, field: str = "traffic_bytes_per_launch"):
+    """A figure of the committed rocprofv3 PMC summary profiles/<kernel>_<name>_pmc.md (None if absent)."""
     p = ROOT / "profiles" / f"{kernel}_{name}_pmc.md"
     if not p.exists():
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    m = re.search(field + r":\s*([0-9.eE+]+)", p.read_text())
     return float(m.group(1)) if m else None
+
+
+def traffic_from_profile(name: str, kernel: str):
+    return from_profile(name, kernel)
+
+
+def host_cpus():
+    """(threads the CPU baseline uses, CPUs this process may run on, CPU model). The thread count is the process's
+    CPU share: OMP_NUM_THREADS when set (the GPU boxes set it to their share), else every CPU of the affinity mask."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(avail, int(env)) if env.isdigit() and int(env) > 0 else avail
+    model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return threads, avail, model
 
 
 def cpu_baseline(q_bits, k_bits, v_bits, cos, sin, S, H, flops_per_row, budget_s=10.0):
@@ -95,14 +110,17 @@ def cpu_baseline(q_bits, k_bits, v_bits, cos, sin, S, H, flops_per_row, budget_s
     import numpy as np
 
     import oracle
-    threads = min(16, os.cpu_count() or 1)
+    threads = host_cpus()[0]
     oracle.set_threads(threads)
     rng = np.random.default_rng(0)
 
     def run(rows):
         t0 = time.perf_counter()
+        # the reference's chain: q and k normalised, rotated and stored as bf16, then the attention
         qh = oracle.rms_rope(q_bits[rows], None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos[rows], tb=sin[rows])
         kh = oracle.rms_rope(k_bits, None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos, tb=sin)
+        qh = oracle.bf16_to_f32(oracle.f32_to_bf16(qh))
+        kh = oracle.bf16_to_f32(oracle.f32_to_bf16(kh))
         vf = oracle.bf16_to_f32(v_bits)
         # all S keys for each sampled query row: the sampled rows are renumbered 0..n-1 (non-causal, so equivalent)
         out = oracle.attention(qh, kh, vf, precise=False)
@@ -130,8 +148,6 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS) + ["h3-int8", "mmdit"])
-    ap.add_argument("--tile-config", type=int, default=0, choices=sorted(KERNELS),
-                    help="LR_ATTN_CFG_* (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -191,41 +207,51 @@ def main():
                   cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, H, 0, ws.data_ptr(), ws_bytes,
                   sh)
 
+    def queries():
+        _lib.call("lr_joint_q_prepare", q.data_ptr(), rs, out.data_ptr(), rs, wq.data_ptr(), ops.TABLE_COSSIN_F32,
+                  cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, H, sh)
+
     def attn():
-        _lib.call("lr_joint_attention_prepared", q.data_ptr(), ws.data_ptr(), ws_bytes, out.data_ptr(), wq.data_ptr(),
-                  ops.TABLE_COSSIN_F32, cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, S, H, H,
-                  0, 0, scale, rs, rs, args.tile_config, sh)
+        _lib.call("lr_joint_attention_images", out.data_ptr(), rs, ws.data_ptr(), ws_bytes, out.data_ptr(), rs, S, S,
+                  H, H, 0, 0, scale, sh)
 
     for _ in range(args.warmup):
         keys()
+        queries()
         attn()
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
 
     K = args.steps
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * K + 1)]
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
     for i in range(K):
-        ev[2 * i].record(stream)
+        ev[3 * i].record(stream)
         keys()
-        ev[2 * i + 1].record(stream)
+        ev[3 * i + 1].record(stream)
+        queries()
+        ev[3 * i + 2].record(stream)
         attn()
-    ev[2 * K].record(stream)
+    ev[3 * K].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
-    t_keys = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(K)]
-    t_attn = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(K)]
-    total_ms = ev[0].elapsed_time(ev[2 * K])
+    t_keys = [ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(K)]
+    t_q = [ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(K)]
+    t_attn = [ev[3 * i + 2].elapsed_time(ev[3 * i + 3]) for i in range(K)]
+    total_ms = ev[0].elapsed_time(ev[3 * K])
     ms_step = total_ms / K
     flops = 4.0 * S * S * 128 * H
     attn_ms = float(np.mean(t_attn))
     keys_ms = float(np.mean(t_keys))
+    q_ms = float(np.mean(t_q))
     value = flops / (ms_step * 1e-3) / 1e12
     achieved = flops / (attn_ms * 1e-3) / 1e12
-    log(f"[bench] step {ms_step:.4f} ms (kv prepare {keys_ms:.4f} ms, attention {attn_ms:.4f} ms, median attention "
-        f"{float(np.median(t_attn)):.4f} ms); {value:.1f} TFLOP/s step, {achieved:.1f} TFLOP/s attention kernel "
-        f"({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); wall {wall:.3f} s")
+    clock = from_profile(args.workload, KERNEL, "clock_ghz")
+    log(f"[bench] step {ms_step:.4f} ms (kv prepare {keys_ms:.4f} ms, q prepare {q_ms:.4f} ms, attention "
+        f"{attn_ms:.4f} ms, median attention {float(np.median(t_attn)):.4f} ms); {value:.1f} TFLOP/s step, "
+        f"{achieved:.1f} TFLOP/s attention kernel ({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); "
+        f"wall {wall:.3f} s")
 
     result = {
         "metric": METRIC,
@@ -242,12 +268,14 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{args.workload}-joint-attention", "batch": 1, "tokens": S, "text_tokens": w["n_text"],
                    "heads": H, "head_dim": 128, "causal": False, "qk_rmsnorm": True, "rope": w["kind"],
-                   "parallelism": "none (1 GPU)", "tile_config": args.tile_config},
+                   "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_from_profile(args.workload, KERNEL_FILES[args.tile_config]),
-                     "kernel": KERNELS[args.tile_config], "kernel_ms": round(attn_ms, 5)},
-        "kernels_ms": {"kv_prepare": round(keys_ms, 5), "attention": round(attn_ms, 5)},
+                     "traffic": traffic_from_profile(args.workload, KERNEL),
+                     "kernel": KERNEL, "kernel_ms": round(attn_ms, 5),
+                     "clock_ghz": clock,
+                     "peak_at_clock": None if clock is None else round(PEAK_BF16_TFLOPS * clock / 2.4, 1)},
+        "kernels_ms": {"kv_prepare": round(keys_ms, 5), "q_prepare": round(q_ms, 5), "attention": round(attn_ms, 5)},
         "flops_per_call": flops,
     }
 
@@ -268,13 +296,16 @@ def main():
         got = out.cpu().view(torch.int16).numpy().view(np.uint16)[cb["rows"]]
         gotf = (got.astype(np.uint32) << 16).view(np.float32)
         d = np.abs(gotf.astype(np.float64) - cb["out"])
+        _, avail, model = host_cpus()
+        rel = float(np.linalg.norm(gotf.astype(np.float64) - cb["out"]) / np.linalg.norm(cb["out"].astype(np.float64)))
         result["cpu_baseline"] = {"value": round(cb["value"], 4), "unit": "TFLOP/s", "cores": cb["threads"],
-                                  "kind": "port",
+                                  "kind": "port", "host_cpus": avail, "cpu_model": model,
                                   "sample": f"{len(cb['rows'])} of {S} query rows x {H} heads over all {S} keys "
                                             f"(norm+rope+attention, fp32): median of {cb['runs']} runs, "
                                             f"{cb['seconds']:.2f} s each"}
         result["check"] = {"rows": int(len(cb["rows"])), "max_abs": float(d.max()), "mean_abs": float(d.mean()),
-                           "bar": {"max_abs": 2e-2, "mean_abs": 2e-3}}
+                           "rel_l2": rel, "bar": {"max_abs": 2e-2, "mean_abs": 2e-3, "rel_l2": 3e-3},
+                           "pass": bool(d.max() <= 2e-2 and d.mean() <= 2e-3 and rel <= 3e-3)}
         log(f"[bench] cpu {cb['value']:.4f} TFLOP/s on {cb['threads']} threads; GPU vs CPU on sampled rows: "
             f"max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
     print(json.dumps(result), flush=True)
@@ -286,7 +317,7 @@ def cpu_baseline_int8(qkv_bits, S, H, budget_s=10.0):
     import numpy as np
 
     import oracle
-    threads = min(16, os.cpu_count() or 1)
+    threads = host_cpus()[0]
     oracle.set_threads(threads)
     rng = np.random.default_rng(0)
     heads = [0, H // 2, H - 1]

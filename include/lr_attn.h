@@ -20,7 +20,9 @@
  *   lr_rms_rope_qk_bf16      <- Kitchen.rmsRope, src/engines/minimax_h3/launch.zig:421-441, and
  *                               kitchen_rms_rope_split_half_, kernels/cuda/minimax/kitchen_launch.cu:284-314
  *   lr_joint_attention_fused <- the chain rope_q -> rope_k -> V copy -> attention of Dit.block,
- *                               src/engines/qwen_image/dit.zig:252-293 (and minimax_h3/dit.zig:663-672), as one call
+ *                               src/engines/qwen_image/dit.zig:252-293 (and minimax_h3/dit.zig:663-672), as one call;
+ *                               its launches one by one: lr_joint_kv_prepare (rope_k + V copy), lr_joint_q_prepare
+ *                               (rope_q), lr_joint_attention_images (the attention launch, Ops.attention's place)
  *   lr_int8_attention*       <- MiniMax H3's INT8 attention: Kitchen.Plan / attentionPrep / attentionKernel /
  *                               attention, src/engines/minimax_h3/launch.zig:317-419, and kitchen_int8_attention
  *                               {,_rows,_workspace_bytes}, kernels/cuda/minimax/kitchen_launch.cu:193-280
@@ -38,7 +40,7 @@ extern "C" {
 /* hipStream_t without pulling in the HIP headers: an opaque pointer (NULL = the default stream). */
 typedef struct ihipStream_t* lr_stream_t;
 
-#define LR_ATTN_ABI_VERSION 5
+#define LR_ATTN_ABI_VERSION 6
 #define LR_HEAD_DIM 128
 
 /* RoPE table kinds: how rotation coefficients are stored per token row, per pair p < rot_dim/2. */
@@ -57,34 +59,17 @@ typedef struct ihipStream_t* lr_stream_t;
 #define LR_WEIGHT_F32 1
 #define LR_WEIGHT_BF16 2
 
-/* Attention tile configurations for the _ex entry points (0 = the library's choice: LR_ATTN_CFG_PAIR_W4 for the fused
- * and prepared calls, LR_ATTN_CFG_PIPE_W8 for attention over value rows). */
+/* Attention tile configurations for the _ex entry points (0 = the library's choice: LR_ATTN_CFG_STREAM_W8 for the
+ * fused and prepared calls, LR_ATTN_CFG_PIPE_W8 for attention over value rows). */
 #define LR_ATTN_CFG_AUTO 0
-#define LR_ATTN_CFG_PIPE_W8 1      /* 256 queries per workgroup (8 waves x 32): direct-to-LDS K/V ring, next tile's
-                                      QK^T overlapped with the current tile's softmax */
+#define LR_ATTN_CFG_PIPE_W8 1      /* attention over value rows: 256 queries per workgroup (8 waves x 32), direct-to-LDS
+                                      K/V ring, next tile's QK^T overlapped with the current tile's softmax */
 #define LR_ATTN_CFG_PIPE_W4 2      /* the same kernel with 128 queries per workgroup (4 waves x 32) */
-#define LR_ATTN_CFG_REGSTAGE_W8 3  /* 256 queries per workgroup, K/V staged through registers (2-stage ring) */
-#define LR_ATTN_CFG_PINGPONG_W8 4  /* 256 queries per workgroup, two groups of 4 waves alternating an MFMA cluster and
-                                      a softmax cluster, 4-stage direct-to-LDS K/V ring */
-#define LR_ATTN_CFG_WIDE_W4 5      /* 256 queries per workgroup (4 waves x 64), 32-key tiles: every K/V operand
-                                      fragment feeds two MFMAs, one wave per SIMD */
-#define LR_ATTN_CFG_PAIR_W4 6      /* 256 queries per workgroup (4 waves x 64), 64-key tiles in a 4-stage direct-to-LDS
-                                      ring, explicit MFMA schedule: every K/V^T operand fragment feeds two MFMAs,
-                                      one wave per SIMD; softmax against a fixed reference (the first key tile's
-                                      maximum), blocks whose sums overflowed it recomputed by a second launch of the
-                                      PIPE_W8 kernel */
-#define LR_ATTN_CFG_WS_W8 7        /* 256 queries per workgroup, 8 waves in 4 pairs per SIMD: one wave of a pair
-                                      computes scores and softmax, the other the PV products, P handed over in LDS;
-                                      fused / prepared calls, non-causal (causal calls run PAIR_W4); same fixed
-                                      reference and second launch as PAIR_W4 */
-#define LR_ATTN_CFG_PAIR_SK_W4 8   /* PAIR_W4 under a stream-K schedule (fused / prepared calls): one workgroup per CU
-                                      over the blocks' key tiles laid end to end, a block cut between two workgroups
-                                      merged from two partials by a second kernel. Runs when the call is non-causal,
-                                      has at least as many 256-query blocks as CUs and whole blocks would leave more
-                                      than 3% of the last round idle (else as PAIR_W4). Needs LR_ATTN_SK_AREA_BYTES
-                                      more workspace. Measured slower than PAIR_W4 at the BASELINE shapes (the
-                                      workgroups of a head no longer stream the same K/V tiles together). */
-#define LR_ATTN_SK_AREA_BYTES ((size_t)2 * 256 * 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64) * 4)
+#define LR_ATTN_CFG_STREAM_W8 9    /* fused / prepared calls: one persistent workgroup per CU (8 waves x 32 queries)
+                                      streaming keys and values prepared as tile images (the LDS image of each
+                                      64-key tile, 16 KB) through 4-stage direct-to-LDS rings; softmax against a
+                                      fixed reference (the block's first key tile's maximum), query rows whose sums
+                                      overflowed it recomputed exactly at the end of the kernel */
 
 int lr_attn_abi_version(void);
 
@@ -162,15 +147,16 @@ int lr_rms_rope_qk_bf16(void* q, void* k, int64_t seq, int heads, int64_t q_row_
                         const void* q_norm, const void* k_norm, const void* freqs, int64_t freqs_row_stride,
                         int rot_dim, float eps, lr_stream_t stream);
 
-/* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys, bf16 [HK][Sk][128], then (at a
- * 256-byte boundary) V packed as transposed 64-key tiles, bf16 [HK][ceil(Sk/64)][128][64]. LR_ATTN_CFG_PAIR_SK_W4
- * needs LR_ATTN_SK_AREA_BYTES more, right after them (the stream-K partials). */
+/* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys, then the values, each as
+ * [HK][ceil(Sk/64)] tile images of 16 KB (one 64-key tile of one kv head laid out as the attention kernel's LDS holds
+ * it; keys past Sk zero): 2 * HK * ceil(Sk/64) * 16384. */
 size_t lr_joint_attention_workspace_bytes(int Sk, int HK);
 
 /*
- * The fused joint attention: QK-RMSNorm + RoPE + attention (keys normalised once and values packed into the
- * workspace; queries normalised and rotated in registers inside the attention kernel).
- *   q_raw [Sq][H][128], k_raw, v [Sk][HK][128], out [Sq][H][128] bf16 rows with the given row strides.
+ * The fused joint attention: QK-RMSNorm + RoPE + attention (keys and values prepared once into the workspace,
+ * queries normalised and rotated into out's rows, which the attention kernel reads before overwriting them).
+ *   q_raw [Sq][H][128], k_raw, v [Sk][HK][128], out [Sq][H][128] bf16 rows with the given row strides
+ *   (out_row_stride <= 2^23 elements).
  *   q_norm_w, k_norm_w: fp32 [128], 16-byte aligned, or NULL (ones). eps >= 0.
  *   Query i uses q-table row i; key j >= n_pre uses k-table row j - n_pre; keys j < n_pre are already normalised and
  *   rotated (a cached text prefix) and are used as they are.
@@ -178,6 +164,7 @@ size_t lr_joint_attention_workspace_bytes(int Sk, int HK);
  *   Attention as lr_attention_bf16 with nkeys = Sk.
  *   workspace: >= lr_joint_attention_workspace_bytes(Sk, HK) bytes, 256-byte aligned, owned by the caller; its
  *   contents are scratch (clobbered by the call, not read before being written).
+ *   out must not overlap the workspace, k_raw or v (q_raw may be out itself: in place).
  */
 int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,
                              const float* k_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
@@ -187,16 +174,13 @@ int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v
                              int n_pre, void* workspace, size_t workspace_bytes, lr_stream_t stream);
 
 /*
- * The two stages of lr_joint_attention_fused as separate calls (same kernels, same results as the default
- * configuration):
+ * The two stages of lr_joint_attention_fused as separate calls (same kernels, same results):
  *   lr_joint_kv_prepare         RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre), rows j < n_pre
- *                               copied, into the workspace's keys; v [Sk][HK][128] packed into its V^T tiles;
- *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated in registers) over that workspace.
- *                               config: LR_ATTN_CFG_AUTO, _PIPE_W8, _PIPE_W4 or _PAIR_W4 (the configurations that
- *                               read V^T tiles; the others are reached through lr_joint_attention_fused_ex).
- * Useful when keys and values are reused (a cached prefix) or to time the stages separately. The attention call
- * reads the keys and V^T tiles and uses the stream-K area (when present) as scratch, so calls sharing one workspace
- * run one at a time (one stream).
+ *                               copied, and the values, into the workspace's tile images;
+ *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated into out's rows first) over
+ *                               that workspace. config: LR_ATTN_CFG_AUTO or _STREAM_W8.
+ * Useful when keys and values are reused (a cached prefix) or to time the stages separately. The attention call only
+ * reads the workspace, so several calls may share one prepared workspace.
  */
 int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,
                         const float* k_norm_w, int table_kind, const void* k_table_a, const void* k_table_b,
@@ -207,6 +191,26 @@ int lr_joint_attention_prepared(const void* q_raw, void* workspace, size_t works
                                 int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sq, int Sk, int H,
                                 int HK, int p0, int causal, float scale, int64_t q_row_stride, int64_t out_row_stride,
                                 int config, lr_stream_t stream);
+
+/*
+ * The fused op's own three launches as separate calls, in the order lr_joint_attention_fused makes them (the
+ * reference's chain rope_k + V copy -> rope_q -> attention, dit.zig:252-293):
+ *   lr_joint_kv_prepare        (above) keys and values into the workspace's tile images;
+ *   lr_joint_q_prepare         q_raw [Sq][H][128] normalised and rotated (as lr_rms_rope_bf16 with an fp32 weight,
+ *                              round_norm 0), rounded once to bf16, into q_prep rows; q_prep may be q_raw itself (in
+ *                              place) or out; otherwise it must not overlap q_raw;
+ *   lr_joint_attention_images  the attention of those prepared queries over the workspace: one persistent workgroup
+ *                              per CU (LR_ATTN_CFG_STREAM_W8). q_prep may be out itself (same row stride: each block
+ *                              reads its queries before it writes its output over them); otherwise they must not
+ *                              overlap. out_row_stride <= 2^23 elements; out must not overlap the workspace.
+ */
+int lr_joint_q_prepare(const void* q_raw, int64_t q_row_stride, void* q_prep, int64_t q_prep_row_stride,
+                       const float* q_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
+                       int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sq, int H,
+                       lr_stream_t stream);
+int lr_joint_attention_images(const void* q_prep, int64_t q_prep_row_stride, const void* workspace,
+                              size_t workspace_bytes, void* out, int64_t out_row_stride, int Sq, int Sk, int H, int HK,
+                              int p0, int causal, float scale, lr_stream_t stream);
 
 /* lr_joint_attention_fused with an explicit tile configuration (LR_ATTN_CFG_*). */
 int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,

@@ -7,6 +7,7 @@ only (MI355X / MI350X), with packed-fp32 instruction selection switched off.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -17,8 +18,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "liblr_attn.so"
-SOURCES = ["attn_fwd.hip", "attn_pair.hip", "attn_ws.hip", "rms_rope.hip", "int8_attn.hip", "keys.hip", "lr_abi.hip", "mmdit.hip",
-           "rope_host.cpp"]
+SOURCES = ["attn_fwd.hip", "attn_stream.hip", "kv_image.hip", "rms_rope.hip", "int8_attn.hip", "keys.hip", "lr_abi.hip",
+           "mmdit.hip", "rope_host.cpp"]
 # libraries the shared object links: hipBLASLt for the MMDiT block's projections and MLP
 LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
 ARCH = "gfx950"
@@ -35,10 +36,9 @@ HIPCC_FLAGS = [
 ]
 
 
-# per-source extra flags: the 64-query-per-wave kernel's fully unrolled 64-slot schedule is larger than clang's
-# default limit for `#pragma unroll`, and a partly unrolled schedule would index its register arrays at run time
-EXTRA_FLAGS = {"attn_pair.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"],
-               "attn_ws.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]}
+# per-source extra flags: the streaming kernel's fully unrolled key-tile step is larger than clang's default limit for
+# `#pragma unroll`, and a partly unrolled step would index its register arrays at run time
+EXTRA_FLAGS = {"attn_stream.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]}
 
 # host-only C++ (the RoPE table builders of include/lr_rope.h): the system compiler, no contraction of f64 products
 # and sums into FMAs, so that tables are the same bits as the numpy builders
@@ -66,7 +66,7 @@ def build(verbose: bool = False) -> Path:
     cc = hipcc()
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
-    objs = []
+    objs, cmds = [], []
     for src in SOURCES:
         obj = objdir / (Path(src).stem + ".o")
         if src.endswith(".cpp"):
@@ -75,8 +75,13 @@ def build(verbose: bool = False) -> Path:
             cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), file=sys.stderr)
-        _run(cmd)
+        cmds.append(cmd)
         objs.append(str(obj))
+    # the sources compile independently: a few at a time (each hipcc process is single-threaded)
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", "0") or 0) or (os.cpu_count() or 1)))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        for f in [pool.submit(_run, c) for c in cmds]:
+            f.result()
     tmp = LIB.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, *LIBS, "-o", str(tmp)])
     os.replace(tmp, LIB)

@@ -1,0 +1,584 @@
+// Persistent streaming joint attention for gfx950: bf16 in, fp32 MFMA accumulation and softmax, bf16 out, over keys
+// and values prepared as tile images (tile_image.h, written by kv_image.hip).
+//
+// Semantics: the reference's kernels/cuda/qwen_image/attention.cu:253-444 (pattn2_kernel) as launched by
+// src/engines/qwen_image/ops_launch.zig:163-172: O_i = softmax_j(scale <q_i, k_j>) v_j over keys j < nkeys (and
+// j <= p0 + i when causal, attention.cu:304), query head h reading kv head h / (H / HK) (attention.cu:264-266), P
+// rounded to bf16 for the P V product (attention.cu:418-424), output rounded to bf16 (attention.cu:432-443). The
+// queries arrive normalised and rotated (bf16 rows, the reference's rope_q output, dit.zig:252-257), the keys and
+// values as tile images.
+//
+// Design (two waves per SIMD, 8 waves = 256 queries per block, 32 queries per wave; each 1 KB operand fragment read
+// from LDS feeds one v_mfma_f32_32x32x16_bf16, 128 bytes per clock per CU at the MFMA rate, half of gfx950's LDS read
+// bandwidth; the two waves of a SIMD overlap one's softmax VALU work and LDS reads with the other's MFMAs):
+//
+//  * Persistent: one workgroup per CU walks the blocks logical, logical + nwg, ... and its key/value tiles form one
+//    continuous stream through two 4-stage LDS rings (64 KB each). The loads of the next block's first tiles are in
+//    flight while the current block finishes, and the query prologue of the next block follows the previous block's
+//    epilogue without a kernel boundary.
+//  * Tile images: a tile is stored in HBM as the LDS image of its 16 fragments, so each ring refill is four
+//    contiguous 1 KB direct global->LDS loads per wave (one M0 write, immediate offsets), and each fragment read is one
+//    conflict-free ds_read_b128 at an immediate offset from a per-step base: no per-fragment address arithmetic.
+//  * Step (one 64-key tile, 32 MFMA slots per wave): two half-steps of 16 slots; half-step j runs the 8 score MFMAs of
+//    the next 32-key half-tile (S(j+1) = K Q^T, accumulator starting at -m) and the 8 P V MFMAs of the previous one
+//    (O += V^T P(j-1)), while the VALU turns S(j) into P(j): one word (two keys of one query) per two slots, exp2 in
+//    the even slot, bf16 pack and the fp32 row sum in the odd slot. Scores and P are double-buffered by half-tile.
+//    Fragments are read three ahead into a register ring; one barrier per step, after a vmcnt wait that leaves the
+//    step's own refills in flight.
+//  * Softmax against a fixed reference: m = ceil of the exact maximum of the block's first 32 scores in the exp2
+//    domain (c = scale * log2 e times the raw q.k product; the queries arrive normalised and rotated as the
+//    reference's rope writes them, bf16), held as m / c and subtracted by the score MFMAs themselves, so
+//    P = exp2(c S') with one multiply per score beside the exp. Softmax is shift-invariant: exact while P, the row
+//    sums and O stay finite, i.e. unless a later key scores ~128 above m. The epilogue checks every row; a wave with a
+//    non-finite row marks the block and, after the streaming loop, recomputes its 32 queries with the exact row
+//    maximum (a two-pass form that reads fragments straight from the images in HBM and needs no LDS), so the output
+//    never depends on the fixed reference.
+#include "lr_common.h"
+#include "lr_kernels.h"
+#include "tile_image.h"
+
+namespace lr {
+
+namespace {
+
+#include "attn_common.inc"
+
+constexpr int SW = 8;             // waves per workgroup, two per SIMD
+constexpr int SBM = 32 * SW;      // queries per block
+constexpr int RING = 4;           // stages of each LDS ring
+constexpr int RA = 3;             // fragments read ahead
+constexpr int FR = 4;             // fragment ring entries
+constexpr int WQ = IMG_TILE_BYTES / SW;   // bytes of a tile each wave loads
+constexpr int REDO_WORDS = 32;            // per wave: a bit per block of the workgroup, for exact recomputation
+constexpr int MAX_WG_BLOCKS = 32 * REDO_WORDS;   // blocks one workgroup may walk (launch_stream splits larger calls)
+
+// S = K Q^T with the accumulator starting at 0 / at c, and S += K Q^T: scores in VGPRs (the VALU reads them), Q in
+// AGPRs. Inline asm, so the compiler cannot move the 64 Q registers into VGPRs; every VALU read of a result below is
+// at least 16 MFMA slots after the MFMA, or behind a fence.
+__device__ __forceinline__ void qk_zero(f32x16& d, const bf16x8& k, const bf16x8& q) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(k), "a"(q));
+}
+__device__ __forceinline__ void qk_init(f32x16& d, const bf16x8& k, const bf16x8& q, const f32x16& c) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "a"(q), "v"(c));
+}
+__device__ __forceinline__ void qk_acc(f32x16& d, const bf16x8& k, const bf16x8& q) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "a"(q));
+}
+// O += V^T P: the builtin, so that the compiler knows it is an MFMA (O stays in AGPRs, hazards are its job)
+__device__ __forceinline__ void pv(f32x16& o, const bf16x8& v, const u32x4& p) {
+    o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, __builtin_bit_cast(bf16x8, p), o, 0, 0, 0);
+}
+#define LR_NOP48 "s_nop 15\n\ts_nop 15\n\ts_nop 15"
+__device__ __forceinline__ void fence_s(f32x16& s) { asm volatile(LR_NOP48 : "+v"(s)); }
+__device__ __forceinline__ void fence_q8(bf16x8 (&q)[8]) {
+    asm volatile(LR_NOP48 : "+a"(q[0]), "+a"(q[1]), "+a"(q[2]), "+a"(q[3]), "+a"(q[4]), "+a"(q[5]), "+a"(q[6]),
+                 "+a"(q[7]));
+}
+
+// Two contiguous 1 KB direct loads, global -> LDS: lane l's 16 bytes of load i come from gaddr + 1024 i + 16 l and
+// land at LDS byte lds + 1024 i + 16 l (the instruction offset applies to both addresses).
+__device__ __forceinline__ void dma2k(uint64_t gaddr, uint32_t voff, uint32_t lds) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:0\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:1024" ::"v"(voff),
+        "s"(gaddr), "s"(lds)
+        : "memory");
+}
+
+template <bool B>
+struct BoolTag {
+    static constexpr bool value = B;
+};
+template <int N>
+struct IntTag {
+    static constexpr int value = N;
+};
+
+typedef __attribute__((address_space(3))) const bf16x8 lds_frag;
+__device__ __forceinline__ bf16x8 frag_at(uint32_t addr) { return *(lds_frag*)(uintptr_t)addr; }
+
+struct BlockInfo {
+    int head, hk, row0, tiles;
+};
+
+// Recompute wave `wave`'s 32 queries of a block with the exact row maximum (the rare case of a non-finite row under the
+// fixed reference): pass 1 takes the maximum of every score, pass 2 accumulates P = exp2(S - max) <= 1, the row sums and
+// O, and the rows are written. The prepared queries are read from a.q (the block's rows, not yet overwritten), the
+// fragments straight from the tile images in HBM (a 1 KB fragment is one 16-byte load per lane): nothing here touches
+// LDS or waits for the other waves. Called after the streaming loop, so that its registers do not add to the loop's.
+__device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, int row0, int tiles, int wave) {
+    const int lane = threadIdx.x & 63, n = lane & 31, hf = lane >> 5;
+    const int wrow0 = row0 + wave * 32, qrow = wrow0 + n;
+    const int T = (a.nkeys + IMG_TILE_KEYS - 1) / IMG_TILE_KEYS;
+    const uint64_t head_off = (uint64_t)hk * T * IMG_TILE_BYTES + (uint64_t)lane * 16;
+    const uint8_t* kh = reinterpret_cast<const uint8_t*>(a.k) + head_off;
+    const uint8_t* vh = reinterpret_cast<const uint8_t*>(a.v) + head_off;
+    bf16x8 qf[8];
+    const uint16_t* src = a.q + (int64_t)min(qrow, a.W - 1) * a.q_rs + head * D + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+    int lim0 = a.nkeys;
+    if (a.causal) lim0 = min(lim0, a.p0 + qrow + 1);
+    auto scores = [&](int j, const f32x16& c) {
+        const uint8_t* kt = kh + (uint64_t)(j >> 1) * IMG_TILE_BYTES + (j & 1) * 8 * IMG_FRAG_BYTES;
+        f32x16 sr = c;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+            sr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(kt + ks * IMG_FRAG_BYTES),
+                                                        qf[ks], sr, 0, 0, 0);
+        const int lim = lim0 - (32 * j + 8 * hf);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (!(16 * (r >> 3) + (r & 7) < lim)) sr[r] = -INFINITY;
+        return sr;
+    };
+    float mx = -INFINITY;
+    for (int j = 0; j < 2 * tiles; ++j) {
+        const f32x16 sr = scores(j, f32x16{});
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sr[r]);
+    }
+    const float m = wave_pair_max(mx);
+    const f32x16 nm = f32x16{} - (m > -INFINITY ? m : 0.0f);
+    const float c = a.c;
+    f32x16 o[4] = {};
+    float ls = 0.0f;
+    for (int j = 0; j < 2 * tiles; ++j) {
+        const f32x16 sr = scores(j, nm);
+        const uint8_t* vt = vh + (uint64_t)(j >> 1) * IMG_TILE_BYTES + (j & 1) * 8 * IMG_FRAG_BYTES;
+        u32x4 pr[2];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const float e0 = __builtin_amdgcn_exp2f(sr[8 * (w >> 2) + 2 * (w & 3)] * c);
+            const float e1 = __builtin_amdgcn_exp2f(sr[8 * (w >> 2) + 2 * (w & 3) + 1] * c);
+            pr[w >> 2][w & 3] = pack_bf16x2(e0, e1);
+            ls += e0 + e1;
+        }
+#pragma unroll
+        for (int x = 0; x < 8; ++x)
+            o[x & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                *reinterpret_cast<const bf16x8*>(vt + x * IMG_FRAG_BYTES), __builtin_bit_cast(bf16x8, pr[x >> 2]),
+                o[x & 3], 0, 0, 0);
+    }
+    const float inv = 1.0f / wave_pair_sum(ls);
+    if (qrow < a.W) {
+        uint16_t* dst = a.out + (int64_t)qrow * a.o_rs + head * D + 4 * hf;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                u32x2 w;
+                w[0] = pack_bf16x2(o[db][4 * gg] * inv, o[db][4 * gg + 1] * inv);
+                w[1] = pack_bf16x2(o[db][4 * gg + 2] * inv, o[db][4 * gg + 3] * inv);
+                *reinterpret_cast<u32x2*>(dst + 32 * db + 8 * gg) = w;
+            }
+    }
+}
+
+__global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_stream_kernel(AttnArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t Kr[RING * IMG_TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t Vr[RING * IMG_TILE_BYTES];
+    // per wave: bit i set = the wave's rows of the workgroup's i-th block must be recomputed exactly
+    __shared__ uint32_t redo_bits[SW][REDO_WORDS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31, hf = lane >> 5;
+
+    // XCD-aware order: hardware workgroup b runs on XCD b % 8; each XCD takes a contiguous range of logical ids, so
+    // the blocks it runs at any time are consecutive query blocks of one or two heads (their K/V stay in its L2)
+    const int nwg = gridDim.x, b = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
+    const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int nqb = (a.W + SBM - 1) / SBM;
+    const int nblk = nqb * a.H;
+    if (logical >= nblk) return;
+    const int T = (a.nkeys + IMG_TILE_KEYS - 1) / IMG_TILE_KEYS;
+    const uint64_t head_bytes = (uint64_t)T * IMG_TILE_BYTES;
+
+    auto info_of = [&](int blk) __attribute__((always_inline)) {
+        BlockInfo bi;
+        bi.head = blk / nqb;
+        bi.hk = bi.head / a.G;
+        bi.row0 = (blk - bi.head * nqb) * SBM;
+        bi.tiles = T;
+        if (a.causal) bi.tiles = min(T, (a.p0 + min(bi.row0 + SBM, a.W) - 1) / IMG_TILE_KEYS + 1);
+        return bi;
+    };
+
+    // ---- the tile stream: cursors of the next key / value tile to load (this wave's WQ bytes of it)
+    struct Cursor {
+        int blk, t, tiles;
+        uint64_t addr;
+    };
+    const uint64_t kimg = (uint64_t)(uintptr_t)a.k, vimg = (uint64_t)(uintptr_t)a.v;
+    auto cur_start = [&](uint64_t img) __attribute__((always_inline)) {
+        const BlockInfo bi = info_of(logical);
+        return Cursor{logical, 0, bi.tiles, img + (uint64_t)bi.hk * head_bytes + (uint64_t)wave * WQ};
+    };
+    // past the last tile of the last block the cursor stays put: its loads refill a free ring slot with a tile that is
+    // never read
+    auto cur_next = [&](Cursor& c, uint64_t img) __attribute__((always_inline)) {
+        if (c.t + 1 < c.tiles) {
+            ++c.t;
+            c.addr += IMG_TILE_BYTES;
+        } else if (c.blk + nwg < nblk) {
+            c.blk += nwg;
+            const BlockInfo bi = info_of(c.blk);
+            c.t = 0;
+            c.tiles = bi.tiles;
+            c.addr = img + (uint64_t)bi.hk * head_bytes + (uint64_t)wave * WQ;
+        }
+    };
+    const uint32_t voff = (uint32_t)lane * 16u;
+    const uint32_t kr0 = lds_addr(Kr), vr0 = lds_addr(Vr);
+    // ring slot x: byte offset x * 16 KB; this wave's loads fill its WQ bytes of the slot
+    auto load_k = [&](Cursor& c, int pos) __attribute__((always_inline)) {
+        dma2k(c.addr, voff, kr0 + (uint32_t)((pos & (RING - 1)) * IMG_TILE_BYTES) + (uint32_t)wave * WQ);
+        cur_next(c, kimg);
+    };
+    auto load_v = [&](Cursor& c, int pos) __attribute__((always_inline)) {
+        dma2k(c.addr, voff, vr0 + (uint32_t)((pos & (RING - 1)) * IMG_TILE_BYTES) + (uint32_t)wave * WQ);
+        cur_next(c, vimg);
+    };
+
+    // ---- registers
+    bf16x8 qa[8];      // AGPR-resident queries (B operand of S^T = K Q^T), per k-step
+    f32x16 o[4];       // O^T accumulators, per 32-dim block
+    f32x16 s[2];       // scores, per half-tile parity
+    u32x4 p[2][2];     // P, [half-tile parity][16-key step of the half-tile]
+    f32x16 negm;       // -m in every slot: the initial accumulator of the score MFMAs
+    float ls = 0.0f;   // this lane's partial row sum (its 8 keys of every 16-key step)
+    bf16x8 fr[FR];     // fragment ring
+    const uint32_t lane16 = (uint32_t)lane * 16u;
+
+    // mask the scores sb of half-tile j (keys 32 j ..) against nkeys and, causal, the query's position
+    auto mask_half = [&](f32x16& sb, int j, int wrow0) __attribute__((always_inline)) {
+        int lim = a.nkeys;
+        if (a.causal) lim = min(lim, a.p0 + wrow0 + n + 1);
+        lim -= 32 * j + 8 * hf;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (!(16 * (r >> 3) + (r & 7) < lim)) sb[r] = -INFINITY;
+    };
+    // first half-tile that needs a mask for this wave
+    auto mask_from = [&](int wrow0) __attribute__((always_inline)) {
+        int jm = a.nkeys >> 5;
+        if (a.causal) jm = min(jm, (a.p0 + wrow0 + 1) >> 5);
+        return jm;
+    };
+
+    // one P word: E = the two exp2 of word w of the scores into e0/e1; C = bf16 pack into the P buffer, and the fp32
+    // pair into the row sum (as the reference, attention.cu:403-407). Word w of a half-tile: 16-key step kk2 = w >> 2,
+    // j = w & 3: score registers 8 kk2 + 2 j, +1 (keys 16 kk2 + 8 hf + 2 j, +1 of the half-tile).
+    float e0 = 0.0f, e1 = 0.0f;
+    const float c = a.c;   // scale * log2 e: scores are raw q.k products, the exponent is their exp2-domain value
+    auto stage_e = [&](const f32x16& sb, int w) __attribute__((always_inline)) {
+        e0 = __builtin_amdgcn_exp2f(sb[8 * (w >> 2) + 2 * (w & 3)] * c);
+        e1 = __builtin_amdgcn_exp2f(sb[8 * (w >> 2) + 2 * (w & 3) + 1] * c);
+        asm volatile("" ::"v"(e0), "v"(e1));   // computed in this slot, not sunk towards the next use
+    };
+    auto stage_c = [&](u32x4 (&pb)[2], int w) __attribute__((always_inline)) {
+        const uint32_t x = pack_bf16x2(e0, e1);
+        pb[w >> 2][w & 3] = x;
+        const float es = e0 + e1;
+        ls += es;
+        asm volatile("" ::"v"(x), "v"(ls));
+    };
+
+    // ---- one half-step of 16 MFMA slots. QK: S so of the next half-tile from fragments 0-7 (k-steps); PV: O += the
+    // V fragments 8-15 (16-key step (f - 8) >> 2, 32-dim block (f - 8) & 3) times P ppv; VALU: P po from S si.
+    // rd(f) reads the fragment of position f (>= 16: the next half-step's position f - 16) into the ring.
+    auto half_step = [&](f32x16& so, const u32x4 (&ppv)[2], const f32x16& si, u32x4 (&po)[2], auto qk_tag, auto pv_tag,
+                         auto valu_tag, auto&& rd) __attribute__((always_inline)) {
+        constexpr bool HAS_QK = decltype(qk_tag)::value;
+        constexpr bool HAS_PV = decltype(pv_tag)::value;
+        constexpr bool HAS_VALU = decltype(valu_tag)::value;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < 16; ++f) {
+            if (f < 8) {
+                if constexpr (HAS_QK) {
+                    if (f == 0) qk_init(so, fr[0], qa[0], negm);
+                    else qk_acc(so, fr[f % FR], qa[f]);
+                }
+            } else {
+                if constexpr (HAS_PV) pv(o[(f - 8) & 3], fr[f % FR], ppv[(f - 8) >> 2]);
+            }
+            if constexpr (HAS_VALU) {
+                if ((f & 1) == 0) stage_e(si, f >> 1);
+                else stage_c(po, f >> 1);
+            }
+            rd(f + RA);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    const BoolTag<true> yes{};
+    const BoolTag<false> no{};
+
+    // ---- per-block state
+    int blk = logical;
+    BlockInfo cur = info_of(blk);
+    int g = 0;   // stream position of the current step (tile)
+
+    // ---- the queries of block bi (prepared rows: normalised, rotated and scaled by scale * log2 e, a.q with row
+    // stride a.q_rs): this wave's 32 rows as the 8 B-operand fragments, loaded straight into the AGPRs. The loads are
+    // asynchronous; LR_WAIT_Q(N) waits for them with N younger memory operations still in flight.
+    auto load_q = [&](const BlockInfo& bi) __attribute__((always_inline)) {
+        const int qrow = min(bi.row0 + wave * 32 + n, a.W - 1);
+        const uint16_t* src = a.q + (int64_t)qrow * a.q_rs + bi.head * D + 8 * hf;
+        asm volatile(
+            "global_load_dwordx4 %0, %8, off\n\t"
+            "global_load_dwordx4 %1, %8, off offset:32\n\t"
+            "global_load_dwordx4 %2, %8, off offset:64\n\t"
+            "global_load_dwordx4 %3, %8, off offset:96\n\t"
+            "global_load_dwordx4 %4, %8, off offset:128\n\t"
+            "global_load_dwordx4 %5, %8, off offset:160\n\t"
+            "global_load_dwordx4 %6, %8, off offset:192\n\t"
+            "global_load_dwordx4 %7, %8, off offset:224"
+            : "=a"(qa[0]), "=a"(qa[1]), "=a"(qa[2]), "=a"(qa[3]), "=a"(qa[4]), "=a"(qa[5]), "=a"(qa[6]), "=a"(qa[7])
+            : "v"(src)
+            : "memory");
+    };
+#define LR_WAIT_Q(N)                                                                                            \
+    asm volatile("s_waitcnt vmcnt(" #N ")"                                                                      \
+                 : "+a"(qa[0]), "+a"(qa[1]), "+a"(qa[2]), "+a"(qa[3]), "+a"(qa[4]), "+a"(qa[5]), "+a"(qa[6]),   \
+                   "+a"(qa[7])::"memory")
+
+    // ---- stream start: the first block's queries, K(0..2), V(0..1); the queries, K(0) and K(1) resident before
+    // step 0
+    Cursor kc = cur_start(kimg), vc = cur_start(vimg);
+    if (lane < REDO_WORDS) redo_bits[wave][lane] = 0u;
+    load_q(cur);
+    load_k(kc, 0);
+    load_k(kc, 1);
+    load_k(kc, 2);
+    load_v(vc, 0);
+    load_v(vc, 1);
+    LR_WAIT_Q(6);
+    block_barrier();
+
+
+    // S(0) of a block: the first half-tile's scores from key fragments 0-7 of slot kslot, accumulator at 0; then the
+    // fixed reference m = ceil(max), S(0) -= m, negm, O = 0, row sum 0
+    auto first_scores = [&](const BlockInfo& bi, uint32_t kslot) __attribute__((always_inline)) {
+        const int wrow0 = bi.row0 + wave * 32;
+        uint32_t kb0 = kslot + lane16;
+        asm volatile("" : "+v"(kb0));   // opaque: offsets stay immediates, nothing is precomputed across the loop
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const bf16x8 kf = frag_at(kb0 + (uint32_t)(ks * IMG_FRAG_BYTES));
+            if (ks == 0) qk_zero(s[0], kf, qa[0]);
+            else qk_acc(s[0], kf, qa[ks]);
+        }
+        fence_s(s[0]);
+        if (mask_from(wrow0) <= 0) mask_half(s[0], 0, wrow0);
+        float mx = s[0][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
+        mx = wave_pair_max(mx);
+        // m in the exp2 domain, held as m / c in score units: the MFMAs then leave S - m / c, and P = exp2(c (S - m / c))
+        // (an error of m / c's rounding shifts every exponent of the row alike, which the normalisation cancels)
+        const float m = mx > -INFINITY ? ceilf(mx * c) : 0.0f;
+        const float mc = m / c;
+        negm = f32x16{} - mc;
+        s[0] -= mc;
+        ls = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+        asm volatile(LR_NOP48 : "+v"(negm));
+    };
+
+    // the output rows of block bi from this wave's 16 packed words (32-dim block db = i >> 2, dims 8 (i & 3) + 4 hf ..
+    // +3): 16 buffer stores, always issued (rows at or past W fall outside the buffer range and are dropped), so that
+    // the number of memory operations after the next block's query loads is fixed
+    auto store_rows = [&](const BlockInfo& bi, const u32x2 (&w)[16]) __attribute__((always_inline)) {
+        const int nrows = min(a.W - bi.row0, SBM);
+        const uint32_t nrec = (uint32_t)((int64_t)nrows * a.o_rs * 2 - (int64_t)bi.head * D * 2);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            a.out + (int64_t)bi.row0 * a.o_rs + bi.head * D, 0, (int)nrec, 0x00020000);
+        const uint32_t vo = (uint32_t)((wave * 32 + n) * a.o_rs * 2 + 8 * hf);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            __builtin_amdgcn_raw_buffer_store_b64(w[i], rs, (int)(vo + 2 * (32 * (i >> 2) + 8 * (i & 3))), 0, 0);
+    };
+    // O / l of this wave's rows as packed bf16 words; returns true when a row is not finite (l >= 1/2 for every row,
+    // the first half-tile's maximum has P >= 1/2, so only overflow makes one)
+    auto pack_rows = [&](u32x2 (&w)[16]) __attribute__((always_inline)) {
+        const float l = wave_pair_sum(ls);
+        const float inv = 1.0f / l;
+        float nan0 = 0.0f * l, nan1 = 0.0f, nan2 = 0.0f, nan3 = 0.0f;   // NaN iff some value is not finite
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                const float y0 = o[db][4 * gg] * inv, y1 = o[db][4 * gg + 1] * inv;
+                const float y2 = o[db][4 * gg + 2] * inv, y3 = o[db][4 * gg + 3] * inv;
+                nan0 = fmaf(y0, 0.0f, nan0);
+                nan1 = fmaf(y1, 0.0f, nan1);
+                nan2 = fmaf(y2, 0.0f, nan2);
+                nan3 = fmaf(y3, 0.0f, nan3);
+                w[4 * db + gg][0] = pack_bf16x2(y0, y1);
+                w[4 * db + gg][1] = pack_bf16x2(y2, y3);
+            }
+        return (nan0 + nan1 + nan2 + nan3) != 0.0f;
+    };
+
+    // epilogue of block bi (logical id bi_blk): O / l to bf16 rows. A wave with a non-finite row stores nothing and
+    // marks the block; after the streaming loop it recomputes those rows exactly (its rows still hold the prepared
+    // queries when they are the output rows).
+    auto epilogue = [&](const BlockInfo& bi, int bi_blk) __attribute__((always_inline)) {
+        const int wrow0 = bi.row0 + wave * 32;
+        u32x2 w[16];
+        const bool bad = pack_rows(w) && wrow0 + n < a.W;
+        if (__builtin_amdgcn_ballot_w64(bad)) {
+            if (lane == 0) {
+                const int i = (bi_blk - logical) / nwg;
+                redo_bits[wave][i >> 5] |= 1u << (i & 31);
+            }
+        } else {
+            store_rows(bi, w);
+        }
+    };
+
+    // The end of a block (in the boundary step, V(g - 1) its last value tile): P of its last half-tile (S buffer 1)
+    // into P buffer 1 beside the P V products of the half-tile before (P buffer 0, value fragments 0-7), then the
+    // last P V products (P buffer 1, fragments 8-15), then the epilogue.
+    auto finish_block = [&](const BlockInfo& bi, int bi_blk, uint32_t vslot) __attribute__((always_inline)) {
+        const int wrow0 = bi.row0 + wave * 32;
+        if (2 * bi.tiles - 1 >= mask_from(wrow0)) mask_half(s[1], 2 * bi.tiles - 1, wrow0);
+        uint32_t vb0 = vslot + lane16;
+        asm volatile("" : "+v"(vb0));
+        bf16x8 vf[4];
+#pragma unroll
+        for (int x = 0; x < 3; ++x) vf[x] = frag_at(vb0 + (uint32_t)(x * IMG_FRAG_BYTES));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+            if (x + 3 < 16) vf[(x + 3) & 3] = frag_at(vb0 + (uint32_t)((x + 3) * IMG_FRAG_BYTES));
+            pv(o[x & 3], vf[x & 3], (x < 8 ? p[0] : p[1])[(x >> 2) & 1]);
+            if (x < 8) {
+                stage_e(s[1], x);
+                stage_c(p[1], x);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        epilogue(bi, bi_blk);
+    };
+
+    // a steady-state step over key tile g (both halves) and value tile g - 1. Fragment positions of the B half: 0-7
+    // keys mb 0, 8-15 values mb 0, 16+ the A half's keys (mb 1); of the A half: 0-7 keys mb 1, 8-15 values mb 1, 16+
+    // the next step's keys (mb 0).
+    auto step = [&](const BlockInfo& bi, int t) __attribute__((always_inline)) {
+        const int wrow0 = bi.row0 + wave * 32;
+        const int jm = mask_from(wrow0);
+        // per-step fragment bases (opaque to the compiler, so that every fragment offset below stays an immediate)
+        uint32_t kb = kr0 + (uint32_t)((g & (RING - 1)) * IMG_TILE_BYTES) + lane16;
+        uint32_t vb = vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES) + lane16;
+        uint32_t kn = kr0 + (uint32_t)(((g + 1) & (RING - 1)) * IMG_TILE_BYTES) + lane16;
+        asm volatile("" : "+v"(kb), "+v"(vb), "+v"(kn));
+        auto rd_b = [&](int f) __attribute__((always_inline)) {
+            const uint32_t ad = f < 8 ? kb + f * IMG_FRAG_BYTES
+                                      : f < 16 ? vb + (f - 8) * IMG_FRAG_BYTES : kb + (f - 8) * IMG_FRAG_BYTES;
+            fr[f % FR] = frag_at(ad);
+        };
+        auto rd_a = [&](int f) __attribute__((always_inline)) {
+            const uint32_t ad = f < 8 ? kb + (8 + f) * IMG_FRAG_BYTES
+                                      : f < 16 ? vb + f * IMG_FRAG_BYTES : kn + (f - 16) * IMG_FRAG_BYTES;
+            fr[f % FR] = frag_at(ad);
+        };
+        // B half: j = 2t - 1
+        if (2 * t - 1 >= jm) mask_half(s[1], 2 * t - 1, wrow0);
+        load_k(kc, g + 3);
+        half_step(s[0], p[0], s[1], p[1], yes, yes, yes, rd_b);
+        // A half: j = 2t
+        if (2 * t >= jm) mask_half(s[0], 2 * t, wrow0);
+        load_v(vc, g + 2);
+        half_step(s[1], p[1], s[0], p[0], yes, yes, yes, rd_a);
+        LR_WAIT_VMCNT(6);   // K(g + 2) and V(g) have landed; only this step's refills and V(g + 1) may be in flight
+        block_barrier();
+    };
+
+    // ---- the blocks of this workgroup
+    BlockInfo prev = cur;
+    bool has_prev = false;
+    for (;;) {
+        // boundary step g: the end of the previous block (value tile g - 1), the start of this one (key tile g)
+        const uint32_t kslot = kr0 + (uint32_t)((g & (RING - 1)) * IMG_TILE_BYTES);
+        if (has_prev) {
+            load_q(cur);   // prev's queries are dead: its last score MFMA ran in the step before
+            finish_block(prev, blk - nwg, vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES));
+            LR_WAIT_Q(16);   // the 16 output stores of prev may still be in flight
+        }
+        first_scores(cur, kslot);
+        load_k(kc, g + 3);
+        load_v(vc, g + 2);
+        // the A half of step 0: S(1) from key fragments 8-15 into S buffer 1, P(0) from S buffer 0 into P buffer 0
+        {
+            uint32_t kb = kslot + lane16;
+            uint32_t kn = kr0 + (uint32_t)(((g + 1) & (RING - 1)) * IMG_TILE_BYTES) + lane16;
+            asm volatile("" : "+v"(kb), "+v"(kn));
+            auto rd0 = [&](int f) __attribute__((always_inline)) {
+                if (f < 8) fr[f % FR] = frag_at(kb + (8 + f) * IMG_FRAG_BYTES);
+                else if (f >= 16) fr[f % FR] = frag_at(kn + (f - 16) * IMG_FRAG_BYTES);
+            };
+#pragma unroll
+            for (int f = 0; f < RA; ++f) rd0(f);
+            half_step(s[1], p[1], s[0], p[0], yes, no, yes, rd0);
+        }
+        LR_WAIT_VMCNT(6);
+        block_barrier();
+        ++g;
+        for (int t = 1; t < cur.tiles; ++t) {
+            step(cur, t);
+            ++g;
+        }
+        prev = cur;
+        has_prev = true;
+        blk += nwg;
+        if (blk >= nblk) break;
+        cur = info_of(blk);
+    }
+    finish_block(prev, blk - nwg, vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES));
+    LR_WAIT_VMCNT(0);   // no direct load is still writing LDS when the workgroup ends
+
+    // ---- the rare exact recomputation of the marked blocks
+    const int nall = (nblk - 1 - logical) / nwg + 1;
+    for (int wd = 0; wd < (nall + 31) / 32; ++wd) {
+        uint32_t bits = __builtin_amdgcn_readfirstlane(redo_bits[wave][wd]);
+        while (bits) {
+            const int i = 32 * wd + __builtin_ctz(bits);
+            bits &= bits - 1;
+            const BlockInfo bi = info_of(logical + i * nwg);
+            redo_exact(a, bi.head, bi.hk, bi.row0, bi.tiles, wave);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream) {
+    if (a.W < 1 || a.H < 1 || nwg < 1) return hipErrorInvalidValue;
+    // at most MAX_WG_BLOCKS blocks per workgroup (its recomputation bits): larger calls run as several launches over
+    // consecutive query-row ranges (queries, outputs and, causal, the diagonal offset p0 shifted)
+    const int64_t rows_per = (int64_t)SBM * std::max<int64_t>(1, (int64_t)MAX_WG_BLOCKS * nwg / a.H);
+    for (int64_t r0 = 0; r0 < a.W; r0 += rows_per) {
+        AttnArgs b = a;
+        b.W = (int)std::min<int64_t>(rows_per, a.W - r0);
+        b.q = a.q + r0 * a.q_rs;
+        b.out = a.out + r0 * a.o_rs;
+        b.p0 = a.p0 + (int)r0;
+        const int64_t blocks = (int64_t)((b.W + SBM - 1) / SBM) * b.H;
+        if (blocks > (int64_t)MAX_WG_BLOCKS * nwg) return hipErrorInvalidValue;
+        const unsigned grid = (unsigned)std::min<int64_t>(blocks, nwg);
+        hipLaunchKernelGGL(attn_stream_kernel, dim3(grid), dim3(SW * 64), 0, stream, b);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace lr

@@ -1,0 +1,203 @@
+// Keys and values of the joint attention into the tile-image layout (tile_image.h): RMSNorm + RoPE of every key row
+// j >= n_pre (table row j - n_pre; rows j < n_pre are an already normalised and rotated prefix and are copied), and V
+// transposed into V^T fragments. The math per key row is the rms_rope kernel's (rms_rope.hip): the reference's
+// kernels/cuda/minimax/kitchen/rms_rope.cu:37-230 / the Qwen-Image form of src/engines/qwen_image/triton_k.zig:44-53
+// (fp32 weight, cos/sin fp32 tables), as wired by src/engines/qwen_image/dit.zig:252-263 (k via rms_rope into the
+// key buffer after the prefix, v copied).
+//
+// One workgroup per (kv head, 64-key tile): it loads the tile's 64 key rows and 64 value rows (256 contiguous bytes
+// each), normalises and rotates the keys in registers, writes both images into LDS, then stores the 32 KB with fully
+// coalesced 16-byte stores. HBM-bound: 32 KB in and 32 KB out per tile.
+#include "lr_common.h"
+#include "lr_kernels.h"
+#include "tile_image.h"
+
+namespace lr {
+
+namespace {
+
+template <int KIND>
+__device__ __forceinline__ Rot2 img_rot(const void* ta, const void* tb, int64_t row_off, int p) {
+    Rot2 r;
+    if constexpr (KIND == TABLE_COSSIN_F32) {
+        const float c = static_cast<const float*>(ta)[row_off + p];
+        const float s = static_cast<const float*>(tb)[row_off + p];
+        r.f00 = c; r.f01 = -s; r.f10 = s; r.f11 = c;
+    } else if constexpr (KIND == TABLE_MAT2_BF16) {
+        const u32x2 m = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(ta) + row_off + 4 * p);
+        r.f00 = lo_bf16(m[0]); r.f01 = hi_bf16(m[0]); r.f10 = lo_bf16(m[1]); r.f11 = hi_bf16(m[1]);
+    } else if constexpr (KIND == TABLE_MAT2_F32) {
+        const f32x4 m = *reinterpret_cast<const f32x4*>(static_cast<const float*>(ta) + row_off + 4 * p);
+        r.f00 = m[0]; r.f01 = m[1]; r.f10 = m[2]; r.f11 = m[3];
+    } else {
+        r.f00 = 1.0f; r.f01 = 0.0f; r.f10 = 0.0f; r.f11 = 1.0f;
+    }
+    return r;
+}
+
+constexpr int KROWS = 4;   // key rows per thread (rows g, g + 16, g + 32, g + 48 of the tile)
+
+template <int KIND, int PAIRING>
+__global__ __launch_bounds__(256) void kv_image_kernel(KvImageArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t img[2 * IMG_TILE_BYTES];   // keys, then values
+    const int tid = threadIdx.x, c = tid & 15, g = tid >> 4;
+    const int64_t tile_id = blockIdx.x;                // kv head * tiles + tile
+    const int hk = (int)(tile_id / a.tiles), t = (int)(tile_id - (int64_t)hk * a.tiles);
+    const int key0 = t * IMG_TILE_KEYS;
+
+    // ---- every load first: 4 key rows (16 bytes each), the weight, the table entries, one 8x8 block of V
+    u32x4 xin[KROWS];
+#pragma unroll
+    for (int i = 0; i < KROWS; ++i) {
+        const int key = min(key0 + g + 16 * i, a.Sk - 1);
+        xin[i] = *reinterpret_cast<const u32x4*>(a.k + (int64_t)key * a.k_rs + (int64_t)hk * D + 8 * c);
+    }
+    u32x4 vin[8];
+    const int vkg = tid >> 4, vdg = tid & 15;           // threads 0-127: keys 8 vkg .. +7, dims 8 vdg .. +7
+    if (tid < 128) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int key = min(key0 + 8 * vkg + i, a.Sk - 1);
+            vin[i] = *reinterpret_cast<const u32x4*>(a.v + (int64_t)key * a.v_rs + (int64_t)hk * D + 8 * vdg);
+        }
+    }
+    float wv[8];
+    if (a.w) {
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(a.w + 8 * c);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(a.w + 8 * c + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { wv[j] = w0[j]; wv[4 + j] = w1[j]; }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wv[j] = 1.0f;
+    }
+    const int P = a.rot >> 1;
+    const int hc = a.rot >> 4;                           // split-half: 16-byte chunks per half
+    Rot2 rt[KROWS][8];   // interleaved: pairs 4c..4c+3 in [0..3]; split-half: pairs of this lane's 8 dims
+    if constexpr (KIND != TABLE_NONE) {
+#pragma unroll
+        for (int i = 0; i < KROWS; ++i) {
+            const int key = key0 + g + 16 * i;
+            const int64_t toff = (int64_t)max(min(key, a.Sk - 1) - a.n_pre, 0) * a.tab_stride;
+            if constexpr (PAIRING == PAIR_INTERLEAVED) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rt[i][j] = img_rot<KIND>(a.ta, a.tb, toff, min(4 * c + j, P - 1));
+            } else {
+                const int pc = c < hc ? c : c - hc;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) rt[i][j] = img_rot<KIND>(a.ta, a.tb, toff, min(8 * pc + j, P - 1));
+            }
+        }
+    }
+
+    // ---- keys: norm, rotation, into the LDS image
+#pragma unroll
+    for (int i = 0; i < KROWS; ++i) {
+        const int r = g + 16 * i, key = key0 + r;
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[2 * j] = lo_bf16(xin[i][j]);
+            x[2 * j + 1] = hi_bf16(xin[i][j]);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(x[j], x[j], ss);
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 16);
+        const float rr = rsqrtf(ss * (1.0f / D) + a.eps);
+        const bool copy = key < a.n_pre;
+        float y[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = x[j] * rr * wv[j];
+        if constexpr (KIND != TABLE_NONE) {
+            if constexpr (PAIRING == PAIR_INTERLEAVED) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool on = 8 * c + 2 * j < a.rot;
+                    const float x0 = y[2 * j], x1 = y[2 * j + 1];
+                    const float y0 = fmaf(rt[i][j].f00, x0, rt[i][j].f01 * x1);
+                    const float y1 = fmaf(rt[i][j].f10, x0, rt[i][j].f11 * x1);
+                    y[2 * j] = on ? y0 : x0;
+                    y[2 * j + 1] = on ? y1 : x1;
+                }
+            } else {
+                const int lane = tid & 63, base = lane & ~15;
+                const bool first = c < hc, second = c >= hc && c < 2 * hc;
+                const int partner = base + (first ? c + hc : (second ? c - hc : c));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float o = __shfl(y[j], partner, 64);
+                    const float a0 = first ? y[j] : o, b0 = first ? o : y[j];   // (x_p, x_{p + rot/2})
+                    const float ya = fmaf(rt[i][j].f00, a0, rt[i][j].f01 * b0);
+                    const float yb = fmaf(rt[i][j].f10, a0, rt[i][j].f11 * b0);
+                    y[j] = first ? ya : (second ? yb : y[j]);
+                }
+            }
+        }
+        u32x4 o;
+        if (key >= a.Sk) {
+            o = u32x4{0, 0, 0, 0};
+        } else if (copy) {
+            o = xin[i];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
+        }
+        *reinterpret_cast<u32x4*>(img + img_k_offset(r, c)) = o;
+    }
+
+    // ---- values: an 8-key x 8-dim block transposed in registers, 8 dims of 16 bytes (8 keys each)
+    if (tid < 128) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (key0 + 8 * vkg + i >= a.Sk) vin[i] = u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            u32x4 y;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t lo = vin[2 * w][e >> 1], hi = vin[2 * w + 1][e >> 1];
+                y[w] = (e & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+            }
+            *reinterpret_cast<u32x4*>(img + IMG_TILE_BYTES + img_v_offset(vkg, 8 * vdg + e)) = y;
+        }
+    }
+    __syncthreads();
+
+    // ---- both images out, 16 contiguous bytes per thread per pass
+    uint8_t* kdst = reinterpret_cast<uint8_t*>(a.img_k) + tile_id * IMG_TILE_BYTES;
+    uint8_t* vdst = reinterpret_cast<uint8_t*>(a.img_v) + tile_id * IMG_TILE_BYTES;
+#pragma unroll
+    for (int p = 0; p < IMG_TILE_BYTES / 4096; ++p) {
+        const int off = p * 4096 + 16 * tid;
+        *reinterpret_cast<u32x4*>(kdst + off) = *reinterpret_cast<const u32x4*>(img + off);
+        *reinterpret_cast<u32x4*>(vdst + off) = *reinterpret_cast<const u32x4*>(img + IMG_TILE_BYTES + off);
+    }
+}
+
+template <int KIND>
+hipError_t launch_kind(const KvImageArgs& a, hipStream_t stream) {
+    const unsigned blocks = (unsigned)(a.tiles * a.HK);
+    if (a.pairing == PAIR_SPLIT_HALF)
+        hipLaunchKernelGGL((kv_image_kernel<KIND, PAIR_SPLIT_HALF>), dim3(blocks), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((kv_image_kernel<KIND, PAIR_INTERLEAVED>), dim3(blocks), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_kv_image(const KvImageArgs& a, hipStream_t stream) {
+    if (a.Sk < 1 || a.HK < 1 || a.tiles != img_tiles(a.Sk) || (int64_t)a.tiles * a.HK > 0x7fffffff)
+        return hipErrorInvalidValue;
+    switch (a.table_kind) {
+        case TABLE_NONE: return launch_kind<TABLE_NONE>(a, stream);
+        case TABLE_COSSIN_F32: return launch_kind<TABLE_COSSIN_F32>(a, stream);
+        case TABLE_MAT2_BF16: return launch_kind<TABLE_MAT2_BF16>(a, stream);
+        case TABLE_MAT2_F32: return launch_kind<TABLE_MAT2_F32>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace lr

@@ -9,8 +9,8 @@
 #include "lr_common.h"
 #include "lr_int8.h"
 #include "lr_kernels.h"
+#include "tile_image.h"
 
-static_assert(LR_ATTN_SK_AREA_BYTES == lr::SK_AREA_BYTES, "stream-K area size");
 
 namespace {
 
@@ -48,7 +48,9 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
                    int causal, float scale, int64_t q_rs, int64_t k_rs, int64_t v_rs, int64_t o_rs, int64_t k_hs,
                    int64_t v_hs, int config, hipStream_t stream, void* workspace = nullptr, size_t ws_bytes = 0) {
     if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || nkeys < 1 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
-    if (!scale_ok(scale) || config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_WS_W8) return ERR_ARGS;
+    if (!scale_ok(scale) || !(config == LR_ATTN_CFG_AUTO || config == LR_ATTN_CFG_PIPE_W8 ||
+                              config == LR_ATTN_CFG_PIPE_W4))
+        return ERR_ARGS;
     if ((int64_t)p0 + W > INT_MAX - 512 || nkeys > INT_MAX - 512 || W > INT_MAX - 512) return ERR_ARGS;
     if (!rows_ok(q, q_rs, H) || !rows_ok(out, o_rs, H)) return ERR_ARGS;
     if (!k || !v || !aligned(k, 16) || !aligned(v, 16) || k_rs % 8 || v_rs % 8 || k_hs % 8 || v_hs % 8) return ERR_ARGS;
@@ -62,7 +64,6 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
     a.k_hs = k_hs; a.v_hs = v_hs;
     a.W = W; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = nkeys; a.p0 = p0; a.causal = causal;
     a.c = scale * 1.4426950408889634f;
-    a.table_kind = lr::TABLE_NONE;
     const int ns = split_count(W, H, nkeys, causal);
     const bool split = workspace && ns > 1 && (config == LR_ATTN_CFG_AUTO || config == LR_ATTN_CFG_PIPE_W8) &&
                        k_hs == lr::D && v_hs == lr::D && ws_bytes >= split_bytes(W, H, ns) && aligned(workspace, 256);
@@ -71,11 +72,11 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
         a.part_o = static_cast<float*>(workspace);
         a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                              (((size_t)H * W * ns * lr::D * 4 + 255) & ~(size_t)255));
-        const hipError_t e = lr::launch_attention(a, false, false, LR_ATTN_CFG_PIPE_W8, stream);
+        const hipError_t e = lr::launch_attention(a, LR_ATTN_CFG_PIPE_W8, stream);
         if (e != hipSuccess) return (int)e;
         return (int)lr::launch_split_combine(a, stream);
     }
-    return (int)lr::launch_attention(a, false, false, config, stream);
+    return (int)lr::launch_attention(a, config, stream);
 }
 
 // Table checks shared by the rope entry points. rows_needed: table rows that will be read.
@@ -92,89 +93,141 @@ bool table_ok(int kind, const void* ta, const void* tb, int64_t stride, int rot,
     return aligned(ta, 16) && stride % 4 == 0 && stride >= 4 * pairs;  // LR_TABLE_MAT2_F32
 }
 
-// Workspace of the fused op: the prepared keys bf16 [HK][Sk][128], then (256-byte aligned) the packed V^T tiles
-// bf16 [HK][ceil(Sk/64)][128][64].
-size_t ws_keys_bytes(int Sk, int HK) { return ((size_t)Sk * (size_t)HK * lr::D * 2 + 255) & ~(size_t)255; }
-int vt_tiles(int Sk) { return (Sk + lr::VT_TILE_KEYS - 1) / lr::VT_TILE_KEYS; }
-size_t ws_bytes_needed(int Sk, int HK) {
-    return ws_keys_bytes(Sk, HK) + (size_t)HK * (size_t)vt_tiles(Sk) * lr::D * lr::VT_TILE_KEYS * 2;
+// Workspace of the fused op and of its two stages: the tile images of the keys, then those of the values
+// (tile_image.h), 16 KB per 64-key tile and kv head each.
+size_t ws_bytes_needed(int Sk, int HK) { return 2 * (size_t)lr::img_bytes(Sk, HK); }
+
+// the configurations of the fused and prepared calls (both the streaming kernel)
+inline bool is_stream(int config) { return config == LR_ATTN_CFG_AUTO || config == LR_ATTN_CFG_STREAM_W8; }
+
+// compute units of the current device: the streaming kernel's grid (one workgroup per CU); queried on every call,
+// nothing is cached
+int device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return n;
 }
 
-// The keys stage: RMSNorm + RoPE of k_raw rows j >= n_pre (rows j < n_pre copied) into the workspace's keys, and,
-// when v is given, V packed into the workspace's V^T tiles.
-int kv_impl(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
-            const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK,
-            int n_pre, void* ws, size_t ws_bytes, hipStream_t stream) {
-    if (rot == 0) rot = lr::D;
+// byte range [lo, hi) of a rows tensor: rows rows of heads heads, row stride rs elements
+struct Span {
+    uintptr_t lo, hi;
+};
+inline Span rows_span(const void* p, int64_t rows, int64_t rs, int heads) {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+    return Span{lo, lo + (uintptr_t)(((rows - 1) * rs + (int64_t)heads * lr::D) * 2)};
+}
+inline Span ws_span(const void* ws, int Sk, int HK) {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(ws);
+    return Span{lo, lo + ws_bytes_needed(Sk, HK)};
+}
+inline bool overlap(Span a, Span b) { return a.lo < b.hi && b.lo < a.hi; }
+
+// Checks of the keys stage: k_raw and v rows, the key norm weight and table, the workspace.
+bool kv_stage_ok(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
+                 const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK,
+                 int n_pre, const void* ws, size_t ws_bytes) {
     if (Sk < 1 || HK < 1 || Sk > INT_MAX - 512 || n_pre < 0 || n_pre > Sk || !(eps >= 0.0f) || !isfinite(eps))
-        return ERR_ARGS;
-    if (!rows_ok(k_raw, k_rs, HK) || (v && !rows_ok(v, v_rs, HK)) || (wk && !aligned(wk, 16))) return ERR_ARGS;
-    if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
-    if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return ERR_ARGS;
-    lr::RopeArgs r{};
-    r.src = static_cast<const uint16_t*>(k_raw);
-    r.dst = static_cast<uint16_t*>(ws);
-    r.src_rs = k_rs; r.src_hs = lr::D;
-    r.dst_rs = lr::D; r.dst_hs = (int64_t)Sk * lr::D;
-    r.rows = Sk; r.heads = HK; r.n_copy = n_pre;
-    r.weight_kind = wk ? lr::W_F32 : lr::W_NONE; r.w = wk;
+        return false;
+    if (!rows_ok(k_raw, k_rs, HK) || !rows_ok(v, v_rs, HK) || (wk && !aligned(wk, 16))) return false;
+    if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return false;
+    return ws && aligned(ws, 256) && ws_bytes >= ws_bytes_needed(Sk, HK);
+}
+
+// The keys stage (arguments checked): RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre; rows j < n_pre
+// copied) and the values, into the workspace's tile images.
+int kv_launch(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
+              const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK,
+              int n_pre, void* ws, hipStream_t stream) {
+    lr::KvImageArgs r{};
+    r.k = static_cast<const uint16_t*>(k_raw);
+    r.v = static_cast<const uint16_t*>(v);
+    r.k_rs = k_rs; r.v_rs = v_rs;
+    r.w = wk;
     r.table_kind = Sk > n_pre ? table_kind : lr::TABLE_NONE; r.pairing = pairing; r.rot = rot;
-    r.ta = kta; r.tb = ktb; r.tab_stride = tab_stride;
-    r.eps = eps; r.round_norm = 0;
-    if (v) {   // packed by extra blocks of the same launch
-        r.vp.v = static_cast<const uint16_t*>(v);
-        r.vp.vt = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + ws_keys_bytes(Sk, HK));
-        r.vp.v_rs = v_rs; r.vp.Sk = Sk; r.vp.HK = HK; r.vp.ntiles = vt_tiles(Sk);
-    }
+    r.ta = kta; r.tb = ktb; r.tab_stride = tab_stride; r.eps = eps;
+    r.Sk = Sk; r.HK = HK; r.n_pre = n_pre;
+    r.tiles = lr::img_tiles(Sk);
+    r.img_k = ws;
+    r.img_v = static_cast<char*>(ws) + lr::img_bytes(Sk, HK);
+    return (int)lr::launch_kv_image(r, stream);
+}
+
+// Checks of the query stage: q_raw and q_prep rows (same shape), the table and weight.
+bool q_stage_ok(const void* q_raw, int64_t q_rs, const void* q_prep, int64_t p_rs, const float* wq, int table_kind,
+                const void* qta, const void* qtb, int64_t tab_stride, int pairing, int rot, float eps, int Sq, int H) {
+    if (Sq < 1 || H < 1 || Sq > INT_MAX - 512 || !(eps >= 0.0f) || !isfinite(eps)) return false;
+    if (!rows_ok(q_raw, q_rs, H) || !rows_ok(q_prep, p_rs, H) || (wq && !aligned(wq, 16))) return false;
+    // in place (the same rows) or apart: each 16-lane group reads its whole row before writing it, nothing else
+    if (q_raw != q_prep && overlap(rows_span(q_raw, Sq, q_rs, H), rows_span(q_prep, Sq, p_rs, H))) return false;
+    if (q_raw == q_prep && q_rs != p_rs) return false;
+    return table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32);
+}
+
+// The query stage (arguments checked): RMSNorm + RoPE of the q_raw rows into q_prep, rounded once to bf16 as the
+// reference's rope_q writes them (rms_rope.hip).
+int q_launch(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, const float* wq, int table_kind,
+             const void* qta, const void* qtb, int64_t tab_stride, int pairing, int rot, float eps, int Sq, int H,
+             hipStream_t stream) {
+    lr::RopeArgs r{};
+    r.src = static_cast<const uint16_t*>(q_raw);
+    r.dst = static_cast<uint16_t*>(q_prep);
+    r.src_rs = q_rs; r.src_hs = lr::D; r.dst_rs = p_rs; r.dst_hs = lr::D;
+    r.rows = Sq; r.heads = H; r.n_copy = 0;
+    r.weight_kind = wq ? lr::W_F32 : lr::W_NONE; r.w = wq;
+    r.table_kind = table_kind; r.pairing = pairing; r.rot = rot;
+    r.ta = qta; r.tb = qtb; r.tab_stride = tab_stride;
+    r.eps = eps; r.round_norm = 0; r.post_scale = 1.0f;
     return (int)lr::launch_rms_rope(r, stream);
 }
 
-// Checks shared by the attention stage's entry points.
-bool attn_stage_ok(const void* q_raw, const void* out, const float* wq, int table_kind, const void* qta,
-                   const void* qtb, int64_t tab_stride, int pairing, int rot, float eps, int Sq, int Sk, int H, int HK,
-                   int p0, int causal, float scale, int64_t q_rs, int64_t o_rs, int config) {
+// Checks of the attention stage. o_rs is bounded so that a block's 256 output rows span less than 4 GiB (the
+// kernel's buffer range); out must not overlap the workspace, and q_prep is either out itself (each block reads its
+// queries before it writes its output over them) or apart from it.
+bool images_stage_ok(const void* q_prep, int64_t p_rs, const void* ws, size_t ws_bytes, const void* out, int64_t o_rs,
+                     int Sq, int Sk, int H, int HK, int p0, int causal, float scale) {
     if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return false;
-    if (!(eps >= 0.0f) || !isfinite(eps) || !scale_ok(scale)) return false;
-    if (config < LR_ATTN_CFG_AUTO || config > LR_ATTN_CFG_PAIR_SK_W4) return false;
+    if (!scale_ok(scale)) return false;
     if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return false;
-    if (!rows_ok(q_raw, q_rs, H) || !rows_ok(out, o_rs, H)) return false;
-    return table_ok(table_kind, qta, qtb, tab_stride, rot, pairing, 32) && (!wq || aligned(wq, 16));
+    if (!rows_ok(q_prep, p_rs, H) || !rows_ok(out, o_rs, H) || o_rs > ((int64_t)1 << 23)) return false;
+    if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return false;
+    const Span so = rows_span(out, Sq, o_rs, H);
+    if (overlap(so, ws_span(ws, Sk, HK))) return false;
+    if (q_prep == out) return p_rs == o_rs;
+    return !overlap(so, rows_span(q_prep, Sq, p_rs, H)) && !overlap(rows_span(q_prep, Sq, p_rs, H), ws_span(ws, Sk, HK));
 }
 
-// The attention stage over prepared keys: values from the workspace's V^T tiles when v is null, else from v rows.
-int prepared_impl(const void* q_raw, void* ws, size_t ws_bytes, const void* v, int64_t v_rs, void* out,
-                  const float* wq, int table_kind, const void* qta, const void* qtb, int64_t tab_stride, int pairing,
-                  int rot, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_rs,
-                  int64_t o_rs, int config, hipStream_t stream) {
-    if (rot == 0) rot = lr::D;
-    if (!attn_stage_ok(q_raw, out, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, Sk, H, HK, p0, causal,
-                       scale, q_rs, o_rs, config))
-        return ERR_ARGS;
-    if (v ? !rows_ok(v, v_rs, HK) : !lr::attention_config_reads_vt(config)) return ERR_ARGS;
-    if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return ERR_ARGS;
+// The attention stage (arguments checked): the persistent streaming kernel, one workgroup per CU.
+int images_launch(const void* q_prep, int64_t p_rs, const void* ws, void* out, int64_t o_rs, int Sq, int Sk, int H,
+                  int HK, int p0, int causal, float scale, hipStream_t stream) {
+    const int cus = device_cus();
+    if (cus < 1) return (int)hipErrorInvalidDevice;
     lr::AttnArgs a{};
-    a.q = static_cast<const uint16_t*>(q_raw);
+    a.q = static_cast<const uint16_t*>(q_prep);
     a.k = static_cast<const uint16_t*>(ws);
+    a.v = reinterpret_cast<const uint16_t*>(static_cast<const char*>(ws) + lr::img_bytes(Sk, HK));
     a.out = static_cast<uint16_t*>(out);
-    a.q_rs = q_rs; a.k_rs = lr::D; a.o_rs = o_rs;
-    a.k_hs = (int64_t)Sk * lr::D;
-    if (v) {
-        a.v = static_cast<const uint16_t*>(v);
-        a.v_rs = v_rs; a.v_hs = lr::D;
-    } else {
-        a.v = reinterpret_cast<const uint16_t*>(static_cast<const char*>(ws) + ws_keys_bytes(Sk, HK));
-        a.v_rs = 0; a.v_hs = (int64_t)vt_tiles(Sk) * lr::D * lr::VT_TILE_KEYS;
-    }
+    a.q_rs = p_rs; a.o_rs = o_rs;
+    a.k_hs = a.v_hs = lr::img_tiles(Sk) * (lr::IMG_TILE_BYTES / 2);
     a.W = Sq; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = Sk; a.p0 = p0; a.causal = causal;
     a.c = scale * 1.4426950408889634f;
-    a.wq = wq;
-    a.table_kind = table_kind; a.pairing = pairing; a.rot = rot;
-    a.qta = qta; a.qtb = qtb; a.tab_stride = tab_stride; a.eps = eps;
-    if (config == LR_ATTN_CFG_PAIR_SK_W4) {   // the stream-K partials follow the V^T tiles
-        if (v || ws_bytes < ws_bytes_needed(Sk, HK) + lr::SK_AREA_BYTES) return ERR_ARGS;
-        a.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_bytes_needed(Sk, HK));
-    }
-    return (int)lr::launch_attention(a, true, v == nullptr, config, stream);
+    return (int)lr::launch_stream(a, cus, stream);
+}
+
+int prepared_impl(const void* q_raw, void* ws, size_t ws_bytes, void* out, const float* wq, int table_kind,
+                  const void* qta, const void* qtb, int64_t tab_stride, int pairing, int rot, float eps, int Sq,
+                  int Sk, int H, int HK, int p0, int causal, float scale, int64_t q_rs, int64_t o_rs, int config,
+                  hipStream_t stream) {
+    if (rot == 0) rot = lr::D;
+    // the queries are prepared into out's rows, then attended in place there
+    if (!is_stream(config) ||
+        !q_stage_ok(q_raw, q_rs, out, o_rs, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, H) ||
+        !images_stage_ok(out, o_rs, ws, ws_bytes, out, o_rs, Sq, Sk, H, HK, p0, causal, scale))
+        return ERR_ARGS;
+    const int e = q_launch(q_raw, q_rs, out, o_rs, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, H,
+                           stream);
+    if (e != 0) return e;
+    return images_launch(out, o_rs, ws, out, o_rs, Sq, Sk, H, HK, p0, causal, scale, stream);
 }
 
 int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, const float* wq, const float* wk,
@@ -182,22 +235,23 @@ int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, c
                int pairing, int rot, float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
                int64_t q_rs, int64_t k_rs, int64_t v_rs, int64_t o_rs, int n_pre, void* ws, size_t ws_bytes,
                int config, hipStream_t stream) {
-    // validate both stages before launching either
+    // every argument of all three launches is checked before the first one
     if (rot == 0) rot = lr::D;
-    if (!attn_stage_ok(q_raw, out, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, Sk, H, HK, p0, causal,
-                       scale, q_rs, o_rs, config))
+    if (!is_stream(config) ||
+        !q_stage_ok(q_raw, q_rs, out, o_rs, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, H) ||
+        !images_stage_ok(out, o_rs, ws, ws_bytes, out, o_rs, Sq, Sk, H, HK, p0, causal, scale) ||
+        !kv_stage_ok(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws,
+                     ws_bytes))
         return ERR_ARGS;
-    if (n_pre < 0 || n_pre > Sk || !rows_ok(k_raw, k_rs, HK) || !rows_ok(v, v_rs, HK)) return ERR_ARGS;
-    if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return ERR_ARGS;
-    if (wk && !aligned(wk, 16)) return ERR_ARGS;
-    if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return ERR_ARGS;
-    // the 64-key pipelined configurations read packed V^T tiles; the others read the v rows directly
-    const bool vt = lr::attention_config_reads_vt(config);
-    const int e = kv_impl(k_raw, k_rs, vt ? v : nullptr, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps,
-                          Sk, HK, n_pre, ws, ws_bytes, stream);
+    // the prepared queries are written into out while the keys and values may still be read: no overlap
+    const Span so = rows_span(out, Sq, o_rs, H);
+    if (overlap(so, rows_span(k_raw, Sk, k_rs, HK)) || overlap(so, rows_span(v, Sk, v_rs, HK))) return ERR_ARGS;
+    int e = kv_launch(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws,
+                      stream);
     if (e != 0) return e;
-    return prepared_impl(q_raw, ws, ws_bytes, vt ? nullptr : v, v_rs, out, wq, table_kind, qta, qtb, tab_stride,
-                         pairing, rot, eps, Sq, Sk, H, HK, p0, causal, scale, q_rs, o_rs, config, stream);
+    e = q_launch(q_raw, q_rs, out, o_rs, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, H, stream);
+    if (e != 0) return e;
+    return images_launch(out, o_rs, ws, out, o_rs, Sq, Sk, H, HK, p0, causal, scale, stream);
 }
 
 int rope_impl(const void* src, int64_t src_rs, int64_t src_off, void* dst, int64_t dst_rs, int64_t n, int b,
@@ -223,7 +277,7 @@ int rope_impl(const void* src, int64_t src_rs, int64_t src_off, void* dst, int64
         r.weight_kind = w_kind; r.w = w;
         r.table_kind = table_kind; r.pairing = pairing; r.rot = rot;
         r.ta = ta; r.tb = tb; r.tab_stride = tab_stride;
-        r.eps = eps; r.round_norm = round_norm;
+        r.eps = eps; r.round_norm = round_norm; r.post_scale = 1.0f;
         const hipError_t e = lr::launch_rms_rope(r, stream);
         if (e != hipSuccess) return (int)e;
     }
@@ -354,7 +408,7 @@ int lr_attention_kmask_bf16(const void* q, const void* k, const void* v, void* o
         return ERR_ARGS;
     // the attention's own checks first, against the compacted keys, so that nothing is launched on a bad call
     if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || !scale_ok(scale) || !rows_ok(q, q_row_stride, H) ||
-        !rows_ok(out, out_row_stride, H))
+        !rows_ok(out, out_row_stride, H) || W > INT_MAX - 512 || nkeys > INT_MAX - 512)
         return ERR_ARGS;
     char* ws = static_cast<char*>(workspace);
     const size_t idx_bytes = ((size_t)n_valid * 4 + 255) & ~(size_t)255;
@@ -417,9 +471,13 @@ int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, 
                         const float* k_norm_w, int table_kind, const void* k_table_a, const void* k_table_b,
                         int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sk, int HK, int n_pre,
                         void* workspace, size_t workspace_bytes, lr_stream_t stream) {
-    if (!v) return ERR_ARGS;
-    return kv_impl(k_raw, k_row_stride, v, v_row_stride, k_norm_w, table_kind, k_table_a, k_table_b, table_row_stride,
-                   pairing, rot_dim, eps, Sk, HK, n_pre, workspace, workspace_bytes, stream);
+    if (rot_dim == 0) rot_dim = lr::D;
+    if (!kv_stage_ok(k_raw, k_row_stride, v, v_row_stride, k_norm_w, table_kind, k_table_a, k_table_b,
+                     table_row_stride, pairing, rot_dim, eps, Sk, HK, n_pre, workspace, workspace_bytes))
+        return ERR_ARGS;
+    return kv_launch(k_raw, k_row_stride, v, v_row_stride, k_norm_w, table_kind, k_table_a, k_table_b,
+                     table_row_stride, pairing, rot_dim, eps, Sk, HK, n_pre, workspace,
+                     reinterpret_cast<hipStream_t>(stream));
 }
 
 int lr_joint_attention_prepared(const void* q_raw, void* workspace, size_t workspace_bytes, void* out,
@@ -427,9 +485,31 @@ int lr_joint_attention_prepared(const void* q_raw, void* workspace, size_t works
                                 int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sq, int Sk, int H,
                                 int HK, int p0, int causal, float scale, int64_t q_row_stride, int64_t out_row_stride,
                                 int config, lr_stream_t stream) {
-    return prepared_impl(q_raw, workspace, workspace_bytes, nullptr, 0, out, q_norm_w, table_kind, q_table_a,
-                         q_table_b, table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale,
-                         q_row_stride, out_row_stride, config, stream);
+    return prepared_impl(q_raw, workspace, workspace_bytes, out, q_norm_w, table_kind, q_table_a, q_table_b,
+                         table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale, q_row_stride,
+                         out_row_stride, config, reinterpret_cast<hipStream_t>(stream));
+}
+
+int lr_joint_q_prepare(const void* q_raw, int64_t q_row_stride, void* q_prep, int64_t q_prep_row_stride,
+                       const float* q_norm_w, int table_kind, const void* q_table_a, const void* q_table_b,
+                       int64_t table_row_stride, int pairing, int rot_dim, float eps, int Sq, int H,
+                       lr_stream_t stream) {
+    if (rot_dim == 0) rot_dim = lr::D;
+    if (!q_stage_ok(q_raw, q_row_stride, q_prep, q_prep_row_stride, q_norm_w, table_kind, q_table_a, q_table_b,
+                    table_row_stride, pairing, rot_dim, eps, Sq, H))
+        return ERR_ARGS;
+    return q_launch(q_raw, q_row_stride, q_prep, q_prep_row_stride, q_norm_w, table_kind, q_table_a, q_table_b,
+                    table_row_stride, pairing, rot_dim, eps, Sq, H, reinterpret_cast<hipStream_t>(stream));
+}
+
+int lr_joint_attention_images(const void* q_prep, int64_t q_prep_row_stride, const void* workspace,
+                              size_t workspace_bytes, void* out, int64_t out_row_stride, int Sq, int Sk, int H, int HK,
+                              int p0, int causal, float scale, lr_stream_t stream) {
+    if (!images_stage_ok(q_prep, q_prep_row_stride, workspace, workspace_bytes, out, out_row_stride, Sq, Sk, H, HK, p0,
+                         causal, scale))
+        return ERR_ARGS;
+    return images_launch(q_prep, q_prep_row_stride, workspace, out, out_row_stride, Sq, Sk, H, HK, p0, causal, scale,
+                         reinterpret_cast<hipStream_t>(stream));
 }
 
 int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,

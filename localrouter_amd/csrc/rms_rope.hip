@@ -10,14 +10,8 @@
 // of them is consumed, the table and weight are shared by the group's heads, the sum of squares is a 4-step xor
 // butterfly inside the group, and a split-half partner chunk comes from lane c +- rot/16 of the same group. The table
 // kind and the pairing are template parameters, so the loop bodies carry no per-element branches.
-// HBM-bound by design: 256 bytes in and 256 bytes out per (row, head).
-//
-// For the prepared-keys attention path the same launch also packs V (blocks past the rope grid): V rows become
-// [HK][tiles][128 dims][64 keys], so that a 64-key tile of V^T is one contiguous 16 KB block the attention kernel
-// loads straight into LDS and reads back with one ds_read_b128 per MFMA operand. A pure relayout of Ops.attention's v
-// operand (src/engines/qwen_image/ops_launch.zig:163-172); keys past Sk are written as zeros, so a masked key (P = 0)
-// meets V = 0. Each thread moves one 8-key x 8-dim block: eight 16-byte row loads (256 contiguous bytes per 16 lanes),
-// a register transpose (two 16-bit halves per output word), eight 16-byte V^T stores.
+// HBM-bound by design: 256 bytes in and 256 bytes out per (row, head). The joint attention's query preparation is
+// this pass with post_scale = scale * log2 e (the streaming kernel's exp2-domain scores).
 #include "lr_common.h"
 #include "lr_kernels.h"
 
@@ -47,41 +41,8 @@ __device__ __forceinline__ Rot2 rot_at(const void* ta, const void* tb, int64_t r
     return r;
 }
 
-// Threads 0-127 / 128-255 of a packing block each pack one 64-key tile (tile index 2 * pb + half).
-__device__ __forceinline__ void v_pack_block(const VPackArgs& a, int pb) {
-    const int tt = threadIdx.x & 127;
-    const int tile = 2 * pb + (threadIdx.x >> 7);
-    if (tile >= a.HK * a.ntiles) return;
-    const int hk = tile / a.ntiles, t = tile - hk * a.ntiles;
-    const int dg = tt & 15, kg = tt >> 4;            // dims 8dg .. 8dg+7, keys 64t + 8kg .. +7
-    const int key0 = VT_TILE_KEYS * t + 8 * kg;
-    const uint16_t* src = a.v + (int64_t)hk * D + 8 * dg;
-    u32x4 x[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)min(key0 + i, a.Sk - 1) * a.v_rs);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-        if (key0 + i >= a.Sk) x[i] = u32x4{0, 0, 0, 0};
-    uint16_t* dst = a.vt + ((int64_t)tile * D + 8 * dg) * VT_TILE_KEYS + 8 * kg;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        // dim 8dg + e of keys 2w and 2w + 1 -> word w
-        u32x4 y;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const uint32_t lo = x[2 * w][e >> 1], hi = x[2 * w + 1][e >> 1];
-            y[w] = (e & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-        }
-        *reinterpret_cast<u32x4*>(dst + e * VT_TILE_KEYS) = y;
-    }
-}
-
 template <int KIND, int PAIRING>
-__global__ __launch_bounds__(256) void rms_rope_kernel(RopeArgs a, int rope_blocks) {
-    if ((int)blockIdx.x >= rope_blocks) {
-        v_pack_block(a.vp, blockIdx.x - rope_blocks);
-        return;
-    }
+__global__ __launch_bounds__(256) void rms_rope_kernel(RopeArgs a) {
     const int tid = threadIdx.x;
     const int c = tid & 15;
     const int hgroups = (a.heads + HPG - 1) / HPG;
@@ -149,7 +110,7 @@ __global__ __launch_bounds__(256) void rms_rope_kernel(RopeArgs a, int rope_bloc
         for (int j = 0; j < 8; ++j) ss = fmaf(x[j], x[j], ss);
 #pragma unroll
         for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 16);
-        const float rr = rsqrtf(ss * (1.0f / D) + a.eps);
+        const float rr = rsqrtf(ss * (1.0f / D) + a.eps) * a.post_scale;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             x[j] = x[j] * rr * wv[j];
@@ -191,13 +152,11 @@ __global__ __launch_bounds__(256) void rms_rope_kernel(RopeArgs a, int rope_bloc
 }
 
 template <int KIND>
-hipError_t launch_kind(const RopeArgs& a, unsigned blocks, int rope_blocks, hipStream_t stream) {
+hipError_t launch_kind(const RopeArgs& a, unsigned blocks, hipStream_t stream) {
     if (a.pairing == PAIR_SPLIT_HALF)
-        hipLaunchKernelGGL((rms_rope_kernel<KIND, PAIR_SPLIT_HALF>), dim3(blocks), dim3(256), 0, stream, a,
-                           rope_blocks);
+        hipLaunchKernelGGL((rms_rope_kernel<KIND, PAIR_SPLIT_HALF>), dim3(blocks), dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((rms_rope_kernel<KIND, PAIR_INTERLEAVED>), dim3(blocks), dim3(256), 0, stream, a,
-                           rope_blocks);
+        hipLaunchKernelGGL((rms_rope_kernel<KIND, PAIR_INTERLEAVED>), dim3(blocks), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -205,20 +164,13 @@ hipError_t launch_kind(const RopeArgs& a, unsigned blocks, int rope_blocks, hipS
 
 hipError_t launch_rms_rope(const RopeArgs& a, hipStream_t stream) {
     const int64_t groups = a.rows * ((a.heads + HPG - 1) / HPG);
-    const int64_t rope_blocks = (groups + 15) / 16;
-    int64_t pack_blocks = 0;
-    if (a.vp.v) {
-        if (a.vp.Sk < 1 || a.vp.HK < 1 || a.vp.ntiles != (a.vp.Sk + VT_TILE_KEYS - 1) / VT_TILE_KEYS)
-            return hipErrorInvalidValue;
-        pack_blocks = ((int64_t)a.vp.HK * a.vp.ntiles + 1) / 2;
-    }
-    const int64_t blocks = rope_blocks + pack_blocks;
-    if (rope_blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const int64_t blocks = (groups + 15) / 16;
+    if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
     switch (a.table_kind) {
-        case TABLE_NONE: return launch_kind<TABLE_NONE>(a, (unsigned)blocks, (int)rope_blocks, stream);
-        case TABLE_COSSIN_F32: return launch_kind<TABLE_COSSIN_F32>(a, (unsigned)blocks, (int)rope_blocks, stream);
-        case TABLE_MAT2_BF16: return launch_kind<TABLE_MAT2_BF16>(a, (unsigned)blocks, (int)rope_blocks, stream);
-        case TABLE_MAT2_F32: return launch_kind<TABLE_MAT2_F32>(a, (unsigned)blocks, (int)rope_blocks, stream);
+        case TABLE_NONE: return launch_kind<TABLE_NONE>(a, (unsigned)blocks, stream);
+        case TABLE_COSSIN_F32: return launch_kind<TABLE_COSSIN_F32>(a, (unsigned)blocks, stream);
+        case TABLE_MAT2_BF16: return launch_kind<TABLE_MAT2_BF16>(a, (unsigned)blocks, stream);
+        case TABLE_MAT2_F32: return launch_kind<TABLE_MAT2_F32>(a, (unsigned)blocks, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -5,6 +5,7 @@
   rms_rope_qk(...)      <- Kitchen.rmsRope, src/engines/minimax_h3/launch.zig:421-441
   joint_attention(...)  <- Dit.block's rope_q / rope_k / V copy / attention chain, src/engines/qwen_image/dit.zig:252-293
   joint_kv_prepare(...), joint_attention_prepared(...)  <- its two stages (keys / values reused across calls)
+  joint_q_prepare(...), joint_attention_images(...)     <- the fused op's query and attention launches one by one
   int8_attention(...)   <- MiniMax H3's INT8 attention, kitchen_int8_attention{,_rows}
                            (kernels/cuda/minimax/kitchen_launch.cu:193-280)
   kitchen_attention(...), kitchen_attention_prep(...), kitchen_attention_kernel(...)
@@ -26,9 +27,7 @@ D = 128
 TABLE_NONE, TABLE_COSSIN_F32, TABLE_MAT2_BF16, TABLE_MAT2_F32 = 0, 1, 2, 3
 PAIR_INTERLEAVED, PAIR_SPLIT_HALF = 0, 1
 WEIGHT_NONE, WEIGHT_F32, WEIGHT_BF16 = 0, 1, 2
-CFG_AUTO, CFG_PIPE_W8, CFG_PIPE_W4, CFG_REGSTAGE_W8, CFG_PINGPONG_W8, CFG_WIDE_W4, CFG_PAIR_W4 = 0, 1, 2, 3, 4, 5, 6
-CFG_WS_W8 = 7
-CFG_PAIR_SK_W4 = 8
+CFG_AUTO, CFG_PIPE_W8, CFG_PIPE_W4, CFG_STREAM_W8 = 0, 1, 2, 9
 SCALE_128 = float(torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32))  # f32 1/sqrt(128) = 0x3DB504F3
 
 
@@ -168,15 +167,9 @@ def rms_rope_qk(q: torch.Tensor, k: torch.Tensor, q_norm: torch.Tensor, k_norm: 
               _ptr(freqs), f_rs, rot, eps, _stream())
 
 
-# the stream-K area at the end of a joint-attention workspace: 512 partial slots of 4 waves x
-# (O [2][4][4][64] float4 + m, l [2][2][64]) fp32
-SK_AREA_BYTES = 2 * 256 * 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64) * 4
-
-
-def workspace_bytes(sk: int, kv_heads: int, stream_k: bool = False) -> int:
-    """lr_joint_attention_workspace_bytes; stream_k=True: plus the stream-K area CFG_PAIR_SK_W4 needs."""
-    n = int(_lib.load().lr_joint_attention_workspace_bytes(sk, kv_heads))
-    return n + SK_AREA_BYTES if stream_k and n else n
+def workspace_bytes(sk: int, kv_heads: int) -> int:
+    """lr_joint_attention_workspace_bytes: key and value tile images, 2 * HK * ceil(Sk / 64) * 16 KB."""
+    return int(_lib.load().lr_joint_attention_workspace_bytes(sk, kv_heads))
 
 
 def joint_attention(q_raw: torch.Tensor, k_raw: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *,
@@ -209,7 +202,7 @@ def joint_attention(q_raw: torch.Tensor, k_raw: torch.Tensor, v: torch.Tensor, o
         stride = qa.stride(0)
         if ka.stride(0) != stride:
             raise ValueError("q and k tables must share a row stride")
-    need = workspace_bytes(Sk, HK, stream_k=config == CFG_PAIR_SK_W4)
+    need = workspace_bytes(Sk, HK)
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q_raw.device)
     if workspace.numel() * workspace.element_size() < need:
@@ -225,8 +218,8 @@ def joint_kv_prepare(k_raw: torch.Tensor, v: torch.Tensor, workspace: torch.Tens
                      k_norm: torch.Tensor | None = None, table_kind: int = TABLE_COSSIN_F32,
                      k_table: tuple | None = None, pairing: int = PAIR_INTERLEAVED, rot: int = 128, eps: float = 1e-6,
                      n_pre: int = 0) -> torch.Tensor:
-    """First stage of joint_attention: k_raw [Sk, HK, 128] normalised and rotated (rows < n_pre copied) and v packed
-    into the workspace (lr_joint_kv_prepare). Returns the workspace."""
+    """First stage of joint_attention: k_raw [Sk, HK, 128] normalised and rotated (rows < n_pre copied) and v laid out
+    as tile images in the workspace (lr_joint_kv_prepare). Returns the workspace."""
     Sk, HK = k_raw.shape[0], k_raw.shape[1]
     k_rs, v_rs = _rows(k_raw, "k_raw", HK), _rows(v, "v", HK)
     if v.shape[0] < Sk:
@@ -272,6 +265,46 @@ def joint_attention_prepared(q_raw: torch.Tensor, workspace: torch.Tensor, sk: i
     _lib.call("lr_joint_attention_prepared", _ptr(q_raw), _ptr(workspace), workspace.numel() * workspace.element_size(),
               _ptr(out), _ptr(q_norm), table_kind, _ptr(qa), _ptr(qb), stride, pairing, rot, eps, Sq, sk, H, kv_heads,
               p0, int(causal), scale, q_rs, o_rs, config, _stream())
+    return out
+
+
+def joint_q_prepare(q_raw: torch.Tensor, q_prep: torch.Tensor | None = None, *, q_norm: torch.Tensor | None = None,
+                    table_kind: int = TABLE_COSSIN_F32, q_table: tuple | None = None,
+                    pairing: int = PAIR_INTERLEAVED, rot: int = 128, eps: float = 1e-6) -> torch.Tensor:
+    """The fused op's query launch (lr_joint_q_prepare): q_raw [Sq, H, 128] normalised and rotated, rounded once to
+    bf16, into q_prep (q_raw itself is allowed: in place)."""
+    Sq, H = q_raw.shape[0], q_raw.shape[1]
+    q_rs = _rows(q_raw, "q_raw", H)
+    if q_prep is None:
+        q_prep = torch.empty((Sq, H, D), dtype=torch.bfloat16, device=q_raw.device)
+    p_rs = _rows(q_prep, "q_prep", H)
+    if q_norm is not None and (q_norm.dtype != torch.float32 or not q_norm.is_contiguous() or q_norm.numel() != D):
+        raise ValueError("q_norm: expected fp32 [128]")
+    qa = qb = None
+    stride = 0
+    if table_kind != TABLE_NONE:
+        if q_table is None:
+            raise ValueError("joint_q_prepare: q_table required")
+        qa, qb = q_table
+        stride = qa.stride(0)
+    _lib.call("lr_joint_q_prepare", _ptr(q_raw), q_rs, _ptr(q_prep), p_rs, _ptr(q_norm), table_kind, _ptr(qa),
+              _ptr(qb), stride, pairing, rot, eps, Sq, H, _stream())
+    return q_prep
+
+
+def joint_attention_images(q_prep: torch.Tensor, workspace: torch.Tensor, sk: int, kv_heads: int,
+                           out: torch.Tensor | None = None, *, causal: bool = False, p0: int = 0,
+                           scale: float = SCALE_128) -> torch.Tensor:
+    """The fused op's attention launch (lr_joint_attention_images): queries prepared by joint_q_prepare over a
+    workspace filled by joint_kv_prepare. out may be q_prep itself."""
+    Sq, H = q_prep.shape[0], q_prep.shape[1]
+    p_rs = _rows(q_prep, "q_prep", H)
+    if out is None:
+        out = torch.empty((Sq, H, D), dtype=torch.bfloat16, device=q_prep.device)
+    o_rs = _rows(out, "out", H)
+    _lib.call("lr_joint_attention_images", _ptr(q_prep), p_rs, _ptr(workspace),
+              workspace.numel() * workspace.element_size(), _ptr(out), o_rs, Sq, sk, H, kv_heads, p0, int(causal),
+              scale, _stream())
     return out
 
 

@@ -40,6 +40,8 @@ MUTANTS = {
     "gqa_mod": 6,
     "no_weight": 7,
     "table_transposed": 8,
+    "no_round_norm": 9,
+    "no_round_prepared": 10,
 }
 
 
@@ -69,6 +71,8 @@ def lib() -> ctypes.CDLL:
         L.lro_bf16_to_f32_array.argtypes = [_P, _P, _I64]
         L.lro_rms_rope.argtypes = [_P, _I64, ctypes.c_int, _I64, _P, _P, ctypes.c_int, _P, _P, _I64, ctypes.c_int,
                                    ctypes.c_int, ctypes.c_float, _P]
+        L.lro_rms_rope_ex.argtypes = [_P, _I64, ctypes.c_int, _I64, _P, _P, ctypes.c_int, _P, _P, _I64, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_float, ctypes.c_int, _P]
         L.lro_attention_f64.argtypes = [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_float]
         L.lro_attention_f32.argtypes = [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -77,6 +81,7 @@ def lib() -> ctypes.CDLL:
                                           ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                           ctypes.c_int, ctypes.c_int, _P]
+        L.lro_joint_attention_ex.argtypes = list(L.lro_joint_attention.argtypes[:-1]) + [ctypes.c_int, _P]
         L.lro_i8_rotate.argtypes = [_P, ctypes.c_int]
         L.lro_i8_anchor.argtypes = [_P, _I64, ctypes.c_int]
         L.lro_i8_anchor.restype = ctypes.c_int
@@ -140,10 +145,11 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
 
 # ------------------------------------------------------------------------------------------ liblro.so wrappers
 def rms_rope(x: np.ndarray, w=None, *, table_kind=TABLE_NONE, ta=None, tb=None, pairing=PAIR_INTERLEAVED,
-             rot=128, eps=1e-6, w_bf16=None) -> np.ndarray:
+             rot=128, eps=1e-6, w_bf16=None, round_norm=False) -> np.ndarray:
     """x: uint16 (bf16 bits) [rows, heads, 128] -> fp32 [rows, heads, 128]. Row r uses table row r.
     Tables: COSSIN: ta = cos, tb = sin fp32 [rows, >= rot/2]; MAT2_BF16: ta uint16 [rows, >= 2*rot];
-    MAT2_F32: ta fp32 [rows, >= 2*rot]."""
+    MAT2_F32: ta fp32 [rows, >= 2*rot]. round_norm: the normalised value rounded to bf16 before the rotation
+    (rms_rope.cu:143-150)."""
     x = np.ascontiguousarray(x)
     rows, heads, d = x.shape
     assert d == D
@@ -157,8 +163,8 @@ def rms_rope(x: np.ndarray, w=None, *, table_kind=TABLE_NONE, ta=None, tb=None, 
             assert tb.shape == ta.shape
     wp = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
     wb = None if w_bf16 is None else np.ascontiguousarray(w_bf16, dtype=np.uint16)
-    lib().lro_rms_rope(_ptr(x), rows, heads, heads * D, _ptr(wp), _ptr(wb), table_kind, _ptr(ta), _ptr(tb), stride,
-                       pairing, rot, ctypes.c_float(eps), _ptr(y))
+    lib().lro_rms_rope_ex(_ptr(x), rows, heads, heads * D, _ptr(wp), _ptr(wb), table_kind, _ptr(ta), _ptr(tb),
+                          stride, pairing, rot, ctypes.c_float(eps), int(bool(round_norm)), _ptr(y))
     return y
 
 
@@ -193,9 +199,11 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, p0=0, nkeys=None, 
 
 def joint_attention(q_raw, k_raw, v, *, wq=None, wk=None, table_kind=TABLE_NONE, qa=None, qb=None, ka=None,
                     kb=None, pairing=PAIR_INTERLEAVED, rot=128, eps=1e-6, p0=0, causal=False, scale=None, n_pre=0,
-                    precise=True) -> np.ndarray:
+                    precise=True, round_prepared=False) -> np.ndarray:
     """The fused op on bf16-bit inputs q_raw [Sq, H, 128], k_raw, v [Sk, HK, 128] -> fp32 [Sq, H, 128].
-    Query i uses q-table row i, key j >= n_pre uses k-table row j - n_pre, keys j < n_pre are used as given."""
+    Query i uses q-table row i, key j >= n_pre uses k-table row j - n_pre, keys j < n_pre are used as given.
+    round_prepared: the normalised, rotated q and k rounded to bf16 before the attention, as the reference's chain
+    stores them (dit.zig:252-263)."""
     q_raw, k_raw, v = (np.ascontiguousarray(a) for a in (q_raw, k_raw, v))
     Sq, H, _ = q_raw.shape
     Sk, HK, _ = k_raw.shape
@@ -212,20 +220,27 @@ def joint_attention(q_raw, k_raw, v, *, wq=None, wk=None, table_kind=TABLE_NONE,
     wq = None if wq is None else np.ascontiguousarray(wq, dtype=np.float32)
     wk = None if wk is None else np.ascontiguousarray(wk, dtype=np.float32)
     out = np.empty((Sq, H, D), dtype=np.float32)
-    lib().lro_joint_attention(_ptr(q_raw), _ptr(k_raw), _ptr(v), H * D, HK * D, HK * D, _ptr(wq), _ptr(wk),
-                              table_kind, _ptr(qa), _ptr(qb), _ptr(ka), _ptr(kb), stride, pairing, rot,
-                              ctypes.c_float(eps), Sq, Sk, H, HK, p0, int(causal), ctypes.c_float(scale), n_pre,
-                              int(precise), _ptr(out))
+    lib().lro_joint_attention_ex(_ptr(q_raw), _ptr(k_raw), _ptr(v), H * D, HK * D, HK * D, _ptr(wq), _ptr(wk),
+                                 table_kind, _ptr(qa), _ptr(qb), _ptr(ka), _ptr(kb), stride, pairing, rot,
+                                 ctypes.c_float(eps), Sq, Sk, H, HK, p0, int(causal), ctypes.c_float(scale), n_pre,
+                                 int(precise), int(bool(round_prepared)), _ptr(out))
     return out
 
 
 # ------------------------------------------------------------------------------------------ pure numpy fp64 brute force
 def brute_rms_rope(x_f32: np.ndarray, w=None, *, cos=None, sin=None, mat=None, pairing=PAIR_INTERLEAVED, rot=128,
-                   eps=1e-6) -> np.ndarray:
-    """fp64 restatement on float inputs [rows, heads, 128]; cos/sin [rows, rot/2] or mat [rows, rot/2, 2, 2]."""
+                   eps=1e-6, round_norm=False) -> np.ndarray:
+    """fp64 restatement on float inputs [rows, heads, 128]; cos/sin [rows, rot/2] or mat [rows, rot/2, 2, 2].
+    round_norm: the normalised value rounded to fp32, then to bf16 (numpy's own rounding, ties to even) before the
+    rotation."""
     x = x_f32.astype(np.float64)
     rr = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
     y = x * rr * (1.0 if w is None else np.asarray(w, np.float64))
+    if round_norm:
+        f = y.astype(np.float32)
+        b = f.view(np.uint32).astype(np.uint64)
+        b = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16       # RNE to the upper 16 bits (finite inputs)
+        y = b.astype(np.uint32).view(np.float32).astype(np.float64)
     if cos is None and mat is None:
         return y
     P = rot // 2

@@ -14,7 +14,8 @@
  *     split-half pairs (i, i + rot/2), dims >= rot norm-only), and the Qwen-Image form
  *     src/engines/qwen_image/triton_k.zig:44-53 + tools/twin/stk_twin/dit.py:225-233 (fp32 weight, fp32 cos/sin
  *     [N, rot/2]); the interleaved pairing (2p, 2p+1) follows kernels/cuda/kandinsky6/dit/ops.cu:197-235.
- *     The oracle keeps the normalised value in full precision (no bf16 rounding before the rotation).
+ *     By default the oracle keeps the normalised value in full precision; with round_norm it rounds it to bf16
+ *     before the rotation, as rms_rope.cu:143-150 does (the MiniMax H3 path).
  *
  * Two attention implementations:
  *   lro_attention_f64  -- brute force, double accumulation, two passes per row. This is the pin.
@@ -46,6 +47,8 @@ enum {
     MUT_GQA_MOD = 6,       /* kv head h % HK instead of h / (H / HK) */
     MUT_NO_WEIGHT = 7,     /* norm weight ignored */
     MUT_TABLE_T = 8,       /* 2x2 rotation matrix transposed */
+    MUT_NO_ROUND = 9,      /* round_norm ignored: the normalised value kept unrounded before the rotation */
+    MUT_NO_ROUND_PREP = 10, /* round_prepared ignored: the joint attention's prepared q / k kept unrounded */
 };
 static int g_mutant = 0;
 void lro_set_mutant(int m) { g_mutant = m; }
@@ -125,10 +128,13 @@ void lro_synth_normal_bf16(uint64_t seed, uint64_t stream, int64_t n, uint16_t* 
  * pairing: 0 = interleaved (2p, 2p+1), 1 = split-half (p, p + rot/2).
  * w: fp32 [128] or NULL (ones); w_bf16: bf16 [128] used when w is NULL and w_bf16 is not.
  * x: bf16 [rows][heads][128] with row stride x_rs (elements, head h at h*128); y: fp32 [rows][heads][128] dense.
- * Row r uses table row r. (rms_rope.cu:83 rrms, :140-141 pairs, :161-164 rotation, :208-228 tail.) */
-void lro_rms_rope(const uint16_t* x, int64_t rows, int heads, int64_t x_rs, const float* w, const uint16_t* w_bf16,
-                  int table_kind, const void* ta, const void* tb, int64_t tab_stride, int pairing, int rot,
-                  float eps, float* y) {
+ * Row r uses table row r. (rms_rope.cu:83 rrms, :140-141 pairs, :161-164 rotation, :208-228 tail.)
+ * round_norm != 0: the normalised, weighted value is rounded to fp32 and then to bf16 (RNE) before the rotation
+ * (rms_rope.cu:143-150 stores x * rrms * w into a bf16 register pair before rotate_pair reads it). */
+void lro_rms_rope_ex(const uint16_t* x, int64_t rows, int heads, int64_t x_rs, const float* w, const uint16_t* w_bf16,
+                     int table_kind, const void* ta, const void* tb, int64_t tab_stride, int pairing, int rot,
+                     float eps, int round_norm, float* y) {
+    if (g_mutant == MUT_NO_ROUND) round_norm = 0;
     int pair_mode = pairing;
     if (g_mutant == MUT_PAIRING) pair_mode = 1 - pairing;
 #pragma omp parallel for schedule(static)
@@ -149,6 +155,7 @@ void lro_rms_rope(const uint16_t* x, int64_t rows, int heads, int64_t x_rs, cons
             double wd = w ? (double)w[d] : (w_bf16 ? (double)lro_bf16_to_f32(w_bf16[d]) : 1.0);
             if (g_mutant == MUT_NO_WEIGHT) wd = 1.0;
             n[d] = xs[d] * rr * wd;
+            if (round_norm) n[d] = lro_bf16_to_f32(lro_f32_to_bf16((float)n[d]));
         }
         if (table_kind != 0) {
             const int P = rot / 2;
@@ -175,6 +182,12 @@ void lro_rms_rope(const uint16_t* x, int64_t rows, int heads, int64_t x_rs, cons
         }
         for (int d = 0; d < LRO_D; ++d) yr[d] = (float)n[d];
     }
+}
+
+void lro_rms_rope(const uint16_t* x, int64_t rows, int heads, int64_t x_rs, const float* w, const uint16_t* w_bf16,
+                  int table_kind, const void* ta, const void* tb, int64_t tab_stride, int pairing, int rot,
+                  float eps, float* y) {
+    lro_rms_rope_ex(x, rows, heads, x_rs, w, w_bf16, table_kind, ta, tb, tab_stride, pairing, rot, eps, 0, y);
 }
 
 static inline int kv_head(int h, int H, int HK) {
@@ -299,10 +312,14 @@ void lro_attention_f32(const float* q, const float* k, const float* v, float* ou
  * (row stride v_rs). Query row i uses q-table row i; key row j >= n_pre uses k-table row j - n_pre; key rows
  * j < n_pre are taken as already normalised and rotated. Output fp32 [Sq][H][128] dense.
  * precise != 0: fp64 brute-force attention; else the fp32 flash-style path. */
-void lro_joint_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v, int64_t q_rs, int64_t k_rs,
-                         int64_t v_rs, const float* wq, const float* wk, int table_kind, const void* qa, const void* qb,
-                         const void* ka, const void* kb, int64_t tab_stride, int pairing, int rot, float eps, int Sq,
-                         int Sk, int H, int HK, int p0, int causal, float scale, int n_pre, int precise, float* out) {
+/* round_prepared != 0: the normalised, rotated q and k rounded to bf16 before the attention, as the reference's chain
+ * stores them (rope_q / rope_k write bf16 rows that Ops.attention reads, src/engines/qwen_image/dit.zig:252-263). */
+void lro_joint_attention_ex(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v, int64_t q_rs,
+                            int64_t k_rs, int64_t v_rs, const float* wq, const float* wk, int table_kind,
+                            const void* qa, const void* qb, const void* ka, const void* kb, int64_t tab_stride,
+                            int pairing, int rot, float eps, int Sq, int Sk, int H, int HK, int p0, int causal,
+                            float scale, int n_pre, int precise, int round_prepared, float* out) {
+    if (g_mutant == MUT_NO_ROUND_PREP) round_prepared = 0;
     float* qh = (float*)malloc(sizeof(float) * (size_t)Sq * H * LRO_D);
     float* kh = (float*)malloc(sizeof(float) * (size_t)Sk * HK * LRO_D);
     float* vf = (float*)malloc(sizeof(float) * (size_t)Sk * HK * LRO_D);
@@ -318,6 +335,11 @@ void lro_joint_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uin
 #pragma omp parallel for schedule(static)
     for (int64_t j = 0; j < Sk; ++j)
         for (int64_t e = 0; e < (int64_t)HK * LRO_D; ++e) vf[j * HK * LRO_D + e] = lro_bf16_to_f32(v[j * v_rs + e]);
+    if (round_prepared) {
+        for (int64_t e = 0; e < (int64_t)Sq * H * LRO_D; ++e) qh[e] = lro_bf16_to_f32(lro_f32_to_bf16(qh[e]));
+        for (int64_t e = (int64_t)n_pre * HK * LRO_D; e < (int64_t)Sk * HK * LRO_D; ++e)
+            kh[e] = lro_bf16_to_f32(lro_f32_to_bf16(kh[e]));
+    }
     if (precise)
         lro_attention_f64(qh, kh, vf, out, p0, Sq, H, HK, Sk, causal, scale);
     else
@@ -325,4 +347,12 @@ void lro_joint_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uin
     free(qh);
     free(kh);
     free(vf);
+}
+
+void lro_joint_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v, int64_t q_rs, int64_t k_rs,
+                         int64_t v_rs, const float* wq, const float* wk, int table_kind, const void* qa, const void* qb,
+                         const void* ka, const void* kb, int64_t tab_stride, int pairing, int rot, float eps, int Sq,
+                         int Sk, int H, int HK, int p0, int causal, float scale, int n_pre, int precise, float* out) {
+    lro_joint_attention_ex(q_raw, k_raw, v, q_rs, k_rs, v_rs, wq, wk, table_kind, qa, qb, ka, kb, tab_stride, pairing,
+                           rot, eps, Sq, Sk, H, HK, p0, causal, scale, n_pre, precise, 0, out);
 }

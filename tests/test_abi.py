@@ -5,9 +5,11 @@ from __future__ import annotations
 import ctypes
 import re
 
+import numpy as np
 import pytest
 
 from localrouter_amd import _lib, ops
+from tests._util import img_index
 
 HIP_ERROR_INVALID_VALUE = 1
 
@@ -30,25 +32,24 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version():
     header = _lib.HEADER.read_text()
     declared = int(re.search(r"#define LR_ATTN_ABI_VERSION (\d+)", header).group(1))
-    assert _lib.load().lr_attn_abi_version() == declared == 5
+    assert _lib.load().lr_attn_abi_version() == declared == 6
 
 
 def test_workspace_bytes():
     L = _lib.load()
-    # prepared keys [HK][Sk][128] rounded up to 256 bytes, then V^T tiles [HK][ceil(Sk/64)][128][64], all bf16
-    assert L.lr_joint_attention_workspace_bytes(4608, 24) == 4608 * 24 * 128 * 2 + 24 * 72 * 128 * 64 * 2
-    assert L.lr_joint_attention_workspace_bytes(3, 1) == 768 + 128 * 64 * 2
-    assert L.lr_joint_attention_workspace_bytes(65, 2) == 65 * 2 * 256 + 2 * 2 * 128 * 64 * 2
-    # LR_ATTN_CFG_PAIR_SK_W4: 512 stream-K partial slots of 4 waves x (O [2][4][4][64] float4 + m, l [2][2][64])
-    header = _lib.HEADER.read_text()
-    assert "#define LR_ATTN_SK_AREA_BYTES ((size_t)2 * 256 * 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64) * 4)" in header
-    assert ops.SK_AREA_BYTES == 2 * 256 * 4 * (2 * 4 * 16 * 64 + 2 * 2 * 64) * 4
-    assert ops.workspace_bytes(65, 2, stream_k=True) == 65 * 2 * 256 + 2 * 2 * 128 * 64 * 2 + ops.SK_AREA_BYTES
+    # key tile images then value tile images, [HK][ceil(Sk/64)] x 16 KB each
+    assert L.lr_joint_attention_workspace_bytes(4608, 24) == 2 * 24 * 72 * 16384
+    assert L.lr_joint_attention_workspace_bytes(3, 1) == 2 * 16384
+    assert L.lr_joint_attention_workspace_bytes(65, 2) == 2 * 2 * 2 * 16384
+    assert ops.workspace_bytes(65, 2) == 2 * 2 * 2 * 16384
     assert L.lr_joint_attention_workspace_bytes(0, 24) == 0
+    header = _lib.HEADER.read_text()
+    assert "SK_AREA" not in header and "#define LR_ATTN_CFG_STREAM_W8 9" in header
 
 
 # fake, well-aligned device addresses: validation must reject before any HIP call is made
 A = 0x10000
+W = 0x100000   # a fake workspace address past every fake tensor
 
 
 @pytest.mark.parametrize("args,why", [
@@ -77,16 +78,21 @@ def test_attention_ex_rejects_bad_config():
 def _fused(**kw):
     a = dict(q=A, k=A, v=A, out=A, wq=None, wk=None, kind=1, qa=A, qb=A, ka=A, kb=A, ts=64, pairing=0, rot=128,
              eps=1e-6, Sq=8, Sk=8, H=2, HK=2, p0=0, causal=0, scale=0.088, qrs=256, krs=256, vrs=256, ors=256, n_pre=0,
-             ws=A, wsb=8 * 2 * 256 + 2 * 128 * 64 * 2, stream=None)
+             ws=W, wsb=2 * 2 * 16384, config=0, stream=None)
     a.update(kw)
-    return _lib.load().lr_joint_attention_fused(*a.values())
+    return _lib.load().lr_joint_attention_fused_ex(*a.values())
 
 
 @pytest.mark.parametrize("kw,why", [
     (dict(ws=0), "no workspace"),
     (dict(ws=A + 16), "workspace not 256-aligned"),
     (dict(wsb=100), "workspace too small"),
-    (dict(wsb=8 * 2 * 256), "workspace holds the keys but not the V^T tiles"),
+    (dict(wsb=2 * 16384), "workspace holds the key images but not the value images"),
+    (dict(ws=A + 256), "out overlaps the workspace"),
+    (dict(out=A + 0x1000, k=A + 0x1000), "out overlaps k_raw"),
+    (dict(out=A + 0x1000, v=A + 0x1100), "out overlaps v"),
+    (dict(ors=(1 << 23) + 8), "out row stride beyond 2^23"),
+    (dict(config=1), "plain-attention configuration on the fused call"),
     (dict(kind=7), "table kind"),
     (dict(pairing=1, rot=48), "split-half rot not a multiple of 32"),
     (dict(rot=130), "rot > 128"),
@@ -105,7 +111,7 @@ def test_stage_entry_points_reject():
     L = _lib.load()
     wsb = L.lr_joint_attention_workspace_bytes(8, 2)
     kv = dict(k=A, krs=256, v=A, vrs=256, wk=None, kind=1, ka=A, kb=A, ts=64, pairing=0, rot=128, eps=1e-6, Sk=8, HK=2,
-              n_pre=0, ws=A, wsb=wsb, stream=None)
+              n_pre=0, ws=W, wsb=wsb, stream=None)
 
     def kv_call(**kw):
         a = dict(kv)
@@ -115,7 +121,7 @@ def test_stage_entry_points_reject():
     assert kv_call(v=0) == HIP_ERROR_INVALID_VALUE              # the values are part of the prepared workspace
     assert kv_call(wsb=wsb - 2) == HIP_ERROR_INVALID_VALUE
     assert kv_call(vrs=200) == HIP_ERROR_INVALID_VALUE
-    pr = dict(q=A, ws=A, wsb=wsb, out=A, wq=None, kind=1, qa=A, qb=A, ts=64, pairing=0, rot=128, eps=1e-6, Sq=8, Sk=8,
+    pr = dict(q=A, ws=W, wsb=wsb, out=A, wq=None, kind=1, qa=A, qb=A, ts=64, pairing=0, rot=128, eps=1e-6, Sq=8, Sk=8,
               H=2, HK=2, p0=0, causal=0, scale=0.088, qrs=256, ors=256, config=0, stream=None)
 
     def pr_call(**kw):
@@ -123,10 +129,10 @@ def test_stage_entry_points_reject():
         a.update(kw)
         return L.lr_joint_attention_prepared(*a.values())
 
-    for cfg in (3, 4, 5, 99):                                   # configurations that read V rows, or none at all
+    for cfg in (1, 2, 3, 8, 99):                                # only AUTO and STREAM_W8 read tile images
         assert pr_call(config=cfg) == HIP_ERROR_INVALID_VALUE, cfg
     assert pr_call(wsb=wsb - 256) == HIP_ERROR_INVALID_VALUE
-    assert pr_call(config=8) == HIP_ERROR_INVALID_VALUE         # stream-K without its partials area
+    assert pr_call(ws=A + 256) == HIP_ERROR_INVALID_VALUE       # out overlaps the workspace
 
 
 def test_rms_rope_rejects():
@@ -250,3 +256,14 @@ def test_split_workspace_sizes_and_rejects():
     assert L.lr_attention_bf16_ws(*args, fake, nb - 1, None) == HIP_ERROR_INVALID_VALUE   # workspace too small
     assert L.lr_attention_bf16_ws(*args, None, nb, None) == HIP_ERROR_INVALID_VALUE       # size without a pointer
     assert L.lr_attention_bf16_ws(*args, fake + 16, nb, None) == HIP_ERROR_INVALID_VALUE  # not 256-aligned
+
+
+def test_image_index_is_a_permutation():
+    """The tile-image restatement the GPU layout tests decode with covers each of a tile's 8192 bf16 slots once."""
+    kidx, vidx = img_index()
+    assert np.array_equal(np.sort(np.concatenate([kidx.ravel(), vidx.ravel()])), np.arange(16384))
+    # (element units: a lane's 16 bytes are 8 elements, a 1 KB fragment 512)
+    assert kidx[0, 0] == 0 and kidx[4, 0] == 8 * 8 and kidx[8, 0] == 4 * 8      # rows 4 and 8 swap lanes
+    assert kidx[0, 8] == 32 * 8 and kidx[0, 16] == 512 and kidx[32, 0] == 8 * 512
+    assert vidx[0, 0] == 8192 and vidx[1, 0] == 8193 and vidx[0, 1] == 8192 + 8 and vidx[8, 0] == 8192 + 32 * 8
+    assert vidx[16, 0] == 8192 + 4 * 512 and vidx[0, 32] == 8192 + 512

@@ -7,7 +7,7 @@
 
 Per-head QK-RMSNorm eps 1e-6 with weights 1.0, RoPE theta 10000 (text rows un-rotated), scale f32(1/sqrt(128)),
 non-causal. The oracle is the CPU fp32 flash-style path (oracle/lro.c, pinned against fp64 and torch SDPA on the
-CPU). Bar: max-abs 2e-2, mean-abs 2e-3 on the bf16 output.
+CPU). Bar: max-abs 2e-2, mean-abs 2e-3, relative L2 3e-3 on the bf16 output.
 """
 from __future__ import annotations
 
@@ -34,15 +34,20 @@ def _run_fused(q, k, v, cos, sin, config=ops.CFG_AUTO):
     return out
 
 
+def _bf16(x):
+    return oracle.bf16_to_f32(oracle.f32_to_bf16(x))
+
+
 def _oracle_rows(qb, kb, vb, cos, sin, rows):
-    """fp32 oracle output for the given query rows: q/k normalised and rotated, then attention over every key."""
+    """fp32 oracle output for the given query rows: q/k normalised and rotated and stored as bf16 (the reference's
+    chain, dit.zig:252-263), then attention over every key."""
     qh = oracle.rms_rope(np.ascontiguousarray(qb[rows]), None, table_kind=oracle.TABLE_COSSIN_F32,
                          ta=np.ascontiguousarray(cos[rows]), tb=np.ascontiguousarray(sin[rows]), eps=1e-6)
     kh = oracle.rms_rope(kb, None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos, tb=sin, eps=1e-6)
-    return oracle.attention(qh, kh, oracle.bf16_to_f32(vb), precise=False)
+    return oracle.attention(_bf16(qh), _bf16(kh), oracle.bf16_to_f32(vb), precise=False)
 
 
-@pytest.mark.parametrize("cfg", [ops.CFG_AUTO, ops.CFG_PAIR_W4, ops.CFG_WS_W8])
+@pytest.mark.parametrize("cfg", [ops.CFG_AUTO])
 @pytest.mark.parametrize("name,n_text,grid", [("cfg1", 256, (32, 32)), ("cfg2", 512, (64, 64))])
 def test_baseline_image_shapes_all_rows(name, n_text, grid, cfg):
     cos, sin = rope.grid2d_table(n_text, *grid)
@@ -109,25 +114,30 @@ def test_video_shape_single_pass_sampled_rows():
                          tb=np.ascontiguousarray(sin[rows]), eps=1e-6)
     kh = oracle.rms_rope(kb, None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos, tb=sin, eps=1e-6)
     del kb
-    ref = oracle.attention(qh, kh, oracle.bf16_to_f32(vb), precise=False)
+    ref = oracle.attention(_bf16(qh), _bf16(kh), oracle.bf16_to_f32(vb), precise=False)
     mx, mn = assert_close(got, ref, what="cfg5")
     print(f"[cfg5] max-abs {mx:.3e} mean-abs {mn:.3e} ({time.time() - t0:.0f} s)", flush=True)
 
 
-def test_default_config_matches_every_config_bitwise_class():
-    """All tile configurations compute the same function: outputs agree to bf16 rounding at a mid-size shape."""
+def test_fused_matches_plain_attention_over_rotated_operands():
+    """Two product paths compute the same function: the fused call (streaming kernel over tile images, queries scaled
+    before their bf16 rounding) and lr_rms_rope_bf16 + lr_attention_bf16 (value rows, running maximum) agree to the
+    bar at a mid-size shape."""
     cos, sin = rope.grid2d_table(64, 16, 16)
     S = cos.shape[0]
+    print(f"\n[fused vs plain] S={S} H=4", flush=True)
     qb = oracle.synth_bf16(106, 1, (S, 4, 128))
     kb = oracle.synth_bf16(106, 2, (S, 4, 128))
     vb = oracle.synth_bf16(106, 3, (S, 4, 128))
-    outs = []
-    for cfg in (ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_REGSTAGE_W8, ops.CFG_PINGPONG_W8, ops.CFG_WIDE_W4,
-                ops.CFG_PAIR_W4, ops.CFG_WS_W8):
-        tc, ts = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
-        o = ops.joint_attention(to_dev(qb), to_dev(kb), to_dev(vb), table_kind=ops.TABLE_COSSIN_F32,
-                                q_table=(tc, ts), config=cfg)
-        torch.cuda.synchronize()
-        outs.append((from_dev(o).astype(np.uint32) << 16).view(np.float32))
-    for o in outs[1:]:
-        assert np.abs(o - outs[0]).max() <= 2e-2
+    tc, ts = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    fused = from_dev(ops.joint_attention(to_dev(qb), to_dev(kb), to_dev(vb), table_kind=ops.TABLE_COSSIN_F32,
+                                         q_table=(tc, ts)))
+    qh, kh = torch.empty_like(to_dev(qb)), torch.empty_like(to_dev(kb))
+    for src, dst in ((to_dev(qb), qh), (to_dev(kb), kh)):
+        ops.rms_rope(src, dst, None, n=S, heads=4, src_row_stride=4 * 128, dst_row_stride=4 * 128,
+                     table_kind=ops.TABLE_COSSIN_F32, table_a=tc, table_b=ts)
+    plain = from_dev(ops.attention(qh, kh, to_dev(vb)))
+    torch.cuda.synchronize()
+    # two bf16 implementations against each other: each carries its own P and output roundings, so the relative L2
+    # bar is sqrt(2) times the one against the oracle
+    assert_close(fused, (plain.astype(np.uint32) << 16).view(np.float32), what="fused vs plain", rel=4.3e-3)

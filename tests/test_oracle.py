@@ -207,6 +207,17 @@ def _rope_pins() -> dict:
                           tb=np.sin(ang).astype(np.float32), eps=eps).astype(np.float64)
     pn = lambda y: (y.reshape(S, H, 64, 2) ** 2).sum(-1)  # noqa: E731
     res["pair_norms"] = np.abs(pn(got) - pn(n)).max() < 1e-5
+    # round_norm (rms_rope.cu:143-150): without a table every output is a bf16 value; with one, the result is the
+    # numpy brute force that rounds the normalised value (fp64 -> fp32 -> bf16 RNE) before rotating
+    y = oracle.rms_rope(x, w, eps=eps, round_norm=True)
+    res["round_norm_on_bf16_grid"] = bool(np.all((y.view(np.uint32) & 0xFFFF) == 0))
+    ang = _angles(S, 64, 6)
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    for pairing in (PAIR_INTERLEAVED, PAIR_SPLIT_HALF):
+        got = oracle.rms_rope(x, w, table_kind=TABLE_COSSIN_F32, ta=c, tb=s, pairing=pairing, eps=eps,
+                              round_norm=True)
+        ref = oracle.brute_rms_rope(xf, w, cos=c, sin=s, pairing=pairing, eps=eps, round_norm=True)
+        res[f"round_norm_brute_{pairing}"] = np.abs(got - ref).max() < 1e-6
     return res
 
 
@@ -258,9 +269,35 @@ def test_fused_is_the_composition():
     assert np.abs(fast - got).max() < 2e-5
 
 
+def _joint_round_pin() -> dict:
+    """round_prepared == the composition rms_rope -> bf16 (numpy's own RNE) -> fp64 attention (torch SDPA)."""
+    Sq, Sk, H, HK = 24, 30, 2, 1
+    q = oracle.synth_bf16(12, 1, (Sq, H, 128))
+    k = oracle.synth_bf16(12, 2, (Sk, HK, 128))
+    v = oracle.synth_bf16(12, 3, (Sk, HK, 128))
+    ang = _angles(max(Sq, Sk), 64, 7)
+    c, s_ = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    got = oracle.joint_attention(q, k, v, table_kind=TABLE_COSSIN_F32, qa=c[:Sq], qb=s_[:Sq], ka=c[:Sk], kb=s_[:Sk],
+                                 round_prepared=True)
+
+    def rne(x):
+        b = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+        return (((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+
+    qh = rne(oracle.rms_rope(q, None, table_kind=TABLE_COSSIN_F32, ta=c[:Sq], tb=s_[:Sq]))
+    kh = rne(oracle.rms_rope(k, None, table_kind=TABLE_COSSIN_F32, ta=c[:Sk], tb=s_[:Sk]))
+    ref = _sdpa(qh, kh, oracle.bf16_to_f32(v))
+    return {"joint_round_prepared": bool(np.abs(got - ref).max() < 2e-6)}
+
+
+def test_joint_round_prepared_pin():
+    assert all(_joint_round_pin().values())
+
+
 # ------------------------------------------------------------------------------------------ planted mistakes
 def _all_pins() -> dict:
     res = {}
+    res.update(_joint_round_pin())
     for i, c in enumerate(CASES):
         for kk, vv in _attn_pins(c).items():
             if kk != "flash_f32" and kk != "brute":   # the brute force is numpy's: it does not see the mutant
