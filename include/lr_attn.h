@@ -6,8 +6,9 @@
  *   0 (hipSuccess)             the work was launched;
  *   1 (hipErrorInvalidValue)   an argument was rejected before anything was launched;
  *   any other value            what the HIP runtime reported for the launch.
- * No entry point synchronises, allocates, sets function attributes or keeps mutable global state, so every call
- * may be captured into a HIP graph and may run concurrently on different streams. The caller owns every buffer.
+ * No entry point synchronises, allocates or sets function attributes, so every call may be captured into a HIP graph.
+ * Apart from lr_joint_attention_fused_noalloc (one static scratch array per GPU) none keeps mutable global state, and
+ * calls on buffers of their own may run concurrently on different streams. The caller owns every buffer.
  *
  * Tensors are bf16 "rows": token-major, heads contiguous, head h of token i at base + i*row_stride + h*128
  * (strides in ELEMENTS). Head dim is 128. Base pointers and row strides must be 16-byte aligned
@@ -220,6 +221,26 @@ int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void
                                 int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
                                 int64_t out_row_stride, int n_pre, void* workspace, size_t workspace_bytes, int config,
                                 lr_stream_t stream);
+
+/*
+ * lr_joint_attention_fused without a workspace argument, for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The tile images live in a
+ * static device array of LR_JOINT_NOALLOC_SCRATCH_BYTES per GPU (held from the library's first use on that GPU until
+ * the process ends), so the call allocates nothing: calls with 2 * HK * ceil(Sk/64) * 16384 bytes of images beyond
+ * it return hipErrorOutOfMemory (2) before launching anything (e.g. HK 24: Sk <= 5440). Every call on one GPU uses
+ * that GPU's one array: calls that overlap on a GPU (two streams, two threads) race and must be serialised by the
+ * caller; the array keeps the last call's images, which the next call overwrites before reading. lr_attn_init sets up
+ * the array's address on the current device (else the first call does). Arguments and results as
+ * lr_joint_attention_fused.
+ */
+#define LR_JOINT_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int lr_joint_attention_fused_noalloc(const void* q_raw, const void* k_raw, const void* v, void* out,
+                                     const float* q_norm_w, const float* k_norm_w, int table_kind,
+                                     const void* q_table_a, const void* q_table_b, const void* k_table_a,
+                                     const void* k_table_b, int64_t table_row_stride, int pairing, int rot_dim,
+                                     float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
+                                     int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                                     int64_t out_row_stride, int n_pre, lr_stream_t stream);
 
 /*
  * MiniMax H3's INT8 attention (the reference's comfy-kitchen SageAttention chain): per kv head a K anchor, Q and K

@@ -5,6 +5,9 @@
 #include <math.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "../../include/lr_attn.h"
 #include "lr_common.h"
 #include "lr_int8.h"
@@ -347,6 +350,34 @@ int i8_attention_impl(const void* q, const void* k, const void* v, void* out, vo
     return i8_kernel_impl(out, ws, B, H, HK, Sq, Sk, D, scale, o_rows, stream);
 }
 
+// ------------------------------------------------------------------------------------------------ no-alloc scratch
+// The scratch of lr_joint_attention_fused_noalloc: a file-scope device array (each GPU the library runs on holds its
+// own copy until the process ends). Host code never uses the array's name as an address: the per-device address
+// comes from hipGetSymbolAddress once per device (at lr_attn_init, else the entry point's first call on the device).
+static __device__ __align__(256) uint8_t scratch[LR_JOINT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::atomic<void*> g_scratch_ptr[MAX_DEVICES];
+std::mutex g_scratch_mutex;
+
+// The current device's scratch address (set up on first use); nullptr and *err set when the device cannot be used.
+void* device_scratch(int* err) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) { *err = (int)e; return nullptr; }
+    if (dev < 0 || dev >= MAX_DEVICES) { *err = (int)hipErrorInvalidDevice; return nullptr; }
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p) return p;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) { *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol; return nullptr; }
+        g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -360,7 +391,9 @@ int lr_attn_init(void) {
     hipDeviceProp_t prop;
     e = hipGetDeviceProperties(&prop, dev);
     if (e != hipSuccess) return (int)e;
-    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 0 : (int)hipErrorInvalidDevice;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return (int)hipErrorInvalidDevice;
+    int err = 0;
+    return device_scratch(&err) ? 0 : err;   // the no-alloc entry point's scratch address on this device
 }
 
 int lr_attention_bf16(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK, int nkeys,
@@ -522,6 +555,25 @@ int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void
     return fused_impl(q_raw, k_raw, v, out, q_norm_w, k_norm_w, table_kind, q_table_a, q_table_b, k_table_a, k_table_b,
                       table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale, q_row_stride,
                       k_row_stride, v_row_stride, out_row_stride, n_pre, workspace, workspace_bytes, config, stream);
+}
+
+int lr_joint_attention_fused_noalloc(const void* q_raw, const void* k_raw, const void* v, void* out,
+                                     const float* q_norm_w, const float* k_norm_w, int table_kind,
+                                     const void* q_table_a, const void* q_table_b, const void* k_table_a,
+                                     const void* k_table_b, int64_t table_row_stride, int pairing, int rot_dim,
+                                     float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
+                                     int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                                     int64_t out_row_stride, int n_pre, lr_stream_t stream) {
+    if (Sk < 1 || HK < 1) return ERR_ARGS;
+    const size_t need = ws_bytes_needed(Sk, HK);
+    if (need > (size_t)LR_JOINT_NOALLOC_SCRATCH_BYTES) return (int)hipErrorOutOfMemory;
+    int err = 0;
+    void* ws = device_scratch(&err);
+    if (!ws) return err;
+    return fused_impl(q_raw, k_raw, v, out, q_norm_w, k_norm_w, table_kind, q_table_a, q_table_b, k_table_a, k_table_b,
+                      table_row_stride, pairing, rot_dim, eps, Sq, Sk, H, HK, p0, causal, scale, q_row_stride,
+                      k_row_stride, v_row_stride, out_row_stride, n_pre, ws, need, LR_ATTN_CFG_AUTO,
+                      reinterpret_cast<hipStream_t>(stream));
 }
 
 size_t lr_int8_attention_workspace_bytes(int B, int H, int HK, int Sq, int Sk, int D) {
