@@ -41,7 +41,7 @@ extern "C" {
 /* hipStream_t without pulling in the HIP headers: an opaque pointer (NULL = the default stream). */
 typedef struct ihipStream_t* lr_stream_t;
 
-#define LR_ATTN_ABI_VERSION 6
+#define LR_ATTN_ABI_VERSION 7
 #define LR_HEAD_DIM 128
 
 /* RoPE table kinds: how rotation coefficients are stored per token row, per pair p < rot_dim/2. */
@@ -148,9 +148,14 @@ int lr_rms_rope_qk_bf16(void* q, void* k, int64_t seq, int heads, int64_t q_row_
                         const void* q_norm, const void* k_norm, const void* freqs, int64_t freqs_row_stride,
                         int rot_dim, float eps, lr_stream_t stream);
 
+/* The part of the joint attention's workspace behind the tile images: the partial results and arrival counters of
+ * query blocks cut over several workgroups (the last, partial round of blocks is spread over all CUs; at most 256
+ * workgroups, two partials of 8 x 16.5 KB each, then 256 int counters). */
+#define LR_JOINT_SPLIT_BYTES ((size_t)69207040)
+
 /* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys, then the values, each as
  * [HK][ceil(Sk/64)] tile images of 16 KB (one 64-key tile of one kv head laid out as the attention kernel's LDS holds
- * it; keys past Sk zero): 2 * HK * ceil(Sk/64) * 16384. */
+ * it; keys past Sk zero), then LR_JOINT_SPLIT_BYTES: 2 * HK * ceil(Sk/64) * 16384 + LR_JOINT_SPLIT_BYTES. */
 size_t lr_joint_attention_workspace_bytes(int Sk, int HK);
 
 /*
@@ -180,8 +185,10 @@ int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v
  *                               copied, and the values, into the workspace's tile images;
  *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated into out's rows first) over
  *                               that workspace. config: LR_ATTN_CFG_AUTO or _STREAM_W8.
- * Useful when keys and values are reused (a cached prefix) or to time the stages separately. The attention call only
- * reads the workspace, so several calls may share one prepared workspace.
+ * Useful when keys and values are reused (a cached prefix) or to time the stages separately. Several attention calls
+ * may share one prepared workspace (its images are only read), one after the other: each call also uses the
+ * workspace's split area (LR_JOINT_SPLIT_BYTES, left zeroed for the next call), so calls that overlap in time on one
+ * workspace race.
  */
 int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,
                         const float* k_norm_w, int table_kind, const void* k_table_a, const void* k_table_b,
@@ -224,16 +231,16 @@ int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void
 
 /*
  * lr_joint_attention_fused without a workspace argument, for callers that cannot allocate (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The tile images live in a
- * static device array of LR_JOINT_NOALLOC_SCRATCH_BYTES per GPU (held from the library's first use on that GPU until
- * the process ends), so the call allocates nothing: calls with 2 * HK * ceil(Sk/64) * 16384 bytes of images beyond
- * it return hipErrorOutOfMemory (2) before launching anything (e.g. HK 24: Sk <= 5440). Every call on one GPU uses
- * that GPU's one array: calls that overlap on a GPU (two streams, two threads) race and must be serialised by the
- * caller; the array keeps the last call's images, which the next call overwrites before reading. lr_attn_init sets up
- * the array's address on the current device (else the first call does). Arguments and results as
- * lr_joint_attention_fused.
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The workspace (tile images
+ * and split area) lives in a static device array of LR_JOINT_NOALLOC_SCRATCH_BYTES per GPU (held from the library's
+ * first use on that GPU until the process ends), so the call allocates nothing: calls with 2 * HK * ceil(Sk/64) *
+ * 16384 bytes of images beyond 64 MiB return hipErrorOutOfMemory (2) before launching anything (e.g. HK 24:
+ * Sk <= 5440). Every call on one GPU uses that GPU's one array: calls that overlap on a GPU (two streams, two threads)
+ * race and must be serialised by the caller; the array keeps the last call's images, which the next call overwrites
+ * before reading, and its split area is left zeroed by each call. lr_attn_init sets up the array's address on the
+ * current device (else the first call does). Arguments and results as lr_joint_attention_fused.
  */
-#define LR_JOINT_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+#define LR_JOINT_NOALLOC_SCRATCH_BYTES (((size_t)64 << 20) + LR_JOINT_SPLIT_BYTES)
 int lr_joint_attention_fused_noalloc(const void* q_raw, const void* k_raw, const void* v, void* out,
                                      const float* q_norm_w, const float* k_norm_w, int table_kind,
                                      const void* q_table_a, const void* q_table_b, const void* k_table_a,

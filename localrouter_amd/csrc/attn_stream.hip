@@ -49,8 +49,13 @@ constexpr int RING = 4;           // stages of each LDS ring
 constexpr int RA = 3;             // fragments read ahead
 constexpr int FR = 4;             // fragment ring entries
 constexpr int WQ = IMG_TILE_BYTES / SW;   // bytes of a tile each wave loads
-constexpr int REDO_WORDS = 32;            // per wave: a bit per block of the workgroup, for exact recomputation
-constexpr int MAX_WG_BLOCKS = 32 * REDO_WORDS;   // blocks one workgroup may walk (launch_stream splits larger calls)
+constexpr int MAX_WG_BLOCKS = 1024;      // whole blocks one workgroup may walk (launch_stream splits larger calls)
+constexpr int REDO_WORDS = (MAX_WG_BLOCKS + 2 + 31) / 32;   // per wave: a bit per work item, for exact recomputation
+constexpr int PMAX = 4;                   // pieces a cut block is split into at most
+// one wave's partial of a cut block: its O^T registers (64 fp32 x 64 lanes, as 16 groups of 4 registers, 1 KB per
+// group) and (m, l) per lane
+constexpr int SLOT_WAVE_BYTES = 64 * 64 * 4 + 64 * 8;
+static_assert(SW * SLOT_WAVE_BYTES == STREAM_SLOT_BYTES, "partial slot size");
 
 // S = K Q^T with the accumulator starting at 0 / at c, and S += K Q^T: scores in VGPRs (the VALU reads them), Q in
 // AGPRs. Inline asm, so the compiler cannot move the 64 Q registers into VGPRs; every VALU read of a result below is
@@ -98,10 +103,6 @@ struct IntTag {
 
 typedef __attribute__((address_space(3))) const bf16x8 lds_frag;
 __device__ __forceinline__ bf16x8 frag_at(uint32_t addr) { return *(lds_frag*)(uintptr_t)addr; }
-
-struct BlockInfo {
-    int head, hk, row0, tiles;
-};
 
 // Recompute wave `wave`'s 32 queries of a block with the exact row maximum (the rare case of a non-finite row under the
 // fixed reference): pass 1 takes the maximum of every score, pass 2 accumulates P = exp2(S - max) <= 1, the row sums and
@@ -180,8 +181,12 @@ __device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, 
 __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_stream_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t Kr[RING * IMG_TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t Vr[RING * IMG_TILE_BYTES];
-    // per wave: bit i set = the wave's rows of the workgroup's i-th block must be recomputed exactly
+    // per wave: bit n set = the wave's rows of the workgroup's n-th work item must be recomputed exactly
     __shared__ uint32_t redo_bits[SW][REDO_WORDS];
+    __shared__ int arrival;   // a cut block's arrival count before this workgroup's piece, broadcast to the waves
+    // this workgroup's tail pieces (at most two): head, row0, t0, t1, tail block, pieces of the block, index of this
+    // piece, then the partial slot of every piece of the block
+    __shared__ int tailtab[2][8 + PMAX];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -190,46 +195,111 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     // XCD-aware order: hardware workgroup b runs on XCD b % 8; each XCD takes a contiguous range of logical ids, so
     // the blocks it runs at any time are consecutive query blocks of one or two heads (their K/V stay in its L2)
     const int nwg = gridDim.x, b = blockIdx.x;
-    const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7, idx = b >> 3;
-    const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int per = nwg >> 3, rem8 = nwg & 7, xcd = b & 7, idx = b >> 3;
+    const int logical = xcd < rem8 ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
     const int nqb = (a.W + SBM - 1) / SBM;
     const int nblk = nqb * a.H;
-    if (logical >= nblk) return;
     const int T = (a.nkeys + IMG_TILE_KEYS - 1) / IMG_TILE_KEYS;
     const uint64_t head_bytes = (uint64_t)T * IMG_TILE_BYTES;
 
-    auto info_of = [&](int blk) __attribute__((always_inline)) {
-        BlockInfo bi;
-        bi.head = blk / nqb;
-        bi.hk = bi.head / a.G;
-        bi.row0 = (blk - bi.head * nqb) * SBM;
-        bi.tiles = T;
-        if (a.causal) bi.tiles = min(T, (a.p0 + min(bi.row0 + SBM, a.W) - 1) / IMG_TILE_KEYS + 1);
-        return bi;
+    // ---- the work of this workgroup. Whole blocks: logical, logical + nwg, ... below nwhole. With a.split, the
+    // blocks from nwhole on (fewer than nwg, the "tail") are laid end to end as U = rem * T key tiles, and tail
+    // workgroup L < a.tail_wg takes tiles [L U / tail_wg, (L + 1) U / tail_wg): at most two pieces, the end of one
+    // block and the start of the next. A cut block's pieces each leave a partial (O, m, l); the last to arrive
+    // merges them in piece order (deterministic) and writes the rows. A workgroup runs its tail pieces first and its
+    // whole blocks after them, so that the merges overlap other workgroups' work instead of ending the kernel.
+    const int nwhole = a.split ? (nblk / nwg) * nwg : nblk;
+    const int nt = a.split ? a.tail_wg : 0;
+    const int64_t U = (int64_t)(nblk - nwhole) * T;
+    const int n_whole = logical < nwhole ? (nwhole - 1 - logical) / nwg + 1 : 0;
+    int64_t u0 = 0, u1 = 0;
+    if (logical < nt) {
+        u0 = (int64_t)logical * U / nt;
+        u1 = (int64_t)(logical + 1) * U / nt;
+    }
+    const int n_pieces = u1 > u0 ? (int)((u1 - 1) / T - u0 / T + 1) : 0;
+    const int nitems = n_whole + n_pieces;
+    if (nitems == 0) return;
+    if (tid < n_pieces) {
+        // tail piece k = tid of this workgroup; tail workgroup owning tail tile u: ceil((u + 1) nt / U) - 1. 32-bit
+        // arithmetic when every product fits (the usual case), else 64-bit.
+        auto fill = [&](auto zero) {
+            using I = decltype(zero);
+            const I UU = (I)U, TT = (I)T, NT = (I)nt, uu0 = (I)u0, uu1 = (I)u1;
+            auto owner = [&](I u) { return (int)(((u + 1) * NT + UU - 1) / UU) - 1; };
+            const int k = tid;
+            const I i = uu0 / TT + (I)k;
+            const int blk = nwhole + (int)i;
+            const int head = blk / nqb;
+            const int lf = owner(i * TT), ll = owner((i + 1) * TT - 1);
+            int* e = tailtab[k];
+            e[0] = head;
+            e[1] = (blk - head * nqb) * SBM;
+            e[2] = k == 0 ? (int)(uu0 - i * TT) : 0;
+            e[3] = (int)(uu1 - i * TT < TT ? uu1 - i * TT : TT);
+            e[4] = (int)i;
+            e[5] = ll - lf + 1;
+            e[6] = logical - lf;
+            for (int j = 0; j < PMAX; ++j) {
+                const int wl = min(lf + j, ll);
+                e[8 + j] = 2 * wl + (i == ((I)wl * UU / NT) / TT ? 0 : 1);
+            }
+        };
+        if ((U + 1) * (int64_t)nt < ((int64_t)1 << 31)) fill(0u);
+        else fill((uint64_t)0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    block_barrier();
+
+    struct Item {
+        int head, hk, row0, t0, t1;
+        int tail;   // tail piece (0 or 1) of this workgroup; -1 for a block computed whole
+    };
+    auto item_of = [&](int it) __attribute__((always_inline)) {
+        Item r;
+        if (it >= n_pieces) {
+            const int blk = logical + (it - n_pieces) * nwg;
+            r.head = blk / nqb;
+            r.row0 = (blk - r.head * nqb) * SBM;
+            r.t0 = 0;
+            r.t1 = T;
+            r.tail = -1;
+        } else {
+            const int k = it;
+            r.head = __builtin_amdgcn_readfirstlane(tailtab[k][0]);
+            r.row0 = __builtin_amdgcn_readfirstlane(tailtab[k][1]);
+            r.t0 = __builtin_amdgcn_readfirstlane(tailtab[k][2]);
+            r.t1 = __builtin_amdgcn_readfirstlane(tailtab[k][3]);
+            r.tail = k;
+        }
+        r.hk = r.head / a.G;
+        if (a.causal) r.t1 = min(r.t1, (a.p0 + min(r.row0 + SBM, a.W) - 1) / IMG_TILE_KEYS + 1);
+        return r;
     };
 
     // ---- the tile stream: cursors of the next key / value tile to load (this wave's WQ bytes of it)
     struct Cursor {
-        int blk, t, tiles;
+        int it, t, t1;
         uint64_t addr;
     };
     const uint64_t kimg = (uint64_t)(uintptr_t)a.k, vimg = (uint64_t)(uintptr_t)a.v;
     auto cur_start = [&](uint64_t img) __attribute__((always_inline)) {
-        const BlockInfo bi = info_of(logical);
-        return Cursor{logical, 0, bi.tiles, img + (uint64_t)bi.hk * head_bytes + (uint64_t)wave * WQ};
+        const Item r = item_of(0);
+        return Cursor{0, r.t0, r.t1,
+                      img + (uint64_t)r.hk * head_bytes + (uint64_t)r.t0 * IMG_TILE_BYTES + (uint64_t)wave * WQ};
     };
-    // past the last tile of the last block the cursor stays put: its loads refill a free ring slot with a tile that is
+    // past the last tile of the last item the cursor stays put: its loads refill a free ring slot with a tile that is
     // never read
     auto cur_next = [&](Cursor& c, uint64_t img) __attribute__((always_inline)) {
-        if (c.t + 1 < c.tiles) {
+        if (c.t + 1 < c.t1) {
             ++c.t;
             c.addr += IMG_TILE_BYTES;
-        } else if (c.blk + nwg < nblk) {
-            c.blk += nwg;
-            const BlockInfo bi = info_of(c.blk);
-            c.t = 0;
-            c.tiles = bi.tiles;
-            c.addr = img + (uint64_t)bi.hk * head_bytes + (uint64_t)wave * WQ;
+        } else if (c.it + 1 < nitems) {
+            ++c.it;
+            const Item r = item_of(c.it);
+            c.t = r.t0;
+            c.t1 = r.t1;
+            c.addr = img + (uint64_t)r.hk * head_bytes + (uint64_t)r.t0 * IMG_TILE_BYTES + (uint64_t)wave * WQ;
         }
     };
     const uint32_t voff = (uint32_t)lane * 16u;
@@ -249,7 +319,8 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     f32x16 o[4];       // O^T accumulators, per 32-dim block
     f32x16 s[2];       // scores, per half-tile parity
     u32x4 p[2][2];     // P, [half-tile parity][16-key step of the half-tile]
-    f32x16 negm;       // -m in every slot: the initial accumulator of the score MFMAs
+    f32x16 negm;       // -m / c in every slot: the initial accumulator of the score MFMAs
+    float mref = 0.0f; // m: the item's fixed softmax reference of this lane's query (exp2 domain)
     float ls = 0.0f;   // this lane's partial row sum (its 8 keys of every 16-key step)
     bf16x8 fr[FR];     // fragment ring
     const uint32_t lane16 = (uint32_t)lane * 16u;
@@ -319,17 +390,17 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     const BoolTag<true> yes{};
     const BoolTag<false> no{};
 
-    // ---- per-block state
-    int blk = logical;
-    BlockInfo cur = info_of(blk);
+    // ---- per-item state
+    int item = 0;
+    Item cur = item_of(0);
     int g = 0;   // stream position of the current step (tile)
 
-    // ---- the queries of block bi (prepared rows: normalised, rotated and scaled by scale * log2 e, a.q with row
-    // stride a.q_rs): this wave's 32 rows as the 8 B-operand fragments, loaded straight into the AGPRs. The loads are
-    // asynchronous; LR_WAIT_Q(N) waits for them with N younger memory operations still in flight.
-    auto load_q = [&](const BlockInfo& bi) __attribute__((always_inline)) {
-        const int qrow = min(bi.row0 + wave * 32 + n, a.W - 1);
-        const uint16_t* src = a.q + (int64_t)qrow * a.q_rs + bi.head * D + 8 * hf;
+    // ---- the queries of item r (prepared rows: normalised and rotated as the reference's rope writes them, a.q with
+    // row stride a.q_rs): this wave's 32 rows as the 8 B-operand fragments, loaded straight into the AGPRs. The loads
+    // are asynchronous; LR_WAIT_Q(N) waits for them with N younger memory operations still in flight.
+    auto load_q = [&](const Item& r) __attribute__((always_inline)) {
+        const int qrow = min(r.row0 + wave * 32 + n, a.W - 1);
+        const uint16_t* src = a.q + (int64_t)qrow * a.q_rs + r.head * D + 8 * hf;
         asm volatile(
             "global_load_dwordx4 %0, %8, off\n\t"
             "global_load_dwordx4 %1, %8, off offset:32\n\t"
@@ -348,10 +419,10 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
                  : "+a"(qa[0]), "+a"(qa[1]), "+a"(qa[2]), "+a"(qa[3]), "+a"(qa[4]), "+a"(qa[5]), "+a"(qa[6]),   \
                    "+a"(qa[7])::"memory")
 
-    // ---- stream start: the first block's queries, K(0..2), V(0..1); the queries, K(0) and K(1) resident before
+    // ---- stream start: the first item's queries, K(0..2), V(0..1); the queries, K(0) and K(1) resident before
     // step 0
     Cursor kc = cur_start(kimg), vc = cur_start(vimg);
-    if (lane < REDO_WORDS) redo_bits[wave][lane] = 0u;
+    for (int x = lane; x < REDO_WORDS; x += 64) redo_bits[wave][x] = 0u;
     load_q(cur);
     load_k(kc, 0);
     load_k(kc, 1);
@@ -361,11 +432,10 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     LR_WAIT_Q(6);
     block_barrier();
 
-
-    // S(0) of a block: the first half-tile's scores from key fragments 0-7 of slot kslot, accumulator at 0; then the
-    // fixed reference m = ceil(max), S(0) -= m, negm, O = 0, row sum 0
-    auto first_scores = [&](const BlockInfo& bi, uint32_t kslot) __attribute__((always_inline)) {
-        const int wrow0 = bi.row0 + wave * 32;
+    // S(t0) of an item: the first half-tile's scores from key fragments 0-7 of slot kslot, accumulator at 0; then the
+    // fixed reference m = ceil(max), S -= m / c, negm, O = 0, row sum 0
+    auto first_scores = [&](const Item& r, uint32_t kslot) __attribute__((always_inline)) {
+        const int wrow0 = r.row0 + wave * 32;
         uint32_t kb0 = kslot + lane16;
         asm volatile("" : "+v"(kb0));   // opaque: offsets stay immediates, nothing is precomputed across the loop
 #pragma unroll
@@ -375,15 +445,16 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
             else qk_acc(s[0], kf, qa[ks]);
         }
         fence_s(s[0]);
-        if (mask_from(wrow0) <= 0) mask_half(s[0], 0, wrow0);
+        if (2 * r.t0 >= mask_from(wrow0)) mask_half(s[0], 2 * r.t0, wrow0);
         float mx = s[0][0];
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
+        for (int q = 1; q < 16; ++q) mx = fmaxf(mx, s[0][q]);
         mx = wave_pair_max(mx);
         // m in the exp2 domain, held as m / c in score units: the MFMAs then leave S - m / c, and P = exp2(c (S - m / c))
         // (an error of m / c's rounding shifts every exponent of the row alike, which the normalisation cancels)
         const float m = mx > -INFINITY ? ceilf(mx * c) : 0.0f;
         const float mc = m / c;
+        mref = m;
         negm = f32x16{} - mc;
         s[0] -= mc;
         ls = 0.0f;
@@ -392,23 +463,23 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
         asm volatile(LR_NOP48 : "+v"(negm));
     };
 
-    // the output rows of block bi from this wave's 16 packed words (32-dim block db = i >> 2, dims 8 (i & 3) + 4 hf ..
+    // the output rows of item r from this wave's 16 packed words (32-dim block db = i >> 2, dims 8 (i & 3) + 4 hf ..
     // +3): 16 buffer stores, always issued (rows at or past W fall outside the buffer range and are dropped), so that
-    // the number of memory operations after the next block's query loads is fixed
-    auto store_rows = [&](const BlockInfo& bi, const u32x2 (&w)[16]) __attribute__((always_inline)) {
-        const int nrows = min(a.W - bi.row0, SBM);
-        const uint32_t nrec = (uint32_t)((int64_t)nrows * a.o_rs * 2 - (int64_t)bi.head * D * 2);
+    // the number of memory operations after the next item's query loads is fixed
+    auto store_rows = [&](const Item& r, const u32x2 (&w)[16]) __attribute__((always_inline)) {
+        const int nrows = min(a.W - r.row0, SBM);
+        const uint32_t nrec = (uint32_t)((int64_t)nrows * a.o_rs * 2 - (int64_t)r.head * D * 2);
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            a.out + (int64_t)bi.row0 * a.o_rs + bi.head * D, 0, (int)nrec, 0x00020000);
-        const uint32_t vo = (uint32_t)((wave * 32 + n) * a.o_rs * 2 + 8 * hf);
+            a.out + (int64_t)r.row0 * a.o_rs + r.head * D, 0, (int)nrec, 0x00020000);
+        uint32_t vo = (uint32_t)((wave * 32 + n) * a.o_rs * 2 + 8 * hf);
+        asm volatile("" : "+v"(vo));   // computed here, the store offsets stay immediates
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             __builtin_amdgcn_raw_buffer_store_b64(w[i], rs, (int)(vo + 2 * (32 * (i >> 2) + 8 * (i & 3))), 0, 0);
     };
     // O / l of this wave's rows as packed bf16 words; returns true when a row is not finite (l >= 1/2 for every row,
     // the first half-tile's maximum has P >= 1/2, so only overflow makes one)
-    auto pack_rows = [&](u32x2 (&w)[16]) __attribute__((always_inline)) {
-        const float l = wave_pair_sum(ls);
+    auto pack_rows = [&](u32x2 (&w)[16], float l) __attribute__((always_inline)) {
         const float inv = 1.0f / l;
         float nan0 = 0.0f * l, nan1 = 0.0f, nan2 = 0.0f, nan3 = 0.0f;   // NaN iff some value is not finite
 #pragma unroll
@@ -426,30 +497,123 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
             }
         return (nan0 + nan1 + nan2 + nan3) != 0.0f;
     };
-
-    // epilogue of block bi (logical id bi_blk): O / l to bf16 rows. A wave with a non-finite row stores nothing and
-    // marks the block; after the streaming loop it recomputes those rows exactly (its rows still hold the prepared
-    // queries when they are the output rows).
-    auto epilogue = [&](const BlockInfo& bi, int bi_blk) __attribute__((always_inline)) {
-        const int wrow0 = bi.row0 + wave * 32;
+    // rows of item r (O / l) out; a wave with a non-finite row stores nothing and marks item it: after the streaming
+    // loop it recomputes those rows exactly (its rows still hold the prepared queries when they are the output rows)
+    auto write_rows = [&](const Item& r, int it, float l) __attribute__((always_inline)) {
+        const int wrow0 = r.row0 + wave * 32;
         u32x2 w[16];
-        const bool bad = pack_rows(w) && wrow0 + n < a.W;
+        const bool bad = pack_rows(w, l) && wrow0 + n < a.W;
         if (__builtin_amdgcn_ballot_w64(bad)) {
-            if (lane == 0) {
-                const int i = (bi_blk - logical) / nwg;
-                redo_bits[wave][i >> 5] |= 1u << (i & 31);
-            }
+            if (lane == 0) redo_bits[wave][it >> 5] |= 1u << (it & 31);
         } else {
-            store_rows(bi, w);
+            store_rows(r, w);
         }
     };
 
-    // The end of a block (in the boundary step, V(g - 1) its last value tile): P of its last half-tile (S buffer 1)
+    // a piece of a cut block: its partial out (sc1: coherent at device scope, not kept in this XCD's L2), then the
+    // block's arrival count; the last piece to arrive reads the others' partials and writes the rows
+    auto finish_piece = [&](const Item& r, int it) __attribute__((always_inline)) {
+        const int* e = tailtab[r.tail];
+        const int i = __builtin_amdgcn_readfirstlane(e[4]);
+        const int np = __builtin_amdgcn_readfirstlane(e[5]);
+        const float l = wave_pair_sum(ls);
+        if (np == 1) {   // the whole block in one piece
+            write_rows(r, it, l);
+            return;
+        }
+        auto slot_rsrc = [&](int slot) __attribute__((always_inline)) {
+            uint8_t* base = static_cast<uint8_t*>(a.part) + (int64_t)slot * STREAM_SLOT_BYTES + wave * SLOT_WAVE_BYTES;
+            return __builtin_amdgcn_make_buffer_rsrc(base, 0, SLOT_WAVE_BYTES, 0x00020000);
+        };
+        {
+            const __amdgpu_buffer_rsrc_t rs = slot_rsrc(__builtin_amdgcn_readfirstlane(e[8 + e[6]]));
+#pragma unroll
+            for (int gi = 0; gi < 16; ++gi) {
+                f32x4 x;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[e] = o[gi >> 2][4 * (gi & 3) + e];
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rs, (gi * 64 + lane) * 16, 0, 16);
+            }
+            u32x2 ml;
+            ml[0] = __float_as_uint(mref);
+            ml[1] = __float_as_uint(l);
+            __builtin_amdgcn_raw_buffer_store_b64(ml, rs, 64 * 64 * 4 + lane * 8, 0, 16);
+        }
+        LR_WAIT_VMCNT(0);
+        block_barrier();   // every wave's partial is complete before the arrival is counted
+        if (tid == 0) {
+            arrival = __hip_atomic_fetch_add(a.cnt + i, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        block_barrier();
+        if (__builtin_amdgcn_readfirstlane(arrival) != np - 1) return;
+        if (tid == 0) __hip_atomic_store(a.cnt + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // merge, in piece order: the weights 2^(m_j - M), then O and l as their weighted sums
+        const int mine = __builtin_amdgcn_readfirstlane(e[6]);
+        int slot_of[PMAX];
+        float mj[PMAX], lj[PMAX];
+        float mmax = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < PMAX; ++j) {
+            slot_of[j] = __builtin_amdgcn_readfirstlane(e[8 + j]);
+            mj[j] = -INFINITY;
+            lj[j] = 0.0f;
+            if (j < np) {
+                if (j == mine) {
+                    mj[j] = mref;
+                    lj[j] = l;
+                } else {
+                    const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(slot_rsrc(slot_of[j]), 64 * 64 * 4 + lane * 8,
+                                                                          0, 16);
+                    mj[j] = __uint_as_float(ml[0]);
+                    lj[j] = __uint_as_float(ml[1]);
+                }
+                mmax = fmaxf(mmax, mj[j]);
+            }
+        }
+        float lsum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PMAX; ++j) {
+            mj[j] = j < np ? __builtin_amdgcn_exp2f(mj[j] - mmax) : 0.0f;
+            lsum += mj[j] * lj[j];
+        }
+        f32x4 acc[16];
+#pragma unroll
+        for (int gi = 0; gi < 16; ++gi) acc[gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < PMAX; ++j) {
+            if (j < np) {
+                f32x4 x[16];
+                if (j == mine) {
+#pragma unroll
+                    for (int gi = 0; gi < 16; ++gi)
+#pragma unroll
+                        for (int e2 = 0; e2 < 4; ++e2) x[gi][e2] = o[gi >> 2][4 * (gi & 3) + e2];
+                } else {   // one batch of 16 loads, then the products
+                    const __amdgpu_buffer_rsrc_t rs = slot_rsrc(slot_of[j]);
+#pragma unroll
+                    for (int gi = 0; gi < 16; ++gi)
+                        x[gi] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (gi * 64 + lane) * 16,
+                                                                                                0, 16));
+                }
+#pragma unroll
+                for (int gi = 0; gi < 16; ++gi) acc[gi] += mj[j] * x[gi];
+            }
+        }
+#pragma unroll
+        for (int gi = 0; gi < 16; ++gi)
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) o[gi >> 2][4 * (gi & 3) + e2] = acc[gi][e2];
+        LR_WAIT_VMCNT(0);
+        write_rows(r, it, lsum);
+    };
+
+    // The end of an item (in the boundary step, V(g - 1) its last value tile): P of its last half-tile (S buffer 1)
     // into P buffer 1 beside the P V products of the half-tile before (P buffer 0, value fragments 0-7), then the
-    // last P V products (P buffer 1, fragments 8-15), then the epilogue.
-    auto finish_block = [&](const BlockInfo& bi, int bi_blk, uint32_t vslot) __attribute__((always_inline)) {
-        const int wrow0 = bi.row0 + wave * 32;
-        if (2 * bi.tiles - 1 >= mask_from(wrow0)) mask_half(s[1], 2 * bi.tiles - 1, wrow0);
+    // last P V products (P buffer 1, fragments 8-15), then its rows (or its partial).
+    auto finish_item = [&](const Item& r, int it, uint32_t vslot) __attribute__((always_inline)) {
+        const int wrow0 = r.row0 + wave * 32;
+        if (2 * r.t1 - 1 >= mask_from(wrow0)) mask_half(s[1], 2 * r.t1 - 1, wrow0);
         uint32_t vb0 = vslot + lane16;
         asm volatile("" : "+v"(vb0));
         bf16x8 vf[4];
@@ -466,14 +630,15 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        epilogue(bi, bi_blk);
+        if (r.tail < 0) write_rows(r, it, wave_pair_sum(ls));
+        else finish_piece(r, it);
     };
 
     // a steady-state step over key tile g (both halves) and value tile g - 1. Fragment positions of the B half: 0-7
     // keys mb 0, 8-15 values mb 0, 16+ the A half's keys (mb 1); of the A half: 0-7 keys mb 1, 8-15 values mb 1, 16+
     // the next step's keys (mb 0).
-    auto step = [&](const BlockInfo& bi, int t) __attribute__((always_inline)) {
-        const int wrow0 = bi.row0 + wave * 32;
+    auto step = [&](const Item& r, int t) __attribute__((always_inline)) {
+        const int wrow0 = r.row0 + wave * 32;
         const int jm = mask_from(wrow0);
         // per-step fragment bases (opaque to the compiler, so that every fragment offset below stays an immediate)
         uint32_t kb = kr0 + (uint32_t)((g & (RING - 1)) * IMG_TILE_BYTES) + lane16;
@@ -502,21 +667,22 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
         block_barrier();
     };
 
-    // ---- the blocks of this workgroup
-    BlockInfo prev = cur;
+    // ---- the items of this workgroup
+    Item prev = cur;
     bool has_prev = false;
     for (;;) {
-        // boundary step g: the end of the previous block (value tile g - 1), the start of this one (key tile g)
+        // boundary step g: the end of the previous item (value tile g - 1), the start of this one (key tile g)
         const uint32_t kslot = kr0 + (uint32_t)((g & (RING - 1)) * IMG_TILE_BYTES);
         if (has_prev) {
             load_q(cur);   // prev's queries are dead: its last score MFMA ran in the step before
-            finish_block(prev, blk - nwg, vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES));
+            finish_item(prev, item - 1, vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES));
             LR_WAIT_Q(16);   // the 16 output stores of prev may still be in flight
         }
         first_scores(cur, kslot);
         load_k(kc, g + 3);
         load_v(vc, g + 2);
-        // the A half of step 0: S(1) from key fragments 8-15 into S buffer 1, P(0) from S buffer 0 into P buffer 0
+        // the A half of the item's first step: S(2 t0 + 1) from key fragments 8-15 into S buffer 1, P(2 t0) from S
+        // buffer 0 into P buffer 0
         {
             uint32_t kb = kslot + lane16;
             uint32_t kn = kr0 + (uint32_t)(((g + 1) & (RING - 1)) * IMG_TILE_BYTES) + lane16;
@@ -532,38 +698,49 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
         LR_WAIT_VMCNT(6);
         block_barrier();
         ++g;
-        for (int t = 1; t < cur.tiles; ++t) {
+        for (int t = cur.t0 + 1; t < cur.t1; ++t) {
             step(cur, t);
             ++g;
         }
         prev = cur;
         has_prev = true;
-        blk += nwg;
-        if (blk >= nblk) break;
-        cur = info_of(blk);
+        if (++item >= nitems) break;
+        cur = item_of(item);
     }
-    finish_block(prev, blk - nwg, vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES));
+    finish_item(prev, item - 1, vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES));
     LR_WAIT_VMCNT(0);   // no direct load is still writing LDS when the workgroup ends
 
-    // ---- the rare exact recomputation of the marked blocks
-    const int nall = (nblk - 1 - logical) / nwg + 1;
-    for (int wd = 0; wd < (nall + 31) / 32; ++wd) {
+    // ---- the rare exact recomputation of the marked items (a cut block: all of it, by the workgroup that merged it)
+    for (int wd = 0; wd < (nitems + 31) / 32; ++wd) {
         uint32_t bits = __builtin_amdgcn_readfirstlane(redo_bits[wave][wd]);
         while (bits) {
-            const int i = 32 * wd + __builtin_ctz(bits);
+            const int it = 32 * wd + __builtin_ctz(bits);
             bits &= bits - 1;
-            const BlockInfo bi = info_of(logical + i * nwg);
-            redo_exact(a, bi.head, bi.hk, bi.row0, bi.tiles, wave);
+            Item r = item_of(it);
+            if (a.causal) r.t1 = min(T, (a.p0 + min(r.row0 + SBM, a.W) - 1) / IMG_TILE_KEYS + 1);
+            else r.t1 = T;
+            redo_exact(a, r.head, r.hk, r.row0, r.t1, wave);
         }
     }
 }
 
 }  // namespace
 
+bool stream_split_params(int W, int H, int nkeys, int causal, int nwg, int* tail_wg) {
+    const int64_t nblk = (int64_t)((W + SBM - 1) / SBM) * H;
+    const int64_t rem = nblk % nwg;
+    const int64_t T = (nkeys + IMG_TILE_KEYS - 1) / IMG_TILE_KEYS;
+    // cut the tail when balancing it saves at least 4 key tiles per workgroup (a piece costs about a tile's time in
+    // partial traffic and its boundary step)
+    if (causal || rem == 0 || T * (nwg - rem) < 4 * (int64_t)nwg) return false;
+    *tail_wg = (int)std::min<int64_t>(std::min<int64_t>(nwg, rem * T), rem * (PMAX - 1));
+    return true;
+}
+
 hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream) {
-    if (a.W < 1 || a.H < 1 || nwg < 1) return hipErrorInvalidValue;
-    // at most MAX_WG_BLOCKS blocks per workgroup (its recomputation bits): larger calls run as several launches over
-    // consecutive query-row ranges (queries, outputs and, causal, the diagonal offset p0 shifted)
+    if (a.W < 1 || a.H < 1 || nwg < 1 || nwg > STREAM_MAX_WG) return hipErrorInvalidValue;
+    // at most MAX_WG_BLOCKS whole blocks per workgroup (its recomputation bits): larger calls run as several launches
+    // over consecutive query-row ranges (queries, outputs and, causal, the diagonal offset p0 shifted)
     const int64_t rows_per = (int64_t)SBM * std::max<int64_t>(1, (int64_t)MAX_WG_BLOCKS * nwg / a.H);
     for (int64_t r0 = 0; r0 < a.W; r0 += rows_per) {
         AttnArgs b = a;
@@ -573,7 +750,14 @@ hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream) {
         b.p0 = a.p0 + (int)r0;
         const int64_t blocks = (int64_t)((b.W + SBM - 1) / SBM) * b.H;
         if (blocks > (int64_t)MAX_WG_BLOCKS * nwg) return hipErrorInvalidValue;
-        const unsigned grid = (unsigned)std::min<int64_t>(blocks, nwg);
+        b.split = 0;
+        b.tail_wg = 0;
+        int tw = 0;
+        if (a.part && a.cnt && stream_split_params(b.W, b.H, b.nkeys, b.causal, nwg, &tw)) {
+            b.split = 1;
+            b.tail_wg = tw;
+        }
+        const unsigned grid = b.split ? (unsigned)nwg : (unsigned)std::min<int64_t>(blocks, nwg);
         hipLaunchKernelGGL(attn_stream_kernel, dim3(grid), dim3(SW * 64), 0, stream, b);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -42,6 +42,8 @@ __global__ __launch_bounds__(256) void kv_image_kernel(KvImageArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t img[2 * IMG_TILE_BYTES];   // keys, then values
     const int tid = threadIdx.x, c = tid & 15, g = tid >> 4;
     const int64_t tile_id = blockIdx.x;                // kv head * tiles + tile
+    if (tile_id == 0 && a.cnt)                         // the attention kernel's counters start each call at zero
+        for (int x = tid; x < a.ncnt; x += 256) a.cnt[x] = 0;
     const int hk = (int)(tile_id / a.tiles), t = (int)(tile_id - (int64_t)hk * a.tiles);
     const int key0 = t * IMG_TILE_KEYS;
 

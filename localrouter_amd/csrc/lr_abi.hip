@@ -97,8 +97,11 @@ bool table_ok(int kind, const void* ta, const void* tb, int64_t stride, int rot,
 }
 
 // Workspace of the fused op and of its two stages: the tile images of the keys, then those of the values
-// (tile_image.h), 16 KB per 64-key tile and kv head each.
-size_t ws_bytes_needed(int Sk, int HK) { return 2 * (size_t)lr::img_bytes(Sk, HK); }
+// (tile_image.h), 16 KB per 64-key tile and kv head each, then the streaming kernel's split area (partials of cut
+// query blocks, then their arrival counters).
+static_assert(lr::STREAM_PART_BYTES + lr::STREAM_CNT_BYTES == (int64_t)LR_JOINT_SPLIT_BYTES, "split area size");
+size_t ws_bytes_needed(int Sk, int HK) { return 2 * (size_t)lr::img_bytes(Sk, HK) + LR_JOINT_SPLIT_BYTES; }
+inline char* split_area(void* ws, int Sk, int HK) { return static_cast<char*>(ws) + 2 * lr::img_bytes(Sk, HK); }
 
 // the configurations of the fused and prepared calls (both the streaming kernel)
 inline bool is_stream(int config) { return config == LR_ATTN_CFG_AUTO || config == LR_ATTN_CFG_STREAM_W8; }
@@ -153,6 +156,8 @@ int kv_launch(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, cons
     r.tiles = lr::img_tiles(Sk);
     r.img_k = ws;
     r.img_v = static_cast<char*>(ws) + lr::img_bytes(Sk, HK);
+    r.cnt = reinterpret_cast<int*>(split_area(ws, Sk, HK) + lr::STREAM_PART_BYTES);
+    r.ncnt = lr::STREAM_MAX_WG;
     return (int)lr::launch_kv_image(r, stream);
 }
 
@@ -200,10 +205,12 @@ bool images_stage_ok(const void* q_prep, int64_t p_rs, const void* ws, size_t ws
     return !overlap(so, rows_span(q_prep, Sq, p_rs, H)) && !overlap(rows_span(q_prep, Sq, p_rs, H), ws_span(ws, Sk, HK));
 }
 
-// The attention stage (arguments checked): the persistent streaming kernel, one workgroup per CU.
+// The attention stage (arguments checked): the persistent streaming kernel, one workgroup per CU (at most
+// STREAM_MAX_WG), its last partial round of query blocks cut over all of them (partials and counters in the
+// workspace's split area).
 int images_launch(const void* q_prep, int64_t p_rs, const void* ws, void* out, int64_t o_rs, int Sq, int Sk, int H,
                   int HK, int p0, int causal, float scale, hipStream_t stream) {
-    const int cus = device_cus();
+    const int cus = std::min(device_cus(), lr::STREAM_MAX_WG);
     if (cus < 1) return (int)hipErrorInvalidDevice;
     lr::AttnArgs a{};
     a.q = static_cast<const uint16_t*>(q_prep);
@@ -214,6 +221,9 @@ int images_launch(const void* q_prep, int64_t p_rs, const void* ws, void* out, i
     a.k_hs = a.v_hs = lr::img_tiles(Sk) * (lr::IMG_TILE_BYTES / 2);
     a.W = Sq; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = Sk; a.p0 = p0; a.causal = causal;
     a.c = scale * 1.4426950408889634f;
+    char* split = split_area(const_cast<void*>(ws), Sk, HK);
+    a.part = split;
+    a.cnt = reinterpret_cast<int*>(split + lr::STREAM_PART_BYTES);
     return (int)lr::launch_stream(a, cus, stream);
 }
 
@@ -564,7 +574,7 @@ int lr_joint_attention_fused_noalloc(const void* q_raw, const void* k_raw, const
                                      float eps, int Sq, int Sk, int H, int HK, int p0, int causal, float scale,
                                      int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
                                      int64_t out_row_stride, int n_pre, lr_stream_t stream) {
-    if (Sk < 1 || HK < 1) return ERR_ARGS;
+    if (Sk < 1 || HK < 1 || Sk > INT_MAX - 512) return ERR_ARGS;
     const size_t need = ws_bytes_needed(Sk, HK);
     if (need > (size_t)LR_JOINT_NOALLOC_SCRATCH_BYTES) return (int)hipErrorOutOfMemory;
     int err = 0;

@@ -22,6 +22,12 @@ struct AttnArgs {
     int nsplit;
     float* part_o;
     float* part_ml;
+    // Persistent streaming kernel (attn_stream.hip) with split = 1: the blocks past the last whole round are cut over
+    // tail_wg workgroups; the pieces' partials go to `part` (2 slots of STREAM_SLOT_BYTES per workgroup) and their
+    // arrivals are counted in `cnt` (one int per cut block, zero between calls). Set by launch_stream.
+    int split, tail_wg;
+    void* part;
+    int* cnt;
 };
 
 // The per-(row, head) RMSNorm + RoPE pass.
@@ -77,6 +83,8 @@ struct KvImageArgs {
     int64_t tiles;        // ceil(Sk / 64)
     void* img_k;          // [HK][tiles] 16 KB key tiles
     void* img_v;          // [HK][tiles] 16 KB value tiles
+    int* cnt;             // the streaming kernel's arrival counters, zeroed by this launch (ncnt ints; null: none)
+    int ncnt;
 };
 hipError_t launch_kv_image(const KvImageArgs& a, hipStream_t stream);
 
@@ -84,6 +92,12 @@ hipError_t launch_kv_image(const KvImageArgs& a, hipStream_t stream);
 // a.q = prepared queries (normalised, rotated and multiplied by scale * log2 e, bf16 rows with stride a.q_rs; they may
 // be the rows of a.out, which each block reads before it overwrites them). nwg = workgroups (at most one per CU).
 // Non-causal and causal (p0) calls, any W, H, HK, nkeys.
+// a.part / a.cnt: the partial area and arrival counters of the workspace (null: whole blocks only); nwg <=
+// STREAM_MAX_WG.
 hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream);
+constexpr int STREAM_MAX_WG = 256;                                      // workgroups of one streaming launch at most
+constexpr int64_t STREAM_SLOT_BYTES = 8 * (64 * 64 * 4 + 64 * 8);        // one piece's partial: 8 waves' O, m and l
+constexpr int64_t STREAM_PART_BYTES = 2 * STREAM_MAX_WG * STREAM_SLOT_BYTES;
+constexpr int64_t STREAM_CNT_BYTES = 4 * STREAM_MAX_WG;                 // arrival counters (one per cut block)
 
 }  // namespace lr

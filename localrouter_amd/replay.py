@@ -103,8 +103,15 @@ def compare(got_bits: np.ndarray, want_bits: np.ndarray) -> tuple[bool, bool, fl
 def classify_mask(m: np.ndarray, B: int, N: int, S: int):
     """An SDPA mask (boolean, True keeps; or additive, 0 keeps) broadcast over [B, 1, N, S]: ("keys", keep [B, S])
     when every query row of a batch is the same (key padding), ("causal", None) when it is exactly lower-triangular
-    over N == S, else (None, None) (per-head or other masks)."""
-    m = m if m.dtype == np.bool_ else (m.astype(np.float32) == 0.0)
+    over N == S, else (None, None) (per-head or other masks). A bf16 additive mask arrives as its uint16 bits (as
+    load_ref returns it): +0.0 and -0.0 (0x8000, what (1 - keep) * -10000 gives for kept keys) both keep. A batch
+    that keeps no key (SDPA gives NaN rows there) is not replayed: (None, None)."""
+    if m.dtype == np.bool_:
+        pass
+    elif m.dtype == np.uint16:
+        m = (m & 0x7FFF) == 0
+    else:
+        m = m.astype(np.float32) == 0.0
     if m.ndim > 4:
         return None, None
     try:
@@ -112,7 +119,10 @@ def classify_mask(m: np.ndarray, B: int, N: int, S: int):
     except ValueError:
         return None, None
     if (m == m[:, :1, :]).all():
-        return "keys", np.ascontiguousarray(m[:, 0, :])
+        keep = np.ascontiguousarray(m[:, 0, :])
+        if not keep.any(axis=1).all():
+            return None, None
+        return "keys", keep
     if N == S and (m == np.tril(np.ones((N, S), bool))[None]).all():
         return "causal", None
     return None, None

@@ -32,24 +32,28 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version():
     header = _lib.HEADER.read_text()
     declared = int(re.search(r"#define LR_ATTN_ABI_VERSION (\d+)", header).group(1))
-    assert _lib.load().lr_attn_abi_version() == declared == 6
+    assert _lib.load().lr_attn_abi_version() == declared == 7
 
 
 def test_workspace_bytes():
     L = _lib.load()
-    # key tile images then value tile images, [HK][ceil(Sk/64)] x 16 KB each
-    assert L.lr_joint_attention_workspace_bytes(4608, 24) == 2 * 24 * 72 * 16384
-    assert L.lr_joint_attention_workspace_bytes(3, 1) == 2 * 16384
-    assert L.lr_joint_attention_workspace_bytes(65, 2) == 2 * 2 * 2 * 16384
-    assert ops.workspace_bytes(65, 2) == 2 * 2 * 2 * 16384
-    assert L.lr_joint_attention_workspace_bytes(0, 24) == 0
+    # key tile images then value tile images, [HK][ceil(Sk/64)] x 16 KB each, then the split area: two partial slots
+    # of 8 waves x (64 x 64 fp32 O + 64 x (m, l)) for each of at most 256 workgroups, then 256 int counters
     header = _lib.HEADER.read_text()
+    split = int(re.search(r"#define LR_JOINT_SPLIT_BYTES \(\(size_t\)(\d+)\)", header).group(1))
+    assert split == 2 * 256 * 8 * (64 * 64 * 4 + 64 * 8) + 4 * 256
+    assert L.lr_joint_attention_workspace_bytes(4608, 24) == 2 * 24 * 72 * 16384 + split
+    assert L.lr_joint_attention_workspace_bytes(3, 1) == 2 * 16384 + split
+    assert L.lr_joint_attention_workspace_bytes(65, 2) == 2 * 2 * 2 * 16384 + split
+    assert ops.workspace_bytes(65, 2) == 2 * 2 * 2 * 16384 + split
+    assert L.lr_joint_attention_workspace_bytes(0, 24) == 0
     assert "SK_AREA" not in header and "#define LR_ATTN_CFG_STREAM_W8 9" in header
 
 
 # fake, well-aligned device addresses: validation must reject before any HIP call is made
 A = 0x10000
 W = 0x100000   # a fake workspace address past every fake tensor
+SPLIT = 69207040   # LR_JOINT_SPLIT_BYTES
 
 
 @pytest.mark.parametrize("args,why", [
@@ -78,7 +82,7 @@ def test_attention_ex_rejects_bad_config():
 def _fused(**kw):
     a = dict(q=A, k=A, v=A, out=A, wq=None, wk=None, kind=1, qa=A, qb=A, ka=A, kb=A, ts=64, pairing=0, rot=128,
              eps=1e-6, Sq=8, Sk=8, H=2, HK=2, p0=0, causal=0, scale=0.088, qrs=256, krs=256, vrs=256, ors=256, n_pre=0,
-             ws=W, wsb=2 * 2 * 16384, config=0, stream=None)
+             ws=W, wsb=2 * 2 * 16384 + SPLIT, config=0, stream=None)
     a.update(kw)
     return _lib.load().lr_joint_attention_fused_ex(*a.values())
 
@@ -87,7 +91,8 @@ def _fused(**kw):
     (dict(ws=0), "no workspace"),
     (dict(ws=A + 16), "workspace not 256-aligned"),
     (dict(wsb=100), "workspace too small"),
-    (dict(wsb=2 * 16384), "workspace holds the key images but not the value images"),
+    (dict(wsb=2 * 16384 + SPLIT), "workspace short of the value images"),
+    (dict(wsb=2 * 2 * 16384), "workspace holds the images but not the split area"),
     (dict(ws=A + 256), "out overlaps the workspace"),
     (dict(out=A + 0x1000, k=A + 0x1000), "out overlaps k_raw"),
     (dict(out=A + 0x1000, v=A + 0x1100), "out overlaps v"),

@@ -51,3 +51,18 @@ def test_classify_mask():
     per_head = np.ones((1, 2, 3, 4), bool); per_head[0, 1, :, 0] = False           # heads differ
     assert replay.classify_mask(per_head, 1, 3, 4)[0] is None
 
+
+def test_classify_mask_bf16_bits():
+    """A bf16 additive mask arrives as uint16 bits: (1 - keep) * -10000 gives -0.0 (0x8000) for kept keys."""
+    keep = np.array([True, True, False, True])
+    add = ((1.0 - keep) * -10000.0).astype(np.float32)
+    assert np.signbit(add[keep]).all()                                              # kept keys are -0.0
+    bits = (add.view(np.uint32) >> 16).astype(np.uint16)[None, None, None, :]       # truncated to bf16
+    how, k = replay.classify_mask(bits, 1, 3, 4)
+    assert how == "keys" and np.array_equal(k, keep[None])
+    # a batch that keeps no key is not replayed (SDPA gives NaN rows)
+    none_kept = np.full((2, 1, 1, 4), 0xC61C, np.uint16)                            # bf16 -1e4 (truncated) everywhere ...
+    none_kept[0] = 0                                                                # ... but batch 0 keeps all
+    assert replay.classify_mask(none_kept, 2, 3, 4) == (None, None)
+    assert replay.classify_mask(np.zeros((1, 1, 3, 4), bool), 1, 3, 4) == (None, None)
+
