@@ -3,11 +3,11 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video|h3-int8|mmdit]
                     [--no-cpu-baseline]
 
-A step is one fused joint-attention call over one synthetic batch, made as the fused call's own three launches so that
-each is timed: keys RMSNorm + RoPE and values into the workspace's tile images (lr_joint_kv_prepare), queries
-RMSNorm + RoPE into the output rows (lr_joint_q_prepare), then the persistent streaming attention kernel over
-them (lr_joint_attention_images) -- together exactly what lr_joint_attention_fused launches. Inputs are resident in
-HBM before timing.
+A step is one fused joint-attention call over one synthetic batch, made as the fused call's own two launches so that
+each is timed: the preparation (lr_joint_prepare: keys RMSNorm + RoPE and values into the workspace's tile images,
+queries RMSNorm + RoPE into the output rows, one launch), then the persistent streaming attention kernel over them
+(lr_joint_attention_images) -- together exactly what lr_joint_attention_fused launches. Inputs are resident in HBM
+before timing.
 The default workload is BASELINE's Qwen-Image-style step: B=1, 24 heads x 128, 512 text + 4096 image tokens (64x64
 grid, 2D RoPE on image tokens, text un-rotated), non-causal, QK-RMSNorm eps 1e-6 with weights 1.0, scale f32(1/sqrt(128)).
 
@@ -202,56 +202,46 @@ def main():
     sh = stream.cuda_stream
     eps, scale, rs = 1e-6, ops.SCALE_128, H * 128
 
-    def keys():
-        _lib.call("lr_joint_kv_prepare", k.data_ptr(), rs, v.data_ptr(), rs, wk.data_ptr(), ops.TABLE_COSSIN_F32,
-                  cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, H, 0, ws.data_ptr(), ws_bytes,
-                  sh)
-
-    def queries():
-        _lib.call("lr_joint_q_prepare", q.data_ptr(), rs, out.data_ptr(), rs, wq.data_ptr(), ops.TABLE_COSSIN_F32,
-                  cos.data_ptr(), sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, H, sh)
+    def prepare():
+        _lib.call("lr_joint_prepare", q.data_ptr(), rs, out.data_ptr(), rs, k.data_ptr(), rs, v.data_ptr(), rs,
+                  wq.data_ptr(), wk.data_ptr(), ops.TABLE_COSSIN_F32, cos.data_ptr(), sin.data_ptr(), cos.data_ptr(),
+                  sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, S, H, H, 0, ws.data_ptr(), ws_bytes, sh)
 
     def attn():
         _lib.call("lr_joint_attention_images", out.data_ptr(), rs, ws.data_ptr(), ws_bytes, out.data_ptr(), rs, S, S,
                   H, H, 0, 0, scale, sh)
 
     for _ in range(args.warmup):
-        keys()
-        queries()
+        prepare()
         attn()
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
 
     K = args.steps
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * K + 1)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
     for i in range(K):
-        ev[3 * i].record(stream)
-        keys()
-        ev[3 * i + 1].record(stream)
-        queries()
-        ev[3 * i + 2].record(stream)
+        ev[2 * i].record(stream)
+        prepare()
+        ev[2 * i + 1].record(stream)
         attn()
-    ev[3 * K].record(stream)
+    ev[2 * K].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
-    t_keys = [ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(K)]
-    t_q = [ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(K)]
-    t_attn = [ev[3 * i + 2].elapsed_time(ev[3 * i + 3]) for i in range(K)]
-    total_ms = ev[0].elapsed_time(ev[3 * K])
+    t_prep = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(K)]
+    t_attn = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(K)]
+    total_ms = ev[0].elapsed_time(ev[2 * K])
     ms_step = total_ms / K
     flops = 4.0 * S * S * 128 * H
     attn_ms = float(np.mean(t_attn))
-    keys_ms = float(np.mean(t_keys))
-    q_ms = float(np.mean(t_q))
+    prep_ms = float(np.mean(t_prep))
     value = flops / (ms_step * 1e-3) / 1e12
     achieved = flops / (attn_ms * 1e-3) / 1e12
     clock = from_profile(args.workload, KERNEL, "clock_ghz")
-    log(f"[bench] step {ms_step:.4f} ms (kv prepare {keys_ms:.4f} ms, q prepare {q_ms:.4f} ms, attention "
-        f"{attn_ms:.4f} ms, median attention {float(np.median(t_attn)):.4f} ms); {value:.1f} TFLOP/s step, "
-        f"{achieved:.1f} TFLOP/s attention kernel ({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); "
-        f"wall {wall:.3f} s")
+    log(f"[bench] step {ms_step:.4f} ms (prepare {prep_ms:.4f} ms, attention {attn_ms:.4f} ms, median attention "
+        f"{float(np.median(t_attn)):.4f} ms); {value:.1f} TFLOP/s step, {achieved:.1f} TFLOP/s attention kernel "
+        f"({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); wall {wall:.3f} s")
 
     result = {
         "metric": METRIC,
@@ -275,7 +265,7 @@ def main():
                      "kernel": KERNEL, "kernel_ms": round(attn_ms, 5),
                      "clock_ghz": clock,
                      "peak_at_clock": None if clock is None else round(PEAK_BF16_TFLOPS * clock / 2.4, 1)},
-        "kernels_ms": {"kv_prepare": round(keys_ms, 5), "q_prepare": round(q_ms, 5), "attention": round(attn_ms, 5)},
+        "kernels_ms": {"prepare": round(prep_ms, 5), "attention": round(attn_ms, 5)},
         "flops_per_call": flops,
     }
 

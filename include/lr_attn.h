@@ -22,8 +22,9 @@
  *                               kitchen_rms_rope_split_half_, kernels/cuda/minimax/kitchen_launch.cu:284-314
  *   lr_joint_attention_fused <- the chain rope_q -> rope_k -> V copy -> attention of Dit.block,
  *                               src/engines/qwen_image/dit.zig:252-293 (and minimax_h3/dit.zig:663-672), as one call;
- *                               its launches one by one: lr_joint_kv_prepare (rope_k + V copy), lr_joint_q_prepare
- *                               (rope_q), lr_joint_attention_images (the attention launch, Ops.attention's place)
+ *                               its two launches one by one: lr_joint_prepare (rope_k + V copy + rope_q, also
+ *                               available as lr_joint_kv_prepare and lr_joint_q_prepare) and
+ *                               lr_joint_attention_images (the attention launch, Ops.attention's place)
  *   lr_int8_attention*       <- MiniMax H3's INT8 attention: Kitchen.Plan / attentionPrep / attentionKernel /
  *                               attention, src/engines/minimax_h3/launch.zig:317-419, and kitchen_int8_attention
  *                               {,_rows,_workspace_bytes}, kernels/cuda/minimax/kitchen_launch.cu:193-280
@@ -201,8 +202,8 @@ int lr_joint_attention_prepared(const void* q_raw, void* workspace, size_t works
                                 int config, lr_stream_t stream);
 
 /*
- * The fused op's own three launches as separate calls, in the order lr_joint_attention_fused makes them (the
- * reference's chain rope_k + V copy -> rope_q -> attention, dit.zig:252-293):
+ * The fused op's work as separate calls, in the order of the reference's chain rope_k + V copy -> rope_q -> attention
+ * (dit.zig:252-293); lr_joint_attention_fused makes the first two as one launch (lr_joint_prepare, below):
  *   lr_joint_kv_prepare        (above) keys and values into the workspace's tile images;
  *   lr_joint_q_prepare         q_raw [Sq][H][128] normalised and rotated (as lr_rms_rope_bf16 with an fp32 weight,
  *                              round_norm 0), rounded once to bf16, into q_prep rows; q_prep may be q_raw itself (in
@@ -219,6 +220,19 @@ int lr_joint_q_prepare(const void* q_raw, int64_t q_row_stride, void* q_prep, in
 int lr_joint_attention_images(const void* q_prep, int64_t q_prep_row_stride, const void* workspace,
                               size_t workspace_bytes, void* out, int64_t out_row_stride, int Sq, int Sk, int H, int HK,
                               int p0, int causal, float scale, lr_stream_t stream);
+
+/*
+ * lr_joint_q_prepare and lr_joint_kv_prepare as one launch: the first of the two launches lr_joint_attention_fused
+ * makes (the second is lr_joint_attention_images). Arguments as those two calls, one table kind and pairing for both
+ * (each tensor with its own table rows); the same results bit for bit. q_prep must not overlap k_raw, v or the
+ * workspace, nor q_raw the workspace.
+ */
+int lr_joint_prepare(const void* q_raw, int64_t q_row_stride, void* q_prep, int64_t q_prep_row_stride,
+                     const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                     const float* q_norm_w, const float* k_norm_w, int table_kind, const void* q_table_a,
+                     const void* q_table_b, const void* k_table_a, const void* k_table_b, int64_t table_row_stride,
+                     int pairing, int rot_dim, float eps, int Sq, int Sk, int H, int HK, int n_pre, void* workspace,
+                     size_t workspace_bytes, lr_stream_t stream);
 
 /* lr_joint_attention_fused with an explicit tile configuration (LR_ATTN_CFG_*). */
 int lr_joint_attention_fused_ex(const void* q_raw, const void* k_raw, const void* v, void* out, const float* q_norm_w,

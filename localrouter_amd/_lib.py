@@ -48,6 +48,8 @@ SIGNATURES = {
                                          _F, _I64, _I64, _I, _P]),
     "lr_joint_q_prepare": (_I, [_P, _I64, _P, _I64, _P, _I, _P, _P, _I64, _I, _I, _F, _I, _I, _P]),
     "lr_joint_attention_images": (_I, [_P, _I64, _P, _SZ, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "lr_joint_prepare": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I, _P, _P, _P, _P, _I64, _I, _I, _F, _I,
+                              _I, _I, _I, _I, _P, _SZ, _P]),
     "lr_joint_attention_fused_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I64, _I, _I, _F, _I, _I,
                                               _I, _I, _I, _I, _F, _I64, _I64, _I64, _I64, _I, _P]),
     "lr_int8_attention_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),

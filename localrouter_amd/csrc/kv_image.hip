@@ -16,32 +16,15 @@ namespace lr {
 
 namespace {
 
-template <int KIND>
-__device__ __forceinline__ Rot2 img_rot(const void* ta, const void* tb, int64_t row_off, int p) {
-    Rot2 r;
-    if constexpr (KIND == TABLE_COSSIN_F32) {
-        const float c = static_cast<const float*>(ta)[row_off + p];
-        const float s = static_cast<const float*>(tb)[row_off + p];
-        r.f00 = c; r.f01 = -s; r.f10 = s; r.f11 = c;
-    } else if constexpr (KIND == TABLE_MAT2_BF16) {
-        const u32x2 m = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(ta) + row_off + 4 * p);
-        r.f00 = lo_bf16(m[0]); r.f01 = hi_bf16(m[0]); r.f10 = lo_bf16(m[1]); r.f11 = hi_bf16(m[1]);
-    } else if constexpr (KIND == TABLE_MAT2_F32) {
-        const f32x4 m = *reinterpret_cast<const f32x4*>(static_cast<const float*>(ta) + row_off + 4 * p);
-        r.f00 = m[0]; r.f01 = m[1]; r.f10 = m[2]; r.f11 = m[3];
-    } else {
-        r.f00 = 1.0f; r.f01 = 0.0f; r.f10 = 0.0f; r.f11 = 1.0f;
-    }
-    return r;
-}
+#include "rope_rows.inc"
 
 constexpr int KROWS = 4;   // key rows per thread (rows g, g + 16, g + 32, g + 48 of the tile)
 
+// One 256-thread block: tile tile_id (kv head * tiles + tile) of the keys and of the values, through img (32 KB of
+// LDS: the key image, then the value image).
 template <int KIND, int PAIRING>
-__global__ __launch_bounds__(256) void kv_image_kernel(KvImageArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t img[2 * IMG_TILE_BYTES];   // keys, then values
+__device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile_id, uint8_t* img) {
     const int tid = threadIdx.x, c = tid & 15, g = tid >> 4;
-    const int64_t tile_id = blockIdx.x;                // kv head * tiles + tile
     if (tile_id == 0 && a.cnt)                         // the attention kernel's counters start each call at zero
         for (int x = tid; x < a.ncnt; x += 256) a.cnt[x] = 0;
     const int hk = (int)(tile_id / a.tiles), t = (int)(tile_id - (int64_t)hk * a.tiles);
@@ -82,12 +65,11 @@ __global__ __launch_bounds__(256) void kv_image_kernel(KvImageArgs a) {
             const int key = key0 + g + 16 * i;
             const int64_t toff = (int64_t)max(min(key, a.Sk - 1) - a.n_pre, 0) * a.tab_stride;
             if constexpr (PAIRING == PAIR_INTERLEAVED) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) rt[i][j] = img_rot<KIND>(a.ta, a.tb, toff, min(4 * c + j, P - 1));
+                rot4<KIND>(a.ta, a.tb, toff, 4 * c, P, a.tab_vec, rt[i]);
             } else {
                 const int pc = c < hc ? c : c - hc;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) rt[i][j] = img_rot<KIND>(a.ta, a.tb, toff, min(8 * pc + j, P - 1));
+                rot4<KIND>(a.ta, a.tb, toff, 8 * pc, P, a.tab_vec, rt[i]);
+                rot4<KIND>(a.ta, a.tb, toff, 8 * pc + 4, P, a.tab_vec, rt[i] + 4);
             }
         }
     }
@@ -178,6 +160,21 @@ __global__ __launch_bounds__(256) void kv_image_kernel(KvImageArgs a) {
     }
 }
 
+template <int KIND, int PAIRING>
+__global__ __launch_bounds__(256) void kv_image_kernel(KvImageArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t img[2 * IMG_TILE_BYTES];   // keys, then values
+    kv_tile_block<KIND, PAIRING>(a, blockIdx.x, img);
+}
+
+// The joint attention's whole preparation in one launch: blocks [0, nkv) are key / value tiles, the rest query rows
+// (rope_rows_block over q: normalised and rotated into the prepared-query rows).
+template <int KIND, int PAIRING>
+__global__ __launch_bounds__(256) void joint_prep_kernel(KvImageArgs kv, RopeArgs q, int64_t nkv) {
+    __shared__ __attribute__((aligned(16))) uint8_t img[2 * IMG_TILE_BYTES];
+    if ((int64_t)blockIdx.x < nkv) kv_tile_block<KIND, PAIRING>(kv, blockIdx.x, img);
+    else rope_rows_block<KIND, PAIRING>(q, (int64_t)blockIdx.x - nkv);
+}
+
 template <int KIND>
 hipError_t launch_kind(const KvImageArgs& a, hipStream_t stream) {
     const unsigned blocks = (unsigned)(a.tiles * a.HK);
@@ -188,16 +185,45 @@ hipError_t launch_kind(const KvImageArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+template <int KIND>
+hipError_t launch_prep_kind(const KvImageArgs& kv, const RopeArgs& q, hipStream_t stream) {
+    const int64_t nkv = kv.tiles * kv.HK;
+    const int64_t nq = (q.rows * ((q.heads + 3) / 4) + 15) / 16;   // rope_rows_block: 16 groups of (row, 4 heads)
+    if (nkv + nq > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(nkv + nq));
+    if (kv.pairing == PAIR_SPLIT_HALF)
+        hipLaunchKernelGGL((joint_prep_kernel<KIND, PAIR_SPLIT_HALF>), grid, dim3(256), 0, stream, kv, q, nkv);
+    else
+        hipLaunchKernelGGL((joint_prep_kernel<KIND, PAIR_INTERLEAVED>), grid, dim3(256), 0, stream, kv, q, nkv);
+    return hipGetLastError();
+}
+
+bool kv_args_ok(const KvImageArgs& a) {
+    return a.Sk >= 1 && a.HK >= 1 && a.tiles == img_tiles(a.Sk) && (int64_t)a.tiles * a.HK <= 0x7fffffff;
+}
+
 }  // namespace
 
 hipError_t launch_kv_image(const KvImageArgs& a, hipStream_t stream) {
-    if (a.Sk < 1 || a.HK < 1 || a.tiles != img_tiles(a.Sk) || (int64_t)a.tiles * a.HK > 0x7fffffff)
-        return hipErrorInvalidValue;
+    if (!kv_args_ok(a)) return hipErrorInvalidValue;
     switch (a.table_kind) {
         case TABLE_NONE: return launch_kind<TABLE_NONE>(a, stream);
         case TABLE_COSSIN_F32: return launch_kind<TABLE_COSSIN_F32>(a, stream);
         case TABLE_MAT2_BF16: return launch_kind<TABLE_MAT2_BF16>(a, stream);
         case TABLE_MAT2_F32: return launch_kind<TABLE_MAT2_F32>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_joint_prep(const KvImageArgs& kv, const RopeArgs& q, hipStream_t stream) {
+    // one table kind and pairing for both (the fused call's); the query blocks use q.table_kind's instantiation
+    if (!kv_args_ok(kv) || q.rows < 1 || q.heads < 1 || q.table_kind != kv.table_kind || q.pairing != kv.pairing)
+        return hipErrorInvalidValue;
+    switch (kv.table_kind) {
+        case TABLE_NONE: return launch_prep_kind<TABLE_NONE>(kv, q, stream);
+        case TABLE_COSSIN_F32: return launch_prep_kind<TABLE_COSSIN_F32>(kv, q, stream);
+        case TABLE_MAT2_BF16: return launch_prep_kind<TABLE_MAT2_BF16>(kv, q, stream);
+        case TABLE_MAT2_F32: return launch_prep_kind<TABLE_MAT2_F32>(kv, q, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -142,9 +142,14 @@ bool kv_stage_ok(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, c
 
 // The keys stage (arguments checked): RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre; rows j < n_pre
 // copied) and the values, into the workspace's tile images.
-int kv_launch(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
-              const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK,
-              int n_pre, void* ws, hipStream_t stream) {
+// cos / sin tables whose rows are 16-byte aligned are read as 16-byte chunks
+inline int tab_vec(int kind, const void* ta, const void* tb, int64_t stride) {
+    return kind == LR_TABLE_COSSIN_F32 && aligned(ta, 16) && aligned(tb, 16) && stride % 4 == 0;
+}
+
+lr::KvImageArgs kv_args(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
+                        const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk,
+                        int HK, int n_pre, void* ws) {
     lr::KvImageArgs r{};
     r.k = static_cast<const uint16_t*>(k_raw);
     r.v = static_cast<const uint16_t*>(v);
@@ -158,7 +163,15 @@ int kv_launch(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, cons
     r.img_v = static_cast<char*>(ws) + lr::img_bytes(Sk, HK);
     r.cnt = reinterpret_cast<int*>(split_area(ws, Sk, HK) + lr::STREAM_PART_BYTES);
     r.ncnt = lr::STREAM_MAX_WG;
-    return (int)lr::launch_kv_image(r, stream);
+    r.tab_vec = tab_vec(r.table_kind, kta, ktb, tab_stride);
+    return r;
+}
+int kv_launch(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
+              const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK,
+              int n_pre, void* ws, hipStream_t stream) {
+    return (int)lr::launch_kv_image(
+        kv_args(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws),
+        stream);
 }
 
 // Checks of the query stage: q_raw and q_prep rows (same shape), the table and weight.
@@ -174,9 +187,9 @@ bool q_stage_ok(const void* q_raw, int64_t q_rs, const void* q_prep, int64_t p_r
 
 // The query stage (arguments checked): RMSNorm + RoPE of the q_raw rows into q_prep, rounded once to bf16 as the
 // reference's rope_q writes them (rms_rope.hip).
-int q_launch(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, const float* wq, int table_kind,
-             const void* qta, const void* qtb, int64_t tab_stride, int pairing, int rot, float eps, int Sq, int H,
-             hipStream_t stream) {
+lr::RopeArgs q_args(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, const float* wq, int table_kind,
+                    const void* qta, const void* qtb, int64_t tab_stride, int pairing, int rot, float eps, int Sq,
+                    int H) {
     lr::RopeArgs r{};
     r.src = static_cast<const uint16_t*>(q_raw);
     r.dst = static_cast<uint16_t*>(q_prep);
@@ -186,7 +199,32 @@ int q_launch(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, const 
     r.table_kind = table_kind; r.pairing = pairing; r.rot = rot;
     r.ta = qta; r.tb = qtb; r.tab_stride = tab_stride;
     r.eps = eps; r.round_norm = 0; r.post_scale = 1.0f;
-    return (int)lr::launch_rms_rope(r, stream);
+    r.tab_vec = tab_vec(table_kind, qta, qtb, tab_stride);
+    return r;
+}
+int q_launch(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, const float* wq, int table_kind,
+             const void* qta, const void* qtb, int64_t tab_stride, int pairing, int rot, float eps, int Sq, int H,
+             hipStream_t stream) {
+    return (int)lr::launch_rms_rope(
+        q_args(q_raw, q_rs, q_prep, p_rs, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, H), stream);
+}
+
+// Both preparations of the fused call (arguments checked) in one launch; when every key is a prefix key (no key table
+// is read) the keys go through their own launch.
+int prep_launch(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, const float* wq, const void* k_raw,
+                int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind, const void* qta,
+                const void* qtb, const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps,
+                int Sq, int Sk, int H, int HK, int n_pre, void* ws, hipStream_t stream) {
+    const lr::RopeArgs q = q_args(q_raw, q_rs, q_prep, p_rs, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps,
+                                  Sq, H);
+    const lr::KvImageArgs kv = kv_args(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps,
+                                       Sk, HK, n_pre, ws);
+    if (kv.table_kind != q.table_kind) {
+        const hipError_t e = lr::launch_kv_image(kv, stream);
+        if (e != hipSuccess) return (int)e;
+        return (int)lr::launch_rms_rope(q, stream);
+    }
+    return (int)lr::launch_joint_prep(kv, q, stream);
 }
 
 // Checks of the attention stage. o_rs is bounded so that a block's 256 output rows span less than 4 GiB (the
@@ -259,10 +297,8 @@ int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, c
     // the prepared queries are written into out while the keys and values may still be read: no overlap
     const Span so = rows_span(out, Sq, o_rs, H);
     if (overlap(so, rows_span(k_raw, Sk, k_rs, HK)) || overlap(so, rows_span(v, Sk, v_rs, HK))) return ERR_ARGS;
-    int e = kv_launch(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws,
-                      stream);
-    if (e != 0) return e;
-    e = q_launch(q_raw, q_rs, out, o_rs, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps, Sq, H, stream);
+    const int e = prep_launch(q_raw, q_rs, out, o_rs, wq, k_raw, k_rs, v, v_rs, wk, table_kind, qta, qtb, kta, ktb,
+                              tab_stride, pairing, rot, eps, Sq, Sk, H, HK, n_pre, ws, stream);
     if (e != 0) return e;
     return images_launch(out, o_rs, ws, out, o_rs, Sq, Sk, H, HK, p0, causal, scale, stream);
 }
@@ -543,6 +579,28 @@ int lr_joint_q_prepare(const void* q_raw, int64_t q_row_stride, void* q_prep, in
         return ERR_ARGS;
     return q_launch(q_raw, q_row_stride, q_prep, q_prep_row_stride, q_norm_w, table_kind, q_table_a, q_table_b,
                     table_row_stride, pairing, rot_dim, eps, Sq, H, reinterpret_cast<hipStream_t>(stream));
+}
+
+int lr_joint_prepare(const void* q_raw, int64_t q_row_stride, void* q_prep, int64_t q_prep_row_stride,
+                     const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                     const float* q_norm_w, const float* k_norm_w, int table_kind, const void* q_table_a,
+                     const void* q_table_b, const void* k_table_a, const void* k_table_b, int64_t table_row_stride,
+                     int pairing, int rot_dim, float eps, int Sq, int Sk, int H, int HK, int n_pre, void* workspace,
+                     size_t workspace_bytes, lr_stream_t stream) {
+    if (rot_dim == 0) rot_dim = lr::D;
+    if (!q_stage_ok(q_raw, q_row_stride, q_prep, q_prep_row_stride, q_norm_w, table_kind, q_table_a, q_table_b,
+                    table_row_stride, pairing, rot_dim, eps, Sq, H) ||
+        !kv_stage_ok(k_raw, k_row_stride, v, v_row_stride, k_norm_w, table_kind, k_table_a, k_table_b,
+                     table_row_stride, pairing, rot_dim, eps, Sk, HK, n_pre, workspace, workspace_bytes))
+        return ERR_ARGS;
+    // the prepared queries are written while the keys and values are read; the workspace is written too
+    const Span sp = rows_span(q_prep, Sq, q_prep_row_stride, H);
+    if (overlap(sp, rows_span(k_raw, Sk, k_row_stride, HK)) || overlap(sp, rows_span(v, Sk, v_row_stride, HK)) ||
+        overlap(sp, ws_span(workspace, Sk, HK)) || overlap(rows_span(q_raw, Sq, q_row_stride, H), ws_span(workspace, Sk, HK)))
+        return ERR_ARGS;
+    return prep_launch(q_raw, q_row_stride, q_prep, q_prep_row_stride, q_norm_w, k_raw, k_row_stride, v, v_row_stride,
+                       k_norm_w, table_kind, q_table_a, q_table_b, k_table_a, k_table_b, table_row_stride, pairing,
+                       rot_dim, eps, Sq, Sk, H, HK, n_pre, workspace, reinterpret_cast<hipStream_t>(stream));
 }
 
 int lr_joint_attention_images(const void* q_prep, int64_t q_prep_row_stride, const void* workspace,

@@ -47,6 +47,7 @@ struct RopeArgs {
     float eps;
     int round_norm;       // 1: round the normalised value to bf16 before the rotation
     float post_scale;     // multiplies the normalised value (before the rotation and the single bf16 rounding)
+    int tab_vec;          // 1: cos / sin rows 16-byte aligned (ta, tb and tab_stride), read as 16-byte chunks
 };
 
 // Attention configurations (the LR_ATTN_CFG_* values of include/lr_attn.h).
@@ -85,8 +86,12 @@ struct KvImageArgs {
     void* img_v;          // [HK][tiles] 16 KB value tiles
     int* cnt;             // the streaming kernel's arrival counters, zeroed by this launch (ncnt ints; null: none)
     int ncnt;
+    int tab_vec;          // as RopeArgs::tab_vec
 };
 hipError_t launch_kv_image(const KvImageArgs& a, hipStream_t stream);
+// The keys / values (as launch_kv_image) and the queries (as launch_rms_rope) of a joint-attention call in one launch;
+// both use the same table kind and pairing.
+hipError_t launch_joint_prep(const KvImageArgs& kv, const RopeArgs& q, hipStream_t stream);
 
 // The persistent streaming attention kernel (attn_stream.hip) over tile images: a.k / a.v = the key / value images;
 // a.q = prepared queries (normalised, rotated and multiplied by scale * log2 e, bf16 rows with stride a.q_rs; they may

@@ -6,6 +6,7 @@
   joint_attention(...)  <- Dit.block's rope_q / rope_k / V copy / attention chain, src/engines/qwen_image/dit.zig:252-293
   joint_kv_prepare(...), joint_attention_prepared(...)  <- its two stages (keys / values reused across calls)
   joint_q_prepare(...), joint_attention_images(...)     <- the fused op's query and attention launches one by one
+  joint_prepare(...)                                    <- its first launch (queries, keys and values) as one call
   int8_attention(...)   <- MiniMax H3's INT8 attention, kitchen_int8_attention{,_rows}
                            (kernels/cuda/minimax/kitchen_launch.cu:193-280)
   kitchen_attention(...), kitchen_attention_prep(...), kitchen_attention_kernel(...)
@@ -289,6 +290,38 @@ def joint_q_prepare(q_raw: torch.Tensor, q_prep: torch.Tensor | None = None, *, 
         stride = qa.stride(0)
     _lib.call("lr_joint_q_prepare", _ptr(q_raw), q_rs, _ptr(q_prep), p_rs, _ptr(q_norm), table_kind, _ptr(qa),
               _ptr(qb), stride, pairing, rot, eps, Sq, H, _stream())
+    return q_prep
+
+
+def joint_prepare(q_raw: torch.Tensor, k_raw: torch.Tensor, v: torch.Tensor, workspace: torch.Tensor,
+                  q_prep: torch.Tensor | None = None, *, q_norm: torch.Tensor | None = None,
+                  k_norm: torch.Tensor | None = None, table_kind: int = TABLE_COSSIN_F32, q_table: tuple | None = None,
+                  k_table: tuple | None = None, pairing: int = PAIR_INTERLEAVED, rot: int = 128, eps: float = 1e-6,
+                  n_pre: int = 0) -> torch.Tensor:
+    """The fused op's first launch (lr_joint_prepare): joint_q_prepare and joint_kv_prepare as one launch. Returns
+    q_prep (allocated when None)."""
+    Sq, H = q_raw.shape[0], q_raw.shape[1]
+    Sk, HK = k_raw.shape[0], k_raw.shape[1]
+    q_rs, k_rs, v_rs = _rows(q_raw, "q_raw", H), _rows(k_raw, "k_raw", HK), _rows(v, "v", HK)
+    if q_prep is None:
+        q_prep = torch.empty((Sq, H, D), dtype=torch.bfloat16, device=q_raw.device)
+    p_rs = _rows(q_prep, "q_prep", H)
+    for name, w in (("q_norm", q_norm), ("k_norm", k_norm)):
+        if w is not None and (w.dtype != torch.float32 or not w.is_contiguous() or w.numel() != D):
+            raise ValueError(f"{name}: expected fp32 [128]")
+    qa = qb = ka = kb = None
+    stride = 0
+    if table_kind != TABLE_NONE:
+        if q_table is None or k_table is None:
+            raise ValueError("joint_prepare: q_table and k_table required")
+        (qa, qb), (ka, kb) = q_table, k_table
+        if qa.stride(0) != ka.stride(0):
+            raise ValueError("q and k tables must share a row stride")
+        stride = qa.stride(0)
+    nbytes = workspace.numel() * workspace.element_size()
+    _lib.call("lr_joint_prepare", _ptr(q_raw), q_rs, _ptr(q_prep), p_rs, _ptr(k_raw), k_rs, _ptr(v), v_rs,
+              _ptr(q_norm), _ptr(k_norm), table_kind, _ptr(qa), _ptr(qb), _ptr(ka), _ptr(kb), stride, pairing, rot, eps,
+              Sq, Sk, H, HK, n_pre, _ptr(workspace), nbytes, _stream())
     return q_prep
 
 

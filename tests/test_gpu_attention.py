@@ -411,6 +411,46 @@ def test_three_launches_equal_fused(causal, p0):
     assert np.array_equal(apart, fused) and np.array_equal(inplace, fused)
 
 
+@pytest.mark.parametrize("kind,pairing,rot,n_pre,offset", [
+    (1, 0, 128, 0, 0),      # cos / sin rows 16-byte aligned: 16-byte table loads
+    (1, 0, 128, 0, 1),      # tables offset by one float: the per-pair loads
+    (1, 1, 64, 30, 0),      # split-half, partial rot, a prefix
+    (2, 1, 96, 0, 0),       # bf16 2x2 table (H3 form)
+    (1, 0, 128, 333, 0),    # every key a prefix key: keys and queries in two launches
+])
+def test_one_launch_prepare_equals_the_stages(kind, pairing, rot, n_pre, offset):
+    """lr_joint_prepare (queries, keys and values in one launch, the fused call's first launch) writes the same
+    prepared queries and tile images, bit for bit, as lr_joint_q_prepare + lr_joint_kv_prepare."""
+    Sq, Sk, H, HK = 300, 333, 4, 2
+    print(f"\n[one-launch prepare] kind={kind} pairing={pairing} rot={rot} n_pre={n_pre} offset={offset}", flush=True)
+    q, k, v, wq, wk, qa, qb, ka, kb = _fused_case(36, Sq, Sk, H, HK, kind, pairing, rot)
+
+    def tab(t):   # the table on the device, starting `offset` floats into its allocation (same row stride)
+        if t is None:
+            return None
+        d = _dev_table(t)
+        if offset == 0:
+            return d
+        flat = torch.zeros(d.numel() + 8, dtype=d.dtype, device="cuda")
+        view = flat[offset:offset + d.numel()].view(d.shape)
+        view.copy_(d)
+        return view
+    tq, tk = (tab(qa), tab(qb)), (tab(ka), tab(kb))
+    dwq, dwk = torch.from_numpy(wq).cuda(), torch.from_numpy(wk).cuda()
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    ws1 = torch.zeros(ops.workspace_bytes(Sk, HK), dtype=torch.uint8, device="cuda")
+    ws2 = torch.full_like(ws1, 0x5A)
+    ops.joint_kv_prepare(dk, dv, ws1, k_norm=dwk, table_kind=kind, k_table=tk, pairing=pairing, rot=rot, n_pre=n_pre)
+    qp1 = ops.joint_q_prepare(dq, q_norm=dwq, table_kind=kind, q_table=tq, pairing=pairing, rot=rot)
+    qp2 = ops.joint_prepare(dq, dk, dv, ws2, q_norm=dwq, k_norm=dwk, table_kind=kind, q_table=tq, k_table=tk,
+                            pairing=pairing, rot=rot, n_pre=n_pre)
+    torch.cuda.synchronize()
+    img = 2 * HK * ((Sk + 63) // 64) * 16384
+    assert np.array_equal(from_dev(qp2), from_dev(qp1)), "prepared queries differ"
+    assert torch.equal(ws2[:img], ws1[:img]), "tile images differ"
+    assert not ws2[-1024:].view(torch.int32).any(), "the arrival counters are zeroed"
+
+
 def test_prepared_rejects_plain_configs():
     """The prepared call runs the streaming kernel only: the plain-attention configurations are rejected."""
     Sk, HK = 64, 1
