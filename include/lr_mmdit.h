@@ -59,9 +59,14 @@ int lr_mmdit_destroy(void* ctx);
  * F not a multiple of 8, sizes <= 0). */
 size_t lr_mmdit_workspace_bytes(int n_txt, int n_img, int hidden, int mlp);
 
+/* Build the plans (hipBLASLt's first heuristic result) of the block's row GEMMs for this shape: host work only (no
+ * device memory, no synchronisation). The block call needs its shape planned by this call or by lr_mmdit_tune first;
+ * it does no planning itself, so it can be recorded under graph capture. Thread-safe per context. */
+int lr_mmdit_plan(void* ctx, int n_txt, int n_img, int hidden, int mlp);
+
 /* Optional: time up to `candidates` (<= 16) hipBLASLt heuristic candidates of each of the block's row GEMMs for
- * this shape on the workspace's buffers and keep the fastest. Synchronises the stream and creates events; call it
- * once per shape before timing or capturing blocks (the block call itself plans with the first heuristic result). */
+ * this shape on the workspace's buffers and keep the fastest (planning the shape as lr_mmdit_plan does).
+ * Synchronises the stream and creates events: call it once per shape before timing or capturing blocks. */
 int lr_mmdit_tune(void* ctx, const lr_mmdit_weights* w, int n_txt, int n_img, int hidden, int mlp, int candidates,
                   void* workspace, size_t workspace_bytes, lr_stream_t stream);
 
@@ -70,14 +75,16 @@ int lr_mmdit_tune(void* ctx, const lr_mmdit_weights* w, int n_txt, int n_img, in
 
 /* One linear as the block runs it: y[M, N] (row stride ldy) = x[M, K] (row stride ldx) w[N, K]^T, bf16 in and out,
  * fp32 compute (hipBLASLt), workspace >= LR_MMDIT_GEMM_WORKSPACE bytes. The engines' dense
- * (src/engines/qwen_image/dit.zig:185) on this path; also what bench.py times alone. */
+ * (src/engines/qwen_image/dit.zig:185) on this path; also what bench.py times alone. The first call of a new shape
+ * builds its plan (host work); later calls launch only. */
 int lr_mmdit_linear_bf16(void* ctx, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int M, int N,
                          int K, void* workspace, size_t workspace_bytes, lr_stream_t stream);
 
 /* One block forward, in place on txt [n_txt, D] and img [n_img, D] bf16 (contiguous rows). t: device pointer to one
- * f32 timestep. cos, sin: device [n_txt + n_img, 64] f32 (text rows first). The first call for a new shape builds
- * its GEMM plans (hipBLASLt heuristics, host memory); later calls of that shape launch only. Not reentrant per
- * context: concurrent calls need a context each. */
+ * f32 timestep. cos, sin: device [n_txt + n_img, 64] f32 (text rows first). Weights 16-byte aligned. The shape
+ * must have been planned (lr_mmdit_plan or lr_mmdit_tune): otherwise it returns hipErrorNotReady (600) and launches
+ * nothing. Launches only (no host planning, no synchronisation); calls on one context may come from several threads,
+ * each with its own workspace. */
 int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* img, int n_txt, int n_img, int hidden,
                         int mlp, const float* t, const float* cos, const float* sin, void* workspace,
                         size_t workspace_bytes, lr_stream_t stream);

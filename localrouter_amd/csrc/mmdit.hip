@@ -10,7 +10,9 @@
 
 #include <cmath>
 #include <map>
+#include <mutex>
 #include <tuple>
+#include <vector>
 
 #include "../../include/lr_mmdit.h"
 #include "lr_common.h"
@@ -197,42 +199,69 @@ struct GemmPlan {
 };
 using GemmKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>;   // M, N, K, ldx, ldy
 
+// A context's plans are built by lr_mmdit_plan / lr_mmdit_tune (and by lr_mmdit_linear_bf16 for a new shape) under
+// `mu`; the block call only looks them up. A plan is never removed before the context is destroyed, so a pointer to
+// it stays valid.
 struct Ctx {
     hipblasLtHandle_t lt = nullptr;
     std::map<GemmKey, GemmPlan> plans;
+    std::mutex mu;
 };
 
 int blas_err(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS ? 0 : 1000 + (int)s; }
 
+void destroy_plan(GemmPlan& p) {
+    if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
+    if (p.lb) hipblasLtMatrixLayoutDestroy(p.lb);
+    if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
+    if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+    p = GemmPlan{};
+}
+
+// The plan of one GEMM shape, if built (caller holds c.mu or only reads a map no one is changing).
+GemmPlan* find_plan(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
+    auto it = c.plans.find(GemmKey{M, N, K, ldx, ldy});
+    return it == c.plans.end() ? nullptr : &it->second;
+}
+
+// Build (heuristic-first) and keep the plan of one GEMM shape; every handle created on a failed path is destroyed.
 int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, GemmPlan** out) {
-    const GemmKey key{M, N, K, ldx, ldy};
-    auto it = c.plans.find(key);
-    if (it != c.plans.end()) {
-        *out = &it->second;
+    std::lock_guard<std::mutex> lock(c.mu);
+    if (GemmPlan* found = find_plan(c, M, N, K, ldx, ldy)) {
+        *out = found;
         return 0;
     }
     GemmPlan p;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    auto fail = [&](int rc) {
+        if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+        destroy_plan(p);
+        return rc;
+    };
     int rc;
-    if ((rc = blas_err(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)))) return rc;
+    if ((rc = blas_err(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)))) return fail(rc);
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
-    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
-    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K)))) return rc;
-    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, ldx)))) return rc;
-    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, ldy)))) return rc;
-    hipblasLtMatmulPreference_t pref;
-    if ((rc = blas_err(hipblasLtMatmulPreferenceCreate(&pref)))) return rc;
+    if ((rc = blas_err(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta))))
+        return fail(rc);
+    if ((rc = blas_err(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb))))
+        return fail(rc);
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K)))) return fail(rc);
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, ldx)))) return fail(rc);
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, ldy)))) return fail(rc);
+    if ((rc = blas_err(hipblasLtMatmulPreferenceCreate(&pref)))) return fail(rc);
     const uint64_t ws = GEMM_WS;
-    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof ws);
+    if ((rc = blas_err(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                                             sizeof ws))))
+        return fail(rc);
     hipblasLtMatmulHeuristicResult_t res[1];
     int found = 0;
-    rc = blas_err(hipblasLtMatmulAlgoGetHeuristic(c.lt, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &found));
+    if ((rc = blas_err(hipblasLtMatmulAlgoGetHeuristic(c.lt, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &found))))
+        return fail(rc);
+    if (found < 1) return fail(1000 + (int)HIPBLAS_STATUS_NOT_SUPPORTED);
     hipblasLtMatmulPreferenceDestroy(pref);
-    if (rc) return rc;
-    if (found < 1) return 1000 + (int)HIPBLAS_STATUS_NOT_SUPPORTED;
     p.algo = res[0].algo;
     p.ws = res[0].workspaceSize;
-    auto ins = c.plans.emplace(key, p);
+    auto ins = c.plans.emplace(GemmKey{M, N, K, ldx, ldy}, p);
     *out = &ins.first->second;
     return 0;
 }
@@ -277,6 +306,7 @@ int tune_gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_
         (void)hipEventElapsedTime(&ms, e0, e1);
         if (ms < best) {
             best = ms;
+            std::lock_guard<std::mutex> lock(c.mu);
             p->algo = res[i].algo;
             p->ws = res[i].workspaceSize;
         }
@@ -286,16 +316,29 @@ int tune_gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_
     return rc;
 }
 
+bool is_vector(int64_t M, int64_t K, const void* X, const void* W) {
+    return M == 1 && K % 8 == 0 && ((uintptr_t)X & 15) == 0 && ((uintptr_t)W & 15) == 0;
+}
+
+// One GEMM on the stream. plan_new: build the shape's plan if missing (lr_mmdit_linear_bf16); otherwise the plan must
+// exist (the block call, which checked every plan before its first launch).
 int gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-         void* ws, hipStream_t s) {
-    if (M == 1 && K % 8 == 0 && ((uintptr_t)X & 15) == 0 && ((uintptr_t)W & 15) == 0) {   // a vector: HBM-bound
+         void* ws, hipStream_t s, bool plan_new = false) {
+    if (is_vector(M, K, X, W)) {   // a vector: HBM-bound
         hipLaunchKernelGGL(gemv_kernel, dim3((unsigned)((N + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), 0,
                            s, static_cast<const uint16_t*>(X), static_cast<const uint16_t*>(W),
                            static_cast<uint16_t*>(Y), (int)N, (int)K);
         return (int)hipGetLastError();
     }
-    GemmPlan* p;
-    int rc = plan_gemm(c, M, N, K, ldx, ldy, &p);
+    GemmPlan* p = nullptr;
+    int rc = 0;
+    if (plan_new) {
+        rc = plan_gemm(c, M, N, K, ldx, ldy, &p);
+    } else {
+        std::lock_guard<std::mutex> lock(c.mu);
+        p = find_plan(c, M, N, K, ldx, ldy);
+        if (!p) rc = (int)hipErrorNotReady;
+    }
     if (rc) return rc;
     const float alpha = 1.0f, beta = 0.0f;
     return blas_err(hipblasLtMatmul(c.lt, p->desc, &alpha, W, p->la, X, p->lb, &beta, Y, p->lc, Y, p->lc, &p->algo, ws,
@@ -303,6 +346,20 @@ int gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// The row GEMMs of one block call (M > 1: the vectors go to gemv_kernel): QKV, out, MLP up and down, per stream of rows,
+// as {M, N, K, ldx, ldy}.
+std::vector<GemmKey> block_gemms(int64_t n_txt, int64_t n_img, int64_t D, int64_t F) {
+    std::vector<GemmKey> g;
+    for (const int64_t M : {n_txt, n_img}) {
+        if (M <= 1) continue;
+        g.push_back(GemmKey{M, 3 * D, D, D, 3 * D});
+        g.push_back(GemmKey{M, D, D, D, D});
+        g.push_back(GemmKey{M, F, D, D, F});
+        g.push_back(GemmKey{M, D, F, F, D});
+    }
+    return g;
+}
 
 // scratch layout of one block call
 struct Scratch {
@@ -373,6 +430,17 @@ size_t lr_mmdit_workspace_bytes(int n_txt, int n_img, int hidden, int mlp) {
     return layout(n_txt, n_img, hidden, mlp).total;
 }
 
+int lr_mmdit_plan(void* ctx, int n_txt, int n_img, int hidden, int mlp) {
+    if (!ctx || lr_mmdit_workspace_bytes(n_txt, n_img, hidden, mlp) == 0) return hipErrorInvalidValue;
+    Ctx& c = *static_cast<Ctx*>(ctx);
+    for (const GemmKey& k : block_gemms(n_txt, n_img, hidden, mlp)) {
+        GemmPlan* p;
+        const int rc = plan_gemm(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k), &p);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 int lr_mmdit_tune(void* ctx, const lr_mmdit_weights* w, int n_txt, int n_img, int hidden, int mlp, int candidates,
                   void* workspace, size_t workspace_bytes, lr_stream_t stream) {
     const size_t need = lr_mmdit_workspace_bytes(n_txt, n_img, hidden, mlp);
@@ -408,7 +476,8 @@ int lr_mmdit_linear_bf16(void* ctx, const void* x, int64_t ldx, const void* w, v
     if (!ctx || !x || !w || !y || !workspace || workspace_bytes < GEMM_WS || M <= 0 || N <= 0 || K <= 0 || ldx < K ||
         ldy < N)
         return hipErrorInvalidValue;
-    return gemm(*static_cast<Ctx*>(ctx), x, ldx, w, y, ldy, M, N, K, workspace, reinterpret_cast<hipStream_t>(stream));
+    return gemm(*static_cast<Ctx*>(ctx), x, ldx, w, y, ldy, M, N, K, workspace, reinterpret_cast<hipStream_t>(stream),
+                true);
 }
 
 int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* img, int n_txt, int n_img, int hidden,
@@ -420,10 +489,16 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     const void* ptrs[] = {w->t1, w->t2, w->q_norm, w->k_norm, w->txt.mod, w->txt.qkv, w->txt.out, w->txt.mlp_up,
                           w->txt.mlp_down, w->img.mod, w->img.qkv, w->img.out, w->img.mlp_up, w->img.mlp_down};
     for (const void* p : ptrs)
-        if (!p) return hipErrorInvalidValue;
+        if (!p || ((uintptr_t)p & 15) != 0) return hipErrorInvalidValue;
     if ((((uintptr_t)txt | (uintptr_t)img | (uintptr_t)workspace) & 15) != 0) return hipErrorInvalidValue;
 
     Ctx& c = *static_cast<Ctx*>(ctx);
+    {   // every row GEMM's plan exists (lr_mmdit_plan / lr_mmdit_tune), checked before anything is launched
+        std::lock_guard<std::mutex> lock(c.mu);
+        for (const GemmKey& k : block_gemms(n_txt, n_img, hidden, mlp))
+            if (!find_plan(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k)))
+                return hipErrorNotReady;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t D = hidden, F = mlp, S = (int64_t)n_txt + n_img, H = D / 128;
     const Scratch L = layout(n_txt, n_img, D, F);

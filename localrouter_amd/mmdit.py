@@ -30,6 +30,7 @@ SIGNATURES = {
     "lr_mmdit_create": (_I, [ctypes.POINTER(_P)]),
     "lr_mmdit_destroy": (_I, [_P]),
     "lr_mmdit_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "lr_mmdit_plan": (_I, [_P, _I, _I, _I, _I]),
     "lr_mmdit_tune": (_I, [_P, ctypes.POINTER(Weights), _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "lr_mmdit_linear_bf16": (_I, [_P, _P, ctypes.c_int64, _P, _P, ctypes.c_int64, _I, _I, _I, _P, _SZ, _P]),
     "lr_mmdit_block_bf16": (_I, [_P, ctypes.POINTER(Weights), _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P]),
@@ -96,6 +97,7 @@ class MMDiTBlock:
             raise _lib.LrError("lr_mmdit_create", rc)
         self.ctx = ctx
         self._ws = None
+        self._planned = set()
 
     def close(self):
         if self.ctx:
@@ -126,6 +128,16 @@ class MMDiTBlock:
                                  ws.data_ptr(), ws.numel(), s)
         if rc != 0:
             raise _lib.LrError("lr_mmdit_tune", rc)
+        self._planned.add((n_txt, n_img))
+
+    def plan(self, n_txt: int, n_img: int):
+        """Build the GEMM plans of this shape (host only); the block call needs them (lr_mmdit_plan)."""
+        if (n_txt, n_img) in self._planned:
+            return
+        rc = lib().lr_mmdit_plan(self.ctx, n_txt, n_img, self.hidden, self.mlp)
+        if rc != 0:
+            raise _lib.LrError("lr_mmdit_plan", rc)
+        self._planned.add((n_txt, n_img))
 
     def linear(self, x, w, y, stream=None):
         """y = x w^T through the block's GEMM path (x [M, K], w [N, K], y [M, N] bf16 CUDA tensors, rows may be
@@ -147,6 +159,7 @@ class MMDiTBlock:
         assert t.dtype == torch.float32 and cos.dtype == sin.dtype == torch.float32
         assert cos.shape == (n_txt + n_img, 64) and sin.shape == cos.shape
         ws = self.workspace(n_txt, n_img)
+        self.plan(n_txt, n_img)
         s = torch.cuda.current_stream().cuda_stream if stream is None else stream
         rc = lib().lr_mmdit_block_bf16(self.ctx, ctypes.byref(self.cw), txt.data_ptr(), img.data_ptr(), n_txt, n_img,
                                        self.hidden, self.mlp, t.data_ptr(), cos.data_ptr(), sin.data_ptr(),

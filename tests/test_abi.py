@@ -226,6 +226,7 @@ def test_mmdit_abi_on_cpu():
                                  None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_mmdit_create(None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_mmdit_destroy(None) == HIP_ERROR_INVALID_VALUE
+    assert L.lr_mmdit_plan(None, 8, 16, 256, 512) == HIP_ERROR_INVALID_VALUE
 
 
 def test_kmask_attention_rejects():

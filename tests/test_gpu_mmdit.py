@@ -112,3 +112,36 @@ def test_block_repeated_calls_reuse_plans():
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     blk.close()
+
+
+def test_block_needs_its_plans_and_launches_nothing_without_them():
+    """The block call does no planning of its own (it may be recorded under graph capture): on a context whose shape
+    was not planned it returns hipErrorNotReady (600) before any launch, and after lr_mmdit_plan the same call runs."""
+    import ctypes
+    from localrouter_amd import mmdit
+    dev = torch.device("cuda", 0)
+    D, F, n_txt, gh, gw = 256, 512, 8, 4, 4
+    n_img = gh * gw
+    w = mmdit.make_weights(D, F, dev, seed=13, std=0.05)
+    blk = mmdit.MMDiTBlock(w)
+    g = torch.Generator(device=dev)
+    g.manual_seed(14)
+    txt = torch.randn((n_txt, D), generator=g, device=dev).to(torch.bfloat16)
+    img = torch.randn((n_img, D), generator=g, device=dev).to(torch.bfloat16)
+    cos_np, sin_np = _rope(n_txt, gh, gw)
+    cos, sin = torch.from_numpy(cos_np).to(dev), torch.from_numpy(sin_np).to(dev)
+    t = torch.tensor([0.5], dtype=torch.float32, device=dev)
+    ws = blk.workspace(n_txt, n_img)
+    before = (_to_np_bits(txt), _to_np_bits(img))
+    call = lambda: mmdit.lib().lr_mmdit_block_bf16(blk.ctx, ctypes.byref(blk.cw), txt.data_ptr(), img.data_ptr(),
+                                                   n_txt, n_img, D, F, t.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                                   ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    assert call() == 600
+    torch.cuda.synchronize()
+    assert np.array_equal(_to_np_bits(txt), before[0]) and np.array_equal(_to_np_bits(img), before[1])
+    assert mmdit.lib().lr_mmdit_plan(blk.ctx, n_txt, n_img, D, F) == 0
+    assert call() == 0
+    torch.cuda.synchronize()
+    assert not np.array_equal(_to_np_bits(img), before[1])
+    blk.close()
+
