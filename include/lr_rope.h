@@ -26,6 +26,11 @@ extern "C" {
 
 /* The 64 Qwen-Image frequencies as the engine loads them (kernels/qwen_image/rope_omega.json, read by smath.omegas,
  * src/engines/qwen_image/smath.zig:112-126), f64 into out[64]. */
+/* The engines' portable sin and cos of n f64 angles (src/engines/qwen_image/smath.zig:18-52: Cody-Waite reduction by
+ * pi/2 in three parts, fdlibm's kernel polynomials, the same operations in the same order), which every table below
+ * uses. Returns 0, or 1 for a bad argument. */
+int lr_rope_sincos(const double* x, int64_t n, double* sin_out, double* cos_out);
+
 void lr_rope_qwen_omegas(double* out);
 
 /* Text ids: position first + i on all three axes (src/engines/qwen_image/rope.zig:11-13). ids [n, 3] f32. */

@@ -3,9 +3,8 @@
 // Qwen-Image: src/engines/qwen_image/rope.zig:7-45 (ids and cos/sin tables), frequencies of
 // kernels/qwen_image/rope_omega.json as smath.omegas reads them (smath.zig:112-126). MiniMax H3:
 // src/engines/minimax_h3/layout.zig:60-134 (packed-layout positions, the [S, 48, 2, 2] bf16 table). The reference
-// computes sin/cos with its own portable f64 routine (smath.zig:40-52), which agrees with libm to 4e-15 by its own
-// test (smath.zig:128-135); this file uses libm's f64 sin/cos, so a table entry can differ from the engine's only
-// where an f64 last-bit difference crosses an f32 rounding boundary.
+// computes sin/cos with its own portable f64 routine (smath.zig:18-52), and so does this file (engine_sincos below),
+// so that the tables are the engine's bits, not libm's.
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -56,6 +55,41 @@ uint16_t f32_to_bf16(float f) {
     return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
 }
 
+// The engine's portable sin / cos of an f64 angle (smath.zig:18-52): Cody-Waite reduction by pi/2 with pi/2 split
+// in three parts (the first 33 bits exact in n * pio2_1 for |n| < 2^20), then the polynomial kernels of fdlibm
+// (Sun Microsystems, 1993: k_sin.c, k_cos.c, the reduction constants of e_rem_pio2.c), and the quadrant n mod 4.
+// The operation order fixes the bits; this file is compiled without FMA contraction.
+constexpr double kInvPio2 = 6.36619772367581382433e-01;
+constexpr double kPio2_1 = 1.57079632673412561417e+00;
+constexpr double kPio2_2 = 6.07710050630396597660e-11;
+constexpr double kPio2_3 = 2.02226624871116645580e-21;
+constexpr double kS[6] = {-1.66666666666666324348e-01, 8.33333333332248946124e-03, -1.98412698298579493134e-04,
+                          2.75573137070700676789e-06, -2.50507602534068634195e-08, 1.58969099521155010221e-10};
+constexpr double kC[6] = {4.16666666666666019037e-02, -1.38888888888741095749e-03, 2.48015872894767294178e-05,
+                          -2.75573143513906633035e-07, 2.08757232129817482790e-09, -1.13596475577881948265e-11};
+
+void engine_sincos(double x, double* sin_out, double* cos_out) {
+    const double fn = std::floor(x * kInvPio2 + 0.5);
+    const int64_t n = (int64_t)fn;
+    const double r = ((x - fn * kPio2_1) - fn * kPio2_2) - fn * kPio2_3;
+    const double z = r * r;
+    // kernel sin: r + r^3 (s1 + z (s2 + z (s3 + z (s4 + z (s5 + z s6)))))
+    const double v = z * r;
+    const double sr = kS[1] + z * (kS[2] + z * (kS[3] + z * (kS[4] + z * kS[5])));
+    const double sv = r + v * (kS[0] + z * sr);
+    // kernel cos: 1 - z/2 + z^2 (c1 + ...), the 1 - z/2 part with its rounding error carried
+    const double cr = z * (kC[0] + z * (kC[1] + z * (kC[2] + z * (kC[3] + z * (kC[4] + z * kC[5])))));
+    const double hz = 0.5 * z;
+    const double w = 1.0 - hz;
+    const double cv = w + (((1.0 - w) - hz) + z * cr);
+    switch ((uint64_t)n & 3u) {
+        case 0: *sin_out = sv; *cos_out = cv; break;
+        case 1: *sin_out = cv; *cos_out = -sv; break;
+        case 2: *sin_out = -sv; *cos_out = -cv; break;
+        default: *sin_out = -cv; *cos_out = sv; break;
+    }
+}
+
 // omega_j = 1 / theta^(2j/d), j < d/2
 double axis_omega(int d, int j, double theta) { return 1.0 / std::pow(theta, 2.0 * (double)j / (double)d); }
 
@@ -70,8 +104,10 @@ void identity_rows(int64_t n, float* c, float* s) {
 void table_row(const double* pos3, const int* axis_of_pair, const double* om, float* c, float* s) {
     for (int p = 0; p < kPairs; ++p) {
         const double ang = pos3[axis_of_pair[p]] * om[p];
-        c[p] = (float)std::cos(ang);
-        s[p] = (float)std::sin(ang);
+        double sv, cv;
+        engine_sincos(ang, &sv, &cv);
+        c[p] = (float)cv;
+        s[p] = (float)sv;
     }
 }
 
@@ -95,6 +131,12 @@ constexpr double kH3FrameRescale = 5.0 / 3.0;                        // layout.z
 }  // namespace
 
 extern "C" {
+
+int lr_rope_sincos(const double* x, int64_t n, double* sin_out, double* cos_out) {
+    if (n < 0 || (n > 0 && (!x || !sin_out || !cos_out))) return 1;
+    for (int64_t i = 0; i < n; ++i) engine_sincos(x[i], sin_out + i, cos_out + i);
+    return 0;
+}
 
 void lr_rope_qwen_omegas(double* out) {
     for (int p = 0; p < kPairs; ++p) out[p] = bits_to_f64(kQwenOmegaBits[p]);
@@ -235,7 +277,9 @@ int lr_rope_h3_table(const double* pos, int64_t rows, const float* inv_freq, uin
             const float p = (float)pos[3 * r + ax];
             for (int j = 0; j < 16; ++j) {
                 const float ang = p * inv_freq[j];   // f32 product
-                const float c = (float)std::cos((double)ang), s = (float)std::sin((double)ang);
+                double sv, cv;
+                engine_sincos((double)ang, &sv, &cv);
+                const float c = (float)cv, s = (float)sv;
                 uint16_t* e = out + (r * 48 + ax * 16 + j) * 4;
                 e[0] = f32_to_bf16(c);
                 e[1] = f32_to_bf16(-s);

@@ -12,8 +12,9 @@ Three families:
 * The synthetic BASELINE shapes (the build's own definition, the reference has no such configs): 2D grid tables for
   the 1024-token and 4096-token images, the three-frame edit layout, and the 3D video grid; text tokens un-rotated.
 
-The reference's portable sincos (src/engines/qwen_image/smath.zig:40-52) agrees with libm to 4e-15 (its own test,
-smath.zig:128-135); these builders use numpy's float64 sin/cos, which can differ from it in the last f64 bit only.
+Every table takes its sin / cos from `engine_sincos`, the reference's portable f64 routine
+(src/engines/qwen_image/smath.zig:18-52) restated operation for operation, so that the tables are the engines' bits
+(numpy's own sin / cos can differ from it in the last f64 bit, and so cross an f32 rounding boundary).
 """
 from __future__ import annotations
 
@@ -23,6 +24,41 @@ QWEN_AXES = (16, 56, 56)
 QWEN_THETA = 10000.0
 H3_FRAME_PER_TOKEN = (1.0, 4.0, 4.0, 4.0, 4.0)   # layout.zig:12
 H3_FRAME_RESCALE = 5.0 / 3.0                      # layout.zig:13
+
+
+# smath.zig:7-20: pi/2 split in three parts for the Cody-Waite reduction (n * PIO2_1 exact for |n| < 2^20), and the
+# kernel polynomials of fdlibm (Sun Microsystems, 1993: k_sin.c, k_cos.c; the reduction constants of e_rem_pio2.c)
+INVPIO2 = 6.36619772367581382433e-01
+PIO2_1 = 1.57079632673412561417e+00
+PIO2_2 = 6.07710050630396597660e-11
+PIO2_3 = 2.02226624871116645580e-21
+SIN_COEF = (-1.66666666666666324348e-01, 8.33333333332248946124e-03, -1.98412698298579493134e-04,
+            2.75573137070700676789e-06, -2.50507602534068634195e-08, 1.58969099521155010221e-10)
+COS_COEF = (4.16666666666666019037e-02, -1.38888888888741095749e-03, 2.48015872894767294178e-05,
+            -2.75573143513906633035e-07, 2.08757232129817482790e-09, -1.13596475577881948265e-11)
+
+
+def engine_sincos(x) -> tuple[np.ndarray, np.ndarray]:
+    """smath.sincos (smath.zig:40-52) elementwise in float64, the same IEEE operations in the same order: n =
+    floor(x 2/pi + 1/2), r = ((x - n pio2_1) - n pio2_2) - n pio2_3, fdlibm's kernel sin and cos of r, quadrant n mod 4.
+    Returns (sin, cos)."""
+    x = np.asarray(x, np.float64)
+    s1, s2, s3, s4, s5, s6 = SIN_COEF
+    c1, c2, c3, c4, c5, c6 = COS_COEF
+    fn = np.floor(x * INVPIO2 + 0.5)
+    n = fn.astype(np.int64)
+    r = ((x - fn * PIO2_1) - fn * PIO2_2) - fn * PIO2_3
+    z = r * r
+    v = z * r
+    sv = r + v * (s1 + z * (s2 + z * (s3 + z * (s4 + z * (s5 + z * s6)))))
+    cr = z * (c1 + z * (c2 + z * (c3 + z * (c4 + z * (c5 + z * c6)))))
+    hz = 0.5 * z
+    w = 1.0 - hz
+    cv = w + (((1.0 - w) - hz) + z * cr)
+    q = n & 3
+    sin = np.select([q == 0, q == 1, q == 2], [sv, cv, -sv], -cv)
+    cos = np.select([q == 0, q == 1, q == 2], [cv, -sv, -cv], sv)
+    return sin, cos
 
 
 def axis_omegas(d: int, theta: float = QWEN_THETA) -> np.ndarray:
@@ -84,7 +120,8 @@ def qwen_table(ids: np.ndarray, om: np.ndarray | None = None, axes=QWEN_AXES):
     om = qwen_omegas(axes) if om is None else np.asarray(om, np.float64)
     cols = np.concatenate([np.full(d // 2, ax) for ax, d in enumerate(axes)])
     ang = ids.astype(np.float64)[:, cols] * om[None, :]
-    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    s, c = engine_sincos(ang)
+    return c.astype(np.float32), s.astype(np.float32)
 
 
 def identity_rows(n: int, pairs: int = 64):
@@ -100,8 +137,8 @@ def grid2d_table(n_text: int, gh: int, gw: int, theta: float = QWEN_THETA):
     r, c = np.meshgrid(np.arange(gh, dtype=np.float64), np.arange(gw, dtype=np.float64), indexing="ij")
     ang = np.concatenate([r.reshape(-1, 1) * om[None, :], c.reshape(-1, 1) * om[None, :]], axis=1)
     tc, ts = identity_rows(n_text)
-    return (np.concatenate([tc, np.cos(ang).astype(np.float32)]),
-            np.concatenate([ts, np.sin(ang).astype(np.float32)]))
+    s, c = engine_sincos(ang)
+    return np.concatenate([tc, c.astype(np.float32)]), np.concatenate([ts, s.astype(np.float32)])
 
 
 def edit_table(n_text: int, frames: int, gh: int, gw: int):
@@ -128,8 +165,9 @@ def video3d_table(n_text: int, t: int, gh: int, gw: int, dims=(32, 48, 48), thet
     step = 1 << 16                                                # chunked: 172k x 64 angles at a time is fine,
     for i in range(0, n, step):                                   # but keep the f64 temporaries small
         ang = pos[i:i + step][:, cols] * om[None, :]
-        cos[n_text + i:n_text + i + step] = np.cos(ang)
-        sin[n_text + i:n_text + i + step] = np.sin(ang)
+        s, c = engine_sincos(ang)
+        cos[n_text + i:n_text + i + step] = c
+        sin[n_text + i:n_text + i + step] = s
     return cos, sin
 
 
@@ -176,8 +214,9 @@ def h3_rope_table(pos: np.ndarray, inv_freq: np.ndarray) -> np.ndarray:
     inv = np.asarray(inv_freq, np.float32)
     assert inv.shape == (16,)
     ang = pos.astype(np.float32)[:, :, None] * inv[None, None, :]            # f32 product, [S, 3, 16]
-    c = np.cos(ang.astype(np.float64)).astype(np.float32).reshape(-1, 48)
-    s = np.sin(ang.astype(np.float64)).astype(np.float32).reshape(-1, 48)
+    s, c = engine_sincos(ang.astype(np.float64))
+    c = c.astype(np.float32).reshape(-1, 48)
+    s = s.astype(np.float32).reshape(-1, 48)
     out = np.empty((pos.shape[0], 48, 2, 2), np.uint16)
     out[..., 0, 0] = f32_to_bf16_bits(c)
     out[..., 0, 1] = f32_to_bf16_bits(-s)

@@ -18,6 +18,7 @@ _P, _I, _I64, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_doubl
 
 # name -> (restype, argtypes); the order mirrors include/lr_rope.h
 SIGNATURES = {
+    "lr_rope_sincos": (_I, [_P, _I64, _P, _P]),
     "lr_rope_qwen_omegas": (None, [_P]),
     "lr_rope_qwen_text_ids": (_I, [_P, _I, _I]),
     "lr_rope_qwen_image_ids": (_I, [_P, _I, _I, _I, _I, _I]),
@@ -51,6 +52,14 @@ def _ptr(a: np.ndarray):
 def _check(name: str, rc: int) -> None:
     if rc != 0:
         raise _lib.LrError(name, rc)
+
+
+def sincos(x: np.ndarray):
+    """The library's engine sincos of f64 angles: (sin, cos)."""
+    x = np.ascontiguousarray(x, np.float64)
+    s, c = np.empty_like(x), np.empty_like(x)
+    _check("lr_rope_sincos", lib().lr_rope_sincos(_ptr(x), x.size, _ptr(s), _ptr(c)))
+    return s, c
 
 
 def qwen_omegas() -> np.ndarray:

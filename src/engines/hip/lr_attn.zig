@@ -106,6 +106,7 @@ pub extern "lr_attn" fn lr_int8_attention_kernel(out: u64, ws: u64, b: c_int, h:
     d: c_int, scale: f32, o_rows: c_int, s: Stream) c_int;
 
 // ---------------------------------------------------------------------------------------------- include/lr_rope.h
+pub extern "lr_attn" fn lr_rope_sincos(x: [*]const f64, n: i64, sin_out: [*]f64, cos_out: [*]f64) c_int;
 pub extern "lr_attn" fn lr_rope_qwen_omegas(out: *[64]f64) void;
 pub extern "lr_attn" fn lr_rope_qwen_text_ids(ids: [*]f32, n: c_int, first: c_int) c_int;
 pub extern "lr_attn" fn lr_rope_qwen_image_ids(ids: [*]f32, h: c_int, w: c_int, pos: c_int, target_h: c_int,

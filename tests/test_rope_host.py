@@ -5,6 +5,7 @@ tests/test_rope_tables.py pins to the same vectors and closed forms."""
 from __future__ import annotations
 
 import re
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -19,6 +20,19 @@ def test_header_and_exports_agree():
     L = rope_host.lib()
     for name in declared:
         assert hasattr(L, name)
+
+
+def test_sincos_is_the_engine_bits():
+    """The library's sincos (every table builder's) on the bits of tests/golden/sincos.npz, and on the angles of a
+    whole Qwen-Image table against the numpy restatement."""
+    f = np.load(Path(__file__).resolve().parent / "golden" / "sincos.npz")
+    s, c = rope_host.sincos(f["x"].view(np.float64))
+    assert np.array_equal(s.view(np.uint64), f["sin"]) and np.array_equal(c.view(np.uint64), f["cos"])
+    x = np.random.default_rng(5).uniform(-2e5, 2e5, 200000)
+    s, c = rope_host.sincos(x)
+    rs, rc = rope.engine_sincos(x)
+    assert np.array_equal(s.view(np.uint64), rs.view(np.uint64)) and np.array_equal(c.view(np.uint64), rc.view(np.uint64))
+    assert rope_host.lib().lr_rope_sincos(None, 4, None, None) == 1
 
 
 def test_omegas_are_the_engine_bits():

@@ -1,6 +1,9 @@
 """Host RoPE table builders (localrouter_amd.rope) against the reference's own data and test vectors:
 kernels/qwen_image/rope_omega.json (committed as tests/golden/rope_omega.json), the image-id test of
-src/engines/qwen_image/rope.zig:47-52 and the layout tests of src/engines/minimax_h3/layout.zig:186-215."""
+src/engines/qwen_image/rope.zig:47-52, the layout tests of src/engines/minimax_h3/layout.zig:186-215, and the engines'
+portable sincos (smath.zig:40-52): its own accuracy bound (smath.zig:128-135), relative accuracy at the zeros, where
+the three-part reduction decides the result, and its bits on tests/golden/sincos.npz (written by
+tests/golden/make_sincos.py from the reference's Python statement of the same routine)."""
 from __future__ import annotations
 
 import json
@@ -19,6 +22,61 @@ def _frozen_omegas():
     d = json.loads((GOLDEN / "rope_omega.json").read_text())
     assert d["theta"] == 10000.0 and d["axes"] == [16, 56, 56]
     return np.array([struct.unpack(">d", bytes.fromhex(h))[0] for h in d["omega_f64_be_hex"]])
+
+
+def _sincos_fixture():
+    f = np.load(GOLDEN / "sincos.npz")
+    return f["x"].view(np.float64), f["sin"], f["cos"]
+
+
+def test_engine_sincos_bits():
+    x, s_bits, c_bits = _sincos_fixture()
+    assert x.size > 4000
+    s, c = rope.engine_sincos(x)
+    assert np.array_equal(s.view(np.uint64), s_bits) and np.array_equal(c.view(np.uint64), c_bits)
+    # the fixture tells the routine from libm: numpy's sin and cos differ from it in the last bit on many angles
+    assert (np.sin(x).view(np.uint64) != s_bits).sum() > 100
+
+
+def test_engine_sincos_accuracy_bound():
+    """smath.zig:128-135: within 4e-15 of libm over -3000, -3000 + 0.7317, ... < 3000; and special values."""
+    x = -3000.0 + 0.7317 * np.arange(8201)
+    x = x[x < 3000.0]
+    s, c = rope.engine_sincos(x)
+    assert np.abs(s - np.sin(x)).max() <= 4e-15 and np.abs(c - np.cos(x)).max() <= 4e-15
+    s, c = rope.engine_sincos(np.array([0.0, np.pi / 6, np.pi / 2, np.pi, -np.pi / 2]))
+    assert s[0] == 0.0 and c[0] == 1.0
+    assert abs(s[1] - 0.5) <= 1.2e-16 and abs(c[2]) <= 1e-16 and c[3] == -1.0 and s[4] == -1.0
+
+
+def test_engine_sincos_relative_accuracy_at_zeros():
+    """The three parts of pi / 2 sum to it within 8.5e-32 (against 60 digits of pi), so near k pi / 2, where the result
+    is tiny, the routine is within k 1e-31 + 4 ulp of libm's exactly reduced sin and cos; a reduction that drops the
+    third part misses by k 2e-21, a sizeable fraction of results of 1e-18."""
+    from fractions import Fraction
+    pi = Fraction("3.141592653589793238462643383279502884197169399375105820974944")
+    assert abs(pi / 2 - (Fraction(rope.PIO2_1) + Fraction(rope.PIO2_2) + Fraction(rope.PIO2_3))) < Fraction(1, 10 ** 31)
+    k = np.concatenate([np.arange(1, 2000), [65535, 2 ** 19]]).astype(np.float64)
+    x = k * (np.pi / 2)
+    s, c = rope.engine_sincos(x)
+    for m, got, ref in ((k % 2 == 0, s, np.sin(x)), (k % 2 == 1, c, np.cos(x))):
+        assert (np.abs(got[m] - ref[m]) <= k[m] * 1e-31 + 4 * np.spacing(np.abs(ref[m]))).all()
+
+
+@pytest.mark.parametrize("name,value", [("PIO2_3", 0.0), ("S6", 0.0), ("C3", 2.48015872894767294178e-04),
+                                        ("INVPIO2", 0.6366)])
+def test_engine_sincos_planted_mistakes_fail(monkeypatch, name, value):
+    """A dropped reduction term, a dropped or mistyped kernel coefficient, a coarse 2/pi: each changes bits of the
+    fixture."""
+    x, s_bits, c_bits = _sincos_fixture()
+    if name in ("S6", "C3"):
+        coef = list(rope.SIN_COEF if name == "S6" else rope.COS_COEF)
+        coef[5 if name == "S6" else 2] = value
+        monkeypatch.setattr(rope, "SIN_COEF" if name == "S6" else "COS_COEF", tuple(coef))
+    else:
+        monkeypatch.setattr(rope, name, value)
+    s, c = rope.engine_sincos(x)
+    assert not (np.array_equal(s.view(np.uint64), s_bits) and np.array_equal(c.view(np.uint64), c_bits))
 
 
 def test_qwen_omegas_are_the_engine_bits():
