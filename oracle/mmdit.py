@@ -13,9 +13,11 @@ where it has them:
   * SiLU: ops.cu:34-39;
   * the joint attention with QK-RMSNorm and RoPE: the attention oracle of this package (liblro.so).
 Pinning (tests/test_oracle_mmdit.py): the sinusoid and GELU against their closed forms and special values, the
-LayerNorm against its moments, the linear layout against a brute-force loop, and the adaLN-zero identity (zero
-modulation weights leave both streams unchanged). The composition itself has no reference to be pinned to:
-parity unpinned beyond those checks.
+LayerNorm against its moments, the linear layout against a brute-force loop, the adaLN-zero identity (zero
+modulation weights leave both streams unchanged), and the meaning of each modulation chunk on zero inputs, where the
+LayerNorm is 0: a scale has no effect, a shift does, and a zero gate shuts its own branch and only that one (planted
+shift/scale and gate swaps fail these). The composition itself has no reference to be pinned to: parity unpinned
+beyond those checks.
 """
 from __future__ import annotations
 
@@ -77,11 +79,17 @@ def gated_residual(x: np.ndarray, a: np.ndarray, g: np.ndarray) -> np.ndarray:
     return bf16r((a.astype(np.float64) * g[None, :].astype(np.float64) + x.astype(np.float64)).astype(np.float32))
 
 
+# the six modulation chunks of a stream, in the order of its mod projection's rows (include/lr_mmdit.h)
+MOD_CHUNKS = ("shift_attn", "scale_attn", "gate_attn", "shift_mlp", "scale_mlp", "gate_mlp")
+
+
 def mmdit_block(txt: np.ndarray, img: np.ndarray, w: dict, t: float, cos: np.ndarray, sin: np.ndarray,
-                precise_attention: bool = False):
+                precise_attention: bool = False, chunk_order=(0, 1, 2, 3, 4, 5)):
     """One block. txt [St, D], img [Si, D]: uint16 bf16 bits. w: bf16 bits (uint16) arrays t1 [D, 256], t2 [D, D],
     and per stream s in (txt, img): s.mod [6D, D], s.qkv [3D, D], s.out [D, D], s.mlp_up [F, D], s.mlp_down [D, F];
-    q_norm, k_norm [128] fp32. cos, sin [St + Si, 64] fp32. Returns (txt, img) fp32 arrays of bf16 values."""
+    q_norm, k_norm [128] fp32. cos, sin [St + Si, 64] fp32. Returns (txt, img) fp32 arrays of bf16 values.
+    chunk_order[i] is the chunk of the mod projection that serves as MOD_CHUNKS[i]; anything but the identity is a
+    planted mistake, for the tests that show the semantic checks catch one."""
     W = {k: (bf16_to_f32(v) if v.dtype == np.uint16 else np.asarray(v, np.float32)) for k, v in w.items()}
     xt, xi = bf16_to_f32(txt), bf16_to_f32(img)
     St, D = xt.shape
@@ -94,6 +102,7 @@ def mmdit_block(txt: np.ndarray, img: np.ndarray, w: dict, t: float, cos: np.nda
     mod = {s: linear(ts, W[f"{s}.mod"])[0] for s in ("txt", "img")}
 
     def chunk(s, i):
+        i = chunk_order[i]
         return mod[s][i * D:(i + 1) * D]
 
     xs = {"txt": xt, "img": xi}

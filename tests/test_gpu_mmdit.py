@@ -145,3 +145,39 @@ def test_block_needs_its_plans_and_launches_nothing_without_them():
     assert not np.array_equal(_to_np_bits(img), before[1])
     blk.close()
 
+
+def test_block_modulation_chunk_meanings():
+    """The oracle's chunk-meaning identities (tests/test_oracle_mmdit.py) on the GPU block: on zero inputs a scale
+    changes no bit, a shift does, and a zero gate shuts its own branch (the output is exactly 0)."""
+    from localrouter_amd import mmdit
+    from tests.test_oracle_mmdit import (MEANING_D, MEANING_F, MEANING_GRID, MEANING_ST, chunk_weights,
+                                         meaning_cases)
+    dev = torch.device("cuda", 0)
+    D, F, St, (gh, gw) = MEANING_D, MEANING_F, MEANING_ST, MEANING_GRID
+    cos_np, sin_np = _rope(St, gh, gw)
+    cos, sin = torch.from_numpy(cos_np).to(dev), torch.from_numpy(sin_np).to(dev)
+    t = torch.zeros(1, dtype=torch.float32, device=dev)
+    rng = np.random.default_rng(11)
+    for name, a, b, extra, outcome in meaning_cases(rng):
+        seed = int(rng.integers(1 << 30))
+        print(f"mmdit chunk meaning: {name} -> {outcome}", flush=True)
+        outs = []
+        for chunks in (a, b):
+            wn = chunk_weights(np.random.default_rng(seed), D, F, {"txt": chunks, "img": chunks}, **extra)
+            w = {k: (torch.from_numpy(v.view(np.int16)).to(dev).view(torch.bfloat16) if v.dtype == np.uint16
+                     else torch.from_numpy(np.ascontiguousarray(v, np.float32)).to(dev)) for k, v in wn.items()}
+            txt = torch.zeros((St, D), dtype=torch.bfloat16, device=dev)
+            img = torch.zeros((gh * gw, D), dtype=torch.bfloat16, device=dev)
+            blk = mmdit.MMDiTBlock(w)
+            blk(txt, img, t, cos, sin)
+            torch.cuda.synchronize()
+            outs.append(np.concatenate([_to_np_bits(txt), _to_np_bits(img)]))
+            blk.close()
+        same = np.array_equal(outs[0], outs[1])
+        if outcome == "zero":
+            assert same and not np.any(oracle.bf16_to_f32(outs[0])), name
+        elif outcome == "same":
+            assert same and np.any(outs[0]), name
+        else:
+            assert not same, name
+

@@ -162,6 +162,50 @@ def _p8_numpy(q8, qs, k8, ks, v8, vs, cta):
     return num / den * vs[None].astype(np.float64)
 
 
+# P of a key whose score sits k log2 steps below its tile's maximum: the nearest integer to 2^(7.9943534 - k) =
+# 254.99997 / 2^k (the offset's fp32 value), i.e. to 255 / 2^k; k = 1 (127.49998) is left out as a near-tie
+P8_AT_STEP = {0: 255, 2: 64, 3: 32, 4: 16, 5: 8, 6: 4, 7: 2, 8: 1, 9: 0, 10: 0}
+
+
+def test_p8_closed_form_at_log2_steps():
+    """Scores at exact log2 steps (qs = 1 / (scale log2 e) in fp32, key scales 1, q a unit vector, so x_j = -k_j to
+    1e-7): every P is known in closed form, every tile's weight is 2^-(its maximum's step), and the output is the
+    P-weighted mean of V. Three tiles of 64 keys (the last one partial) with maxima at steps 0, 3 and 2; row 1 doubles
+    the steps of another column."""
+    qs1 = np.float32(1.0 / (SCALE * np.log2(np.e)))
+    nk, cta = 170, 64
+    rng = np.random.default_rng(12)
+    tiles = [(0, 64, 0), (64, 128, 3), (128, 170, 2)]
+    steps0 = np.zeros(nk, np.int64)
+    for a, b, lo in tiles:
+        rel = rng.choice(list(P8_AT_STEP), b - a)
+        rel[0] = 0
+        steps0[a:b] = lo + rel
+    steps1 = rng.integers(0, 6, nk)
+    for a, b, _ in tiles:
+        steps1[a] = 0
+    q8 = np.zeros((2, 128), np.int8)
+    q8[0, 0], q8[1, 1] = 1, 2
+    k8 = rng.integers(-127, 128, (nk, 128)).astype(np.int8)
+    k8[:, 0], k8[:, 1] = -steps0, -steps1
+    v8 = rng.integers(-127, 128, (nk, 128)).astype(np.int8)
+    vs = rng.uniform(0.005, 0.02, 128).astype(np.float32)
+    got = oracle.i8_attention_p8(q8, np.full(2, qs1), k8, np.ones((nk + 15) // 16, np.float32), v8, vs, cta)
+    for row, steps, mult in ((0, steps0, 1), (1, steps1, 2)):
+        num, den = np.zeros(128), 0.0
+        for a, b, _ in tiles:
+            x = mult * steps[a:b]
+            top = x.min()
+            p = np.array([P8_AT_STEP[int(k)] for k in x - top], np.float64)
+            num += 2.0 ** -top * (p @ v8[a:b].astype(np.float64))
+            den += 2.0 ** -top * p.sum()
+        exp = num / den * vs
+        assert np.abs(got[row] - exp).max() <= 1e-6 * np.abs(exp).max(), row
+    # the closed form is not the exact softmax: the rounding shows
+    assert np.abs(got - oracle.i8_attention(q8, np.full(2, qs1), k8, np.ones((nk + 15) // 16, np.float32), v8,
+                                            vs)).max() > 1e-4
+
+
 def test_p8_rounding_against_numpy():
     rng = np.random.default_rng(4)
     for W, nk, cta in ((7, 200, 64), (5, 300, 128), (3, 64, 64), (4, 65, 64)):
