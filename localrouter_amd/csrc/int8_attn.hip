@@ -458,6 +458,7 @@ __device__ __forceinline__ T lds_load(const uint8_t* p) {
 // (scores) or by the column-sum MFMA (P V).
 constexpr int MAGIC = 0x4B400000;
 constexpr float MAGF = 12582912.0f;
+constexpr float LAZY = 64.0f;
 
 // One workgroup: 8 waves x 32 queries. Per key tile t a wave runs two phases, each an explicit slot schedule (one
 // MFMA per slot; a sched_barrier closes every slot, so its VALU work stays with it):
@@ -561,8 +562,12 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     float cc[NB], nbias[NB];
 
     // tile constants from the biased int row maxima mi of a tile's scores (K scales from its aux block):
-    // c = q_scale * k_scale * scale * log2(e) per 16-key group, m_t = tile max - log2(255), the running max and the
-    // two scales, then the per-block FMA bias -(12582912 c + m_t) that takes out the accumulator bias too.
+    // c = q_scale * k_scale * scale * log2(e) per 16-key group, m_t = tile max - log2(255), the row's reference m_run
+    // and the two scales, then the per-block FMA bias -(12582912 c + m_t) that takes out the accumulator bias too.
+    // The reference moves only when a tile's m_t passes it by more than LAZY (log2 units): a tile then enters O with
+    // weight ts = 2^(m_t - m_run) <= 2^LAZY, so O stays below 2^64 * 255 * 127 * cta * ntiles (far from the fp32
+    // range) and the rescale of O, which a running maximum would need on most tiles, is rare. O / l is the same
+    // softmax: every tile's weight relative to any fixed reference cancels in the quotient.
     auto constants = [&](const int (&mi)[NB], const uint8_t* st) {
         const uint8_t* ksp = st + 2 * TB + AUX_KS_OFF + 4 * NB * hf;
         float tmx = -INFINITY;
@@ -572,7 +577,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             tmx = fmaxf(tmx, (__int_as_float(mi[kb]) - MAGF) * cc[kb]);
         }
         tmx = pair_max(tmx) - S_U8_OFFSET;
-        const float m_new = fmaxf(m_run, tmx);
+        const float m_new = tmx > m_run + LAZY ? tmx : m_run;
         const float os = __builtin_amdgcn_exp2f(m_run - m_new);
         ts = __builtin_amdgcn_exp2f(tmx - m_new);
         m_run = m_new;
@@ -601,34 +606,38 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         if (t < ntiles) issue(t);
     wait_for(1, min(NS - 2, ntiles - 1));
     block_barrier();
-    i32x16 S[NB];
+    i32x16 SS[2][NB];  // S(t) in SS[t & 1]
     {
 #pragma unroll
-        for (int kb = 0; kb < NB; ++kb) S[kb] = magic;
+        for (int kb = 0; kb < NB; ++kb) SS[0][kb] = magic;
 #pragma unroll
         for (int f = 0; f < QS; ++f) {
             const int kb = NB == 4 ? 2 * (f >> 3) + (f & 1) : (f & 1);
             const int ks = NB == 4 ? (f >> 1) & 3 : f >> 1;
-            S[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kfrag(ring, f), Qf[ks], S[kb], 0, 0, 0);
+            SS[0][kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kfrag(ring, f), Qf[ks], SS[0][kb], 0, 0, 0);
         }
         int mi[NB];
-        rowmax(S, mi);
+        rowmax(SS[0], mi);
         constants(mi, ring);
     }
 
-    // One key tile. NEXT: S(t+1) is computed in phase A (every tile but the last); LAST: tile t is the last one (P
-    // of keys past Sk zeroed when it is partial). A partial last tile needs no mask for its row max: the prep fills
-    // its key rows past Sk with duplicates of real keys (same int8 row, same scale), which never exceed the max.
-    auto step = [&](int t, auto next_c, auto last_c) {
+    // One key tile: S holds S(t); NEXT: S(t+1) is computed into Sn in phase A (every tile but the last); LAST: tile t
+    // is the last one (P of keys past Sk zeroed when it is partial). A partial last tile needs no mask for its row
+    // max: the prep fills its key rows past Sk with duplicates of real keys (same int8 row, same scale), which never
+    // exceed the max. The two score arrays swap roles from tile to tile (the loop below takes tiles in pairs), so no
+    // registers are copied.
+    auto step = [&](int t, auto par_c, auto next_c, auto last_c) {
+        constexpr int PAR = decltype(par_c)::value;
         constexpr bool NEXT = decltype(next_c)::value;
         constexpr bool LAST = decltype(last_c)::value;
+        i32x16 (&S)[NB] = SS[PAR];
+        i32x16 (&Sn)[NB] = SS[PAR ^ 1];
         if (t + NS - 1 < ntiles) issue(t + NS - 1);
         const uint8_t* stK = ring + ((t + 1) % NS) * STAGE;
         const uint8_t* stV = ring + (t % NS) * STAGE;
         const bool mask_p = LAST && tail < CTA;
 
         // ---- phase A: S(t+1) on MFMA, P(t) on VALU
-        i32x16 Sn[NB];
         uint32_t P[NB][4];
         uint32_t rs = 0;
         i32x4 fr[3];
@@ -681,10 +690,11 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             const int bb = s / NB, j = s % NB;
             const i32x4 B = {(int)P[j][0], (int)P[j][1], (int)P[j][2], (int)P[j][3]};
             acc[bb & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[s % 3], B, j == 0 ? magic : acc[bb & 1], 0, 0, 0);
-            if (NEXT) {  // max of S(t+1): 4 registers per slot
+            if (NEXT) {  // max of S(t+1): its NB * 16 registers spread evenly over the PS slots (4 per slot)
+                static_assert(NB * 16 % (4 * PS) == 0, "whole groups of 4 registers per slot");
 #pragma unroll
-                for (int u = 0; u < 4 * NB * 16 / PS / 4; ++u) {
-                    const int g = (4 * NB * 16 / PS) * s + 4 * u;  // flat register index kb * 16 + r
+                for (int u = 0; u < NB * 16 / PS / 4; ++u) {
+                    const int g = (NB * 16 / PS) * s + 4 * u;  // flat register index kb * 16 + r, < NB * 16
                     const int kb = g >> 4, r = g & 15;
                     mi[kb] = max(max(mi[kb], Sn[kb][r]), max(max(Sn[kb][r + 1], Sn[kb][r + 2]), Sn[kb][r + 3]));
                 }
@@ -711,16 +721,25 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
         if (NEXT) {
             constants(mi, stK);
-#pragma unroll
-            for (int kb = 0; kb < NB; ++kb) S[kb] = Sn[kb];
             if (t + 2 < ntiles) wait_for(t + 2, min(ntiles - 1, t + NS - 1));
             else LR_I8_WAIT_VMCNT(0);
             block_barrier();
         }
     };
+    // the last tile (every load has landed: the wait before the previous barrier) has no S(t+1)
     int t = 0;
-    for (; t < ntiles - 1; ++t) step(t, std::true_type{}, std::false_type{});
-    step(t, std::false_type{}, std::true_type{});  // the last tile; every load has landed (the wait before the previous barrier)
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    for (; t + 2 < ntiles; t += 2) {
+        step(t, P0{}, std::true_type{}, std::false_type{});
+        step(t + 1, P1{}, std::true_type{}, std::false_type{});
+    }
+    if (t + 1 < ntiles) {
+        step(t, P0{}, std::true_type{}, std::false_type{});
+        step(t + 1, P1{}, std::false_type{}, std::true_type{});
+    } else {
+        step(t, P0{}, std::false_type{}, std::true_type{});
+    }
 
     if (!qok) return;
     const float inv = 1.0f / pair_sum(l_run);
