@@ -41,16 +41,24 @@ constexpr float S_U8_OFFSET = 7.9943534f;  // log2(255): the tile's largest P be
 // ------------------------------------------------------------------------------------------------ prep helpers
 // Exchange with lane ^ M inside each 32-lane half (ds_swizzle, bit-mask mode: and 0x1f, xor M).
 template <int M>
-__device__ __forceinline__ float xor32(float x) {
+__device__ __forceinline__ float xor_lane(float x) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (M << 10)));
 }
 
-__device__ __forceinline__ float max32(float x) {
-    x = fmaxf(x, xor32<1>(x));
-    x = fmaxf(x, xor32<2>(x));
-    x = fmaxf(x, xor32<4>(x));
-    x = fmaxf(x, xor32<8>(x));
-    return fmaxf(x, xor32<16>(x));
+// max over each 16-lane group (one row of 128 channels, 8 per lane)
+__device__ __forceinline__ float max16(float x) {
+    x = fmaxf(x, xor_lane<1>(x));
+    x = fmaxf(x, xor_lane<2>(x));
+    x = fmaxf(x, xor_lane<4>(x));
+    return fmaxf(x, xor_lane<8>(x));
+}
+
+// max over the wave
+__device__ __forceinline__ float max64(float x) {
+    x = max16(x);
+    x = fmaxf(x, xor_lane<16>(x));
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Round to nearest even, saturate to [-128, 127]; NaN -> 0 (float_utils.cuh:40-51).
@@ -60,59 +68,77 @@ __device__ __forceinline__ int rn_sat(float x) {
     return (int)r;
 }
 
+// The reference rotates a 128-channel row held as 4 channels per lane of 32 lanes (quant_qk_int8.cu:75-155):
+// [sign flip], H4 on the lane's 4 channels, [five butterflies over lane bits 1, 2, 4, 8, 16, then * 1/sqrt(128)].
+// Here a lane L of a 16-lane group holds 8 channels, those of the reference's lanes r = 2L and 2L + 1: the sign
+// flip and the H4 act on each 4-channel half, the butterfly over lane bit 1 pairs the two halves in registers, and
+// those over lane bits 2 .. 16 are butterflies over L's bits 1 .. 8. Every value sees the same operations in the
+// same order as in the reference, so the results are the same bits.
 template <int M>
-__device__ __forceinline__ void butterfly(float (&x)[4], int j) {
+__device__ __forceinline__ void butterfly8(float (&x)[8], int L) {
 #pragma clang fp contract(off)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const float o = xor32<M>(x[c]);
-        x[c] = (j & M) ? o - x[c] : x[c] + o;
+    for (int c = 0; c < 8; ++c) {
+        const float o = xor_lane<M>(x[c]);
+        x[c] = (L & M) ? o - x[c] : x[c] + o;
     }
 }
 
-// The rotation of one 128-channel row held as 4 channels (4j .. 4j+3) per lane j of a 32-lane half, in the
-// reference's operation order: [sign flip], H4 on the lane's 4 channels, [five butterflies over the lane index,
-// then * 1/sqrt(128)].
 template <int ROT>
-__device__ __forceinline__ void rotate(float (&x)[4], int j) {
+__device__ __forceinline__ void rotate8(float (&x)[8], int L) {
 #pragma clang fp contract(off)
     if (ROT == 128) {
-        const uint32_t w = j < 8 ? 0x1035997bu : j < 16 ? 0x8087f5eeu : j < 24 ? 0xee2e4e1au : 0x71132418u;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint32_t flip = ((w >> ((j & 7) * 4 + c)) & 1u) ^ 1u;
-            x[c] = __uint_as_float(__float_as_uint(x[c]) ^ (flip << 31));
+        for (int g = 0; g < 2; ++g) {
+            const int r = 2 * L + g;
+            const uint32_t w = r < 8 ? 0x1035997bu : r < 16 ? 0x8087f5eeu : r < 24 ? 0xee2e4e1au : 0x71132418u;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t flip = ((w >> ((r & 7) * 4 + c)) & 1u) ^ 1u;
+                x[4 * g + c] = __uint_as_float(__float_as_uint(x[4 * g + c]) ^ (flip << 31));
+            }
         }
     }
-    const float a0 = x[0] + x[1], a1 = x[0] - x[1], a2 = x[2] + x[3], a3 = x[2] - x[3];
-    x[0] = (a0 + a2) * 0.5f;
-    x[1] = (a1 + a3) * 0.5f;
-    x[2] = (a0 - a2) * 0.5f;
-    x[3] = (a1 - a3) * 0.5f;
-    if (ROT == 128) {
-        butterfly<1>(x, j);
-        butterfly<2>(x, j);
-        butterfly<4>(x, j);
-        butterfly<8>(x, j);
-        butterfly<16>(x, j);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) x[c] *= 0.1767766952966369f;
+    for (int g = 0; g < 2; ++g) {
+        float* y = x + 4 * g;
+        const float a0 = y[0] + y[1], a1 = y[0] - y[1], a2 = y[2] + y[3], a3 = y[2] - y[3];
+        y[0] = (a0 + a2) * 0.5f;
+        y[1] = (a1 + a3) * 0.5f;
+        y[2] = (a0 - a2) * 0.5f;
+        y[3] = (a1 - a3) * 0.5f;
+    }
+    if (ROT == 128) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {  // lane bit 1: reference lane 2L adds, lane 2L + 1 subtracts its own value
+            const float e = x[c], o = x[4 + c];
+            x[c] = e + o;
+            x[4 + c] = e - o;
+        }
+        butterfly8<1>(x, L);
+        butterfly8<2>(x, L);
+        butterfly8<4>(x, L);
+        butterfly8<8>(x, L);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) x[c] *= 0.1767766952966369f;
     }
 }
 
-__device__ __forceinline__ void load4(const uint16_t* p, float (&x)[4]) {
-    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
-    x[0] = lo_bf16(w[0]);
-    x[1] = hi_bf16(w[0]);
-    x[2] = lo_bf16(w[1]);
-    x[3] = hi_bf16(w[1]);
+__device__ __forceinline__ void load8(const uint16_t* p, float (&x)[8]) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[2 * j] = lo_bf16(w[j]);
+        x[2 * j + 1] = hi_bf16(w[j]);
+    }
 }
 
-__device__ __forceinline__ uint32_t pack_s8(const float (&x)[4], float inv) {
+// 8 values * inv, rounded and saturated to int8, as two little-endian words
+__device__ __forceinline__ u32x2 pack_s8x8(const float (&x)[8], float inv) {
 #pragma clang fp contract(off)
-    uint32_t w = 0;
+    u32x2 w = {0u, 0u};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) w |= (uint32_t)(rn_sat(x[c] * inv) & 0xff) << (8 * c);
+    for (int c = 0; c < 8; ++c) w[c >> 2] |= (uint32_t)(rn_sat(x[c] * inv) & 0xff) << (8 * (c & 3));
     return w;
 }
 
@@ -221,103 +247,105 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ prep launch 2
-// Q: 16 rows of head h per block; each 32-lane half holds one row (4 channels per lane), one scale per row.
+// Rows are read 16 bytes (8 channels) a lane, 16 lanes a row.
+constexpr int QROWS = 64;  // query rows per block
+constexpr int KROWS = 64;  // key rows per block: four scale groups of 16, one per wave
+
+// Q: QROWS rows of head h per block, 16 per pass, one scale per row.
 template <int ROT>
 __device__ void quant_q(const PrepArgs& a, int b, int h, int qb) {
 #pragma clang fp contract(off)
     const Plan& p = a.p;
-    const int t = threadIdx.x, slot = t >> 5, j = t & 31;
+    const int t = threadIdx.x, slot = t >> 4, L = t & 15;
+    float xs[QROWS / 16][8];  // every row of the lane loaded before the first rotation: all loads in flight at once
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int row = qb * 16 + slot + 8 * i;
+    for (int i = 0; i < QROWS / 16; ++i) {
+        const int row = qb * QROWS + 16 * i + slot;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) xs[i][c] = 0.0f;
+        if (row < a.Sq) load8(a.q + b * a.q_sb + h * a.q_sh + (int64_t)row * a.q_sn + 8 * L, xs[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < QROWS / 16; ++i) {
+        const int row = qb * QROWS + 16 * i + slot;
         const bool ok = row < a.Sq;
-        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (ok) load4(a.q + b * a.q_sb + h * a.q_sh + (int64_t)row * a.q_sn + 4 * j, x);
-        rotate<ROT>(x, j);
-        const float mx = max32(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
+        float (&x)[8] = xs[i];
+        rotate8<ROT>(x, L);
+        float m = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) m = fmaxf(m, fabsf(x[c]));
+        const float mx = max16(m);
         const float sc = mx / 127.0f + 1e-7f;
         const float inv = 1.0f / sc;
         if (ok) {
             const size_t r = (size_t)(b * a.H + h) * a.Sq + row;
-            *reinterpret_cast<uint32_t*>(a.ws + p.q8 + r * 128 + 4 * j) = pack_s8(x, inv);
-            if (j == 0) reinterpret_cast<float*>(a.ws + p.qs)[r] = sc;
+            *reinterpret_cast<u32x2*>(a.ws + p.q8 + r * 128 + 8 * L) = pack_s8x8(x, inv);
+            if (L == 0) reinterpret_cast<float*>(a.ws + p.qs)[r] = sc;
         }
     }
 }
 
-// K: 32 key rows (two scale groups of 16) of kv head hk per block, the anchor row subtracted before the rotation.
+// K: KROWS key rows of kv head hk per block; wave w holds scale group 4 kb + w (16 rows, 4 a pass), the anchor row
+// subtracted before the rotation.
 template <int ROT>
 __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
 #pragma clang fp contract(off)
-    __shared__ float red[2][8];
     const Plan& p = a.p;
-    const int t = threadIdx.x, slot = t >> 5, j = t & 31;
+    const int t = threadIdx.x, wave = t >> 6, rsub = (t >> 4) & 3, L = t & 15;
+    const int grp = kb * (KROWS / KGROUP) + wave;  // keys 16 grp .. + 15
     const int anc = reinterpret_cast<const int*>(a.ws + p.anchor)[b * a.HK + hk];
-    const uint16_t* kbase = a.k + b * a.k_sb + hk * a.k_sh + 4 * j;
-    float av[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (anc >= 0) load4(kbase + (int64_t)anc * a.k_sn, av);
+    const uint16_t* kbase = a.k + b * a.k_sb + hk * a.k_sh + 8 * L;
+    float av[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (anc >= 0) load8(kbase + (int64_t)anc * a.k_sn, av);
     // Rows past Sk (the last tile's padding) repeat real keys: those of the last key's scale group gL, key Sk - 1
     // standing in past its end. A padded row of group gL then equals key Sk - 1 and leaves the group's scale as it
     // is; a wholly padded group is a copy of group gL, scale included. Their scores equal real scores, so they never
     // raise a row max; the attention zeroes their P.
     const int last = a.Sk - 1, gl = last / KGROUP;
-    float x[4][4], m[4];
+    float x[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // all four rows in flight before the first rotation
+        const int row = grp * KGROUP + 4 * i + rsub;
+        const int src = row <= last ? row : min(gl * KGROUP + (row & (KGROUP - 1)), last);
+        load8(kbase + (int64_t)src * a.k_sn, x[i]);
+    }
+    float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int row = kb * 32 + slot + 8 * i;
-        const int src = row <= last ? row : min(gl * KGROUP + (row & (KGROUP - 1)), last);
-        float v[4];
-        load4(kbase + (int64_t)src * a.k_sn, v);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = v[c] - av[c];
-        rotate<ROT>(v, j);
+        for (int c = 0; c < 8; ++c) x[i][c] = x[i][c] - av[c];
+        rotate8<ROT>(x[i], L);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) x[i][c] = v[c];
-        m[i] = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        for (int c = 0; c < 8; ++c) m = fmaxf(m, fabsf(x[i][c]));
     }
-    const float g0 = max32(fmaxf(m[0], m[1])), g1 = max32(fmaxf(m[2], m[3]));
-    if (j == 0) {
-        red[0][slot] = g0;
-        red[1][slot] = g1;
-    }
-    __syncthreads();
-    float mx[2] = {0.0f, 0.0f};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        mx[0] = fmaxf(mx[0], red[0][s]);
-        mx[1] = fmaxf(mx[1], red[1][s]);
-    }
-    float sc[2], inv[2];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        sc[g] = mx[g] / 127.0f + 1e-7f;
-        inv[g] = 1.0f / sc[g];
-    }
+    const float mx = max64(m);
+    const float sc = mx / 127.0f + 1e-7f;
+    const float inv = 1.0f / sc;
     uint8_t* k8 = a.ws + p.k8 + (size_t)(b * a.HK + hk) * p.skp * 128;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int row = kb * 32 + slot + 8 * i;
-        *reinterpret_cast<uint32_t*>(k8 + (size_t)row * 128 + 16 * ((j >> 2) ^ k_swz(row & 31)) + 4 * (j & 3)) =
-            pack_s8(x[i], inv[i >> 1]);
+        const int row = grp * KGROUP + 4 * i + rsub;
+        *reinterpret_cast<u32x2*>(k8 + (size_t)row * 128 + 16 * ((L >> 1) ^ k_swz(row & 31)) + 8 * (L & 1)) =
+            pack_s8x8(x[i], inv);
     }
-    if (t == 0 || t == 32) {
-        const int g = t >> 5, grp = kb * 2 + g;  // keys 16 grp .. + 15
+    if ((t & 63) == 0) {
         const int tile = grp * KGROUP / p.cta, local = grp * KGROUP - tile * p.cta;
         const int blk = local >> 5, half = (local >> 4) & 1;
         float* ks = reinterpret_cast<float*>(a.ws + p.aux + ((size_t)(b * a.HK + hk) * p.ntiles + tile) * AUX_BYTES +
                                              AUX_KS_OFF);
-        ks[half * (p.cta / 32) + blk] = sc[g];
+        ks[half * (p.cta / 32) + blk] = sc;
     }
 }
 
 // V: one tile of cta keys of kv head hk per block: per-channel scales from the abs-max partials, int8, transposed into
-// [128 dims][cta keys], column sums per half tile into the aux block, then stored swizzled.
+// [128 dims][cta keys] in LDS (rows padded by 4 bytes, so that the lanes of a wave, which write different dims, spread
+// over the banks), column sums per half tile into the aux block, then stored swizzled.
 __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
 #pragma clang fp contract(off)
     __shared__ float inv_s[128];
-    __shared__ __attribute__((aligned(16))) uint8_t vts[128 * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t vts[128 * (128 + 4)];
     const Plan& p = a.p;
-    const int cta = p.cta, t = threadIdx.x;
+    const int cta = p.cta, vs = cta + 4, t = threadIdx.x;
     const size_t bhk = (size_t)b * a.HK + hk;
     if (t < 128) {
         const float* vpart = reinterpret_cast<const float*>(a.ws + p.vpart) + bhk * p.nvchunk * 128;
@@ -328,26 +356,32 @@ __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
         if (tile == 0) reinterpret_cast<float*>(a.ws + p.vs)[bhk * 128 + t] = sc;
     }
     __syncthreads();
-    const int cq = t & 31, k0 = t >> 5;
-    float inv[4];
+    const int c8 = t & 15, k0 = t >> 4;  // channels 8 c8 .. + 7; key quads k0, k0 + 16, ...
+    float inv[8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) inv[c] = inv_s[4 * cq + c];
-    const uint16_t* vb = a.v + b * a.v_sb + hk * a.v_sh + 4 * cq;
-    for (int i = 0; i < cta / 32; ++i) {
-        const int kq = k0 + 8 * i;  // keys 4 kq .. 4 kq + 3 of the tile
-        uint32_t col[4] = {0u, 0u, 0u, 0u};
+    for (int c = 0; c < 8; ++c) inv[c] = inv_s[8 * c8 + c];
+    const uint16_t* vb = a.v + b * a.v_sb + hk * a.v_sh + 8 * c8;
+    for (int i = 0; i < cta / 64; ++i) {
+        const int kq = k0 + 16 * i;  // keys 4 kq .. 4 kq + 3 of the tile
+        u32x4 raw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {  // the four keys in flight together
+            const int key = tile * cta + 4 * kq + r;
+            raw[r] = key < a.Sk ? *reinterpret_cast<const u32x4*>(vb + (int64_t)key * a.v_sn) : u32x4{0u, 0u, 0u, 0u};
+        }
+        uint32_t col[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int key = tile * cta + 4 * kq + r;
-            if (key < a.Sk) {
-                float x[4];
-                load4(vb + (int64_t)key * a.v_sn, x);
+            if (tile * cta + 4 * kq + r < a.Sk) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) col[c] |= (uint32_t)(rn_sat(x[c] * inv[c]) & 0xff) << (8 * r);
+                for (int j = 0; j < 4; ++j) {
+                    col[2 * j] |= (uint32_t)(rn_sat(lo_bf16(raw[r][j]) * inv[2 * j]) & 0xff) << (8 * r);
+                    col[2 * j + 1] |= (uint32_t)(rn_sat(hi_bf16(raw[r][j]) * inv[2 * j + 1]) & 0xff) << (8 * r);
+                }
             }
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) *reinterpret_cast<uint32_t*>(vts + (4 * cq + c) * cta + 4 * kq) = col[c];
+        for (int c = 0; c < 8; ++c) *reinterpret_cast<uint32_t*>(vts + (8 * c8 + c) * vs + 4 * kq) = col[c];
     }
     __syncthreads();
     uint8_t* aux = a.ws + p.aux + (bhk * p.ntiles + tile) * AUX_BYTES;
@@ -355,7 +389,7 @@ __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
         const int d = t & 127, half = t >> 7;
         int s = 0;
         for (int w = 0; w < cta / 8; ++w)
-            s = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(vts + d * cta + half * (cta / 2) + 4 * w),
+            s = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(vts + d * vs + half * (cta / 2) + 4 * w),
                                        0x01010101, s, false);
         reinterpret_cast<int16_t*>(aux)[(half * 32 + (d & 31)) * 4 + (d >> 5)] = (int16_t)s;
     }
@@ -363,16 +397,17 @@ __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
     const int cpr = cta / 16;  // chunks per dim row
     for (int idx = t; idx < 128 * cpr; idx += 256) {
         const int d = idx / cpr, c = idx - d * cpr;
-        *reinterpret_cast<u32x4*>(vt + d * cta + 16 * (c ^ v_swz(d, cta))) =
-            *reinterpret_cast<const u32x4*>(vts + d * cta + 16 * c);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(vts + d * vs + 16 * c);
+        const u32x4 w = {src[0], src[1], src[2], src[3]};
+        *reinterpret_cast<u32x4*>(vt + d * cta + 16 * (c ^ v_swz(d, cta))) = w;
     }
 }
 
-// grid (ceil(Sq/16) + skp/32 + ntiles, max(H, HK), B): Q blocks, then K blocks, then V tiles.
+// grid (ceil(Sq / QROWS) + skp / KROWS + ntiles, max(H, HK), B): Q blocks, then K blocks, then V tiles.
 template <int ROT>
 __global__ __launch_bounds__(256) void i8_quant_kernel(PrepArgs a) {
     const int b = blockIdx.z, y = blockIdx.y;
-    const int nqb = (a.Sq + 15) / 16, nkb = a.p.skp / 32;
+    const int nqb = (a.Sq + QROWS - 1) / QROWS, nkb = a.p.skp / KROWS;
     int x = blockIdx.x;
     if (x < nqb) {
         if (y < a.H) quant_q<ROT>(a, b, y, x);
@@ -765,7 +800,7 @@ hipError_t launch_prep(const PrepArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(i8_stats_kernel, dim3(p.nvchunk + 1, a.HK, a.B), dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 grid((a.Sq + 15) / 16 + p.skp / 32 + p.ntiles, a.H > a.HK ? a.H : a.HK, a.B);
+    const dim3 grid((a.Sq + QROWS - 1) / QROWS + p.skp / KROWS + p.ntiles, a.H > a.HK ? a.H : a.HK, a.B);
     if (p.rot == 4)
         hipLaunchKernelGGL(i8_quant_kernel<4>, grid, dim3(256), 0, stream, a);
     else
