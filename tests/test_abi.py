@@ -174,6 +174,8 @@ def test_int8_workspace_bytes():
                  (1, 2, 2, 1025, 1025)):
         assert L.lr_int8_attention_workspace_bytes(*args, 128) == _i8_plan(*args), args
     assert L.lr_int8_attention_workspace_bytes(1, 2, 2, 8, 8, 64) == 0       # head dim 64 is not built
+    # the wheel's head-dim-64 case (kitchen_launch.cu:196), e.g. 1797 tokens of 32 heads x 64: rejected, not computed
+    assert L.lr_int8_attention_workspace_bytes(1, 32, 32, 1797, 1797, 64) == 0
     assert L.lr_int8_attention_workspace_bytes(1, 3, 2, 8, 8, 128) == 0      # H % HK
     assert L.lr_int8_attention_workspace_bytes(0, 2, 2, 8, 8, 128) == 0
 
@@ -194,6 +196,9 @@ def test_int8_rejects():
                     (dict(o=A + 2), "misaligned out")):
         assert call(**kw) == HIP_ERROR_INVALID_VALUE, why
     assert call("lr_int8_attention_rows", B=2, q_sb=8 * 768) == HIP_ERROR_INVALID_VALUE  # rows: B 1 only
+    d64 = dict(H=32, HK=32, Sq=1797, Sk=1797, D=64, q_sh=64, q_sn=3 * 32 * 64, k_sh=64, k_sn=3 * 32 * 64, v_sh=64,
+               v_sn=3 * 32 * 64)
+    assert call(**d64) == HIP_ERROR_INVALID_VALUE and call("lr_int8_attention_rows", **d64) == HIP_ERROR_INVALID_VALUE
     assert L.lr_int8_attention_kernel(A, 0x100000, 1, 2, 2, 8, 8, 128, 0.088, 2, None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_int8_attention_prep(A, A, A, A + 64, 1, 2, 2, 8, 8, 128, 0, 768, 1536, 0, 768, 1536, 0, 768, 1536,
                                     None) == HIP_ERROR_INVALID_VALUE
