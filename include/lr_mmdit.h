@@ -16,7 +16,9 @@
  *
  * Weights are bf16 row-major [out, in] (torch nn.Linear layout), no biases; LayerNorm without affine, eps 1e-6;
  * activations bf16 between the steps (fp32 inside each kernel and GEMM). The GEMMs are hipBLASLt's (bf16 in and out,
- * fp32 compute); everything else is this library's HIP kernels.
+ * fp32 compute); the up-projection carries hipBLASLt's GELU epilogue where an algorithm has it, so its GELU acts on
+ * the fp32 product (one bf16 rounding, not two; a shape without such an algorithm runs the library's GELU-tanh
+ * kernel on the bf16 product). Everything else is this library's HIP kernels.
  *
  * Return values follow lr_attn.h: 0 launched, 1 (hipErrorInvalidValue) an argument rejected before any launch, other
  * hipError_t / hipblasStatus_t failures as returned (a hipBLASLt status is reported as 1000 + the status).

@@ -197,7 +197,10 @@ struct GemmPlan {
     hipblasLtMatmulAlgo_t algo{};
     size_t ws = 0;
 };
-using GemmKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>;   // M, N, K, ldx, ldy
+// M, N, K, ldx, ldy, epilogue (EPI_NONE, or EPI_GELU: y = GELU(x w^T) applied to the fp32 result before the bf16
+// store, hipBLASLt's GELU epilogue, which takes the place of gelu_tanh_kernel for the MLP up-projection)
+using GemmKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int>;
+constexpr int EPI_NONE = 0, EPI_GELU = 1;
 
 // A context's plans are built by lr_mmdit_plan / lr_mmdit_tune (and by lr_mmdit_linear_bf16 for a new shape) under
 // `mu`; the block call only looks them up. A plan is never removed before the context is destroyed, so a pointer to
@@ -219,15 +222,16 @@ void destroy_plan(GemmPlan& p) {
 }
 
 // The plan of one GEMM shape, if built (caller holds c.mu or only reads a map no one is changing).
-GemmPlan* find_plan(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
-    auto it = c.plans.find(GemmKey{M, N, K, ldx, ldy});
+GemmPlan* find_plan(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, int epi = EPI_NONE) {
+    auto it = c.plans.find(GemmKey{M, N, K, ldx, ldy, epi});
     return it == c.plans.end() ? nullptr : &it->second;
 }
 
 // Build (heuristic-first) and keep the plan of one GEMM shape; every handle created on a failed path is destroyed.
-int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, GemmPlan** out) {
+// A GELU plan for which hipBLASLt has no algorithm fails with 1000 + HIPBLAS_STATUS_NOT_SUPPORTED.
+int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, int epi, GemmPlan** out) {
     std::lock_guard<std::mutex> lock(c.mu);
-    if (GemmPlan* found = find_plan(c, M, N, K, ldx, ldy)) {
+    if (GemmPlan* found = find_plan(c, M, N, K, ldx, ldy, epi)) {
         *out = found;
         return 0;
     }
@@ -245,6 +249,11 @@ int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
         return fail(rc);
     if ((rc = blas_err(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb))))
         return fail(rc);
+    if (epi == EPI_GELU) {
+        const hipblasLtEpilogue_t e = HIPBLASLT_EPILOGUE_GELU;
+        if ((rc = blas_err(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &e, sizeof e))))
+            return fail(rc);
+    }
     if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K)))) return fail(rc);
     if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, ldx)))) return fail(rc);
     if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, ldy)))) return fail(rc);
@@ -261,7 +270,7 @@ int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
     hipblasLtMatmulPreferenceDestroy(pref);
     p.algo = res[0].algo;
     p.ws = res[0].workspaceSize;
-    auto ins = c.plans.emplace(GemmKey{M, N, K, ldx, ldy}, p);
+    auto ins = c.plans.emplace(GemmKey{M, N, K, ldx, ldy, epi}, p);
     *out = &ins.first->second;
     return 0;
 }
@@ -269,9 +278,9 @@ int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
 // Time up to `cands` heuristic candidates of one GEMM on the given buffers and keep the fastest as its plan
 // (replacing a heuristic-first plan). Synchronises on its own events.
 int tune_gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, int64_t M, int64_t N,
-              int64_t K, void* ws, hipStream_t s, int cands) {
+              int64_t K, int epi, void* ws, hipStream_t s, int cands) {
     GemmPlan* p;
-    int rc = plan_gemm(c, M, N, K, ldx, ldy, &p);
+    int rc = plan_gemm(c, M, N, K, ldx, ldy, epi, &p);
     if (rc) return rc;
     hipblasLtMatmulPreference_t pref;
     if ((rc = blas_err(hipblasLtMatmulPreferenceCreate(&pref)))) return rc;
@@ -323,7 +332,7 @@ bool is_vector(int64_t M, int64_t K, const void* X, const void* W) {
 // One GEMM on the stream. plan_new: build the shape's plan if missing (lr_mmdit_linear_bf16); otherwise the plan must
 // exist (the block call, which checked every plan before its first launch).
 int gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-         void* ws, hipStream_t s, bool plan_new = false) {
+         void* ws, hipStream_t s, bool plan_new = false, int epi = EPI_NONE) {
     if (is_vector(M, K, X, W)) {   // a vector: HBM-bound
         hipLaunchKernelGGL(gemv_kernel, dim3((unsigned)((N + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), 0,
                            s, static_cast<const uint16_t*>(X), static_cast<const uint16_t*>(W),
@@ -333,10 +342,10 @@ int gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy
     GemmPlan* p = nullptr;
     int rc = 0;
     if (plan_new) {
-        rc = plan_gemm(c, M, N, K, ldx, ldy, &p);
+        rc = plan_gemm(c, M, N, K, ldx, ldy, epi, &p);
     } else {
         std::lock_guard<std::mutex> lock(c.mu);
-        p = find_plan(c, M, N, K, ldx, ldy);
+        p = find_plan(c, M, N, K, ldx, ldy, epi);
         if (!p) rc = (int)hipErrorNotReady;
     }
     if (rc) return rc;
@@ -348,17 +357,36 @@ int gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // The row GEMMs of one block call (M > 1: the vectors go to gemv_kernel): QKV, out, MLP up and down, per stream of rows,
-// as {M, N, K, ldx, ldy}.
+// as {M, N, K, ldx, ldy, epilogue}. The up-projection is listed with its GELU epilogue; a context where hipBLASLt has no
+// algorithm for that holds the plain plan instead and the block applies gelu_tanh_kernel (up_epi).
 std::vector<GemmKey> block_gemms(int64_t n_txt, int64_t n_img, int64_t D, int64_t F) {
     std::vector<GemmKey> g;
     for (const int64_t M : {n_txt, n_img}) {
         if (M <= 1) continue;
-        g.push_back(GemmKey{M, 3 * D, D, D, 3 * D});
-        g.push_back(GemmKey{M, D, D, D, D});
-        g.push_back(GemmKey{M, F, D, D, F});
-        g.push_back(GemmKey{M, D, F, F, D});
+        g.push_back(GemmKey{M, 3 * D, D, D, 3 * D, EPI_NONE});
+        g.push_back(GemmKey{M, D, D, D, D, EPI_NONE});
+        g.push_back(GemmKey{M, F, D, D, F, EPI_GELU});
+        g.push_back(GemmKey{M, D, F, F, D, EPI_NONE});
     }
     return g;
+}
+
+// The epilogue the context's plan of an up-projection shape has: EPI_GELU when hipBLASLt had an algorithm for it,
+// else EPI_NONE (-1: neither is planned). Caller holds c.mu.
+int up_epi(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
+    if (find_plan(c, M, N, K, ldx, ldy, EPI_GELU)) return EPI_GELU;
+    return find_plan(c, M, N, K, ldx, ldy, EPI_NONE) ? EPI_NONE : -1;
+}
+
+// Plan one block GEMM; the up-projection falls back to the plain plan (and gelu_tanh_kernel) when hipBLASLt has no
+// algorithm with the GELU epilogue for it.
+int plan_block_gemm(Ctx& c, const GemmKey& k) {
+    GemmPlan* p;
+    int rc = plan_gemm(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k),
+                       std::get<5>(k), &p);
+    if (rc && std::get<5>(k) == EPI_GELU)
+        rc = plan_gemm(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k), EPI_NONE, &p);
+    return rc;
 }
 
 // scratch layout of one block call
@@ -434,8 +462,7 @@ int lr_mmdit_plan(void* ctx, int n_txt, int n_img, int hidden, int mlp) {
     if (!ctx || lr_mmdit_workspace_bytes(n_txt, n_img, hidden, mlp) == 0) return hipErrorInvalidValue;
     Ctx& c = *static_cast<Ctx*>(ctx);
     for (const GemmKey& k : block_gemms(n_txt, n_img, hidden, mlp)) {
-        GemmPlan* p;
-        const int rc = plan_gemm(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k), &p);
+        const int rc = plan_block_gemm(c, k);
         if (rc) return rc;
     }
     return 0;
@@ -463,10 +490,18 @@ int lr_mmdit_tune(void* ctx, const lr_mmdit_weights* w, int n_txt, int n_img, in
     for (int k = 0; k < 2 && rc == 0; ++k) {
         const int64_t M = rows[k], r0 = row0[k];
         if (M <= 1) continue;
-        if (!rc) rc = tune_gemm(c, hn + r0 * D, D, sw[k]->qkv, qkv + r0 * 3 * D, 3 * D, M, 3 * D, D, gws, s, candidates);
-        if (!rc) rc = tune_gemm(c, attn + r0 * D, D, sw[k]->out, hn + r0 * D, D, M, D, D, gws, s, candidates);
-        if (!rc) rc = tune_gemm(c, hn + r0 * D, D, sw[k]->mlp_up, big + r0 * F, F, M, F, D, gws, s, candidates);
-        if (!rc) rc = tune_gemm(c, big + r0 * F, F, sw[k]->mlp_down, attn + r0 * D, D, M, D, F, gws, s, candidates);
+        if (!rc) rc = plan_block_gemm(c, GemmKey{M, F, D, D, F, EPI_GELU});
+        int epi = EPI_NONE;
+        if (!rc) {
+            std::lock_guard<std::mutex> lock(c.mu);
+            epi = up_epi(c, M, F, D, D, F);
+        }
+        if (!rc) rc = tune_gemm(c, hn + r0 * D, D, sw[k]->qkv, qkv + r0 * 3 * D, 3 * D, M, 3 * D, D, EPI_NONE, gws, s,
+                                candidates);
+        if (!rc) rc = tune_gemm(c, attn + r0 * D, D, sw[k]->out, hn + r0 * D, D, M, D, D, EPI_NONE, gws, s, candidates);
+        if (!rc) rc = tune_gemm(c, hn + r0 * D, D, sw[k]->mlp_up, big + r0 * F, F, M, F, D, epi, gws, s, candidates);
+        if (!rc) rc = tune_gemm(c, big + r0 * F, F, sw[k]->mlp_down, attn + r0 * D, D, M, D, F, EPI_NONE, gws, s,
+                                candidates);
     }
     return rc;
 }
@@ -493,11 +528,21 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     if ((((uintptr_t)txt | (uintptr_t)img | (uintptr_t)workspace) & 15) != 0) return hipErrorInvalidValue;
 
     Ctx& c = *static_cast<Ctx*>(ctx);
-    {   // every row GEMM's plan exists (lr_mmdit_plan / lr_mmdit_tune), checked before anything is launched
+    // every row GEMM's plan exists (lr_mmdit_plan / lr_mmdit_tune), checked before anything is launched; the
+    // up-projection of a stream of rows (text 0, image 1) has its GELU fused when its plan carries the epilogue
+    bool gelu_fused[2] = {false, false};
+    {
         std::lock_guard<std::mutex> lock(c.mu);
-        for (const GemmKey& k : block_gemms(n_txt, n_img, hidden, mlp))
-            if (!find_plan(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k)))
+        const int64_t rows[2] = {n_txt, n_img}, D = hidden, F = mlp;
+        for (int k = 0; k < 2; ++k) {
+            const int64_t M = rows[k];
+            if (M <= 1) continue;   // a vector: gemv_kernel, no plan
+            if (!find_plan(c, M, 3 * D, D, D, 3 * D) || !find_plan(c, M, D, D, D, D) || !find_plan(c, M, D, F, F, D))
                 return hipErrorNotReady;
+            const int e = up_epi(c, M, F, D, D, F);
+            if (e < 0) return hipErrorNotReady;
+            gelu_fused[k] = e == EPI_GELU;
+        }
     }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t D = hidden, F = mlp, S = (int64_t)n_txt + n_img, H = D / 128;
@@ -560,11 +605,20 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     hipLaunchKernelGGL(ln_modulate_kernel, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D, mod_txt,
                        mod_img, 1, hn);
     LR_LAUNCHED();
-    LR_TRY(pair_gemm(hn, hn + tD, D, w->txt.mlp_up, w->img.mlp_up, big, big + tF, F, F, D));
-    const int64_t n8 = S * F / 8;
-    hipLaunchKernelGGL(gelu_tanh_kernel, dim3((unsigned)((n8 + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s,
-                       big, n8);
-    LR_LAUNCHED();
+    if (n_txt > 0)
+        LR_TRY(gemm(c, hn, D, w->txt.mlp_up, big, F, n_txt, F, D, gws, s, false, gelu_fused[0] ? EPI_GELU : EPI_NONE));
+    if (n_img > 0)
+        LR_TRY(gemm(c, hn + tD, D, w->img.mlp_up, big + tF, F, n_img, F, D, gws, s, false,
+                    gelu_fused[1] ? EPI_GELU : EPI_NONE));
+    {   // GELU-tanh over the hidden rows whose up-projection did not apply it (text rows first in `big`)
+        const int64_t r0 = gelu_fused[0] ? n_txt : 0, r1 = gelu_fused[1] ? n_txt : S;
+        const int64_t n8 = (r1 - r0) * F / 8;
+        if (n8 > 0) {
+            hipLaunchKernelGGL(gelu_tanh_kernel, dim3((unsigned)((n8 + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS),
+                               0, s, big + r0 * F, n8);
+            LR_LAUNCHED();
+        }
+    }
     LR_TRY(pair_gemm(big, big + tF, F, w->txt.mlp_down, w->img.mlp_down, attn, attn + tD, D, D, F));
     hipLaunchKernelGGL(gated_residual_kernel, dim3(res_blocks), dim3(EW_THREADS), 0, s, xt, xi, n_txt, (int)S, (int)D,
                        attn, mod_txt, mod_img, 1);
