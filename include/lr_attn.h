@@ -265,14 +265,14 @@ int lr_joint_attention_fused_noalloc(const void* q_raw, const void* k_raw, const
 
 /*
  * MiniMax H3's INT8 attention (the reference's comfy-kitchen SageAttention chain): per kv head a K anchor, Q and K
- * rotated (H4 blocks when Sk <= 256, else the signed H128) and quantised to int8, V quantised per channel, then
- * out = softmax(scale * Q K^T) V with int8 Q K^T and u8 P x s8 V products (P rounded per key tile of 64 keys, 128 past
- * Sk = 1024). Arguments as kitchen_int8_attention (kitchen_launch.cu:193-270):
+ * rotated (H4 blocks when Sk <= 256, else the signed H128 / the plain H64) and quantised to int8, V quantised per
+ * channel, then out = softmax(scale * Q K^T) V with int8 Q K^T and u8 P x s8 V products (P rounded per key tile of
+ * 64 keys, 128 past Sk = 1024 at head dim 128). Arguments as kitchen_int8_attention (kitchen_launch.cu:193-270):
  *   q [B][H][Sq][D], k and v [B][HK][Sk][D] bf16 with element strides (sb, sh, sn) per tensor, last stride 1; each
  *   stride a multiple of 8 elements and each base 16-byte aligned (views into one packed qkv buffer qualify);
- *   D must be 128 (the wheel's head dim 64, kitchen_launch.cu:196-241, is not built here: the engines call the chain
- *   with 128 only, launch.zig:331; D 64 returns hipErrorInvalidValue and a workspace size of 0); H a multiple of HK;
- *   scale > 0 (the reference passes 128^-0.5 rounded to fp32, 0x3db504f3);
+ *   D 128 (the engine's, launch.zig:331) or 64 (the wheel's other case, kitchen_launch.cu:196-241: H4 up to 256 keys,
+ *   else the plain H64 without the sign flip, 64-key tiles at every length); H a multiple of HK; scale > 0 (the
+ *   reference passes D^-0.5 rounded to fp32: 0x3db504f3 for 128);
  *   workspace: lr_int8_attention_workspace_bytes(B, H, HK, Sq, Sk, D) bytes, 256-byte aligned, no initial contents.
  * lr_int8_attention writes out bf16 [B][H][Sq][D] contiguous; lr_int8_attention_rows writes rows [Sq][H * D]
  * (B must be 1), the same values. The workspace layout is this library's own (quantised operands, scales, per-tile

@@ -45,17 +45,19 @@ __device__ __forceinline__ float xor_lane(float x) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (M << 10)));
 }
 
-// max over each 16-lane group (one row of 128 channels, 8 per lane)
-__device__ __forceinline__ float max16(float x) {
+// max over each group of LPR lanes (one row of 8 * LPR channels, 8 per lane)
+template <int LPR>
+__device__ __forceinline__ float max_row(float x) {
     x = fmaxf(x, xor_lane<1>(x));
     x = fmaxf(x, xor_lane<2>(x));
     x = fmaxf(x, xor_lane<4>(x));
-    return fmaxf(x, xor_lane<8>(x));
+    if (LPR == 16) x = fmaxf(x, xor_lane<8>(x));
+    return x;
 }
 
 // max over the wave
 __device__ __forceinline__ float max64(float x) {
-    x = max16(x);
+    x = max_row<16>(x);
     x = fmaxf(x, xor_lane<16>(x));
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -69,11 +71,12 @@ __device__ __forceinline__ int rn_sat(float x) {
 }
 
 // The reference rotates a 128-channel row held as 4 channels per lane of 32 lanes (quant_qk_int8.cu:75-155):
-// [sign flip], H4 on the lane's 4 channels, [five butterflies over lane bits 1, 2, 4, 8, 16, then * 1/sqrt(128)].
-// Here a lane L of a 16-lane group holds 8 channels, those of the reference's lanes r = 2L and 2L + 1: the sign
-// flip and the H4 act on each 4-channel half, the butterfly over lane bit 1 pairs the two halves in registers, and
-// those over lane bits 2 .. 16 are butterflies over L's bits 1 .. 8. Every value sees the same operations in the
-// same order as in the reference, so the results are the same bits.
+// [sign flip], H4 on the lane's 4 channels, [five butterflies over lane bits 1, 2, 4, 8, 16, then * 1/sqrt(128)];
+// a 64-channel row (convrot64) as 4 channels per lane of 16 lanes: H4, four butterflies over lane bits 1 .. 8, * 1/4.
+// Here a lane L of a group of 16 (8 at head dim 64) holds 8 channels, those of the reference's lanes r = 2L and
+// 2L + 1: the sign flip and the H4 act on each 4-channel half, the butterfly over lane bit 1 pairs the two halves in
+// registers, and those over lane bits 2 .. 16 (2 .. 8) are butterflies over L's bits 1 .. 8 (1 .. 4). Every value
+// sees the same operations in the same order as in the reference, so the results are the same bits.
 template <int M>
 __device__ __forceinline__ void butterfly8(float (&x)[8], int L) {
 #pragma clang fp contract(off)
@@ -108,7 +111,7 @@ __device__ __forceinline__ void rotate8(float (&x)[8], int L) {
         y[2] = (a0 - a2) * 0.5f;
         y[3] = (a1 - a3) * 0.5f;
     }
-    if (ROT == 128) {
+    if (ROT == 128 || ROT == 64) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {  // lane bit 1: reference lane 2L adds, lane 2L + 1 subtracts its own value
             const float e = x[c], o = x[4 + c];
@@ -118,9 +121,10 @@ __device__ __forceinline__ void rotate8(float (&x)[8], int L) {
         butterfly8<1>(x, L);
         butterfly8<2>(x, L);
         butterfly8<4>(x, L);
-        butterfly8<8>(x, L);
+        if (ROT == 128) butterfly8<8>(x, L);
+        const float norm = ROT == 128 ? 0.1767766952966369f : 0.25f;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) x[c] *= 0.1767766952966369f;
+        for (int c = 0; c < 8; ++c) x[c] *= norm;
     }
 }
 
@@ -150,17 +154,19 @@ __device__ __forceinline__ u32x2 pack_s8x8(const float (&x)[8], float inv) {
 __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
 #pragma clang fp contract(off)
     const Plan& p = a.p;
+    const int D = p.d;
     const int b = blockIdx.z, hk = blockIdx.y, t = threadIdx.x;
     if ((int)blockIdx.x < p.nvchunk) {
-        __shared__ float red[16][128];
-        const int cg = t & 15, r0 = t >> 4;
+        __shared__ float red[32][128];
+        const int cgs = D / 8, rpp = 256 / cgs;  // 8-channel groups a row; rows a pass
+        const int cg = t % cgs, r0 = t / cgs;
         float m[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) m[j] = 0.0f;
         const int base = blockIdx.x * VCHUNK;
         const uint16_t* vb = a.v + b * a.v_sb + hk * a.v_sh + 8 * cg;
-        for (int i = 0; i < VCHUNK / 16; ++i) {
-            const int row = base + r0 + 16 * i;
+        for (int i = 0; i < VCHUNK / rpp; ++i) {
+            const int row = base + r0 + rpp * i;
             if (row < a.Sk) {
                 const u32x4 w = *reinterpret_cast<const u32x4*>(vb + (int64_t)row * a.v_sn);
 #pragma unroll
@@ -173,12 +179,11 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) red[r0][8 * cg + j] = m[j];
         __syncthreads();
-        if (t < 128) {
+        if (t < D) {
             float mx = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, red[r][t]);
+            for (int r = 0; r < rpp; ++r) mx = fmaxf(mx, red[r][t]);
             float* vpart = reinterpret_cast<float*>(a.ws + p.vpart);
-            vpart[((size_t)(b * a.HK + hk) * p.nvchunk + blockIdx.x) * 128 + t] = mx;
+            vpart[((size_t)(b * a.HK + hk) * p.nvchunk + blockIdx.x) * D + t] = mx;
         }
         return;
     }
@@ -187,7 +192,7 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
     __shared__ double sd[NSAMP + 2][128];
     double s[NSAMP];
     const uint16_t* kb = a.k + b * a.k_sb + hk * a.k_sh;
-    if (t < 128) {
+    if (t < D) {
         double e = 0.0, mx = 0.0, sum = 0.0;
 #pragma unroll
         for (int i = 0; i < NSAMP; ++i) {
@@ -206,7 +211,7 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
         }
     }
     __syncthreads();
-    for (int st = 64; st > 0; st >>= 1) {
+    for (int st = D / 2; st > 0; st >>= 1) {
         if (t < st) {
             sd[1][t] = fmax(sd[1][t], sd[1][t + st]);
             sd[0][t] += sd[0][t + st];
@@ -220,7 +225,7 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
     for (int j = 1; j < NSAMP; ++j)
         if (sd[2 + j][0] < sd[2 + best][0]) best = j;
     __syncthreads();
-    if (t < 128) {
+    if (t < D) {
         double be = 0.0, bm = 0.0;
 #pragma unroll
         for (int i = 0; i < NSAMP; ++i) {
@@ -232,7 +237,7 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
         sd[1][t] = bm;
     }
     __syncthreads();
-    for (int st = 64; st > 0; st >>= 1) {
+    for (int st = D / 2; st > 0; st >>= 1) {
         if (t < st) {
             sd[0][t] += sd[0][t + st];
             sd[1][t] = fmax(sd[1][t], sd[1][t + st]);
@@ -247,51 +252,53 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ prep launch 2
-// Rows are read 16 bytes (8 channels) a lane, 16 lanes a row.
+// Rows are read 16 bytes (8 channels) a lane, HD / 8 lanes a row.
 constexpr int QROWS = 64;  // query rows per block
 constexpr int KROWS = 64;  // key rows per block: four scale groups of 16, one per wave
 
-// Q: QROWS rows of head h per block, 16 per pass, one scale per row.
-template <int ROT>
+// Q: QROWS rows of head h per block, 256 / LPR per pass, one scale per row.
+template <int ROT, int HD>
 __device__ void quant_q(const PrepArgs& a, int b, int h, int qb) {
 #pragma clang fp contract(off)
+    constexpr int LPR = HD / 8, RPB = 256 / LPR;  // lanes a row, rows a block pass
     const Plan& p = a.p;
-    const int t = threadIdx.x, slot = t >> 4, L = t & 15;
-    float xs[QROWS / 16][8];  // every row of the lane loaded before the first rotation: all loads in flight at once
+    const int t = threadIdx.x, slot = t / LPR, L = t % LPR;
+    float xs[QROWS / RPB][8];  // every row of the lane loaded before the first rotation: all loads in flight at once
 #pragma unroll
-    for (int i = 0; i < QROWS / 16; ++i) {
-        const int row = qb * QROWS + 16 * i + slot;
+    for (int i = 0; i < QROWS / RPB; ++i) {
+        const int row = qb * QROWS + RPB * i + slot;
 #pragma unroll
         for (int c = 0; c < 8; ++c) xs[i][c] = 0.0f;
         if (row < a.Sq) load8(a.q + b * a.q_sb + h * a.q_sh + (int64_t)row * a.q_sn + 8 * L, xs[i]);
     }
 #pragma unroll
-    for (int i = 0; i < QROWS / 16; ++i) {
-        const int row = qb * QROWS + 16 * i + slot;
+    for (int i = 0; i < QROWS / RPB; ++i) {
+        const int row = qb * QROWS + RPB * i + slot;
         const bool ok = row < a.Sq;
         float (&x)[8] = xs[i];
         rotate8<ROT>(x, L);
         float m = 0.0f;
 #pragma unroll
         for (int c = 0; c < 8; ++c) m = fmaxf(m, fabsf(x[c]));
-        const float mx = max16(m);
+        const float mx = max_row<LPR>(m);
         const float sc = mx / 127.0f + 1e-7f;
         const float inv = 1.0f / sc;
         if (ok) {
             const size_t r = (size_t)(b * a.H + h) * a.Sq + row;
-            *reinterpret_cast<u32x2*>(a.ws + p.q8 + r * 128 + 8 * L) = pack_s8x8(x, inv);
+            *reinterpret_cast<u32x2*>(a.ws + p.q8 + r * HD + 8 * L) = pack_s8x8(x, inv);
             if (L == 0) reinterpret_cast<float*>(a.ws + p.qs)[r] = sc;
         }
     }
 }
 
-// K: KROWS key rows of kv head hk per block; wave w holds scale group 4 kb + w (16 rows, 4 a pass), the anchor row
-// subtracted before the rotation.
-template <int ROT>
+// K: KROWS key rows of kv head hk per block; wave w holds scale group 4 kb + w (16 rows, 64 / LPR a pass), the anchor
+// row subtracted before the rotation.
+template <int ROT, int HD>
 __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
 #pragma clang fp contract(off)
+    constexpr int LPR = HD / 8, RPW = 64 / LPR, NP = KGROUP / RPW;  // lanes a row, rows a wave pass, passes
     const Plan& p = a.p;
-    const int t = threadIdx.x, wave = t >> 6, rsub = (t >> 4) & 3, L = t & 15;
+    const int t = threadIdx.x, wave = t >> 6, rsub = (t & 63) / LPR, L = t % LPR;
     const int grp = kb * (KROWS / KGROUP) + wave;  // keys 16 grp .. + 15
     const int anc = reinterpret_cast<const int*>(a.ws + p.anchor)[b * a.HK + hk];
     const uint16_t* kbase = a.k + b * a.k_sb + hk * a.k_sh + 8 * L;
@@ -302,16 +309,16 @@ __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
     // is; a wholly padded group is a copy of group gL, scale included. Their scores equal real scores, so they never
     // raise a row max; the attention zeroes their P.
     const int last = a.Sk - 1, gl = last / KGROUP;
-    float x[4][8];
+    float x[NP][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // all four rows in flight before the first rotation
-        const int row = grp * KGROUP + 4 * i + rsub;
+    for (int i = 0; i < NP; ++i) {  // all the lane's rows in flight before the first rotation
+        const int row = grp * KGROUP + RPW * i + rsub;
         const int src = row <= last ? row : min(gl * KGROUP + (row & (KGROUP - 1)), last);
         load8(kbase + (int64_t)src * a.k_sn, x[i]);
     }
     float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NP; ++i) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) x[i][c] = x[i][c] - av[c];
         rotate8<ROT>(x[i], L);
@@ -321,11 +328,11 @@ __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
     const float mx = max64(m);
     const float sc = mx / 127.0f + 1e-7f;
     const float inv = 1.0f / sc;
-    uint8_t* k8 = a.ws + p.k8 + (size_t)(b * a.HK + hk) * p.skp * 128;
+    uint8_t* k8 = a.ws + p.k8 + (size_t)(b * a.HK + hk) * p.skp * HD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = grp * KGROUP + 4 * i + rsub;
-        *reinterpret_cast<u32x2*>(k8 + (size_t)row * 128 + 16 * ((L >> 1) ^ k_swz(row & 31)) + 8 * (L & 1)) =
+    for (int i = 0; i < NP; ++i) {
+        const int row = grp * KGROUP + RPW * i + rsub;
+        *reinterpret_cast<u32x2*>(k8 + (size_t)row * HD + 16 * ((L >> 1) ^ k_swz(row & 31, HD)) + 8 * (L & 1)) =
             pack_s8x8(x[i], inv);
     }
     if ((t & 63) == 0) {
@@ -338,31 +345,32 @@ __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
 }
 
 // V: one tile of cta keys of kv head hk per block: per-channel scales from the abs-max partials, int8, transposed into
-// [128 dims][cta keys] in LDS (rows padded by 4 bytes, so that the lanes of a wave, which write different dims, spread
+// [HD dims][cta keys] in LDS (rows padded by 4 bytes, so that the lanes of a wave, which write different dims, spread
 // over the banks), column sums per half tile into the aux block, then stored swizzled.
+template <int HD>
 __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
 #pragma clang fp contract(off)
-    __shared__ float inv_s[128];
-    __shared__ __attribute__((aligned(16))) uint8_t vts[128 * (128 + 4)];
+    constexpr int CG = HD / 8, KQP = 256 / CG;  // 8-channel groups a key; key quads a block pass
+    __shared__ float inv_s[HD];
+    __shared__ __attribute__((aligned(16))) uint8_t vts[HD * (128 + 4)];
     const Plan& p = a.p;
     const int cta = p.cta, vs = cta + 4, t = threadIdx.x;
     const size_t bhk = (size_t)b * a.HK + hk;
-    if (t < 128) {
-        const float* vpart = reinterpret_cast<const float*>(a.ws + p.vpart) + bhk * p.nvchunk * 128;
+    if (t < HD) {
+        const float* vpart = reinterpret_cast<const float*>(a.ws + p.vpart) + bhk * p.nvchunk * HD;
         float mx = 0.0f;
-        for (int c = 0; c < p.nvchunk; ++c) mx = fmaxf(mx, vpart[c * 128 + t]);
+        for (int c = 0; c < p.nvchunk; ++c) mx = fmaxf(mx, vpart[c * HD + t]);
         const float sc = fmaxf(mx * (1.0f / 127.0f), 1e-12f);
         inv_s[t] = 1.0f / sc;
-        if (tile == 0) reinterpret_cast<float*>(a.ws + p.vs)[bhk * 128 + t] = sc;
+        if (tile == 0) reinterpret_cast<float*>(a.ws + p.vs)[bhk * HD + t] = sc;
     }
     __syncthreads();
-    const int c8 = t & 15, k0 = t >> 4;  // channels 8 c8 .. + 7; key quads k0, k0 + 16, ...
+    const int c8 = t % CG, k0 = t / CG;  // channels 8 c8 .. + 7; key quads k0, k0 + KQP, ...
     float inv[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) inv[c] = inv_s[8 * c8 + c];
     const uint16_t* vb = a.v + b * a.v_sb + hk * a.v_sh + 8 * c8;
-    for (int i = 0; i < cta / 64; ++i) {
-        const int kq = k0 + 16 * i;  // keys 4 kq .. 4 kq + 3 of the tile
+    for (int kq = k0; kq < cta / 4; kq += KQP) {  // keys 4 kq .. 4 kq + 3 of the tile
         u32x4 raw[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {  // the four keys in flight together
@@ -385,17 +393,17 @@ __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
     }
     __syncthreads();
     uint8_t* aux = a.ws + p.aux + (bhk * p.ntiles + tile) * AUX_BYTES;
-    {
-        const int d = t & 127, half = t >> 7;
+    if (t < 2 * HD) {
+        const int d = t % HD, half = t / HD;
         int s = 0;
         for (int w = 0; w < cta / 8; ++w)
             s = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(vts + d * vs + half * (cta / 2) + 4 * w),
                                        0x01010101, s, false);
-        reinterpret_cast<int16_t*>(aux)[(half * 32 + (d & 31)) * 4 + (d >> 5)] = (int16_t)s;
+        reinterpret_cast<int16_t*>(aux)[(half * 32 + (d & 31)) * (HD / 32) + (d >> 5)] = (int16_t)s;
     }
-    uint8_t* vt = a.ws + p.vt + (bhk * p.ntiles + tile) * (size_t)(128 * cta);
+    uint8_t* vt = a.ws + p.vt + (bhk * p.ntiles + tile) * (size_t)(HD * cta);
     const int cpr = cta / 16;  // chunks per dim row
-    for (int idx = t; idx < 128 * cpr; idx += 256) {
+    for (int idx = t; idx < HD * cpr; idx += 256) {
         const int d = idx / cpr, c = idx - d * cpr;
         const uint32_t* src = reinterpret_cast<const uint32_t*>(vts + d * vs + 16 * c);
         const u32x4 w = {src[0], src[1], src[2], src[3]};
@@ -404,22 +412,22 @@ __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
 }
 
 // grid (ceil(Sq / QROWS) + skp / KROWS + ntiles, max(H, HK), B): Q blocks, then K blocks, then V tiles.
-template <int ROT>
+template <int ROT, int HD>
 __global__ __launch_bounds__(256) void i8_quant_kernel(PrepArgs a) {
     const int b = blockIdx.z, y = blockIdx.y;
     const int nqb = (a.Sq + QROWS - 1) / QROWS, nkb = a.p.skp / KROWS;
     int x = blockIdx.x;
     if (x < nqb) {
-        if (y < a.H) quant_q<ROT>(a, b, y, x);
+        if (y < a.H) quant_q<ROT, HD>(a, b, y, x);
         return;
     }
     x -= nqb;
     if (x < nkb) {
-        if (y < a.HK) quant_k<ROT>(a, b, y, x);
+        if (y < a.HK) quant_k<ROT, HD>(a, b, y, x);
         return;
     }
     x -= nkb;
-    if (y < a.HK) quant_v(a, b, y, x);
+    if (y < a.HK) quant_v<HD>(a, b, y, x);
 }
 
 // ------------------------------------------------------------------------------------------------ attention
@@ -504,16 +512,21 @@ constexpr float LAZY = 64.0f;
 //   operand fragments are read from LDS two slots ahead;
 //   then the column-sum correction (one f32 MFMA per 32-dim block) and tile t+1's constants (max, scales).
 // K, V^T and the aux block of tile t+3 are loaded into a 4-stage LDS ring while tiles t and t+1 are read.
-template <int CTA, int NS>
+template <int CTA, int NS, int HD>
 __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void i8_attn_kernel(AttnArgs a) {
     constexpr int NB = CTA / 32;                   // 32-key blocks per tile
-    constexpr int TB = CTA * 128;                  // bytes of a K (or V^T) tile
+    constexpr int DB = HD / 32;                    // 32-dim blocks of a row (and k-steps of a score MFMA chain)
+    constexpr int TB = CTA * HD;                   // bytes of a K (or V^T) tile
     constexpr int STAGE = 2 * TB + AUX_BYTES;
     constexpr int NW = 8;                          // waves per workgroup, 32 queries each
-    constexpr int KVL = TB / 1024 / NW;            // 1 KB direct loads per wave per K (or V^T) tile
-    constexpr int QS = 4 * NB;                     // score MFMAs per tile (NB blocks x 4 dim steps)
-    constexpr int PS = 4 * NB;                     // P V MFMAs per tile (4 dim blocks x NB key steps)
-    static_assert(KVL >= 1 && NS == 4, "every wave loads; K(t+2) gets two tiles to land");
+    constexpr int NBLK = TB / 1024;                // 1 KB direct loads per K (or V^T) tile
+    constexpr int KVL = NBLK >= NW ? NBLK / NW : 0;  // ... per wave, when every wave loads K and V alike
+    // this wave's direct loads per tile (with NBLK = NW / 2 each wave loads one block: waves 0-3 K, 4-7 V)
+    constexpr int LPT = KVL > 0 ? 2 * KVL : 1;
+    constexpr int QS = DB * NB;                    // score MFMAs per tile (NB blocks x DB dim steps)
+    constexpr int PS = DB * NB;                    // P V MFMAs per tile (DB dim blocks x NB key steps)
+    constexpr int SPM = 4 * NB / QS;               // phase-A slots (P dwords) per score MFMA
+    static_assert(NS == 4 && (KVL > 0 || 2 * NBLK == NW) && 4 * NB % QS == 0, "the ring and slot schedules");
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
 
     const Plan& p = a.p;
@@ -530,8 +543,8 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const int hk = head / a.G;
     const size_t bhk = (size_t)b * a.HK + hk;
 
-    const uint8_t* k8 = a.ws + p.k8 + bhk * p.skp * 128;
-    const uint8_t* vt = a.ws + p.vt + bhk * p.skp * 128;
+    const uint8_t* k8 = a.ws + p.k8 + bhk * p.skp * HD;
+    const uint8_t* vt = a.ws + p.vt + bhk * p.skp * HD;
     const uint8_t* aux = a.ws + p.aux + bhk * p.ntiles * AUX_BYTES;
     const int ntiles = p.ntiles;
     const int tail = a.Sk - (ntiles - 1) * CTA;  // valid keys of the last tile
@@ -540,23 +553,24 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const int q = qblk * 256 + wave * 32 + n;
     const bool qok = q < a.Sq;
     const size_t qr = (size_t)(b * a.H + head) * a.Sq + (qok ? q : a.Sq - 1);
-    i32x4 Qf[4];
+    i32x4 Qf[DB];
     {
-        const uint8_t* src = a.ws + p.q8 + qr * 128 + 16 * hf;
+        const uint8_t* src = a.ws + p.q8 + qr * HD + 16 * hf;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) Qf[s] = qok ? *reinterpret_cast<const i32x4*>(src + 32 * s) : i32x4{0, 0, 0, 0};
+        for (int s = 0; s < DB; ++s) Qf[s] = qok ? *reinterpret_cast<const i32x4*>(src + 32 * s) : i32x4{0, 0, 0, 0};
     }
     const float cq = (qok ? reinterpret_cast<const float*>(a.ws + p.qs)[qr] : 1.0f) * a.c;
 
     // Fragment addresses: chunk (2 s + hf) ^ x of a row is chunk hf ^ x with bits 5-6 of the byte address flipped by
     // 32 s (every other address term has those bits clear), so each fragment is one XOR from a per-stage base.
-    const int kp = key_perm(n), kx = k_swz(kp), vx = v_swz(n, CTA);
-    const uint32_t k_lane = (uint32_t)(kp * 128 + 16 * (hf ^ kx));
+    const int kp = key_perm(n), kx = k_swz(kp, HD), vx = v_swz(n, CTA);
+    const uint32_t k_lane = (uint32_t)(kp * HD + 16 * (hf ^ kx));
     const uint32_t v_lane = (uint32_t)(TB + n * CTA + 16 * (hf ^ vx));
-    auto kfrag = [&](const uint8_t* st, int f) -> i32x4 {  // score MFMA f of a tile: block kb, dim step ks
-        const int kb = NB == 4 ? 2 * (f >> 3) + (f & 1) : (f & 1);
-        const int ks = NB == 4 ? (f >> 1) & 3 : f >> 1;
-        return lds_at<i32x4>(xor_opaque(lds_addr(st) + k_lane, 32 * ks) + 4096 * kb);
+    // score MFMA f of a tile: two 32-key blocks' chains alternate, each over the DB dim steps
+    auto kb_of = [](int f) { return 2 * (f / (2 * DB)) + (f & 1); };
+    auto ks_of = [](int f) { return (f >> 1) % DB; };
+    auto kfrag = [&](const uint8_t* st, int f) -> i32x4 {
+        return lds_at<i32x4>(xor_opaque(lds_addr(st) + k_lane, 32 * ks_of(f)) + 32 * HD * kb_of(f));
     };
     auto vfrag = [&](const uint8_t* st, int f) -> i32x4 {  // P V MFMA f: dim block f / NB, key step f % NB
         const int bb = f / NB, j = f % NB;
@@ -565,11 +579,17 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
     auto issue = [&](int t) {
         uint8_t* st = ring + (t % NS) * STAGE;
+        if constexpr (KVL > 0) {
 #pragma unroll
-        for (int i = 0; i < KVL; ++i) {
-            const int blk = wave * KVL + i;
-            dma16(k8 + (size_t)t * TB + blk * 1024, lane * 16, lds_addr(st + blk * 1024));
-            dma16(vt + (size_t)t * TB + blk * 1024, lane * 16, lds_addr(st + TB + blk * 1024));
+            for (int i = 0; i < KVL; ++i) {
+                const int blk = wave * KVL + i;
+                dma16(k8 + (size_t)t * TB + blk * 1024, lane * 16, lds_addr(st + blk * 1024));
+                dma16(vt + (size_t)t * TB + blk * 1024, lane * 16, lds_addr(st + TB + blk * 1024));
+            }
+        } else if (wave < NBLK) {
+            dma16(k8 + (size_t)t * TB + wave * 1024, lane * 16, lds_addr(st + wave * 1024));
+        } else {
+            dma16(vt + (size_t)t * TB + (wave - NBLK) * 1024, lane * 16, lds_addr(st + TB + (wave - NBLK) * 1024));
         }
         if (wave == 0) dma16(aux + (size_t)t * AUX_BYTES, lane * 16, lds_addr(st + 2 * TB));
     };
@@ -577,10 +597,10 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     auto wait_for = [&](int need, int issued) {
         const bool one = issued > need;  // at most one later tile (NS = 4: issued <= need + 1)
         if (wave == 0) {
-            if (one) LR_I8_WAIT_VMCNT(2 * KVL + 1);
+            if (one) LR_I8_WAIT_VMCNT(LPT + 1);
             else LR_I8_WAIT_VMCNT(0);
         } else {
-            if (one) LR_I8_WAIT_VMCNT(2 * KVL);
+            if (one) LR_I8_WAIT_VMCNT(LPT);
             else LR_I8_WAIT_VMCNT(0);
         }
     };
@@ -588,9 +608,9 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     i32x16 magic;
 #pragma unroll
     for (int r = 0; r < 16; ++r) magic[r] = MAGIC;
-    f32x16 O[4];
+    f32x16 O[DB];
 #pragma unroll
-    for (int bb = 0; bb < 4; ++bb)
+    for (int bb = 0; bb < DB; ++bb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) O[bb][r] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f, ts = 0.0f;
@@ -621,7 +641,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         if (__builtin_amdgcn_ballot_w64(os != 1.0f) != 0) {
             l_run *= os;
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb)
+            for (int bb = 0; bb < DB; ++bb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) O[bb][r] *= os;
         }
@@ -646,11 +666,8 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
         for (int kb = 0; kb < NB; ++kb) SS[0][kb] = magic;
 #pragma unroll
-        for (int f = 0; f < QS; ++f) {
-            const int kb = NB == 4 ? 2 * (f >> 3) + (f & 1) : (f & 1);
-            const int ks = NB == 4 ? (f >> 1) & 3 : f >> 1;
-            SS[0][kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kfrag(ring, f), Qf[ks], SS[0][kb], 0, 0, 0);
-        }
+        for (int f = 0; f < QS; ++f)
+            SS[0][kb_of(f)] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kfrag(ring, f), Qf[ks_of(f)], SS[0][kb_of(f)], 0, 0, 0);
         int mi[NB];
         rowmax(SS[0], mi);
         constants(mi, ring);
@@ -682,12 +699,12 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < QS; ++s) {
-            if (NEXT) {
-                if (s + 2 < QS) fr[(s + 2) % 3] = kfrag(stK, s + 2);
-                const int kb = NB == 4 ? 2 * (s >> 3) + (s & 1) : (s & 1);
-                const int ks = NB == 4 ? (s >> 1) & 3 : s >> 1;
-                Sn[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[s % 3], Qf[ks], ks == 0 ? magic : Sn[kb], 0, 0, 0);
+        for (int s = 0; s < 4 * NB; ++s) {
+            if (NEXT && s % SPM == 0) {  // score MFMA f in the first slot of its group of SPM
+                const int f = s / SPM;
+                if (f + 2 < QS) fr[(f + 2) % 3] = kfrag(stK, f + 2);
+                const int kb = kb_of(f), ks = ks_of(f);
+                Sn[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[f % 3], Qf[ks], ks == 0 ? magic : Sn[kb], 0, 0, 0);
             }
             {
                 const int kb = s >> 2, qd = s & 3;  // P dword s: block kb, keys 16 hf + 4 qd .. + 3
@@ -725,7 +742,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             const int bb = s / NB, j = s % NB;
             const i32x4 B = {(int)P[j][0], (int)P[j][1], (int)P[j][2], (int)P[j][3]};
             acc[bb & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[s % 3], B, j == 0 ? magic : acc[bb & 1], 0, 0, 0);
-            if (NEXT) {  // max of S(t+1): its NB * 16 registers spread evenly over the PS slots (4 per slot)
+            if (NEXT) {  // max of S(t+1): its NB * 16 registers spread evenly over the PS slots
                 static_assert(NB * 16 % (4 * PS) == 0, "whole groups of 4 registers per slot");
 #pragma unroll
                 for (int u = 0; u < NB * 16 / PS / 4; ++u) {
@@ -745,13 +762,22 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) O[3][r] = fmaf(__int_as_float(acc[1][r]), ts, O[3][r]);
+        for (int r = 0; r < 16; ++r) O[DB - 1][r] = fmaf(__int_as_float(acc[(DB - 1) & 1][r]), ts, O[DB - 1][r]);
         {
             // + 128 * ts * (column sums of V(t)) - 12582912 * ts (the P V accumulator bias), per 32-dim block
-            const i16x4 cs = lds_load<i16x4>(stV + 2 * TB + 8 * lane);
+            int16_t cs[DB];
+            if constexpr (DB == 4) {
+                const i16x4 c4 = lds_load<i16x4>(stV + 2 * TB + 8 * lane);
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) cs[bb] = c4[bb];
+            } else {
+                const uint32_t c2 = lds_load<uint32_t>(stV + 2 * TB + 4 * lane);
+                cs[0] = (int16_t)(c2 & 0xffffu);
+                cs[1] = (int16_t)(c2 >> 16);
+            }
             const float w128 = 128.0f * ts;
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb)
+            for (int bb = 0; bb < DB; ++bb)
                 O[bb] = __builtin_amdgcn_mfma_f32_32x32x2f32((float)cs[bb] - 49152.0f, w128, O[bb], 0, 0, 0);
         }
         if (NEXT) {
@@ -778,10 +804,10 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
     if (!qok) return;
     const float inv = 1.0f / pair_sum(l_run);
-    const float* vs = reinterpret_cast<const float*>(a.ws + p.vs) + bhk * 128;
+    const float* vs = reinterpret_cast<const float*>(a.ws + p.vs) + bhk * HD;
     uint16_t* orow = a.out + b * a.o_sb + head * a.o_sh + (int64_t)q * a.o_sn;
 #pragma unroll
-    for (int bb = 0; bb < 4; ++bb)
+    for (int bb = 0; bb < DB; ++bb)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d0 = 32 * bb + 8 * g + 4 * hf;
@@ -801,20 +827,25 @@ hipError_t launch_prep(const PrepArgs& a, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid((a.Sq + QROWS - 1) / QROWS + p.skp / KROWS + p.ntiles, a.H > a.HK ? a.H : a.HK, a.B);
-    if (p.rot == 4)
-        hipLaunchKernelGGL(i8_quant_kernel<4>, grid, dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL(i8_quant_kernel<128>, grid, dim3(256), 0, stream, a);
+    if (p.d == 128) {
+        if (p.rot == 4) hipLaunchKernelGGL((i8_quant_kernel<4, 128>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((i8_quant_kernel<128, 128>), grid, dim3(256), 0, stream, a);
+    } else {
+        if (p.rot == 4) hipLaunchKernelGGL((i8_quant_kernel<4, 64>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((i8_quant_kernel<64, 64>), grid, dim3(256), 0, stream, a);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
     const int nqb = (a.Sq + 255) / 256;
     const dim3 grid((unsigned)((int64_t)nqb * a.H * a.B));
-    if (a.p.cta == 128)
-        hipLaunchKernelGGL((i8_attn_kernel<128, 4>), grid, dim3(512), 0, stream, a);
+    if (a.p.d == 64)
+        hipLaunchKernelGGL((i8_attn_kernel<64, 4, 64>), grid, dim3(512), 0, stream, a);
+    else if (a.p.cta == 128)
+        hipLaunchKernelGGL((i8_attn_kernel<128, 4, 128>), grid, dim3(512), 0, stream, a);
     else
-        hipLaunchKernelGGL((i8_attn_kernel<64, 4>), grid, dim3(512), 0, stream, a);
+        hipLaunchKernelGGL((i8_attn_kernel<64, 4, 128>), grid, dim3(512), 0, stream, a);
     return hipGetLastError();
 }
 

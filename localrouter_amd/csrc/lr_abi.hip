@@ -334,10 +334,11 @@ int rope_impl(const void* src, int64_t src_rs, int64_t src_off, void* dst, int64
 }
 
 // ------------------------------------------------------------------------------------------------ INT8 chain
-// The checks of kitchen_int8_attention_impl (kernels/cuda/minimax/kitchen_launch.cu:199-214): sizes, head dim,
-// H % HK, 16-byte aligned bases and strides (a stride whose extent is 1 is never used), a 256-byte aligned workspace.
+// The checks of kitchen_int8_attention_impl (kernels/cuda/minimax/kitchen_launch.cu:199-214): sizes, head dim 64 or
+// 128, H % HK, 16-byte aligned bases and strides (a stride whose extent is 1 is never used), a 256-byte aligned
+// workspace.
 bool i8_sizes_ok(int B, int H, int HK, int Sq, int Sk, int D) {
-    if (B < 1 || H < 1 || HK < 1 || Sq < 1 || Sk < 1 || D != lr::D || H % HK != 0) return false;
+    if (B < 1 || H < 1 || HK < 1 || Sq < 1 || Sk < 1 || (D != 64 && D != 128) || H % HK != 0) return false;
     if (B > 65535 || H > 65535 || Sq > INT_MAX - 512 || Sk > INT_MAX - 512) return false;
     return (int64_t)((Sq + 255) / 256) * H * B <= INT_MAX;
 }
@@ -363,7 +364,7 @@ int i8_prep_impl(const void* q, const void* k, const void* v, void* ws, int B, i
     a.v_sb = v_sb; a.v_sh = v_sh; a.v_sn = v_sn;
     a.B = B; a.H = H; a.HK = HK; a.Sq = Sq; a.Sk = Sk;
     a.ws = static_cast<uint8_t*>(ws);
-    a.p = lr::i8::plan_of(B, H, HK, Sq, Sk);
+    a.p = lr::i8::plan_of(B, H, HK, Sq, Sk, D);
     return (int)lr::i8::launch_prep(a, stream);
 }
 
@@ -374,12 +375,12 @@ int i8_kernel_impl(void* out, const void* ws, int B, int H, int HK, int Sq, int 
     lr::i8::AttnArgs a{};
     a.ws = static_cast<const uint8_t*>(ws);
     a.out = static_cast<uint16_t*>(out);
-    a.o_sb = (int64_t)H * Sq * lr::D;
-    a.o_sh = o_rows ? lr::D : (int64_t)Sq * lr::D;
-    a.o_sn = o_rows ? (int64_t)H * lr::D : lr::D;
+    a.o_sb = (int64_t)H * Sq * D;
+    a.o_sh = o_rows ? D : (int64_t)Sq * D;
+    a.o_sn = o_rows ? (int64_t)H * D : D;
     a.B = B; a.H = H; a.HK = HK; a.G = H / HK; a.Sq = Sq; a.Sk = Sk;
     a.c = scale * 1.4426950408889634f;
-    a.p = lr::i8::plan_of(B, H, HK, Sq, Sk);
+    a.p = lr::i8::plan_of(B, H, HK, Sq, Sk, D);
     return (int)lr::i8::launch_attention(a, stream);
 }
 
@@ -646,7 +647,7 @@ int lr_joint_attention_fused_noalloc(const void* q_raw, const void* k_raw, const
 
 size_t lr_int8_attention_workspace_bytes(int B, int H, int HK, int Sq, int Sk, int D) {
     if (!i8_sizes_ok(B, H, HK, Sq, Sk, D)) return 0;
-    return lr::i8::plan_of(B, H, HK, Sq, Sk).total;
+    return lr::i8::plan_of(B, H, HK, Sq, Sk, D).total;
 }
 
 int lr_int8_attention(const void* q, const void* k, const void* v, void* out, void* workspace, int B, int H, int HK,

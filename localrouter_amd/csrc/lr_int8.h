@@ -3,20 +3,21 @@
 //
 // The chain follows src/engines/minimax_h3/launch.zig:317-419 (Kitchen.Plan / attentionPrep / attentionKernel) and
 // kernels/cuda/minimax/kitchen_launch.cu:193-280: a K anchor per kv head, Q and K rotated (H4 when Sk <= 256, else
-// the signed H128) and quantised to int8, V quantised per channel, then softmax(scale Q K^T) V with int8 QK^T and
-// u8 P x s8 V products. The workspace layout is this library's own, laid out for the gfx950 kernels:
-//   q8     int8 [B][H][Sq][128]                     rotated queries, plain rows
-//   k8     int8 [B][HK][skp][128]                   rotated keys minus the anchor; 16-byte chunk c of key row r stored at
-//                                                   c ^ k_swz(r); rows past Sk (skp = ntiles * cta) repeat real keys
+// the signed H128 at head dim 128 or the plain H64 at head dim 64) and quantised to int8, V quantised per channel,
+// then softmax(scale Q K^T) V with int8 QK^T and u8 P x s8 V products. Head dim D is 128 (the engine's) or 64 (the
+// wheel's other case). The workspace layout is this library's own, laid out for the gfx950 kernels:
+//   q8     int8 [B][H][Sq][D]                       rotated queries, plain rows
+//   k8     int8 [B][HK][skp][D]                     rotated keys minus the anchor; 16-byte chunk c of key row r stored at
+//                                                   c ^ k_swz(r, D); rows past Sk (skp = ntiles * cta) repeat real keys
 //                                                   (see quant_k), so that their scores never raise a row max
-//   vt     int8 [B][HK][ntiles][128][cta]           V^T tiles; chunk c of dim row d at c ^ v_swz(d), keys past Sk zero
+//   vt     int8 [B][HK][ntiles][D][cta]             V^T tiles; chunk c of dim row d at c ^ v_swz(d), keys past Sk zero
 //   aux    [B][HK][ntiles] blocks of 1 KB           per tile: int16 column sums of vt over each half tile, laid out
-//                                                   [half][lane 0..31][dim block 0..3] (dim = 32 * block + lane), then
-//                                                   the tile's K scales as fp32 [half][block] (key block b, half h ->
-//                                                   scale of keys 32 b + 16 h .. + 15)
+//                                                   [half][lane 0..31][dim block 0..D/32-1] (dim = 32 * block + lane),
+//                                                   then the tile's K scales as fp32 [half][block] (key block b, half
+//                                                   h -> scale of keys 32 b + 16 h .. + 15)
 //   qs     fp32 [B][H][Sq]                          one scale per query row
-//   vs     fp32 [B][HK][128]                        one scale per channel
-//   vpart  fp32 [B][HK][nvchunk][128]               per-chunk channel abs-max of V (the V scales' first pass)
+//   vs     fp32 [B][HK][D]                          one scale per channel
+//   vpart  fp32 [B][HK][nvchunk][D]                 per-chunk channel abs-max of V (the V scales' first pass)
 //   anchor int32 [B][HK]                            anchor key row or -1
 // Scale granularity (per query row; per 16 keys; per channel) is this library's choice. The reference's per-thread
 // groups follow its mma fragment layout (kernels/cuda/minimax/kitchen/quant_qk_int8.cu:245-247); the arithmetic
@@ -34,25 +35,27 @@ constexpr int VCHUNK = 256;   // keys per V abs-max partial
 constexpr int AUX_BYTES = 1024;
 constexpr int AUX_KS_OFF = 512;  // byte offset of the K scales in an aux block
 
-// Tile width: 128 keys past 1024 keys, else 64 (launch.zig:333, kitchen_launch.cu:15).
-inline int cta_for(int Sk) { return Sk > 1024 ? 128 : 64; }
-// Hadamard of Q and K: H4 blocks up to 256 keys, else the signed H128 (kitchen_launch.cu:17, launch.zig:387-391).
-inline int rotation_for(int Sk) { return Sk <= 256 ? 4 : 128; }
+// Tile width: 128 keys past 1024 keys at head dim 128, else 64 (launch.zig:333, kitchen_launch.cu:107).
+inline int cta_for(int Sk, int D) { return D >= 128 && Sk > 1024 ? 128 : 64; }
+// Hadamard of Q and K: H4 blocks up to 256 keys, else the signed H128 / plain H64 (kitchen_launch.cu:233-241,
+// launch.zig:387-391).
+inline int rotation_for(int Sk, int D) { return Sk <= 256 ? 4 : D; }
 
 struct Plan {
-    int cta, ntiles, skp, nvchunk, rot;
+    int d, cta, ntiles, skp, nvchunk, rot;
     size_t q8, k8, vt, aux, qs, vs, vpart, anchor, total;
 };
 
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-inline Plan plan_of(int B, int H, int HK, int Sq, int Sk) {
+inline Plan plan_of(int B, int H, int HK, int Sq, int Sk, int D) {
     Plan p;
-    p.cta = cta_for(Sk);
+    p.d = D;
+    p.cta = cta_for(Sk, D);
     p.ntiles = (Sk + p.cta - 1) / p.cta;
     p.skp = p.ntiles * p.cta;
     p.nvchunk = (Sk + VCHUNK - 1) / VCHUNK;
-    p.rot = rotation_for(Sk);
+    p.rot = rotation_for(Sk, D);
     const size_t bh = (size_t)B * H, bhk = (size_t)B * HK;
     size_t at = 0;
     auto take = [&](size_t bytes) {
@@ -60,22 +63,26 @@ inline Plan plan_of(int B, int H, int HK, int Sq, int Sk) {
         at = align256(at + bytes);
         return o;
     };
-    p.q8 = take(bh * Sq * 128);
-    p.k8 = take(bhk * p.skp * 128);
-    p.vt = take(bhk * p.skp * 128);
+    p.q8 = take(bh * Sq * D);
+    p.k8 = take(bhk * p.skp * D);
+    p.vt = take(bhk * p.skp * D);
     p.aux = take(bhk * p.ntiles * AUX_BYTES);
     p.qs = take(bh * Sq * 4);
-    p.vs = take(bhk * 128 * 4);
-    p.vpart = take(bhk * p.nvchunk * 128 * 4);
+    p.vs = take(bhk * D * 4);
+    p.vpart = take(bhk * p.nvchunk * D * 4);
     p.anchor = take(bhk * 4);
     p.total = at;
     return p;
 }
 
 // LDS / workspace swizzles (16-byte chunk index XOR). k_swz: the K operand read (lanes 0..15 take rows
-// key_perm(0..15)) hits distinct chunk positions per 8 lanes and distinct (row parity, position) per 16 lanes.
-// v_swz: the same property for V^T rows read 32 consecutive dims at a time.
-__host__ __device__ inline int k_swz(int r) { return ((r >> 2) & 4) | ((((r >> 2) ^ r) & 1) << 1) | ((r >> 1) & 1); }
+// key_perm(0..15)) hits distinct chunk positions per 8 lanes and distinct (row parity, position) per 16 lanes; with
+// 64-byte rows (head dim 64, four chunks a row, two rows a bank line) the lanes of each group of 8 take distinct
+// (row parity, chunk) pairs. v_swz: the same property for V^T rows read 32 consecutive dims at a time.
+__host__ __device__ inline int k_swz(int r, int D) {
+    return D == 128 ? ((r >> 2) & 4) | ((((r >> 2) ^ r) & 1) << 1) | ((r >> 1) & 1)
+                    : ((r >> 1) & 1) | (((r >> 4) & 1) << 1);
+}
 __host__ __device__ inline int v_swz(int d, int cta) {
     return cta == 128 ? (((d >> 1) & 7) ^ ((d & 1) << 2)) : (((d >> 1) ^ (d >> 3)) & 3);
 }

@@ -342,19 +342,25 @@ def joint_attention_images(q_prep: torch.Tensor, workspace: torch.Tensor, sk: in
 
 
 # ------------------------------------------------------------------------------------------------ INT8 chain
+def int8_scale(head_dim: int) -> float:
+    """head_dim^-0.5 rounded to fp32, the scale the reference's callers pass (0x3DB504F3 for 128)."""
+    return float(torch.tensor(1.0 / math.sqrt(head_dim), dtype=torch.float32))
+
+
 def int8_workspace_bytes(heads: int, sq: int, *, sk: int | None = None, kv_heads: int | None = None,
-                         batch: int = 1) -> int:
+                         batch: int = 1, head_dim: int = D) -> int:
     """Kitchen.Plan.of(heads, S).total for this library's workspace layout (0 when the case is unsupported)."""
     sk = sq if sk is None else sk
     kv_heads = heads if kv_heads is None else kv_heads
-    return int(_lib.load().lr_int8_attention_workspace_bytes(batch, heads, kv_heads, sq, sk, D))
+    return int(_lib.load().lr_int8_attention_workspace_bytes(batch, heads, kv_heads, sq, sk, head_dim))
 
 
 def _bhsd(t: torch.Tensor, name: str) -> tuple[int, int, int]:
     if not t.is_cuda or t.dtype != torch.bfloat16:
         raise ValueError(f"{name}: expected a bf16 tensor on the GPU, got {t.dtype} on {t.device}")
-    if t.dim() != 4 or t.shape[3] != D or t.stride(3) != 1:
-        raise ValueError(f"{name}: expected [B, heads, S, 128] with unit last stride, got {tuple(t.shape)} / {t.stride()}")
+    if t.dim() != 4 or t.shape[3] not in (64, 128) or t.stride(3) != 1:
+        raise ValueError(f"{name}: expected [B, heads, S, 64 or 128] with unit last stride, got {tuple(t.shape)} / "
+                         f"{t.stride()}")
     return t.stride(0), t.stride(1), t.stride(2)
 
 
@@ -371,64 +377,70 @@ def _workspace(workspace: torch.Tensor | None, need: int, device) -> torch.Tenso
 def int8_attention_prep(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                         workspace: torch.Tensor | None = None) -> torch.Tensor:
     """The K anchor, Q / K rotation and int8 quantisation, V per-channel int8 into the workspace (returned)."""
-    B, H, Sq, _ = q.shape
+    B, H, Sq, d = q.shape
     HK, Sk = k.shape[1], k.shape[2]
     qs, ks, vs = _bhsd(q, "q"), _bhsd(k, "k"), _bhsd(v, "v")
-    workspace = _workspace(workspace, int8_workspace_bytes(H, Sq, sk=Sk, kv_heads=HK, batch=B), q.device)
-    _lib.call("lr_int8_attention_prep", _ptr(q), _ptr(k), _ptr(v), _ptr(workspace), B, H, HK, Sq, Sk, D, *qs, *ks,
+    workspace = _workspace(workspace, int8_workspace_bytes(H, Sq, sk=Sk, kv_heads=HK, batch=B, head_dim=d), q.device)
+    _lib.call("lr_int8_attention_prep", _ptr(q), _ptr(k), _ptr(v), _ptr(workspace), B, H, HK, Sq, Sk, d, *qs, *ks,
               *vs, _stream())
     return workspace
 
 
 def int8_attention_kernel(workspace: torch.Tensor, out: torch.Tensor, *, batch: int, heads: int, kv_heads: int,
-                          sq: int, sk: int, scale: float = SCALE_128, rows: bool = False) -> torch.Tensor:
-    """The attention over a workspace int8_attention_prep filled; out [B, H, Sq, 128] or rows [Sq, H * 128] (B 1)."""
+                          sq: int, sk: int, scale: float | None = None, rows: bool = False,
+                          head_dim: int = D) -> torch.Tensor:
+    """The attention over a workspace int8_attention_prep filled; out [B, H, Sq, d] or rows [Sq, H * d] (B 1); the
+    scale defaults to d^-0.5 in fp32."""
     if not out.is_cuda or out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise ValueError("out: expected a contiguous bf16 tensor on the GPU")
-    _lib.call("lr_int8_attention_kernel", _ptr(out), _ptr(workspace), batch, heads, kv_heads, sq, sk, D, scale,
+    scale = int8_scale(head_dim) if scale is None else scale
+    _lib.call("lr_int8_attention_kernel", _ptr(out), _ptr(workspace), batch, heads, kv_heads, sq, sk, head_dim, scale,
               1 if rows else 0, _stream())
     return out
 
 
 def int8_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *,
-                   scale: float = SCALE_128, rows: bool = False,
+                   scale: float | None = None, rows: bool = False,
                    workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """kitchen_int8_attention: q [B, H, Sq, 128], k / v [B, HK, Sk, 128] bf16 views (any strides, unit last) ->
-    out [B, H, Sq, 128] bf16, or rows [Sq, H * 128] when rows (B 1)."""
-    B, H, Sq, _ = q.shape
+    """kitchen_int8_attention: q [B, H, Sq, d], k / v [B, HK, Sk, d] bf16 views (any strides, unit last; d 64 or
+    128) -> out [B, H, Sq, d] bf16, or rows [Sq, H * d] when rows (B 1); the scale defaults to d^-0.5 in fp32."""
+    B, H, Sq, d = q.shape
     HK, Sk = k.shape[1], k.shape[2]
     qs, ks, vs = _bhsd(q, "q"), _bhsd(k, "k"), _bhsd(v, "v")
-    workspace = _workspace(workspace, int8_workspace_bytes(H, Sq, sk=Sk, kv_heads=HK, batch=B), q.device)
+    scale = int8_scale(d) if scale is None else scale
+    workspace = _workspace(workspace, int8_workspace_bytes(H, Sq, sk=Sk, kv_heads=HK, batch=B, head_dim=d), q.device)
     if out is None:
-        out = torch.empty((Sq, H * D) if rows else (B, H, Sq, D), dtype=torch.bfloat16, device=q.device)
+        out = torch.empty((Sq, H * d) if rows else (B, H, Sq, d), dtype=torch.bfloat16, device=q.device)
     name = "lr_int8_attention_rows" if rows else "lr_int8_attention"
-    _lib.call(name, _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(workspace), B, H, HK, Sq, Sk, D, *qs, *ks, *vs, scale,
+    _lib.call(name, _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(workspace), B, H, HK, Sq, Sk, d, *qs, *ks, *vs, scale,
               _stream())
     return out
 
 
-def qkv_views(qkv: torch.Tensor, heads: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """q, k, v [1, heads, S, 128] views of a packed qkv buffer [S, 3 * heads * 128] (launch.zig:362-366)."""
+def qkv_views(qkv: torch.Tensor, heads: int, head_dim: int = D) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """q, k, v [1, heads, S, d] views of a packed qkv buffer [S, 3 * heads * d] (launch.zig:362-366)."""
     S = qkv.shape[0]
-    parts = qkv.view(S, 3, heads, D)
+    parts = qkv.view(S, 3, heads, head_dim)
     return tuple(parts[:, i].permute(1, 0, 2).unsqueeze(0) for i in range(3))
 
 
-def kitchen_attention_prep(qkv: torch.Tensor, workspace: torch.Tensor | None, heads: int) -> torch.Tensor:
+def kitchen_attention_prep(qkv: torch.Tensor, workspace: torch.Tensor | None, heads: int,
+                           head_dim: int = D) -> torch.Tensor:
     """Kitchen.attentionPrep(qkv, ws, heads, seq)."""
-    return int8_attention_prep(*qkv_views(qkv, heads), workspace)
+    return int8_attention_prep(*qkv_views(qkv, heads, head_dim), workspace)
 
 
 def kitchen_attention_kernel(out: torch.Tensor, workspace: torch.Tensor, heads: int, seq: int,
-                             rows: bool) -> torch.Tensor:
+                             rows: bool, head_dim: int = D) -> torch.Tensor:
     """Kitchen.attentionKernel(out, ws, heads, seq, rows)."""
-    return int8_attention_kernel(workspace, out, batch=1, heads=heads, kv_heads=heads, sq=seq, sk=seq, rows=rows)
+    return int8_attention_kernel(workspace, out, batch=1, heads=heads, kv_heads=heads, sq=seq, sk=seq, rows=rows,
+                                 head_dim=head_dim)
 
 
 def kitchen_attention(qkv: torch.Tensor, heads: int, out: torch.Tensor | None = None,
-                      workspace: torch.Tensor | None = None, rows: bool = False) -> torch.Tensor:
-    """Kitchen.attention(qkv, out, ws, heads, seq): out [heads, S, 128] (rows: [S, heads * 128])."""
+                      workspace: torch.Tensor | None = None, rows: bool = False, head_dim: int = D) -> torch.Tensor:
+    """Kitchen.attention(qkv, out, ws, heads, seq): out [heads, S, d] (rows: [S, heads * d])."""
     S = qkv.shape[0]
-    o = int8_attention(*qkv_views(qkv, heads), None if out is None else out.view(
-        (S, heads * D) if rows else (1, heads, S, D)), rows=rows, workspace=workspace)
-    return o if rows else o.view(heads, S, D)
+    o = int8_attention(*qkv_views(qkv, heads, head_dim), None if out is None else out.view(
+        (S, heads * head_dim) if rows else (1, heads, S, head_dim)), rows=rows, workspace=workspace)
+    return o if rows else o.view(heads, S, head_dim)

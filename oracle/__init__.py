@@ -82,14 +82,16 @@ def lib() -> ctypes.CDLL:
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                           ctypes.c_int, ctypes.c_int, _P]
         L.lro_joint_attention_ex.argtypes = list(L.lro_joint_attention.argtypes[:-1]) + [ctypes.c_int, _P]
-        L.lro_i8_rotate.argtypes = [_P, ctypes.c_int]
-        L.lro_i8_anchor.argtypes = [_P, _I64, ctypes.c_int]
+        L.lro_i8_rotate.argtypes = [_P, ctypes.c_int, ctypes.c_int]
+        L.lro_i8_anchor.argtypes = [_P, _I64, ctypes.c_int, ctypes.c_int]
         L.lro_i8_anchor.restype = ctypes.c_int
-        L.lro_i8_quant_rows.argtypes = [_P, _I64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P]
-        L.lro_i8_quant_v.argtypes = [_P, _I64, ctypes.c_int, _P, _P]
-        L.lro_i8_attention.argtypes = [_P, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, _P]
+        L.lro_i8_quant_rows.argtypes = [_P, _I64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        _P, _P]
+        L.lro_i8_quant_v.argtypes = [_P, _I64, ctypes.c_int, ctypes.c_int, _P, _P]
+        L.lro_i8_attention.argtypes = [_P, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_float, _P]
         L.lro_i8_attention_p8.argtypes = [_P, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int,
-                                          ctypes.c_int, _P]
+                                          ctypes.c_int, ctypes.c_float, ctypes.c_int, _P]
         _lib = L
     return _lib
 
@@ -262,14 +264,14 @@ def brute_rms_rope(x_f32: np.ndarray, w=None, *, cos=None, sin=None, mat=None, p
 
 
 def brute_attention(q, k, v, *, p0=0, nkeys=None, causal=False, scale=None) -> np.ndarray:
-    """fp64 dense softmax attention: q [W, H, 128], k, v [nk, HK, 128]."""
+    """fp64 dense softmax attention: q [W, H, d], k, v [nk, HK, d] (scale d^-0.5 in fp32 by default)."""
     q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
-    W, H, _ = q.shape
+    W, H, d = q.shape
     nk, HK, _ = k.shape
     nkeys = nk if nkeys is None else nkeys
-    scale = float(np.float32(1.0 / np.sqrt(np.float32(D)))) if scale is None else float(scale)
+    scale = float(np.float32(1.0 / np.sqrt(np.float32(d)))) if scale is None else float(scale)
     G = H // HK
-    out = np.zeros((W, H, D))
+    out = np.zeros((W, H, v.shape[-1]))
     j = np.arange(nk)
     for h in range(H):
         s = q[:, h, :] @ k[:, h // G, :].T * scale
@@ -288,75 +290,91 @@ def brute_attention(q, k, v, *, p0=0, nkeys=None, causal=False, scale=None) -> n
 I8_KGROUP = 16   # keys per K scale
 
 
-def i8_rotation_for(seq: int) -> int:
-    """H4 for sequences up to 256 tokens, the signed H128 above (src/engines/minimax_h3/launch.zig:387-391)."""
-    return 4 if seq <= 256 else 128
+def i8_rotation_for(seq: int, d: int = D) -> int:
+    """H4 for sequences up to 256 tokens, else the signed H128 (head dim 128) or the plain H64 (head dim 64)
+    (src/engines/minimax_h3/launch.zig:387-391, kernels/cuda/minimax/kitchen_launch.cu:236-241)."""
+    return 4 if seq <= 256 else d
+
+
+def i8_scale(d: int = D) -> float:
+    """The softmax scale a caller passes for head dim d: d^-0.5 rounded to fp32 (0x3db504f3 for 128)."""
+    return float(np.float32(1.0 / np.sqrt(d)))
 
 
 def i8_rotate(x: np.ndarray, kind: int) -> np.ndarray:
-    """Rotate every 128-channel row of x (fp32) in place order of the reference's convrot helpers; returns a copy."""
+    """Rotate every row of x (fp32 [..., d], d 64 or 128) in the operation order of the reference's convrot helpers;
+    returns a copy."""
     y = np.ascontiguousarray(x, dtype=np.float32).copy()
-    for row in y.reshape(-1, D):
-        lib().lro_i8_rotate(_ptr(row), kind)
+    d = y.shape[-1]
+    for row in y.reshape(-1, d):
+        lib().lro_i8_rotate(_ptr(row), d, kind)
     return y
 
 
 def i8_anchor(k_head_bits: np.ndarray) -> int:
-    """Anchor row of one kv head's keys (uint16 bf16 bits [Lk, 128] or a strided [Lk, ..., 128] view's head slice)."""
+    """Anchor row of one kv head's keys (uint16 bf16 bits [Lk, d])."""
     k = np.ascontiguousarray(k_head_bits, dtype=np.uint16)
-    return int(lib().lro_i8_anchor(_ptr(k), D, k.shape[0]))
+    d = k.shape[-1]
+    return int(lib().lro_i8_anchor(_ptr(k), d, k.shape[0], d))
 
 
 def i8_quant_rows(x_bits: np.ndarray, rot: int, anchor: int = -1, group: int = 1):
-    """int8 [rows, 128] and the per-group scales of one head's rows (bf16 bits [rows, 128])."""
+    """int8 [rows, d] and the per-group scales of one head's rows (bf16 bits [rows, d])."""
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
-    rows = x.shape[0]
-    out = np.zeros((rows, D), np.int8)
+    rows, d = x.shape
+    out = np.zeros((rows, d), np.int8)
     sc = np.zeros(((rows + group - 1) // group,), np.float32)
-    lib().lro_i8_quant_rows(_ptr(x), D, rows, rot, anchor, group, _ptr(out), _ptr(sc))
+    lib().lro_i8_quant_rows(_ptr(x), d, rows, d, rot, anchor, group, _ptr(out), _ptr(sc))
     return out, sc
 
 
 def i8_quant_v(v_bits: np.ndarray):
     v = np.ascontiguousarray(v_bits, dtype=np.uint16)
-    out = np.zeros((v.shape[0], D), np.int8)
-    sc = np.zeros((D,), np.float32)
-    lib().lro_i8_quant_v(_ptr(v), D, v.shape[0], _ptr(out), _ptr(sc))
+    rows, d = v.shape
+    out = np.zeros((rows, d), np.int8)
+    sc = np.zeros((d,), np.float32)
+    lib().lro_i8_quant_v(_ptr(v), d, rows, d, _ptr(out), _ptr(sc))
     return out, sc
 
 
-def i8_attention(q8, qs, k8, ks, v8, vs, kgroup: int = I8_KGROUP) -> np.ndarray:
+def i8_attention(q8, qs, k8, ks, v8, vs, kgroup: int = I8_KGROUP, scale: float | None = None) -> np.ndarray:
     q8, k8, v8 = (np.ascontiguousarray(a, dtype=np.int8) for a in (q8, k8, v8))
     qs, ks, vs = (np.ascontiguousarray(a, dtype=np.float32) for a in (qs, ks, vs))
-    out = np.zeros((q8.shape[0], D), np.float32)
+    d = q8.shape[1]
+    scale = i8_scale(d) if scale is None else scale
+    out = np.zeros((q8.shape[0], d), np.float32)
     lib().lro_i8_attention(_ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), kgroup, _ptr(v8), _ptr(vs), q8.shape[0],
-                           k8.shape[0], _ptr(out))
+                           k8.shape[0], d, scale, _ptr(out))
     return out
 
 
-def i8_attention_p8(q8, qs, k8, ks, v8, vs, cta: int, kgroup: int = I8_KGROUP) -> np.ndarray:
+def i8_attention_p8(q8, qs, k8, ks, v8, vs, cta: int, kgroup: int = I8_KGROUP, scale: float | None = None) -> np.ndarray:
     """i8_attention with P rounded to u8 against each cta-key tile's row max, as the reference's kernel rounds it."""
     q8, k8, v8 = (np.ascontiguousarray(a, dtype=np.int8) for a in (q8, k8, v8))
     qs, ks, vs = (np.ascontiguousarray(a, dtype=np.float32) for a in (qs, ks, vs))
-    out = np.zeros((q8.shape[0], D), np.float32)
+    d = q8.shape[1]
+    scale = i8_scale(d) if scale is None else scale
+    out = np.zeros((q8.shape[0], d), np.float32)
     lib().lro_i8_attention_p8(_ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), kgroup, _ptr(v8), _ptr(vs), q8.shape[0],
-                              k8.shape[0], cta, _ptr(out))
+                              k8.shape[0], d, scale, cta, _ptr(out))
     return out
 
 
-def i8_cta_for(sk: int) -> int:
-    """Key tile of the P rounding: 128 keys past 1024 keys, else 64 (src/engines/minimax_h3/launch.zig:333)."""
-    return 128 if sk > 1024 else 64
+def i8_cta_for(sk: int, d: int = D) -> int:
+    """Key tile of the P rounding: 128 keys past 1024 keys at head dim 128, else 64 (src/engines/minimax_h3/
+    launch.zig:333, kernels/cuda/minimax/kitchen_launch.cu:107)."""
+    return 128 if sk > 1024 and d >= 128 else 64
 
 
 def int8_attention(qkv_bits: np.ndarray, heads: int, rows=None) -> tuple[np.ndarray, dict]:
-    """The whole chain for packed qkv (bf16 bits [S, 3, heads, 128]): per head the K anchor, Q (one scale per row) and
-    K (one scale per 16 keys, anchor subtracted) rotated and quantised, V quantised per channel, then attention of the
-    selected query rows (all by default). Returns fp32 [heads, len(rows), 128] and the quantised operands."""
-    S = qkv_bits.shape[0]
-    rot = i8_rotation_for(S)
+    """The whole chain for packed qkv (bf16 bits [S, 3, heads, d], d 64 or 128): per head the K anchor, Q (one scale
+    per row) and K (one scale per 16 keys, anchor subtracted) rotated and quantised, V quantised per channel, then
+    attention of the selected query rows (all by default) at scale d^-0.5. Returns fp32 [heads, len(rows), d] and the
+    quantised operands."""
+    S, d = qkv_bits.shape[0], qkv_bits.shape[-1]
+    rot = i8_rotation_for(S, d)
     rows = np.arange(S) if rows is None else np.asarray(rows)
-    out = np.zeros((heads, len(rows), D), np.float32)
+    out = np.zeros((heads, len(rows), d), np.float32)
     parts = {"q8": [], "qs": [], "k8": [], "ks": [], "v8": [], "vs": [], "anchor": []}
     for h in range(heads):
         q, k, v = (np.ascontiguousarray(qkv_bits[:, i, h]) for i in range(3))

@@ -11,14 +11,16 @@
  *     raising their abs-max by more than 12.5 %. Subtracting one key from all keys shifts every score of a query by
  *     the same amount, so softmax is unchanged;
  *   - the Hadamard rotations applied to Q and K before quantisation (quant_qk_int8.cu:75-155), in the same
- *     operation order: H4 on each lane's 4 channels, or a fixed sign flip followed by the normalised H128 built as H4
- *     within a lane and five xor butterflies across 32 lanes (channel 4l + c belongs to lane l). Q and K get the same
- *     orthogonal rotation, so their dot products are unchanged;
+ *     operation order: H4 on each lane's 4 channels; or, for head dim 128, a fixed sign flip followed by the
+ *     normalised H128 built as H4 within a lane and five xor butterflies across 32 lanes (channel 4l + c belongs to
+ *     lane l); or, for head dim 64, the plain normalised H64: H4 within a lane and four xor butterflies across 16
+ *     lanes, times 1/4 (convrot64). Q and K get the same orthogonal rotation, so their dot products are unchanged;
  *   - int8 quantisation by round-to-nearest-even with saturation of x * (1 / scale) (float_utils.cuh:40-51), with
  *     scale = absmax / 127 + 1e-7 for Q and K (quant_qk_int8.cu:245-247) and max(absmax / 127, 1e-12) per channel for
  *     V (quant_v_int8.cu:113-116);
- *   - the attention over the quantised operands: s = (q8 . k8) * q_scale * k_scale / sqrt(128) (scale 0x3DB504F3,
- *     launch.zig:414), softmax over all keys, O = sum_j P_j (v8_j * v_scale).
+ *   - the attention over the quantised operands: s = (q8 . k8) * q_scale * k_scale * scale (the caller's scale: H3
+ *     passes 128^-0.5 as fp32, 0x3DB504F3, launch.zig:414), softmax over all keys, O = sum_j P_j (v8_j * v_scale).
+ * Head dims 128 (the engine's) and 64 (the wheel's other case, kitchen_launch.cu:196-241); d is an argument.
  * Scale granularity is this build's choice (one Q scale per query row, one K scale per 16 consecutive keys, one V
  * scale per channel), not the reference's thread-group layout; the arithmetic inside a group is the reference's.
  */
@@ -27,7 +29,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#define D 128
+#define DMAX 128
 
 static float bf16f(uint16_t h) {
     union { uint32_t u; float f; } v;
@@ -60,9 +62,11 @@ static void convrot4(float* v) {
     v[3] = (a1 - a3) * 0.5f;
 }
 
-/* kind 0: none; 4: H4 per lane; 128: sign flip + H128 */
-void lro_i8_rotate(float* x, int kind) {
+/* One row of d channels (d / 4 lanes of 4). kind 0: none; 4: H4 per lane; 128: sign flip + H128 (d 128);
+ * 64: H64 (d 64). */
+void lro_i8_rotate(float* x, int d, int kind) {
     if (kind == 0) return;
+    const int lanes = d / 4;
     if (kind == 128) {
         static const uint32_t signs[4] = {0x1035997bu, 0x8087f5eeu, 0xee2e4e1au, 0x71132418u};
         for (int lane = 0; lane < 32; ++lane) {
@@ -71,30 +75,31 @@ void lro_i8_rotate(float* x, int kind) {
             for (int c = 0; c < 4; ++c) x[4 * lane + c] = flip_sign(x[4 * lane + c], ((s >> (shift + c)) & 1u) ^ 1u);
         }
     }
-    for (int lane = 0; lane < 32; ++lane) convrot4(x + 4 * lane);
-    if (kind != 128) return;
-    float prev[D];
-    for (int bit = 1; bit < 32; bit <<= 1) {
-        memcpy(prev, x, sizeof(prev));
-        for (int lane = 0; lane < 32; ++lane)
+    for (int lane = 0; lane < lanes; ++lane) convrot4(x + 4 * lane);
+    if (kind != 128 && kind != 64) return;
+    float prev[DMAX];
+    for (int bit = 1; bit < lanes; bit <<= 1) {
+        memcpy(prev, x, sizeof(float) * (size_t)d);
+        for (int lane = 0; lane < lanes; ++lane)
             for (int c = 0; c < 4; ++c) {
                 const float mine = prev[4 * lane + c], other = prev[4 * (lane ^ bit) + c];
                 x[4 * lane + c] = (lane & bit) ? other - mine : mine + other;
             }
     }
-    for (int i = 0; i < D; ++i) x[i] *= 0.1767766952966369f;
+    const float norm = kind == 128 ? 0.1767766952966369f : 0.25f;
+    for (int i = 0; i < d; ++i) x[i] *= norm;
 }
 
-/* One kv head's anchor row, or -1. k: the head's first key, rows k_rs elements apart, Lk keys. */
-int lro_i8_anchor(const uint16_t* k, int64_t k_rs, int Lk) {
+/* One kv head's anchor row, or -1. k: the head's first key, rows k_rs elements apart, Lk keys of d channels. */
+int lro_i8_anchor(const uint16_t* k, int64_t k_rs, int Lk, int d) {
     enum { NS = 9 };
-    double s[NS][D];
+    double s[NS][DMAX];
     for (int i = 0; i < NS; ++i) {
         const int row = (int)((int64_t)i * (Lk - 1) / (NS - 1));
-        for (int c = 0; c < D; ++c) s[i][c] = bf16f(k[(int64_t)row * k_rs + c]);
+        for (int c = 0; c < d; ++c) s[i][c] = bf16f(k[(int64_t)row * k_rs + c]);
     }
     double orig_e = 0.0, orig_m = 0.0, dist[NS] = {0};
-    for (int c = 0; c < D; ++c) {
+    for (int c = 0; c < d; ++c) {
         double sum = 0.0;
         for (int i = 0; i < NS; ++i) {
             orig_e += s[i][c] * s[i][c];
@@ -110,7 +115,7 @@ int lro_i8_anchor(const uint16_t* k, int64_t k_rs, int Lk) {
     for (int j = 1; j < NS; ++j)
         if (dist[j] < dist[best]) best = j;
     double best_e = 0.0, best_m = 0.0;
-    for (int c = 0; c < D; ++c)
+    for (int c = 0; c < d; ++c)
         for (int i = 0; i < NS; ++i) {
             const double r = s[i][c] - s[best][c];
             best_e += r * r;
@@ -120,47 +125,46 @@ int lro_i8_anchor(const uint16_t* k, int64_t k_rs, int Lk) {
     return improves ? (int)((int64_t)best * (Lk - 1) / (NS - 1)) : -1;
 }
 
-/* Quantise `rows` rows of one head: subtract row `anchor` (>= 0) first, rotate, then one scale per `group` rows
- * (group 1: per row). out: int8 [rows][128]; scales: [ceil(rows / group)]. */
-void lro_i8_quant_rows(const uint16_t* x, int64_t x_rs, int rows, int rot, int anchor, int group, int8_t* out,
+/* Quantise `rows` rows of one head (d channels): subtract row `anchor` (>= 0) first, rotate, then one scale per
+ * `group` rows (group 1: per row). out: int8 [rows][d]; scales: [ceil(rows / group)]. */
+void lro_i8_quant_rows(const uint16_t* x, int64_t x_rs, int rows, int d, int rot, int anchor, int group, int8_t* out,
                        float* scales) {
-    float a[D];
-    for (int c = 0; c < D; ++c) a[c] = anchor >= 0 ? bf16f(x[(int64_t)anchor * x_rs + c]) : 0.0f;
+    float a[DMAX];
+    for (int c = 0; c < d; ++c) a[c] = anchor >= 0 ? bf16f(x[(int64_t)anchor * x_rs + c]) : 0.0f;
     for (int g0 = 0; g0 < rows; g0 += group) {
         const int n = rows - g0 < group ? rows - g0 : group;
-        float v[64][D];   /* group <= 64 */
+        float v[64][DMAX];   /* group <= 64 */
         float mx = 0.0f;
         for (int r = 0; r < n; ++r) {
-            for (int c = 0; c < D; ++c) v[r][c] = bf16f(x[(int64_t)(g0 + r) * x_rs + c]) - a[c];
-            lro_i8_rotate(v[r], rot);
-            for (int c = 0; c < D; ++c) mx = fmaxf(mx, fabsf(v[r][c]));
+            for (int c = 0; c < d; ++c) v[r][c] = bf16f(x[(int64_t)(g0 + r) * x_rs + c]) - a[c];
+            lro_i8_rotate(v[r], d, rot);
+            for (int c = 0; c < d; ++c) mx = fmaxf(mx, fabsf(v[r][c]));
         }
         const float sc = mx / 127.0f + 1e-7f;
         const float inv = 1.0f / sc;
         scales[g0 / group] = sc;
         for (int r = 0; r < n; ++r)
-            for (int c = 0; c < D; ++c) out[(int64_t)(g0 + r) * D + c] = rn_sat_s8(v[r][c] * inv);
+            for (int c = 0; c < d; ++c) out[(int64_t)(g0 + r) * d + c] = rn_sat_s8(v[r][c] * inv);
     }
 }
 
-/* V of one head: one scale per channel over all rows. out: int8 [rows][128]; scales: [128]. */
-void lro_i8_quant_v(const uint16_t* v, int64_t v_rs, int rows, int8_t* out, float* scales) {
-    for (int c = 0; c < D; ++c) {
+/* V of one head: one scale per channel over all rows. out: int8 [rows][d]; scales: [d]. */
+void lro_i8_quant_v(const uint16_t* v, int64_t v_rs, int rows, int d, int8_t* out, float* scales) {
+    for (int c = 0; c < d; ++c) {
         float mx = 0.0f;
         for (int r = 0; r < rows; ++r) mx = fmaxf(mx, fabsf(bf16f(v[(int64_t)r * v_rs + c])));
         const float sc = fmaxf(mx * (1.0f / 127.0f), 1e-12f);
         const float inv = 1.0f / sc;
         scales[c] = sc;
-        for (int r = 0; r < rows; ++r) out[(int64_t)r * D + c] = rn_sat_s8(bf16f(v[(int64_t)r * v_rs + c]) * inv);
+        for (int r = 0; r < rows; ++r) out[(int64_t)r * d + c] = rn_sat_s8(bf16f(v[(int64_t)r * v_rs + c]) * inv);
     }
 }
 
-/* Attention of one head over its quantised operands, fp64: q8 [W][128] with qs [W] (one per row); k8 [nk][128] with
- * ks [ceil(nk / kgroup)]; v8 [nk][128] with vs [128]; out fp32 [W][128]. */
+/* Attention of one head over its quantised operands, fp64: q8 [W][d] with qs [W] (one per row); k8 [nk][d] with
+ * ks [ceil(nk / kgroup)]; v8 [nk][d] with vs [d]; out fp32 [W][d]; scale the softmax scale (fp32). */
 void lro_i8_attention(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, int kgroup,
-                      const int8_t* v8, const float* vs, int W, int nk, float* out) {
-    union { uint32_t u; float f; } sm;
-    sm.u = 0x3db504f3u;   /* f32(1/sqrt(128)) */
+                      const int8_t* v8, const float* vs, int W, int nk, int d, float scale, float* out) {
+    const int D = d;
 #pragma omp parallel
     {
     double* s = (double*)malloc(sizeof(double) * (size_t)nk);
@@ -170,10 +174,10 @@ void lro_i8_attention(const int8_t* q8, const float* qs, const int8_t* k8, const
         for (int j = 0; j < nk; ++j) {
             int64_t dot = 0;
             for (int c = 0; c < D; ++c) dot += (int64_t)q8[(int64_t)i * D + c] * k8[(int64_t)j * D + c];
-            s[j] = (double)dot * qs[i] * ks[j / kgroup] * (double)sm.f;
+            s[j] = (double)dot * qs[i] * ks[j / kgroup] * (double)scale;
             if (s[j] > m) m = s[j];
         }
-        double l = 0.0, o[D] = {0};
+        double l = 0.0, o[DMAX] = {0};
         for (int j = 0; j < nk; ++j) {
             const double p = exp(s[j] - m);
             l += p;
@@ -190,9 +194,8 @@ void lro_i8_attention(const int8_t* q8, const float* qs, const int8_t* k8, const
  * P_j = round(exp2(x_j - m_t)) in [0, 255]; the row sum is taken over the rounded P; tile t enters O and the row sum
  * with weight exp2(m_t - M), M = max_t m_t. fp64 otherwise. */
 void lro_i8_attention_p8(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, int kgroup,
-                         const int8_t* v8, const float* vs, int W, int nk, int cta, float* out) {
-    union { uint32_t u; float f; } sm;
-    sm.u = 0x3db504f3u;
+                         const int8_t* v8, const float* vs, int W, int nk, int d, float scale, int cta, float* out) {
+    const int D = d;
     const double log2e = 1.4426950408889634, offset = (double)7.9943534f;
     const int ntiles = (nk + cta - 1) / cta;
 #pragma omp parallel
@@ -204,7 +207,7 @@ void lro_i8_attention_p8(const int8_t* q8, const float* qs, const int8_t* k8, co
         for (int j = 0; j < nk; ++j) {
             int64_t dot = 0;
             for (int c = 0; c < D; ++c) dot += (int64_t)q8[(int64_t)i * D + c] * k8[(int64_t)j * D + c];
-            x[j] = (double)dot * qs[i] * ks[j / kgroup] * (double)sm.f * log2e;
+            x[j] = (double)dot * qs[i] * ks[j / kgroup] * (double)scale * log2e;
         }
         double M = -INFINITY;
         for (int t = 0; t < ntiles; ++t) {
@@ -213,10 +216,10 @@ void lro_i8_attention_p8(const int8_t* q8, const float* qs, const int8_t* k8, co
             mt[t] = m - offset;
             if (mt[t] > M) M = mt[t];
         }
-        double l = 0.0, o[D] = {0};
+        double l = 0.0, o[DMAX] = {0};
         for (int t = 0; t < ntiles; ++t) {
             const double w = exp2(mt[t] - M);
-            double lt = 0.0, ot[D] = {0};
+            double lt = 0.0, ot[DMAX] = {0};
             for (int j = t * cta; j < nk && j < (t + 1) * cta; ++j) {
                 double p = rint(exp2(x[j] - mt[t]));
                 p = p < 0.0 ? 0.0 : p > 255.0 ? 255.0 : p;

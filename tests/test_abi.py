@@ -158,13 +158,13 @@ def test_rms_rope_rejects():
     assert L.lr_rms_rope_qk_bf16(A, A, 4, 2, 768, 768, None, A, A, 192, 96, 1e-5, None) == HIP_ERROR_INVALID_VALUE
 
 
-def _i8_plan(B, H, HK, Sq, Sk):
+def _i8_plan(B, H, HK, Sq, Sk, d=128):
     """The INT8 workspace layout, restated: parts in order, each starting on a 256-byte boundary."""
-    cta = 128 if Sk > 1024 else 64
+    cta = 128 if Sk > 1024 and d == 128 else 64
     nt = -(-Sk // cta)
     skp, nvc = nt * cta, -(-Sk // 256)
-    parts = [B * H * Sq * 128, B * HK * skp * 128, B * HK * skp * 128, B * HK * nt * 1024, B * H * Sq * 4,
-             B * HK * 128 * 4, B * HK * nvc * 128 * 4, B * HK * 4]
+    parts = [B * H * Sq * d, B * HK * skp * d, B * HK * skp * d, B * HK * nt * 1024, B * H * Sq * 4,
+             B * HK * d * 4, B * HK * nvc * d * 4, B * HK * 4]
     return sum(-(-p // 256) * 256 for p in parts)
 
 
@@ -173,9 +173,11 @@ def test_int8_workspace_bytes():
     for args in ((1, 56, 56, 5967, 5967), (1, 2, 2, 80, 80), (2, 4, 2, 300, 1100), (1, 3, 1, 1, 1), (1, 2, 2, 1024, 1024),
                  (1, 2, 2, 1025, 1025)):
         assert L.lr_int8_attention_workspace_bytes(*args, 128) == _i8_plan(*args), args
-    assert L.lr_int8_attention_workspace_bytes(1, 2, 2, 8, 8, 64) == 0       # head dim 64 is not built
-    # the wheel's head-dim-64 case (kitchen_launch.cu:196), e.g. 1797 tokens of 32 heads x 64: rejected, not computed
-    assert L.lr_int8_attention_workspace_bytes(1, 32, 32, 1797, 1797, 64) == 0
+    # head dim 64 (kitchen_launch.cu:196-241): 64-key tiles at every length, e.g. the gate's 1797 tokens x 32 heads
+    for args in ((1, 32, 32, 1797, 1797), (1, 2, 2, 80, 80), (2, 4, 2, 300, 1100)):
+        assert L.lr_int8_attention_workspace_bytes(*args, 64) == _i8_plan(*args, 64), args
+    for d in (32, 96, 256):
+        assert L.lr_int8_attention_workspace_bytes(1, 2, 2, 8, 8, d) == 0, d
     assert L.lr_int8_attention_workspace_bytes(1, 3, 2, 8, 8, 128) == 0      # H % HK
     assert L.lr_int8_attention_workspace_bytes(0, 2, 2, 8, 8, 128) == 0
 
@@ -190,7 +192,7 @@ def test_int8_rejects():
         a.update(kw)
         return getattr(L, fn)(*a.values())
 
-    for kw, why in ((dict(D=64), "head dim"), (dict(H=3), "H % HK"), (dict(q=A + 8), "misaligned q"),
+    for kw, why in ((dict(D=96), "head dim"), (dict(H=3), "H % HK"), (dict(q=A + 8), "misaligned q"),
                     (dict(k_sn=100), "stride not a multiple of 8"), (dict(ws=A + 16), "workspace alignment"),
                     (dict(ws=0), "no workspace"), (dict(scale=0.0), "scale"), (dict(Sk=0), "empty"),
                     (dict(o=A + 2), "misaligned out")):
@@ -198,7 +200,8 @@ def test_int8_rejects():
     assert call("lr_int8_attention_rows", B=2, q_sb=8 * 768) == HIP_ERROR_INVALID_VALUE  # rows: B 1 only
     d64 = dict(H=32, HK=32, Sq=1797, Sk=1797, D=64, q_sh=64, q_sn=3 * 32 * 64, k_sh=64, k_sn=3 * 32 * 64, v_sh=64,
                v_sn=3 * 32 * 64)
-    assert call(**d64) == HIP_ERROR_INVALID_VALUE and call("lr_int8_attention_rows", **d64) == HIP_ERROR_INVALID_VALUE
+    assert call(**dict(d64, D=96)) == HIP_ERROR_INVALID_VALUE             # only 64 and 128
+    assert call(**dict(d64, k_sn=100)) == HIP_ERROR_INVALID_VALUE          # head dim 64 keeps the stride rule
     assert L.lr_int8_attention_kernel(A, 0x100000, 1, 2, 2, 8, 8, 128, 0.088, 2, None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_int8_attention_prep(A, A, A, A + 64, 1, 2, 2, 8, 8, 128, 0, 768, 1536, 0, 768, 1536, 0, 768, 1536,
                                     None) == HIP_ERROR_INVALID_VALUE

@@ -8,7 +8,8 @@ through the C ABI.
   * the rows output equals the [H, S, D] output transposed, bit for bit; the one-call entry point equals prep + kernel.
 Cases follow the reference's own gate (tools/twin/stk_twin/h3/test_kitchen.py:22-100): packed qkv views, S on both
 sides of the H4 / H128 switch (256) and of the 64 / 128 key tile switch (1024), a biased K that makes the anchor fire,
-GQA and batches, and H3's shape (5,967 tokens x 56 heads).
+GQA and batches, and H3's shape (5,967 tokens x 56 heads); at head dim 64 (the wheel's other case,
+kitchen_launch.cu:196-241: H4 or the plain H64, 64-key tiles, scale 1/8) the gate's 1,797 x 32 x 64 and small cases.
 """
 from __future__ import annotations
 
@@ -26,7 +27,9 @@ from localrouter_amd import ops  # noqa: E402
 
 
 # ------------------------------------------------------------------------------------------ workspace layout, restated
-def _k_swz(r):
+def _k_swz(r, d=128):
+    if d == 64:
+        return ((r >> 1) & 1) | (((r >> 4) & 1) << 1)
     return ((r >> 2) & 4) | ((((r >> 2) ^ r) & 1) << 1) | ((r >> 1) & 1)
 
 
@@ -34,44 +37,45 @@ def _v_swz(d, cta):
     return (((d >> 1) & 7) ^ ((d & 1) << 2)) if cta == 128 else (((d >> 1) ^ (d >> 3)) & 3)
 
 
-def _decode(ws: np.ndarray, B, H, HK, Sq, Sk) -> dict:
-    cta = oracle.i8_cta_for(Sk)
+def _decode(ws: np.ndarray, B, H, HK, Sq, Sk, d=128) -> dict:
+    cta = oracle.i8_cta_for(Sk, d)
     nt = -(-Sk // cta)
     skp, nvc = nt * cta, -(-Sk // 256)
-    sizes = [B * H * Sq * 128, B * HK * skp * 128, B * HK * skp * 128, B * HK * nt * 1024, B * H * Sq * 4,
-             B * HK * 128 * 4, B * HK * nvc * 128 * 4, B * HK * 4]
+    sizes = [B * H * Sq * d, B * HK * skp * d, B * HK * skp * d, B * HK * nt * 1024, B * H * Sq * 4,
+             B * HK * d * 4, B * HK * nvc * d * 4, B * HK * 4]
     off, at = [], 0
     for s in sizes:
         off.append(at)
         at += -(-s // 256) * 256
     part = lambda i: ws[off[i]:off[i] + sizes[i]]  # noqa: E731
     r = np.arange(skp)
-    kst = part(1).view(np.int8).reshape(B, HK, skp, 8, 16)
-    kidx = np.arange(8)[None, :] ^ np.array([_k_swz(x & 31) for x in r])[:, None]
-    k8 = np.take_along_axis(kst, kidx[None, None, :, :, None], axis=3).reshape(B, HK, skp, 128)
+    kst = part(1).view(np.int8).reshape(B, HK, skp, d // 16, 16)
+    kidx = np.arange(d // 16)[None, :] ^ np.array([_k_swz(x & 31, d) for x in r])[:, None]
+    k8 = np.take_along_axis(kst, kidx[None, None, :, :, None], axis=3).reshape(B, HK, skp, d)
     cpr = cta // 16
-    vst = part(2).view(np.int8).reshape(B, HK, nt, 128, cpr, 16)
-    vidx = np.arange(cpr)[None, :] ^ np.array([_v_swz(d, cta) for d in range(128)])[:, None]
-    vt = np.take_along_axis(vst, vidx[None, None, None, :, :, None], axis=4).reshape(B, HK, nt, 128, cta)
-    v8 = vt.transpose(0, 1, 2, 4, 3).reshape(B, HK, skp, 128)
+    vst = part(2).view(np.int8).reshape(B, HK, nt, d, cpr, 16)
+    vidx = np.arange(cpr)[None, :] ^ np.array([_v_swz(c, cta) for c in range(d)])[:, None]
+    vt = np.take_along_axis(vst, vidx[None, None, None, :, :, None], axis=4).reshape(B, HK, nt, d, cta)
+    v8 = vt.transpose(0, 1, 2, 4, 3).reshape(B, HK, skp, d)
     aux = part(3).reshape(B, HK, nt, 1024)
-    cs = aux[..., :512].copy().view(np.int16).reshape(B, HK, nt, 2, 32, 4)
-    cs = cs.transpose(0, 1, 2, 3, 5, 4).reshape(B, HK, nt, 2, 128)          # [half][dim]
+    db = d // 32
+    cs = aux[..., :128 * db].copy().view(np.int16).reshape(B, HK, nt, 2, 32, db)
+    cs = cs.transpose(0, 1, 2, 3, 5, 4).reshape(B, HK, nt, 2, d)            # [half][dim]
     nb = cta // 32
     ks = aux[..., 512:512 + 8 * nb].copy().view(np.float32).reshape(B, HK, nt, 2, nb)
     ks = ks.transpose(0, 1, 2, 4, 3).reshape(B, HK, nt * 2 * nb)              # group order 2 kb + half per tile
-    return dict(cta=cta, skp=skp, q8=part(0).view(np.int8).reshape(B, H, Sq, 128),
+    return dict(cta=cta, skp=skp, q8=part(0).view(np.int8).reshape(B, H, Sq, d),
                 qs=part(4).view(np.float32).reshape(B, H, Sq), k8=k8, ks=ks, v8=v8, cs=cs,
-                vs=part(5).view(np.float32).reshape(B, HK, 128), anchor=part(7).view(np.int32).reshape(B, HK))
+                vs=part(5).view(np.float32).reshape(B, HK, d), anchor=part(7).view(np.int32).reshape(B, HK))
 
 
 # ------------------------------------------------------------------------------------------ inputs and the oracle
-def _qkv(seed, S, H, bias_heads=()):
-    """Packed qkv bits [S, 3, H, 128] ~ N(0, 1); heads in bias_heads get a large common key offset (anchor fires)."""
-    qkv = oracle.synth_bf16(seed, 1, (S, 3, H, 128))
+def _qkv(seed, S, H, bias_heads=(), d=128):
+    """Packed qkv bits [S, 3, H, d] ~ N(0, 1); heads in bias_heads get a large common key offset (anchor fires)."""
+    qkv = oracle.synth_bf16(seed, 1, (S, 3, H, d))
     if bias_heads:
         f = bf16_f32(qkv)
-        off = 3.0 * bf16_f32(oracle.synth_bf16(seed, 2, (1, 128)))
+        off = 3.0 * bf16_f32(oracle.synth_bf16(seed, 2, (1, d)))
         for h in bias_heads:
             f[:, 1, h] += off[0]
         qkv = oracle.f32_to_bf16(f)
@@ -79,8 +83,8 @@ def _qkv(seed, S, H, bias_heads=()):
 
 
 def _oracle_head(q, k, v, Sk):
-    """The oracle's quantised operands of one (query head, kv head) pair: bf16 bits [Sq,128], [Sk,128], [Sk,128]."""
-    rot = oracle.i8_rotation_for(Sk)
+    """The oracle's quantised operands of one (query head, kv head) pair: bf16 bits [Sq, d], [Sk, d], [Sk, d]."""
+    rot = oracle.i8_rotation_for(Sk, q.shape[-1])
     a = oracle.i8_anchor(k)
     q8, qs = oracle.i8_quant_rows(q, rot)
     k8, ks = oracle.i8_quant_rows(k, rot, a, oracle.I8_KGROUP)
@@ -105,18 +109,19 @@ def _check_parts(dec, ref, b, h, hk, Sk, what):
     assert np.array_equal(dec["v8"][b, hk, :Sk], ref["v8"]), f"{what}: v8"
     assert not dec["v8"][b, hk, Sk:].any(), f"{what}: v8 padding"
     assert np.array_equal(dec["vs"][b, hk].view(np.uint32), ref["vs"].view(np.uint32)), f"{what}: v scales"
-    v8p = np.zeros((dec["skp"], 128), np.int64)
+    d = ref["v8"].shape[1]
+    v8p = np.zeros((dec["skp"], d), np.int64)
     v8p[:Sk] = ref["v8"]
-    halves = v8p.reshape(-1, 2, cta // 2, 128).sum(2)
+    halves = v8p.reshape(-1, 2, cta // 2, d).sum(2)
     assert np.array_equal(dec["cs"][b, hk].astype(np.int64), halves), f"{what}: column sums"
 
 
 def _check_out(got_bits, ref, rows, what):
-    """got: bf16 [Sq_sel, 128] of one head; ref: the oracle's quantised operands of that head."""
+    """got: bf16 [Sq_sel, d] of one head; ref: the oracle's quantised operands of that head."""
     got = bf16_f32(got_bits).astype(np.float64)
     assert np.all(np.isfinite(got)), f"{what}: non-finite"
     args = (ref["q8"][rows], ref["qs"][rows], ref["k8"], ref["ks"], ref["v8"], ref["vs"])
-    emu = oracle.i8_attention_p8(*args, oracle.i8_cta_for(len(ref["k8"]))).astype(np.float64)
+    emu = oracle.i8_attention_p8(*args, oracle.i8_cta_for(len(ref["k8"]), ref["q8"].shape[1])).astype(np.float64)
     # the emulation differs only by fp32 exponent arithmetic (a u8 step flips now and then: <= 2 * max|v| / rowsum)
     # and the bf16 output rounding (<= 2^-9 relative)
     d = np.abs(got - emu)
@@ -233,3 +238,74 @@ def test_int8_h3_shape():
         _check_parts(dec, ref, 0, h, h, S, f"h={h}")
         stats = _check_out(got[h][sel], ref, sel, f"h={h}")
         print(f"  h={h} emu {stats[0]:.2e}/{stats[1]:.2e} fp64q {stats[2]:.2e}/{stats[3]:.2e}", flush=True)
+
+
+def _exact_bar_d64(ref, rows, exact):
+    """Against exact attention at head dim 64: BASELINE's bar, or 1.25x the error the reference's algorithm itself
+    makes (fp64 attention over the oracle's quantised operands) where that is larger: 64 channels and few keys leave
+    more quantisation error than the bar allows."""
+    args = (ref["q8"][rows], ref["qs"][rows], ref["k8"], ref["ks"], ref["v8"], ref["vs"])
+    e = np.abs(oracle.i8_attention(*args).astype(np.float64) - exact)
+    return max(MAX_ABS, 1.25 * e.max()), max(MEAN_ABS, 1.25 * e.mean())
+
+
+@pytest.mark.parametrize("S,H,bias", [(80, 2, ()), (300, 2, (1,)), (1100, 2, (0,))])
+def test_int8_head_dim_64(S, H, bias):
+    """Head dim 64: H4 up to 256 keys, else the plain H64; 64-key tiles at every length; scale 1/8. Prep bit-exact,
+    attention within the bars, against exact attention too; rows == transpose; one call == prep + kernel."""
+    print(f"\n[int8 d64] S={S} H={H} bias={bias}", flush=True)
+    qkv = _qkv(25, S, H, bias, d=64)
+    dq = to_dev(qkv.reshape(S, 3 * H * 64))
+    ws = ops.kitchen_attention_prep(dq, None, H, head_dim=64)
+    out = ops.kitchen_attention_kernel(torch.empty((H, S, 64), dtype=torch.bfloat16, device="cuda"), ws, H, S, False,
+                                       head_dim=64)
+    rows = ops.kitchen_attention_kernel(torch.empty((S, H * 64), dtype=torch.bfloat16, device="cuda"), ws, H, S, True,
+                                        head_dim=64)
+    one = ops.kitchen_attention(dq, H, head_dim=64)
+    torch.cuda.synchronize()
+    dec = _decode(ws.cpu().numpy(), 1, H, H, S, S, d=64)
+    got, got_rows, got_one = from_dev(out), from_dev(rows), from_dev(one)
+    assert np.array_equal(got_rows.reshape(S, H, 64).transpose(1, 0, 2), got), "rows != [H, S, D] transposed"
+    assert np.array_equal(got_one, got), "one call != prep + kernel"
+    qf = bf16_f32(qkv)
+    for h in range(H):
+        ref = _oracle_head(*(np.ascontiguousarray(qkv[:, i, h]) for i in range(3)), S)
+        if h in bias:
+            assert ref["anchor"] >= 0, "the biased head must use its anchor"
+        _check_parts(dec, ref, 0, h, h, S, f"d64 S={S} h={h}")
+        stats = _check_out(got[h], ref, np.arange(S), f"d64 S={S} h={h}")
+        exact = oracle.brute_attention(qf[:, 0, h][:, None], qf[:, 1, h][:, None], qf[:, 2, h][:, None], scale=0.125)[:, 0]
+        d = np.abs(bf16_f32(got[h]).astype(np.float64) - exact)
+        bar = _exact_bar_d64(ref, np.arange(S), exact)
+        print(f"  h={h} anchor={ref['anchor']} emu {stats[0]:.2e}/{stats[1]:.2e} fp64q {stats[2]:.2e}/{stats[3]:.2e} "
+              f"exact {d.max():.2e}/{d.mean():.2e} (bar {bar[0]:.2e}/{bar[1]:.2e})", flush=True)
+        assert d.max() <= bar[0] and d.mean() <= bar[1], f"d64 S={S} h={h}: vs exact {d.max():.3e} {d.mean():.3e}"
+
+
+def test_int8_head_dim_64_gate_shape():
+    """The reference gate's head-dim-64 case (tools/twin/stk_twin/h3/test_kitchen.py:22): 1,797 tokens x 32 heads x 64
+    from one packed qkv buffer, rows output. The oracle checks three heads (every prep part, 96 query rows each)."""
+    S, H = 1797, 32
+    print(f"\n[int8 d64 gate] S={S} H={H}", flush=True)
+    qkv = _qkv(26, S, H, bias_heads=(31,), d=64)
+    dq = to_dev(qkv.reshape(S, 3 * H * 64))
+    ws = torch.empty(ops.int8_workspace_bytes(H, S, head_dim=64), dtype=torch.uint8, device="cuda")
+    rows = ops.kitchen_attention(dq, H, workspace=ws, rows=True, head_dim=64)
+    torch.cuda.synchronize()
+    got = from_dev(rows).reshape(S, H, 64).transpose(1, 0, 2)
+    dec = _decode(ws.cpu().numpy(), 1, H, H, S, S, d=64)
+    sel = np.unique(np.concatenate([np.arange(32), np.linspace(32, S - 33, 32).astype(int), np.arange(S - 32, S)]))
+    qf = bf16_f32(qkv)
+    for h in (0, 17, 31):
+        ref = _oracle_head(*(np.ascontiguousarray(qkv[:, i, h]) for i in range(3)), S)
+        if h == 31:
+            assert ref["anchor"] >= 0
+        _check_parts(dec, ref, 0, h, h, S, f"d64 gate h={h}")
+        stats = _check_out(got[h][sel], ref, sel, f"d64 gate h={h}")
+        exact = oracle.brute_attention(qf[sel, 0, h][:, None], qf[:, 1, h][:, None], qf[:, 2, h][:, None], scale=0.125)[:, 0]
+        d = np.abs(bf16_f32(got[h][sel]).astype(np.float64) - exact)
+        bar = _exact_bar_d64(ref, sel, exact)
+        print(f"  h={h} emu {stats[0]:.2e}/{stats[1]:.2e} fp64q {stats[2]:.2e}/{stats[3]:.2e} "
+              f"exact {d.max():.2e}/{d.mean():.2e} (bar {bar[0]:.2e}/{bar[1]:.2e})", flush=True)
+        assert d.max() <= bar[0] and d.mean() <= bar[1], f"d64 gate h={h}: vs exact {d.max():.3e} {d.mean():.3e}"
+    assert np.all(np.isfinite(bf16_f32(got)))

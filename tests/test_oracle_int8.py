@@ -30,9 +30,9 @@ def _sign_vector():
     return out
 
 
-def _rotation_matrix(kind):
+def _rotation_matrix(kind, d=128):
     # row i of the result is the rotation of basis vector e_i, so its transpose maps inputs to outputs
-    return oracle.i8_rotate(np.eye(128, dtype=np.float32), kind).T.astype(np.float64)
+    return oracle.i8_rotate(np.eye(d, dtype=np.float32), kind).T.astype(np.float64)
 
 
 def test_signed_h128_closed_form():
@@ -45,10 +45,19 @@ def test_signed_h128_closed_form():
     assert (_sign_vector() < 0).sum() not in (0, 128)
 
 
+def test_plain_h64_closed_form():
+    """Head dim 64 (convrot64, quant_qk_int8.cu:110-129): the Sylvester-Hadamard matrix of order 64, entries
+    (-1)^popcount(i & j) / 8, no sign flip; orthogonal."""
+    M = _rotation_matrix(64, 64)
+    pc = np.array([[bin(i & j).count("1") & 1 for j in range(64)] for i in range(64)])
+    assert np.abs(M - np.where(pc == 1, -1.0, 1.0) / 8.0).max() < 1e-7
+    assert np.abs(M @ M.T - np.eye(64)).max() < 1e-6
+
+
 def test_h4_blocks():
-    M = _rotation_matrix(4)
     h4 = 0.5 * np.array([[1, 1, 1, 1], [1, -1, 1, -1], [1, 1, -1, -1], [1, -1, -1, 1]], np.float64)
-    assert np.array_equal(M, np.kron(np.eye(32), h4))
+    for d in (128, 64):
+        assert np.array_equal(_rotation_matrix(4, d), np.kron(np.eye(d // 4), h4))
 
 
 def test_rotation_keeps_dot_products():
@@ -56,6 +65,10 @@ def test_rotation_keeps_dot_products():
     q = rng.standard_normal((5, 128)).astype(np.float32)
     k = rng.standard_normal((7, 128)).astype(np.float32)
     for kind in (4, 128):
+        qr, kr = oracle.i8_rotate(q, kind), oracle.i8_rotate(k, kind)
+        assert np.allclose(qr @ kr.T, q @ k.T, atol=1e-4)
+    q, k = q[:, :64].copy(), k[:, :64].copy()
+    for kind in (4, 64):
         qr, kr = oracle.i8_rotate(q, kind), oracle.i8_rotate(k, kind)
         assert np.allclose(qr @ kr.T, q @ k.T, atol=1e-4)
 
@@ -223,3 +236,26 @@ def test_p8_rounding_against_numpy():
         d = np.abs(got - exact)
         assert 0 < d.max() < 4 * 127 * vs.max() / 255, (W, nk, cta, d.max())
     assert oracle.i8_cta_for(1024) == 64 and oracle.i8_cta_for(1025) == 128
+
+
+def test_chain_head_dim_64_close_to_exact_attention():
+    """Head dim 64 at scale 1/8: the chain (H64 or H4, anchor, per-row / per-16-key / per-channel scales, cta 64)
+    within BASELINE's bar of fp64 attention of the bf16 inputs; P rounded per 64-key tile within a few u8 steps."""
+    rng = np.random.default_rng(21)
+    for S, H in ((300, 3), (200, 2)):
+        x = (rng.standard_normal((S, 3, H, 64)) * np.array([1.0, 1.0, 1.0])[None, :, None, None]).astype(np.float32)
+        qkv = oracle.f32_to_bf16(x)
+        out, parts = oracle.int8_attention(qkv, H)
+        assert out.shape == (H, S, 64) and oracle.i8_rotation_for(S, 64) == (4 if S <= 256 else 64)
+        xf = oracle.bf16_to_f32(qkv).astype(np.float64)
+        for h in range(H):
+            s = xf[:, 0, h] @ xf[:, 1, h].T / 8.0
+            p = np.exp(s - s.max(1, keepdims=True))
+            exact = (p / p.sum(1, keepdims=True)) @ xf[:, 2, h]
+            d = np.abs(out[h] - exact)
+            assert d.max() < 2e-2 and d.mean() < 2e-3, (S, h, d.max(), d.mean())
+            args = [parts[n][h] for n in ("q8", "qs", "k8", "ks", "v8", "vs")]
+            p8 = oracle.i8_attention_p8(*args, oracle.i8_cta_for(S, 64))
+            assert np.abs(p8 - out[h]).max() < 4 * 127 * parts["vs"][h].max() / 255
+    assert oracle.i8_cta_for(5000, 64) == 64 and oracle.i8_scale(64) == 0.125
+
