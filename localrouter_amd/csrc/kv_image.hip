@@ -6,8 +6,8 @@
 // key buffer after the prefix, v copied).
 //
 // One workgroup per (kv head, 64-key tile): it loads the tile's 64 key rows and 64 value rows (256 contiguous bytes
-// each), normalises and rotates the keys in registers, writes both images into LDS, then stores the 32 KB with fully
-// coalesced 16-byte stores. HBM-bound: 32 KB in and 32 KB out per tile.
+// each), normalises and rotates the keys in registers, writes both images into LDS (a staging copy, see stg), then
+// stores the 32 KB with fully coalesced 16-byte stores. HBM-bound: 32 KB in and 32 KB out per tile.
 #include "lr_common.h"
 #include "lr_kernels.h"
 #include "tile_image.h"
@@ -19,6 +19,14 @@ namespace {
 #include "rope_rows.inc"
 
 constexpr int KROWS = 4;   // key rows per thread (rows g, g + 16, g + 32, g + 48 of the tile)
+
+// Where the 16 bytes at image offset o sit in the LDS staging copy: o with its 16-byte position inside the 128-byte
+// line XORed by bits of the line index (a bijection on 16-byte units that keeps every line in place). The eight
+// lanes of a write group put one key row's chunks 512-1024 bytes apart, all at the same position of their lines
+// (eight lanes on four banks each: an 8-way conflict), and an 8-dim block of values the same way; the XOR spreads
+// both over the line (conflict-free for the keys, 2-way for the values), while the copy-out, eight consecutive
+// 16-byte units of one line per group, stays conflict-free.
+__device__ __forceinline__ int stg(int o) { return o ^ ((((o >> 7) ^ (o >> 10)) & 7) << 4); }
 
 // One 256-thread block: tile tile_id (kv head * tiles + tile) of the keys and of the values, through img (32 KB of
 // LDS: the key image, then the value image).
@@ -128,7 +136,7 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
 #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
         }
-        *reinterpret_cast<u32x4*>(img + img_k_offset(r, c)) = o;
+        *reinterpret_cast<u32x4*>(img + stg(img_k_offset(r, c))) = o;
     }
 
     // ---- values: an 8-key x 8-dim block transposed in registers, 8 dims of 16 bytes (8 keys each)
@@ -144,7 +152,7 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
                 const uint32_t lo = vin[2 * w][e >> 1], hi = vin[2 * w + 1][e >> 1];
                 y[w] = (e & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
             }
-            *reinterpret_cast<u32x4*>(img + IMG_TILE_BYTES + img_v_offset(vkg, 8 * vdg + e)) = y;
+            *reinterpret_cast<u32x4*>(img + IMG_TILE_BYTES + stg(img_v_offset(vkg, 8 * vdg + e))) = y;
         }
     }
     __syncthreads();
@@ -155,8 +163,8 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
 #pragma unroll
     for (int p = 0; p < IMG_TILE_BYTES / 4096; ++p) {
         const int off = p * 4096 + 16 * tid;
-        *reinterpret_cast<u32x4*>(kdst + off) = *reinterpret_cast<const u32x4*>(img + off);
-        *reinterpret_cast<u32x4*>(vdst + off) = *reinterpret_cast<const u32x4*>(img + IMG_TILE_BYTES + off);
+        *reinterpret_cast<u32x4*>(kdst + off) = *reinterpret_cast<const u32x4*>(img + stg(off));
+        *reinterpret_cast<u32x4*>(vdst + off) = *reinterpret_cast<const u32x4*>(img + IMG_TILE_BYTES + stg(off));
     }
 }
 
