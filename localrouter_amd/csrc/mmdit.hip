@@ -86,13 +86,18 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 // out row r (txt rows 0..n_txt-1, then img rows) = LayerNorm(x_r) * (1 + scale) + shift with the row's stream's
 // modulation chunk (shift = mod[which * 3 D .. + D), scale = the next D), two-pass mean and variance in fp32.
-__global__ __launch_bounds__(LN_THREADS) void ln_modulate_kernel(const uint16_t* txt, const uint16_t* img, int n_txt,
-                                                                 int D, const uint16_t* mod_txt,
-                                                                 const uint16_t* mod_img, int which, uint16_t* out) {
+// RES: first the gated residual of the half before, x_r += g * a_r (gated_residual_kernel's arithmetic, g the gate
+// chunk of `res_which`), x_r stored and normalised as the bf16 values stored. out may be a (each workgroup reads its
+// whole row of a before the first barrier and writes out after the second).
+template <bool RES>
+__global__ __launch_bounds__(LN_THREADS) void ln_modulate_kernel(uint16_t* txt, uint16_t* img, int n_txt, int D,
+                                                                 const uint16_t* mod_txt, const uint16_t* mod_img,
+                                                                 int which, uint16_t* out, const uint16_t* a,
+                                                                 int res_which) {
     __shared__ float red[LN_THREADS / 64];
     const int r = blockIdx.x;
     const bool is_txt = r < n_txt;
-    const uint16_t* x = is_txt ? txt + (int64_t)r * D : img + (int64_t)(r - n_txt) * D;
+    uint16_t* x = is_txt ? txt + (int64_t)r * D : img + (int64_t)(r - n_txt) * D;
     const uint16_t* mod = (is_txt ? mod_txt : mod_img) + (int64_t)which * 3 * D;
     const int chunks = D / 8;
     Chunk8 c[LN_MAX_CHUNKS];
@@ -102,6 +107,13 @@ __global__ __launch_bounds__(LN_THREADS) void ln_modulate_kernel(const uint16_t*
         const int ch = threadIdx.x + k * LN_THREADS;
         if (ch < chunks) {
             c[k] = load8(x + 8 * ch);
+            if constexpr (RES) {
+                const uint16_t* g = (is_txt ? mod_txt : mod_img) + (int64_t)res_which * 3 * D + 2 * D;
+                const Chunk8 av = load8(a + (int64_t)r * D + 8 * ch), gv = load8(g + 8 * ch);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) c[k].v[e] = bf(tobf(fmaf(av.v[e], gv.v[e], c[k].v[e])));   // as stored
+                store8(x + 8 * ch, c[k]);
+            }
 #pragma unroll
             for (int e = 0; e < 8; ++e) s += c[k].v[e];
         }
@@ -170,8 +182,10 @@ __global__ void gated_residual_kernel(uint16_t* txt, uint16_t* img, int n_txt, i
 }
 
 // y[n] = sum_k x[k] w[n, k] for one input row (the time and modulation vectors): HBM-bound on w, one wave per
-// output, 16-byte loads along the weight row, a butterfly sum. K a multiple of 8.
+// output, 16-byte loads along the weight row, a butterfly sum. K a multiple of 8. SILU: y = SiLU of the bf16 result,
+// the arithmetic of silu_kernel (the time MLP's two activations without launches of their own).
 constexpr int GEMV_WAVES = 4;
+template <bool SILU>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(const uint16_t* x, const uint16_t* w, uint16_t* y, int N,
                                                                int K) {
     const int n = blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -185,7 +199,14 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(const uint16_t* x
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane == 0) y[n] = tobf(acc);
+    if (lane == 0) {
+        if constexpr (SILU) {
+            const float v = bf(tobf(acc));
+            y[n] = tobf(v / (1.0f + expf(-v)));
+        } else {
+            y[n] = tobf(acc);
+        }
+    }
 }
 
 // ---- hipBLASLt GEMMs: row-major Y[M, N] (row stride ldy) = X[M, K] (row stride ldx) W[N, K]^T, bf16 in and out,
@@ -334,7 +355,7 @@ bool is_vector(int64_t M, int64_t K, const void* X, const void* W) {
 int gemm(Ctx& c, const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
          void* ws, hipStream_t s, bool plan_new = false, int epi = EPI_NONE) {
     if (is_vector(M, K, X, W)) {   // a vector: HBM-bound
-        hipLaunchKernelGGL(gemv_kernel, dim3((unsigned)((N + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), 0,
+        hipLaunchKernelGGL(gemv_kernel<false>, dim3((unsigned)((N + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), 0,
                            s, static_cast<const uint16_t*>(X), static_cast<const uint16_t*>(W),
                            static_cast<uint16_t*>(Y), (int)N, (int)K);
         return (int)hipGetLastError();
@@ -574,20 +595,27 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     // time embedding and modulation (vectors: one row)
     hipLaunchKernelGGL(time_sinusoid_kernel, dim3(1), dim3(256), 0, s, t, emb);
     LR_LAUNCHED();
-    LR_TRY(gemm(c, emb, 256, w->t1, h1, D, 1, D, 256, gws, s));
-    hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((D + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s, h1, h1,
-                       (int)D);
-    LR_LAUNCHED();
-    LR_TRY(gemm(c, h1, D, w->t2, temb, D, 1, D, D, gws, s));
-    hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((D + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s, temb,
-                       ts, (int)D);
-    LR_LAUNCHED();
+    // linear -> SiLU twice: the GEMV applies the SiLU when it serves the vector (aligned, K a multiple of 8)
+    auto linear_silu = [&](const uint16_t* x_, const void* w_, uint16_t* pre, uint16_t* y_, int64_t N, int64_t K) -> int {
+        if (is_vector(1, K, x_, w_)) {
+            hipLaunchKernelGGL(gemv_kernel<true>, dim3((unsigned)((N + GEMV_WAVES - 1) / GEMV_WAVES)),
+                               dim3(64 * GEMV_WAVES), 0, s, x_, static_cast<const uint16_t*>(w_), y_, (int)N, (int)K);
+            return (int)hipGetLastError();
+        }
+        int r = gemm(c, x_, K, w_, pre, N, 1, N, K, gws, s);
+        if (r) return r;
+        hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((N + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s, pre,
+                           y_, (int)N);
+        return (int)hipGetLastError();
+    };
+    LR_TRY(linear_silu(emb, w->t1, h1, h1, D, 256));
+    LR_TRY(linear_silu(h1, w->t2, temb, ts, D, D));
     LR_TRY(gemm(c, ts, D, w->txt.mod, mod_txt, 6 * D, 1, 6 * D, D, gws, s));
     LR_TRY(gemm(c, ts, D, w->img.mod, mod_img, 6 * D, 1, 6 * D, D, gws, s));
 
     // attention half: LN + modulation (both streams, one launch), QKV per stream into the joint rows
-    hipLaunchKernelGGL(ln_modulate_kernel, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D, mod_txt,
-                       mod_img, 0, hn);
+    hipLaunchKernelGGL(ln_modulate_kernel<false>, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D,
+                       mod_txt, mod_img, 0, hn, nullptr, 0);
     LR_LAUNCHED();
     const int64_t tD = (int64_t)n_txt * D, tF = (int64_t)n_txt * F;
     LR_TRY(pair_gemm(hn, hn + tD, D, w->txt.qkv, w->img.qkv, qkv, qkv + 3 * tD, 3 * D, 3 * D, D));
@@ -597,13 +625,10 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
                                     lr_joint_attention_workspace_bytes((int)S, (int)H), stream));
     LR_TRY(pair_gemm(attn, attn + tD, D, w->txt.out, w->img.out, hn, hn + tD, D, D, D));
     const unsigned res_blocks = (unsigned)((S * (D / 8) + EW_THREADS - 1) / EW_THREADS);
-    hipLaunchKernelGGL(gated_residual_kernel, dim3(res_blocks), dim3(EW_THREADS), 0, s, xt, xi, n_txt, (int)S, (int)D,
-                       hn, mod_txt, mod_img, 0);
-    LR_LAUNCHED();
 
-    // MLP half
-    hipLaunchKernelGGL(ln_modulate_kernel, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D, mod_txt,
-                       mod_img, 1, hn);
+    // MLP half: the attention half's gated residual (x += gate_0 * hn) and the LayerNorm + modulation in one launch
+    hipLaunchKernelGGL(ln_modulate_kernel<true>, dim3((unsigned)S), dim3(LN_THREADS), 0, s, xt, xi, n_txt, (int)D,
+                       mod_txt, mod_img, 1, hn, hn, 0);
     LR_LAUNCHED();
     if (n_txt > 0)
         LR_TRY(gemm(c, hn, D, w->txt.mlp_up, big, F, n_txt, F, D, gws, s, false, gelu_fused[0] ? EPI_GELU : EPI_NONE));
