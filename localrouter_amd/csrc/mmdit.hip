@@ -181,6 +181,29 @@ __global__ void gated_residual_kernel(uint16_t* txt, uint16_t* img, int n_txt, i
     store8(x + 8 * ch, xv);
 }
 
+// The gated residual of rows whose down-projection ran as KSPLIT slices: a = bf16(sum of the slices' fp32 partials, in
+// slice order), as the unsliced GEMM's bf16 output; then x = fma(a, g, x) as gated_residual_kernel. part is
+// [KSPLIT][rows][D] fp32, g the gate chunk (mod[which * 3 D + 2 D .. + D)); one 8-element chunk per thread.
+__global__ void ksum_residual_kernel(uint16_t* x, const float* part, int rows, int D, const uint16_t* mod, int which,
+                                     int nslices) {
+    const int chunks = D / 8;
+    const int64_t i = (int64_t)blockIdx.x * EW_THREADS + threadIdx.x;
+    if (i >= (int64_t)rows * chunks) return;
+    const int64_t slice = (int64_t)rows * D, off = 8 * i;   // element offset of this chunk in one slice
+    f32x4 s0 = *reinterpret_cast<const f32x4*>(part + off), s1 = *reinterpret_cast<const f32x4*>(part + off + 4);
+    for (int j = 1; j < nslices; ++j) {
+        s0 += *reinterpret_cast<const f32x4*>(part + j * slice + off);
+        s1 += *reinterpret_cast<const f32x4*>(part + j * slice + off + 4);
+    }
+    const int64_t r = i / chunks, ch = i - r * chunks;
+    uint16_t* xr = x + r * D + 8 * ch;
+    const Chunk8 gv = load8(mod + (int64_t)which * 3 * D + 2 * D + 8 * ch);
+    Chunk8 xv = load8(xr);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xv.v[e] = fmaf(bf(tobf(e < 4 ? s0[e] : s1[e - 4])), gv.v[e], xv.v[e]);
+    store8(xr, xv);
+}
+
 // y[n] = sum_k x[k] w[n, k] for one input row (the time and modulation vectors): HBM-bound on w, one wave per
 // output, 16-byte loads along the weight row, a butterfly sum. K a multiple of 8. SILU: y = SiLU of the bf16 result,
 // the arithmetic of silu_kernel (the time MLP's two activations without launches of their own).
@@ -221,7 +244,13 @@ struct GemmPlan {
 // M, N, K, ldx, ldy, epilogue (EPI_NONE, or EPI_GELU: y = GELU(x w^T) applied to the fp32 result before the bf16
 // store, hipBLASLt's GELU epilogue, which takes the place of gelu_tanh_kernel for the MLP up-projection)
 using GemmKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int>;
-constexpr int EPI_NONE = 0, EPI_GELU = 1;
+constexpr int EPI_NONE = 0, EPI_GELU = 1, EPI_KSPLIT = 2;
+// EPI_KSPLIT: the down-projection of a stream of at most KSPLIT_ROWS rows as one strided-batched GEMM over KSPLIT
+// slices of K with fp32 partials (row-major [slice][M][N]), summed by ksum_residual_kernel: a 512-row down-projection
+// alone gives hipBLASLt too few output tiles for the 256 CUs.
+constexpr int KSPLIT = 4;
+constexpr int64_t KSPLIT_ROWS = 1024;
+bool ksplit_rows(int64_t M, int64_t F) { return M > 1 && M <= KSPLIT_ROWS && F % (8 * KSPLIT) == 0; }
 
 // A context's plans are built by lr_mmdit_plan / lr_mmdit_tune (and by lr_mmdit_linear_bf16 for a new shape) under
 // `mu`; the block call only looks them up. A plan is never removed before the context is destroyed, so a pointer to
@@ -275,9 +304,25 @@ int plan_gemm(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
         if ((rc = blas_err(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &e, sizeof e))))
             return fail(rc);
     }
-    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K)))) return fail(rc);
-    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, ldx)))) return fail(rc);
-    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, ldy)))) return fail(rc);
+    const int64_t Ks = epi == EPI_KSPLIT ? K / KSPLIT : K;
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, Ks, N, K)))) return fail(rc);
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, Ks, M, ldx)))) return fail(rc);
+    if ((rc = blas_err(hipblasLtMatrixLayoutCreate(&p.lc, epi == EPI_KSPLIT ? HIP_R_32F : HIP_R_16BF, N, M, ldy))))
+        return fail(rc);
+    if (epi == EPI_KSPLIT) {   // slice i: K columns [i Ks, (i + 1) Ks) of W and X, partial i at i M N floats
+        const int32_t bc = KSPLIT;
+        const int64_t sa = Ks, sb = Ks, sc = N * M;
+        for (hipblasLtMatrixLayout_t l : {p.la, p.lb, p.lc})
+            if ((rc = blas_err(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof bc))))
+                return fail(rc);
+        if ((rc = blas_err(hipblasLtMatrixLayoutSetAttribute(p.la, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sa,
+                                                             sizeof sa))) ||
+            (rc = blas_err(hipblasLtMatrixLayoutSetAttribute(p.lb, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sb,
+                                                             sizeof sb))) ||
+            (rc = blas_err(hipblasLtMatrixLayoutSetAttribute(p.lc, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sc,
+                                                             sizeof sc))))
+            return fail(rc);
+    }
     if ((rc = blas_err(hipblasLtMatmulPreferenceCreate(&pref)))) return fail(rc);
     const uint64_t ws = GEMM_WS;
     if ((rc = blas_err(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
@@ -387,7 +432,7 @@ std::vector<GemmKey> block_gemms(int64_t n_txt, int64_t n_img, int64_t D, int64_
         g.push_back(GemmKey{M, 3 * D, D, D, 3 * D, EPI_NONE});
         g.push_back(GemmKey{M, D, D, D, D, EPI_NONE});
         g.push_back(GemmKey{M, F, D, D, F, EPI_GELU});
-        g.push_back(GemmKey{M, D, F, F, D, EPI_NONE});
+        g.push_back(ksplit_rows(M, F) ? GemmKey{M, D, F, F, D, EPI_KSPLIT} : GemmKey{M, D, F, F, D, EPI_NONE});
     }
     return g;
 }
@@ -398,21 +443,26 @@ int up_epi(Ctx& c, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
     if (find_plan(c, M, N, K, ldx, ldy, EPI_GELU)) return EPI_GELU;
     return find_plan(c, M, N, K, ldx, ldy, EPI_NONE) ? EPI_NONE : -1;
 }
+// Likewise for a down-projection: EPI_KSPLIT when its stream qualifies and the sliced plan exists, else EPI_NONE.
+int down_epi(Ctx& c, int64_t M, int64_t D, int64_t F) {
+    if (ksplit_rows(M, F) && find_plan(c, M, D, F, F, D, EPI_KSPLIT)) return EPI_KSPLIT;
+    return find_plan(c, M, D, F, F, D, EPI_NONE) ? EPI_NONE : -1;
+}
 
 // Plan one block GEMM; the up-projection falls back to the plain plan (and gelu_tanh_kernel) when hipBLASLt has no
-// algorithm with the GELU epilogue for it.
+// algorithm with the GELU epilogue for it, a sliced down-projection to the plain plan when it has none for the slices.
 int plan_block_gemm(Ctx& c, const GemmKey& k) {
     GemmPlan* p;
     int rc = plan_gemm(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k),
                        std::get<5>(k), &p);
-    if (rc && std::get<5>(k) == EPI_GELU)
+    if (rc && (std::get<5>(k) == EPI_GELU || std::get<5>(k) == EPI_KSPLIT))
         rc = plan_gemm(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k), EPI_NONE, &p);
     return rc;
 }
 
 // scratch layout of one block call
 struct Scratch {
-    size_t emb, h1, temb, ts, mod_txt, mod_img, hn, qkv, attn, big, gws, attn_ws, total;
+    size_t emb, h1, temb, ts, mod_txt, mod_img, hn, qkv, attn, big, gws, attn_ws, kpart_txt, kpart_img, total;
 };
 Scratch layout(int64_t n_txt, int64_t n_img, int64_t D, int64_t F) {
     const int64_t S = n_txt + n_img;
@@ -435,6 +485,9 @@ Scratch layout(int64_t n_txt, int64_t n_img, int64_t D, int64_t F) {
     s.attn = take(S * D * 2);        // attention output
     s.big = take(S * F * 2);         // MLP hidden
     s.attn_ws = take(lr_joint_attention_workspace_bytes((int)S, (int)(D / 128)));
+    // the sliced down-projections' fp32 partials (streams that qualify)
+    s.kpart_txt = take(ksplit_rows(n_txt, F) ? (size_t)KSPLIT * n_txt * D * 4 : 0);
+    s.kpart_img = take(ksplit_rows(n_img, F) ? (size_t)KSPLIT * n_img * D * 4 : 0);
     s.total = o;
     return s;
 }
@@ -521,8 +574,15 @@ int lr_mmdit_tune(void* ctx, const lr_mmdit_weights* w, int n_txt, int n_img, in
                                 candidates);
         if (!rc) rc = tune_gemm(c, attn + r0 * D, D, sw[k]->out, hn + r0 * D, D, M, D, D, EPI_NONE, gws, s, candidates);
         if (!rc) rc = tune_gemm(c, hn + r0 * D, D, sw[k]->mlp_up, big + r0 * F, F, M, F, D, epi, gws, s, candidates);
-        if (!rc) rc = tune_gemm(c, big + r0 * F, F, sw[k]->mlp_down, attn + r0 * D, D, M, D, F, EPI_NONE, gws, s,
-                                candidates);
+        if (!rc)
+            rc = plan_block_gemm(c, ksplit_rows(M, F) ? GemmKey{M, D, F, F, D, EPI_KSPLIT} : GemmKey{M, D, F, F, D, EPI_NONE});
+        int depi = EPI_NONE;
+        if (!rc) {
+            std::lock_guard<std::mutex> lock(c.mu);
+            depi = down_epi(c, M, D, F);
+        }
+        void* ydown = depi == EPI_KSPLIT ? (void*)(ws + (k == 0 ? L.kpart_txt : L.kpart_img)) : (void*)(attn + r0 * D);
+        if (!rc) rc = tune_gemm(c, big + r0 * F, F, sw[k]->mlp_down, ydown, D, M, D, F, depi, gws, s, candidates);
     }
     return rc;
 }
@@ -551,18 +611,18 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     Ctx& c = *static_cast<Ctx*>(ctx);
     // every row GEMM's plan exists (lr_mmdit_plan / lr_mmdit_tune), checked before anything is launched; the
     // up-projection of a stream of rows (text 0, image 1) has its GELU fused when its plan carries the epilogue
-    bool gelu_fused[2] = {false, false};
+    bool gelu_fused[2] = {false, false}, ksplit[2] = {false, false};
     {
         std::lock_guard<std::mutex> lock(c.mu);
         const int64_t rows[2] = {n_txt, n_img}, D = hidden, F = mlp;
         for (int k = 0; k < 2; ++k) {
             const int64_t M = rows[k];
             if (M <= 1) continue;   // a vector: gemv_kernel, no plan
-            if (!find_plan(c, M, 3 * D, D, D, 3 * D) || !find_plan(c, M, D, D, D, D) || !find_plan(c, M, D, F, F, D))
-                return hipErrorNotReady;
-            const int e = up_epi(c, M, F, D, D, F);
-            if (e < 0) return hipErrorNotReady;
+            if (!find_plan(c, M, 3 * D, D, D, 3 * D) || !find_plan(c, M, D, D, D, D)) return hipErrorNotReady;
+            const int e = up_epi(c, M, F, D, D, F), de = down_epi(c, M, D, F);
+            if (e < 0 || de < 0) return hipErrorNotReady;
             gelu_fused[k] = e == EPI_GELU;
+            ksplit[k] = de == EPI_KSPLIT;
         }
     }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -644,10 +704,35 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
             LR_LAUNCHED();
         }
     }
-    LR_TRY(pair_gemm(big, big + tF, F, w->txt.mlp_down, w->img.mlp_down, attn, attn + tD, D, D, F));
-    hipLaunchKernelGGL(gated_residual_kernel, dim3(res_blocks), dim3(EW_THREADS), 0, s, xt, xi, n_txt, (int)S, (int)D,
-                       attn, mod_txt, mod_img, 1);
-    LR_LAUNCHED();
+    // down-projections, then the MLP half's gated residual: a sliced stream's rows by ksum_residual_kernel (which
+    // sums its partials), the other rows by gated_residual_kernel
+    float* kpart[2] = {reinterpret_cast<float*>(ws + L.kpart_txt), reinterpret_cast<float*>(ws + L.kpart_img)};
+    if (n_txt > 0)
+        LR_TRY(gemm(c, big, F, w->txt.mlp_down, ksplit[0] ? (void*)kpart[0] : (void*)attn, D, n_txt, D, F, gws, s, false,
+                    ksplit[0] ? EPI_KSPLIT : EPI_NONE));
+    if (n_img > 0)
+        LR_TRY(gemm(c, big + tF, F, w->img.mlp_down, ksplit[1] ? (void*)kpart[1] : (void*)(attn + tD), D, n_img, D, F,
+                    gws, s, false, ksplit[1] ? EPI_KSPLIT : EPI_NONE));
+    if (!ksplit[0] && !ksplit[1]) {
+        hipLaunchKernelGGL(gated_residual_kernel, dim3(res_blocks), dim3(EW_THREADS), 0, s, xt, xi, n_txt, (int)S,
+                           (int)D, attn, mod_txt, mod_img, 1);
+        LR_LAUNCHED();
+    } else {
+        uint16_t* xs[2] = {xt, xi};
+        const uint16_t* mods[2] = {mod_txt, mod_img};
+        const int64_t rows[2] = {n_txt, n_img}, row0[2] = {0, n_txt};
+        for (int k = 0; k < 2; ++k) {
+            if (rows[k] == 0) continue;
+            const unsigned blocks = (unsigned)((rows[k] * (D / 8) + EW_THREADS - 1) / EW_THREADS);
+            if (ksplit[k])
+                hipLaunchKernelGGL(ksum_residual_kernel, dim3(blocks), dim3(EW_THREADS), 0, s, xs[k], kpart[k],
+                                   (int)rows[k], (int)D, mods[k], 1, KSPLIT);
+            else   // this stream's rows alone: gated_residual_kernel with no text rows
+                hipLaunchKernelGGL(gated_residual_kernel, dim3(blocks), dim3(EW_THREADS), 0, s, xs[k], xs[k], 0,
+                                   (int)rows[k], (int)D, attn + row0[k] * D, mods[k], mods[k], 1);
+            LR_LAUNCHED();
+        }
+    }
 #undef LR_LAUNCHED
 #undef LR_TRY
     return 0;
