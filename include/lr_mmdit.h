@@ -18,7 +18,9 @@
  * activations bf16 between the steps (fp32 inside each kernel and GEMM). The GEMMs are hipBLASLt's (bf16 in and out,
  * fp32 compute); the up-projection carries hipBLASLt's GELU epilogue where an algorithm has it, so its GELU acts on
  * the fp32 product (one bf16 rounding, not two; a shape without such an algorithm runs the library's GELU-tanh
- * kernel on the bf16 product). Everything else is this library's HIP kernels.
+ * kernel on the bf16 product). The down-projection of a stream of at most 1024 rows runs as 4 slices of K into fp32
+ * partials, summed in slice order and rounded to bf16 before its gated residual (where hipBLASLt serves the sliced
+ * shape; else as one GEMM). Everything else is this library's HIP kernels.
  *
  * Return values follow lr_attn.h: 0 launched, 1 (hipErrorInvalidValue) an argument rejected before any launch, other
  * hipError_t / hipblasStatus_t failures as returned (a hipBLASLt status is reported as 1000 + the status).
