@@ -8,7 +8,9 @@ only (MI355X / MI350X), with packed-fp32 instruction selection switched off.
 from __future__ import annotations
 
 import concurrent.futures
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -40,6 +42,15 @@ HIPCC_FLAGS = [
 # `#pragma unroll`, and a partly unrolled step would index its register arrays at run time
 EXTRA_FLAGS = {"attn_stream.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]}
 
+# Scratch (spill) budget per kernel, bytes per lane. The streaming attention kernel and the INT8 attention kernel count
+# their direct global->LDS refills with explicit `s_waitcnt vmcnt(N)`; a scratch access among those loads would be
+# counted too, and the waits would no longer name the loads they wait for. Each keeps one 4-byte value in scratch
+# that is stored and reloaded only outside its streaming loop (read from the generated assembly). Every other kernel
+# uses none. The build fails when a kernel needs more: the spill must then be found and removed, not accepted.
+SCRATCH_BUDGET = {"attn_stream_kernel": 8, "i8_attn_kernel": 8}
+REMARK_FLAGS = ["-Rpass-analysis=kernel-resource-usage"]
+RESOURCES = PKG / "_build" / "resources.json"
+
 # host-only C++ (the RoPE table builders of include/lr_rope.h): the system compiler, no contraction of f64 products
 # and sums into FMAs, so that tables are the same bits as the numpy builders
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-ffp-contract=off"]
@@ -52,13 +63,48 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build localrouter_amd)")
 
 
-def _run(cmd: list[str]) -> None:
+def kernel_resources(text: str) -> dict[str, dict[str, int]]:
+    """The compiler's kernel-resource-usage remarks: {mangled kernel name: {"VGPRs": n, "AGPRs": n, "ScratchSize": n,
+    ...}} (ScratchSize in bytes per lane)."""
+    out: dict[str, dict[str, int]] = {}
+    cur = None
+    for line in text.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([A-Za-z ]+?)(?: \[bytes/lane\])?(?: \[waves/SIMD\])?: (\d+) \[-Rpass-analysis", line)
+        if m and cur is not None:
+            cur[m.group(1).strip()] = int(m.group(2))
+    return out
+
+
+def scratch_violations(res: dict[str, dict[str, int]]) -> list[str]:
+    """Kernels whose scratch exceeds SCRATCH_BUDGET (0 for a kernel not listed)."""
+    bad = []
+    for name, r in res.items():
+        budget = next((b for k, b in SCRATCH_BUDGET.items() if k in name), 0)
+        if r.get("ScratchSize", 0) > budget:
+            bad.append(f"{name}: {r.get('ScratchSize')} bytes of scratch per lane (budget {budget})")
+    return bad
+
+
+def _run(cmd: list[str]) -> str:
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(l for l in res.stdout.splitlines() if "packed-fp32-ops" not in l)
+    lines = [l for l in res.stdout.splitlines() if "packed-fp32-ops" not in l]
+    shown, in_remark = [], False   # the resource remarks and their source excerpts are parsed, not shown
+    for l in lines:
+        if "-Rpass-analysis=kernel-resource-usage" in l:
+            in_remark = True
+        elif not (in_remark and re.match(r"^\s*\d*\s*\|", l)):
+            in_remark = False
+            shown.append(l)
+    out = "\n".join(shown)
     if res.returncode != 0:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
     if out.strip():
         print(out, file=sys.stderr)
+    return "\n".join(lines)
 
 
 def build(verbose: bool = False) -> Path:
@@ -72,16 +118,21 @@ def build(verbose: bool = False) -> Path:
         if src.endswith(".cpp"):
             cmd = [shutil.which("g++") or "g++", *CXX_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
         else:
-            cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
+            cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), *REMARK_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), file=sys.stderr)
         cmds.append(cmd)
         objs.append(str(obj))
     # the sources compile independently: a few at a time (each hipcc process is single-threaded)
     jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", "0") or 0) or (os.cpu_count() or 1)))
+    res: dict[str, dict[str, int]] = {}
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         for f in [pool.submit(_run, c) for c in cmds]:
-            f.result()
+            res.update(kernel_resources(f.result()))
+    RESOURCES.write_text(json.dumps(res, indent=1, sort_keys=True))
+    bad = scratch_violations(res)
+    if bad:
+        raise RuntimeError("kernels over their scratch budget:\n  " + "\n  ".join(bad))
     tmp = LIB.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, *LIBS, "-o", str(tmp)])
     os.replace(tmp, LIB)
