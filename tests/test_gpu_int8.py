@@ -167,6 +167,28 @@ def test_int8_packed_qkv(S, H, bias):
         assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS, f"S={S} h={h}: vs exact {d.max():.3e} {d.mean():.3e}"
 
 
+def test_int8_anchor_closed_forms():
+    """The prep's anchor on keys whose outcome the criterion fixes in closed form (tests/test_oracle_int8.py
+    _anchor_cases): accepted at sample 3's row, declined on energy, declined on the 12.5 % abs-max cap; the other
+    prep parts bit-exact against the oracle."""
+    from tests.test_oracle_int8 import _anchor_cases
+    cases = _anchor_cases()
+    S, H = 101, len(cases)
+    print(f"\n[int8 anchor closed forms] S={S} H={H}", flush=True)
+    qkv = bf16_f32(_qkv(31, S, H))
+    for h, (name, (k, want)) in enumerate(cases.items()):
+        qkv[:, 1, h] = k
+    qkv = oracle.f32_to_bf16(qkv)
+    dq = to_dev(qkv.reshape(S, 3 * H * 128))
+    ws = ops.kitchen_attention_prep(dq, None, H)
+    torch.cuda.synchronize()
+    dec = _decode(ws.cpu().numpy(), 1, H, H, S, S)
+    for h, (name, (k, want)) in enumerate(cases.items()):
+        assert dec["anchor"][0, h] == want, f"{name}: anchor {dec['anchor'][0, h]}, closed form {want}"
+        ref = _oracle_head(*(np.ascontiguousarray(qkv[:, i, h]) for i in range(3)), S)
+        _check_parts(dec, ref, 0, h, h, S, f"anchor case {name}")
+
+
 @pytest.mark.parametrize("B,H,HK,Sq,Sk", [(2, 4, 2, 200, 333), (1, 3, 1, 513, 1500), (2, 2, 2, 1, 70)])
 def test_int8_gqa_batch_cross(B, H, HK, Sq, Sk):
     """Separate q [B,H,Sq,D] and k, v [B,HK,Sk,D] tensors: GQA (query head h reads kv head h // (H / HK)), batches,

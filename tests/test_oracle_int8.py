@@ -4,8 +4,9 @@ Each part is checked against something it does not share code with:
   * the rotations: the signed H128 equals the closed form (-1)^popcount(i & j) / sqrt(128) times the reference's sign
     vector (the constants of kernels/cuda/minimax/kitchen/quant_qk_int8.cu:93-97), H4 is block-diagonal with the
     4-point Sylvester Hadamard, both are orthogonal and leave dot products of rotated pairs unchanged;
-  * the K anchor: an independent numpy restatement of the criterion of quant_qk_int8.cu:461-596, on data where the
-    centring helps (it must pick an anchor) and where it does not (it must decline);
+  * the K anchor: three key sets whose outcome the criterion of quant_qk_int8.cu:461-596 fixes in closed form
+    (accepted at a known sample, declined on energy, declined on the abs-max cap), with planted slips in the rule
+    failing them, and an independent numpy restatement on random heads where both outcomes occur;
   * the quantisers: scale = absmax / 127 + 1e-7 (Q, K) and absmax / 127 per channel (V), the largest magnitude maps to
     +-127, every element within half a step, ties to even;
   * the attention over quantised operands: an independent numpy fp64 softmax over the dequantised operands, and the
@@ -98,6 +99,61 @@ def test_anchor_against_numpy():
         assert got == _anchor_numpy(oracle.bf16_to_f32(bits)), trial
         seen.add(got >= 0)
     assert seen == {True, False}, "both outcomes must occur"
+
+
+def _anchor_cases(L=101, d=128):
+    """Keys whose anchor outcome the criterion fixes in closed form (all values exact in bf16). The 9 samples are rows
+    i (L-1) // 8; the other rows are noise that the rule never reads.
+      accept: samples = c + delta_j, delta in +- pairs and one zero at sample 3, c large: sample 3 is exactly the mean
+              (distance 0), the residuals are the deltas (energy drops, abs-max shrinks) -> row 3 (L-1) // 8;
+      energy: the same deltas with c = 0: subtracting the zero sample changes nothing (energy equal) -> -1;
+      absmax: delta = +8A at sample 0, -A at the other 8 (sum 0), c0 = -4A: the energy drops (216 A^2 -> 81 A^2) but
+              the abs-max grows from 5A to 9A (> 12.5 %) -> -1."""
+    rng = np.random.default_rng(7)
+    idx = [i * (L - 1) // 8 for i in range(9)]
+    v = [np.zeros(d) for _ in range(4)]
+    for m in range(4):
+        v[m][8 * m:8 * m + 8] = 2.0 ** (m - 2)
+    deltas = [v[0], -v[0], v[1], np.zeros(d), -v[1], v[2], -v[2], v[3], -v[3]]
+    cases = {}
+    for name, c in (("accept", np.full(d, 6.0)), ("energy", np.zeros(d))):
+        k = rng.standard_normal((L, d)).round(2)
+        for j, i in enumerate(idx):
+            k[i] = c + deltas[j]
+        cases[name] = (k, idx[3] if name == "accept" else -1)
+    A = 0.5
+    k = rng.standard_normal((L, d)).round(2)
+    for j, i in enumerate(idx):
+        k[i] = 0.0
+        k[i][0] = -4 * A + (8 * A if j == 0 else -A)
+    cases["absmax"] = (k, -1)
+    return cases
+
+
+def test_anchor_closed_forms():
+    for name, (k, want) in _anchor_cases().items():
+        bits = oracle.f32_to_bf16(k.astype(np.float32))
+        assert np.array_equal(oracle.bf16_to_f32(bits)[[i * 100 // 8 for i in range(9)]],
+                              k[[i * 100 // 8 for i in range(9)]].astype(np.float32)), "samples exact in bf16"
+        assert oracle.i8_anchor(bits) == want, name
+        assert _anchor_numpy(oracle.bf16_to_f32(bits)) == want, name
+
+
+def test_anchor_planted_mistakes_fail():
+    """Each plausible slip in the criterion changes the outcome of one closed-form case."""
+    def variant(k, no_cap=False, bad_index=False, le_energy=False):
+        L = k.shape[0]
+        idx = [i * L // 9 for i in range(9)] if bad_index else [i * (L - 1) // 8 for i in range(9)]
+        s = k[idx].astype(np.float64)
+        best = int(np.argmin(((9 * s - s.sum(0)[None]) ** 2).sum(1)))
+        r = s - s[best][None]
+        e_ok = (r ** 2).sum() <= (s ** 2).sum() if le_energy else (r ** 2).sum() < (s ** 2).sum()
+        m_ok = True if no_cap else np.abs(r).max() <= np.abs(s).max() * 1.125
+        return idx[best] if e_ok and m_ok else -1
+    cases = {n: (oracle.bf16_to_f32(oracle.f32_to_bf16(k.astype(np.float32))), w) for n, (k, w) in _anchor_cases().items()}
+    assert all(variant(k) == w for k, w in cases.values())
+    for slip in ({"no_cap": True}, {"bad_index": True}, {"le_energy": True}):
+        assert any(variant(k, **slip) != w for k, w in cases.values()), slip
 
 
 def test_quantisers():
