@@ -62,7 +62,10 @@ typedef struct ihipStream_t* lr_stream_t;
 #define LR_WEIGHT_BF16 2
 
 /* Attention tile configurations for the _ex entry points (0 = the library's choice: LR_ATTN_CFG_STREAM_W8 for the
- * fused and prepared calls, LR_ATTN_CFG_PIPE_W8 for attention over value rows). */
+ * fused and prepared calls; for attention over value rows LR_ATTN_CFG_PIPE_W4, or LR_ATTN_CFG_PIPE_W8 when the call
+ * is non-causal and its 256-query blocks fill whole rounds of the device's compute units, and LR_ATTN_CFG_PIPE_W8 for a
+ * call split over its
+ * keys through a workspace). */
 #define LR_ATTN_CFG_AUTO 0
 #define LR_ATTN_CFG_PIPE_W8 1      /* attention over value rows: 256 queries per workgroup (8 waves x 32), direct-to-LDS
                                       K/V ring, next tile's QK^T overlapped with the current tile's softmax */

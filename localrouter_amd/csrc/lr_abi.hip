@@ -47,6 +47,8 @@ size_t split_bytes(int W, int H, int ns) {
     return ((rows * lr::D * 4 + 255) & ~(size_t)255) + ((rows * 8 + 255) & ~(size_t)255);
 }
 
+int device_cus();
+
 int attention_impl(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK, int nkeys,
                    int causal, float scale, int64_t q_rs, int64_t k_rs, int64_t v_rs, int64_t o_rs, int64_t k_hs,
                    int64_t v_hs, int config, hipStream_t stream, void* workspace = nullptr, size_t ws_bytes = 0) {
@@ -78,6 +80,15 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
         const hipError_t e = lr::launch_attention(a, LR_ATTN_CFG_PIPE_W8, stream);
         if (e != hipSuccess) return (int)e;
         return (int)lr::launch_split_combine(a, stream);
+    }
+    if (config == LR_ATTN_CFG_AUTO) {
+        // 128 queries per workgroup, two workgroups per CU, unless non-causal 256-query blocks fill whole rounds of
+        // the CUs: measured at cfg1 / cfg2 / causal GQA shapes W4 takes 0.72 / 0.93 / 0.89 of W8's time, at 12,800
+        // and 50,220 tokens the two are within 1.5 %, at 16,384 x 4 heads (exactly one round of 256-query blocks) W8
+        // is 2 % faster; causal blocks differ in work, and W4 stays faster there even when the rounds are whole
+        const int cus = device_cus();
+        const int64_t w8_blocks = (int64_t)((W + 255) / 256) * H;
+        config = !causal && cus > 0 && w8_blocks % cus == 0 ? LR_ATTN_CFG_PIPE_W8 : LR_ATTN_CFG_PIPE_W4;
     }
     return (int)lr::launch_attention(a, config, stream);
 }
