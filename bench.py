@@ -3,11 +3,12 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video|h3-int8|mmdit]
                     [--no-cpu-baseline]
 
-A step is one fused joint-attention call over one synthetic batch, made as the fused call's own two launches so that
-each is timed: the preparation (lr_joint_prepare: keys RMSNorm + RoPE and values into the workspace's tile images,
-queries RMSNorm + RoPE into the output rows, one launch), then the persistent streaming attention kernel over them
-(lr_joint_attention_images) -- together exactly what lr_joint_attention_fused launches. Inputs are resident in HBM
-before timing.
+A step is one lr_joint_attention_fused call over one synthetic batch: the preparation launch (keys RMSNorm + RoPE and
+values into the workspace's tile images, queries RMSNorm + RoPE into the output rows), then the persistent streaming
+attention kernel over them. The K timed steps are K such calls back to back, with HIP events only before and after
+them; `value` and `ms_per_step` come from those. A second loop of K calls made as the same two launches through the
+stage entry points (lr_joint_prepare, lr_joint_attention_images), with an event between them, times the attention
+kernel alone for `roofline` and the preparation. Inputs are resident in HBM before timing.
 The default workload is BASELINE's Qwen-Image-style step: B=1, 24 heads x 128, 512 text + 4096 image tokens (64x64
 grid, 2D RoPE on image tokens, text un-rotated), non-causal, QK-RMSNorm eps 1e-6 with weights 1.0, scale f32(1/sqrt(128)).
 
@@ -211,16 +212,34 @@ def main():
         _lib.call("lr_joint_attention_images", out.data_ptr(), rs, ws.data_ptr(), ws_bytes, out.data_ptr(), rs, S, S,
                   H, H, 0, 0, scale, sh)
 
+    def fused():
+        _lib.call("lr_joint_attention_fused", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), wq.data_ptr(),
+                  wk.data_ptr(), ops.TABLE_COSSIN_F32, cos.data_ptr(), sin.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                  64, ops.PAIR_INTERLEAVED, 128, eps, S, S, H, H, 0, 0, scale, rs, rs, rs, rs, 0, ws.data_ptr(),
+                  ws_bytes, sh)
+
     for _ in range(args.warmup):
+        fused()
         prepare()
         attn()
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
 
     K = args.steps
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
+    # the timed steps: K fused calls, events around the whole loop only
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
+    e0.record(stream)
+    for _ in range(K):
+        fused()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms_step = e0.elapsed_time(e1) / K
+    # the same K calls as their two launches with an event between them: the attention kernel and the preparation
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
+    torch.cuda.synchronize()
     for i in range(K):
         ev[2 * i].record(stream)
         prepare()
@@ -228,20 +247,19 @@ def main():
         attn()
     ev[2 * K].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
     t_prep = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(K)]
     t_attn = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(K)]
-    total_ms = ev[0].elapsed_time(ev[2 * K])
-    ms_step = total_ms / K
+    staged_ms = ev[0].elapsed_time(ev[2 * K]) / K
     flops = 4.0 * S * S * 128 * H
     attn_ms = float(np.mean(t_attn))
     prep_ms = float(np.mean(t_prep))
     value = flops / (ms_step * 1e-3) / 1e12
     achieved = flops / (attn_ms * 1e-3) / 1e12
     clock = from_profile(args.workload, KERNEL, "clock_ghz")
-    log(f"[bench] step {ms_step:.4f} ms (prepare {prep_ms:.4f} ms, attention {attn_ms:.4f} ms, median attention "
-        f"{float(np.median(t_attn)):.4f} ms); {value:.1f} TFLOP/s step, {achieved:.1f} TFLOP/s attention kernel "
-        f"({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); wall {wall:.3f} s")
+    log(f"[bench] step {ms_step:.4f} ms (fused calls; as two timed launches {staged_ms:.4f} ms: prepare {prep_ms:.4f} "
+        f"ms, attention {attn_ms:.4f} ms, median attention {float(np.median(t_attn)):.4f} ms); {value:.1f} TFLOP/s "
+        f"step, {achieved:.1f} TFLOP/s attention kernel ({100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); "
+        f"wall {wall:.3f} s")
 
     result = {
         "metric": METRIC,
