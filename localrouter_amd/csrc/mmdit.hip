@@ -29,15 +29,20 @@ __device__ __forceinline__ uint16_t tobf(float f) { return __builtin_bit_cast(ui
 
 // emb[256] from t (ops.cu:84-99): t scaled by 1000 and rounded to bf16, divided by 1000 (reciprocal multiply) and
 // rounded again, times 1000; freq_i = exp(-ln(10000) i / 128); cos for j < 128, sin for j >= 128.
-__global__ void time_sinusoid_kernel(const float* t, uint16_t* emb) {
-    const int j = threadIdx.x, i = j & 127;
+__device__ __forceinline__ float time_scaled(const float* t) {
     float tr = bf(tobf(t[0] * 1000.0f));
     tr = bf(tobf(tr * (1.0f / 1000.0f)));
-    tr = tr * 1000.0f;
+    return tr * 1000.0f;
+}
+__device__ __forceinline__ uint16_t sinusoid_at(float tr, int j) {
+    const int i = j & 127;
     const float c = -9.210340371976184f;   // -ln(10000)
     const float freq = expf((c * (float)i) * (1.0f / 128.0f));
     const float arg = tr * freq;
-    emb[j] = tobf(j < 128 ? cosf(arg) : sinf(arg));
+    return tobf(j < 128 ? cosf(arg) : sinf(arg));
+}
+__global__ void time_sinusoid_kernel(const float* t, uint16_t* emb) {
+    emb[threadIdx.x] = sinusoid_at(time_scaled(t), threadIdx.x);
 }
 
 // y = x / (1 + exp(-x)), n elements (small vectors)
@@ -206,17 +211,27 @@ __global__ void ksum_residual_kernel(uint16_t* x, const float* part, int rows, i
 
 // y[n] = sum_k x[k] w[n, k] for one input row (the time and modulation vectors): HBM-bound on w, one wave per
 // output, 16-byte loads along the weight row, a butterfly sum. K a multiple of 8. SILU: y = SiLU of the bf16 result,
-// the arithmetic of silu_kernel (the time MLP's two activations without launches of their own).
+// the arithmetic of silu_kernel (the time MLP's two activations without launches of their own). SIN: x is the time
+// sinusoid of *t (K = 256), each element computed where it is used, as time_sinusoid_kernel computes it.
 constexpr int GEMV_WAVES = 4;
-template <bool SILU>
+template <bool SILU, bool SIN = false>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(const uint16_t* x, const uint16_t* w, uint16_t* y, int N,
-                                                               int K) {
+                                                               int K, const float* t = nullptr) {
     const int n = blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (n >= N) return;
     const uint16_t* row = w + (int64_t)n * K;
+    float tr = 0.0f;
+    if constexpr (SIN) tr = time_scaled(t);
     float acc = 0.0f;
     for (int c = lane; c < K / 8; c += 64) {
-        const Chunk8 a = load8(row + 8 * c), b = load8(x + 8 * c);
+        const Chunk8 a = load8(row + 8 * c);
+        Chunk8 b;
+        if constexpr (SIN) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) b.v[e] = bf(sinusoid_at(tr, 8 * c + e));
+        } else {
+            b = load8(x + 8 * c);
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc = fmaf(a.v[e], b.v[e], acc);
     }
@@ -653,8 +668,7 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     };
 
     // time embedding and modulation (vectors: one row)
-    hipLaunchKernelGGL(time_sinusoid_kernel, dim3(1), dim3(256), 0, s, t, emb);
-    LR_LAUNCHED();
+
     // linear -> SiLU twice: the GEMV applies the SiLU when it serves the vector (aligned, K a multiple of 8)
     auto linear_silu = [&](const uint16_t* x_, const void* w_, uint16_t* pre, uint16_t* y_, int64_t N, int64_t K) -> int {
         if (is_vector(1, K, x_, w_)) {
@@ -668,7 +682,15 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
                            y_, (int)N);
         return (int)hipGetLastError();
     };
-    LR_TRY(linear_silu(emb, w->t1, h1, h1, D, 256));
+    if (is_vector(1, 256, emb, w->t1)) {   // sinusoid -> linear -> SiLU in one launch
+        hipLaunchKernelGGL((gemv_kernel<true, true>), dim3((unsigned)((D + GEMV_WAVES - 1) / GEMV_WAVES)),
+                           dim3(64 * GEMV_WAVES), 0, s, nullptr, static_cast<const uint16_t*>(w->t1), h1, (int)D, 256, t);
+        LR_LAUNCHED();
+    } else {
+        hipLaunchKernelGGL(time_sinusoid_kernel, dim3(1), dim3(256), 0, s, t, emb);
+        LR_LAUNCHED();
+        LR_TRY(linear_silu(emb, w->t1, h1, h1, D, 256));
+    }
     LR_TRY(linear_silu(h1, w->t2, temb, ts, D, D));
     LR_TRY(gemm(c, ts, D, w->txt.mod, mod_txt, 6 * D, 1, 6 * D, D, gws, s));
     LR_TRY(gemm(c, ts, D, w->img.mod, mod_img, 6 * D, 1, 6 * D, D, gws, s));
