@@ -1,14 +1,16 @@
 """Benchmark of the DiT joint-attention hot path on one MI355X (gfx950).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen-step|plumbing|edit|video|h3-int8|mmdit]
-                    [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--preroll-s SECONDS]
+                    [--workload qwen-step|plumbing|edit|video|qwen21|h3-int8|mmdit] [--no-cpu-baseline]
 
 A step is one lr_joint_attention_fused call over one synthetic batch: the preparation launch (keys RMSNorm + RoPE and
 values into the workspace's tile images, queries RMSNorm + RoPE into the output rows), then the persistent streaming
-attention kernel over them. The K timed steps are K such calls back to back, with HIP events only before and after
-them; `value` and `ms_per_step` come from those. A second loop of K calls made as the same two launches through the
-stage entry points (lr_joint_prepare, lr_joint_attention_images), with an event between them, times the attention
-kernel alone for `roofline` and the preparation. Inputs are resident in HBM before timing.
+attention kernel over them. After the W warm-up steps, fused calls run untimed for a fixed --preroll-s seconds (1 s by
+default, whatever W is), so that the timed region starts at the GPU's working clock; the line states both. The K
+timed steps are K such calls back to back, with HIP events only before and after them; `value` and `ms_per_step`
+come from those. A second loop of K calls made as the same two launches through the stage entry points
+(lr_joint_prepare, lr_joint_attention_images), with an event between them, times the attention kernel alone for
+`roofline` and the preparation (`staged_ms_per_step`). Inputs are resident in HBM before timing.
 The default workload is BASELINE's Qwen-Image-style step: B=1, 24 heads x 128, 512 text + 4096 image tokens (64x64
 grid, 2D RoPE on image tokens, text un-rotated), non-causal, QK-RMSNorm eps 1e-6 with weights 1.0, scale f32(1/sqrt(128)).
 
@@ -18,6 +20,9 @@ events on the stream it is launched on, against MI355X's published dense bf16 pe
 the shader clock come from the committed rocprofv3 PMC summary of the same command (profiles/). `cpu_baseline` times
 the CPU oracle's fp32 flash-style path (OpenMP, every core the process may use) on a bounded sample of query rows of
 the same workload, as a reported baseline only.
+
+--workload qwen21 is the reference's own call shape (Qwen-Image 2.1, dit.zig:252-293): 4,096 image queries, 32 heads,
+over an 80-key cached text prefix (already rotated, used as given: n_pre = 80) plus the 4,096 image keys.
 
 --workload h3-int8 measures MiniMax H3's INT8 attention instead (5,967 tokens x 56 heads, the reference's headline
 shape for it): a step is Kitchen.attention on one packed qkv buffer, i.e. the prep (anchor, rotation, int8 Q / K / V,
@@ -56,7 +61,14 @@ WORKLOADS = {
     "qwen-step": dict(n_text=512, kind="grid2d", gh=64, gw=64, heads=24),
     "edit": dict(n_text=512, kind="edit", frames=3, gh=64, gw=64, heads=24),
     "video": dict(n_text=512, kind="video3d", t=49, gh=44, gw=80, heads=24),
+    # the reference's own call shape (Qwen-Image 2.1, src/engines/qwen_image/dit.zig:252-293): 4096 image queries over
+    # an 80-row cached text prefix (keys already rotated, copied as they are) plus the 4096 image keys, 32 heads
+    "qwen21": dict(n_text=80, kind="prefix2d", gh=64, gw=64, heads=32),
 }
+# seconds of back-to-back fused calls run after --warmup and before the timed region, whatever --warmup is: the
+# shader clock ramps up over the first ~100 ms of a busy GPU, and a timed region that starts on a cold GPU measures
+# that ramp rather than the kernel (a 5-call warm-up gave 0.312 ms per call, 300 calls 0.2625 ms, same box and build)
+PREROLL_S = 1.0
 
 
 def log(*a):
@@ -70,6 +82,9 @@ def tables(w):
         return rope.grid2d_table(w["n_text"], w["gh"], w["gw"])
     if w["kind"] == "edit":
         return rope.edit_table(w["n_text"], w["frames"], w["gh"], w["gw"])
+    if w["kind"] == "prefix2d":   # the image rows of a text + image table: queries and the keys behind the prefix
+        cos, sin = rope.grid2d_table(w["n_text"], w["gh"], w["gw"])
+        return cos[w["n_text"]:].copy(), sin[w["n_text"]:].copy()
     return rope.video3d_table(w["n_text"], w["t"], w["gh"], w["gw"])
 
 
@@ -106,34 +121,39 @@ def host_cpus():
     return threads, avail, model
 
 
-def cpu_baseline(q_bits, k_bits, v_bits, cos, sin, S, H, flops_per_row, budget_s=10.0):
-    """The oracle's fp32 flash-style path (norm + rope + attention) on a sample of query rows, timed on host cores."""
+def cpu_baseline(q_bits, k_bits, v_bits, cos, sin, Sq, H, flops_per_row, n_pre=0, budget_s=10.0):
+    """The oracle's fp32 flash-style path (norm + rope + attention) on a sample of query rows, timed on host cores.
+    Query row i uses table row i; key j >= n_pre uses table row j - n_pre, keys j < n_pre are used as given."""
     import numpy as np
 
     import oracle
     threads = host_cpus()[0]
     oracle.set_threads(threads)
     rng = np.random.default_rng(0)
+    Sk = k_bits.shape[0]
 
     def run(rows):
         t0 = time.perf_counter()
         # the reference's chain: q and k normalised, rotated and stored as bf16, then the attention
         qh = oracle.rms_rope(q_bits[rows], None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos[rows], tb=sin[rows])
-        kh = oracle.rms_rope(k_bits, None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos, tb=sin)
+        kh = oracle.rms_rope(k_bits[n_pre:], None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos[:Sk - n_pre],
+                             tb=sin[:Sk - n_pre])
         qh = oracle.bf16_to_f32(oracle.f32_to_bf16(qh))
         kh = oracle.bf16_to_f32(oracle.f32_to_bf16(kh))
+        if n_pre:
+            kh = np.concatenate([oracle.bf16_to_f32(k_bits[:n_pre]), kh])
         vf = oracle.bf16_to_f32(v_bits)
-        # all S keys for each sampled query row: the sampled rows are renumbered 0..n-1 (non-causal, so equivalent)
+        # all Sk keys for each sampled query row: the sampled rows are renumbered 0..n-1 (non-causal, so equivalent)
         out = oracle.attention(qh, kh, vf, precise=False)
         return time.perf_counter() - t0, out
 
-    probe = np.sort(rng.choice(S, size=64, replace=False))
+    probe = np.sort(rng.choice(Sq, size=64, replace=False))
     dt, _ = run(probe)
     rate = 64 * flops_per_row / dt
     # as many query rows as fit in a third of the budget (all of them for the image shapes), then repeated runs of that
     # sample until the budget is spent; the median run is reported
-    n = int(min(S, max(64, budget_s / 3 * rate / flops_per_row)) // 32 * 32)
-    rows = np.sort(rng.choice(S, size=n, replace=False))
+    n = int(min(Sq, max(64, budget_s / 3 * rate / flops_per_row)) // 32 * 32)
+    rows = np.sort(rng.choice(Sq, size=n, replace=False))
     times, out, spent = [], None, 0.0
     while spent < budget_s or len(times) < 3:
         dt, out = run(rows)
@@ -141,6 +161,21 @@ def cpu_baseline(q_bits, k_bits, v_bits, cos, sin, S, H, flops_per_row, budget_s
         spent += dt
     dt = float(np.median(times))
     return dict(value=n * flops_per_row / dt / 1e12, threads=threads, rows=rows, out=out, seconds=dt, runs=len(times))
+
+
+def preroll(call, seconds: float):
+    """Back-to-back calls for `seconds` of wall time (synchronised every 50 calls), so that the timed region starts on a
+    GPU already at its working clock. Returns (calls made, seconds spent)."""
+    import torch
+    t0, calls = time.perf_counter(), 0
+    while True:
+        for _ in range(50):
+            call()
+        calls += 50
+        torch.cuda.synchronize()
+        spent = time.perf_counter() - t0
+        if spent >= seconds:
+            return calls, spent
 
 
 def main():
@@ -151,6 +186,8 @@ def main():
     ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS) + ["h3-int8", "mmdit"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--preroll-s", type=float, default=PREROLL_S,
+                    help="seconds of untimed calls after the warm-up and before timing (the GPU's clock settles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 256 MiB device-to-device copy after timing (the known-size kernel that scales "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE into bytes)")
@@ -176,7 +213,11 @@ def main():
     w = WORKLOADS[args.workload]
     H = w["heads"]
     cos_np, sin_np = tables(w)
-    S = cos_np.shape[0]
+    # queries: the table's rows; keys: an n_pre-row cached prefix (already rotated: used as given) plus one key per
+    # query row (key j >= n_pre uses table row j - n_pre)
+    n_pre = w["n_text"] if w["kind"] == "prefix2d" else 0
+    Sq = cos_np.shape[0]
+    Sk = n_pre + Sq
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     L = _lib.load()
@@ -185,19 +226,19 @@ def main():
         raise SystemExit(f"lr_attn_init: {rc} (not a gfx950?)")
     props = torch.cuda.get_device_properties(dev)
     log(f"[bench] device {props.name} {getattr(props, 'gcnArchName', '')} CUs {props.multi_processor_count}; "
-        f"workload {args.workload}: S={S} H={H}")
+        f"workload {args.workload}: Sq={Sq} Sk={Sk} (prefix {n_pre}) H={H}")
 
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed)
-    q = torch.randn((S, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    k = torch.randn((S, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    v = torch.randn((S, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    q = torch.randn((Sq, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    k = torch.randn((Sk, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    v = torch.randn((Sk, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     out = torch.empty_like(q)
     cos = torch.from_numpy(cos_np).to(dev)
     sin = torch.from_numpy(sin_np).to(dev)
     wq = torch.ones(128, dtype=torch.float32, device=dev)
     wk = torch.ones(128, dtype=torch.float32, device=dev)
-    ws_bytes = ops.workspace_bytes(S, H)
+    ws_bytes = ops.workspace_bytes(Sk, H)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
@@ -206,16 +247,16 @@ def main():
     def prepare():
         _lib.call("lr_joint_prepare", q.data_ptr(), rs, out.data_ptr(), rs, k.data_ptr(), rs, v.data_ptr(), rs,
                   wq.data_ptr(), wk.data_ptr(), ops.TABLE_COSSIN_F32, cos.data_ptr(), sin.data_ptr(), cos.data_ptr(),
-                  sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, S, S, H, H, 0, ws.data_ptr(), ws_bytes, sh)
+                  sin.data_ptr(), 64, ops.PAIR_INTERLEAVED, 128, eps, Sq, Sk, H, H, n_pre, ws.data_ptr(), ws_bytes, sh)
 
     def attn():
-        _lib.call("lr_joint_attention_images", out.data_ptr(), rs, ws.data_ptr(), ws_bytes, out.data_ptr(), rs, S, S,
+        _lib.call("lr_joint_attention_images", out.data_ptr(), rs, ws.data_ptr(), ws_bytes, out.data_ptr(), rs, Sq, Sk,
                   H, H, 0, 0, scale, sh)
 
     def fused():
         _lib.call("lr_joint_attention_fused", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), wq.data_ptr(),
                   wk.data_ptr(), ops.TABLE_COSSIN_F32, cos.data_ptr(), sin.data_ptr(), cos.data_ptr(), sin.data_ptr(),
-                  64, ops.PAIR_INTERLEAVED, 128, eps, S, S, H, H, 0, 0, scale, rs, rs, rs, rs, 0, ws.data_ptr(),
+                  64, ops.PAIR_INTERLEAVED, 128, eps, Sq, Sk, H, H, 0, 0, scale, rs, rs, rs, rs, n_pre, ws.data_ptr(),
                   ws_bytes, sh)
 
     for _ in range(args.warmup):
@@ -223,7 +264,8 @@ def main():
         prepare()
         attn()
     torch.cuda.synchronize()
-    log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
+    pre_calls, pre_s = preroll(fused, args.preroll_s)
+    log(f"[bench] warmup {args.warmup} done, pre-roll {pre_calls} calls in {pre_s:.2f} s; timing {args.steps} steps")
 
     K = args.steps
     # the timed steps: K fused calls, events around the whole loop only
@@ -250,7 +292,7 @@ def main():
     t_prep = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(K)]
     t_attn = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(K)]
     staged_ms = ev[0].elapsed_time(ev[2 * K]) / K
-    flops = 4.0 * S * S * 128 * H
+    flops = 4.0 * Sq * Sk * 128 * H
     attn_ms = float(np.mean(t_attn))
     prep_ms = float(np.mean(t_prep))
     value = flops / (ms_step * 1e-3) / 1e12
@@ -268,15 +310,18 @@ def main():
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
+        "preroll": {"calls": pre_calls, "seconds": round(pre_s, 3),
+                    "note": "untimed fused calls after the warm-up, the same for every --warmup"},
         "ms_per_step": round(ms_step, 5),
+        "staged_ms_per_step": round(staged_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"{args.workload}-joint-attention", "batch": 1, "tokens": S, "text_tokens": w["n_text"],
-                   "heads": H, "head_dim": 128, "causal": False, "qk_rmsnorm": True, "rope": w["kind"],
-                   "parallelism": "none (1 GPU)"},
+        "config": {"workload": f"{args.workload}-joint-attention", "batch": 1, "tokens": Sq, "keys": Sk,
+                   "prefix_keys": n_pre, "text_tokens": w["n_text"], "heads": H, "head_dim": 128, "causal": False,
+                   "qk_rmsnorm": True, "rope": w["kind"], "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic_from_profile(args.workload, KERNEL),
@@ -295,12 +340,12 @@ def main():
         del src, dst
 
     if not args.no_cpu_baseline:
-        fl_row = 4.0 * S * 128 * H
+        fl_row = 4.0 * Sk * 128 * H
         log("[bench] cpu baseline (oracle fp32 flash path, sampled query rows) ...")
         qb = q.cpu().view(torch.int16).numpy().view(np.uint16)
         kb = k.cpu().view(torch.int16).numpy().view(np.uint16)
         vb = v.cpu().view(torch.int16).numpy().view(np.uint16)
-        cb = cpu_baseline(qb, kb, vb, cos_np, sin_np, S, H, fl_row)
+        cb = cpu_baseline(qb, kb, vb, cos_np, sin_np, Sq, H, fl_row, n_pre=n_pre)
         got = out.cpu().view(torch.int16).numpy().view(np.uint16)[cb["rows"]]
         gotf = (got.astype(np.uint32) << 16).view(np.float32)
         d = np.abs(gotf.astype(np.float64) - cb["out"])
@@ -308,7 +353,7 @@ def main():
         rel = float(np.linalg.norm(gotf.astype(np.float64) - cb["out"]) / np.linalg.norm(cb["out"].astype(np.float64)))
         result["cpu_baseline"] = {"value": round(cb["value"], 4), "unit": "TFLOP/s", "cores": cb["threads"],
                                   "kind": "port", "host_cpus": avail, "cpu_model": model,
-                                  "sample": f"{len(cb['rows'])} of {S} query rows x {H} heads over all {S} keys "
+                                  "sample": f"{len(cb['rows'])} of {Sq} query rows x {H} heads over all {Sk} keys "
                                             f"(norm+rope+attention, fp32): median of {cb['runs']} runs, "
                                             f"{cb['seconds']:.2f} s each"}
         result["check"] = {"rows": int(len(cb["rows"])), "max_abs": float(d.max()), "mean_abs": float(d.mean()),
@@ -395,7 +440,13 @@ def bench_int8(args):
         prep()
         attn()
     torch.cuda.synchronize()
-    log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
+
+    def pair():
+        prep()
+        attn()
+
+    pre_calls, pre_s = preroll(pair, args.preroll_s)
+    log(f"[bench] warmup {args.warmup} done, pre-roll {pre_calls} calls in {pre_s:.2f} s; timing {args.steps} steps")
     K = args.steps
     # the timed steps: K (prep, kernel) call pairs back to back, as the engine makes them; events around the loop only
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -437,7 +488,10 @@ def bench_int8(args):
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
+        "preroll": {"calls": pre_calls, "seconds": round(pre_s, 3),
+                    "note": "untimed (prep, kernel) pairs after the warm-up, the same for every --warmup"},
         "ms_per_step": round(ms_step, 5),
+        "staged_ms_per_step": round(staged_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -511,7 +565,8 @@ def bench_mmdit(args):
     for _ in range(args.warmup):
         blk(txt, img, t, cos, sin)
     torch.cuda.synchronize()
-    log(f"[bench] warmup {args.warmup} done; timing {args.steps} blocks")
+    pre_calls, pre_s = preroll(lambda: blk(txt, img, t, cos, sin), args.preroll_s)
+    log(f"[bench] warmup {args.warmup} done, pre-roll {pre_calls} blocks in {pre_s:.2f} s; timing {args.steps} blocks")
     K = args.steps
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -549,6 +604,8 @@ def bench_mmdit(args):
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
+        "preroll": {"calls": pre_calls, "seconds": round(pre_s, 3),
+                    "note": "untimed block calls after the warm-up, the same for every --warmup"},
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",

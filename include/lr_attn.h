@@ -78,8 +78,11 @@ typedef struct ihipStream_t* lr_stream_t;
 
 int lr_attn_abi_version(void);
 
-/* Checks that the current HIP device is a gfx950 (MI355X / MI350X). 0 on success, hipErrorInvalidDevice (101)
- * otherwise. Optional: nothing else needs it, it sets no state. */
+/* Checks that the current HIP device is a gfx950 (MI355X / MI350X) and sets up, once per device, the address of the
+ * current device's no-alloc scratch (the static array lr_joint_attention_fused_noalloc uses; its address is looked up
+ * with hipGetSymbolAddress and cached per device under a mutex). 0 on success, hipErrorInvalidDevice (101) otherwise,
+ * or the error of the address lookup. Optional: lr_joint_attention_fused_noalloc sets the address up at its first
+ * call on a device when lr_attn_init was not called there; no other entry point needs it. */
 int lr_attn_init(void);
 
 /*

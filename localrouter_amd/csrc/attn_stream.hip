@@ -83,13 +83,15 @@ __device__ __forceinline__ void fence_q8(bf16x8 (&q)[8]) {
 // Two contiguous 1 KB direct loads, global -> LDS: lane l's 16 bytes of load i come from gaddr + 1024 i + 16 l and
 // land at LDS byte lds + 1024 i + 16 l (the instruction offset applies to both addresses).
 __device__ __forceinline__ void dma2k(uint64_t gaddr, uint32_t voff, uint32_t lds) {
+    LR_ASM_M0_BEGIN
     asm volatile(
         "s_mov_b32 m0, %2\n\t"
         "s_nop 0\n\t"
         "global_load_lds_dwordx4 %0, %1 offset:0\n\t"
         "global_load_lds_dwordx4 %0, %1 offset:1024" ::"v"(voff),
         "s"(gaddr), "s"(lds)
-        : "memory");
+        : "memory", "m0");
+    LR_ASM_M0_END
 }
 
 template <bool B>

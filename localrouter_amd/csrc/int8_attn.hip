@@ -441,9 +441,13 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
     const uint64_t b = (uint64_t)(uintptr_t)base;
     const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
                         (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    // M0 named as clobbered: the compiler keeps no value of its own in it across the statement (the pragmas only
+    // silence clang's warning that M0 is a reserved register)
+    _Pragma("clang diagnostic push") _Pragma("clang diagnostic ignored \"-Winline-asm\"")
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
                  "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory");
+                 : "memory", "m0");
+    _Pragma("clang diagnostic pop")
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {

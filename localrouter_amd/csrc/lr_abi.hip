@@ -1,6 +1,10 @@
 // The C ABI (include/lr_attn.h): argument validation, then launches on the caller's stream.
 // Like kernels/cuda/minimax/kitchen_launch.cu:193-316 every function checks its arguments before launching and
-// returns an int error code; nothing here synchronises, allocates or keeps state between calls.
+// returns an int error code. Nothing here synchronises or allocates. The one state kept between calls is that of the
+// allocation-free entry point (lr_joint_attention_fused_noalloc): a file-scope static __device__ scratch array
+// (LR_JOINT_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends) and a per-device cache of its address, set
+// once per device under a mutex (at lr_attn_init, else at the entry point's first call on that device). Calls of that
+// entry point that overlap on one GPU share the array and race.
 #include <limits.h>
 #include <math.h>
 #include <string.h>
@@ -148,7 +152,10 @@ bool kv_stage_ok(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, c
         return false;
     if (!rows_ok(k_raw, k_rs, HK) || !rows_ok(v, v_rs, HK) || (wk && !aligned(wk, 16))) return false;
     if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return false;
-    return ws && aligned(ws, 256) && ws_bytes >= ws_bytes_needed(Sk, HK);
+    if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return false;
+    // the launch writes the workspace while it reads the keys and values
+    const Span w = ws_span(ws, Sk, HK);
+    return !overlap(w, rows_span(k_raw, Sk, k_rs, HK)) && !overlap(w, rows_span(v, Sk, v_rs, HK));
 }
 
 // The keys stage (arguments checked): RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre; rows j < n_pre
@@ -239,14 +246,15 @@ int prep_launch(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, con
 }
 
 // Checks of the attention stage. o_rs is bounded so that a block's 256 output rows span less than 4 GiB (the
-// kernel's buffer range); out must not overlap the workspace, and q_prep is either out itself (each block reads its
-// queries before it writes its output over them) or apart from it.
+// kernel's 32-bit buffer range: 256 rows * o_rs * 2 bytes < 2^32, i.e. o_rs < 2^23); out must not overlap the
+// workspace, and q_prep is either out itself (each block reads its queries before it writes its output over them) or
+// apart from it.
 bool images_stage_ok(const void* q_prep, int64_t p_rs, const void* ws, size_t ws_bytes, const void* out, int64_t o_rs,
                      int Sq, int Sk, int H, int HK, int p0, int causal, float scale) {
     if (Sq < 1 || Sk < 1 || H < 1 || HK < 1 || H % HK != 0 || p0 < 0 || (causal != 0 && causal != 1)) return false;
     if (!scale_ok(scale)) return false;
     if ((int64_t)p0 + Sq > INT_MAX - 512 || Sk > INT_MAX - 512 || Sq > INT_MAX - 512) return false;
-    if (!rows_ok(q_prep, p_rs, H) || !rows_ok(out, o_rs, H) || o_rs > ((int64_t)1 << 23)) return false;
+    if (!rows_ok(q_prep, p_rs, H) || !rows_ok(out, o_rs, H) || o_rs >= ((int64_t)1 << 23)) return false;
     if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return false;
     const Span so = rows_span(out, Sq, o_rs, H);
     if (overlap(so, ws_span(ws, Sk, HK))) return false;
@@ -305,9 +313,11 @@ int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, c
         !kv_stage_ok(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws,
                      ws_bytes))
         return ERR_ARGS;
-    // the prepared queries are written into out while the keys and values may still be read: no overlap
+    // the prepared queries are written into out while the keys and values may still be read, and the preparation
+    // writes the workspace while it reads q_raw, k_raw and v: no overlap
     const Span so = rows_span(out, Sq, o_rs, H);
     if (overlap(so, rows_span(k_raw, Sk, k_rs, HK)) || overlap(so, rows_span(v, Sk, v_rs, HK))) return ERR_ARGS;
+    if (overlap(rows_span(q_raw, Sq, q_rs, H), ws_span(ws, Sk, HK))) return ERR_ARGS;
     const int e = prep_launch(q_raw, q_rs, out, o_rs, wq, k_raw, k_rs, v, v_rs, wk, table_kind, qta, qtb, kta, ktb,
                               tab_stride, pairing, rot, eps, Sq, Sk, H, HK, n_pre, ws, stream);
     if (e != 0) return e;

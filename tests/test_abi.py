@@ -97,6 +97,10 @@ def _fused(**kw):
     (dict(out=A + 0x1000, k=A + 0x1000), "out overlaps k_raw"),
     (dict(out=A + 0x1000, v=A + 0x1100), "out overlaps v"),
     (dict(ors=(1 << 23) + 8), "out row stride beyond 2^23"),
+    (dict(ors=1 << 23), "out row stride 2^23: a block's 256 rows would span 4 GiB, past the 32-bit buffer range"),
+    (dict(q=W), "q_raw overlaps the workspace the preparation writes"),
+    (dict(k=W + 4096), "k_raw overlaps the workspace"),
+    (dict(v=W + 4096), "v overlaps the workspace"),
     (dict(config=1), "plain-attention configuration on the fused call"),
     (dict(kind=7), "table kind"),
     (dict(pairing=1, rot=48), "split-half rot not a multiple of 32"),
@@ -126,6 +130,8 @@ def test_stage_entry_points_reject():
     assert kv_call(v=0) == HIP_ERROR_INVALID_VALUE              # the values are part of the prepared workspace
     assert kv_call(wsb=wsb - 2) == HIP_ERROR_INVALID_VALUE
     assert kv_call(vrs=200) == HIP_ERROR_INVALID_VALUE
+    assert kv_call(k=W + 256) == HIP_ERROR_INVALID_VALUE          # k_raw inside the workspace it writes
+    assert kv_call(v=W + 4096) == HIP_ERROR_INVALID_VALUE         # v inside the workspace
     pr = dict(q=A, ws=W, wsb=wsb, out=A, wq=None, kind=1, qa=A, qb=A, ts=64, pairing=0, rot=128, eps=1e-6, Sq=8, Sk=8,
               H=2, HK=2, p0=0, causal=0, scale=0.088, qrs=256, ors=256, config=0, stream=None)
 

@@ -4,6 +4,8 @@
   cfg2  512 text + 4096 image tokens (64x64 grid), 24 heads x 128      -- every query row checked
   cfg4  512 text + 3 x 4096 image tokens (3-frame edit layout)          -- sampled query rows
   cfg5  512 text + 49 x 44 x 80 video tokens (172,992), one pass        -- sampled query rows
+  qwen21  4096 image queries x 32 heads over an 80-key cached prefix + 4096 keys (the reference's own call shape,
+          dit.zig:252-293)                                              -- sampled query rows
 
 Per-head QK-RMSNorm eps 1e-6 with weights 1.0, RoPE theta 10000 (text rows un-rotated), scale f32(1/sqrt(128)),
 non-causal. The oracle is the CPU fp32 flash-style path (oracle/lro.c, pinned against fp64 and torch SDPA on the
@@ -77,6 +79,34 @@ def test_edit_shape_sampled_rows():
     ref = _oracle_rows(qb, kb, vb, cos, sin, rows)
     mx, mn = assert_close(out[rows], ref, what="cfg4")
     print(f"[cfg4] {len(rows)} rows: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
+
+
+def test_qwen21_reference_shape_sampled_rows():
+    """The reference's own call shape (Qwen-Image 2.1, src/engines/qwen_image/dit.zig:252-293, the shape of its
+    published pattn2 / cuDNN timings): 4,096 image queries x 32 heads over an 80-row cached text prefix (keys already
+    rotated, used as given: n_pre = 80) plus the 4,096 image keys, whose k-table row is j - 80."""
+    n_pre, gh, gw, Hq = 80, 64, 64, 32
+    cos_all, sin_all = rope.grid2d_table(n_pre, gh, gw)
+    cos, sin = np.ascontiguousarray(cos_all[n_pre:]), np.ascontiguousarray(sin_all[n_pre:])
+    Sq = cos.shape[0]
+    Sk = n_pre + Sq
+    print(f"\n[qwen21] Sq={Sq} Sk={Sk} n_pre={n_pre} H={Hq}", flush=True)
+    qb = oracle.synth_bf16(108, 1, (Sq, Hq, 128))
+    kb = oracle.synth_bf16(108, 2, (Sk, Hq, 128))
+    vb = oracle.synth_bf16(108, 3, (Sk, Hq, 128))
+    tc, ts = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    out = from_dev(ops.joint_attention(to_dev(qb), to_dev(kb), to_dev(vb), table_kind=ops.TABLE_COSSIN_F32,
+                                       q_table=(tc, ts), eps=1e-6, n_pre=n_pre))
+    rows = np.unique(np.concatenate([[0, 63, 64, Sq - 1],
+                                     np.random.default_rng(8).choice(Sq, size=380, replace=False)]))
+    qh = oracle.rms_rope(np.ascontiguousarray(qb[rows]), None, table_kind=oracle.TABLE_COSSIN_F32,
+                         ta=np.ascontiguousarray(cos[rows]), tb=np.ascontiguousarray(sin[rows]), eps=1e-6)
+    kh = oracle.rms_rope(np.ascontiguousarray(kb[n_pre:]), None, table_kind=oracle.TABLE_COSSIN_F32, ta=cos, tb=sin,
+                         eps=1e-6)
+    kall = np.concatenate([oracle.bf16_to_f32(kb[:n_pre]), _bf16(kh)])
+    ref = oracle.attention(_bf16(qh), kall, oracle.bf16_to_f32(vb), precise=False)
+    mx, mn = assert_close(out[rows], ref, what="qwen21")
+    print(f"[qwen21] {len(rows)} rows: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
 
 
 @pytest.mark.slow

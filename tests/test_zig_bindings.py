@@ -99,3 +99,34 @@ def test_build_hip_zig_matches_the_in_tree_build():
     for src, extra in build.EXTRA_FLAGS.items():
         line = next(l for l in text.splitlines() if f'.file = "{src}"' in l)
         assert all(f'"{f}"' in line for f in extra), src
+
+
+def test_engine_tree_layout_matches_build_hip_zig(tmp_path):
+    """localrouter_amd.engine_tree lays the sources out as the kernels/hip tree build/hip.zig compiles: every file
+    build/hip.zig names exists there, the Zig module and headers sit where it and the sources expect them, and every
+    source of the tree preprocesses (its includes, ../../include/lr_*.h among them, resolve inside the tree)."""
+    import shutil
+    import subprocess
+
+    from localrouter_amd import engine_tree
+    written = engine_tree.lay_out(tmp_path)
+    assert written
+    text = BUILD.read_text()
+    named = set(re.findall(r'\.file = "([\w.]+)"', text)) | set(re.findall(r'kernels/hip/([\w.]+)"', text))
+    assert "attn_stream.hip" in named and "rope_host.cpp" in named
+    for f in named:
+        assert (tmp_path / "kernels" / "hip" / f).is_file(), f
+    assert (tmp_path / "build" / "hip.zig").read_text() == text
+    assert re.search(r'b\.path\("src/engines/hip/lr_attn\.zig"\)', text)
+    assert (tmp_path / "src" / "engines" / "hip" / "lr_attn.zig").is_file()
+    for h in HEADERS:
+        assert (tmp_path / "include" / h.name).read_bytes() == h.read_bytes()
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        return
+    for f in sorted(named):
+        src = tmp_path / "kernels" / "hip" / f
+        cmd = ([hipcc, "-std=c++17", "-E", "--cuda-host-only"] if f.endswith(".hip") else
+               [shutil.which("g++") or "g++", "-std=c++17", "-E"])
+        r = subprocess.run(cmd + [str(src), "-o", "/dev/null"], capture_output=True, text=True)
+        assert r.returncode == 0, f"{f}: {r.stderr[-2000:]}"
