@@ -1,5 +1,5 @@
 // Persistent streaming joint attention for gfx950: bf16 in, fp32 MFMA accumulation and softmax, bf16 out, over keys
-// and values prepared as tile images (tile_image.h, written by kv_image.hip).
+// prepared as tile images (tile_image.h, written by kv_image.hip) and values read as they are, as bf16 rows.
 //
 // Semantics: the reference's kernels/cuda/qwen_image/attention.cu:253-444 (pattn2_kernel) as launched by
 // src/engines/qwen_image/ops_launch.zig:163-172: O_i = softmax_j(scale <q_i, k_j>) v_j over keys j < nkeys (and
@@ -16,9 +16,14 @@
 //    continuous stream through two 4-stage LDS rings (64 KB each). The loads of the next block's first tiles are in
 //    flight while the current block finishes, and the query prologue of the next block follows the previous block's
 //    epilogue without a kernel boundary.
-//  * Tile images: a tile is stored in HBM as the LDS image of its 16 fragments, so each ring refill is four
+//  * Key tile images: a key tile is stored in HBM as the LDS image of its 16 fragments, so each ring refill is two
 //    contiguous 1 KB direct global->LDS loads per wave (one M0 write, immediate offsets), and each fragment read is one
 //    conflict-free ds_read_b128 at an immediate offset from a per-step base: no per-fragment address arithmetic.
+//  * Values as rows: a value tile (64 rows of 256 bytes at the caller's row stride) is brought into LDS by the same
+//    direct loads, each lane fetching the 16-byte chunk that belongs at its LDS position in the "row-block" layout
+//    (vt_offset below: 4-row x 64-byte blocks of 256 contiguous bytes); the P V operand (V^T, 8 consecutive keys of one
+//    dim per lane) is then two ds_read_b64_tr_b16 (transposed) reads at immediate offsets from one per-lane base, with
+//    no bank conflicts. The preparation launch no longer writes, and this kernel no longer reads, a value image.
 //  * Step (one 64-key tile, 32 MFMA slots per wave): two half-steps of 16 slots; half-step j runs the 8 score MFMAs of
 //    the next 32-key half-tile (S(j+1) = K Q^T, accumulator starting at -m) and the 8 P V MFMAs of the previous one
 //    (O += V^T P(j-1)), while the VALU turns S(j) into P(j): one word (two keys of one query) per two slots, exp2 in
@@ -94,6 +99,65 @@ __device__ __forceinline__ void dma2k(uint64_t gaddr, uint32_t voff, uint32_t ld
     LR_ASM_M0_END
 }
 
+// Value tile rows in LDS: the 16 bytes of dims 8 c .. 8 c + 7 of tile row r (r < 64, c < 16) sit at byte
+// vt_offset(r, c) of the 16 KB slot: 4-row x 4-chunk blocks of 256 contiguous bytes, block (r >> 2, c >> 2) at
+// 256 (4 (r >> 2) + (c >> 2)), row r & 3 of it at + 64 (r & 3), chunk c & 3 at + 16 (c & 3). The address a lane reads
+// for value fragment (16-key step kk, 32-dim block db) is then additive: a per-lane part (VT_LANE) plus
+// 4096 kk + 256 db (+ 1024 for the fragment's second four keys), all immediates.
+__host__ __device__ constexpr int vt_offset(int r, int c) {
+    return 256 * (4 * (r >> 2) + (c >> 2)) + 64 * (r & 3) + 16 * (c & 3);
+}
+// Direct loads of a value tile: wave w's load i (i < 2) fills the slot's bytes 2048 w + 1024 i + 16 l (lane l), i.e.
+// rows 8 w + 4 i + vt_lane_row(l), chunk vt_lane_chunk(l) of the tile.
+__host__ __device__ constexpr int vt_lane_row(int l) { return (l >> 2) & 3; }
+__host__ __device__ constexpr int vt_lane_chunk(int l) { return 4 * (l >> 4) + (l & 3); }
+// The per-lane part of a transposed fragment read: lane l = 16 g + s reads (ds_read_b64_tr_b16: each group of 16
+// lanes takes a 4-row x 16-dim block, lane s pointing at row s >> 2, dims 4 (s & 3) .. +3, and gets dim s of the four
+// rows) keys 8 (l >> 5) + (s >> 2) of dims 16 (g & 1) + 4 (s & 3) .. of the fragment's 32-dim block.
+__host__ __device__ constexpr int vt_lane(int l) {
+    return 2048 * (l >> 5) + 64 * ((l >> 2) & 3) + 32 * ((l >> 4) & 1) + 8 * (l & 3);
+}
+
+// Two 1 KB direct loads of value rows, global -> LDS: lane l's 16 bytes of load 0 come from gaddr + voff0 and land at
+// LDS byte lds + 16 l; those of load 1 from gaddr + voff1 + 1024 to lds + 1024 + 16 l (the instruction offset applies
+// to both addresses; voff1 = voff0 + 4 rows - 1024 >= 0).
+__device__ __forceinline__ void dma2v(uint64_t gaddr, uint32_t voff0, uint32_t voff1, uint32_t lds) {
+    LR_ASM_M0_BEGIN
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %2 offset:0\n\t"
+        "global_load_lds_dwordx4 %1, %2 offset:1024" ::"v"(voff0),
+        "v"(voff1), "s"(gaddr), "s"(lds)
+        : "memory", "m0");
+    LR_ASM_M0_END
+}
+// The same two loads with their own M0 each and no instruction offset (the last, clamped tile of a head, whose
+// offsets may be smaller than 1024).
+__device__ __forceinline__ void dma2v_clamped(uint64_t gaddr, uint32_t voff0, uint32_t voff1, uint32_t lds) {
+    LR_ASM_M0_BEGIN
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %2 offset:0\n\t"
+        "s_add_u32 m0, %3, 0x400\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2 offset:0" ::"v"(voff0),
+        "v"(voff1), "s"(gaddr), "s"(lds)
+        : "memory", "m0", "scc");
+    LR_ASM_M0_END
+}
+
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+// One value fragment (the A operand V^T of O^T += V^T P^T: lane l = 32 hf + n gets keys 8 hf .. 8 hf + 7 of dim n of
+// the 16-key x 32-dim block) from the row-block LDS layout: addr = slot + VT_LANE + 4096 kk + 256 db.
+__device__ __forceinline__ bf16x8 vfrag_at(uint32_t addr) {
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)addr);
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)(addr + 1024));
+    return __builtin_shufflevector(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi), 0, 1, 2, 3, 4, 5, 6,
+                                   7);
+}
+
 template <bool B>
 struct BoolTag {
     static constexpr bool value = B;
@@ -117,7 +181,7 @@ __device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, 
     const int T = (a.nkeys + IMG_TILE_KEYS - 1) / IMG_TILE_KEYS;
     const uint64_t head_off = (uint64_t)hk * T * IMG_TILE_BYTES + (uint64_t)lane * 16;
     const uint8_t* kh = reinterpret_cast<const uint8_t*>(a.k) + head_off;
-    const uint8_t* vh = reinterpret_cast<const uint8_t*>(a.v) + head_off;
+    const uint16_t* vh = a.v + (int64_t)hk * D + n;   // dim n of this lane's 32-dim blocks
     bf16x8 qf[8];
     const uint16_t* src = a.q + (int64_t)min(qrow, a.W - 1) * a.q_rs + head * D + 8 * hf;
 #pragma unroll
@@ -150,7 +214,20 @@ __device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, 
     float ls = 0.0f;
     for (int j = 0; j < 2 * tiles; ++j) {
         const f32x16 sr = scores(j, nm);
-        const uint8_t* vt = vh + (uint64_t)(j >> 1) * IMG_TILE_BYTES + (j & 1) * 8 * IMG_FRAG_BYTES;
+        // value fragment x of the half-tile (16-key step x >> 2, 32-dim block x & 3): keys 32 j + 16 (x >> 2) +
+        // 8 hf .. +7 of dim 32 (x & 3) + n, eight 2-byte loads (rows past nkeys read the last row: their P is 0)
+        auto vfrag = [&](int x) {
+            uint16_t e[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int key = min(32 * j + 16 * (x >> 2) + 8 * hf + i, a.nkeys - 1);
+                e[i] = vh[(int64_t)key * a.v_rs + 32 * (x & 3)];
+            }
+            u32x4 w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = (uint32_t)e[2 * i] | ((uint32_t)e[2 * i + 1] << 16);
+            return __builtin_bit_cast(bf16x8, w);
+        };
         u32x4 pr[2];
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
@@ -161,9 +238,8 @@ __device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, 
         }
 #pragma unroll
         for (int x = 0; x < 8; ++x)
-            o[x & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                *reinterpret_cast<const bf16x8*>(vt + x * IMG_FRAG_BYTES), __builtin_bit_cast(bf16x8, pr[x >> 2]),
-                o[x & 3], 0, 0, 0);
+            o[x & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfrag(x), __builtin_bit_cast(bf16x8, pr[x >> 2]),
+                                                            o[x & 3], 0, 0, 0);
     }
     const float inv = 1.0f / wave_pair_sum(ls);
     if (qrow < a.W) {
@@ -279,41 +355,60 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
         return r;
     };
 
-    // ---- the tile stream: cursors of the next key / value tile to load (this wave's WQ bytes of it)
+    // ---- the tile stream: cursors of the next key / value tile to load. Keys: this wave's WQ bytes of the tile image;
+    // values: row 0 of the tile in the kv head's rows (each lane adds its own row and chunk offset).
     struct Cursor {
         int it, t, t1;
         uint64_t addr;
     };
-    const uint64_t kimg = (uint64_t)(uintptr_t)a.k, vimg = (uint64_t)(uintptr_t)a.v;
-    auto cur_start = [&](uint64_t img) __attribute__((always_inline)) {
+    const uint64_t kimg = (uint64_t)(uintptr_t)a.k, vrows = (uint64_t)(uintptr_t)a.v;
+    const uint32_t rowb = (uint32_t)a.v_rs * 2u;   // bytes per value row (< 2^25: launch_stream checks)
+    const uint64_t vtile = (uint64_t)IMG_TILE_KEYS * rowb;
+    auto k_at = [&](const Item& r) __attribute__((always_inline)) {
+        return kimg + (uint64_t)r.hk * head_bytes + (uint64_t)r.t0 * IMG_TILE_BYTES + (uint64_t)wave * WQ;
+    };
+    auto v_at = [&](const Item& r) __attribute__((always_inline)) {
+        return vrows + (uint64_t)r.hk * (D * 2) + (uint64_t)r.t0 * vtile;
+    };
+    auto cur_start = [&](auto at) __attribute__((always_inline)) {
         const Item r = item_of(0);
-        return Cursor{0, r.t0, r.t1,
-                      img + (uint64_t)r.hk * head_bytes + (uint64_t)r.t0 * IMG_TILE_BYTES + (uint64_t)wave * WQ};
+        return Cursor{0, r.t0, r.t1, at(r)};
     };
     // past the last tile of the last item the cursor stays put: its loads refill a free ring slot with a tile that is
     // never read
-    auto cur_next = [&](Cursor& c, uint64_t img) __attribute__((always_inline)) {
+    auto cur_next = [&](Cursor& c, uint64_t step, auto at) __attribute__((always_inline)) {
         if (c.t + 1 < c.t1) {
             ++c.t;
-            c.addr += IMG_TILE_BYTES;
+            c.addr += step;
         } else if (c.it + 1 < nitems) {
             ++c.it;
             const Item r = item_of(c.it);
             c.t = r.t0;
             c.t1 = r.t1;
-            c.addr = img + (uint64_t)r.hk * head_bytes + (uint64_t)r.t0 * IMG_TILE_BYTES + (uint64_t)wave * WQ;
+            c.addr = at(r);
         }
     };
     const uint32_t voff = (uint32_t)lane * 16u;
     const uint32_t kr0 = lds_addr(Kr), vr0 = lds_addr(Vr);
+    // the value rows this lane loads: rows vrow and vrow + 4 of a tile, chunk vt_lane_chunk(lane)
+    const uint32_t vrow = (uint32_t)(8 * wave + vt_lane_row(lane));
+    const uint32_t vchunk = (uint32_t)(16 * vt_lane_chunk(lane));
+    const uint32_t vo0 = vrow * rowb + vchunk, vo1 = vo0 + 4 * rowb - 1024;
+    const int vfull = a.nkeys >> 6;   // value tiles t < vfull hold 64 rows; tile vfull (when nkeys % 64) fewer
     // ring slot x: byte offset x * 16 KB; this wave's loads fill its WQ bytes of the slot
     auto load_k = [&](Cursor& c, int pos) __attribute__((always_inline)) {
         dma2k(c.addr, voff, kr0 + (uint32_t)((pos & (RING - 1)) * IMG_TILE_BYTES) + (uint32_t)wave * WQ);
-        cur_next(c, kimg);
+        cur_next(c, (uint64_t)IMG_TILE_BYTES, k_at);
     };
     auto load_v = [&](Cursor& c, int pos) __attribute__((always_inline)) {
-        dma2k(c.addr, voff, vr0 + (uint32_t)((pos & (RING - 1)) * IMG_TILE_BYTES) + (uint32_t)wave * WQ);
-        cur_next(c, vimg);
+        const uint32_t lds = vr0 + (uint32_t)((pos & (RING - 1)) * IMG_TILE_BYTES) + (uint32_t)wave * WQ;
+        if (c.t < vfull) {
+            dma2v(c.addr, vo0, vo1, lds);
+        } else {   // the head's last, partial tile: rows past nkeys read the last row (finite; their P is 0)
+            const uint32_t lim = (uint32_t)(a.nkeys - 1 - IMG_TILE_KEYS * c.t);
+            dma2v_clamped(c.addr, min(vrow, lim) * rowb + vchunk, min(vrow + 4, lim) * rowb + vchunk, lds);
+        }
+        cur_next(c, vtile, v_at);
     };
 
     // ---- registers
@@ -326,6 +421,9 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     float ls = 0.0f;   // this lane's partial row sum (its 8 keys of every 16-key step)
     bf16x8 fr[FR];     // fragment ring
     const uint32_t lane16 = (uint32_t)lane * 16u;
+    const uint32_t vlane = (uint32_t)vt_lane(lane);   // per-lane part of every value fragment read
+    // the immediate part of value fragment x (16-key step x >> 2, 32-dim block x & 3) of a tile
+    auto vfrag_off = [](int x) __attribute__((always_inline)) { return 4096 * (x >> 2) + 256 * (x & 3); };
 
     // mask the scores sb of half-tile j (keys 32 j ..) against nkeys and, causal, the query's position
     auto mask_half = [&](f32x16& sb, int j, int wrow0) __attribute__((always_inline)) {
@@ -423,7 +521,7 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
 
     // ---- stream start: the first item's queries, K(0..2), V(0..1); the queries, K(0) and K(1) resident before
     // step 0
-    Cursor kc = cur_start(kimg), vc = cur_start(vimg);
+    Cursor kc = cur_start(k_at), vc = cur_start(v_at);
     for (int x = lane; x < REDO_WORDS; x += 64) redo_bits[wave][x] = 0u;
     load_q(cur);
     load_k(kc, 0);
@@ -616,15 +714,15 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     auto finish_item = [&](const Item& r, int it, uint32_t vslot) __attribute__((always_inline)) {
         const int wrow0 = r.row0 + wave * 32;
         if (2 * r.t1 - 1 >= mask_from(wrow0)) mask_half(s[1], 2 * r.t1 - 1, wrow0);
-        uint32_t vb0 = vslot + lane16;
+        uint32_t vb0 = vslot + vlane;
         asm volatile("" : "+v"(vb0));
         bf16x8 vf[4];
 #pragma unroll
-        for (int x = 0; x < 3; ++x) vf[x] = frag_at(vb0 + (uint32_t)(x * IMG_FRAG_BYTES));
+        for (int x = 0; x < 3; ++x) vf[x] = vfrag_at(vb0 + (uint32_t)vfrag_off(x));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
-            if (x + 3 < 16) vf[(x + 3) & 3] = frag_at(vb0 + (uint32_t)((x + 3) * IMG_FRAG_BYTES));
+            if (x + 3 < 16) vf[(x + 3) & 3] = vfrag_at(vb0 + (uint32_t)vfrag_off(x + 3));
             pv(o[x & 3], vf[x & 3], (x < 8 ? p[0] : p[1])[(x >> 2) & 1]);
             if (x < 8) {
                 stage_e(s[1], x);
@@ -644,18 +742,18 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
         const int jm = mask_from(wrow0);
         // per-step fragment bases (opaque to the compiler, so that every fragment offset below stays an immediate)
         uint32_t kb = kr0 + (uint32_t)((g & (RING - 1)) * IMG_TILE_BYTES) + lane16;
-        uint32_t vb = vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES) + lane16;
+        uint32_t vb = vr0 + (uint32_t)(((g - 1) & (RING - 1)) * IMG_TILE_BYTES) + vlane;
         uint32_t kn = kr0 + (uint32_t)(((g + 1) & (RING - 1)) * IMG_TILE_BYTES) + lane16;
         asm volatile("" : "+v"(kb), "+v"(vb), "+v"(kn));
         auto rd_b = [&](int f) __attribute__((always_inline)) {
-            const uint32_t ad = f < 8 ? kb + f * IMG_FRAG_BYTES
-                                      : f < 16 ? vb + (f - 8) * IMG_FRAG_BYTES : kb + (f - 8) * IMG_FRAG_BYTES;
-            fr[f % FR] = frag_at(ad);
+            if (f < 8) fr[f % FR] = frag_at(kb + f * IMG_FRAG_BYTES);
+            else if (f < 16) fr[f % FR] = vfrag_at(vb + vfrag_off(f - 8));
+            else fr[f % FR] = frag_at(kb + (f - 8) * IMG_FRAG_BYTES);
         };
         auto rd_a = [&](int f) __attribute__((always_inline)) {
-            const uint32_t ad = f < 8 ? kb + (8 + f) * IMG_FRAG_BYTES
-                                      : f < 16 ? vb + f * IMG_FRAG_BYTES : kn + (f - 16) * IMG_FRAG_BYTES;
-            fr[f % FR] = frag_at(ad);
+            if (f < 8) fr[f % FR] = frag_at(kb + (8 + f) * IMG_FRAG_BYTES);
+            else if (f < 16) fr[f % FR] = vfrag_at(vb + vfrag_off(f));
+            else fr[f % FR] = frag_at(kn + (f - 16) * IMG_FRAG_BYTES);
         };
         // B half: j = 2t - 1
         if (2 * t - 1 >= jm) mask_half(s[1], 2 * t - 1, wrow0);
@@ -741,6 +839,8 @@ bool stream_split_params(int W, int H, int nkeys, int causal, int nwg, int* tail
 
 hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream) {
     if (a.W < 1 || a.H < 1 || nwg < 1 || nwg > STREAM_MAX_WG) return hipErrorInvalidValue;
+    // value rows: a lane's 32-bit load offset reaches 63 rows into a tile (< 2^31 bytes)
+    if (a.v_rs < D || a.v_rs > STREAM_MAX_V_RS || a.v_rs % 8) return hipErrorInvalidValue;
     // at most MAX_WG_BLOCKS whole blocks per workgroup (its recomputation bits): larger calls run as several launches
     // over consecutive query-row ranges (queries, outputs and, causal, the diagonal offset p0 shifted)
     const int64_t rows_per = (int64_t)SBM * std::max<int64_t>(1, (int64_t)MAX_WG_BLOCKS * nwg / a.H);

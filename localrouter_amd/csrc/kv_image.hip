@@ -1,13 +1,15 @@
-// Keys and values of the joint attention into the tile-image layout (tile_image.h): RMSNorm + RoPE of every key row
-// j >= n_pre (table row j - n_pre; rows j < n_pre are an already normalised and rotated prefix and are copied), and V
-// transposed into V^T fragments. The math per key row is the rms_rope kernel's (rms_rope.hip): the reference's
+// Keys of the joint attention into the tile-image layout (tile_image.h): RMSNorm + RoPE of every key row j >= n_pre
+// (table row j - n_pre; rows j < n_pre are an already normalised and rotated prefix and are copied). The values stay
+// rows: the attention kernel reads the caller's value rows; the stage calls (copy_v) copy them into the workspace so
+// that it holds everything a later call needs. The math per key row is the rms_rope kernel's (rms_rope.hip): the reference's
 // kernels/cuda/minimax/kitchen/rms_rope.cu:37-230 / the Qwen-Image form of src/engines/qwen_image/triton_k.zig:44-53
 // (fp32 weight, cos/sin fp32 tables), as wired by src/engines/qwen_image/dit.zig:252-263 (k via rms_rope into the
 // key buffer after the prefix, v copied).
 //
-// One workgroup per (kv head, 64-key tile): it loads the tile's 64 key rows and 64 value rows (256 contiguous bytes
-// each), normalises and rotates the keys in registers, writes both images into LDS (a staging copy, see stg), then
-// stores the 32 KB with fully coalesced 16-byte stores. HBM-bound: 32 KB in and 32 KB out per tile.
+// One workgroup per (kv head, 64-key tile): it loads the tile's 64 key rows (256 contiguous bytes each), normalises
+// and rotates them in registers, writes the image into LDS (a staging copy, see stg), then stores the 16 KB with fully
+// coalesced 16-byte stores (copy_v: the 64 value rows too, 16 bytes a thread at a time). HBM-bound: 16 KB in and 16 KB
+// out per tile (32 KB each with copy_v).
 #include "lr_common.h"
 #include "lr_kernels.h"
 #include "tile_image.h"
@@ -23,13 +25,12 @@ constexpr int KROWS = 4;   // key rows per thread (rows g, g + 16, g + 32, g + 4
 // Where the 16 bytes at image offset o sit in the LDS staging copy: o with its 16-byte position inside the 128-byte
 // line XORed by bits of the line index (a bijection on 16-byte units that keeps every line in place). The eight
 // lanes of a write group put one key row's chunks 512-1024 bytes apart, all at the same position of their lines
-// (eight lanes on four banks each: an 8-way conflict), and an 8-dim block of values the same way; the XOR spreads
-// both over the line (conflict-free for the keys, 2-way for the values), while the copy-out, eight consecutive
-// 16-byte units of one line per group, stays conflict-free.
+// (eight lanes on four banks each: an 8-way conflict); the XOR spreads them over the line (conflict-free), while the
+// copy-out, eight consecutive 16-byte units of one line per group, stays conflict-free.
 __device__ __forceinline__ int stg(int o) { return o ^ ((((o >> 7) ^ (o >> 10)) & 7) << 4); }
 
-// One 256-thread block: tile tile_id (kv head * tiles + tile) of the keys and of the values, through img (32 KB of
-// LDS: the key image, then the value image).
+// One 256-thread block: tile tile_id (kv head * tiles + tile) of the keys (and, copy_v, of the values), through img
+// (16 KB of LDS: the key image).
 template <int KIND, int PAIRING>
 __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile_id, uint8_t* img) {
     const int tid = threadIdx.x, c = tid & 15, g = tid >> 4;
@@ -45,13 +46,13 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
         const int key = min(key0 + g + 16 * i, a.Sk - 1);
         xin[i] = *reinterpret_cast<const u32x4*>(a.k + (int64_t)key * a.k_rs + (int64_t)hk * D + 8 * c);
     }
-    u32x4 vin[8];
-    const int vkg = tid >> 4, vdg = tid & 15;           // threads 0-127: keys 8 vkg .. +7, dims 8 vdg .. +7
-    if (tid < 128) {
+    u32x4 vin[KROWS];                                   // copy_v: value rows g + 16 i, dims 8 c .. +7
+    if (a.copy_v) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int key = min(key0 + 8 * vkg + i, a.Sk - 1);
-            vin[i] = *reinterpret_cast<const u32x4*>(a.v + (int64_t)key * a.v_rs + (int64_t)hk * D + 8 * vdg);
+        for (int i = 0; i < KROWS; ++i) {
+            const int key = key0 + g + 16 * i;
+            vin[i] = key < a.Sk ? *reinterpret_cast<const u32x4*>(a.v + (int64_t)key * a.v_rs + (int64_t)hk * D + 8 * c)
+                                : u32x4{0, 0, 0, 0};
         }
     }
     float wv[8];
@@ -139,46 +140,35 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
         *reinterpret_cast<u32x4*>(img + stg(img_k_offset(r, c))) = o;
     }
 
-    // ---- values: an 8-key x 8-dim block transposed in registers, 8 dims of 16 bytes (8 keys each)
-    if (tid < 128) {
+    // ---- values (copy_v): the tile's rows into the workspace's value rows [tiles * 64][HK][128], zero past Sk
+    if (a.copy_v) {
+        uint16_t* vdst = static_cast<uint16_t*>(a.img_v) + (int64_t)hk * D + 8 * c;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (key0 + 8 * vkg + i >= a.Sk) vin[i] = u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            u32x4 y;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const uint32_t lo = vin[2 * w][e >> 1], hi = vin[2 * w + 1][e >> 1];
-                y[w] = (e & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-            }
-            *reinterpret_cast<u32x4*>(img + IMG_TILE_BYTES + stg(img_v_offset(vkg, 8 * vdg + e))) = y;
-        }
+        for (int i = 0; i < KROWS; ++i)
+            *reinterpret_cast<u32x4*>(vdst + ((int64_t)(key0 + g + 16 * i) * a.HK) * D) = vin[i];
     }
     __syncthreads();
 
-    // ---- both images out, 16 contiguous bytes per thread per pass
+    // ---- the key image out, 16 contiguous bytes per thread per pass
     uint8_t* kdst = reinterpret_cast<uint8_t*>(a.img_k) + tile_id * IMG_TILE_BYTES;
-    uint8_t* vdst = reinterpret_cast<uint8_t*>(a.img_v) + tile_id * IMG_TILE_BYTES;
 #pragma unroll
     for (int p = 0; p < IMG_TILE_BYTES / 4096; ++p) {
         const int off = p * 4096 + 16 * tid;
         *reinterpret_cast<u32x4*>(kdst + off) = *reinterpret_cast<const u32x4*>(img + stg(off));
-        *reinterpret_cast<u32x4*>(vdst + off) = *reinterpret_cast<const u32x4*>(img + IMG_TILE_BYTES + stg(off));
     }
 }
 
 template <int KIND, int PAIRING>
 __global__ __launch_bounds__(256) void kv_image_kernel(KvImageArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t img[2 * IMG_TILE_BYTES];   // keys, then values
+    __shared__ __attribute__((aligned(16))) uint8_t img[IMG_TILE_BYTES];   // the key image
     kv_tile_block<KIND, PAIRING>(a, blockIdx.x, img);
 }
 
-// The joint attention's whole preparation in one launch: blocks [0, nkv) are key / value tiles, the rest query rows
+// The joint attention's whole preparation in one launch: blocks [0, nkv) are key tiles (and value rows), the rest query rows
 // (rope_rows_block over q: normalised and rotated into the prepared-query rows).
 template <int KIND, int PAIRING>
 __global__ __launch_bounds__(256) void joint_prep_kernel(KvImageArgs kv, RopeArgs q, int64_t nkv) {
-    __shared__ __attribute__((aligned(16))) uint8_t img[2 * IMG_TILE_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t img[IMG_TILE_BYTES];
     if ((int64_t)blockIdx.x < nkv) kv_tile_block<KIND, PAIRING>(kv, blockIdx.x, img);
     else rope_rows_block<KIND, PAIRING>(q, (int64_t)blockIdx.x - nkv);
 }

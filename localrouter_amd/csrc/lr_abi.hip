@@ -111,9 +111,10 @@ bool table_ok(int kind, const void* ta, const void* tb, int64_t stride, int rot,
     return aligned(ta, 16) && stride % 4 == 0 && stride >= 4 * pairs;  // LR_TABLE_MAT2_F32
 }
 
-// Workspace of the fused op and of its two stages: the tile images of the keys, then those of the values
-// (tile_image.h), 16 KB per 64-key tile and kv head each, then the streaming kernel's split area (partials of cut
-// query blocks, then their arrival counters).
+// Workspace of the fused op and of its two stages: the tile images of the keys (tile_image.h), 16 KB per 64-key tile
+// and kv head; then the value area, the same size: value rows [tiles * 64][HK][128] bf16, written by the stage calls
+// (the fused call reads the caller's value rows and leaves it unused); then the streaming kernel's split area
+// (partials of cut query blocks, then their arrival counters).
 static_assert(lr::STREAM_PART_BYTES + lr::STREAM_CNT_BYTES == (int64_t)LR_JOINT_SPLIT_BYTES, "split area size");
 size_t ws_bytes_needed(int Sk, int HK) { return 2 * (size_t)lr::img_bytes(Sk, HK) + LR_JOINT_SPLIT_BYTES; }
 inline char* split_area(void* ws, int Sk, int HK) { return static_cast<char*>(ws) + 2 * lr::img_bytes(Sk, HK); }
@@ -151,6 +152,7 @@ bool kv_stage_ok(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, c
     if (Sk < 1 || HK < 1 || Sk > INT_MAX - 512 || n_pre < 0 || n_pre > Sk || !(eps >= 0.0f) || !isfinite(eps))
         return false;
     if (!rows_ok(k_raw, k_rs, HK) || !rows_ok(v, v_rs, HK) || (wk && !aligned(wk, 16))) return false;
+    if (v_rs > lr::STREAM_MAX_V_RS) return false;   // the attention kernel's 32-bit value-row offsets
     if (Sk > n_pre && !table_ok(table_kind, kta, ktb, tab_stride, rot, pairing, 32)) return false;
     if (!ws || !aligned(ws, 256) || ws_bytes < ws_bytes_needed(Sk, HK)) return false;
     // the launch writes the workspace while it reads the keys and values
@@ -167,7 +169,7 @@ inline int tab_vec(int kind, const void* ta, const void* tb, int64_t stride) {
 
 lr::KvImageArgs kv_args(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
                         const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk,
-                        int HK, int n_pre, void* ws) {
+                        int HK, int n_pre, void* ws, int copy_v) {
     lr::KvImageArgs r{};
     r.k = static_cast<const uint16_t*>(k_raw);
     r.v = static_cast<const uint16_t*>(v);
@@ -179,6 +181,7 @@ lr::KvImageArgs kv_args(const void* k_raw, int64_t k_rs, const void* v, int64_t 
     r.tiles = lr::img_tiles(Sk);
     r.img_k = ws;
     r.img_v = static_cast<char*>(ws) + lr::img_bytes(Sk, HK);
+    r.copy_v = copy_v;
     r.cnt = reinterpret_cast<int*>(split_area(ws, Sk, HK) + lr::STREAM_PART_BYTES);
     r.ncnt = lr::STREAM_MAX_WG;
     r.tab_vec = tab_vec(r.table_kind, kta, ktb, tab_stride);
@@ -188,7 +191,7 @@ int kv_launch(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, cons
               const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps, int Sk, int HK,
               int n_pre, void* ws, hipStream_t stream) {
     return (int)lr::launch_kv_image(
-        kv_args(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws),
+        kv_args(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps, Sk, HK, n_pre, ws, 1),
         stream);
 }
 
@@ -228,15 +231,17 @@ int q_launch(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, const 
 }
 
 // Both preparations of the fused call (arguments checked) in one launch; when every key is a prefix key (no key table
-// is read) the keys go through their own launch.
+// is read) the keys go through their own launch. copy_v: the value rows are copied into the workspace too (the stage
+// call lr_joint_prepare, whose workspace must serve lr_joint_attention_images alone; the fused call reads them where
+// they are).
 int prep_launch(const void* q_raw, int64_t q_rs, void* q_prep, int64_t p_rs, const float* wq, const void* k_raw,
                 int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind, const void* qta,
                 const void* qtb, const void* kta, const void* ktb, int64_t tab_stride, int pairing, int rot, float eps,
-                int Sq, int Sk, int H, int HK, int n_pre, void* ws, hipStream_t stream) {
+                int Sq, int Sk, int H, int HK, int n_pre, void* ws, int copy_v, hipStream_t stream) {
     const lr::RopeArgs q = q_args(q_raw, q_rs, q_prep, p_rs, wq, table_kind, qta, qtb, tab_stride, pairing, rot, eps,
                                   Sq, H);
     const lr::KvImageArgs kv = kv_args(k_raw, k_rs, v, v_rs, wk, table_kind, kta, ktb, tab_stride, pairing, rot, eps,
-                                       Sk, HK, n_pre, ws);
+                                       Sk, HK, n_pre, ws, copy_v);
     if (kv.table_kind != q.table_kind) {
         const hipError_t e = lr::launch_kv_image(kv, stream);
         if (e != hipSuccess) return (int)e;
@@ -264,18 +269,26 @@ bool images_stage_ok(const void* q_prep, int64_t p_rs, const void* ws, size_t ws
 
 // The attention stage (arguments checked): the persistent streaming kernel, one workgroup per CU (at most
 // STREAM_MAX_WG), its last partial round of query blocks cut over all of them (partials and counters in the
-// workspace's split area).
+// workspace's split area). v / v_rs: the value rows it reads (the caller's, or null for the workspace's value area).
 int images_launch(const void* q_prep, int64_t p_rs, const void* ws, void* out, int64_t o_rs, int Sq, int Sk, int H,
-                  int HK, int p0, int causal, float scale, hipStream_t stream) {
+                  int HK, int p0, int causal, float scale, hipStream_t stream, const void* v = nullptr,
+                  int64_t v_rs = 0) {
     const int cus = std::min(device_cus(), lr::STREAM_MAX_WG);
     if (cus < 1) return (int)hipErrorInvalidDevice;
     lr::AttnArgs a{};
     a.q = static_cast<const uint16_t*>(q_prep);
     a.k = static_cast<const uint16_t*>(ws);
-    a.v = reinterpret_cast<const uint16_t*>(static_cast<const char*>(ws) + lr::img_bytes(Sk, HK));
+    if (v) {
+        a.v = static_cast<const uint16_t*>(v);
+        a.v_rs = v_rs;
+    } else {
+        a.v = reinterpret_cast<const uint16_t*>(static_cast<const char*>(ws) + lr::img_bytes(Sk, HK));
+        a.v_rs = (int64_t)HK * lr::D;
+    }
     a.out = static_cast<uint16_t*>(out);
     a.q_rs = p_rs; a.o_rs = o_rs;
-    a.k_hs = a.v_hs = lr::img_tiles(Sk) * (lr::IMG_TILE_BYTES / 2);
+    a.k_hs = lr::img_tiles(Sk) * (lr::IMG_TILE_BYTES / 2);
+    a.v_hs = lr::D;
     a.W = Sq; a.H = H; a.HK = HK; a.G = H / HK; a.nkeys = Sk; a.p0 = p0; a.causal = causal;
     a.c = scale * 1.4426950408889634f;
     char* split = split_area(const_cast<void*>(ws), Sk, HK);
@@ -319,9 +332,9 @@ int fused_impl(const void* q_raw, const void* k_raw, const void* v, void* out, c
     if (overlap(so, rows_span(k_raw, Sk, k_rs, HK)) || overlap(so, rows_span(v, Sk, v_rs, HK))) return ERR_ARGS;
     if (overlap(rows_span(q_raw, Sq, q_rs, H), ws_span(ws, Sk, HK))) return ERR_ARGS;
     const int e = prep_launch(q_raw, q_rs, out, o_rs, wq, k_raw, k_rs, v, v_rs, wk, table_kind, qta, qtb, kta, ktb,
-                              tab_stride, pairing, rot, eps, Sq, Sk, H, HK, n_pre, ws, stream);
+                              tab_stride, pairing, rot, eps, Sq, Sk, H, HK, n_pre, ws, 0, stream);
     if (e != 0) return e;
-    return images_launch(out, o_rs, ws, out, o_rs, Sq, Sk, H, HK, p0, causal, scale, stream);
+    return images_launch(out, o_rs, ws, out, o_rs, Sq, Sk, H, HK, p0, causal, scale, stream, v, v_rs);
 }
 
 int rope_impl(const void* src, int64_t src_rs, int64_t src_off, void* dst, int64_t dst_rs, int64_t n, int b,
@@ -622,7 +635,7 @@ int lr_joint_prepare(const void* q_raw, int64_t q_row_stride, void* q_prep, int6
         return ERR_ARGS;
     return prep_launch(q_raw, q_row_stride, q_prep, q_prep_row_stride, q_norm_w, k_raw, k_row_stride, v, v_row_stride,
                        k_norm_w, table_kind, q_table_a, q_table_b, k_table_a, k_table_b, table_row_stride, pairing,
-                       rot_dim, eps, Sq, Sk, H, HK, n_pre, workspace, reinterpret_cast<hipStream_t>(stream));
+                       rot_dim, eps, Sq, Sk, H, HK, n_pre, workspace, 1, reinterpret_cast<hipStream_t>(stream));
 }
 
 int lr_joint_attention_images(const void* q_prep, int64_t q_prep_row_stride, const void* workspace,

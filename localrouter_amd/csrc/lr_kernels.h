@@ -10,7 +10,7 @@ namespace lr {
 struct AttnArgs {
     const uint16_t* q;   // bf16 [W][...] rows, head h at h*128 (+ row stride q_rs)
     const uint16_t* k;   // bf16 keys: key j of kv head g at k + g*k_hs + j*k_rs
-    const uint16_t* v;   // bf16 values, same addressing with v_hs / v_rs
+    const uint16_t* v;   // bf16 values, same addressing with v_hs / v_rs (the streaming kernel: rows, v_hs = 128)
     uint16_t* out;       // bf16 [W][...] rows, head h at h*128 (+ row stride o_rs)
     int64_t q_rs, k_rs, v_rs, o_rs;  // row strides (elements)
     int64_t k_hs, v_hs;              // kv-head strides (elements)
@@ -68,8 +68,8 @@ hipError_t launch_compact_keys(const void* k, const void* v, int64_t kv_rs, cons
 hipError_t launch_split_combine(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_rms_rope(const RopeArgs& a, hipStream_t stream);
 
-// Keys (RMSNorm + RoPE, rows j < n_pre copied) and values of a joint-attention call into the tile-image layout of
-// tile_image.h (kv_image.hip).
+// Keys (RMSNorm + RoPE, rows j < n_pre copied) of a joint-attention call into the tile-image layout of tile_image.h,
+// and (copy_v) its values into the workspace as rows (kv_image.hip).
 struct KvImageArgs {
     const uint16_t* k;    // bf16 key rows, key j of kv head g at k + j*k_rs + g*128
     const uint16_t* v;    // bf16 value rows, same addressing with v_rs
@@ -83,7 +83,8 @@ struct KvImageArgs {
     int Sk, HK, n_pre;
     int64_t tiles;        // ceil(Sk / 64)
     void* img_k;          // [HK][tiles] 16 KB key tiles
-    void* img_v;          // [HK][tiles] 16 KB value tiles
+    void* img_v;          // value rows [tiles * 64][HK][128] (copy_v), else unused
+    int copy_v;           // 1: copy the value rows into img_v (rows past Sk zero), for the stage calls
     int* cnt;             // the streaming kernel's arrival counters, zeroed by this launch (ncnt ints; null: none)
     int ncnt;
     int tab_vec;          // as RopeArgs::tab_vec
@@ -93,13 +94,15 @@ hipError_t launch_kv_image(const KvImageArgs& a, hipStream_t stream);
 // both use the same table kind and pairing.
 hipError_t launch_joint_prep(const KvImageArgs& kv, const RopeArgs& q, hipStream_t stream);
 
-// The persistent streaming attention kernel (attn_stream.hip) over tile images: a.k / a.v = the key / value images;
-// a.q = prepared queries (normalised, rotated and multiplied by scale * log2 e, bf16 rows with stride a.q_rs; they may
-// be the rows of a.out, which each block reads before it overwrites them). nwg = workgroups (at most one per CU).
+// The persistent streaming attention kernel (attn_stream.hip): a.k = the key tile images; a.v = the value rows (bf16,
+// key j of kv head g at a.v + j * a.v_rs + g * 128, a.v_rs <= STREAM_MAX_V_RS; rows j < a.nkeys are read); a.q =
+// prepared queries (normalised and rotated, bf16 rows with stride a.q_rs; they may be the rows of a.out, which each
+// block reads before it overwrites them). nwg = workgroups (at most one per CU).
 // Non-causal and causal (p0) calls, any W, H, HK, nkeys.
 // a.part / a.cnt: the partial area and arrival counters of the workspace (null: whole blocks only); nwg <=
 // STREAM_MAX_WG.
 hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream);
+constexpr int64_t STREAM_MAX_V_RS = (int64_t)1 << 24;                   // value row stride (elements) at most
 constexpr int STREAM_MAX_WG = 256;                                      // workgroups of one streaming launch at most
 constexpr int64_t STREAM_SLOT_BYTES = 8 * (64 * 64 * 4 + 64 * 8);        // one piece's partial: 8 waves' O, m and l
 constexpr int64_t STREAM_PART_BYTES = 2 * STREAM_MAX_WG * STREAM_SLOT_BYTES;

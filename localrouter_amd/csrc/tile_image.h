@@ -1,5 +1,5 @@
-// The "tile image" layout of prepared keys and values: every 64-key tile of a kv head is stored in HBM exactly as the
-// attention kernel keeps it in LDS, as 16 operand fragments of 1 KB. A fragment is the operand of one
+// The "tile image" layout of prepared keys: every 64-key tile of a kv head is stored in HBM exactly as the attention
+// kernel keeps it in LDS, as 16 operand fragments of 1 KB. A fragment is the operand of one
 // v_mfma_f32_32x32x16_bf16 for all 64 lanes of a wave, lane l's 16 bytes at byte 16 l, so that
 //   - one contiguous 1 KB global -> LDS load (16 bytes per lane) moves one fragment, and
 //   - one ds_read_b128 at (fragment base + 16 l), the base an immediate offset, reads it back without bank conflicts.
@@ -10,10 +10,10 @@
 // 4 (g & 1) + r: registers 0-7 are keys 8 hf .. 8 hf + 7 of the block's first 16-key step, registers 8-15 those of its
 // second -- exactly the B operand (P^T, 8 consecutive keys per lane) of the P V product, so P needs no shuffle.
 //
-// Values (A operand of O^T = V^T P^T, rows = dims, k = keys): fragment f = 4 kk + db of a tile (16-key step kk < 4,
-// 32-dim block db < 4), lane l = 32 hf + n holds keys 16 kk + 8 hf .. +7 of dim 32 db + n.
+// The values are not imaged: the attention kernel reads value rows and transposes them with its LDS reads
+// (attn_stream.hip).
 //
-// Keys and values past the last key of a head are zero. Tile t of kv head g starts at byte (g * tiles + t) * 16384.
+// Keys past the last key of a head are zero. Tile t of kv head g starts at byte (g * tiles + t) * 16384.
 #pragma once
 #include <stdint.h>
 
@@ -31,13 +31,8 @@ __host__ __device__ constexpr int img_k_offset(int r, int c) {
     return (8 * (r >> 5) + (c >> 1)) * IMG_FRAG_BYTES + (32 * (c & 1) + img_key_perm(r & 31)) * 16;
 }
 
-// byte offset, within a tile, of the 16 bytes holding keys 8 a .. 8 a + 7 (a < 8) of dim d (d < 128)
-__host__ __device__ constexpr int img_v_offset(int a, int d) {
-    return (4 * (a >> 1) + (d >> 5)) * IMG_FRAG_BYTES + (32 * (a & 1) + (d & 31)) * 16;
-}
-
 inline int64_t img_tiles(int Sk) { return (Sk + IMG_TILE_KEYS - 1) / IMG_TILE_KEYS; }
-// bytes of one tensor (keys or values) for HK kv heads
+// bytes of the key images of HK kv heads (and of the workspace's value area: tiles * 64 rows of HK * 256 bytes)
 inline int64_t img_bytes(int Sk, int HK) { return img_tiles(Sk) * HK * IMG_TILE_BYTES; }
 
 }  // namespace lr

@@ -56,26 +56,21 @@ def bf16_ulps(got_bits: np.ndarray, ref: np.ndarray, floor: float = 2.0 ** -10) 
 
 # ------------------------------------------------------------------------------------------ tile images
 def img_index():
-    """Element indices (uint16 units within a 16 KB tile image) of key r dim d and of value key r dim d: the layout of
-    tile_image.h restated -- key fragments f = 8 (r >> 5) + (d >> 4), lane 32 ((d >> 3) & 1) + perm(r & 31) with perm
-    swapping bits 2 and 3; value fragments f = 4 (r >> 4) + (d >> 5), lane 32 ((r >> 3) & 1) + (d & 31)."""
+    """Element indices (uint16 units within a 16 KB key tile image) of key r dim d: the layout of tile_image.h restated --
+    key fragments f = 8 (r >> 5) + (d >> 4), lane 32 ((d >> 3) & 1) + perm(r & 31) with perm swapping bits 2 and 3."""
     r = np.arange(64)[:, None]
     d = np.arange(128)[None, :]
     m = r & 31
     perm = (m & 0x13) | ((m & 4) << 1) | ((m & 8) >> 1)
-    kidx = ((8 * (r >> 5) + (d >> 4)) * 1024 + (32 * ((d >> 3) & 1) + perm) * 16) // 2 + (d & 7)
-    a = r >> 3
-    vidx = 8192 + ((4 * (a >> 1) + (d >> 5)) * 1024 + (32 * (a & 1) + (d & 31)) * 16) // 2 + (r & 7)
-    return kidx, vidx
+    return ((8 * (r >> 5) + (d >> 4)) * 1024 + (32 * ((d >> 3) & 1) + perm) * 16) // 2 + (d & 7)
 
 
 def decode_images(raw: np.ndarray, Sk: int, HK: int):
-    """Workspace bytes -> keys, values uint16 [HK][ceil(Sk/64)*64][128] (rows past Sk included)."""
+    """Workspace bytes -> keys, values uint16 [HK][ceil(Sk/64)*64][128] (rows past Sk included): the key tile images,
+    then the value area, rows [tiles * 64][HK][128]."""
     nt = (Sk + 63) // 64
     u = raw[: 2 * HK * nt * 16384].view(np.uint16)
     kimg = u[: HK * nt * 8192].reshape(HK, nt, 8192)
-    vimg = u[HK * nt * 8192:].reshape(HK, nt, 8192)
-    kidx, vidx = img_index()
-    keys = kimg[:, :, kidx].reshape(HK, nt * 64, 128)
-    vals = vimg[:, :, vidx - 8192].reshape(HK, nt * 64, 128)
+    keys = kimg[:, :, img_index()].reshape(HK, nt * 64, 128)
+    vals = u[HK * nt * 8192:].reshape(nt * 64, HK, 128).transpose(1, 0, 2)
     return keys, vals

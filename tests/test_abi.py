@@ -279,11 +279,9 @@ def test_split_workspace_sizes_and_rejects():
 
 
 def test_image_index_is_a_permutation():
-    """The tile-image restatement the GPU layout tests decode with covers each of a tile's 8192 bf16 slots once."""
-    kidx, vidx = img_index()
-    assert np.array_equal(np.sort(np.concatenate([kidx.ravel(), vidx.ravel()])), np.arange(16384))
+    """The key tile-image restatement the GPU layout tests decode with covers each of a tile's 8192 bf16 slots once."""
+    kidx = img_index()
+    assert np.array_equal(np.sort(kidx.ravel()), np.arange(8192))
     # (element units: a lane's 16 bytes are 8 elements, a 1 KB fragment 512)
     assert kidx[0, 0] == 0 and kidx[4, 0] == 8 * 8 and kidx[8, 0] == 4 * 8      # rows 4 and 8 swap lanes
     assert kidx[0, 8] == 32 * 8 and kidx[0, 16] == 512 and kidx[32, 0] == 8 * 512
-    assert vidx[0, 0] == 8192 and vidx[1, 0] == 8193 and vidx[0, 1] == 8192 + 8 and vidx[8, 0] == 8192 + 32 * 8
-    assert vidx[16, 0] == 8192 + 4 * 512 and vidx[0, 32] == 8192 + 512

@@ -356,8 +356,9 @@ def test_fused_overflow_in_every_block_of_a_workgroup():
 # ------------------------------------------------------------------------------------------ the two stages
 @pytest.mark.parametrize("Sk,HK,n_pre", [(190, 2, 0), (64, 1, 0), (1, 1, 0), (200, 3, 50)])
 def test_kv_prepare_layout_and_prepared_equals_fused(Sk, HK, n_pre):
-    """lr_joint_kv_prepare writes the normalised keys and the values as tile images (zero past Sk, exact copies of V
-    and of the prefix keys); lr_joint_attention_prepared over that workspace equals the fused call bit for bit."""
+    """lr_joint_kv_prepare writes the normalised keys as tile images and the values as rows into the workspace (zero
+    past Sk, exact copies of V and of the prefix keys); lr_joint_attention_prepared over that workspace equals the
+    fused call (which reads the caller's value rows) bit for bit."""
     print(f"\n[kv-prepare] Sk={Sk} HK={HK} n_pre={n_pre}", flush=True)
     Sq, H = 130, 2 * HK
     q = oracle.synth_bf16(41, 1, (Sq, H, 128))
@@ -370,7 +371,7 @@ def test_kv_prepare_layout_and_prepared_equals_fused(Sk, HK, n_pre):
     ops.joint_kv_prepare(to_dev(k), to_dev(v), ws, k_table=(_dev_table(ka), _dev_table(kb)), n_pre=n_pre)
     torch.cuda.synchronize()
     keys, vals = decode_images(ws.cpu().numpy(), Sk, HK)
-    assert np.array_equal(vals[:, :Sk], v.transpose(1, 0, 2)), "value images"
+    assert np.array_equal(vals[:, :Sk], v.transpose(1, 0, 2)), "value rows"
     assert not vals[:, Sk:].any() and not keys[:, Sk:].any(), "rows past Sk must be zero"
     assert np.array_equal(keys[:, :n_pre], k[:n_pre].transpose(1, 0, 2)), "prefix keys copied"
     if Sk > n_pre:
@@ -419,8 +420,9 @@ def test_three_launches_equal_fused(causal, p0):
     (1, 0, 128, 333, 0),    # every key a prefix key: keys and queries in two launches
 ])
 def test_one_launch_prepare_equals_the_stages(kind, pairing, rot, n_pre, offset):
-    """lr_joint_prepare (queries, keys and values in one launch, the fused call's first launch) writes the same
-    prepared queries and tile images, bit for bit, as lr_joint_q_prepare + lr_joint_kv_prepare."""
+    """lr_joint_prepare (queries, keys and values in one launch: the fused call's first launch, plus the value rows
+    copied into the workspace) writes the same prepared queries, key images and value rows, bit for bit, as
+    lr_joint_q_prepare + lr_joint_kv_prepare."""
     Sq, Sk, H, HK = 300, 333, 4, 2
     print(f"\n[one-launch prepare] kind={kind} pairing={pairing} rot={rot} n_pre={n_pre} offset={offset}", flush=True)
     q, k, v, wq, wk, qa, qb, ka, kb = _fused_case(36, Sq, Sk, H, HK, kind, pairing, rot)

@@ -12,6 +12,8 @@ from __future__ import annotations
 
 import itertools
 
+import numpy as np
+
 import pytest
 
 SBM, PMAX, MAX_WG = 256, 4, 256
@@ -120,3 +122,74 @@ def test_owner_formula_matches_ranges():
         for L in range(nt):
             for u in {L * U // nt, (L + 1) * U // nt - 1}:
                 assert owner(u) == L
+
+
+# ---- the value tile in LDS (attn_stream.hip: vt_offset, vt_lane_row, vt_lane_chunk, vt_lane), restated
+def vt_offset(r, c):
+    return 256 * (4 * (r >> 2) + (c >> 2)) + 64 * (r & 3) + 16 * (c & 3)
+
+
+def vt_lane_row(l):
+    return (l >> 2) & 3
+
+
+def vt_lane_chunk(l):
+    return 4 * (l >> 4) + (l & 3)
+
+
+def vt_lane(l):
+    return 2048 * (l >> 5) + 64 * ((l >> 2) & 3) + 32 * ((l >> 4) & 1) + 8 * (l & 3)
+
+
+def _ds_read_tr16_b64(lds_u16, addr_bytes):
+    """ds_read_b64_tr_b16 on 64 lanes: in each group of 16 lanes, lane 4 j + q supplies four 16-bit elements (its 8
+    bytes) as columns 4 q .. 4 q + 3 of row j of a 4 x 16 block; lane s of the group receives column s of rows 0-3."""
+    out = np.zeros((64, 4), dtype=lds_u16.dtype)
+    for g in range(4):
+        block = np.zeros((4, 16), dtype=lds_u16.dtype)
+        for s in range(16):
+            a = addr_bytes[16 * g + s]
+            assert a % 8 == 0
+            block[s >> 2, 4 * (s & 3):4 * (s & 3) + 4] = lds_u16[a // 2:a // 2 + 4]
+        for s in range(16):
+            out[16 * g + s] = block[:, s]
+    return out
+
+
+def test_value_rows_lds_layout_gives_the_pv_operand():
+    """The direct loads of a value tile (wave w, load i, lane l: LDS bytes 2048 w + 1024 i + 16 l <- row
+    8 w + 4 i + vt_lane_row(l), chunk vt_lane_chunk(l)) fill every 16-byte unit of the slot once, at vt_offset; and two
+    transposed reads at vt_lane(l) + 4096 kk + 256 db (+ 1024) give lane l = 32 hf + n the A operand of the P V MFMA:
+    keys 16 kk + 8 hf .. +7 of dim 32 db + n. The eight-byte addresses of one read fall on distinct banks in each
+    half-wave (64 banks of 4 bytes: the read takes the minimum two passes)."""
+    rng = np.random.default_rng(0)
+    V = rng.integers(0, 1 << 16, size=(64, 128), dtype=np.uint16)
+    lds = np.full(8192, 0xFFFF, dtype=np.uint16)
+    seen = set()
+    for w in range(8):
+        for i in range(2):
+            for l in range(64):
+                o = 2048 * w + 1024 * i + 16 * l
+                r, c = 8 * w + 4 * i + vt_lane_row(l), vt_lane_chunk(l)
+                assert vt_offset(r, c) == o
+                seen.add((r, c))
+                lds[o // 2:o // 2 + 8] = V[r, 8 * c:8 * c + 8]
+    assert len(seen) == 64 * 16
+    lanes = np.arange(64)
+    for kk in range(4):
+        for db in range(4):
+            parts = []
+            for p in range(2):
+                addr = np.array([vt_lane(l) + 4096 * kk + 256 * db + 1024 * p for l in lanes])
+                for half in (addr[:32], addr[32:]):
+                    banks = set()
+                    for a in half:
+                        for b in (a // 4 % 64, a // 4 % 64 + 1):
+                            assert b not in banks, "bank conflict"
+                            banks.add(b)
+                parts.append(_ds_read_tr16_b64(lds, addr))
+            frag = np.concatenate(parts, axis=1)
+            for l in lanes:
+                hf, n = l >> 5, l & 31
+                want = V[16 * kk + 8 * hf:16 * kk + 8 * hf + 8, 32 * db + n]
+                assert np.array_equal(frag[l], want), (kk, db, l)
