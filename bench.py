@@ -25,10 +25,12 @@ the same workload, as a reported baseline only.
 over an 80-key cached text prefix (already rotated, used as given: n_pre = 80) plus the 4,096 image keys.
 
 --workload h3-int8 measures MiniMax H3's INT8 attention instead (5,967 tokens x 56 heads, the reference's headline
-shape for it): a step is Kitchen.attention on one packed qkv buffer, i.e. the prep (anchor, rotation, int8 Q / K / V,
-lr_int8_attention_prep) then the attention kernel (lr_int8_attention_kernel, rows output). Ops per call = 4 * S^2 *
-128 * H; `roofline` is the attention kernel against MI355X's dense int8 peak of 5.0 POP/s; `cpu_baseline` is the
-CPU oracle of the same chain (prep + fp64 attention over the quantised operands) on a sample of heads and rows.
+shape for it): a step is H3's whole chain on one packed qkv buffer (dit.zig:665-671), Kitchen.rmsRope fused into the
+prep (lr_int8_attention_prep_rope: norm, rotary, anchor, Hadamard rotation, int8 Q / K / V) then the attention kernel
+(lr_int8_attention_kernel, rows output); the unfused chain (lr_rms_rope_qk_bf16, lr_int8_attention_prep, the kernel)
+is timed beside it. Ops per call = 4 * S^2 * 128 * H; `roofline` is the attention kernel against MI355X's dense int8
+peak of 5.0 POP/s; `cpu_baseline` is the CPU oracle of the same chain (rmsRope + prep + fp64 attention over the
+quantised operands) on a sample of heads and rows.
 
 --workload mmdit measures BASELINE configs[2], the MMDiT double-stream block forward at the same shape (512 text +
 4096 image tokens, hidden 3072, 24 heads, GELU-tanh MLP 12288, adaLN-zero modulation from the 256-d time sinusoid,
@@ -364,9 +366,25 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def cpu_baseline_int8(qkv_bits, S, H, budget_s=10.0):
-    """The oracle's INT8 chain (anchor, rotation, quantisers, fp64 attention over the quantised operands) for a sample
-    of heads and query rows, timed on host cores. Returns ops/s over the sampled rows and the outputs."""
+def h3_table(S: int):
+    """A bf16 H3 rotary table [S, 48, 2, 2] (rows [S, 192]) from H3's own layout arithmetic (rope.h3_positions /
+    h3_rope_table: a text + video layout's positions, 16 frequencies per axis), tiled to S rows."""
+    import numpy as np
+
+    from localrouter_amd import rope
+    pos = rope.h3_positions(24, 3, 8, 12, 15)
+    inv = (1.0 / np.power(10000.0, np.arange(16) / 16.0)).astype(np.float32)
+    tab = rope.h3_rope_table(pos, inv).reshape(-1, 192)
+    return np.ascontiguousarray(np.tile(tab, (-(-S // tab.shape[0]), 1))[:S])
+
+
+H3_ROT, H3_EPS = 96, 1e-6
+
+
+def cpu_baseline_int8(qkv_bits, qn, kn, tab, S, H, budget_s=10.0):
+    """The oracle's H3 chain (rmsRope in its bf16 rounding mode, anchor, rotation, quantisers, fp64 attention over the
+    quantised operands) for a sample of heads and query rows, timed on host cores. Returns ops/s over the sampled
+    rows and the outputs."""
     import numpy as np
 
     import oracle
@@ -375,11 +393,17 @@ def cpu_baseline_int8(qkv_bits, S, H, budget_s=10.0):
     rng = np.random.default_rng(0)
     heads = [0, H // 2, H - 1]
 
+    def rope(x, w):
+        y = oracle.rms_rope(np.ascontiguousarray(x)[:, None, :], None, w_bf16=w, table_kind=oracle.TABLE_MAT2_BF16,
+                            ta=tab, pairing=oracle.PAIR_SPLIT_HALF, rot=H3_ROT, eps=H3_EPS, round_norm=True)
+        return oracle.f32_to_bf16(y[:, 0, :])
+
     def run(rows):
         t0 = time.perf_counter()
         outs = {}
         for h in heads:
             q, k, v = (np.ascontiguousarray(qkv_bits[:, i, h]) for i in range(3))
+            q, k = rope(q, qn), rope(k, kn)
             rot = oracle.i8_rotation_for(S)
             a = oracle.i8_anchor(k)
             q8, qs = oracle.i8_quant_rows(q[rows], rot)
@@ -416,71 +440,98 @@ def bench_int8(args):
     rc = L.lr_attn_init()
     if rc != 0:
         raise SystemExit(f"lr_attn_init: {rc} (not a gfx950?)")
-    log(f"[bench] workload h3-int8: S={S} H={H}, packed qkv [S, 3*H*128]")
+    log(f"[bench] workload h3-int8: S={S} H={H}, packed qkv [S, 3*H*128], rmsRope rot {H3_ROT}")
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed)
     qkv = torch.randn((S, 3 * H * 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    qkv_u = qkv.clone()   # the unfused chain's buffer (its rmsRope works in place)
+    qn = (1.0 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1.0 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+    tab_np = h3_table(S)
+    tab = torch.from_numpy(tab_np.view(np.int16)).to(dev).view(torch.bfloat16)
     out = torch.empty((S, H * 128), dtype=torch.bfloat16, device=dev)
     ws_bytes = ops.int8_workspace_bytes(H, S)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
     row = 3 * H * 128
-    q_ptr, k_ptr, v_ptr = (qkv.data_ptr() + i * H * 128 * 2 for i in range(3))
     strides = (S * row, 128, row)
 
-    def prep():
-        _lib.call("lr_int8_attention_prep", q_ptr, k_ptr, v_ptr, ws.data_ptr(), 1, H, H, S, S, 128, *strides, *strides,
-                  *strides, sh)
+    def qkv_ptrs(t):
+        return tuple(t.data_ptr() + i * H * 128 * 2 for i in range(3))
+
+    q_ptr, k_ptr, v_ptr = qkv_ptrs(qkv)
+    qu_ptr, ku_ptr, vu_ptr = qkv_ptrs(qkv_u)
+
+    def prep_rope():   # Kitchen.rmsRope + Kitchen.attentionPrep, fused (qkv unmodified)
+        _lib.call("lr_int8_attention_prep_rope", q_ptr, k_ptr, v_ptr, ws.data_ptr(), 1, H, H, S, S, 128, *strides,
+                  *strides, *strides, qn.data_ptr(), kn.data_ptr(), tab.data_ptr(), 192, H3_ROT, H3_EPS, sh)
 
     def attn():
         _lib.call("lr_int8_attention_kernel", out.data_ptr(), ws.data_ptr(), 1, H, H, S, S, 128, ops.SCALE_128, 1, sh)
 
+    def rms_rope_u():   # the unfused chain: Kitchen.rmsRope in place, then Kitchen.attentionPrep
+        _lib.call("lr_rms_rope_qk_bf16", qu_ptr, ku_ptr, S, H, row, row, qn.data_ptr(), kn.data_ptr(), tab.data_ptr(),
+                  192, H3_ROT, H3_EPS, sh)
+
+    def prep_u():
+        _lib.call("lr_int8_attention_prep", qu_ptr, ku_ptr, vu_ptr, ws.data_ptr(), 1, H, H, S, S, 128, *strides,
+                  *strides, *strides, sh)
+
+    def chain():
+        prep_rope()
+        attn()
+
     for _ in range(args.warmup):
-        prep()
-        attn()
+        chain()
     torch.cuda.synchronize()
-
-    def pair():
-        prep()
-        attn()
-
-    pre_calls, pre_s = preroll(pair, args.preroll_s)
-    log(f"[bench] warmup {args.warmup} done, pre-roll {pre_calls} calls in {pre_s:.2f} s; timing {args.steps} steps")
+    pre_calls, pre_s = preroll(chain, args.preroll_s)
+    log(f"[bench] warmup {args.warmup} done, pre-roll {pre_calls} chains in {pre_s:.2f} s; timing {args.steps} steps")
     K = args.steps
-    # the timed steps: K (prep, kernel) call pairs back to back, as the engine makes them; events around the loop only
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+
+    def timed(fns):
+        """K steps of the calls fns back to back: (ms per step from events around the loop, ms per call from events
+        between the calls of a second loop)."""
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(K):
+            for f in fns:
+                f()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        step = e0.elapsed_time(e1) / K
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(fns) * K + 1)]
+        torch.cuda.synchronize()
+        for i in range(K):
+            for j, f in enumerate(fns):
+                ev[len(fns) * i + j].record(stream)
+                f()
+        ev[-1].record(stream)
+        torch.cuda.synchronize()
+        per = [float(np.mean([ev[len(fns) * i + j].elapsed_time(ev[len(fns) * i + j + 1]) for i in range(K)]))
+               for j in range(len(fns))]
+        return step, per
+
     t_wall = time.perf_counter()
-    e0.record(stream)
-    for _ in range(K):
-        prep()
-        attn()
-    e1.record(stream)
-    torch.cuda.synchronize()
+    ms_step, (prep_ms, attn_ms) = timed([prep_rope, attn])
     wall = time.perf_counter() - t_wall
-    ms_step_calls = e0.elapsed_time(e1) / K
-    # the same pairs with an event between the calls: the attention kernel and the prep timed alone
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
+    got = out.cpu()
+    # the engine's unfused chain on the same inputs, for comparison (and its output: the same bits)
+    ms_unfused, (rope_u_ms, prep_u_ms, attn_u_ms) = timed([rms_rope_u, prep_u, attn])
+    qkv_u.copy_(qkv)
+    rms_rope_u()
+    prep_u()
+    attn()
     torch.cuda.synchronize()
-    for i in range(K):
-        ev[2 * i].record(stream)
-        prep()
-        ev[2 * i + 1].record(stream)
-        attn()
-    ev[2 * K].record(stream)
-    torch.cuda.synchronize()
-    t_prep = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(K)]
-    t_attn = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(K)]
-    staged_ms = ev[0].elapsed_time(ev[2 * K]) / K
-    ms_step = ms_step_calls
+    same = bool(torch.equal(out.cpu(), got))
     ops_call = 4.0 * S * S * 128 * H
-    attn_ms, prep_ms = float(np.mean(t_attn)), float(np.mean(t_prep))
     value = ops_call / (ms_step * 1e-3) / 1e12
     achieved = ops_call / (attn_ms * 1e-3) / 1e12
-    log(f"[bench] step {ms_step:.4f} ms (calls back to back; with an event between them {staged_ms:.4f} ms: prep "
-        f"{prep_ms:.4f} ms, attention {attn_ms:.4f} ms, median {float(np.median(t_attn)):.4f} ms); {value:.1f} TOP/s step, {achieved:.1f} TOP/s attention kernel "
-        f"({100 * achieved / PEAK_INT8_TOPS:.1f}% of int8 peak); wall {wall:.3f} s")
+    log(f"[bench] step {ms_step:.4f} ms (fused rmsRope + prep {prep_ms:.4f} ms, attention {attn_ms:.4f} ms); "
+        f"{value:.1f} TOP/s step, {achieved:.1f} TOP/s attention kernel ({100 * achieved / PEAK_INT8_TOPS:.1f}% of "
+        f"int8 peak); unfused chain {ms_unfused:.4f} ms (rmsRope {rope_u_ms:.4f} + prep {prep_u_ms:.4f} + attention "
+        f"{attn_u_ms:.4f} ms), same output bits: {same}; wall {wall:.3f} s")
     result = {
         "metric": "int8 attention TOP/s + % int8 MFMA peak; ms/call at 5967 tokens, 56x128 (MiniMax H3)",
         "value": round(value, 2),
@@ -489,21 +540,27 @@ def bench_int8(args):
         "steps": K,
         "warmup": args.warmup,
         "preroll": {"calls": pre_calls, "seconds": round(pre_s, 3),
-                    "note": "untimed (prep, kernel) pairs after the warm-up, the same for every --warmup"},
+                    "note": "untimed chains after the warm-up, the same for every --warmup"},
         "ms_per_step": round(ms_step, 5),
-        "staged_ms_per_step": round(staged_ms, 5),
+        "unfused_ms_per_step": round(ms_unfused, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "h3-int8-attention", "batch": 1, "tokens": S, "heads": H, "head_dim": 128,
-                   "causal": False, "input": "packed qkv [S, 3*H*128] bf16 ~ N(0,1)", "output": "rows [S, H*128]",
-                   "parallelism": "none (1 GPU)"},
+                   "causal": False, "input": "packed qkv [S, 3*H*128] bf16 ~ N(0,1), before rmsRope",
+                   "rms_rope": {"rot": H3_ROT, "eps": H3_EPS, "weights": "bf16 1 + 0.1 N(0,1)",
+                                "table": "bf16 [S, 48, 2, 2] of H3's layout arithmetic"},
+                   "step": "lr_int8_attention_prep_rope (rmsRope + prep) then lr_int8_attention_kernel (rows out)",
+                   "output": "rows [S, H*128]", "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profile("h3-int8", "i8_attn"),
                      "kernel": "i8_attn_kernel<128, 4>", "kernel_ms": round(attn_ms, 5)},
-        "kernels_ms": {"prep": round(prep_ms, 5), "attention": round(attn_ms, 5)},
+        "kernels_ms": {"prep_rope": round(prep_ms, 5), "attention": round(attn_ms, 5),
+                       "unfused": {"rms_rope": round(rope_u_ms, 5), "prep": round(prep_u_ms, 5),
+                                   "attention": round(attn_u_ms, 5)}},
+        "fused_equals_unfused": same,
         "ops_per_call": ops_call,
     }
     if args.calibrate_copy:
@@ -513,17 +570,19 @@ def bench_int8(args):
         torch.cuda.synchronize()
         del src, dst
     if not args.no_cpu_baseline:
-        log("[bench] cpu baseline (oracle INT8 chain, sampled heads and query rows) ...")
+        log("[bench] cpu baseline (oracle H3 chain, sampled heads and query rows) ...")
         qb = qkv.cpu().view(torch.int16).numpy().view(np.uint16).reshape(S, 3, H, 128)
-        cb = cpu_baseline_int8(qb, S, H)
-        got = out.cpu().view(torch.int16).numpy().view(np.uint16).reshape(S, H, 128)
-        d = np.concatenate([np.abs(((got[cb["rows"], h].astype(np.uint32) << 16).view(np.float32)).astype(np.float64)
+        qnb = qn.cpu().view(torch.int16).numpy().view(np.uint16)
+        knb = kn.cpu().view(torch.int16).numpy().view(np.uint16)
+        cb = cpu_baseline_int8(qb, qnb, knb, tab_np, S, H)
+        gb = got.view(torch.int16).numpy().view(np.uint16).reshape(S, H, 128)
+        d = np.concatenate([np.abs(((gb[cb["rows"], h].astype(np.uint32) << 16).view(np.float32)).astype(np.float64)
                                    - cb["outs"][h]).ravel() for h in cb["heads"]])
         result["cpu_baseline"] = {"value": round(cb["value"], 4), "unit": "TOP/s", "cores": cb["threads"],
                                   "kind": "port",
                                   "sample": f"{len(cb['rows'])} of {S} query rows x heads {cb['heads']} over all {S} "
-                                            f"keys (anchor + quantisers + fp64 attention): median of {cb['runs']} runs, "
-                                            f"{cb['seconds']:.2f} s each"}
+                                            f"keys (rmsRope + anchor + quantisers + fp64 attention): median of "
+                                            f"{cb['runs']} runs, {cb['seconds']:.2f} s each"}
         result["check"] = {"rows": int(len(cb["rows"])), "heads": cb["heads"], "max_abs": float(d.max()),
                            "mean_abs": float(d.mean()), "bar": {"max_abs": 2e-2, "mean_abs": 2e-3}}
         log(f"[bench] cpu {cb['value']:.4f} TOP/s on {cb['threads']} threads; GPU vs CPU on sampled rows: "

@@ -42,7 +42,7 @@ extern "C" {
 /* hipStream_t without pulling in the HIP headers: an opaque pointer (NULL = the default stream). */
 typedef struct ihipStream_t* lr_stream_t;
 
-#define LR_ATTN_ABI_VERSION 7
+#define LR_ATTN_ABI_VERSION 8
 #define LR_HEAD_DIM 128
 
 /* RoPE table kinds: how rotation coefficients are stored per token row, per pair p < rot_dim/2. */
@@ -301,6 +301,23 @@ int lr_int8_attention_prep(const void* q, const void* k, const void* v, void* wo
                            int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, lr_stream_t stream);
 int lr_int8_attention_kernel(void* out, const void* workspace, int B, int H, int HK, int Sq, int Sk, int D,
                              float scale, int o_rows, lr_stream_t stream);
+
+/*
+ * Kitchen.rmsRope fused into Kitchen.attentionPrep: the H3 chain rmsRope -> attentionPrep -> attentionKernel
+ * (src/engines/minimax_h3/dit.zig:665-671; the fold the reference names as its next step, docs/dev/RESULTS.md:325-327)
+ * as prep_rope -> kernel. The workspace is written exactly as lr_rms_rope_qk_bf16 (in place on q and k) followed by
+ * lr_int8_attention_prep would write it -- the same bits -- but q and k are read once and not modified: each row is
+ * normalised and rotated in registers, rounded to bf16 as the standalone pass stores it, and quantised.
+ *   q, k, v, workspace, strides, B, H, HK, Sq, Sk as lr_int8_attention_prep; D 128; Sq == Sk (token n of q and of k
+ *   uses table row n, as in Kitchen.rmsRope over one packed qkv buffer);
+ *   q_norm, k_norm, freqs, freqs_row_stride, rot_dim, eps as lr_rms_rope_qk_bf16 (rot_dim 0 = 128, else a multiple of
+ *   16); the weights and the table rows 16-byte aligned (freqs_row_stride a multiple of 8 elements).
+ */
+int lr_int8_attention_prep_rope(const void* q, const void* k, const void* v, void* workspace, int B, int H, int HK,
+                                int Sq, int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb,
+                                int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                                const void* q_norm, const void* k_norm, const void* freqs, int64_t freqs_row_stride,
+                                int rot_dim, float eps, lr_stream_t stream);
 
 
 #ifdef __cplusplus

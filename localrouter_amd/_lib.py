@@ -57,6 +57,8 @@ SIGNATURES = {
     "lr_int8_attention_rows": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I] + [_I64] * 9 + [_F, _P]),
     "lr_int8_attention_prep": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I] + [_I64] * 9 + [_P]),
     "lr_int8_attention_kernel": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
+    "lr_int8_attention_prep_rope": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I] + [_I64] * 9 +
+                                    [_P, _P, _P, _I64, _I, _F, _P]),
     "lr_attention_ws_bytes": (_SZ, [_I, _I, _I, _I]),
     "lr_attention_bf16_ws": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I64, _I64, _I64, _P, _SZ, _P]),
     "lr_attention_kmask_workspace_bytes": (_SZ, [_I, _I]),

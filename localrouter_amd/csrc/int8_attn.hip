@@ -39,10 +39,35 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 constexpr float S_U8_OFFSET = 7.9943534f;  // log2(255): the tile's largest P becomes 255 (attn_utils.cuh:41)
 
 // ------------------------------------------------------------------------------------------------ prep helpers
-// Exchange with lane ^ M inside each 32-lane half (ds_swizzle, bit-mask mode: and 0x1f, xor M).
+// Exchange with lane ^ M. M < 16: inside each row of 16 lanes by DPP (a register move across lanes, no LDS round
+// trip): quad_perm [1,0,3,2] / [2,3,0,1] for M = 1 / 2; for M = 4 / 8 the lanes with bit M clear take row_shl:M (lane
+// i + M), the others row_shr:M (lane i - M). M = 16: inside each 32-lane half (ds_swizzle, and 0x1f, xor 16).
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, true);
+}
+template <int M>
+__device__ __forceinline__ int xor_lane_i(int x) {
+    if constexpr (M == 1) {
+        return dpp_mov<0xb1>(x);
+    } else if constexpr (M == 2) {
+        return dpp_mov<0x4e>(x);
+    } else if constexpr (M == 4 || M == 8) {
+        const int up = dpp_mov<0x100 + M>(x), dn = dpp_mov<0x110 + M>(x);
+        return (threadIdx.x & M) ? dn : up;
+    } else {
+        return __builtin_amdgcn_ds_swizzle(x, 0x1f | (M << 10));
+    }
+}
 template <int M>
 __device__ __forceinline__ float xor_lane(float x) {
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (M << 10)));
+    return __int_as_float(xor_lane_i<M>(__float_as_int(x)));
+}
+template <int M>
+__device__ __forceinline__ double xor_lane(double x) {
+    const uint64_t b = (uint64_t)__double_as_longlong(x);
+    const uint32_t lo = (uint32_t)xor_lane_i<M>((int)(uint32_t)b), hi = (uint32_t)xor_lane_i<M>((int)(uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
 // max over each group of LPR lanes (one row of 8 * LPR channels, 8 per lane)
@@ -146,11 +171,97 @@ __device__ __forceinline__ u32x2 pack_s8x8(const float (&x)[8], float inv) {
     return w;
 }
 
+// ------------------------------------------------------------------------------------------------ fused rmsRope
+// Kitchen.rmsRope (kernels/cuda/minimax/kitchen/rms_rope.cu:37-230, as src/engines/minimax_h3/launch.zig:421-441
+// launches it) of one row held by a group of 16 lanes, lane L holding channels 8 L .. 8 L + 7, for the prep of
+// lr_int8_attention_prep_rope:
+//   rrms = 1 / sqrt(sum(x^2) / 128 + eps) and x * rrms * w, in double, rounded to fp32 and then to bf16 (the
+//   normalised value the reference rounds before the rotation, rms_rope.cu:143-150);
+//   pairs (i, i + rot / 2), i < rot / 2, rotated by the table's [f00 f01; f10 f11] (rope_device.cuh:65-98) in fp32
+//   and rounded to bf16 (the value the reference stores); channels >= rot keep the normalised value.
+// The sum of squares of bf16 values is exact in double (for rows whose values span less than 2^30 in magnitude), sqrt
+// and division are correctly rounded, the normalised values are those of the double computation (norm_bf16_exact),
+// and the products in the rotation are products of bf16 values (exact in fp32), so each result is the same bits as
+// the CPU restatement (oracle/lro.c, lro_rms_rope_ex with round_norm) rounded to bf16.
+struct RopeTab {
+    uint32_t w[8];  // this lane's row of each of its 8 pairs' matrices: (f00, f01) or (f10, f11), bf16
+};
+
+// The table entries of token `token` for lane L: pairs 8 pc .. 8 pc + 7 (pc = L or L - rot / 16), of each pair's
+// [2][2] matrix the row this lane's output needs (row 0 for the first half's lanes, row 1 for the second's): eight
+// 4-byte loads. (Lanes past the rotated channels load pair chunk 0 too, unused: no branch around the loads.)
+__device__ __forceinline__ RopeTab rope_tab_load(const PrepArgs& a, int token, int L) {
+    RopeTab t;
+    const int hc = a.rope_rot >> 4;
+    const int pc = L < hc ? L : (L < 2 * hc ? L - hc : 0);
+    const uint16_t* src = a.rope_tab + (int64_t)token * a.tab_rs + 32 * pc + (L >= hc && L < 2 * hc ? 2 : 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t.w[j] = *reinterpret_cast<const uint32_t*>(src + 4 * j);
+    return t;
+}
+
+// The table rows of a block's 64 rows staged in LDS (rows of TAB_LDS_STRIDE bytes, the table row's first 4 rot bytes:
+// [rot/2 pairs][2][2] bf16), loaded once per block with coalesced 16-byte loads instead of per lane and row. The pad
+// of 16 bytes a row puts the four row groups of a wave on different banks.
+constexpr int TAB_LDS_STRIDE = 4 * 128 + 16;
+constexpr int TAB_LDS_BYTES = 64 * TAB_LDS_STRIDE;
+
+// Stage table rows row_of(r), r < 64, into lds; the caller synchronises the block before reading them.
+template <typename RowOf>
+__device__ __forceinline__ void rope_tab_stage(const PrepArgs& a, uint8_t* lds, RowOf row_of) {
+    const int nch = a.rope_rot >> 2;   // 16-byte chunks of a row's 4 rot bytes
+    for (int idx = threadIdx.x; idx < 64 * nch; idx += 256) {
+        const int r = idx / nch, c = idx - r * nch;
+        *reinterpret_cast<u32x4*>(lds + r * TAB_LDS_STRIDE + 16 * c) =
+            *reinterpret_cast<const u32x4*>(a.rope_tab + (int64_t)row_of(r) * a.tab_rs + 8 * c);
+    }
+}
+
+// rope_tab_load's entries of staged row r
+__device__ __forceinline__ RopeTab rope_tab_lds(const uint8_t* lds, int r, int L, int rot) {
+    RopeTab t;
+    const int hc = rot >> 4;
+    const int pc = L < hc ? L : (L < 2 * hc ? L - hc : 0);
+    const uint8_t* src = lds + r * TAB_LDS_STRIDE + 64 * pc + (L >= hc && L < 2 * hc ? 4 : 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t.w[j] = *reinterpret_cast<const uint32_t*>(src + 8 * j);
+    return t;
+}
+
+// the lane's 8 weights (bf16 [128]) as floats
+__device__ __forceinline__ void rope_w_load(const uint16_t* w, int L, float (&wv)[8]) { load8(w + 8 * L, wv); }
+
+__device__ __forceinline__ float bf16_round(float x) { return (float)(bf16)x; }
+
+__device__ __forceinline__ void h3_rms_rope(float (&x)[8], int L, const float (&w)[8], const RopeTab& t, int rot,
+                                            float eps) {
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ss = fma((double)x[c], (double)x[c], ss);
+    ss += xor_lane<1>(ss);
+    ss += xor_lane<2>(ss);
+    ss += xor_lane<4>(ss);
+    ss += xor_lane<8>(ss);
+    norm_bf16_exact8(x, 1.0 / sqrt(ss / 128.0 + (double)eps), w);
+    const int hc = rot >> 4;
+    const bool first = L < hc, second = L >= hc && L < 2 * hc;
+    const int partner = first ? L + hc : (second ? L - hc : L);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const float y = __shfl(x[c], partner, 16);
+        const float a0 = first ? x[c] : y, b0 = first ? y : x[c];   // (x_i, x_{i + rot/2})
+        // first half: f00 x_i + f01 x_{i+rot/2}; second half: f10 x_i + f11 x_{i+rot/2}
+        const float yo = fmaf(lo_bf16(t.w[c]), a0, hi_bf16(t.w[c]) * b0);
+        x[c] = first || second ? bf16_round(yo) : x[c];
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ prep launch 1
 // Blocks x < nvchunk: channel abs-max of V over keys [x * 256, x * 256 + 256) of kv head y -> vpart.
 // Block x == nvchunk: the anchor of kv head y (nine sample keys at i * (Sk - 1) / 8; the sample with the least
 // squared distance to the others is subtracted from every key when that lowers the samples' energy and raises their
 // abs-max by at most 12.5 %), in fp64 like the checker.
+template <bool ROPE>
 __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
 #pragma clang fp contract(off)
     const Plan& p = a.p;
@@ -192,12 +303,29 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
     __shared__ double sd[NSAMP + 2][128];
     double s[NSAMP];
     const uint16_t* kb = a.k + b * a.k_sb + hk * a.k_sh;
+    // fused rmsRope: the sample rows normalised and rotated first (16 lanes a row, groups 0-8), exactly as quant_k
+    // prepares every key row
+    __shared__ float rows[ROPE ? NSAMP : 1][128];
+    if constexpr (ROPE) {
+        const int grp = t >> 4, L = t & 15;
+        if (grp < NSAMP) {
+            const int row = (int)((int64_t)grp * (a.Sk - 1) / (NSAMP - 1));
+            float x[8], wv[8];
+            load8(kb + (int64_t)row * a.k_sn + 8 * L, x);
+            rope_w_load(a.kw, L, wv);
+            h3_rms_rope(x, L, wv, rope_tab_load(a, row, L), a.rope_rot, a.rope_eps);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) rows[grp][8 * L + c] = x[c];
+        }
+        __syncthreads();
+    }
     if (t < D) {
         double e = 0.0, mx = 0.0, sum = 0.0;
 #pragma unroll
         for (int i = 0; i < NSAMP; ++i) {
             const int row = (int)((int64_t)i * (a.Sk - 1) / (NSAMP - 1));
-            s[i] = (double)bf16_bits_to_f32(kb[(int64_t)row * a.k_sn + t]);
+            if constexpr (ROPE) s[i] = (double)rows[i][t];
+            else s[i] = (double)bf16_bits_to_f32(kb[(int64_t)row * a.k_sn + t]);
             e += s[i] * s[i];
             mx = fmax(mx, fabs(s[i]));
             sum += s[i];
@@ -257,25 +385,43 @@ constexpr int QROWS = 64;  // query rows per block
 constexpr int KROWS = 64;  // key rows per block: four scale groups of 16, one per wave
 
 // Q: QROWS rows of head h per block, 256 / LPR per pass, one scale per row.
-template <int ROT, int HD>
-__device__ void quant_q(const PrepArgs& a, int b, int h, int qb) {
+template <int ROT, int HD, bool ROPE>
+__device__ void quant_q(const PrepArgs& a, int b, int h, int qb, uint8_t* lds) {
 #pragma clang fp contract(off)
     constexpr int LPR = HD / 8, RPB = 256 / LPR;  // lanes a row, rows a block pass
     const Plan& p = a.p;
     const int t = threadIdx.x, slot = t / LPR, L = t % LPR;
     float xs[QROWS / RPB][8];  // every row of the lane loaded before the first rotation: all loads in flight at once
+    float wv[8];
+    if constexpr (ROPE) rope_tab_stage(a, lds, [&](int r) { return min(qb * QROWS + r, a.Sq - 1); });
 #pragma unroll
     for (int i = 0; i < QROWS / RPB; ++i) {
         const int row = qb * QROWS + RPB * i + slot;
+        if constexpr (ROPE) {   // no branch around the loads: rows past Sq read the last row, then zeroed
+            load8(a.q + b * a.q_sb + h * a.q_sh + (int64_t)min(row, a.Sq - 1) * a.q_sn + 8 * L, xs[i]);
+        } else {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) xs[i][c] = 0.0f;
-        if (row < a.Sq) load8(a.q + b * a.q_sb + h * a.q_sh + (int64_t)row * a.q_sn + 8 * L, xs[i]);
+            for (int c = 0; c < 8; ++c) xs[i][c] = 0.0f;
+            if (row < a.Sq) load8(a.q + b * a.q_sb + h * a.q_sh + (int64_t)row * a.q_sn + 8 * L, xs[i]);
+        }
+    }
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int i = 0; i < QROWS / RPB; ++i)
+            if (qb * QROWS + RPB * i + slot >= a.Sq)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) xs[i][c] = 0.0f;
+    }
+    if constexpr (ROPE) {
+        rope_w_load(a.qw, L, wv);
+        __syncthreads();   // the staged table rows
     }
 #pragma unroll
     for (int i = 0; i < QROWS / RPB; ++i) {
         const int row = qb * QROWS + RPB * i + slot;
         const bool ok = row < a.Sq;
         float (&x)[8] = xs[i];
+        if constexpr (ROPE) h3_rms_rope(x, L, wv, rope_tab_lds(lds, RPB * i + slot, L, a.rope_rot), a.rope_rot, a.rope_eps);
         rotate8<ROT>(x, L);
         float m = 0.0f;
 #pragma unroll
@@ -293,8 +439,8 @@ __device__ void quant_q(const PrepArgs& a, int b, int h, int qb) {
 
 // K: KROWS key rows of kv head hk per block; wave w holds scale group 4 kb + w (16 rows, 64 / LPR a pass), the anchor
 // row subtracted before the rotation.
-template <int ROT, int HD>
-__device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
+template <int ROT, int HD, bool ROPE>
+__device__ void quant_k(const PrepArgs& a, int b, int hk, int kb, uint8_t* lds) {
 #pragma clang fp contract(off)
     constexpr int LPR = HD / 8, RPW = 64 / LPR, NP = KGROUP / RPW;  // lanes a row, rows a wave pass, passes
     const Plan& p = a.p;
@@ -303,22 +449,32 @@ __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
     const int anc = reinterpret_cast<const int*>(a.ws + p.anchor)[b * a.HK + hk];
     const uint16_t* kbase = a.k + b * a.k_sb + hk * a.k_sh + 8 * L;
     float av[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    if (anc >= 0) load8(kbase + (int64_t)anc * a.k_sn, av);
+    float wv[8];
+    if constexpr (ROPE) rope_w_load(a.kw, L, wv);
+    if (anc >= 0) {
+        load8(kbase + (int64_t)anc * a.k_sn, av);
+        if constexpr (ROPE) h3_rms_rope(av, L, wv, rope_tab_load(a, anc, L), a.rope_rot, a.rope_eps);
+    }
     // Rows past Sk (the last tile's padding) repeat real keys: those of the last key's scale group gL, key Sk - 1
     // standing in past its end. A padded row of group gL then equals key Sk - 1 and leaves the group's scale as it
     // is; a wholly padded group is a copy of group gL, scale included. Their scores equal real scores, so they never
     // raise a row max; the attention zeroes their P.
     const int last = a.Sk - 1, gl = last / KGROUP;
+    auto src_of = [&](int row) { return row <= last ? row : min(gl * KGROUP + (row & (KGROUP - 1)), last); };
+    if constexpr (ROPE) rope_tab_stage(a, lds, [&](int r) { return src_of(kb * KROWS + r); });
     float x[NP][8];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {  // all the lane's rows in flight before the first rotation
         const int row = grp * KGROUP + RPW * i + rsub;
-        const int src = row <= last ? row : min(gl * KGROUP + (row & (KGROUP - 1)), last);
-        load8(kbase + (int64_t)src * a.k_sn, x[i]);
+        load8(kbase + (int64_t)src_of(row) * a.k_sn, x[i]);
     }
+    if constexpr (ROPE) __syncthreads();   // the staged table rows
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
+        if constexpr (ROPE)
+            h3_rms_rope(x[i], L, wv, rope_tab_lds(lds, wave * KGROUP + RPW * i + rsub, L, a.rope_rot), a.rope_rot,
+                        a.rope_eps);
 #pragma unroll
         for (int c = 0; c < 8; ++c) x[i][c] = x[i][c] - av[c];
         rotate8<ROT>(x[i], L);
@@ -347,12 +503,16 @@ __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb) {
 // V: one tile of cta keys of kv head hk per block: per-channel scales from the abs-max partials, int8, transposed into
 // [HD dims][cta keys] in LDS (rows padded by 4 bytes, so that the lanes of a wave, which write different dims, spread
 // over the banks), column sums per half tile into the aux block, then stored swizzled.
-template <int HD>
-__device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
+// ext: the kernel's own LDS buffer to use (the fused-rmsRope kernel shares one with the table staging), else null.
+constexpr int VTS_BYTES = 128 * (128 + 4);
+template <int HD, bool EXT>
+__device__ void quant_v(const PrepArgs& a, int b, int hk, int tile, uint8_t* ext) {
 #pragma clang fp contract(off)
     constexpr int CG = HD / 8, KQP = 256 / CG;  // 8-channel groups a key; key quads a block pass
-    __shared__ float inv_s[HD];
-    __shared__ __attribute__((aligned(16))) uint8_t vts[HD * (128 + 4)];
+    __shared__ float inv_own[EXT ? 1 : HD];
+    __shared__ __attribute__((aligned(16))) uint8_t vts_own[EXT ? 1 : HD * (128 + 4)];
+    uint8_t* vts = EXT ? ext : vts_own;
+    float* inv_s = EXT ? reinterpret_cast<float*>(ext + VTS_BYTES) : inv_own;
     const Plan& p = a.p;
     const int cta = p.cta, vs = cta + 4, t = threadIdx.x;
     const size_t bhk = (size_t)b * a.HK + hk;
@@ -412,22 +572,24 @@ __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile) {
 }
 
 // grid (ceil(Sq / QROWS) + skp / KROWS + ntiles, max(H, HK), B): Q blocks, then K blocks, then V tiles.
-template <int ROT, int HD>
+template <int ROT, int HD, bool ROPE = false>
 __global__ __launch_bounds__(256) void i8_quant_kernel(PrepArgs a) {
+    static_assert(!ROPE || TAB_LDS_BYTES >= VTS_BYTES + 4 * 128, "the shared buffer holds quant_v's arrays");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[ROPE ? TAB_LDS_BYTES : 1];
     const int b = blockIdx.z, y = blockIdx.y;
     const int nqb = (a.Sq + QROWS - 1) / QROWS, nkb = a.p.skp / KROWS;
     int x = blockIdx.x;
     if (x < nqb) {
-        if (y < a.H) quant_q<ROT, HD>(a, b, y, x);
+        if (y < a.H) quant_q<ROT, HD, ROPE>(a, b, y, x, lds);
         return;
     }
     x -= nqb;
     if (x < nkb) {
-        if (y < a.HK) quant_k<ROT, HD>(a, b, y, x);
+        if (y < a.HK) quant_k<ROT, HD, ROPE>(a, b, y, x, lds);
         return;
     }
     x -= nkb;
-    if (y < a.HK) quant_v<HD>(a, b, y, x);
+    if (y < a.HK) quant_v<HD, ROPE>(a, b, y, x, lds);
 }
 
 // ------------------------------------------------------------------------------------------------ attention
@@ -827,11 +989,16 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
 hipError_t launch_prep(const PrepArgs& a, hipStream_t stream) {
     const Plan& p = a.p;
-    hipLaunchKernelGGL(i8_stats_kernel, dim3(p.nvchunk + 1, a.HK, a.B), dim3(256), 0, stream, a);
+    if (a.rope_tab) hipLaunchKernelGGL(i8_stats_kernel<true>, dim3(p.nvchunk + 1, a.HK, a.B), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(i8_stats_kernel<false>, dim3(p.nvchunk + 1, a.HK, a.B), dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid((a.Sq + QROWS - 1) / QROWS + p.skp / KROWS + p.ntiles, a.H > a.HK ? a.H : a.HK, a.B);
-    if (p.d == 128) {
+    if (a.rope_tab) {   // the fused rmsRope: head dim 128 only (checked by the caller)
+        if (p.d != 128) return hipErrorInvalidValue;
+        if (p.rot == 4) hipLaunchKernelGGL((i8_quant_kernel<4, 128, true>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((i8_quant_kernel<128, 128, true>), grid, dim3(256), 0, stream, a);
+    } else if (p.d == 128) {
         if (p.rot == 4) hipLaunchKernelGGL((i8_quant_kernel<4, 128>), grid, dim3(256), 0, stream, a);
         else hipLaunchKernelGGL((i8_quant_kernel<128, 128>), grid, dim3(256), 0, stream, a);
     } else {

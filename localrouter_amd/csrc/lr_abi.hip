@@ -382,9 +382,11 @@ bool i8_tensor_ok(const void* p, int64_t sb, int64_t sh, int64_t sn, int nb, int
     return p && aligned(p, 16) && ok(sb, nb) && ok(sh, nh) && ok(sn, nn);
 }
 
+// rope_tab non-null: Kitchen.rmsRope fused into the prep (lr_int8_attention_prep_rope, arguments checked there)
 int i8_prep_impl(const void* q, const void* k, const void* v, void* ws, int B, int H, int HK, int Sq, int Sk, int D,
                  int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn, int64_t v_sb,
-                 int64_t v_sh, int64_t v_sn, hipStream_t stream) {
+                 int64_t v_sh, int64_t v_sn, hipStream_t stream, const void* rope_tab = nullptr, int64_t tab_rs = 0,
+                 const void* qw = nullptr, const void* kw = nullptr, int rot = 0, float eps = 0.0f) {
     if (!i8_sizes_ok(B, H, HK, Sq, Sk, D) || !ws || !aligned(ws, 256)) return ERR_ARGS;
     if (!i8_tensor_ok(q, q_sb, q_sh, q_sn, B, H, Sq) || !i8_tensor_ok(k, k_sb, k_sh, k_sn, B, HK, Sk) ||
         !i8_tensor_ok(v, v_sb, v_sh, v_sn, B, HK, Sk))
@@ -399,6 +401,12 @@ int i8_prep_impl(const void* q, const void* k, const void* v, void* ws, int B, i
     a.B = B; a.H = H; a.HK = HK; a.Sq = Sq; a.Sk = Sk;
     a.ws = static_cast<uint8_t*>(ws);
     a.p = lr::i8::plan_of(B, H, HK, Sq, Sk, D);
+    a.rope_tab = static_cast<const uint16_t*>(rope_tab);
+    a.tab_rs = tab_rs;
+    a.qw = static_cast<const uint16_t*>(qw);
+    a.kw = static_cast<const uint16_t*>(kw);
+    a.rope_rot = rot;
+    a.rope_eps = eps;
     return (int)lr::i8::launch_prep(a, stream);
 }
 
@@ -704,6 +712,23 @@ int lr_int8_attention_prep(const void* q, const void* k, const void* v, void* wo
                            int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, lr_stream_t stream) {
     return i8_prep_impl(q, k, v, workspace, B, H, HK, Sq, Sk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn,
                         stream);
+}
+
+int lr_int8_attention_prep_rope(const void* q, const void* k, const void* v, void* workspace, int B, int H, int HK,
+                                int Sq, int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb,
+                                int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                                const void* q_norm, const void* k_norm, const void* freqs, int64_t freqs_row_stride,
+                                int rot_dim, float eps, lr_stream_t stream) {
+    // Kitchen.rmsRope's arguments (lr_rms_rope_qk_bf16): bf16 weights, bf16 [rot/2][2][2] table rows (16-byte
+    // aligned: a lane reads its eight pairs as four 16-byte loads), split-half pairs within 16-lane groups
+    if (rot_dim == 0) rot_dim = lr::D;
+    if (D != 128 || Sq != Sk || rot_dim < 16 || rot_dim > 128 || rot_dim % 16) return ERR_ARGS;
+    if (!q_norm || !k_norm || !aligned(q_norm, 16) || !aligned(k_norm, 16) || !(eps >= 0.0f) || !isfinite(eps))
+        return ERR_ARGS;
+    if (!freqs || !aligned(freqs, 16) || freqs_row_stride % 8 || freqs_row_stride < 2 * (int64_t)rot_dim)
+        return ERR_ARGS;
+    return i8_prep_impl(q, k, v, workspace, B, H, HK, Sq, Sk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn,
+                        reinterpret_cast<hipStream_t>(stream), freqs, freqs_row_stride, q_norm, k_norm, rot_dim, eps);
 }
 
 int lr_int8_attention_kernel(void* out, const void* workspace, int B, int H, int HK, int Sq, int Sk, int D,

@@ -39,6 +39,50 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// The normalised value of H3's RMSNorm as the CPU restatement computes it -- fl32(fl64(fl64(x * rr) * w)), then
+// rounded to bf16 (RNE) -- for a bf16 value x, a bf16 weight w and the row's factor rr in double. It is computed in
+// fp32, y = (x * fl32(rr)) * w, which lies within 3.5 fp32 ulps of that fl32 value (three fp32 roundings against
+// double ones). Unless y's low 16 bits lie within 8 ulps of a bf16 rounding tie (0x8000), both therefore round to the
+// same bf16 value; near a tie (about 2^-12 of the values) the double computation itself decides, with an opaque step
+// that keeps its two roundings (double -> fp32 -> bf16) from being folded into one double -> bf16 conversion.
+// norm_bf16_exact8: the same for a lane's 8 values, with one (rarely taken) branch for the whole wave.
+__device__ __forceinline__ float norm_bf16_slow(float x, double rr, float w) {
+    // (the conversions are opaque so that the compiler computes them here, in the rare branch, and does not hoist
+    // double copies of every x and w out of it)
+    double xd, wd;
+    asm volatile("v_cvt_f64_f32 %0, %1" : "=v"(xd) : "v"(x));
+    asm volatile("v_cvt_f64_f32 %0, %1" : "=v"(wd) : "v"(w));
+    float f = (float)(xd * rr * wd);
+    asm volatile("" : "+v"(f));
+    return (float)(bf16)f;
+}
+__device__ __forceinline__ bool near_bf16_tie(float y) { return (__float_as_uint(y) & 0xffffu) - (0x8000u - 8u) <= 16u; }
+__device__ __forceinline__ float norm_bf16_exact(float x, double rr, float rr32, float w) {
+    const float y = x * rr32 * w;
+    return near_bf16_tie(y) ? norm_bf16_slow(x, rr, w) : (float)(bf16)y;
+}
+__device__ __forceinline__ void norm_bf16_exact8(float (&x)[8], double rr, const float (&w)[8]) {
+    const float rr32 = (float)rr;
+    float y[8];
+    bool near = false;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        y[c] = x[c] * rr32 * w[c];
+        near |= near_bf16_tie(y[c]);
+    }
+    if (__builtin_amdgcn_ballot_w64(near)) {
+        // one value at a time: the double temporaries of eight would raise the register count of every caller
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            __builtin_amdgcn_sched_barrier(0);
+            y[c] = near_bf16_tie(y[c]) ? norm_bf16_slow(x[c], rr, w[c]) : y[c];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) x[c] = (float)(bf16)y[c];
+}
+
 // Rotation coefficients of pair p at table row `row`: y_a = f00 x_a + f01 x_b, y_b = f10 x_a + f11 x_b.
 struct Rot2 {
     float f00, f01, f10, f11;

@@ -95,6 +95,17 @@ struct PrepArgs {
     int B, H, HK, Sq, Sk;
     uint8_t* ws;
     Plan p;
+    // Kitchen.rmsRope fused into the prep (lr_int8_attention_prep_rope; rope_tab null: off). Every q and k row is
+    // first normalised and rotated as the standalone pass stores it -- bf16 weights qw / kw [D], split-half pairs
+    // (i, i + rope_rot / 2) from the bf16 table rope_tab [tokens][rope_rot / 2][2][2] (row stride tab_rs elements;
+    // token n of any batch and head uses row n), the normalised value rounded to bf16 before the rotation -- and the
+    // result is rounded to bf16 and quantised without being written back. Head dim 128, Sq == Sk.
+    const uint16_t* rope_tab;
+    int64_t tab_rs;
+    const uint16_t* qw;
+    const uint16_t* kw;
+    int rope_rot;
+    float rope_eps;
 };
 
 struct AttnArgs {

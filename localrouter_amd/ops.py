@@ -386,6 +386,32 @@ def int8_attention_prep(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return workspace
 
 
+def int8_attention_prep_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm: torch.Tensor,
+                             k_norm: torch.Tensor, freqs: torch.Tensor, *, rot: int = 96, eps: float = 1e-6,
+                             workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Kitchen.rmsRope fused into the prep (lr_int8_attention_prep_rope): the workspace int8_attention_prep would
+    write after rms_rope_qk(q, k, ...) in place, with q and k left unmodified. q_norm / k_norm bf16 [128], freqs bf16
+    [S, >= 2 * rot] ([rot/2][2][2] per row); head dim 128, Sq == Sk."""
+    B, H, Sq, d = q.shape
+    HK, Sk = k.shape[1], k.shape[2]
+    qs, ks, vs = _bhsd(q, "q"), _bhsd(k, "k"), _bhsd(v, "v")
+    for t, nm in ((q_norm, "q_norm"), (k_norm, "k_norm"), (freqs, "freqs")):
+        if not t.is_cuda or t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError(f"{nm}: expected bf16 on the GPU with unit last stride")
+    workspace = _workspace(workspace, int8_workspace_bytes(H, Sq, sk=Sk, kv_heads=HK, batch=B, head_dim=d), q.device)
+    _lib.call("lr_int8_attention_prep_rope", _ptr(q), _ptr(k), _ptr(v), _ptr(workspace), B, H, HK, Sq, Sk, d, *qs,
+              *ks, *vs, _ptr(q_norm), _ptr(k_norm), _ptr(freqs), freqs.stride(0), rot, eps, _stream())
+    return workspace
+
+
+def kitchen_attention_prep_rope(qkv: torch.Tensor, workspace: torch.Tensor | None, heads: int, freqs: torch.Tensor,
+                                q_norm: torch.Tensor, k_norm: torch.Tensor, rot: int = 96,
+                                eps: float = 1e-6) -> torch.Tensor:
+    """Kitchen.rmsRope + Kitchen.attentionPrep on one packed qkv buffer, as one prep (qkv is not modified)."""
+    q, k, v = qkv_views(qkv, heads)
+    return int8_attention_prep_rope(q, k, v, q_norm, k_norm, freqs, rot=rot, eps=eps, workspace=workspace)
+
+
 def int8_attention_kernel(workspace: torch.Tensor, out: torch.Tensor, *, batch: int, heads: int, kv_heads: int,
                           sq: int, sk: int, scale: float | None = None, rows: bool = False,
                           head_dim: int = D) -> torch.Tensor:

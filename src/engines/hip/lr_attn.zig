@@ -19,7 +19,7 @@ const std = @import("std");
 pub const Stream = ?*anyopaque;
 
 pub const HEAD_DIM = 128;
-pub const ABI_VERSION: c_int = 7;
+pub const ABI_VERSION: c_int = 8;
 
 pub const TABLE_NONE: c_int = 0;
 pub const TABLE_COSSIN_F32: c_int = 1;
@@ -104,6 +104,10 @@ pub extern "lr_attn" fn lr_int8_attention_prep(q: u64, k: u64, v: u64, ws: u64, 
     v_sn: i64, s: Stream) c_int;
 pub extern "lr_attn" fn lr_int8_attention_kernel(out: u64, ws: u64, b: c_int, h: c_int, hk: c_int, sq: c_int, sk: c_int,
     d: c_int, scale: f32, o_rows: c_int, s: Stream) c_int;
+pub extern "lr_attn" fn lr_int8_attention_prep_rope(q: u64, k: u64, v: u64, ws: u64, b: c_int, h: c_int, hk: c_int,
+    sq: c_int, sk: c_int, d: c_int, q_sb: i64, q_sh: i64, q_sn: i64, k_sb: i64, k_sh: i64, k_sn: i64, v_sb: i64,
+    v_sh: i64, v_sn: i64, q_norm: u64, k_norm: u64, freqs: u64, freqs_row_stride: i64, rot_dim: c_int, eps: f32,
+    s: Stream) c_int;
 
 // ---------------------------------------------------------------------------------------------- include/lr_rope.h
 pub extern "lr_attn" fn lr_rope_sincos(x: [*]const f64, n: i64, sin_out: [*]f64, cos_out: [*]f64) c_int;
@@ -209,6 +213,19 @@ pub fn int8Prep(s: Stream, qkv: u64, ws: u64, heads: u32, seq: u32) Error!void {
     const h2: u64 = @as(u64, heads) * HEAD_DIM * 2;
     try check(lr_int8_attention_prep(qkv, qkv + h2, qkv + 2 * h2, ws, 1, @intCast(heads), @intCast(heads),
         @intCast(seq), @intCast(seq), HEAD_DIM, sb, HEAD_DIM, row, sb, HEAD_DIM, row, sb, HEAD_DIM, row, s));
+}
+
+/// Kitchen.rmsRope + Kitchen.attentionPrep as one launch pair on one packed qkv buffer (dit.zig:665-668): q and k are
+/// normalised and rotated while they are quantised, and left unmodified in qkv; the workspace holds the same bits as
+/// after rmsRope (in place) then attentionPrep.
+pub fn int8PrepRope(s: Stream, qkv: u64, ws: u64, freqs: u64, qw: u64, kw: u64, heads: u32, seq: u32, rot: u32,
+    eps: f32) Error!void {
+    const row: i64 = 3 * @as(i64, heads) * HEAD_DIM;
+    const sb: i64 = @as(i64, seq) * row;
+    const h2: u64 = @as(u64, heads) * HEAD_DIM * 2;
+    try check(lr_int8_attention_prep_rope(qkv, qkv + h2, qkv + 2 * h2, ws, 1, @intCast(heads), @intCast(heads),
+        @intCast(seq), @intCast(seq), HEAD_DIM, sb, HEAD_DIM, row, sb, HEAD_DIM, row, sb, HEAD_DIM, row, qw, kw, freqs,
+        @as(i64, rot) * 2, @intCast(rot), eps, s));
 }
 
 /// Kitchen.attentionKernel: out [heads, seq, 128], or rows [seq, heads 128] when `rows`.

@@ -222,7 +222,8 @@ def test_rms_rope(kind, pairing, rot, round_norm):
 
 def test_rms_rope_qk_h3_in_place():
     """Kitchen.rmsRope semantics: q and k of a packed qkv, in place, bf16 weights, bf16 [S,48,2,2] table, rot 96, the
-    normalised value rounded to bf16 before the rotation: within 1 bf16 ulp of the oracle's rounding mode."""
+    normalised value rounded to bf16 before the rotation: the oracle's rounding mode bit for bit (the norm in double,
+    the rotation's products exact), and farther from the other mode."""
     print("\n[rms_rope_qk] H3 packed in place", flush=True)
     from localrouter_amd import rope
     pos = rope.h3_positions(10, 2, 8, 10, 15)
@@ -241,6 +242,7 @@ def test_rms_rope_qk_h3_in_place():
                               rot=96, eps=1e-5, round_norm=True)
         u = bf16_ulps(np.ascontiguousarray(got[:, part]), ref)
         assert u.max() <= 1.0, f"part {part}: {u.max():.2f} ulp"
+        assert np.array_equal(got[:, part], oracle.f32_to_bf16(ref)), f"part {part}: not the oracle's bits"
     assert np.array_equal(got[:, 2], qkv[:, 2]), "V must be untouched"
 
 
