@@ -166,18 +166,24 @@ def cpu_baseline(q_bits, k_bits, v_bits, cos, sin, Sq, H, flops_per_row, n_pre=0
 
 
 def preroll(call, seconds: float):
-    """Back-to-back calls for `seconds` of wall time (synchronised every 50 calls), so that the timed region starts on a
-    GPU already at its working clock. Returns (calls made, seconds spent)."""
+    """Back-to-back calls for `seconds` of wall time, so that the timed region starts on a GPU already at its working
+    clock (synchronised every batch of calls: about 50 ms of work, at least one call). Returns (calls made, seconds
+    spent); seconds 0 makes no call."""
     import torch
-    t0, calls = time.perf_counter(), 0
+    if seconds <= 0:
+        return 0, 0.0
+    t0, calls, batch = time.perf_counter(), 0, 1
     while True:
-        for _ in range(50):
+        t1 = time.perf_counter()
+        for _ in range(batch):
             call()
-        calls += 50
+        calls += batch
         torch.cuda.synchronize()
-        spent = time.perf_counter() - t0
-        if spent >= seconds:
-            return calls, spent
+        now = time.perf_counter()
+        if now - t0 >= seconds:
+            return calls, now - t0
+        per = (now - t1) / batch
+        batch = max(1, min(200, int(0.05 / max(per, 1e-6))))
 
 
 def main():
