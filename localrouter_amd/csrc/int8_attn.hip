@@ -38,6 +38,30 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 constexpr float S_U8_OFFSET = 7.9943534f;  // log2(255): the tile's largest P becomes 255 (attn_utils.cuh:41)
 
+// ------------------------------------------------------------------------------------------------ direct loads
+#define LR_I8_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+
+// One 16-byte-per-lane direct load, global -> LDS: lane l reads 16 bytes at base + voff and they land at LDS byte
+// address lds + 16 * l. base and lds are wave-uniform (SGPRs); only the 32-bit offset is per lane.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+    // readfirstlane returns a signed int: widen through uint32_t, or the low half would be sign-extended into the
+    // high half of the address
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    // M0 named as clobbered: the compiler keeps no value of its own in it across the statement (the pragmas only
+    // silence clang's warning that M0 is a reserved register)
+    _Pragma("clang diagnostic push") _Pragma("clang diagnostic ignored \"-Winline-asm\"")
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+    _Pragma("clang diagnostic pop")
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
 // ------------------------------------------------------------------------------------------------ prep helpers
 // Exchange with lane ^ M. M < 16: inside each row of 16 lanes by DPP (a register move across lanes, no LDS round
 // trip): quad_perm [1,0,3,2] / [2,3,0,1] for M = 1 / 2; for M = 4 / 8 the lanes with bit M clear take row_shl:M (lane
@@ -102,13 +126,21 @@ __device__ __forceinline__ int rn_sat(float x) {
 // 2L + 1: the sign flip and the H4 act on each 4-channel half, the butterfly over lane bit 1 pairs the two halves in
 // registers, and those over lane bits 2 .. 16 (2 .. 8) are butterflies over L's bits 1 .. 8 (1 .. 4). Every value
 // sees the same operations in the same order as in the reference, so the results are the same bits.
+// (M = 4, 8: the lanes with bit M clear add lane i + M's value, the others subtract from lane i - M's: the shifted
+// operand read straight into the add / subtract, v_add_f32_dpp / v_sub_f32_dpp, then one select)
 template <int M>
 __device__ __forceinline__ void butterfly8(float (&x)[8], int L) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        const float o = xor_lane<M>(x[c]);
-        x[c] = (L & M) ? o - x[c] : x[c] + o;
+        if constexpr (M == 4 || M == 8) {
+            const float up = __int_as_float(dpp_mov<0x100 + M>(__float_as_int(x[c])));
+            const float dn = __int_as_float(dpp_mov<0x110 + M>(__float_as_int(x[c])));
+            x[c] = (L & M) ? dn - x[c] : x[c] + up;
+        } else {
+            const float o = xor_lane<M>(x[c]);
+            x[c] = (L & M) ? o - x[c] : x[c] + o;
+        }
     }
 }
 
@@ -200,20 +232,24 @@ __device__ __forceinline__ RopeTab rope_tab_load(const PrepArgs& a, int token, i
     return t;
 }
 
-// The table rows of a block's 64 rows staged in LDS (rows of TAB_LDS_STRIDE bytes, the table row's first 4 rot bytes:
-// [rot/2 pairs][2][2] bf16), loaded once per block with coalesced 16-byte loads instead of per lane and row. The pad
-// of 16 bytes a row puts the four row groups of a wave on different banks.
-constexpr int TAB_LDS_STRIDE = 4 * 128 + 16;
-constexpr int TAB_LDS_BYTES = 64 * TAB_LDS_STRIDE;
+// The table rows of a block's 64 rows staged in LDS, row r at byte 4 rot r (the table row's first 4 rot bytes:
+// [rot/2 pairs][2][2] bf16), moved by direct global -> LDS loads: rot / 4 loads of 1 KB (64 lanes x 16 bytes), spread
+// over the block's four waves and issued before the block's own row loads, so that one wait covers both. Rows
+// row_of(r) never precede row_of(0) and lie within 64 rows of it: the per-lane byte offsets from row row_of(0) fit in
+// 32 bits (tab_rs <= 2^24, checked by the caller).
+__host__ __device__ constexpr int tab_lds_bytes(int rot) { return 64 * 4 * rot; }
 
-// Stage table rows row_of(r), r < 64, into lds; the caller synchronises the block before reading them.
+// Issue the loads of table rows row_of(r), r < 64, into lds; the caller waits (vmcnt 0) and synchronises the block
+// before reading them.
 template <typename RowOf>
-__device__ __forceinline__ void rope_tab_stage(const PrepArgs& a, uint8_t* lds, RowOf row_of) {
-    const int nch = a.rope_rot >> 2;   // 16-byte chunks of a row's 4 rot bytes
-    for (int idx = threadIdx.x; idx < 64 * nch; idx += 256) {
-        const int r = idx / nch, c = idx - r * nch;
-        *reinterpret_cast<u32x4*>(lds + r * TAB_LDS_STRIDE + 16 * c) =
-            *reinterpret_cast<const u32x4*>(a.rope_tab + (int64_t)row_of(r) * a.tab_rs + 8 * c);
+__device__ __forceinline__ void rope_tab_dma(const PrepArgs& a, uint8_t* lds, RowOf row_of) {
+    const int nch = a.rope_rot >> 2;   // 16-byte chunks a row
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int r0 = row_of(0);
+    const uint16_t* base = a.rope_tab + (int64_t)r0 * a.tab_rs;
+    for (int i = wave; i < nch; i += 4) {   // load i: chunks 64 i .. 64 i + 63 of the staged rows
+        const int idx = 64 * i + l, r = idx / nch, c = idx - r * nch;
+        dma16(base, (uint32_t)(((int64_t)(row_of(r) - r0) * a.tab_rs + 8 * c) * 2), lds_addr(lds + 1024 * i));
     }
 }
 
@@ -222,7 +258,7 @@ __device__ __forceinline__ RopeTab rope_tab_lds(const uint8_t* lds, int r, int L
     RopeTab t;
     const int hc = rot >> 4;
     const int pc = L < hc ? L : (L < 2 * hc ? L - hc : 0);
-    const uint8_t* src = lds + r * TAB_LDS_STRIDE + 64 * pc + (L >= hc && L < 2 * hc ? 4 : 0);
+    const uint8_t* src = lds + r * 4 * rot + 64 * pc + (L >= hc && L < 2 * hc ? 4 : 0);
 #pragma unroll
     for (int j = 0; j < 8; ++j) t.w[j] = *reinterpret_cast<const uint32_t*>(src + 8 * j);
     return t;
@@ -372,11 +408,14 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
         }
         __syncthreads();
     }
-    if (t == 0) {
-        const bool improves = sd[0][0] < orig_e && sd[1][0] <= orig_m * 1.125;
+    const bool improves = sd[0][0] < orig_e && sd[1][0] <= orig_m * 1.125;
+    if (t == 0)
         reinterpret_cast<int*>(a.ws + p.anchor)[b * a.HK + hk] =
             improves ? (int)((int64_t)best * (a.Sk - 1) / (NSAMP - 1)) : -1;
-    }
+    // the anchor row as quant_k subtracts it (a bf16 value, exact in the double sample), zeros when there is none
+    if (t < D)
+        reinterpret_cast<uint16_t*>(a.ws + p.arow)[(size_t)(b * a.HK + hk) * D + t] =
+            improves ? (uint16_t)(__float_as_uint((float)s[best]) >> 16) : (uint16_t)0;
 }
 
 // ------------------------------------------------------------------------------------------------ prep launch 2
@@ -384,43 +423,43 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
 constexpr int QROWS = 64;  // query rows per block
 constexpr int KROWS = 64;  // key rows per block: four scale groups of 16, one per wave
 
-// Q: QROWS rows of head h per block, 256 / LPR per pass, one scale per row.
+// The 8 bf16 values of a lane's 16-byte row piece as floats
+__device__ __forceinline__ void unpack8(const u32x4& w, float (&x)[8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[2 * j] = lo_bf16(w[j]);
+        x[2 * j + 1] = hi_bf16(w[j]);
+    }
+}
+
+// Q: QROWS rows of head h per block, 256 / LPR per pass, one scale per row. Every row of the lane is in flight before
+// the first is used (kept as bf16 until then); rows past Sq read row Sq - 1 and are zeroed.
 template <int ROT, int HD, bool ROPE>
 __device__ void quant_q(const PrepArgs& a, int b, int h, int qb, uint8_t* lds) {
 #pragma clang fp contract(off)
-    constexpr int LPR = HD / 8, RPB = 256 / LPR;  // lanes a row, rows a block pass
+    constexpr int LPR = HD / 8, RPB = 256 / LPR, NR = QROWS / RPB;  // lanes a row, rows a block pass, rows a lane
     const Plan& p = a.p;
     const int t = threadIdx.x, slot = t / LPR, L = t % LPR;
-    float xs[QROWS / RPB][8];  // every row of the lane loaded before the first rotation: all loads in flight at once
+    const uint16_t* qbase = a.q + b * a.q_sb + h * a.q_sh + 8 * L;
+    if constexpr (ROPE) rope_tab_dma(a, lds, [&](int r) { return min(qb * QROWS + r, a.Sq - 1); });
+    u32x4 raw[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+        raw[i] = *reinterpret_cast<const u32x4*>(qbase + (int64_t)min(qb * QROWS + RPB * i + slot, a.Sq - 1) * a.q_sn);
     float wv[8];
-    if constexpr (ROPE) rope_tab_stage(a, lds, [&](int r) { return min(qb * QROWS + r, a.Sq - 1); });
-#pragma unroll
-    for (int i = 0; i < QROWS / RPB; ++i) {
-        const int row = qb * QROWS + RPB * i + slot;
-        if constexpr (ROPE) {   // no branch around the loads: rows past Sq read the last row, then zeroed
-            load8(a.q + b * a.q_sb + h * a.q_sh + (int64_t)min(row, a.Sq - 1) * a.q_sn + 8 * L, xs[i]);
-        } else {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) xs[i][c] = 0.0f;
-            if (row < a.Sq) load8(a.q + b * a.q_sb + h * a.q_sh + (int64_t)row * a.q_sn + 8 * L, xs[i]);
-        }
-    }
-    if constexpr (ROPE) {
-#pragma unroll
-        for (int i = 0; i < QROWS / RPB; ++i)
-            if (qb * QROWS + RPB * i + slot >= a.Sq)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) xs[i][c] = 0.0f;
-    }
     if constexpr (ROPE) {
         rope_w_load(a.qw, L, wv);
-        __syncthreads();   // the staged table rows
+        LR_I8_WAIT_VMCNT(0);   // the table rows (and the lane's own loads)
+        __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < QROWS / RPB; ++i) {
+    for (int i = 0; i < NR; ++i) {
         const int row = qb * QROWS + RPB * i + slot;
         const bool ok = row < a.Sq;
-        float (&x)[8] = xs[i];
+        float x[8];
+        unpack8(raw[i], x);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) x[c] = ok ? x[c] : 0.0f;
         if constexpr (ROPE) h3_rms_rope(x, L, wv, rope_tab_lds(lds, RPB * i + slot, L, a.rope_rot), a.rope_rot, a.rope_eps);
         rotate8<ROT>(x, L);
         float m = 0.0f;
@@ -437,66 +476,75 @@ __device__ void quant_q(const PrepArgs& a, int b, int h, int qb, uint8_t* lds) {
     }
 }
 
-// K: KROWS key rows of kv head hk per block; wave w holds scale group 4 kb + w (16 rows, 64 / LPR a pass), the anchor
-// row subtracted before the rotation.
+// K: KROWS key rows of kv head hk per block, 256 / LPR rows a pass (row RPB pass + t / LPR), four scale groups of 16
+// rows; each wave's rows of a pass lie in one group, a group spans WPG waves. The anchor row (written by the stats
+// launch: zeros when there is none) is subtracted before the rotation. The passes run two at a time: the lane keeps
+// two rotated rows while the group maxima are combined across waves through LDS.
 template <int ROT, int HD, bool ROPE>
 __device__ void quant_k(const PrepArgs& a, int b, int hk, int kb, uint8_t* lds) {
 #pragma clang fp contract(off)
-    constexpr int LPR = HD / 8, RPW = 64 / LPR, NP = KGROUP / RPW;  // lanes a row, rows a wave pass, passes
+    constexpr int LPR = HD / 8, RPW = 64 / LPR, RPB = 256 / LPR;  // lanes a row, rows a wave, rows a block pass
+    constexpr int NPASS = KROWS / RPB, WPG = KGROUP / RPW;        // passes (4 or 2), waves a group (4 or 2)
+    static_assert(NPASS % 2 == 0 && KGROUP % RPW == 0, "passes run in pairs; a wave's rows lie in one group");
+    __shared__ float gmax[KROWS / KGROUP][4];   // [group][wave within the group]
     const Plan& p = a.p;
-    const int t = threadIdx.x, wave = t >> 6, rsub = (t & 63) / LPR, L = t % LPR;
-    const int grp = kb * (KROWS / KGROUP) + wave;  // keys 16 grp .. + 15
-    const int anc = reinterpret_cast<const int*>(a.ws + p.anchor)[b * a.HK + hk];
+    const int t = threadIdx.x, wave = t >> 6, prow = t / LPR, L = t % LPR;
     const uint16_t* kbase = a.k + b * a.k_sb + hk * a.k_sh + 8 * L;
-    float av[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    float wv[8];
-    if constexpr (ROPE) rope_w_load(a.kw, L, wv);
-    if (anc >= 0) {
-        load8(kbase + (int64_t)anc * a.k_sn, av);
-        if constexpr (ROPE) h3_rms_rope(av, L, wv, rope_tab_load(a, anc, L), a.rope_rot, a.rope_eps);
-    }
     // Rows past Sk (the last tile's padding) repeat real keys: those of the last key's scale group gL, key Sk - 1
     // standing in past its end. A padded row of group gL then equals key Sk - 1 and leaves the group's scale as it
     // is; a wholly padded group is a copy of group gL, scale included. Their scores equal real scores, so they never
     // raise a row max; the attention zeroes their P.
     const int last = a.Sk - 1, gl = last / KGROUP;
     auto src_of = [&](int row) { return row <= last ? row : min(gl * KGROUP + (row & (KGROUP - 1)), last); };
-    if constexpr (ROPE) rope_tab_stage(a, lds, [&](int r) { return src_of(kb * KROWS + r); });
-    float x[NP][8];
+    if constexpr (ROPE) rope_tab_dma(a, lds, [&](int r) { return src_of(kb * KROWS + r); });
+    u32x4 raw[NPASS];
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {  // all the lane's rows in flight before the first rotation
-        const int row = grp * KGROUP + RPW * i + rsub;
-        load8(kbase + (int64_t)src_of(row) * a.k_sn, x[i]);
+    for (int i = 0; i < NPASS; ++i)  // all the lane's rows in flight before the first is used
+        raw[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)src_of(kb * KROWS + RPB * i + prow) * a.k_sn);
+    float av[8], wv[8];
+    load8(reinterpret_cast<const uint16_t*>(a.ws + p.arow) + (size_t)(b * a.HK + hk) * HD + 8 * L, av);
+    if constexpr (ROPE) {
+        rope_w_load(a.kw, L, wv);
+        LR_I8_WAIT_VMCNT(0);   // the table rows (and the lane's own loads)
+        __syncthreads();
     }
-    if constexpr (ROPE) __syncthreads();   // the staged table rows
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        if constexpr (ROPE)
-            h3_rms_rope(x[i], L, wv, rope_tab_lds(lds, wave * KGROUP + RPW * i + rsub, L, a.rope_rot), a.rope_rot,
-                        a.rope_eps);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) x[i][c] = x[i][c] - av[c];
-        rotate8<ROT>(x[i], L);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) m = fmaxf(m, fabsf(x[i][c]));
-    }
-    const float mx = max64(m);
-    const float sc = mx / 127.0f + 1e-7f;
-    const float inv = 1.0f / sc;
     uint8_t* k8 = a.ws + p.k8 + (size_t)(b * a.HK + hk) * p.skp * HD;
+    float* aux_ks = reinterpret_cast<float*>(a.ws + p.aux + (size_t)(b * a.HK + hk) * p.ntiles * AUX_BYTES + AUX_KS_OFF);
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int row = grp * KGROUP + RPW * i + rsub;
-        *reinterpret_cast<u32x2*>(k8 + (size_t)row * HD + 16 * ((L >> 1) ^ k_swz(row & 31, HD)) + 8 * (L & 1)) =
-            pack_s8x8(x[i], inv);
-    }
-    if ((t & 63) == 0) {
-        const int tile = grp * KGROUP / p.cta, local = grp * KGROUP - tile * p.cta;
-        const int blk = local >> 5, half = (local >> 4) & 1;
-        float* ks = reinterpret_cast<float*>(a.ws + p.aux + ((size_t)(b * a.HK + hk) * p.ntiles + tile) * AUX_BYTES +
-                                             AUX_KS_OFF);
-        ks[half * (p.cta / 32) + blk] = sc;
+    for (int ph = 0; ph < NPASS; ph += 2) {
+        float x[2][8];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int lr = RPB * (ph + j) + prow;   // row within the block
+            unpack8(raw[ph + j], x[j]);
+            if constexpr (ROPE) h3_rms_rope(x[j], L, wv, rope_tab_lds(lds, lr, L, a.rope_rot), a.rope_rot, a.rope_eps);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) x[j][c] = x[j][c] - av[c];
+            rotate8<ROT>(x[j], L);
+            float m = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) m = fmaxf(m, fabsf(x[j][c]));
+            m = max64(m);
+            if ((t & 63) == 0) gmax[lr / KGROUP][wave % WPG] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int lr = RPB * (ph + j) + prow, g = lr / KGROUP;
+            float mx = gmax[g][0];
+#pragma unroll
+            for (int w = 1; w < WPG; ++w) mx = fmaxf(mx, gmax[g][w]);
+            const float sc = mx / 127.0f + 1e-7f;
+            const float inv = 1.0f / sc;
+            const int row = kb * KROWS + lr;
+            *reinterpret_cast<u32x2*>(k8 + (size_t)row * HD + 16 * ((L >> 1) ^ k_swz(row & 31, HD)) + 8 * (L & 1)) =
+                pack_s8x8(x[j], inv);
+            if (t % (64 * WPG) == 0) {   // the group's first wave, lane 0
+                const int grp = kb * (KROWS / KGROUP) + g;
+                const int tile = grp * KGROUP / p.cta, local = grp * KGROUP - tile * p.cta;
+                aux_ks[(size_t)tile * (AUX_BYTES / 4) + ((local >> 4) & 1) * (p.cta / 32) + (local >> 5)] = sc;
+            }
+        }
     }
 }
 
@@ -571,11 +619,17 @@ __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile, uint8_t* ext
     }
 }
 
-// grid (ceil(Sq / QROWS) + skp / KROWS + ntiles, max(H, HK), B): Q blocks, then K blocks, then V tiles.
+// Dynamic LDS of the fused-rmsRope instantiations: the staged table rows (Q and K blocks) or quant_v's arrays (V).
+inline size_t quant_lds_bytes(int rot) {
+    const size_t t = tab_lds_bytes(rot), v = VTS_BYTES + 4 * 128;
+    return t > v ? t : v;
+}
+
+// grid (ceil(Sq / QROWS) + skp / KROWS + ntiles, max(H, HK), B): Q blocks, then K blocks, then V tiles. The
+// fused-rmsRope instantiations run with quant_lds_bytes(rope_rot) bytes of dynamic LDS.
 template <int ROT, int HD, bool ROPE = false>
 __global__ __launch_bounds__(256) void i8_quant_kernel(PrepArgs a) {
-    static_assert(!ROPE || TAB_LDS_BYTES >= VTS_BYTES + 4 * 128, "the shared buffer holds quant_v's arrays");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[ROPE ? TAB_LDS_BYTES : 1];
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int b = blockIdx.z, y = blockIdx.y;
     const int nqb = (a.Sq + QROWS - 1) / QROWS, nkb = a.p.skp / KROWS;
     int x = blockIdx.x;
@@ -593,29 +647,6 @@ __global__ __launch_bounds__(256) void i8_quant_kernel(PrepArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ attention
-#define LR_I8_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
-
-// One 16-byte-per-lane direct load, global -> LDS: lane l reads 16 bytes at base + voff and they land at LDS byte
-// address lds + 16 * l. base and lds are wave-uniform (SGPRs); only the 32-bit offset is per lane.
-__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
-    // readfirstlane returns a signed int: widen through uint32_t, or the low half would be sign-extended into the
-    // high half of the address
-    const uint64_t b = (uint64_t)(uintptr_t)base;
-    const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
-                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-    // M0 named as clobbered: the compiler keeps no value of its own in it across the statement (the pragmas only
-    // silence clang's warning that M0 is a reserved register)
-    _Pragma("clang diagnostic push") _Pragma("clang diagnostic ignored \"-Winline-asm\"")
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
-                 "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory", "m0");
-    _Pragma("clang diagnostic pop")
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
 // A workgroup barrier that neither waits for outstanding memory operations nor lets the compiler move any
 // instruction across it (the waits that matter are issued explicitly; the clusters on either side stay apart).
 __device__ __forceinline__ void block_barrier() {
@@ -996,8 +1027,9 @@ hipError_t launch_prep(const PrepArgs& a, hipStream_t stream) {
     const dim3 grid((a.Sq + QROWS - 1) / QROWS + p.skp / KROWS + p.ntiles, a.H > a.HK ? a.H : a.HK, a.B);
     if (a.rope_tab) {   // the fused rmsRope: head dim 128 only (checked by the caller)
         if (p.d != 128) return hipErrorInvalidValue;
-        if (p.rot == 4) hipLaunchKernelGGL((i8_quant_kernel<4, 128, true>), grid, dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((i8_quant_kernel<128, 128, true>), grid, dim3(256), 0, stream, a);
+        const size_t lds = quant_lds_bytes(a.rope_rot);
+        if (p.rot == 4) hipLaunchKernelGGL((i8_quant_kernel<4, 128, true>), grid, dim3(256), lds, stream, a);
+        else hipLaunchKernelGGL((i8_quant_kernel<128, 128, true>), grid, dim3(256), lds, stream, a);
     } else if (p.d == 128) {
         if (p.rot == 4) hipLaunchKernelGGL((i8_quant_kernel<4, 128>), grid, dim3(256), 0, stream, a);
         else hipLaunchKernelGGL((i8_quant_kernel<128, 128>), grid, dim3(256), 0, stream, a);

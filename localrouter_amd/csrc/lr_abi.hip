@@ -725,7 +725,9 @@ int lr_int8_attention_prep_rope(const void* q, const void* k, const void* v, voi
     if (D != 128 || Sq != Sk || rot_dim < 16 || rot_dim > 128 || rot_dim % 16) return ERR_ARGS;
     if (!q_norm || !k_norm || !aligned(q_norm, 16) || !aligned(k_norm, 16) || !(eps >= 0.0f) || !isfinite(eps))
         return ERR_ARGS;
-    if (!freqs || !aligned(freqs, 16) || freqs_row_stride % 8 || freqs_row_stride < 2 * (int64_t)rot_dim)
+    // (the prep stages a block's 64 table rows by 32-bit offsets from its first row: a row stride up to 2^24)
+    if (!freqs || !aligned(freqs, 16) || freqs_row_stride % 8 || freqs_row_stride < 2 * (int64_t)rot_dim ||
+        freqs_row_stride > (int64_t)1 << 24)
         return ERR_ARGS;
     return i8_prep_impl(q, k, v, workspace, B, H, HK, Sq, Sk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn,
                         reinterpret_cast<hipStream_t>(stream), freqs, freqs_row_stride, q_norm, k_norm, rot_dim, eps);

@@ -19,6 +19,8 @@
 //   vs     fp32 [B][HK][D]                          one scale per channel
 //   vpart  fp32 [B][HK][nvchunk][D]                 per-chunk channel abs-max of V (the V scales' first pass)
 //   anchor int32 [B][HK]                            anchor key row or -1
+//   arow   bf16 [B][HK][D]                          the anchor row as the keys are shifted by it (the key row as
+//                                                   the prep sees it: raw, or normalised and rotated); zeros if none
 // Scale granularity (per query row; per 16 keys; per channel) is this library's choice. The reference's per-thread
 // groups follow its mma fragment layout (kernels/cuda/minimax/kitchen/quant_qk_int8.cu:245-247); the arithmetic
 // inside a group is the reference's.
@@ -43,7 +45,7 @@ inline int rotation_for(int Sk, int D) { return Sk <= 256 ? 4 : D; }
 
 struct Plan {
     int d, cta, ntiles, skp, nvchunk, rot;
-    size_t q8, k8, vt, aux, qs, vs, vpart, anchor, total;
+    size_t q8, k8, vt, aux, qs, vs, vpart, anchor, arow, total;
 };
 
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -71,6 +73,7 @@ inline Plan plan_of(int B, int H, int HK, int Sq, int Sk, int D) {
     p.vs = take(bhk * D * 4);
     p.vpart = take(bhk * p.nvchunk * D * 4);
     p.anchor = take(bhk * 4);
+    p.arow = take(bhk * D * 2);
     p.total = at;
     return p;
 }

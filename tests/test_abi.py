@@ -170,7 +170,7 @@ def _i8_plan(B, H, HK, Sq, Sk, d=128):
     nt = -(-Sk // cta)
     skp, nvc = nt * cta, -(-Sk // 256)
     parts = [B * H * Sq * d, B * HK * skp * d, B * HK * skp * d, B * HK * nt * 1024, B * H * Sq * 4,
-             B * HK * d * 4, B * HK * nvc * d * 4, B * HK * 4]
+             B * HK * d * 4, B * HK * nvc * d * 4, B * HK * 4, B * HK * d * 2]
     return sum(-(-p // 256) * 256 for p in parts)
 
 

@@ -42,7 +42,7 @@ def _decode(ws: np.ndarray, B, H, HK, Sq, Sk, d=128) -> dict:
     nt = -(-Sk // cta)
     skp, nvc = nt * cta, -(-Sk // 256)
     sizes = [B * H * Sq * d, B * HK * skp * d, B * HK * skp * d, B * HK * nt * 1024, B * H * Sq * 4,
-             B * HK * d * 4, B * HK * nvc * d * 4, B * HK * 4]
+             B * HK * d * 4, B * HK * nvc * d * 4, B * HK * 4, B * HK * d * 2]
     off, at = [], 0
     for s in sizes:
         off.append(at)
@@ -66,7 +66,8 @@ def _decode(ws: np.ndarray, B, H, HK, Sq, Sk, d=128) -> dict:
     ks = ks.transpose(0, 1, 2, 4, 3).reshape(B, HK, nt * 2 * nb)              # group order 2 kb + half per tile
     return dict(cta=cta, skp=skp, q8=part(0).view(np.int8).reshape(B, H, Sq, d),
                 qs=part(4).view(np.float32).reshape(B, H, Sq), k8=k8, ks=ks, v8=v8, cs=cs,
-                vs=part(5).view(np.float32).reshape(B, HK, d), anchor=part(7).view(np.int32).reshape(B, HK))
+                vs=part(5).view(np.float32).reshape(B, HK, d), anchor=part(7).view(np.int32).reshape(B, HK),
+                arow=part(8).view(np.uint16).reshape(B, HK, d))
 
 
 # ------------------------------------------------------------------------------------------ inputs and the oracle
@@ -89,12 +90,14 @@ def _oracle_head(q, k, v, Sk):
     q8, qs = oracle.i8_quant_rows(q, rot)
     k8, ks = oracle.i8_quant_rows(k, rot, a, oracle.I8_KGROUP)
     v8, vs = oracle.i8_quant_v(v)
-    return dict(anchor=a, q8=q8, qs=qs, k8=k8, ks=ks, v8=v8, vs=vs)
+    arow = np.asarray(k[a], np.uint16) if a >= 0 else np.zeros(k.shape[-1], np.uint16)
+    return dict(anchor=a, arow=arow, q8=q8, qs=qs, k8=k8, ks=ks, v8=v8, vs=vs)
 
 
 def _check_parts(dec, ref, b, h, hk, Sk, what):
     cta = dec["cta"]
     assert dec["anchor"][b, hk] == ref["anchor"], f"{what}: anchor"
+    assert np.array_equal(dec["arow"][b, hk], ref["arow"]), f"{what}: anchor row"
     assert np.array_equal(dec["q8"][b, h], ref["q8"]), f"{what}: q8"
     assert np.array_equal(dec["qs"][b, h].view(np.uint32), ref["qs"].view(np.uint32)), f"{what}: q scales"
     assert np.array_equal(dec["k8"][b, hk, :Sk], ref["k8"]), f"{what}: k8"
