@@ -71,8 +71,8 @@ typedef struct ihipStream_t* lr_stream_t;
                                       K/V ring, next tile's QK^T overlapped with the current tile's softmax */
 #define LR_ATTN_CFG_PIPE_W4 2      /* the same kernel with 128 queries per workgroup (4 waves x 32) */
 #define LR_ATTN_CFG_STREAM_W8 9    /* fused / prepared calls: one persistent workgroup per CU (8 waves x 32 queries)
-                                      streaming keys and values prepared as tile images (the LDS image of each
-                                      64-key tile, 16 KB) through 4-stage direct-to-LDS rings; softmax against a
+                                      streaming keys prepared as tile images (the LDS image of each 64-key tile,
+                                      16 KB) and value rows through 4-stage direct-to-LDS rings; softmax against a
                                       fixed reference (the block's first key tile's maximum), query rows whose sums
                                       overflowed it recomputed exactly at the end of the kernel */
 
@@ -155,19 +155,22 @@ int lr_rms_rope_qk_bf16(void* q, void* k, int64_t seq, int heads, int64_t q_row_
                         const void* q_norm, const void* k_norm, const void* freqs, int64_t freqs_row_stride,
                         int rot_dim, float eps, lr_stream_t stream);
 
-/* The part of the joint attention's workspace behind the tile images: the partial results and arrival counters of
- * query blocks cut over several workgroups (the last, partial round of blocks is spread over all CUs; at most 256
- * workgroups, two partials of 8 x 16.5 KB each, then 256 int counters). */
+/* The part of the joint attention's workspace behind the key images and value rows: the partial results and arrival
+ * counters of query blocks cut over several workgroups (the last, partial round of blocks is spread over all CUs; at
+ * most 256 workgroups, two partials of 8 x 16.5 KB each, then 256 int counters). */
 #define LR_JOINT_SPLIT_BYTES ((size_t)69207040)
 
-/* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys, then the values, each as
- * [HK][ceil(Sk/64)] tile images of 16 KB (one 64-key tile of one kv head laid out as the attention kernel's LDS holds
- * it; keys past Sk zero), then LR_JOINT_SPLIT_BYTES: 2 * HK * ceil(Sk/64) * 16384 + LR_JOINT_SPLIT_BYTES. */
+/* Bytes of workspace lr_joint_attention_fused needs: the normalised, rotated keys as [HK][ceil(Sk/64)] tile images of
+ * 16 KB (one 64-key tile of one kv head laid out as the attention kernel's LDS holds it; keys past Sk zero), then an
+ * area of the same size for value rows, bf16 [ceil(Sk/64) * 64][HK][128] (written by the stage calls
+ * lr_joint_kv_prepare / lr_joint_prepare, rows past Sk zero; the fused call reads the caller's v and leaves it
+ * unused), then LR_JOINT_SPLIT_BYTES: 2 * HK * ceil(Sk/64) * 16384 + LR_JOINT_SPLIT_BYTES. */
 size_t lr_joint_attention_workspace_bytes(int Sk, int HK);
 
 /*
- * The fused joint attention: QK-RMSNorm + RoPE + attention (keys and values prepared once into the workspace,
- * queries normalised and rotated into out's rows, which the attention kernel reads before overwriting them).
+ * The fused joint attention: QK-RMSNorm + RoPE + attention (keys prepared once into the workspace's tile images,
+ * queries normalised and rotated into out's rows, which the attention kernel reads before overwriting them; the
+ * values are read from v's rows as they are).
  *   q_raw [Sq][H][128], k_raw, v [Sk][HK][128], out [Sq][H][128] bf16 rows with the given row strides
  *   (out_row_stride <= 2^23 elements).
  *   q_norm_w, k_norm_w: fp32 [128], 16-byte aligned, or NULL (ones). eps >= 0.
@@ -189,13 +192,14 @@ int lr_joint_attention_fused(const void* q_raw, const void* k_raw, const void* v
 /*
  * The two stages of lr_joint_attention_fused as separate calls (same kernels, same results):
  *   lr_joint_kv_prepare         RMSNorm + RoPE of k_raw rows j >= n_pre (k-table row j - n_pre), rows j < n_pre
- *                               copied, and the values, into the workspace's tile images;
+ *                               copied, into the workspace's key tile images, and the values copied into its
+ *                               value rows (so that the workspace alone holds the prepared keys and values);
  *   lr_joint_attention_prepared the attention of q_raw (normalised and rotated into out's rows first) over
  *                               that workspace. config: LR_ATTN_CFG_AUTO or _STREAM_W8.
  * Useful when keys and values are reused (a cached prefix) or to time the stages separately. Several attention calls
- * may share one prepared workspace (its images are only read), one after the other: each call also uses the
- * workspace's split area (LR_JOINT_SPLIT_BYTES, left zeroed for the next call), so calls that overlap in time on one
- * workspace race.
+ * may share one prepared workspace (its key images and value rows are only read), one after the other: each call
+ * also uses the workspace's split area (LR_JOINT_SPLIT_BYTES, left zeroed for the next call), so calls that overlap
+ * in time on one workspace race.
  */
 int lr_joint_kv_prepare(const void* k_raw, int64_t k_row_stride, const void* v, int64_t v_row_stride,
                         const float* k_norm_w, int table_kind, const void* k_table_a, const void* k_table_b,
@@ -210,7 +214,7 @@ int lr_joint_attention_prepared(const void* q_raw, void* workspace, size_t works
 /*
  * The fused op's work as separate calls, in the order of the reference's chain rope_k + V copy -> rope_q -> attention
  * (dit.zig:252-293); lr_joint_attention_fused makes the first two as one launch (lr_joint_prepare, below):
- *   lr_joint_kv_prepare        (above) keys and values into the workspace's tile images;
+ *   lr_joint_kv_prepare        (above) keys into the workspace's tile images, values into its value rows;
  *   lr_joint_q_prepare         q_raw [Sq][H][128] normalised and rotated (as lr_rms_rope_bf16 with an fp32 weight,
  *                              round_norm 0), rounded once to bf16, into q_prep rows; q_prep may be q_raw itself (in
  *                              place) or out; otherwise it must not overlap q_raw;
@@ -311,7 +315,7 @@ int lr_int8_attention_kernel(void* out, const void* workspace, int B, int H, int
  *   q, k, v, workspace, strides, B, H, HK, Sq, Sk as lr_int8_attention_prep; D 128; Sq == Sk (token n of q and of k
  *   uses table row n, as in Kitchen.rmsRope over one packed qkv buffer);
  *   q_norm, k_norm, freqs, freqs_row_stride, rot_dim, eps as lr_rms_rope_qk_bf16 (rot_dim 0 = 128, else a multiple of
- *   16); the weights and the table rows 16-byte aligned (freqs_row_stride a multiple of 8 elements).
+ *   16); the weights and the table rows 16-byte aligned (freqs_row_stride a multiple of 8 elements, at most 2^24).
  */
 int lr_int8_attention_prep_rope(const void* q, const void* k, const void* v, void* workspace, int B, int H, int HK,
                                 int Sq, int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb,

@@ -36,8 +36,8 @@
 //    P = exp2(c S') with one multiply per score beside the exp. Softmax is shift-invariant: exact while P, the row
 //    sums and O stay finite, i.e. unless a later key scores ~128 above m. The epilogue checks every row; a wave with a
 //    non-finite row marks the block and, after the streaming loop, recomputes its 32 queries with the exact row
-//    maximum (a two-pass form that reads fragments straight from the images in HBM and needs no LDS), so the output
-//    never depends on the fixed reference.
+//    maximum (a two-pass form that reads key fragments and value rows straight from HBM and needs no LDS), so the
+//    output never depends on the fixed reference.
 #include "lr_common.h"
 #include "lr_kernels.h"
 #include "tile_image.h"
@@ -172,9 +172,9 @@ __device__ __forceinline__ bf16x8 frag_at(uint32_t addr) { return *(lds_frag*)(u
 
 // Recompute wave `wave`'s 32 queries of a block with the exact row maximum (the rare case of a non-finite row under the
 // fixed reference): pass 1 takes the maximum of every score, pass 2 accumulates P = exp2(S - max) <= 1, the row sums and
-// O, and the rows are written. The prepared queries are read from a.q (the block's rows, not yet overwritten), the
-// fragments straight from the tile images in HBM (a 1 KB fragment is one 16-byte load per lane): nothing here touches
-// LDS or waits for the other waves. Called after the streaming loop, so that its registers do not add to the loop's.
+// O, and the rows are written. The prepared queries are read from a.q (the block's rows, not yet overwritten), the key
+// fragments straight from the tile images in HBM (a 1 KB fragment is one 16-byte load per lane) and the value
+// fragments from the value rows (eight 2-byte loads per lane): nothing here touches LDS or waits for the other waves. Called after the streaming loop, so that its registers do not add to the loop's.
 __device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, int row0, int tiles, int wave) {
     const int lane = threadIdx.x & 63, n = lane & 31, hf = lane >> 5;
     const int wrow0 = row0 + wave * 32, qrow = wrow0 + n;

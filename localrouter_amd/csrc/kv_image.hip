@@ -39,7 +39,7 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
     const int hk = (int)(tile_id / a.tiles), t = (int)(tile_id - (int64_t)hk * a.tiles);
     const int key0 = t * IMG_TILE_KEYS;
 
-    // ---- every load first: 4 key rows (16 bytes each), the weight, the table entries, one 8x8 block of V
+    // ---- every load first: 4 key rows (16 bytes each), with copy_v the 4 value rows, the weight, the table entries
     u32x4 xin[KROWS];
 #pragma unroll
     for (int i = 0; i < KROWS; ++i) {
