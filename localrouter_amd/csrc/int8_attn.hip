@@ -64,21 +64,23 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 // ------------------------------------------------------------------------------------------------ prep helpers
 // Exchange with lane ^ M. M < 16: inside each row of 16 lanes by DPP (a register move across lanes, no LDS round
-// trip): quad_perm [1,0,3,2] / [2,3,0,1] for M = 1 / 2; for M = 4 / 8 the lanes with bit M clear take row_shl:M (lane
-// i + M), the others row_shr:M (lane i - M). M = 16: inside each 32-lane half (ds_swizzle, and 0x1f, xor 16).
+// trip): quad_perm [1,0,3,2] / [2,3,0,1] for M = 1 / 2, row_ror:8 for M = 8 (a rotation by 8 inside a 16-lane row is
+// xor 8); for M = 4 the lanes with bit 2 clear take row_shl:4 (lane i + 4), the others row_shr:4 (lane i - 4). M = 16:
+// inside each 32-lane half (ds_swizzle, and 0x1f, xor 16).
 template <int CTRL>
 __device__ __forceinline__ int dpp_mov(int x) {
     return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, true);
 }
+// the DPP control of the single-move exchanges (M = 1, 2, 8)
+template <int M>
+constexpr int xor_dpp_ctrl() { return M == 1 ? 0xb1 : M == 2 ? 0x4e : 0x128; }
 template <int M>
 __device__ __forceinline__ int xor_lane_i(int x) {
-    if constexpr (M == 1) {
-        return dpp_mov<0xb1>(x);
-    } else if constexpr (M == 2) {
-        return dpp_mov<0x4e>(x);
-    } else if constexpr (M == 4 || M == 8) {
-        const int up = dpp_mov<0x100 + M>(x), dn = dpp_mov<0x110 + M>(x);
-        return (threadIdx.x & M) ? dn : up;
+    if constexpr (M == 1 || M == 2 || M == 8) {
+        return dpp_mov<xor_dpp_ctrl<M>()>(x);
+    } else if constexpr (M == 4) {
+        const int up = dpp_mov<0x104>(x), dn = dpp_mov<0x114>(x);
+        return (threadIdx.x & 4) ? dn : up;
     } else {
         return __builtin_amdgcn_ds_swizzle(x, 0x1f | (M << 10));
     }
@@ -112,11 +114,20 @@ __device__ __forceinline__ float max64(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Round to nearest even, saturate to [-128, 127]; NaN -> 0 (float_utils.cuh:40-51).
+// Round to nearest even, saturate to [-128, 127]; NaN -> 0 (float_utils.cuh:40-51). v_cvt_i32_f32 itself turns NaN
+// into 0 and saturates out-of-range values (infinities included) to the int32 range, so after the rounding one
+// integer clamp remains (written as asm: the conversion of NaN or of an out-of-range value is undefined in C++).
 __device__ __forceinline__ int rn_sat(float x) {
-    if (x != x) return 0;
-    const float r = fminf(fmaxf(rintf(x), -128.0f), 127.0f);
-    return (int)r;
+    int i;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(rintf(x)));
+    return min(max(i, -128), 127);
+}
+
+// The low bytes of four ints as one little-endian word (v_perm_b32: byte selector 0x0c is zero)
+__device__ __forceinline__ uint32_t pack_lo_bytes(int b0, int b1, int b2, int b3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b1, (uint32_t)b0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)b3, (uint32_t)b2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 // The reference rotates a 128-channel row held as 4 channels per lane of 32 lanes (quant_qk_int8.cu:75-155):
@@ -126,20 +137,24 @@ __device__ __forceinline__ int rn_sat(float x) {
 // 2L + 1: the sign flip and the H4 act on each 4-channel half, the butterfly over lane bit 1 pairs the two halves in
 // registers, and those over lane bits 2 .. 16 (2 .. 8) are butterflies over L's bits 1 .. 8 (1 .. 4). Every value
 // sees the same operations in the same order as in the reference, so the results are the same bits.
-// (M = 4, 8: the lanes with bit M clear add lane i + M's value, the others subtract from lane i - M's: the shifted
-// operand read straight into the add / subtract, v_add_f32_dpp / v_sub_f32_dpp, then one select)
+// A butterfly gives the lane with bit M clear x + o and the other o - x (o the partner's value). For M = 1, 2, 8 the
+// partner is one DPP move away, so it is o + (+-x): this lane's value with its sign flipped where bit M is set (exactly
+// o - x in IEEE arithmetic), and the partner's value read straight into the add (v_add_f32_dpp): two instructions a
+// value. For M = 4 the two directions are separate shifts: x + (lane i + 4) and (lane i - 4) - x, each with the shifted
+// operand read into the add / subtract, then one select.
 template <int M>
 __device__ __forceinline__ void butterfly8(float (&x)[8], int L) {
 #pragma clang fp contract(off)
+    const uint32_t sgn = (L & M) ? 0x80000000u : 0u;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        if constexpr (M == 4 || M == 8) {
-            const float up = __int_as_float(dpp_mov<0x100 + M>(__float_as_int(x[c])));
-            const float dn = __int_as_float(dpp_mov<0x110 + M>(__float_as_int(x[c])));
+        if constexpr (M == 4) {
+            const float up = __int_as_float(dpp_mov<0x104>(__float_as_int(x[c])));
+            const float dn = __int_as_float(dpp_mov<0x114>(__float_as_int(x[c])));
             x[c] = (L & M) ? dn - x[c] : x[c] + up;
         } else {
-            const float o = xor_lane<M>(x[c]);
-            x[c] = (L & M) ? o - x[c] : x[c] + o;
+            const float o = __int_as_float(dpp_mov<xor_dpp_ctrl<M>()>(__float_as_int(x[c])));
+            x[c] = o + __uint_as_float(__float_as_uint(x[c]) ^ sgn);
         }
     }
 }
@@ -197,10 +212,10 @@ __device__ __forceinline__ void load8(const uint16_t* p, float (&x)[8]) {
 // 8 values * inv, rounded and saturated to int8, as two little-endian words
 __device__ __forceinline__ u32x2 pack_s8x8(const float (&x)[8], float inv) {
 #pragma clang fp contract(off)
-    u32x2 w = {0u, 0u};
+    int q[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) w[c >> 2] |= (uint32_t)(rn_sat(x[c] * inv) & 0xff) << (8 * (c & 3));
-    return w;
+    for (int c = 0; c < 8; ++c) q[c] = rn_sat(x[c] * inv);
+    return u32x2{pack_lo_bytes(q[0], q[1], q[2], q[3]), pack_lo_bytes(q[4], q[5], q[6], q[7])};
 }
 
 // ------------------------------------------------------------------------------------------------ fused rmsRope
@@ -282,12 +297,16 @@ __device__ __forceinline__ void h3_rms_rope(float (&x)[8], int L, const float (&
     const int hc = rot >> 4;
     const bool first = L < hc, second = L >= hc && L < 2 * hc;
     const int partner = first ? L + hc : (second ? L - hc : L);
+    // first half: f00 x_i + f01 x_{i+rot/2} (own value x_i); second half: f10 x_i + f11 x_{i+rot/2} (own value
+    // x_{i+rot/2}): with the second half's (f10, f11) swapped once, both are (own coefficient) * own + (partner's
+    // coefficient) * partner. Both products are exact (bf16 times bf16), so the one rounding of the fma is the exact
+    // sum's whichever product it takes.
+    const uint32_t sel = first ? 0x03020100u : 0x01000302u;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const float y = __shfl(x[c], partner, 16);
-        const float a0 = first ? x[c] : y, b0 = first ? y : x[c];   // (x_i, x_{i + rot/2})
-        // first half: f00 x_i + f01 x_{i+rot/2}; second half: f10 x_i + f11 x_{i+rot/2}
-        const float yo = fmaf(lo_bf16(t.w[c]), a0, hi_bf16(t.w[c]) * b0);
+        const uint32_t w = __builtin_amdgcn_perm(t.w[c], t.w[c], sel);
+        const float yo = fmaf(lo_bf16(w), x[c], hi_bf16(w) * y);
         x[c] = first || second ? bf16_round(yo) : x[c];
     }
 }
@@ -585,16 +604,18 @@ __device__ void quant_v(const PrepArgs& a, int b, int hk, int tile, uint8_t* ext
             const int key = tile * cta + 4 * kq + r;
             raw[r] = key < a.Sk ? *reinterpret_cast<const u32x4*>(vb + (int64_t)key * a.v_sn) : u32x4{0u, 0u, 0u, 0u};
         }
-        uint32_t col[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        // (keys past Sk arrive as zero rows: their bytes are 0)
+        uint32_t col[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if (tile * cta + 4 * kq + r < a.Sk) {
+        for (int j = 0; j < 4; ++j) {
+            int lo[4], hi[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    col[2 * j] |= (uint32_t)(rn_sat(lo_bf16(raw[r][j]) * inv[2 * j]) & 0xff) << (8 * r);
-                    col[2 * j + 1] |= (uint32_t)(rn_sat(hi_bf16(raw[r][j]) * inv[2 * j + 1]) & 0xff) << (8 * r);
-                }
+            for (int r = 0; r < 4; ++r) {
+                lo[r] = rn_sat(lo_bf16(raw[r][j]) * inv[2 * j]);
+                hi[r] = rn_sat(hi_bf16(raw[r][j]) * inv[2 * j + 1]);
             }
+            col[2 * j] = pack_lo_bytes(lo[0], lo[1], lo[2], lo[3]);
+            col[2 * j + 1] = pack_lo_bytes(hi[0], hi[1], hi[2], hi[3]);
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c) *reinterpret_cast<uint32_t*>(vts + (8 * c8 + c) * vs + 4 * kq) = col[c];
