@@ -316,23 +316,29 @@ __device__ __forceinline__ void h3_rms_rope(float (&x)[8], int L, const float (&
 // Block x == nvchunk: the anchor of kv head y (nine sample keys at i * (Sk - 1) / 8; the sample with the least
 // squared distance to the others is subtracted from every key when that lowers the samples' energy and raises their
 // abs-max by at most 12.5 %), in fp64 like the checker.
-template <bool ROPE>
+template <bool ROPE, int HD>
 __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
 #pragma clang fp contract(off)
+    constexpr int D = HD;
+    constexpr int CGS = HD / 8, RPP = 256 / CGS;  // 8-channel groups a row; rows a pass
+    constexpr int NSAMP = 9;
+    // the V blocks' partial maxima and the anchor block's sums and sample rows share one buffer
+    constexpr int RED_BYTES = RPP * HD * 4, SD_BYTES = (NSAMP + 2) * 128 * 8, ROWS_BYTES = ROPE ? NSAMP * 128 * 4 : 0;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[RED_BYTES > SD_BYTES + ROWS_BYTES ? RED_BYTES
+                                                                                            : SD_BYTES + ROWS_BYTES];
     const Plan& p = a.p;
-    const int D = p.d;
     const int b = blockIdx.z, hk = blockIdx.y, t = threadIdx.x;
     if ((int)blockIdx.x < p.nvchunk) {
-        __shared__ float red[32][128];
-        const int cgs = D / 8, rpp = 256 / cgs;  // 8-channel groups a row; rows a pass
-        const int cg = t % cgs, r0 = t / cgs;
+        float (*red)[HD] = reinterpret_cast<float (*)[HD]>(smem);
+        const int cg = t % CGS, r0 = t / CGS;
         float m[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) m[j] = 0.0f;
         const int base = blockIdx.x * VCHUNK;
         const uint16_t* vb = a.v + b * a.v_sb + hk * a.v_sh + 8 * cg;
-        for (int i = 0; i < VCHUNK / rpp; ++i) {
-            const int row = base + r0 + rpp * i;
+#pragma unroll
+        for (int i = 0; i < VCHUNK / RPP; ++i) {   // every load of the lane in flight together
+            const int row = base + r0 + RPP * i;
             if (row < a.Sk) {
                 const u32x4 w = *reinterpret_cast<const u32x4*>(vb + (int64_t)row * a.v_sn);
 #pragma unroll
@@ -347,20 +353,20 @@ __global__ __launch_bounds__(256) void i8_stats_kernel(PrepArgs a) {
         __syncthreads();
         if (t < D) {
             float mx = 0.0f;
-            for (int r = 0; r < rpp; ++r) mx = fmaxf(mx, red[r][t]);
+#pragma unroll
+            for (int r = 0; r < RPP; ++r) mx = fmaxf(mx, red[r][t]);
             float* vpart = reinterpret_cast<float*>(a.ws + p.vpart);
             vpart[((size_t)(b * a.HK + hk) * p.nvchunk + blockIdx.x) * D + t] = mx;
         }
         return;
     }
     // the anchor
-    constexpr int NSAMP = 9;
-    __shared__ double sd[NSAMP + 2][128];
+    double (*sd)[128] = reinterpret_cast<double (*)[128]>(smem);
     double s[NSAMP];
     const uint16_t* kb = a.k + b * a.k_sb + hk * a.k_sh;
     // fused rmsRope: the sample rows normalised and rotated first (16 lanes a row, groups 0-8), exactly as quant_k
     // prepares every key row
-    __shared__ float rows[ROPE ? NSAMP : 1][128];
+    float (*rows)[128] = reinterpret_cast<float (*)[128]>(smem + SD_BYTES);
     if constexpr (ROPE) {
         const int grp = t >> 4, L = t & 15;
         if (grp < NSAMP) {
@@ -1041,8 +1047,11 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
 hipError_t launch_prep(const PrepArgs& a, hipStream_t stream) {
     const Plan& p = a.p;
-    if (a.rope_tab) hipLaunchKernelGGL(i8_stats_kernel<true>, dim3(p.nvchunk + 1, a.HK, a.B), dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(i8_stats_kernel<false>, dim3(p.nvchunk + 1, a.HK, a.B), dim3(256), 0, stream, a);
+    const dim3 sgrid(p.nvchunk + 1, a.HK, a.B);
+    if (a.rope_tab && p.d == 128) hipLaunchKernelGGL((i8_stats_kernel<true, 128>), sgrid, dim3(256), 0, stream, a);
+    else if (a.rope_tab) return hipErrorInvalidValue;   // the fused rmsRope: head dim 128 only
+    else if (p.d == 128) hipLaunchKernelGGL((i8_stats_kernel<false, 128>), sgrid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((i8_stats_kernel<false, 64>), sgrid, dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid((a.Sq + QROWS - 1) / QROWS + p.skp / KROWS + p.ntiles, a.H > a.HK ? a.H : a.HK, a.B);
