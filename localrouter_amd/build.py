@@ -45,8 +45,9 @@ EXTRA_FLAGS = {"attn_stream.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]
 # Scratch (spill) budget per kernel, bytes per lane. The streaming attention kernel and the INT8 attention kernel count
 # their direct global->LDS refills with explicit `s_waitcnt vmcnt(N)`; a scratch access among those loads would be
 # counted too, and the waits would no longer name the loads they wait for. Each keeps one 4-byte value in scratch
-# that is stored and reloaded only outside its streaming loop (read from the generated assembly). Every other kernel
-# uses none. The build fails when a kernel needs more: the spill must then be found and removed, not accepted.
+# that is stored and reloaded only outside its streaming loop: the build generates their assembly and fails when a
+# scratch access sits in a loop block (LOOP_SCAN, loop_scratch_ops). Every other kernel uses none. The build fails
+# when a kernel needs more: the spill must then be found and removed, not accepted.
 SCRATCH_BUDGET = {"attn_stream_kernel": 8, "i8_attn_kernel": 8}
 REMARK_FLAGS = ["-Rpass-analysis=kernel-resource-usage"]
 RESOURCES = PKG / "_build" / "resources.json"
@@ -87,6 +88,29 @@ def scratch_violations(res: dict[str, dict[str, int]]) -> list[str]:
         if r.get("ScratchSize", 0) > budget:
             bad.append(f"{name}: {r.get('ScratchSize')} bytes of scratch per lane (budget {budget})")
     return bad
+
+
+def loop_scratch_ops(asm: str, kernel: str) -> tuple[int, list[str]]:
+    """(scratch instructions of `kernel`, those inside one of its loops) in the gfx950 assembly `asm`. A basic block is
+    in a loop when the compiler's own block comment says so ("in Loop:" or "Loop Header"); a spill there would sit
+    among the streaming loop's direct-to-LDS refills and be counted by their explicit vmcnt waits."""
+    m = re.search(r"^(\S*" + re.escape(kernel) + r"\S*):", asm, re.M)
+    if not m:
+        raise RuntimeError(f"kernel {kernel} not found in the assembly")
+    body = asm[m.start():asm.find(".Lfunc_end", m.start())].splitlines()
+    total, inside, in_loop = 0, [], False
+    for line in body:
+        if re.match(r"^(\.LBB\S*:|; %bb\.\d+:)", line):
+            in_loop = "in Loop:" in line or "Loop Header" in line
+        if re.match(r"^\s+scratch_(load|store)", line):
+            total += 1
+            if in_loop:
+                inside.append(line.strip())
+    return total, inside
+
+
+# kernels with a scratch budget: (source, kernel) whose assembly is scanned for scratch inside loops
+LOOP_SCAN = [("attn_stream.hip", "attn_stream_kernel"), ("int8_attn.hip", "i8_attn_kernel")]
 
 
 def _run(cmd: list[str]) -> str:
@@ -133,6 +157,16 @@ def build(verbose: bool = False) -> Path:
     bad = scratch_violations(res)
     if bad:
         raise RuntimeError("kernels over their scratch budget:\n  " + "\n  ".join(bad))
+    # the kernels allowed a spill keep it outside their loops: their device assembly is generated and scanned
+    for src, kernel in LOOP_SCAN:
+        asm_path = objdir / (Path(src).stem + ".s")
+        _run([cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "--cuda-device-only", "-S", str(CSRC / src),
+              "-o", str(asm_path)])
+        asm = asm_path.read_text()
+        for name in sorted(set(re.findall(r"^(_Z\S*" + re.escape(kernel) + r"\S*):", asm, re.M))):
+            _, inside = loop_scratch_ops(asm, name)
+            if inside:
+                raise RuntimeError(f"{name}: scratch accesses inside a loop:\n  " + "\n  ".join(inside))
     tmp = LIB.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, *LIBS, "-o", str(tmp)])
     os.replace(tmp, LIB)

@@ -50,3 +50,47 @@ def test_built_library_is_within_budget():
     assert any("attn_stream_kernel" in k for k in res) and any("i8_attn_kernel" in k for k in res)
     stream = next(v for k, v in res.items() if "attn_stream_kernel" in k)
     assert stream["VGPRs"] + stream["AGPRs"] <= 256 and stream["Occupancy"] == 2
+
+
+ASM = """\
+_ZN2lr12_GLOBAL__N_118attn_stream_kernelENS_8AttnArgsE: ; @_ZN2lr12_GLOBAL__N_118attn_stream_kernelENS_8AttnArgsE
+; %bb.0:
+	s_load_dwordx2 s[0:1], s[0:1], 0x0
+	scratch_store_dword off, v6, off        ; 4-byte Folded Spill
+.LBB0_168:                              ; =>This Loop Header: Depth=1
+	v_mfma_f32_32x32x16_bf16 a[0:15], v[0:3], v[4:7], a[0:15]
+.LBB0_172:                              ;   in Loop: Header=BB0_168 Depth=1
+	s_barrier
+	s_cbranch_scc1 .LBB0_168
+; %bb.407:
+	scratch_load_dword v0, off, off         ; 4-byte Folded Reload
+	s_endpgm
+.Lfunc_end0:
+"""
+
+
+def test_loop_scan_finds_a_spill_inside_the_loop():
+    """The assembly scan (build.loop_scratch_ops): the present spill, stored before the loop and reloaded after it,
+    passes; the same store planted in a loop block (header or body) is reported."""
+    k = "attn_stream_kernel"
+    assert build.loop_scratch_ops(ASM, k) == (2, [])
+    planted = ASM.replace("\ts_barrier\n", "\ts_barrier\n\tscratch_store_dword off, v9, off offset:4\n")
+    total, inside = build.loop_scratch_ops(planted, k)
+    assert total == 3 and len(inside) == 1 and "v9" in inside[0]
+    planted = ASM.replace("\tv_mfma_f32", "\tscratch_load_dword v1, off, off\n\tv_mfma_f32")
+    assert len(build.loop_scratch_ops(planted, k)[1]) == 1
+
+
+def test_built_kernels_keep_scratch_out_of_their_loops():
+    """The last build's generated assembly of the two kernels with a scratch budget: no scratch access in a loop."""
+    import re
+    import pytest
+    for src, kernel in build.LOOP_SCAN:
+        path = build.PKG / "_build" / src.replace(".hip", ".s")
+        if not path.exists():
+            pytest.skip("no generated assembly (build() writes it)")
+        asm = path.read_text()
+        names = set(re.findall(r"^(_Z\S*" + re.escape(kernel) + r"\S*):", asm, re.M))
+        assert names
+        for name in names:
+            assert build.loop_scratch_ops(asm, name)[1] == [], name
