@@ -170,6 +170,31 @@ def test_int8_packed_qkv(S, H, bias):
         assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS, f"S={S} h={h}: vs exact {d.max():.3e} {d.mean():.3e}"
 
 
+def test_int8_prep_nonfinite_values():
+    """NaN and infinities in q, k and v: the quantisers' NaN -> 0 and saturation (float_utils.cuh:40-51; the
+    kernels convert through v_cvt_i32_f32, which maps NaN to 0 and saturates), the abs-max that skips NaN (fmaxf),
+    and the infinite scales: the prep still bit-exact against the oracle. The planted rows are not anchor samples."""
+    S, H = 300, 2
+    print(f"\n[int8 non-finite] S={S} H={H}", flush=True)
+    qkv = _qkv(61, S, H)
+    nan, pinf, ninf = np.uint16(0x7FC0), np.uint16(0x7F80), np.uint16(0xFF80)
+    qkv[5, 0, 0, 3] = nan         # a query row that becomes NaN throughout (the rotation mixes it): all zeros
+    qkv[50, 0, 1, 77] = pinf      # a query row of infinities: scale inf, every value 0 or saturated
+    qkv[120, 1, 0, 10] = ninf     # a key scale group with an infinite scale
+    qkv[6, 1, 1, 0] = nan         # a key row of NaN inside a finite group
+    qkv[77, 2, 0, 5] = nan        # one NaN value of V (skipped by the channel abs-max, quantised to 0)
+    qkv[200, 2, 1, 100] = ninf    # an infinite V channel scale
+    dq = to_dev(qkv.reshape(S, 3 * H * 128))
+    ws = ops.kitchen_attention_prep(dq, None, H)
+    torch.cuda.synchronize()
+    dec = _decode(ws.cpu().numpy(), 1, H, H, S, S)
+    for h in range(H):
+        ref = _oracle_head(*(np.ascontiguousarray(qkv[:, i, h]) for i in range(3)), S)
+        _check_parts(dec, ref, 0, h, h, S, f"non-finite h={h}")
+    assert not dec["q8"][0, 0, 5].any(), "a NaN query row quantises to zeros"
+    assert np.isinf(dec["vs"][0, 1, 100]), "an infinite V value makes its channel scale infinite"
+
+
 def test_int8_anchor_closed_forms():
     """The prep's anchor on keys whose outcome the criterion fixes in closed form (tests/test_oracle_int8.py
     _anchor_cases): accepted at sample 3's row, declined on energy, declined on the 12.5 % abs-max cap; the other
