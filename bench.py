@@ -390,7 +390,8 @@ def h3_table(S: int):
     return np.ascontiguousarray(np.tile(tab, (-(-S // tab.shape[0]), 1))[:S])
 
 
-H3_ROT, H3_EPS = 96, 1e-6
+# H3's rmsRope arguments: rot 96 and the engine's eps 1e-5 (src/engines/minimax_h3/dit.zig:40, :665)
+H3_ROT, H3_EPS = 96, 1e-5
 
 
 def cpu_baseline_int8(qkv_bits, qn, kn, tab, S, H, budget_s=10.0):

@@ -27,7 +27,7 @@ torch = pytest.importorskip("torch")
 
 from localrouter_amd import ops, rope  # noqa: E402
 
-ROT, EPS = 96, 1e-6
+ROT, EPS = 96, 1e-5   # H3's rmsRope arguments (src/engines/minimax_h3/dit.zig:40, :665)
 
 
 def _table(S, seed):
