@@ -121,6 +121,28 @@ def test_prep_rope_zero_rows_and_partial_rotation():
         _check_parts(dec, _oracle_head(qh, kh, qkv[:, 2, h], S), 0, h, h, S, f"rot {rot} head {h}")
 
 
+def test_prep_rope_gqa_batches():
+    """Separate q [B, H, S, 128] and k, v [B, HK, S, 128] tensors: two batches, GQA 4 / 2 (query head h reads kv head
+    h // 2); token n of every batch and head uses table row n. Bit-exact against the oracle chain per (batch, head)."""
+    B, H, HK, S = 2, 4, 2, 200
+    print(f"\n[int8 prep_rope gqa] B={B} H={H} HK={HK} S={S}", flush=True)
+    q = oracle.synth_bf16(91, 1, (B, H, S, 128))
+    k = oracle.synth_bf16(91, 2, (B, HK, S, 128))
+    v = oracle.synth_bf16(91, 3, (B, HK, S, 128))
+    qn, kn = _weights(91)
+    tab = _table(S, 9)
+    ws = ops.int8_attention_prep_rope(to_dev(q), to_dev(k), to_dev(v), to_dev(qn), to_dev(kn), to_dev(tab), rot=ROT,
+                                      eps=EPS)
+    torch.cuda.synchronize()
+    dec = _decode(ws.cpu().numpy(), B, H, HK, S, S)
+    for b in range(B):
+        kr = [_oracle_rope(k[b, hk], kn, tab) for hk in range(HK)]
+        for h in range(H):
+            hk = h // (H // HK)
+            ref = _oracle_head(_oracle_rope(q[b, h], qn, tab), kr[hk], v[b, hk], S)
+            _check_parts(dec, ref, b, h, hk, S, f"b={b} h={h}")
+
+
 def test_prep_rope_rejects():
     """Head dim 64, Sq != Sk, a misaligned table row stride, rot not a multiple of 16: rejected before any launch."""
     from localrouter_amd import _lib
