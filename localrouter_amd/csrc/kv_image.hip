@@ -39,21 +39,28 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
     const int hk = (int)(tile_id / a.tiles), t = (int)(tile_id - (int64_t)hk * a.tiles);
     const int key0 = t * IMG_TILE_KEYS;
 
-    // ---- every load first: 4 key rows (16 bytes each), with copy_v the 4 value rows, the weight, the table entries
+    // ---- the loads first: 4 key rows (16 bytes each), the weight, the first key row's table entries (the next row's
+    // are loaded while a row is computed: two rows of entries live at a time)
     u32x4 xin[KROWS];
 #pragma unroll
     for (int i = 0; i < KROWS; ++i) {
         const int key = min(key0 + g + 16 * i, a.Sk - 1);
         xin[i] = *reinterpret_cast<const u32x4*>(a.k + (int64_t)key * a.k_rs + (int64_t)hk * D + 8 * c);
     }
-    u32x4 vin[KROWS];                                   // copy_v: value rows g + 16 i, dims 8 c .. +7
+    // ---- values (copy_v): the tile's rows g + 16 i, dims 8 c .. +7, into the workspace's value rows
+    // [tiles * 64][HK][128], zero past Sk; loaded and stored here, so that they hold no registers through the keys
     if (a.copy_v) {
+        u32x4 vin[KROWS];
 #pragma unroll
         for (int i = 0; i < KROWS; ++i) {
             const int key = key0 + g + 16 * i;
             vin[i] = key < a.Sk ? *reinterpret_cast<const u32x4*>(a.v + (int64_t)key * a.v_rs + (int64_t)hk * D + 8 * c)
                                 : u32x4{0, 0, 0, 0};
         }
+        uint16_t* vdst = static_cast<uint16_t*>(a.img_v) + (int64_t)hk * D + 8 * c;
+#pragma unroll
+        for (int i = 0; i < KROWS; ++i)
+            *reinterpret_cast<u32x4*>(vdst + ((int64_t)(key0 + g + 16 * i) * a.HK) * D) = vin[i];
     }
     float wv[8];
     if (a.w) {
@@ -67,25 +74,29 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
     }
     const int P = a.rot >> 1;
     const int hc = a.rot >> 4;                           // split-half: 16-byte chunks per half
-    Rot2 rt[KROWS][8];   // interleaved: pairs 4c..4c+3 in [0..3]; split-half: pairs of this lane's 8 dims
-    if constexpr (KIND != TABLE_NONE) {
-#pragma unroll
-        for (int i = 0; i < KROWS; ++i) {
+    // table entries of key row i in rt[i & 1]: interleaved, pairs 4c..4c+3 in [0..3]; split-half, the pairs of this
+    // lane's 8 dims
+    Rot2 rt[2][8];
+    auto load_rt = [&](int i) __attribute__((always_inline)) {
+        if constexpr (KIND != TABLE_NONE) {
             const int key = key0 + g + 16 * i;
             const int64_t toff = (int64_t)max(min(key, a.Sk - 1) - a.n_pre, 0) * a.tab_stride;
             if constexpr (PAIRING == PAIR_INTERLEAVED) {
-                rot4<KIND>(a.ta, a.tb, toff, 4 * c, P, a.tab_vec, rt[i]);
+                rot4<KIND>(a.ta, a.tb, toff, 4 * c, P, a.tab_vec, rt[i & 1]);
             } else {
                 const int pc = c < hc ? c : c - hc;
-                rot4<KIND>(a.ta, a.tb, toff, 8 * pc, P, a.tab_vec, rt[i]);
-                rot4<KIND>(a.ta, a.tb, toff, 8 * pc + 4, P, a.tab_vec, rt[i] + 4);
+                rot4<KIND>(a.ta, a.tb, toff, 8 * pc, P, a.tab_vec, rt[i & 1]);
+                rot4<KIND>(a.ta, a.tb, toff, 8 * pc + 4, P, a.tab_vec, rt[i & 1] + 4);
             }
         }
-    }
+    };
+    load_rt(0);
 
     // ---- keys: norm, rotation, into the LDS image
 #pragma unroll
     for (int i = 0; i < KROWS; ++i) {
+        if (i + 1 < KROWS) load_rt(i + 1);
+        __builtin_amdgcn_sched_barrier(0);   // row i + 1's entries in flight while row i is computed, no earlier
         const int r = g + 16 * i, key = key0 + r;
         float x[8];
 #pragma unroll
@@ -109,8 +120,8 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
                 for (int j = 0; j < 4; ++j) {
                     const bool on = 8 * c + 2 * j < a.rot;
                     const float x0 = y[2 * j], x1 = y[2 * j + 1];
-                    const float y0 = fmaf(rt[i][j].f00, x0, rt[i][j].f01 * x1);
-                    const float y1 = fmaf(rt[i][j].f10, x0, rt[i][j].f11 * x1);
+                    const float y0 = fmaf(rt[i & 1][j].f00, x0, rt[i & 1][j].f01 * x1);
+                    const float y1 = fmaf(rt[i & 1][j].f10, x0, rt[i & 1][j].f11 * x1);
                     y[2 * j] = on ? y0 : x0;
                     y[2 * j + 1] = on ? y1 : x1;
                 }
@@ -122,8 +133,8 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
                 for (int j = 0; j < 8; ++j) {
                     const float o = __shfl(y[j], partner, 64);
                     const float a0 = first ? y[j] : o, b0 = first ? o : y[j];   // (x_p, x_{p + rot/2})
-                    const float ya = fmaf(rt[i][j].f00, a0, rt[i][j].f01 * b0);
-                    const float yb = fmaf(rt[i][j].f10, a0, rt[i][j].f11 * b0);
+                    const float ya = fmaf(rt[i & 1][j].f00, a0, rt[i & 1][j].f01 * b0);
+                    const float yb = fmaf(rt[i & 1][j].f10, a0, rt[i & 1][j].f11 * b0);
                     y[j] = first ? ya : (second ? yb : y[j]);
                 }
             }
@@ -138,14 +149,6 @@ __device__ __forceinline__ void kv_tile_block(const KvImageArgs& a, int64_t tile
             for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
         }
         *reinterpret_cast<u32x4*>(img + stg(img_k_offset(r, c))) = o;
-    }
-
-    // ---- values (copy_v): the tile's rows into the workspace's value rows [tiles * 64][HK][128], zero past Sk
-    if (a.copy_v) {
-        uint16_t* vdst = static_cast<uint16_t*>(a.img_v) + (int64_t)hk * D + 8 * c;
-#pragma unroll
-        for (int i = 0; i < KROWS; ++i)
-            *reinterpret_cast<u32x4*>(vdst + ((int64_t)(key0 + g + 16 * i) * a.HK) * D) = vin[i];
     }
     __syncthreads();
 
