@@ -62,19 +62,22 @@ typedef struct ihipStream_t* lr_stream_t;
 #define LR_WEIGHT_BF16 2
 
 /* Attention tile configurations for the _ex entry points (0 = the library's choice: LR_ATTN_CFG_STREAM_W8 for the
- * fused and prepared calls; for attention over value rows LR_ATTN_CFG_PIPE_W4, or LR_ATTN_CFG_PIPE_W8 when the call
- * is non-causal and its 256-query blocks fill whole rounds of the device's compute units, and LR_ATTN_CFG_PIPE_W8 for a
- * call split over its
- * keys through a workspace). */
+ * fused and prepared calls; for attention over key and value rows, non-causal calls of at least 4,096 keys run
+ * LR_ATTN_CFG_STREAM_W8 over the key rows when their 256-query blocks fill at least half a round of the device's
+ * compute units without leaving a last round less than half full; other calls run LR_ATTN_CFG_PIPE_W4, or
+ * LR_ATTN_CFG_PIPE_W8 when non-causal and the 256-query blocks fill whole rounds of the compute units. The workspace
+ * call lr_attention_bf16_ws chooses as described there.) */
 #define LR_ATTN_CFG_AUTO 0
 #define LR_ATTN_CFG_PIPE_W8 1      /* attention over value rows: 256 queries per workgroup (8 waves x 32), direct-to-LDS
                                       K/V ring, next tile's QK^T overlapped with the current tile's softmax */
 #define LR_ATTN_CFG_PIPE_W4 2      /* the same kernel with 128 queries per workgroup (4 waves x 32) */
-#define LR_ATTN_CFG_STREAM_W8 9    /* fused / prepared calls: one persistent workgroup per CU (8 waves x 32 queries)
-                                      streaming keys prepared as tile images (the LDS image of each 64-key tile,
-                                      16 KB) and value rows through 4-stage direct-to-LDS rings; softmax against a
-                                      fixed reference (the block's first key tile's maximum), query rows whose sums
-                                      overflowed it recomputed exactly at the end of the kernel */
+#define LR_ATTN_CFG_STREAM_W8 9    /* one persistent workgroup per CU (8 waves x 32 queries) streaming key tile
+                                      images (the LDS image of each 64-key tile, 16 KB: prepared by the fused and
+                                      prepared calls, gathered from the key rows by the calls over rows) and value rows
+                                      through 4-stage direct-to-LDS rings; softmax against a fixed reference (the
+                                      block's first key tile's maximum), query rows whose sums overflowed it recomputed
+                                      exactly at the end of the kernel. Over rows it needs out_row_stride < 2^23 and
+                                      k / v row strides <= 2^24 elements */
 
 int lr_attn_abi_version(void);
 
@@ -106,10 +109,14 @@ int lr_attention_bf16_ex(const void* q, const void* k, const void* v, void* out,
                          int config, lr_stream_t stream);
 
 /*
- * lr_attention_bf16 with device scratch: a call with few query blocks (fewer than 128 blocks of 256 queries x heads,
- * non-causal, e.g. 218 queries over 50,220 keys) is split over the keys into ranges that fill the GPU, each range's
- * partial result written to the workspace, then merged (flash-decoding). lr_attention_ws_bytes is the workspace the
- * call needs (0: it will not split; workspace may then be NULL). Results equal lr_attention_bf16's to fp32 rounding.
+ * lr_attention_bf16 with device scratch. A non-causal call with at most 32 blocks of 256 queries x heads and at least
+ * 961 keys (16 tiles of 64; e.g. 218 queries over 50,220 keys) is split over the keys into ranges that fill the GPU,
+ * each range's partial result written to the workspace, then merged (flash-decoding). Other non-causal calls of at least 4,096 keys
+ * run LR_ATTN_CFG_STREAM_W8 over the key rows, whose last partial round of query blocks is cut over all workgroups
+ * along the keys, the pieces' partials and arrival counters in the workspace (LR_JOINT_SPLIT_BYTES; the call clears
+ * the counters itself). Every other call runs as lr_attention_bf16. lr_attention_ws_bytes is the workspace the call
+ * needs (0: none; workspace may then be NULL). Results equal lr_attention_bf16's to fp32 rounding. Calls that overlap
+ * on one workspace race.
  */
 size_t lr_attention_ws_bytes(int W, int H, int nkeys, int causal);
 int lr_attention_bf16_ws(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK,

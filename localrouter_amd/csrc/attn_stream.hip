@@ -133,8 +133,8 @@ __device__ __forceinline__ void dma2v(uint64_t gaddr, uint32_t voff0, uint32_t v
     LR_ASM_M0_END
 }
 // The same two loads with their own M0 each and no instruction offset (the last, clamped tile of a head, whose
-// offsets may be smaller than 1024).
-__device__ __forceinline__ void dma2v_clamped(uint64_t gaddr, uint32_t voff0, uint32_t voff1, uint32_t lds) {
+// offsets may be smaller than 1024; and the key gathers of a call over key rows, whose lanes' offsets are rows apart).
+__device__ __forceinline__ void dma2_apart(uint64_t gaddr, uint32_t voff0, uint32_t voff1, uint32_t lds) {
     LR_ASM_M0_BEGIN
     asm volatile(
         "s_mov_b32 m0, %3\n\t"
@@ -144,6 +144,22 @@ __device__ __forceinline__ void dma2v_clamped(uint64_t gaddr, uint32_t voff0, ui
         "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, %2 offset:0" ::"v"(voff0),
         "v"(voff1), "s"(gaddr), "s"(lds)
+        : "memory", "m0", "scc");
+    LR_ASM_M0_END
+}
+// Key rows gathered into a tile image: lane l's 16 bytes of the two fragments a wave fills (at LDS byte lds + 16 l and
+// lds + 1024 + 16 l) are 8 dims of the same key row, 16 dims (32 bytes) apart: load 0 from gaddr + koff, load 1 from
+// gaddr + koff + 32 (its instruction offset 32 also adds to the LDS address, so M0 takes the other 992 bytes).
+__device__ __forceinline__ void dma2k_rows(uint64_t gaddr, uint32_t koff, uint32_t lds) {
+    LR_ASM_M0_BEGIN
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:0\n\t"
+        "s_add_u32 m0, %2, 0x3e0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:32" ::"v"(koff),
+        "s"(gaddr), "s"(lds)
         : "memory", "m0", "scc");
     LR_ASM_M0_END
 }
@@ -173,15 +189,19 @@ __device__ __forceinline__ bf16x8 frag_at(uint32_t addr) { return *(lds_frag*)(u
 // Recompute wave `wave`'s 32 queries of a block with the exact row maximum (the rare case of a non-finite row under the
 // fixed reference): pass 1 takes the maximum of every score, pass 2 accumulates P = exp2(S - max) <= 1, the row sums and
 // O, and the rows are written. The prepared queries are read from a.q (the block's rows, not yet overwritten), the key
-// fragments straight from the tile images in HBM (a 1 KB fragment is one 16-byte load per lane) and the value
-// fragments from the value rows (eight 2-byte loads per lane): nothing here touches LDS or waits for the other waves. Called after the streaming loop, so that its registers do not add to the loop's.
+// fragments straight from the tile images in HBM (a 1 KB fragment is one 16-byte load per lane) or, KR, from the key
+// rows (lane 32 hf + n: 16 bytes of key 32 j + key_perm(n) for fragment ks, the tile image's content), and the value
+// fragments from the value rows (eight 2-byte loads per lane): nothing here touches LDS or waits for the other waves.
+// Called after the streaming loop, so that its registers do not add to the loop's.
+template <bool KR>
 __device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, int row0, int tiles, int wave) {
     const int lane = threadIdx.x & 63, n = lane & 31, hf = lane >> 5;
     const int wrow0 = row0 + wave * 32, qrow = wrow0 + n;
     const int T = (a.nkeys + IMG_TILE_KEYS - 1) / IMG_TILE_KEYS;
     const uint64_t head_off = (uint64_t)hk * T * IMG_TILE_BYTES + (uint64_t)lane * 16;
     const uint8_t* kh = reinterpret_cast<const uint8_t*>(a.k) + head_off;
-    const uint16_t* vh = a.v + (int64_t)hk * D + n;   // dim n of this lane's 32-dim blocks
+    const uint16_t* krows = a.k + (int64_t)hk * a.k_hs + 8 * hf;
+    const uint16_t* vh = a.v + (int64_t)hk * a.v_hs + n;   // dim n of this lane's 32-dim blocks
     bf16x8 qf[8];
     const uint16_t* src = a.q + (int64_t)min(qrow, a.W - 1) * a.q_rs + head * D + 8 * hf;
 #pragma unroll
@@ -190,11 +210,15 @@ __device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, 
     if (a.causal) lim0 = min(lim0, a.p0 + qrow + 1);
     auto scores = [&](int j, const f32x16& c) {
         const uint8_t* kt = kh + (uint64_t)(j >> 1) * IMG_TILE_BYTES + (j & 1) * 8 * IMG_FRAG_BYTES;
+        // KR: keys past nkeys read the last row (finite; masked below)
+        const uint16_t* kr = krows + (int64_t)min(32 * j + img_key_perm(n), a.nkeys - 1) * a.k_rs;
         f32x16 sr = c;
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
-            sr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(kt + ks * IMG_FRAG_BYTES),
-                                                        qf[ks], sr, 0, 0, 0);
+        for (int ks = 0; ks < 8; ++ks) {
+            const bf16x8 kf = KR ? *reinterpret_cast<const bf16x8*>(kr + 16 * ks)
+                                 : *reinterpret_cast<const bf16x8*>(kt + ks * IMG_FRAG_BYTES);
+            sr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], sr, 0, 0, 0);
+        }
         const int lim = lim0 - (32 * j + 8 * hf);
 #pragma unroll
         for (int r = 0; r < 16; ++r)
@@ -256,6 +280,9 @@ __device__ __forceinline__ void redo_exact(const AttnArgs& a, int head, int hk, 
     }
 }
 
+// KR: a.k holds key rows (key j of kv head g at a.k + g * a.k_hs + j * a.k_rs), gathered into the tile-image layout by
+// the ring's direct loads; otherwise a.k holds the tile images.
+template <bool KR>
 __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_stream_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t Kr[RING * IMG_TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t Vr[RING * IMG_TILE_BYTES];
@@ -278,7 +305,8 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     const int nqb = (a.W + SBM - 1) / SBM;
     const int nblk = nqb * a.H;
     const int T = (a.nkeys + IMG_TILE_KEYS - 1) / IMG_TILE_KEYS;
-    const uint64_t head_bytes = (uint64_t)T * IMG_TILE_BYTES;
+    // bytes from one kv head's keys to the next: its tile images, or (KR) the caller's kv-head stride
+    const uint64_t head_bytes = KR ? (uint64_t)a.k_hs * 2 : (uint64_t)T * IMG_TILE_BYTES;
 
     // ---- the work of this workgroup. Whole blocks: logical, logical + nwg, ... below nwhole. With a.split, the
     // blocks from nwhole on (fewer than nwg, the "tail") are laid end to end as U = rem * T key tiles, and tail
@@ -355,8 +383,9 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
         return r;
     };
 
-    // ---- the tile stream: cursors of the next key / value tile to load. Keys: this wave's WQ bytes of the tile image;
-    // values: row 0 of the tile in the kv head's rows (each lane adds its own row and chunk offset).
+    // ---- the tile stream: cursors of the next key / value tile to load. Keys: this wave's WQ bytes of the tile image
+    // (KR: row 0 of the tile in the kv head's key rows, each lane adding its own row and dims); values: row 0 of the
+    // tile in the kv head's rows (each lane adds its own row and chunk offset).
     struct Cursor {
         int it, t, t1;
         uint64_t addr;
@@ -364,11 +393,14 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     const uint64_t kimg = (uint64_t)(uintptr_t)a.k, vrows = (uint64_t)(uintptr_t)a.v;
     const uint32_t rowb = (uint32_t)a.v_rs * 2u;   // bytes per value row (< 2^25: launch_stream checks)
     const uint64_t vtile = (uint64_t)IMG_TILE_KEYS * rowb;
+    // KR: bytes per tile of 64 key rows (< 2^31: launch_stream checks the row stride)
+    const uint32_t ktile = KR ? (uint32_t)a.k_rs * (2u * IMG_TILE_KEYS) : (uint32_t)IMG_TILE_BYTES;
     auto k_at = [&](const Item& r) __attribute__((always_inline)) {
-        return kimg + (uint64_t)r.hk * head_bytes + (uint64_t)r.t0 * IMG_TILE_BYTES + (uint64_t)wave * WQ;
+        if constexpr (KR) return kimg + (uint64_t)r.hk * head_bytes + (uint64_t)r.t0 * ktile;
+        else return kimg + (uint64_t)r.hk * head_bytes + (uint64_t)r.t0 * IMG_TILE_BYTES + (uint64_t)wave * WQ;
     };
     auto v_at = [&](const Item& r) __attribute__((always_inline)) {
-        return vrows + (uint64_t)r.hk * (D * 2) + (uint64_t)r.t0 * vtile;
+        return vrows + (uint64_t)r.hk * (uint64_t)a.v_hs * 2 + (uint64_t)r.t0 * vtile;
     };
     auto cur_start = [&](auto at) __attribute__((always_inline)) {
         const Item r = item_of(0);
@@ -376,7 +408,7 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     };
     // past the last tile of the last item the cursor stays put: its loads refill a free ring slot with a tile that is
     // never read
-    auto cur_next = [&](Cursor& c, uint64_t step, auto at) __attribute__((always_inline)) {
+    auto cur_next = [&](Cursor& c, auto step, auto at) __attribute__((always_inline)) {
         if (c.t + 1 < c.t1) {
             ++c.t;
             c.addr += step;
@@ -395,18 +427,42 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     const uint32_t vchunk = (uint32_t)(16 * vt_lane_chunk(lane));
     const uint32_t vo0 = vrow * rowb + vchunk, vo1 = vo0 + 4 * rowb - 1024;
     const int vfull = a.nkeys >> 6;   // value tiles t < vfull hold 64 rows; tile vfull (when nkeys % 64) fewer
+    // KR: this wave fills fragments 2 wave and 2 wave + 1 of the image (32-key block mb = wave >> 2, k-steps
+    // 2 (wave & 3) and + 1): lane 32 hf + n takes key row 32 mb + key_perm(n), dims 32 (wave & 3) + 8 hf .. +7, and
+    // the 8 dims 16 further on (img_k_offset)
+    // (computed at each load from the lane's byte offset, opaque to the compiler: nothing extra stays live in the loop)
     // ring slot x: byte offset x * 16 KB; this wave's loads fill its WQ bytes of the slot
     auto load_k = [&](Cursor& c, int pos) __attribute__((always_inline)) {
-        dma2k(c.addr, voff, kr0 + (uint32_t)((pos & (RING - 1)) * IMG_TILE_BYTES) + (uint32_t)wave * WQ);
-        cur_next(c, (uint64_t)IMG_TILE_BYTES, k_at);
+        const uint32_t lds = kr0 + (uint32_t)((pos & (RING - 1)) * IMG_TILE_BYTES) + (uint32_t)wave * WQ;
+        if constexpr (KR) {
+            uint32_t l16 = voff;   // 16 lane
+            int w = wave;
+            asm volatile("" : "+v"(l16), "+s"(w));
+            const uint32_t krow = (uint32_t)(32 * (w >> 2)) + (uint32_t)img_key_perm((int)(l16 >> 4) & 31);
+            const uint32_t kcol = (uint32_t)(64 * (w & 3)) + ((l16 >> 5) & 16u);
+            // rows past nkeys (the head's last, partial tile) read the last row: finite, and their scores are masked
+            const uint32_t lim = c.t < vfull ? 63u : (uint32_t)(a.nkeys - 1 - IMG_TILE_KEYS * c.t);
+            dma2k_rows(c.addr, min(krow, lim) * (ktile / IMG_TILE_KEYS) + kcol, lds);
+        } else {
+            dma2k(c.addr, voff, lds);
+        }
+        cur_next(c, ktile, k_at);
     };
     auto load_v = [&](Cursor& c, int pos) __attribute__((always_inline)) {
         const uint32_t lds = vr0 + (uint32_t)((pos & (RING - 1)) * IMG_TILE_BYTES) + (uint32_t)wave * WQ;
-        if (c.t < vfull) {
+        if constexpr (KR) {   // the lane's rows and chunk recomputed here, as for the keys (vrow, vchunk)
+            uint32_t l16 = voff;
+            int w = wave;
+            asm volatile("" : "+v"(l16), "+s"(w));
+            const uint32_t r = (uint32_t)(8 * w) + ((l16 >> 6) & 3u);
+            const uint32_t ch = ((l16 >> 2) & 0xc0u) + (l16 & 0x30u);
+            const uint32_t lim = c.t < vfull ? 63u : (uint32_t)(a.nkeys - 1 - IMG_TILE_KEYS * c.t);
+            dma2_apart(c.addr, min(r, lim) * rowb + ch, min(r + 4, lim) * rowb + ch, lds);
+        } else if (c.t < vfull) {
             dma2v(c.addr, vo0, vo1, lds);
         } else {   // the head's last, partial tile: rows past nkeys read the last row (finite; their P is 0)
             const uint32_t lim = (uint32_t)(a.nkeys - 1 - IMG_TILE_KEYS * c.t);
-            dma2v_clamped(c.addr, min(vrow, lim) * rowb + vchunk, min(vrow + 4, lim) * rowb + vchunk, lds);
+            dma2_apart(c.addr, min(vrow, lim) * rowb + vchunk, min(vrow + 4, lim) * rowb + vchunk, lds);
         }
         cur_next(c, vtile, v_at);
     };
@@ -819,10 +875,13 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
             Item r = item_of(it);
             if (a.causal) r.t1 = min(T, (a.p0 + min(r.row0 + SBM, a.W) - 1) / IMG_TILE_KEYS + 1);
             else r.t1 = T;
-            redo_exact(a, r.head, r.hk, r.row0, r.t1, wave);
+            redo_exact<KR>(a, r.head, r.hk, r.row0, r.t1, wave);
         }
     }
 }
+
+// the split tail's arrival counters, cleared (a fill kernel, not a memset: safe under graph capture)
+__global__ __launch_bounds__(STREAM_MAX_WG) void zero_cnt_kernel(int* cnt) { cnt[threadIdx.x] = 0; }
 
 }  // namespace
 
@@ -837,13 +896,16 @@ bool stream_split_params(int W, int H, int nkeys, int causal, int nwg, int* tail
     return true;
 }
 
-hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream) {
+hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream, bool key_rows) {
     if (a.W < 1 || a.H < 1 || nwg < 1 || nwg > STREAM_MAX_WG) return hipErrorInvalidValue;
-    // value rows: a lane's 32-bit load offset reaches 63 rows into a tile (< 2^31 bytes)
-    if (a.v_rs < D || a.v_rs > STREAM_MAX_V_RS || a.v_rs % 8) return hipErrorInvalidValue;
+    // value (and key) rows: a lane's 32-bit load offset reaches 63 rows into a tile (< 2^31 bytes)
+    if (a.v_rs < D || a.v_rs > STREAM_MAX_V_RS || a.v_rs % 8 || a.v_hs < 0 || a.v_hs % 8) return hipErrorInvalidValue;
+    if (key_rows && (a.k_rs < D || a.k_rs > STREAM_MAX_V_RS || a.k_rs % 8 || a.k_hs < 0 || a.k_hs % 8))
+        return hipErrorInvalidValue;
     // at most MAX_WG_BLOCKS whole blocks per workgroup (its recomputation bits): larger calls run as several launches
     // over consecutive query-row ranges (queries, outputs and, causal, the diagonal offset p0 shifted)
     const int64_t rows_per = (int64_t)SBM * std::max<int64_t>(1, (int64_t)MAX_WG_BLOCKS * nwg / a.H);
+    bool cleared = false;
     for (int64_t r0 = 0; r0 < a.W; r0 += rows_per) {
         AttnArgs b = a;
         b.W = (int)std::min<int64_t>(rows_per, a.W - r0);
@@ -858,9 +920,18 @@ hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream) {
         if (a.part && a.cnt && stream_split_params(b.W, b.H, b.nkeys, b.causal, nwg, &tw)) {
             b.split = 1;
             b.tail_wg = tw;
+            // over key rows no preparation launch has cleared the arrival counters: a fill launch first (every launch
+            // leaves them zero again)
+            if (key_rows && !cleared) {
+                hipLaunchKernelGGL(zero_cnt_kernel, dim3(1), dim3(STREAM_MAX_WG), 0, stream, a.cnt);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                cleared = true;
+            }
         }
         const unsigned grid = b.split ? (unsigned)nwg : (unsigned)std::min<int64_t>(blocks, nwg);
-        hipLaunchKernelGGL(attn_stream_kernel, dim3(grid), dim3(SW * 64), 0, stream, b);
+        if (key_rows) hipLaunchKernelGGL(attn_stream_kernel<true>, dim3(grid), dim3(SW * 64), 0, stream, b);
+        else hipLaunchKernelGGL(attn_stream_kernel<false>, dim3(grid), dim3(SW * 64), 0, stream, b);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

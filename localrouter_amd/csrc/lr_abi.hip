@@ -32,19 +32,48 @@ inline bool rows_ok(const void* p, int64_t rs, int heads) {
 
 inline bool scale_ok(float s) { return s > 0.0f && isfinite(s); }
 
-// Key-split count for plain attention over value rows (the pipelined kernel, 256-query blocks): a launch with fewer
-// than 128 query blocks is split over the keys into enough ranges of at least 4 key tiles to give ~256 workgroups,
-// then merged by a combine pass. 1 = no split (causal calls are never split).
+// Key-split count for plain attention over value rows (the pipelined kernel, 256-query blocks): a non-causal launch
+// with at most 32 query blocks and at least 16 key tiles is split over the keys into enough ranges of at least 4 key
+// tiles to give ~256 workgroups, then merged by a combine pass. 1 = no split (causal calls are never split). Measured
+// at 218 queries x 16 / 24 heads the split takes 0.77 / 0.47 / 0.22 of the 128-query pipelined kernel's time at
+// 2,000 / 8,000 / 50,220 keys and 1.34 at 600 keys; at 600-1,280 queries the streaming kernel's split tail is faster.
 int split_count(int W, int H, int nkeys, int causal) {
     if (causal || W < 1 || H < 1 || nkeys < 1) return 1;
     const int64_t blocks = (int64_t)((W + 255) / 256) * H;
     const int tiles = (nkeys + 63) / 64;
-    if (blocks >= 128 || tiles < 8) return 1;
+    if (blocks > 32 || tiles < 16) return 1;
     int ns = (int)std::min<int64_t>((256 + blocks - 1) / blocks, tiles / 4);
     ns = std::max(1, std::min(ns, 64));
     const int per = (tiles + ns - 1) / ns;
     return (tiles + per - 1) / per;   // no empty range
 }
+
+// Whether a non-causal call over key and value rows that is not key-split runs the streaming kernel (reading key rows
+// into tile images in LDS) instead of the pipelined kernels. Measured from 218 to 50,220 queries x 4-32 heads: below
+// 4,096 keys the 128-query pipelined kernel is as fast or faster. From 4,096 keys on, with a workspace (its split tail
+// cutting the last partial round of blocks over the workgroups) the streaming kernel takes 0.55-0.93 of the pipelined
+// kernel's time from 33 query blocks on. Without one it runs whole 256-query blocks, and wins (0.88-0.99) when they
+// fill between half a round and a round of the CUs or leave a last round at least half full; a last round of a few
+// blocks (288 blocks on 256 CUs: 1.04-1.08) favours the pipelined kernel's 128-query blocks.
+bool stream_rows(int W, int H, int nkeys, int causal, bool workspace, int cus) {
+    if (causal || nkeys < 4096 || cus < 1) return false;
+    const int64_t blocks = (int64_t)((W + 255) / 256) * H;
+    if (workspace) return blocks > 32;
+    const int64_t tail = blocks % cus;
+    return blocks <= cus ? 2 * blocks >= cus : tail == 0 || 2 * tail >= cus;
+}
+
+// Whether the streaming kernel over key rows cuts the last partial round of blocks over the workgroups (its split
+// tail). The pieces of one block stream different key ranges, so blocks of one head no longer share each key tile in
+// the caches: at 50,220 keys x 24 heads (617 MB of keys and values) a tail of 216 blocks on 256 CUs ran 1.17-1.23x
+// the unsplit time, 144 blocks about the same, 120 blocks 0.78x. Beyond 16,384 keys a tail of three quarters of the
+// CUs or more runs unsplit.
+bool stream_rows_split(int W, int H, int nkeys, int cus) {
+    const int64_t blocks = (int64_t)((W + 255) / 256) * H;
+    const int64_t tail = blocks % cus;
+    return !(nkeys > 16384 && 4 * tail >= 3 * (int64_t)cus);
+}
+
 size_t split_bytes(int W, int H, int ns) {
     if (ns <= 1) return 0;
     const size_t rows = (size_t)H * W * ns;
@@ -58,7 +87,7 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
                    int64_t v_hs, int config, hipStream_t stream, void* workspace = nullptr, size_t ws_bytes = 0) {
     if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || nkeys < 1 || p0 < 0 || (causal != 0 && causal != 1)) return ERR_ARGS;
     if (!scale_ok(scale) || !(config == LR_ATTN_CFG_AUTO || config == LR_ATTN_CFG_PIPE_W8 ||
-                              config == LR_ATTN_CFG_PIPE_W4))
+                              config == LR_ATTN_CFG_PIPE_W4 || config == LR_ATTN_CFG_STREAM_W8))
         return ERR_ARGS;
     if ((int64_t)p0 + W > INT_MAX - 512 || nkeys > INT_MAX - 512 || W > INT_MAX - 512) return ERR_ARGS;
     if (!rows_ok(q, q_rs, H) || !rows_ok(out, o_rs, H)) return ERR_ARGS;
@@ -85,7 +114,10 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
         if (e != hipSuccess) return (int)e;
         return (int)lr::launch_split_combine(a, stream);
     }
-    if (config == LR_ATTN_CFG_AUTO) {
+    const bool ws_split_area = workspace && ws_bytes >= (size_t)LR_JOINT_SPLIT_BYTES && aligned(workspace, 256);
+    if (config == LR_ATTN_CFG_AUTO && stream_rows(W, H, nkeys, causal, ws_split_area, device_cus())) {
+        config = LR_ATTN_CFG_STREAM_W8;
+    } else if (config == LR_ATTN_CFG_AUTO) {
         // 128 queries per workgroup, two workgroups per CU, unless non-causal 256-query blocks fill whole rounds of
         // the CUs: measured at cfg1 / cfg2 / causal GQA shapes W4 takes 0.72 / 0.93 / 0.89 of W8's time, at 12,800
         // and 50,220 tokens the two are within 1.5 %, at 16,384 x 4 heads (exactly one round of 256-query blocks) W8
@@ -93,6 +125,18 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int p
         const int cus = device_cus();
         const int64_t w8_blocks = (int64_t)((W + 255) / 256) * H;
         config = !causal && cus > 0 && w8_blocks % cus == 0 ? LR_ATTN_CFG_PIPE_W8 : LR_ATTN_CFG_PIPE_W4;
+    }
+    if (config == LR_ATTN_CFG_STREAM_W8) {
+        // the streaming kernel over the key rows: the output's 32-bit buffer range (256 rows * o_rs * 2 bytes < 2^32)
+        // and 32-bit per-lane row offsets (k_rs, v_rs <= STREAM_MAX_V_RS); with a workspace, its split tail
+        if (o_rs >= ((int64_t)1 << 23) || k_rs > lr::STREAM_MAX_V_RS || v_rs > lr::STREAM_MAX_V_RS) return ERR_ARGS;
+        const int cus = std::min(device_cus(), lr::STREAM_MAX_WG);
+        if (cus < 1) return (int)hipErrorInvalidDevice;
+        if (ws_split_area && stream_rows_split(W, H, nkeys, cus)) {
+            a.part = workspace;
+            a.cnt = reinterpret_cast<int*>(static_cast<char*>(workspace) + lr::STREAM_PART_BYTES);
+        }
+        return (int)lr::launch_stream(a, cus, stream, true);
     }
     return (int)lr::launch_attention(a, config, stream);
 }
@@ -494,7 +538,10 @@ int lr_attention_bf16(const void* q, const void* k, const void* v, void* out, in
 }
 
 size_t lr_attention_ws_bytes(int W, int H, int nkeys, int causal) {
-    return split_bytes(W, H, split_count(W, H, nkeys, causal));
+    const int ns = split_count(W, H, nkeys, causal);
+    if (ns > 1) return split_bytes(W, H, ns);
+    // calls the streaming kernel runs with a workspace: its split tail's partials and arrival counters
+    return W >= 1 && H >= 1 && stream_rows(W, H, nkeys, causal, true, 1) ? (size_t)LR_JOINT_SPLIT_BYTES : 0;
 }
 
 int lr_attention_bf16_ws(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK,

@@ -94,14 +94,15 @@ hipError_t launch_kv_image(const KvImageArgs& a, hipStream_t stream);
 // both use the same table kind and pairing.
 hipError_t launch_joint_prep(const KvImageArgs& kv, const RopeArgs& q, hipStream_t stream);
 
-// The persistent streaming attention kernel (attn_stream.hip): a.k = the key tile images; a.v = the value rows (bf16,
-// key j of kv head g at a.v + j * a.v_rs + g * 128, a.v_rs <= STREAM_MAX_V_RS; rows j < a.nkeys are read); a.q =
-// prepared queries (normalised and rotated, bf16 rows with stride a.q_rs; they may be the rows of a.out, which each
-// block reads before it overwrites them). nwg = workgroups (at most one per CU).
+// The persistent streaming attention kernel (attn_stream.hip): a.k = the key tile images, or with key_rows the key
+// rows (bf16, key j of kv head g at a.k + j * a.k_rs + g * a.k_hs, a.k_rs <= STREAM_MAX_V_RS); a.v = the value rows
+// (bf16, key j of kv head g at a.v + j * a.v_rs + g * a.v_hs, a.v_rs <= STREAM_MAX_V_RS; rows j < a.nkeys are read);
+// a.q = the queries as the attention reads them (bf16 rows with stride a.q_rs; they may be the rows of a.out, which
+// each block reads before it overwrites them). nwg = workgroups (at most one per CU).
 // Non-causal and causal (p0) calls, any W, H, HK, nkeys.
 // a.part / a.cnt: the partial area and arrival counters of the workspace (null: whole blocks only); nwg <=
 // STREAM_MAX_WG.
-hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream);
+hipError_t launch_stream(const AttnArgs& a, int nwg, hipStream_t stream, bool key_rows = false);
 constexpr int64_t STREAM_MAX_V_RS = (int64_t)1 << 24;                   // value row stride (elements) at most
 constexpr int STREAM_MAX_WG = 256;                                      // workgroups of one streaming launch at most
 constexpr int64_t STREAM_SLOT_BYTES = 8 * (64 * 64 * 4 + 64 * 8);        // one piece's partial: 8 waves' O, m and l

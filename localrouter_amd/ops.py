@@ -80,11 +80,17 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tens
     return out
 
 
+def attention_ws_bytes(w: int, heads: int, nkeys: int, causal: bool = False) -> int:
+    """lr_attention_ws_bytes: the workspace lr_attention_bf16_ws uses (0: none)."""
+    return int(_lib.load().lr_attention_ws_bytes(w, heads, nkeys, int(causal)))
+
+
 def attention_ws(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *,
                  causal: bool = False, p0: int = 0, scale: float = SCALE_128,
                  workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """lr_attention_bf16_ws: attention over value rows that splits few-query calls over the keys (flash-decoding);
-    q [w, heads, 128], k / v [nkeys, kv_heads, 128] with the same row stride."""
+    """lr_attention_bf16_ws: attention over key and value rows with device scratch: few-query calls split over the
+    keys (flash-decoding), other non-causal calls run the streaming kernel with its split tail; q [w, heads, 128],
+    k / v [nkeys, kv_heads, 128] with the same row stride."""
     w, heads = q.shape[0], q.shape[1]
     nkeys, kv_heads = k.shape[0], k.shape[1]
     q_rs, k_rs = _rows(q, "q", heads), _rows(k, "k", kv_heads)
@@ -93,7 +99,7 @@ def attention_ws(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.T
     if out is None:
         out = torch.empty((w, heads, D), dtype=torch.bfloat16, device=q.device)
     o_rs = _rows(out, "out", heads)
-    nb = int(_lib.load().lr_attention_ws_bytes(w, heads, nkeys, int(causal)))
+    nb = attention_ws_bytes(w, heads, nkeys, causal)
     if workspace is None and nb:
         workspace = torch.empty(nb, dtype=torch.uint8, device=q.device)
     _lib.call("lr_attention_bf16_ws", _ptr(q), _ptr(k), _ptr(v), _ptr(out), p0, w, heads, kv_heads, nkeys,

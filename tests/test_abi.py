@@ -266,11 +266,16 @@ def test_kmask_attention_rejects():
 
 def test_split_workspace_sizes_and_rejects():
     L = _lib.load()
-    assert L.lr_attention_ws_bytes(50220, 32, 50220, 0) == 0          # plenty of query blocks: no split
+    split_area = 2 * 256 * 8 * (64 * 64 * 4 + 64 * 8) + 4 * 256        # the streaming kernel's partials + counters
+    assert split_area == 69207040                                        # LR_JOINT_SPLIT_BYTES
+    assert L.lr_attention_ws_bytes(50220, 32, 50220, 0) == split_area   # plenty of query blocks: the split tail
     assert L.lr_attention_ws_bytes(218, 16, 50220, 1) == 0            # causal: never split
-    nb = L.lr_attention_ws_bytes(218, 16, 50220, 0)                   # K6 audio-from-video: split
-    assert nb >= 218 * 16 * 2 * 130 * 4
-    assert L.lr_attention_ws_bytes(218, 16, 300, 0) == 0              # too few key tiles to split
+    nb = L.lr_attention_ws_bytes(218, 16, 50220, 0)                   # K6 audio-from-video: split over the keys
+    assert nb >= 218 * 16 * 2 * 130 * 4 and nb != split_area
+    assert L.lr_attention_ws_bytes(218, 16, 300, 0) == 0              # too few key tiles to split or stream
+    assert L.lr_attention_ws_bytes(600, 16, 4096, 0) == split_area    # 48 blocks, 4,096 keys: the streaming kernel
+    assert L.lr_attention_ws_bytes(600, 16, 4095, 0) == 0             # fewer keys: the pipelined kernel
+    assert L.lr_attention_ws_bytes(2304, 16, 2000, 0) == 0
     fake = 1 << 20
     args = [fake, fake, fake, fake, 0, 218, 16, 16, 50220, 0, 0.088, 2048, 2048, 2048]
     assert L.lr_attention_bf16_ws(*args, fake, nb - 1, None) == HIP_ERROR_INVALID_VALUE   # workspace too small

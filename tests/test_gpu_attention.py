@@ -19,8 +19,9 @@ torch = pytest.importorskip("torch")
 
 from localrouter_amd import ops  # noqa: E402
 
-# plain attention over value rows (lr_attention_bf16_ex); the fused and prepared calls run the streaming kernel
-CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4]
+# attention over key and value rows (lr_attention_bf16_ex): the pipelined kernel's two tile shapes and the streaming
+# kernel reading key rows; the fused and prepared calls run the streaming kernel over key tile images
+CONFIGS = [ops.CFG_PIPE_W8, ops.CFG_PIPE_W4, ops.CFG_STREAM_W8]
 FUSED_CONFIGS = [ops.CFG_AUTO, ops.CFG_STREAM_W8]
 
 
@@ -115,31 +116,79 @@ def test_attention_overflowing_scores(cfg):
     assert_close(from_dev(out), _ref(q, kk, v), what=f"cfg{cfg}")
 
 
-def test_attention_keys_past_nkeys_ignored():
+@pytest.mark.parametrize("cfg", CONFIGS)
+def test_attention_keys_past_nkeys_ignored(cfg):
     """Rows past nkeys hold NaN; the kernel must neither read them into the result nor propagate them."""
-    print("\n[attention nkeys] W=100 nk=77 of 128 rows", flush=True)
+    print(f"\n[attention nkeys] cfg={cfg} W=100 nk=77 of 128 rows", flush=True)
     q, k, v = _qkv(13, 100, 128, 2, 2)
     k2, v2 = k.copy(), v.copy()
     k2[77:] = 0x7FC0  # bf16 NaN
     v2[77:] = 0x7FC0
-    out = ops.attention(to_dev(q), to_dev(k2), to_dev(v2), nkeys=77)
+    out = ops.attention(to_dev(q), to_dev(k2), to_dev(v2), nkeys=77, config=cfg)
     torch.cuda.synchronize()
     assert_close(from_dev(out), _ref(q[:, :, :], k[:77], v[:77]), what="nkeys")
 
 
-def test_attention_packed_qkv_strides():
+@pytest.mark.parametrize("cfg", CONFIGS)
+def test_attention_packed_qkv_strides(cfg):
     """q, k, v as views of one packed [S, 3, H, 128] buffer (row stride 3*H*128), output into a wider row buffer."""
-    print("\n[attention packed] S=190 H=3", flush=True)
+    print(f"\n[attention packed] cfg={cfg} S=190 H=3", flush=True)
     S, H = 190, 3
     qkv = oracle.synth_bf16(14, 1, (S, 3, H, 128))
     d = to_dev(qkv)
     outbuf = torch.zeros((S, 2 * H * 128), dtype=torch.bfloat16, device="cuda")
     out = outbuf[:, H * 128:].view(S, H, 128)
-    ops.attention(d[:, 0], d[:, 1], d[:, 2], out)
+    ops.attention(d[:, 0], d[:, 1], d[:, 2], out, config=cfg)
     torch.cuda.synchronize()
     ref = _ref(np.ascontiguousarray(qkv[:, 0]), np.ascontiguousarray(qkv[:, 1]), np.ascontiguousarray(qkv[:, 2]))
     assert_close(from_dev(out), ref, what="packed")
     assert not outbuf[:, : H * 128].any(), "wrote outside the output rows"
+
+
+@pytest.mark.parametrize("cfg", CONFIGS)
+def test_attention_head_major_kv(cfg):
+    """k and v head-major ([HK][nkeys][128]: kv-head stride nkeys*128, row stride 128) through lr_attention_bf16_ex,
+    GQA 4 / 2, causal with p0 and a ragged last key tile."""
+    from localrouter_amd import _lib
+    W, nk, H, HK, p0 = 200, 333, 4, 2, 133
+    print(f"\n[attention head-major] cfg={cfg} W={W} nk={nk} H={H} HK={HK}", flush=True)
+    q, k, v = _qkv(19, W, nk, H, HK)
+    dq = to_dev(q)
+    dk = to_dev(np.ascontiguousarray(k.transpose(1, 0, 2)))
+    dv = to_dev(np.ascontiguousarray(v.transpose(1, 0, 2)))
+    out = torch.zeros_like(dq)
+    _lib.call("lr_attention_bf16_ex", dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), p0, W, H, HK, nk, 1,
+              ops.SCALE_128, H * 128, 128, 128, H * 128, nk * 128, nk * 128, cfg,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert_close(from_dev(out), _ref(q, k, v, causal=True, p0=p0), what=f"head-major cfg{cfg}")
+
+
+@pytest.mark.parametrize("W,nk,H,HK,causal,p0", [(300, 4100, 17, 17, 0, 0), (513, 4097, 12, 6, 0, 0),
+                                                 (700, 999, 3, 1, 1, 299), (64, 4160, 33, 33, 0, 0)])
+def test_stream_rows_equal_images(W, nk, H, HK, causal, p0):
+    """The streaming kernel over key rows gathers each key tile into the layout of a tile image; over images of the same
+    keys (lr_joint_kv_prepare with every key a prefix key: copied unchanged) and the same queries
+    (lr_joint_attention_images, which cuts the last partial round of blocks over the workgroups when that pays) the
+    output must be the same bits. Non-causal: lr_attention_bf16_ws, which takes the streaming kernel from 4,096 keys and
+    33 query blocks on (the same split tail, its partials and counters in the caller's workspace); causal (never
+    split): lr_attention_bf16_ex with LR_ATTN_CFG_STREAM_W8."""
+    print(f"\n[stream rows = images] W={W} nk={nk} H={H} HK={HK} causal={causal}", flush=True)
+    q, k, v = _qkv(20, W, nk, H, HK)
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    ws = torch.empty(ops.workspace_bytes(nk, HK), dtype=torch.uint8, device="cuda")
+    ops.joint_kv_prepare(dk, dv, ws, table_kind=ops.TABLE_NONE, n_pre=nk)
+    img = ops.joint_attention_images(dq, ws, nk, HK, causal=bool(causal), p0=p0)
+    if causal:
+        rows = ops.attention(dq, dk, dv, causal=True, p0=p0, config=ops.CFG_STREAM_W8)
+    else:
+        # a workspace of stale bytes: the call clears the counters it needs
+        assert ops.attention_ws_bytes(W, H, nk, False) == 69207040   # the streaming kernel's split area
+        wsr = torch.full((ops.attention_ws_bytes(W, H, nk, False),), 0x5A, dtype=torch.uint8, device="cuda")
+        rows = ops.attention_ws(dq, dk, dv, workspace=wsr)
+    torch.cuda.synchronize()
+    assert torch.equal(rows, img)
+    assert_close(from_dev(rows), _ref(q, k, v, causal=bool(causal), p0=p0), what="stream rows")
 
 
 def test_attention_deterministic():

@@ -113,3 +113,33 @@ def test_split_overflow_reaches_exact_recomputation():
     rows = np.arange(0, Sq, 5)
     exp = _sign_ramp_expected(q[rows], k, v, 5.0, ops.SCALE_128)
     assert_close(got[rows], exp, what="split overflow")
+
+
+@pytest.mark.parametrize("Sq,Sk,H,HK", [(1280, 4500, 24, 24), (2048, 4096, 8, 2), (999, 4100, 9, 9),
+                                        (65792, 4096, 1, 1)])
+def test_rows_split_tail_parity(Sq, Sk, H, HK):
+    """The split tail over key rows (lr_attention_bf16_ws: the streaming kernel gathering key tiles from the rows, its
+    partials and counters in the caller's workspace): rows of cut blocks against the CPU oracle, three calls the same
+    bits."""
+    work, pieces, p = schedule(Sq, H, Sk, _cus())
+    assert p["nt"] is not None, "the shape must take the split schedule"
+    print(f"\n[rows split] Sq={Sq} Sk={Sk} H={H} HK={HK} cut blocks {len(pieces)}", flush=True)
+    q, k, v, _, _ = _case(64, Sq, Sk, H, HK)
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    ws = torch.empty(ops.attention_ws_bytes(Sq, H, Sk), dtype=torch.uint8, device="cuda")
+    got = from_dev(ops.attention_ws(dq, dk, dv, workspace=ws))
+    for _ in range(2):
+        again = from_dev(ops.attention_ws(dq, dk, dv, workspace=ws))
+        assert np.array_equal(again, got)
+    nqb = (Sq + 255) // 256
+    cut = sorted(p["nwhole"] + i for i in pieces)
+    rows = set()
+    for blk in [b for b in cut if b // nqb in (0, H - 1)][:12]:
+        r0 = (blk % nqb) * 256
+        rows.update(range(r0, min(r0 + 256, Sq), 3))
+    rows.update(np.random.default_rng(2).choice(Sq, size=min(Sq, 64), replace=False).tolist())
+    rows = np.array(sorted(rows))
+    ref = oracle.attention(bf16_f32(np.ascontiguousarray(q[rows])), bf16_f32(k), bf16_f32(v), precise=False)
+    for h in sorted({0, H - 1}):
+        assert_close(got[rows][:, h], ref[:, h], what=f"rows split Sq={Sq} head {h}")
+    assert np.isfinite(bf16_f32(got)).all()
