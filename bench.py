@@ -195,6 +195,10 @@ def main():
     ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS) + ["h3-int8", "mmdit"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--operands", default="randn", choices=["randn", "zeros"],
+                    help="q, k, v data: randn = N(0, 1) (BASELINE's, the default); zeros = all zero, a power study: the "
+                         "same kernels and schedule with operands that toggle no multiplier bits (not a BASELINE "
+                         "measurement)")
     ap.add_argument("--preroll-s", type=float, default=PREROLL_S,
                     help="seconds of untimed calls after the warm-up and before timing (the GPU's clock settles)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -209,6 +213,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.operands != "randn" and args.workload in ("h3-int8", "mmdit"):
+        raise SystemExit("bench.py: --operands applies to the joint-attention workloads")
     if args.workload == "h3-int8":
         return bench_int8(args)
     if args.workload == "mmdit":
@@ -242,6 +248,8 @@ def main():
     q = torch.randn((Sq, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     k = torch.randn((Sk, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     v = torch.randn((Sk, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    if args.operands == "zeros":
+        q.zero_(), k.zero_(), v.zero_()
     out = torch.empty_like(q)
     cos = torch.from_numpy(cos_np).to(dev)
     sin = torch.from_numpy(sin_np).to(dev)
@@ -332,10 +340,11 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic",
+        "data": "synthetic" if args.operands == "randn" else "synthetic zeros (power study, not BASELINE's N(0,1))",
         "config": {"workload": f"{args.workload}-joint-attention", "batch": 1, "tokens": Sq, "keys": Sk,
                    "prefix_keys": n_pre, "text_tokens": w["n_text"], "heads": H, "head_dim": 128, "causal": False,
-                   "qk_rmsnorm": True, "rope": w["kind"], "parallelism": "none (1 GPU)"},
+                   "qk_rmsnorm": True, "rope": w["kind"], "operands": "N(0,1)" if args.operands == "randn" else "zeros",
+                   "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic_from_profile(args.workload, KERNEL),

@@ -59,6 +59,8 @@ def _oracle_rows(q, k, v, cos, sin, Sq, Sk, rows):
     (2048, 2048, 8, 2),       # GQA 4:1, 64 blocks of 32 tiles
     (999, 1100, 7, 7),        # ragged last key tile and query block
     (65792, 512, 1, 1),       # 257 blocks: one whole round, then one block cut over 3 workgroups
+    (4608, 4608, 24, 24),     # BASELINE cfg2: 176 of 432 blocks cut, 2-3 pieces each
+    (2304, 4000, 24, 6),      # 216 blocks of 63 tiles, all tail, GQA 4:1
 ])
 def test_split_tail_parity(Sq, Sk, H, HK):
     nwg = _cus()
