@@ -88,9 +88,10 @@ def attention_ws_bytes(w: int, heads: int, nkeys: int, causal: bool = False) -> 
 def attention_ws(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *,
                  causal: bool = False, p0: int = 0, scale: float = SCALE_128,
                  workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """lr_attention_bf16_ws: attention over key and value rows with device scratch: few-query calls split over the
-    keys (flash-decoding), other non-causal calls run the streaming kernel with its split tail; q [w, heads, 128],
-    k / v [nkeys, kv_heads, 128] with the same row stride."""
+    """lr_attention_bf16_ws: attention over key and value rows with device scratch: non-causal calls of at most 32
+    query blocks split over the keys (flash-decoding), others of at least 4,096 keys run the streaming kernel over the
+    key rows with its split tail, the rest run as lr_attention_bf16; q [w, heads, 128], k / v [nkeys, kv_heads, 128]
+    with the same row stride. A workspace of attention_ws_bytes is allocated when none is given."""
     w, heads = q.shape[0], q.shape[1]
     nkeys, kv_heads = k.shape[0], k.shape[1]
     q_rs, k_rs = _rows(q, "q", heads), _rows(k, "k", kv_heads)

@@ -1,11 +1,12 @@
 """Graph capture of the library's calls: lr_joint_attention_fused, lr_joint_attention_fused_noalloc (after
-lr_attn_init), lr_int8_attention_rows and lr_mmdit_block_bf16 recorded into one HIP graph (torch.cuda.CUDAGraph) and
-replayed, each replay compared bit for bit with the same calls made eagerly.
+lr_attn_init), lr_attention_bf16_ws (the streaming kernel over key rows with its split tail, and the key split of a
+few-query call), lr_int8_attention_rows and lr_mmdit_block_bf16 recorded into one HIP graph (torch.cuda.CUDAGraph)
+and replayed, each replay compared bit for bit with the same calls made eagerly.
 
 The reference records whole denoising steps the same way and falls back to eager launches when capture fails
 (src/engines/qwen_image/dit.zig:469-484, src/engines/minimax_h3/dit.zig:557-577). The library's calls neither
 synchronise nor allocate and issue no memset (the split tail's arrival counters are cleared by the preparation
-kernel), so the captured graph holds kernels only. Between the replays the program does eager work of its own (the
+kernel, or over key rows by a one-workgroup fill kernel), so the captured graph holds kernels only. Between the replays the program does eager work of its own (the
 outputs are cleared with torch's fill kernel, the MMDiT streams restored) and synchronises; every replay must give
 the eager bits."""
 from __future__ import annotations
@@ -45,6 +46,14 @@ def test_graph_capture_replays_equal_eager():
     Si, Hi = 300, 4
     qkv = to_dev(oracle.synth_bf16(12, 1, (Si, 3 * Hi * 128)))
     ws8 = torch.empty(ops.int8_workspace_bytes(Hi, Si), dtype=torch.uint8, device=dev)
+    # attention over rows with a workspace: 1,280 queries x 8 heads over 4,096 keys (40 query blocks: the streaming
+    # kernel over key rows, its split tail's partials and counters in the workspace) and 218 x 4 heads over 2,000 keys
+    # (4 query blocks: split over the keys, then merged)
+    rows_cases = [(1280, 8, 4096), (218, 4, 2000)]
+    rows_in = [tuple(to_dev(oracle.synth_bf16(13 + i, j, (nk if j else W, Hr, 128))) for j in (0, 1, 2))
+               for i, (W, Hr, nk) in enumerate(rows_cases)]
+    rows_ws = [torch.empty(ops.attention_ws_bytes(W, Hr, nk), dtype=torch.uint8, device=dev) for W, Hr, nk in rows_cases]
+    assert rows_ws[0].numel() == 69207040 and 0 < rows_ws[1].numel() != 69207040
     # MMDiT block: 16 text + 6x8 image rows, hidden 256 (2 heads), MLP 512
     Dm, Fm, n_txt, gh, gw = 256, 512, 16, 6, 8
     wts = mmdit.make_weights(Dm, Fm, dev, seed=3, std=0.05)
@@ -58,6 +67,8 @@ def test_graph_capture_replays_equal_eager():
     tt = torch.tensor([0.3], dtype=torch.float32, device=dev)
 
     outs = {name: torch.empty_like(q) for name in ("fused", "noalloc")}
+    for i, (qr, _, _) in enumerate(rows_in):
+        outs[f"rows{i}"] = torch.empty_like(qr)
     out8 = torch.empty((Si, Hi * 128), dtype=torch.bfloat16, device=dev)
     txt, img = txt0.clone(), img0.clone()
 
@@ -67,6 +78,8 @@ def test_graph_capture_replays_equal_eager():
                                           ws.numel(), sh) == 0
         assert L.lr_joint_attention_fused_noalloc(*_fused_args(q, k, v, outs["noalloc"], cos, sin, S, S, H, H),
                                                   sh) == 0
+        for i, (qr, kr, vr) in enumerate(rows_in):
+            ops.attention_ws(qr, kr, vr, outs[f"rows{i}"], workspace=rows_ws[i])
         ops.kitchen_attention(qkv, Hi, out=out8, workspace=ws8, rows=True)
         blk(txt, img, tt, mcos, msin)
 
