@@ -1,12 +1,13 @@
 // Persistent streaming joint attention for gfx950: bf16 in, fp32 MFMA accumulation and softmax, bf16 out, over keys
-// prepared as tile images (tile_image.h, written by kv_image.hip) and values read as they are, as bf16 rows.
+// prepared as tile images (tile_image.h, written by kv_image.hip) or, in the key-rows instantiation, gathered into the
+// same tile layout in LDS straight from the caller's key rows, and values read as they are, as bf16 rows.
 //
 // Semantics: the reference's kernels/cuda/qwen_image/attention.cu:253-444 (pattn2_kernel) as launched by
 // src/engines/qwen_image/ops_launch.zig:163-172: O_i = softmax_j(scale <q_i, k_j>) v_j over keys j < nkeys (and
 // j <= p0 + i when causal, attention.cu:304), query head h reading kv head h / (H / HK) (attention.cu:264-266), P
 // rounded to bf16 for the P V product (attention.cu:418-424), output rounded to bf16 (attention.cu:432-443). The
-// queries arrive normalised and rotated (bf16 rows, the reference's rope_q output, dit.zig:252-257), the keys and
-// values as tile images.
+// queries arrive normalised and rotated (bf16 rows, the reference's rope_q output, dit.zig:252-257), the keys as tile
+// images or rows, the values as rows.
 //
 // Design (two waves per SIMD, 8 waves = 256 queries per block, 32 queries per wave; each 1 KB operand fragment read
 // from LDS feeds one v_mfma_f32_32x32x16_bf16, 128 bytes per clock per CU at the MFMA rate, half of gfx950's LDS read
