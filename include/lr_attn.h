@@ -115,8 +115,8 @@ int lr_attention_bf16_ex(const void* q, const void* k, const void* v, void* out,
  * run LR_ATTN_CFG_STREAM_W8 over the key rows, whose last partial round of query blocks is cut over all workgroups
  * along the keys, the pieces' partials and arrival counters in the workspace (LR_JOINT_SPLIT_BYTES; the call clears
  * the counters itself). Every other call runs as lr_attention_bf16. lr_attention_ws_bytes is the workspace the call
- * needs (0: none; workspace may then be NULL). Results equal lr_attention_bf16's to fp32 rounding. Calls that overlap
- * on one workspace race.
+ * needs (0: none; workspace may then be NULL); those bytes must not overlap q, k, v or out (rejected). Results equal
+ * lr_attention_bf16's to fp32 rounding. Calls that overlap on one workspace race.
  */
 size_t lr_attention_ws_bytes(int W, int H, int nkeys, int causal);
 int lr_attention_bf16_ws(const void* q, const void* k, const void* v, void* out, int p0, int W, int H, int HK,

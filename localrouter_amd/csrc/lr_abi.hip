@@ -551,6 +551,15 @@ int lr_attention_bf16_ws(const void* q, const void* k, const void* v, void* out,
     if (workspace_bytes < lr_attention_ws_bytes(W, H, nkeys, causal) || (workspace && !aligned(workspace, 256)))
         return ERR_ARGS;
     if (workspace_bytes > 0 && !workspace) return ERR_ARGS;
+    // the call writes partials to the bytes of the workspace it needs while it reads q, k and v and writes out
+    const size_t need = lr_attention_ws_bytes(W, H, nkeys, causal);
+    if (need > 0 && HK >= 1 && q && k && v && out) {
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(workspace);
+        const Span w{lo, lo + need};
+        if (overlap(w, rows_span(q, W, q_row_stride, H)) || overlap(w, rows_span(k, nkeys, kv_row_stride, HK)) ||
+            overlap(w, rows_span(v, nkeys, kv_row_stride, HK)) || overlap(w, rows_span(out, W, out_row_stride, H)))
+            return ERR_ARGS;
+    }
     return attention_impl(q, k, v, out, p0, W, H, HK, nkeys, causal, scale, q_row_stride, kv_row_stride,
                           kv_row_stride, out_row_stride, lr::D, lr::D, LR_ATTN_CFG_AUTO,
                           reinterpret_cast<hipStream_t>(stream), workspace, workspace_bytes);

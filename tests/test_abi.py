@@ -277,6 +277,13 @@ def test_split_workspace_sizes_and_rejects():
     assert L.lr_attention_ws_bytes(600, 16, 4095, 0) == 0             # fewer keys: the pipelined kernel
     assert L.lr_attention_ws_bytes(2304, 16, 2000, 0) == 0
     fake = 1 << 20
+    # a workspace overlapping q, k, v or out is rejected before any launch (the call writes partials there)
+    q_, k_, v_, o_ = 1 << 40, 2 << 40, 3 << 40, 4 << 40
+    rows_args = [q_, k_, v_, o_, 0, 600, 16, 16, 8000, 0, 0.088, 2048, 2048, 2048]
+    nbs = L.lr_attention_ws_bytes(600, 16, 8000, 0)
+    assert nbs == split_area
+    for bad in (q_ + 256, k_ + (8000 - 1) * 2048 * 2, v_, o_ - nbs + 256):
+        assert L.lr_attention_bf16_ws(*rows_args, bad, nbs, None) == HIP_ERROR_INVALID_VALUE, hex(bad)
     args = [fake, fake, fake, fake, 0, 218, 16, 16, 50220, 0, 0.088, 2048, 2048, 2048]
     assert L.lr_attention_bf16_ws(*args, fake, nb - 1, None) == HIP_ERROR_INVALID_VALUE   # workspace too small
     assert L.lr_attention_bf16_ws(*args, None, nb, None) == HIP_ERROR_INVALID_VALUE       # size without a pointer
