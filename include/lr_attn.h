@@ -129,8 +129,9 @@ int lr_attention_bf16_ws(const void* q, const void* k, const void* v, void* out,
  * (src/engines/kandinsky6/dit/attention.zig:21-27, dispatched by launch.zig:239-255). Non-causal; q, out rows
  * [W][H*128], k, v rows [nkeys][HK*128] (kv_row_stride for both). kmask: device u8 [nkeys]; n_valid: the number of
  * nonzero bytes, known on the host as the engine's `valid` (1 <= n_valid <= nkeys). The kept keys and value rows are
- * gathered into the workspace, then attended as lr_attention_bf16 does. kmask = NULL: no mask (n_valid = nkeys, no
- * workspace needed).
+ * gathered into the workspace, then attended as lr_attention_bf16 does; the workspace's first
+ * lr_attention_kmask_workspace_bytes bytes must not overlap kmask, q, k, v or out (rejected). kmask = NULL: no mask
+ * (n_valid = nkeys, no workspace needed).
  */
 size_t lr_attention_kmask_workspace_bytes(int n_valid, int HK);
 int lr_attention_kmask_bf16(const void* q, const void* k, const void* v, void* out, const void* kmask, int n_valid,

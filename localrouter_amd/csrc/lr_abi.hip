@@ -588,6 +588,16 @@ int lr_attention_kmask_bf16(const void* q, const void* k, const void* v, void* o
     if (W < 1 || H < 1 || HK < 1 || H % HK != 0 || !scale_ok(scale) || !rows_ok(q, q_row_stride, H) ||
         !rows_ok(out, out_row_stride, H) || W > INT_MAX - 512 || nkeys > INT_MAX - 512)
         return ERR_ARGS;
+    // the compaction writes the kept keys' indices, keys and values to the workspace while it reads kmask, k and v,
+    // and the attention then reads them beside q and writes out: the workspace's bytes overlap none of those
+    {
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(workspace), mk = reinterpret_cast<uintptr_t>(kmask);
+        const Span w{lo, lo + need};
+        if (overlap(w, Span{mk, mk + (uintptr_t)nkeys}) || overlap(w, rows_span(k, nkeys, kv_row_stride, HK)) ||
+            overlap(w, rows_span(v, nkeys, kv_row_stride, HK)) || overlap(w, rows_span(q, W, q_row_stride, H)) ||
+            overlap(w, rows_span(out, W, out_row_stride, H)))
+            return ERR_ARGS;
+    }
     char* ws = static_cast<char*>(workspace);
     const size_t idx_bytes = ((size_t)n_valid * 4 + 255) & ~(size_t)255;
     const size_t rows = (((size_t)n_valid * HK * lr::D * 2) + 255) & ~(size_t)255;

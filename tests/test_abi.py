@@ -262,6 +262,10 @@ def test_kmask_attention_rejects():
     assert call(kv_rs=255) == HIP_ERROR_INVALID_VALUE
     assert call(H=3) == HIP_ERROR_INVALID_VALUE                 # H % HK
     assert call(scale=0.0) == HIP_ERROR_INVALID_VALUE
+    # a workspace overlapping kmask, k, v, q or out (the compaction writes it while they are read)
+    base = dict(q=1 << 40, k=2 << 40, v=3 << 40, out=4 << 40, kmask=5 << 40)
+    for name in base:
+        assert call(**base, ws=base[name]) == HIP_ERROR_INVALID_VALUE, name
 
 
 def test_split_workspace_sizes_and_rejects():
