@@ -291,7 +291,9 @@ int lr_joint_attention_fused_noalloc(const void* q_raw, const void* k_raw, const
  *   D 128 (the engine's, launch.zig:331) or 64 (the wheel's other case, kitchen_launch.cu:196-241: H4 up to 256 keys,
  *   else the plain H64 without the sign flip, 64-key tiles at every length); H a multiple of HK; scale > 0 (the
  *   reference passes D^-0.5 rounded to fp32: 0x3db504f3 for 128);
- *   workspace: lr_int8_attention_workspace_bytes(B, H, HK, Sq, Sk, D) bytes, 256-byte aligned, no initial contents.
+ *   workspace: lr_int8_attention_workspace_bytes(B, H, HK, Sq, Sk, D) bytes, 256-byte aligned, no initial contents;
+ *              those bytes must not overlap q, k, v, out (or, fused with rmsRope, the table and the norm weights):
+ *              rejected before any launch.
  * lr_int8_attention writes out bf16 [B][H][Sq][D] contiguous; lr_int8_attention_rows writes rows [Sq][H * D]
  * (B must be 1), the same values. The workspace layout is this library's own (quantised operands, scales, per-tile
  * column sums): it is written by the prep and read by the kernel, nothing else.

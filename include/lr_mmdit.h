@@ -88,7 +88,8 @@ int lr_mmdit_linear_bf16(void* ctx, const void* x, int64_t ldx, const void* w, v
  * f32 timestep. cos, sin: device [n_txt + n_img, 64] f32 (text rows first). Weights 16-byte aligned. The shape
  * must have been planned (lr_mmdit_plan or lr_mmdit_tune): otherwise it returns hipErrorNotReady (600) and launches
  * nothing. Launches only (no host planning, no synchronisation); calls on one context may come from several threads,
- * each with its own workspace. */
+ * each with its own workspace. The workspace's first lr_mmdit_workspace_bytes bytes must not overlap txt, img, t, cos,
+ * sin or a weight (rejected before any launch). */
 int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* img, int n_txt, int n_img, int hidden,
                         int mlp, const float* t, const float* cos, const float* sin, void* workspace,
                         size_t workspace_bytes, lr_stream_t stream);

@@ -188,6 +188,11 @@ inline Span ws_span(const void* ws, int Sk, int HK) {
     return Span{lo, lo + ws_bytes_needed(Sk, HK)};
 }
 inline bool overlap(Span a, Span b) { return a.lo < b.hi && b.lo < a.hi; }
+// byte range of a bf16 [B][X][S][D] tensor with element strides sb, sx, sn (a row's D elements contiguous)
+inline Span t4_span(const void* p, int B, int X, int S, int D, int64_t sb, int64_t sx, int64_t sn) {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+    return Span{lo, lo + (uintptr_t)(((int64_t)(B - 1) * sb + (int64_t)(X - 1) * sx + (int64_t)(S - 1) * sn + D) * 2)};
+}
 
 // Checks of the keys stage: k_raw and v rows, the key norm weight and table, the workspace.
 bool kv_stage_ok(const void* k_raw, int64_t k_rs, const void* v, int64_t v_rs, const float* wk, int table_kind,
@@ -435,6 +440,22 @@ int i8_prep_impl(const void* q, const void* k, const void* v, void* ws, int B, i
     if (!i8_tensor_ok(q, q_sb, q_sh, q_sn, B, H, Sq) || !i8_tensor_ok(k, k_sb, k_sh, k_sn, B, HK, Sk) ||
         !i8_tensor_ok(v, v_sb, v_sh, v_sn, B, HK, Sk))
         return ERR_ARGS;
+    // the prep writes the workspace while it reads q, k, v (and, fused with rmsRope, the table and the norm weights)
+    {
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(ws);
+        const Span w{lo, lo + lr::i8::plan_of(B, H, HK, Sq, Sk, D).total};
+        if (overlap(w, t4_span(q, B, H, Sq, D, q_sb, q_sh, q_sn)) ||
+            overlap(w, t4_span(k, B, HK, Sk, D, k_sb, k_sh, k_sn)) ||
+            overlap(w, t4_span(v, B, HK, Sk, D, v_sb, v_sh, v_sn)))
+            return ERR_ARGS;
+        if (rope_tab) {
+            const uintptr_t t = reinterpret_cast<uintptr_t>(rope_tab);
+            const uintptr_t qn = reinterpret_cast<uintptr_t>(qw), kn = reinterpret_cast<uintptr_t>(kw);
+            if (overlap(w, Span{t, t + (uintptr_t)(((int64_t)(Sk - 1) * tab_rs + 2 * (int64_t)rot) * 2)}) ||
+                overlap(w, Span{qn, qn + 2 * (uintptr_t)D}) || overlap(w, Span{kn, kn + 2 * (uintptr_t)D}))
+                return ERR_ARGS;
+        }
+    }
     lr::i8::PrepArgs a{};
     a.q = static_cast<const uint16_t*>(q);
     a.k = static_cast<const uint16_t*>(k);
@@ -458,6 +479,11 @@ int i8_kernel_impl(void* out, const void* ws, int B, int H, int HK, int Sq, int 
                    hipStream_t stream) {
     if (!i8_sizes_ok(B, H, HK, Sq, Sk, D) || !ws || !aligned(ws, 256) || !out || !aligned(out, 16)) return ERR_ARGS;
     if (!scale_ok(scale) || (o_rows != 0 && o_rows != 1) || (o_rows && B != 1)) return ERR_ARGS;
+    {   // the kernel writes out while it reads the workspace
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(ws), o = reinterpret_cast<uintptr_t>(out);
+        const Span w{lo, lo + lr::i8::plan_of(B, H, HK, Sq, Sk, D).total};
+        if (overlap(w, Span{o, o + (uintptr_t)B * H * Sq * D * 2})) return ERR_ARGS;
+    }
     lr::i8::AttnArgs a{};
     a.ws = static_cast<const uint8_t*>(ws);
     a.out = static_cast<uint16_t*>(out);
@@ -477,6 +503,11 @@ int i8_attention_impl(const void* q, const void* k, const void* v, void* out, vo
     // every argument is checked before the first launch
     if (!i8_sizes_ok(B, H, HK, Sq, Sk, D) || !out || !aligned(out, 16) || !scale_ok(scale) || (o_rows && B != 1))
         return ERR_ARGS;
+    {   // out against the workspace (the kernel stage's check) before the prep launches
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(ws), o = reinterpret_cast<uintptr_t>(out);
+        const Span w{lo, lo + lr::i8::plan_of(B, H, HK, Sq, Sk, D).total};
+        if (overlap(w, Span{o, o + (uintptr_t)B * H * Sq * D * 2})) return ERR_ARGS;
+    }
     const int e = i8_prep_impl(q, k, v, ws, B, H, HK, Sq, Sk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn,
                                stream);
     if (e != 0) return e;

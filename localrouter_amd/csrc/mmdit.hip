@@ -622,6 +622,21 @@ int lr_mmdit_block_bf16(void* ctx, const lr_mmdit_weights* w, void* txt, void* i
     for (const void* p : ptrs)
         if (!p || ((uintptr_t)p & 15) != 0) return hipErrorInvalidValue;
     if ((((uintptr_t)txt | (uintptr_t)img | (uintptr_t)workspace) & 15) != 0) return hipErrorInvalidValue;
+    {   // the workspace holds the block's intermediates while txt and img are updated and everything else is read
+        const uintptr_t lo = (uintptr_t)workspace, hi = lo + need;
+        const size_t D = (size_t)hidden, F = (size_t)mlp, S = (size_t)n_txt + (size_t)n_img;
+        const struct { const void* p; size_t bytes; } spans[] = {
+            {txt, (size_t)n_txt * D * 2}, {img, (size_t)n_img * D * 2}, {cos, S * 64 * 4}, {sin, S * 64 * 4},
+            {t, 4}, {w->t1, D * 256 * 2}, {w->t2, D * D * 2}, {w->q_norm, 128 * 4}, {w->k_norm, 128 * 4},
+            {w->txt.mod, 6 * D * D * 2}, {w->txt.qkv, 3 * D * D * 2}, {w->txt.out, D * D * 2},
+            {w->txt.mlp_up, F * D * 2}, {w->txt.mlp_down, D * F * 2}, {w->img.mod, 6 * D * D * 2},
+            {w->img.qkv, 3 * D * D * 2}, {w->img.out, D * D * 2}, {w->img.mlp_up, F * D * 2},
+            {w->img.mlp_down, D * F * 2}};
+        for (const auto& sp : spans) {
+            const uintptr_t a = (uintptr_t)sp.p;
+            if (sp.bytes > 0 && a < hi && lo < a + sp.bytes) return hipErrorInvalidValue;
+        }
+    }
 
     Ctx& c = *static_cast<Ctx*>(ctx);
     // every row GEMM's plan exists (lr_mmdit_plan / lr_mmdit_tune), checked before anything is launched; the

@@ -4,6 +4,7 @@ from __future__ import annotations
 
 import ctypes
 import re
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -209,6 +210,12 @@ def test_int8_rejects():
     assert call(**dict(d64, D=96)) == HIP_ERROR_INVALID_VALUE             # only 64 and 128
     assert call(**dict(d64, k_sn=100)) == HIP_ERROR_INVALID_VALUE          # head dim 64 keeps the stride rule
     assert L.lr_int8_attention_kernel(A, 0x100000, 1, 2, 2, 8, 8, 128, 0.088, 2, None) == HIP_ERROR_INVALID_VALUE
+    # a workspace overlapping q, k, v (written by the prep while they are read) or out (read while out is written)
+    for name in ("q", "k", "v", "o"):
+        far = dict(q=1 << 40, k=2 << 40, v=3 << 40, o=4 << 40)
+        assert call(**far, ws=far[name] + 256) == HIP_ERROR_INVALID_VALUE, name
+    assert L.lr_int8_attention_kernel(0x100000 + 4096, 0x100000, 1, 2, 2, 8, 8, 128, 0.088, 1,
+                                      None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_int8_attention_prep(A, A, A, A + 64, 1, 2, 2, 8, 8, 128, 0, 768, 1536, 0, 768, 1536, 0, 768, 1536,
                                     None) == HIP_ERROR_INVALID_VALUE
 
@@ -240,6 +247,30 @@ def test_mmdit_abi_on_cpu():
                                  None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_mmdit_create(None) == HIP_ERROR_INVALID_VALUE
     assert L.lr_mmdit_destroy(None) == HIP_ERROR_INVALID_VALUE
+    # a workspace overlapping txt, img, the tables, t or a weight is rejected before the context is used (run in a child
+    # process: a missed check would dereference the stand-in context)
+    code = """
+import ctypes, sys
+sys.path.insert(0, %r)
+from localrouter_amd import mmdit
+L = mmdit.lib()
+T = 1 << 40
+w = mmdit.Weights(t1=T + (1 << 30), t2=T + (2 << 30), q_norm=T + (3 << 30), k_norm=T + (4 << 30),
+                  txt=mmdit.StreamWeights(*[T + ((5 + i) << 30) for i in range(5)]),
+                  img=mmdit.StreamWeights(*[T + ((10 + i) << 30) for i in range(5)]))
+txt, img, tt, cos, sin = T + (20 << 30), T + (21 << 30), T + (22 << 30), T + (23 << 30), T + (24 << 30)
+need = mmdit.workspace_bytes(16, 48, 256, 512)
+ctx = ctypes.c_void_p(0x1000)
+for ws in (txt + 4096, img, tt - need + 16, cos + 256, sin, w.t1, w.txt.qkv + 1024, w.img.mlp_down):
+    print(L.lr_mmdit_block_bf16(ctx, ctypes.byref(w), ctypes.c_void_p(txt), ctypes.c_void_p(img), 16, 48, 256, 512,
+                                ctypes.c_void_p(tt), ctypes.c_void_p(cos), ctypes.c_void_p(sin), ctypes.c_void_p(ws),
+                                need, None))
+""" % str(Path(__file__).resolve().parents[1])
+    import subprocess
+    import sys
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    assert res.stdout.split() == [str(HIP_ERROR_INVALID_VALUE)] * 8
     assert L.lr_mmdit_plan(None, 8, 16, 256, 512) == HIP_ERROR_INVALID_VALUE
 
 
