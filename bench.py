@@ -1,7 +1,7 @@
 """Benchmark of the DiT joint-attention hot path on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--preroll-s SECONDS]
-                    [--workload qwen-step|plumbing|edit|video|qwen21|h3-int8|mmdit] [--no-cpu-baseline]
+                    [--workload qwen-step|plumbing|edit|video|qwen21|h3-int8|mmdit|k6] [--no-cpu-baseline]
 
 A step is one lr_joint_attention_fused call over one synthetic batch: the preparation launch (keys RMSNorm + RoPE into
 the workspace's tile images, queries RMSNorm + RoPE into the output rows), then the persistent streaming attention
@@ -39,6 +39,14 @@ weights N(0, 0.02), activations N(0, 1)): a step is one lr_mmdit_block_bf16 call
 FLOPs per block = the GEMMs + the joint attention (elementwise work not counted). `roofline` is the block's largest
 GEMM (the image stream's MLP up-projection, 4096 x 12288 x 3072) timed alone through lr_mmdit_linear_bf16;
 `cpu_baseline` is the numpy fp32 oracle of the whole block (multithreaded BLAS) on the same inputs.
+
+--workload k6 measures Kandinsky-6's attention calls (src/engines/kandinsky6/dit/launch.zig:260-300): a step is one
+call of each of the four unmasked shapes its flash dispatch takes (visual self-attention 50,220 x 32 heads,
+video-from-audio 50,220 <- 218 keys x 32 heads, audio-from-video 218 <- 50,220 keys x 16 heads, audio self 218 x 16
+heads; rows of heads x 128, scale f32(1/sqrt(128))), each through lr_attention_bf16_ws, the library's route for
+attention over key and value rows with device scratch. FLOPs per step = the sum of 4 * Sq * Sk * 128 * H. `roofline`
+is the visual self-attention (the streaming kernel over key rows, attn_stream_kernel<true>, 99 % of the FLOPs) timed
+alone; `cpu_baseline` is the CPU oracle's fp32 flash path on a sample of the visual call's query rows.
 """
 from __future__ import annotations
 
@@ -192,7 +200,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS) + ["h3-int8", "mmdit"])
+    ap.add_argument("--workload", default="qwen-step", choices=sorted(WORKLOADS) + ["h3-int8", "mmdit", "k6"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--operands", default="randn", choices=["randn", "zeros"],
@@ -213,12 +221,14 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    if args.operands != "randn" and args.workload in ("h3-int8", "mmdit"):
+    if args.operands != "randn" and args.workload in ("h3-int8", "mmdit", "k6"):
         raise SystemExit("bench.py: --operands applies to the joint-attention workloads")
     if args.workload == "h3-int8":
         return bench_int8(args)
     if args.workload == "mmdit":
         return bench_mmdit(args)
+    if args.workload == "k6":
+        return bench_k6(args)
 
     import numpy as np
     import torch
@@ -723,6 +733,166 @@ def bench_mmdit(args):
         log(f"[bench] cpu {flops / cpu_s / 1e12:.4f} TFLOP/s ({cpu_s:.2f} s); GPU vs oracle max-abs {d.max():.3e} "
             f"mean-abs {d.mean():.3e}")
     blk.close()
+    print(json.dumps(result), flush=True)
+
+
+
+# Kandinsky-6's flash-dispatched attention shapes (src/engines/kandinsky6/dit/launch.zig:260-300): (name, queries, keys,
+# heads); q, k, v and out are rows of heads x 128 (row stride 4096 for 32 heads, 2048 for 16)
+K6_SHAPES = [("visual-self", 50220, 50220, 32), ("video-from-audio", 50220, 218, 32),
+             ("audio-from-video", 218, 50220, 16), ("audio-self", 218, 218, 16)]
+
+
+def bench_k6(args):
+    import numpy as np
+    import torch
+
+    from localrouter_amd import _lib, ops
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    L = _lib.load()
+    rc = L.lr_attn_init()
+    if rc != 0:
+        raise SystemExit(f"lr_attn_init: {rc} (not a gfx950?)")
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    scale = ops.SCALE_128
+    ws_bytes = max(ops.attention_ws_bytes(W, H, S) for _, W, S, H in K6_SHAPES)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    calls = []
+    for name, W, S, H in K6_SHAPES:
+        q = torch.randn((W, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        k = torch.randn((S, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        v = torch.randn((S, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        rs = H * 128
+        argv = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), 0, W, H, H, S, 0, scale, rs, rs, rs,
+                ws.data_ptr(), ws_bytes, sh)
+        calls.append(dict(name=name, W=W, S=S, H=H, q=q, k=k, v=v, out=out, argv=argv,
+                          flops=4.0 * W * S * 128 * H))
+        log(f"[bench] k6 {name}: {W} queries over {S} keys, {H} heads; workspace route "
+            f"{'split/stream' if ops.attention_ws_bytes(W, H, S) else 'plain'}")
+
+    def run(c):
+        _lib.call("lr_attention_bf16_ws", *c["argv"])
+
+    def step():
+        for c in calls:
+            run(c)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    pre_calls, pre_s = preroll(step, args.preroll_s)
+    log(f"[bench] warmup {args.warmup} done, pre-roll {pre_calls} steps in {pre_s:.2f} s; timing {args.steps} steps")
+
+    K = args.steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    e0.record(stream)
+    for _ in range(K):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms_step = e0.elapsed_time(e1) / K
+    # the same steps with an event between the calls: each shape's time
+    n = len(calls)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n * K + 1)]
+    torch.cuda.synchronize()
+    for i in range(K):
+        for j, c in enumerate(calls):
+            ev[n * i + j].record(stream)
+            run(c)
+    ev[n * K].record(stream)
+    torch.cuda.synchronize()
+    per = {c["name"]: float(np.mean([ev[n * i + j].elapsed_time(ev[n * i + j + 1]) for i in range(K)]))
+           for j, c in enumerate(calls)}
+    flops = sum(c["flops"] for c in calls)
+    value = flops / (ms_step * 1e-3) / 1e12
+    vis = calls[0]
+    achieved = vis["flops"] / (per[vis["name"]] * 1e-3) / 1e12
+    clock = from_profile("k6", KERNEL, "clock_ghz")
+    log(f"[bench] step {ms_step:.4f} ms = {value:.1f} TFLOP/s; " + ", ".join(
+        f"{c['name']} {per[c['name']]:.4f} ms ({c['flops'] / (per[c['name']] * 1e-3) / 1e12:.1f} TFLOP/s)"
+        for c in calls) + f"; visual self-attention {100 * achieved / PEAK_BF16_TFLOPS:.1f}% of bf16 peak; "
+        f"wall {wall:.3f} s")
+    result = {
+        "metric": "K6 attention TFLOP/s + % bf16 MFMA peak; ms per step of the four Kandinsky-6 attention shapes",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "preroll": {"calls": pre_calls, "seconds": round(pre_s, 3),
+                    "note": "untimed steps after the warm-up, the same for every --warmup"},
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "k6-attention", "shapes": [dict(name=c["name"], queries=c["W"], keys=c["S"],
+                                                                 heads=c["H"]) for c in calls],
+                   "head_dim": 128, "causal": False, "operands": "N(0,1)", "entry_point": "lr_attention_bf16_ws",
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic_from_profile("k6", KERNEL),
+                     "kernel": KERNEL + "<true> (visual self-attention)", "kernel_ms": round(per[vis["name"]], 5),
+                     "clock_ghz": clock,
+                     "peak_at_clock": None if clock is None else round(PEAK_BF16_TFLOPS * clock / 2.4, 1)},
+        "calls_ms": {c["name"]: round(per[c["name"]], 5) for c in calls},
+        "flops_per_step": flops,
+    }
+
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    if not args.no_cpu_baseline:
+        import oracle
+        log("[bench] cpu baseline (oracle fp32 flash path, sampled query rows of the visual self-attention) ...")
+        threads, avail, model = host_cpus()
+        oracle.set_threads(threads)
+        f32 = lambda t: oracle.bf16_to_f32(t.cpu().view(torch.int16).numpy().view(np.uint16))
+        qf, kf, vf = f32(vis["q"]), f32(vis["k"]), f32(vis["v"])
+        W, fl_row = vis["W"], 4.0 * vis["S"] * 128 * vis["H"]
+        rng = np.random.default_rng(0)
+
+        def cpu(rows):
+            t0 = time.perf_counter()
+            o = oracle.attention(qf, kf, vf, scale=scale, precise=False, rows=rows)
+            return time.perf_counter() - t0, o
+
+        dt, _ = cpu(np.sort(rng.choice(W, size=32, replace=False)))
+        nrows = int(min(W, max(32, 10.0 / 3 * 32 / dt)) // 32 * 32)
+        rows = np.sort(rng.choice(W, size=nrows, replace=False))
+        times, ref, spent = [], None, 0.0
+        while spent < 10.0 or len(times) < 3:
+            dt, ref = cpu(rows)
+            times.append(dt)
+            spent += dt
+        dt = float(np.median(times))
+        got = f32(vis["out"])[rows].astype(np.float64)
+        d = np.abs(got - ref)
+        rel = float(np.linalg.norm(got - ref) / np.linalg.norm(ref.astype(np.float64)))
+        result["cpu_baseline"] = {"value": round(nrows * fl_row / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+                                  "kind": "port", "host_cpus": avail, "cpu_model": model,
+                                  "sample": f"{nrows} of {W} query rows x {vis['H']} heads of the visual "
+                                            f"self-attention over all {vis['S']} keys (fp32 flash path): median of "
+                                            f"{len(times)} runs, {dt:.2f} s each"}
+        result["check"] = {"rows": nrows, "max_abs": float(d.max()), "mean_abs": float(d.mean()), "rel_l2": rel,
+                           "bar": {"max_abs": 2e-2, "mean_abs": 2e-3, "rel_l2": 3e-3},
+                           "pass": bool(d.max() <= 2e-2 and d.mean() <= 2e-3 and rel <= 3e-3)}
+        log(f"[bench] cpu {result['cpu_baseline']['value']:.4f} TFLOP/s on {threads} threads; GPU vs CPU on sampled "
+            f"rows: max-abs {d.max():.3e} mean-abs {d.mean():.3e} rel-L2 {rel:.3e}")
     print(json.dumps(result), flush=True)
 
 
