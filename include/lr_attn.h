@@ -64,9 +64,9 @@ typedef struct ihipStream_t* lr_stream_t;
 /* Attention tile configurations for the _ex entry points (0 = the library's choice: LR_ATTN_CFG_STREAM_W8 for the
  * fused and prepared calls; for attention over key and value rows, non-causal calls of at least 4,096 keys run
  * LR_ATTN_CFG_STREAM_W8 over the key rows when their 256-query blocks fill at least half a round of the device's
- * compute units without leaving a last round less than half full; other calls run LR_ATTN_CFG_PIPE_W4, or
- * LR_ATTN_CFG_PIPE_W8 when non-causal and the 256-query blocks fill whole rounds of the compute units. The workspace
- * call lr_attention_bf16_ws chooses as described there.) */
+ * compute units without leaving a last round less than half full, or fill two rounds or more; other calls run
+ * LR_ATTN_CFG_PIPE_W4, or LR_ATTN_CFG_PIPE_W8 when non-causal and the 256-query blocks fill whole rounds of the
+ * compute units. The workspace call lr_attention_bf16_ws chooses as described there.) */
 #define LR_ATTN_CFG_AUTO 0
 #define LR_ATTN_CFG_PIPE_W8 1      /* attention over value rows: 256 queries per workgroup (8 waves x 32), direct-to-LDS
                                       K/V ring, next tile's QK^T overlapped with the current tile's softmax */

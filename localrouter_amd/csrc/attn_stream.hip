@@ -309,7 +309,10 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     // bytes from one kv head's keys to the next: its tile images, or (KR) the caller's kv-head stride
     const uint64_t head_bytes = KR ? (uint64_t)a.k_hs * 2 : (uint64_t)T * IMG_TILE_BYTES;
 
-    // ---- the work of this workgroup. Whole blocks: logical, logical + nwg, ... below nwhole. With a.split, the
+    // ---- the work of this workgroup. Whole blocks: logical, logical + nwg, ... for the nwhole / nwg full passes over
+    // the workgroups; a last, partial pass of r = nwhole % nwg blocks (no split) is shared by the XCDs in proportion to
+    // their workgroups (XCD x, holding logical ids f .. f + n - 1, takes the contiguous blocks from
+    // base + r f / nwg to base + r (f + n) / nwg), so that no XCD idles while another runs two blocks a CU. With a.split, the
     // blocks from nwhole on (fewer than nwg, the "tail") are laid end to end as U = rem * T key tiles, and tail
     // workgroup L < a.tail_wg takes tiles [L U / tail_wg, (L + 1) U / tail_wg): at most two pieces, the end of one
     // block and the start of the next. A cut block's pieces each leave a partial (O, m, l); the last to arrive
@@ -318,7 +321,11 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     const int nwhole = a.split ? (nblk / nwg) * nwg : nblk;
     const int nt = a.split ? a.tail_wg : 0;
     const int64_t U = (int64_t)(nblk - nwhole) * T;
-    const int n_whole = logical < nwhole ? (nwhole - 1 - logical) / nwg + 1 : 0;
+    const int full = nwhole / nwg, r_last = nwhole - full * nwg;
+    const int xf = logical - idx, xn = per + (xcd < rem8 ? 1 : 0);   // this XCD's first logical id and workgroups
+    const int last0 = (int)((int64_t)r_last * xf / nwg);                // this XCD's first block of the last pass
+    const int last_n = (int)((int64_t)r_last * (xf + xn) / nwg) - last0;
+    const int n_whole = full + (idx < last_n ? 1 : 0);
     int64_t u0 = 0, u1 = 0;
     if (logical < nt) {
         u0 = (int64_t)logical * U / nt;
@@ -365,7 +372,8 @@ __global__ __launch_bounds__(SW * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2
     auto item_of = [&](int it) __attribute__((always_inline)) {
         Item r;
         if (it >= n_pieces) {
-            const int blk = logical + (it - n_pieces) * nwg;
+            const int pass = it - n_pieces;
+            const int blk = pass < full ? logical + pass * nwg : full * nwg + last0 + idx;
             r.head = blk / nqb;
             r.row0 = (blk - r.head * nqb) * SBM;
             r.t0 = 0;

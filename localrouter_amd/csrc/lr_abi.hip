@@ -52,15 +52,17 @@ int split_count(int W, int H, int nkeys, int causal) {
 // into tile images in LDS) instead of the pipelined kernels. Measured from 218 to 50,220 queries x 4-32 heads: below
 // 4,096 keys the 128-query pipelined kernel is as fast or faster. From 4,096 keys on, with a workspace (its split tail
 // cutting the last partial round of blocks over the workgroups) the streaming kernel takes 0.55-0.93 of the pipelined
-// kernel's time from 33 query blocks on. Without one it runs whole 256-query blocks, and wins (0.88-0.99) when they
-// fill between half a round and a round of the CUs or leave a last round at least half full; a last round of a few
-// blocks (288 blocks on 256 CUs: 1.04-1.08) favours the pipelined kernel's 128-query blocks.
+// kernel's time from 33 query blocks on. Without one it runs whole 256-query blocks (a last partial pass shared by
+// the XCDs), and wins when they fill between half a round and a round of the CUs, leave a last round at least half
+// full, or fill two rounds or more (432 blocks on 256 CUs: 0.86-0.93 of the 256-query pipelined kernel's time; 800
+// and 1,600 blocks with a last round of 32 and 64: 0.98 and 0.94 of the 128-query one's); a few blocks past one round
+// (288 blocks: 1.08) favour the pipelined kernel's 128-query blocks.
 bool stream_rows(int W, int H, int nkeys, int causal, bool workspace, int cus) {
     if (causal || nkeys < 4096 || cus < 1) return false;
     const int64_t blocks = (int64_t)((W + 255) / 256) * H;
     if (workspace) return blocks > 32;
     const int64_t tail = blocks % cus;
-    return blocks <= cus ? 2 * blocks >= cus : tail == 0 || 2 * tail >= cus;
+    return blocks <= cus ? 2 * blocks >= cus : blocks >= 2 * (int64_t)cus || tail == 0 || 2 * tail >= cus;
 }
 
 // Whether the streaming kernel over key rows cuts the last partial round of blocks over the workgroups (its split

@@ -191,6 +191,28 @@ def test_stream_rows_equal_images(W, nk, H, HK, causal, p0):
     assert_close(from_dev(rows), _ref(q, k, v, causal=bool(causal), p0=p0), what="stream rows")
 
 
+@pytest.mark.parametrize("W,nk,H,HK", [(6400, 4100, 12, 12), (6400, 4100, 12, 4), (4608, 4096, 24, 24)])
+def test_stream_rows_unsplit_last_pass(W, nk, H, HK):
+    """The streaming kernel over key rows without a workspace runs whole 256-query blocks, L, L + 256, ... per
+    workgroup, and shares the last partial pass (300 blocks on 256 CUs: 44, five or six per XCD; 432 blocks: 176)
+    between the XCDs. Every block must be computed once: the whole output against the pipelined kernel's (an
+    independent schedule, to within the parity bar), and the first and last row of every query block of every head
+    against the oracle."""
+    print(f"\n[stream rows, unsplit last pass] W={W} nk={nk} H={H} HK={HK}", flush=True)
+    q, k, v = _qkv(23, W, nk, H, HK)
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    st = ops.attention(dq, dk, dv, config=ops.CFG_STREAM_W8)
+    w8 = ops.attention(dq, dk, dv, config=ops.CFG_PIPE_W8)
+    torch.cuda.synchronize()
+    got = from_dev(st)
+    # two bf16 outputs, each rounded once from its own fp32 result: twice the relative-L2 bar (a block left uncomputed
+    # or computed from the wrong rows is off by the output's own magnitude)
+    assert_close(got, bf16_f32(from_dev(w8)).astype(np.float64), rel=6e-3, what="stream unsplit vs pipelined W8")
+    rows = np.unique(np.concatenate([np.arange(0, W, 256), np.minimum(np.arange(255, W + 255, 256), W - 1)]))
+    ref = oracle.attention(bf16_f32(q), bf16_f32(k), bf16_f32(v), precise=False, rows=rows)
+    assert_close(got[rows], ref, what="stream unsplit vs oracle")
+
+
 def test_attention_deterministic():
     print("\n[attention determinism] W=600 nk=700 H=4", flush=True)
     q, k, v = _qkv(15, 600, 700, 4, 2)
