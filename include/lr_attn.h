@@ -296,7 +296,10 @@ int lr_joint_attention_fused_noalloc(const void* q_raw, const void* k_raw, const
  *              rejected before any launch.
  * lr_int8_attention writes out bf16 [B][H][Sq][D] contiguous; lr_int8_attention_rows writes rows [Sq][H * D]
  * (B must be 1), the same values. The workspace layout is this library's own (quantised operands, scales, per-tile
- * column sums): it is written by the prep and read by the kernel, nothing else.
+ * column sums, a partial area): the prep writes the operands and the kernel reads them. When the query blocks (256
+ * rows of a head) leave a last round of at most half the device's compute units, the kernel cuts that round's blocks
+ * into up to 4 key ranges and merges them with a second launch, through the workspace's partial area: kernel calls
+ * on one workspace must not overlap.
  *   lr_int8_attention_workspace_bytes  <- Kitchen.Plan.of / kitchen_int8_attention_workspace_bytes (0: unsupported)
  *   lr_int8_attention_prep             <- Kitchen.attentionPrep (launch.zig:360-397): anchor, Q/K and V to int8
  *   lr_int8_attention_kernel           <- Kitchen.attentionKernel (launch.zig:399-419); o_rows 0: out [B][H][Sq][D],
@@ -313,7 +316,7 @@ int lr_int8_attention_rows(const void* q, const void* k, const void* v, void* ou
 int lr_int8_attention_prep(const void* q, const void* k, const void* v, void* workspace, int B, int H, int HK, int Sq,
                            int Sk, int D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
                            int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, lr_stream_t stream);
-int lr_int8_attention_kernel(void* out, const void* workspace, int B, int H, int HK, int Sq, int Sk, int D,
+int lr_int8_attention_kernel(void* out, void* workspace, int B, int H, int HK, int Sq, int Sk, int D,
                              float scale, int o_rows, lr_stream_t stream);
 
 /*

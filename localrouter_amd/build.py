@@ -44,12 +44,13 @@ EXTRA_FLAGS = {"attn_stream.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]
 
 # Scratch (spill) budget per kernel, bytes per lane. The streaming attention kernel and the INT8 attention kernel count
 # their direct global->LDS refills with explicit `s_waitcnt vmcnt(N)`; a scratch access among those loads would be
-# counted too, and the waits would no longer name the loads they wait for. Each keeps one 4-byte value in scratch
-# (the streaming kernel over key rows, attn_stream_kernel<true>, three) that is stored and reloaded only outside its
-# streaming loop: the build generates their assembly and fails when a scratch access sits in a loop block (LOOP_SCAN,
+# counted too, and the waits would no longer name the loads they wait for. The streaming kernel keeps one 4-byte value
+# in scratch (over key rows, attn_stream_kernel<true>, three), stored and reloaded only outside its streaming loop; the
+# INT8 kernel at 128-key tiles three, around the peeled step of its last tile (the partial tile's P mask), the others
+# none: the build generates their assembly and fails when a scratch access sits in a loop block (LOOP_SCAN,
 # loop_scratch_ops). Every other kernel uses none. The build fails when a kernel needs more: the spill must then be
 # found and removed, not accepted. The first entry whose name is part of the kernel's mangled name applies.
-SCRATCH_BUDGET = {"attn_stream_kernelILb1E": 16, "attn_stream_kernel": 8, "i8_attn_kernel": 8}
+SCRATCH_BUDGET = {"attn_stream_kernelILb1E": 16, "attn_stream_kernel": 8, "i8_attn_kernel": 16}
 REMARK_FLAGS = ["-Rpass-analysis=kernel-resource-usage"]
 RESOURCES = PKG / "_build" / "resources.json"
 

@@ -20,6 +20,8 @@
 //   tile's precomputed int16 column sums and B operand 128 * tile_scale, accumulating straight into O.
 //   K, V^T and the per-tile aux block stream through a 3-stage LDS ring with direct global->LDS loads.
 #include <limits.h>
+
+#include <algorithm>
 #include <math.h>
 
 #include <type_traits>
@@ -736,6 +738,9 @@ constexpr float LAZY = 64.0f;
 //   operand fragments are read from LDS two slots ahead;
 //   then the column-sum correction (one f32 MFMA per 32-dim block) and tile t+1's constants (max, scales).
 // K, V^T and the aux block of tile t+3 are loaded into a 4-stage LDS ring while tiles t and t+1 are read.
+// A workgroup below a.nwhole computes one query block over all key tiles and writes its rows; one at or past it (a
+// piece) computes a block of the last partial round over its key range [t0, t1) and leaves the unnormalised rows and
+// (reference, row sum) in the partial area for i8_split_combine_kernel.
 template <int CTA, int NS, int HD>
 __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void i8_attn_kernel(AttnArgs a) {
     constexpr int NB = CTA / 32;                   // 32-key blocks per tile
@@ -757,10 +762,21 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, hf = lane >> 5;
 
-    // XCD-aware order: consecutive logical blocks (same head) land on the same XCD and share its L2
-    const int nwg = gridDim.x, bx = blockIdx.x;
-    const int per = nwg >> 3, rem = nwg & 7, xcd = bx & 7, idx = bx >> 3;
-    const int logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    // Whole blocks (workgroups below nwhole) in XCD-aware order: consecutive logical blocks (same head) land on the
+    // same XCD and share its L2. Pieces: workgroup nwhole + P i + r takes key tiles [r T / P, (r + 1) T / P) of block
+    // nwhole + i, with the cuts rounded to the nearest multiple of NS (cuts at least NS apart: T >= NS P).
+    const int bx = blockIdx.x;
+    const bool piece = bx >= a.nwhole;
+    int logical, t0 = 0, t1 = p.ntiles;
+    if (!piece) {
+        const int nwg = a.nwhole, per = nwg >> 3, rem = nwg & 7, xcd = bx & 7, idx = bx >> 3;
+        logical = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    } else {
+        const int i = (bx - a.nwhole) / a.P, r = bx - a.nwhole - i * a.P;
+        logical = a.nwhole + i;
+        t0 = (r * p.ntiles / a.P + NS / 2) / NS * NS;
+        t1 = r + 1 == a.P ? p.ntiles : ((r + 1) * p.ntiles / a.P + NS / 2) / NS * NS;
+    }
     const int nqb = (a.Sq + 255) / 256;
     const int qblk = logical % nqb, bh = logical / nqb;
     const int head = bh % a.H, b = bh / a.H;
@@ -801,8 +817,10 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         return lds_at<i32x4>(xor_opaque(lds_addr(st) + v_lane, 32 * j) + 32 * CTA * bb);
     };
 
+    // ring stage of tile t (a piece's first tile t0 is a multiple of NS: its ring starts at stage 0 too)
+    auto stage = [&](int t) { return ring + (t % NS) * STAGE; };
     auto issue = [&](int t) {
-        uint8_t* st = ring + (t % NS) * STAGE;
+        uint8_t* st = stage(t);
         if constexpr (KVL > 0) {
 #pragma unroll
             for (int i = 0; i < KVL; ++i) {
@@ -879,11 +897,11 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
     };
 
-    // prologue: tiles 0 .. NS-2 in flight, S(0) and its constants
+    // prologue: tiles t0 .. t0 + NS-2 in flight, S(t0) and its constants
 #pragma unroll
-    for (int t = 0; t < NS - 1; ++t)
-        if (t < ntiles) issue(t);
-    wait_for(1, min(NS - 2, ntiles - 1));
+    for (int j = 0; j < NS - 1; ++j)
+        if (t0 + j < t1) issue(t0 + j);
+    wait_for(1, min(NS - 2, t1 - t0 - 1));
     block_barrier();
     i32x16 SS[2][NB];  // S(t) in SS[t & 1]
     {
@@ -908,10 +926,10 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         constexpr bool LAST = decltype(last_c)::value;
         i32x16 (&S)[NB] = SS[PAR];
         i32x16 (&Sn)[NB] = SS[PAR ^ 1];
-        if (t + NS - 1 < ntiles) issue(t + NS - 1);
-        const uint8_t* stK = ring + ((t + 1) % NS) * STAGE;
-        const uint8_t* stV = ring + (t % NS) * STAGE;
-        const bool mask_p = LAST && tail < CTA;
+        if (t + NS - 1 < t1) issue(t + NS - 1);
+        const uint8_t* stK = stage(t + 1);
+        const uint8_t* stV = stage(t);
+        const bool mask_p = LAST && t1 == ntiles && tail < CTA;
 
         // ---- phase A: S(t+1) on MFMA, P(t) on VALU
         uint32_t P[NB][4];
@@ -1006,20 +1024,20 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
         if (NEXT) {
             constants(mi, stK);
-            if (t + 2 < ntiles) wait_for(t + 2, min(ntiles - 1, t + NS - 1));
+            if (t + 2 < t1) wait_for(t + 2, min(t1 - 1, t + NS - 1));
             else LR_I8_WAIT_VMCNT(0);
             block_barrier();
         }
     };
     // the last tile (every load has landed: the wait before the previous barrier) has no S(t+1)
-    int t = 0;
+    int t = t0;
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
-    for (; t + 2 < ntiles; t += 2) {
+    for (; t + 2 < t1; t += 2) {
         step(t, P0{}, std::true_type{}, std::false_type{});
         step(t + 1, P1{}, std::true_type{}, std::false_type{});
     }
-    if (t + 1 < ntiles) {
+    if (t + 1 < t1) {
         step(t, P0{}, std::true_type{}, std::false_type{});
         step(t + 1, P1{}, std::false_type{}, std::true_type{});
     } else {
@@ -1027,8 +1045,28 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     }
 
     if (!qok) return;
-    const float inv = 1.0f / pair_sum(l_run);
     const float* vs = reinterpret_cast<const float*>(a.ws + p.vs) + bhk * HD;
+    if (piece) {   // the piece's unnormalised rows times the V scales, and (reference, row sum), to the partial area
+        const int pc = bx - a.nwhole, ql = wave * 32 + n;
+        float* po = a.part + ((size_t)pc * 256 + ql) * HD;
+#pragma unroll
+        for (int bb = 0; bb < DB; ++bb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d0 = 32 * bb + 8 * g + 4 * hf;
+                const f32x4 v = *reinterpret_cast<const f32x4*>(vs + d0);
+                *reinterpret_cast<f32x4*>(po + d0) = f32x4{O[bb][4 * g] * v[0], O[bb][4 * g + 1] * v[1],
+                                                           O[bb][4 * g + 2] * v[2], O[bb][4 * g + 3] * v[3]};
+            }
+        const float l = pair_sum(l_run);
+        if (hf == 0) {
+            float* pm = a.part + (size_t)p.part_n * 256 * HD + ((size_t)pc * 256 + ql) * 2;
+            pm[0] = m_run;
+            pm[1] = l;
+        }
+        return;
+    }
+    const float inv = 1.0f / pair_sum(l_run);
     uint16_t* orow = a.out + b * a.o_sb + head * a.o_sh + (int64_t)q * a.o_sn;
 #pragma unroll
     for (int bb = 0; bb < DB; ++bb)
@@ -1041,6 +1079,39 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             w[1] = pack_bf16x2(O[bb][4 * g + 2] * inv * v[2], O[bb][4 * g + 3] * inv * v[3]);
             *reinterpret_cast<u32x2*>(orow + d0) = w;
         }
+}
+
+// The rows of the split query blocks: one wave per query row, O = sum_r 2^(m_r - M) O_r / sum_r 2^(m_r - M) l_r over
+// the block's P pieces (M = max_r m_r; every piece covers at least one key tile, so m_r is finite), two dims a lane.
+template <int HD>
+__global__ __launch_bounds__(256) void i8_split_combine_kernel(AttnArgs a) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int nqb = (a.Sq + 255) / 256;
+    if (row >= (nqb * a.H * a.B - a.nwhole) * 256 || 2 * lane >= HD) return;
+    const int i = row >> 8, ql = row & 255;
+    const int blk = a.nwhole + i, qblk = blk % nqb, bh = blk / nqb, head = bh % a.H, b = bh / a.H;
+    const int q = qblk * 256 + ql;
+    if (q >= a.Sq) return;
+    const float* ml = a.part + (size_t)a.p.part_n * 256 * HD;
+    float M = -INFINITY;
+    for (int r = 0; r < a.P; ++r) M = fmaxf(M, ml[((size_t)(i * a.P + r) * 256 + ql) * 2]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int r = 0; r < a.P; ++r) {
+        const size_t pr = (size_t)(i * a.P + r) * 256 + ql;
+        const float w = __builtin_amdgcn_exp2f(ml[2 * pr] - M);
+        L = fmaf(w, ml[2 * pr + 1], L);
+        const float2 ov = *reinterpret_cast<const float2*>(a.part + pr * HD + 2 * lane);
+        o0 = fmaf(w, ov.x, o0);
+        o1 = fmaf(w, ov.y, o1);
+    }
+    const float inv = 1.0f / L;
+    *reinterpret_cast<uint32_t*>(a.out + b * a.o_sb + head * a.o_sh + (int64_t)q * a.o_sn + 2 * lane) =
+        pack_bf16x2(o0 * inv, o1 * inv);
+}
+
+template <int CTA, int HD>
+void launch_blocks(const AttnArgs& a, unsigned grid, hipStream_t stream) {
+    hipLaunchKernelGGL((i8_attn_kernel<CTA, 4, HD>), dim3(grid), dim3(512), 0, stream, a);
 }
 
 }  // namespace
@@ -1070,15 +1141,34 @@ hipError_t launch_prep(const PrepArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
-    const int nqb = (a.Sq + 255) / 256;
-    const dim3 grid((unsigned)((int64_t)nqb * a.H * a.B));
+// One workgroup per query block of 256 rows. When the blocks leave a last round of at most half the compute units
+// and there are at least 4 SPLIT_MAX key tiles, that round's blocks are cut into P key ranges each (P up to SPLIT_MAX,
+// at most one piece per compute unit), and a second launch merges the pieces' rows.
+hipError_t launch_attention(AttnArgs a, int cus, hipStream_t stream) {
+    const int64_t nqb = (a.Sq + 255) / 256, nblk = nqb * a.H * a.B;
+    if (nblk > 0x7fffffff / SPLIT_MAX) return hipErrorInvalidValue;
+    a.nwhole = (int)nblk;
+    a.P = 1;
+    a.part = reinterpret_cast<float*>(a.ws + a.p.part);
+    const int64_t rem = cus > 0 ? nblk % cus : 0;
+    if (rem > 0 && 2 * rem <= cus && a.p.ntiles >= 4 * SPLIT_MAX) {
+        const int P = (int)std::min<int64_t>(std::min<int64_t>(SPLIT_MAX, cus / rem), a.p.part_n / rem);
+        if (P >= 2) {
+            a.nwhole = (int)(nblk - rem);
+            a.P = P;
+        }
+    }
+    const unsigned grid = (unsigned)(a.nwhole + (nblk - a.nwhole) * a.P);
+    if (a.p.d == 64) launch_blocks<64, 64>(a, grid, stream);
+    else if (a.p.cta == 128) launch_blocks<128, 128>(a, grid, stream);
+    else launch_blocks<64, 128>(a, grid, stream);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.P == 1) return e;
+    const int64_t rows = (nblk - a.nwhole) * 256;
     if (a.p.d == 64)
-        hipLaunchKernelGGL((i8_attn_kernel<64, 4, 64>), grid, dim3(512), 0, stream, a);
-    else if (a.p.cta == 128)
-        hipLaunchKernelGGL((i8_attn_kernel<128, 4, 128>), grid, dim3(512), 0, stream, a);
+        hipLaunchKernelGGL(i8_split_combine_kernel<64>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((i8_attn_kernel<64, 4, 128>), grid, dim3(512), 0, stream, a);
+        hipLaunchKernelGGL(i8_split_combine_kernel<128>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -477,7 +477,7 @@ int i8_prep_impl(const void* q, const void* k, const void* v, void* ws, int B, i
     return (int)lr::i8::launch_prep(a, stream);
 }
 
-int i8_kernel_impl(void* out, const void* ws, int B, int H, int HK, int Sq, int Sk, int D, float scale, int o_rows,
+int i8_kernel_impl(void* out, void* ws, int B, int H, int HK, int Sq, int Sk, int D, float scale, int o_rows,
                    hipStream_t stream) {
     if (!i8_sizes_ok(B, H, HK, Sq, Sk, D) || !ws || !aligned(ws, 256) || !out || !aligned(out, 16)) return ERR_ARGS;
     if (!scale_ok(scale) || (o_rows != 0 && o_rows != 1) || (o_rows && B != 1)) return ERR_ARGS;
@@ -487,7 +487,7 @@ int i8_kernel_impl(void* out, const void* ws, int B, int H, int HK, int Sq, int 
         if (overlap(w, Span{o, o + (uintptr_t)B * H * Sq * D * 2})) return ERR_ARGS;
     }
     lr::i8::AttnArgs a{};
-    a.ws = static_cast<const uint8_t*>(ws);
+    a.ws = static_cast<uint8_t*>(ws);
     a.out = static_cast<uint16_t*>(out);
     a.o_sb = (int64_t)H * Sq * D;
     a.o_sh = o_rows ? D : (int64_t)Sq * D;
@@ -495,7 +495,7 @@ int i8_kernel_impl(void* out, const void* ws, int B, int H, int HK, int Sq, int 
     a.B = B; a.H = H; a.HK = HK; a.G = H / HK; a.Sq = Sq; a.Sk = Sk;
     a.c = scale * 1.4426950408889634f;
     a.p = lr::i8::plan_of(B, H, HK, Sq, Sk, D);
-    return (int)lr::i8::launch_attention(a, stream);
+    return (int)lr::i8::launch_attention(a, device_cus(), stream);
 }
 
 int i8_attention_impl(const void* q, const void* k, const void* v, void* out, void* ws, int B, int H, int HK, int Sq,
@@ -832,7 +832,7 @@ int lr_int8_attention_prep_rope(const void* q, const void* k, const void* v, voi
                         reinterpret_cast<hipStream_t>(stream), freqs, freqs_row_stride, q_norm, k_norm, rot_dim, eps);
 }
 
-int lr_int8_attention_kernel(void* out, const void* workspace, int B, int H, int HK, int Sq, int Sk, int D,
+int lr_int8_attention_kernel(void* out, void* workspace, int B, int H, int HK, int Sq, int Sk, int D,
                              float scale, int o_rows, lr_stream_t stream) {
     return i8_kernel_impl(out, workspace, B, H, HK, Sq, Sk, D, scale, o_rows, stream);
 }

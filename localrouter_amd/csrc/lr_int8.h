@@ -21,6 +21,8 @@
 //   anchor int32 [B][HK]                            anchor key row or -1
 //   arow   bf16 [B][HK][D]                          the anchor row as the keys are shifted by it (the key row as
 //                                                   the prep sees it: raw, or normalised and rotated); zeros if none
+//   part   fp32 [part_n][256][D] then [part_n][256][2]  the attention's split pieces (see AttnArgs): each piece's
+//                                                   unnormalised rows (O times the V scales) and (reference, row sum)
 // Scale granularity (per query row; per 16 keys; per channel) is this library's choice. The reference's per-thread
 // groups follow its mma fragment layout (kernels/cuda/minimax/kitchen/quant_qk_int8.cu:245-247); the arithmetic
 // inside a group is the reference's.
@@ -43,9 +45,12 @@ inline int cta_for(int Sk, int D) { return D >= 128 && Sk > 1024 ? 128 : 64; }
 // launch.zig:387-391).
 inline int rotation_for(int Sk, int D) { return Sk <= 256 ? 4 : D; }
 
+constexpr int SPLIT_MAX = 4;        // key ranges a split query block is cut into
+constexpr int PART_PIECES = 256;    // pieces the partial area holds at most
+
 struct Plan {
-    int d, cta, ntiles, skp, nvchunk, rot;
-    size_t q8, k8, vt, aux, qs, vs, vpart, anchor, arow, total;
+    int d, cta, ntiles, skp, nvchunk, rot, part_n;
+    size_t q8, k8, vt, aux, qs, vs, vpart, anchor, arow, part, total;
 };
 
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -74,6 +79,10 @@ inline Plan plan_of(int B, int H, int HK, int Sq, int Sk, int D) {
     p.vpart = take(bhk * p.nvchunk * D * 4);
     p.anchor = take(bhk * 4);
     p.arow = take(bhk * D * 2);
+    // the attention's split pieces: at most SPLIT_MAX a query block of 256 rows, PART_PIECES in all
+    const size_t nblk = bh * (size_t)((Sq + 255) / 256);
+    p.part_n = (int)(nblk * SPLIT_MAX < (size_t)PART_PIECES ? nblk * SPLIT_MAX : (size_t)PART_PIECES);
+    p.part = take((size_t)p.part_n * 256 * (D + 2) * 4);
     p.total = at;
     return p;
 }
@@ -112,16 +121,22 @@ struct PrepArgs {
 };
 
 struct AttnArgs {
-    const uint8_t* ws;
+    uint8_t* ws;   // read, and (split blocks) written in its partial area
     uint16_t* out;  // bf16, element (b, h, n, c) at out + b*o_sb + h*o_sh + n*o_sn + c
     int64_t o_sb, o_sh, o_sn;
     int B, H, HK, G, Sq, Sk;
     float c;  // scale * log2(e)
     Plan p;
+    // Query blocks (256 rows of one head) 0 .. nwhole - 1 run whole, one workgroup each; the rest (the last partial
+    // round of the device's compute units) are cut into P key ranges each, one workgroup a range, whose rows go to the
+    // partial area (part: the workspace's, Plan::part) and are merged by a second launch. Set by launch_attention.
+    int nwhole, P;
+    float* part;
 };
 
 hipError_t launch_prep(const PrepArgs& a, hipStream_t stream);
-hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+// cus: the device's compute units (the split of the last partial round of query blocks is chosen for them)
+hipError_t launch_attention(AttnArgs a, int cus, hipStream_t stream);
 
 }  // namespace i8
 }  // namespace lr

@@ -241,6 +241,37 @@ def test_int8_gqa_batch_cross(B, H, HK, Sq, Sk):
             _check_out(got[b, h], ref, np.arange(Sq), f"b={b} h={h}")
 
 
+@pytest.mark.parametrize("B,H,HK,Sq,Sk,d", [(1, 4, 2, 2100, 2100, 128), (2, 3, 3, 600, 2200, 128),
+                                             (1, 4, 4, 2100, 2100, 64)])
+def test_int8_split_last_round(B, H, HK, Sq, Sk, d):
+    """Query blocks that fill at most half a round of the compute units, over at least 16 key tiles: the kernel cuts
+    each block into key ranges (starting on 4-tile boundaries; the last range holds the partial last tile and its P
+    mask), and a second launch merges the ranges' rows. Every row of every head against the u8-P emulation and the
+    fp64 attention over the quantised operands; the rows output equals the head-major one bit for bit, and a second
+    call over the same workspace gives the same bits."""
+    print(f"\n[int8 split] B={B} H={H} HK={HK} Sq={Sq} Sk={Sk} d={d}", flush=True)
+    q = oracle.synth_bf16(24, 1, (B, H, Sq, d))
+    k = oracle.synth_bf16(24, 2, (B, HK, Sk, d))
+    v = oracle.synth_bf16(24, 3, (B, HK, Sk, d))
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    ws = ops.int8_attention_prep(dq, dk, dv)
+    kw = dict(batch=B, heads=H, kv_heads=HK, sq=Sq, sk=Sk, head_dim=d)
+    out = ops.int8_attention_kernel(ws, torch.empty((B, H, Sq, d), dtype=torch.bfloat16, device="cuda"), **kw)
+    again = ops.int8_attention_kernel(ws, torch.empty((B, H, Sq, d), dtype=torch.bfloat16, device="cuda"), **kw)
+    got = from_dev(out)
+    assert np.array_equal(from_dev(again), got), "second call over the same workspace"
+    if B == 1:
+        rows = ops.int8_attention_kernel(ws, torch.empty((Sq, H * d), dtype=torch.bfloat16, device="cuda"), rows=True,
+                                         **kw)
+        assert np.array_equal(from_dev(rows).reshape(Sq, H, d).transpose(1, 0, 2), got[0]), "rows != head-major"
+    G = H // HK
+    for b in range(B):
+        for h in range(H):
+            ref = _oracle_head(q[b, h], k[b, h // G], v[b, h // G], Sk)
+            st = _check_out(got[b, h], ref, np.arange(Sq), f"b={b} h={h}")
+            print(f"  b={b} h={h} emu {st[0]:.2e}/{st[1]:.2e} fp64q {st[2]:.2e}/{st[3]:.2e}", flush=True)
+
+
 def test_int8_degenerate_inputs():
     """Zero query rows (uniform attention), identical keys (the anchor removes everything: all scores 0), constant V
     channels, on a tail tile: the masked keys past Sk must not enter the row sums."""
