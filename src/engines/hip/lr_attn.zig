@@ -19,7 +19,7 @@ const std = @import("std");
 pub const Stream = ?*anyopaque;
 
 pub const HEAD_DIM = 128;
-pub const ABI_VERSION: c_int = 8;
+pub const ABI_VERSION: c_int = 9;
 
 pub const TABLE_NONE: c_int = 0;
 pub const TABLE_COSSIN_F32: c_int = 1;

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version():
     header = _lib.HEADER.read_text()
     declared = int(re.search(r"#define LR_ATTN_ABI_VERSION (\d+)", header).group(1))
-    assert _lib.load().lr_attn_abi_version() == declared == 8
+    assert _lib.load().lr_attn_abi_version() == declared == 9
 
 
 def test_workspace_bytes():
