@@ -18,7 +18,9 @@
 //   The MFMA is signed x signed, the reference's P is unsigned: P is stored as P ^ 0x80 (= P - 128) and the missing
 //   128 * sum_j v_j is added back per tile by one v_mfma_f32_32x32x2_f32 per 32-dim block whose A operand is the
 //   tile's precomputed int16 column sums and B operand 128 * tile_scale, accumulating straight into O.
-//   K, V^T and the per-tile aux block stream through a 3-stage LDS ring with direct global->LDS loads.
+//   K, V^T and the per-tile aux block stream through a 4-stage LDS ring with direct global->LDS loads.
+//   The query blocks of a last partial round of the compute units (at most half of them) are cut into up to 4 key
+//   ranges, one workgroup each, whose rows i8_split_combine_kernel merges (launch_attention).
 #include <limits.h>
 
 #include <algorithm>
