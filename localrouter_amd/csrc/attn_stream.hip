@@ -13,7 +13,8 @@
 // from LDS feeds one v_mfma_f32_32x32x16_bf16, 128 bytes per clock per CU at the MFMA rate, half of gfx950's LDS read
 // bandwidth; the two waves of a SIMD overlap one's softmax VALU work and LDS reads with the other's MFMAs):
 //
-//  * Persistent: one workgroup per CU walks the blocks logical, logical + nwg, ... and its key/value tiles form one
+//  * Persistent: one workgroup per CU walks the blocks logical, logical + nwg, ... (a last partial pass shared by the
+//    XCDs; or, split, cut into key ranges over all workgroups) and its key/value tiles form one
 //    continuous stream through two 4-stage LDS rings (64 KB each). The loads of the next block's first tiles are in
 //    flight while the current block finishes, and the query prologue of the next block follows the previous block's
 //    epilogue without a kernel boundary.
