@@ -79,9 +79,11 @@ inline Plan plan_of(int B, int H, int HK, int Sq, int Sk, int D) {
     p.vpart = take(bhk * p.nvchunk * D * 4);
     p.anchor = take(bhk * 4);
     p.arow = take(bhk * D * 2);
-    // the attention's split pieces: at most SPLIT_MAX a query block of 256 rows, PART_PIECES in all
+    // the attention's split pieces: at most SPLIT_MAX a query block of 256 rows, PART_PIECES in all; none below
+    // 4 SPLIT_MAX key tiles, where launch_attention never cuts
     const size_t nblk = bh * (size_t)((Sq + 255) / 256);
-    p.part_n = (int)(nblk * SPLIT_MAX < (size_t)PART_PIECES ? nblk * SPLIT_MAX : (size_t)PART_PIECES);
+    p.part_n = p.ntiles < 4 * SPLIT_MAX ? 0
+             : (int)(nblk * SPLIT_MAX < (size_t)PART_PIECES ? nblk * SPLIT_MAX : (size_t)PART_PIECES);
     p.part = take((size_t)p.part_n * 256 * (D + 2) * 4);
     p.total = at;
     return p;

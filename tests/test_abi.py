@@ -170,8 +170,9 @@ def _i8_plan(B, H, HK, Sq, Sk, d=128):
     cta = 128 if Sk > 1024 and d == 128 else 64
     nt = -(-Sk // cta)
     skp, nvc = nt * cta, -(-Sk // 256)
-    # the attention's split pieces: up to 4 per query block of 256 rows, 256 in all; rows of d + 2 fp32
-    pieces = min(4 * B * H * -(-Sq // 256), 256)
+    # the attention's split pieces: up to 4 per query block of 256 rows, 256 in all, none below 16 key tiles; rows of
+    # d + 2 fp32
+    pieces = min(4 * B * H * -(-Sq // 256), 256) if nt >= 16 else 0
     parts = [B * H * Sq * d, B * HK * skp * d, B * HK * skp * d, B * HK * nt * 1024, B * H * Sq * 4,
              B * HK * d * 4, B * HK * nvc * d * 4, B * HK * 4, B * HK * d * 2, pieces * 256 * (d + 2) * 4]
     return sum(-(-p // 256) * 256 for p in parts)
